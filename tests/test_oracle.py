@@ -1,0 +1,354 @@
+"""Pin the CPU oracle (oracle/pxs_oracle.cpp) before trusting it.
+
+Checks, per oracle function:
+* the reference's own KAT outputs (tests/sparse_numeric_fixture.cpp and
+  tests/sparse_transformer_numeric_fixture.cpp, run from oracle/_ref and
+  committed as tests/golden/*.json);
+* seeded vectors from the compiled reference library (tests/golden/ref_vectors.npz);
+* closed forms and brute force that a plausible mistake would fail.
+All comparisons against the reference are bit-exact: the oracle follows the
+reference's accumulation order and is built with its Release flags.
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle as O
+import workloads as W
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return O.Oracle()
+
+
+@pytest.fixture(scope="module")
+def vec():
+    return dict(np.load(GOLD / "ref_vectors.npz"))
+
+
+# --- the reference's own KAT (tests/sparse_numeric_fixture.cpp:23-170) ----------
+
+def kat_inputs():
+    coords = np.array([[0, 0, 0, 0], [0, 0, 0, 1], [0, 0, 1, 0], [0, 1, 1, 1], [0, 2, 2, 2],
+                       [1, 0, 0, 0], [1, 0, 1, 0], [1, 1, 1, 1], [1, 2, 1, 2], [1, 3, 3, 3]],
+                      np.int32)
+    n = 10
+    f32 = np.float32
+    feats = np.array([f32(-0.31) + f32(0.047) * f32(i) for i in range(n * 3)], f32).reshape(n, 3)
+    lw = np.array([f32(-0.11) + f32(0.013) * f32(i) for i in range(12)], f32).reshape(4, 3)
+    lb = np.array([-0.07, 0.02, 0.11, 0.20], f32)
+    cw = np.array([f32(-0.021) + f32(0.0017) * f32(i) for i in range(27 * 12)], f32).reshape(27, 4, 3)
+    cb = np.array([-0.03, 0.01, 0.05, 0.09], f32)
+    q = np.array([f32(-0.23) + f32(0.017) * f32(i) for i in range(n * 12)], f32).reshape(n, 12)
+    k = np.array([f32(0.17) - f32(0.021) * f32(i) for i in range(n * 12)], f32).reshape(n, 12)
+    v = np.array([f32(-0.13) + f32(0.031) * f32(i) for i in range(n * 12)], f32).reshape(n, 12)
+    ck = np.array([f32(0.09) - f32(0.014) * f32(i) for i in range(60)], f32).reshape(5, 12)
+    cv = np.array([f32(-0.18) + f32(0.022) * f32(i) for i in range(60)], f32).reshape(5, 12)
+    rg = np.array([f32(0.7) + f32(0.013) * f32(i) for i in range(12)], f32)
+    pc = np.array([[0, 0, 0, 0], [0, 1, 0, 1], [1, 0, 1, 0]], np.int32)
+    pf = np.array([f32(-0.17) + f32(0.011) * f32(i) for i in range(48)], f32).reshape(3, 16)
+    sub = np.array([[1, 0, 1, 0, 0, 1, 0, 0], [0, 1, 1, 0, 1, 0, 0, 1], [1, 1, 0, 0, 0, 0, 1, 0]], f32)
+    return dict(coords=coords, feats=feats, lw=lw, lb=lb, cw=cw, cb=cb, q=q, k=k, v=v, ck=ck,
+                cv=cv, rg=rg, pc=pc, pf=pf, sub=sub)
+
+
+def test_kat_sparse_numeric_fixture(orc):
+    gold = {k: np.array(v, np.float32) for k, v in
+            json.loads((GOLD / "sparse_numeric_fixture.json").read_text()).items()}
+    a = kat_inputs()
+    c = a["coords"]
+    np.testing.assert_array_equal(orc.linear(a["feats"], a["lw"], a["lb"]).ravel(),
+                                  gold["sparse_linear_output"])
+    np.testing.assert_array_equal(orc.subm_conv3d(c, a["feats"], a["cw"], a["cb"]).ravel(),
+                                  gold["sparse_conv_output"])
+    np.testing.assert_array_equal(
+        orc.layer_norm(a["feats"], 1e-5, np.array([0.8, 1.1, 1.4], np.float32),
+                       np.array([-0.2, 0.03, 0.17], np.float32)).ravel(),
+        gold["sparse_norm_output"])
+    dco, dfo = orc.downsample_mean(c, a["feats"], 2)
+    np.testing.assert_array_equal(dco.ravel().astype(np.float32), gold["sparse_downsample_coords"])
+    np.testing.assert_array_equal(dfo.ravel(), gold["sparse_downsample_output"])
+    cu = orc.batch_cu_seqlens(c, 2)
+    np.testing.assert_array_equal(
+        orc.varlen_attention(a["q"], a["k"], a["v"], cu, cu, 2, 6, np.float32(0.37)).ravel(),
+        gold["sparse_attention_output"])
+    np.testing.assert_array_equal(orc.rope(c, a["q"], 2, 6).ravel(), gold["sparse_rope_output"])
+    np.testing.assert_array_equal(orc.mh_rms_norm(a["q"], 2, 6, a["rg"]).ravel(),
+                                  gold["sparse_rms_output"])
+    np.testing.assert_array_equal(
+        orc.varlen_attention(a["q"], a["ck"], a["cv"], cu, np.array([0, 3, 5]), 2, 6,
+                             np.float32(0.29)).ravel(),
+        gold["sparse_cross_output"])
+    sco, sfo = orc.channel_to_spatial(a["pc"], a["pf"], 2, a["sub"])
+    np.testing.assert_array_equal(sco.ravel().astype(np.float32),
+                                  gold["sparse_channel_to_spatial_coords"])
+    np.testing.assert_array_equal(sfo.ravel(), gold["sparse_channel_to_spatial_output"])
+
+
+def stable_param(name, count):
+    """tests/sparse_transformer_numeric_fixture.cpp:36-50 (hash-of-name values)."""
+    stable = sum((i + 1) * ord(ch) for i, ch in enumerate(name))
+    out = np.array([(np.float32((i + stable) % 29) - np.float32(14.0)) * np.float32(0.018)
+                    for i in range(count)], np.float32)
+    if name.endswith("gamma"):
+        out = np.abs(out) + np.float32(0.5)
+    return out
+
+
+def test_kat_transformer_block(orc):
+    gold = np.array(json.loads((GOLD / "sparse_transformer_fixture.json").read_text())
+                    ["sparse_transformer_output"], np.float32)
+    C, H, M, CC, PC, n = 12, 2, 18, 5, 7, 10
+    names = [("modulation", 6 * C), ("self_attn.to_qkv.weight", 3 * C * C),
+             ("self_attn.to_qkv.bias", 3 * C), ("self_attn.q_rms_norm.gamma", C),
+             ("self_attn.k_rms_norm.gamma", C), ("self_attn.to_out.weight", C * C),
+             ("self_attn.to_out.bias", C), ("norm2.weight", C), ("norm2.bias", C),
+             ("cross_attn.cross_attn_block.to_q.weight", C * C),
+             ("cross_attn.cross_attn_block.to_q.bias", C),
+             ("cross_attn.cross_attn_block.to_kv.weight", 2 * C * CC),
+             ("cross_attn.cross_attn_block.to_kv.bias", 2 * C),
+             ("cross_attn.cross_attn_block.q_rms_norm.gamma", C),
+             ("cross_attn.cross_attn_block.k_rms_norm.gamma", C),
+             ("cross_attn.cross_attn_block.to_out.weight", C * C),
+             ("cross_attn.cross_attn_block.to_out.bias", C),
+             ("cross_attn.proj_linear.weight", C * PC), ("cross_attn.proj_linear.bias", C),
+             ("mlp.mlp.0.weight", M * C), ("mlp.mlp.0.bias", M), ("mlp.mlp.2.weight", C * M),
+             ("mlp.mlp.2.bias", C)]
+    ws = [stable_param(nm, cnt) for nm, cnt in names]
+    seq = lambda cnt, off, step: np.array([np.float32(off) + np.float32(step) * np.float32(i)  # noqa: E731
+                                           for i in range(cnt)], np.float32)
+    coords = kat_inputs()["coords"]
+    x = seq(n * C, -0.27, 0.013).reshape(n, C)
+    proj = seq(n * PC, 0.19, -0.017).reshape(n, PC)
+    ctx = seq(5 * CC, -0.11, 0.021).reshape(5, CC)
+    tmod = seq(2 * 6 * C, 0.07, -0.009)
+    out = orc.transformer_block(coords, 2, x, tmod, ctx, [0, 3, 5], [C, H, M, CC, PC, 1, 1, 1, 1],
+                                [1e-6, 1.0, 10000.0], ws, projected=proj)
+    np.testing.assert_array_equal(out.ravel(), gold)
+
+
+# --- seeded vectors from the compiled reference --------------------------------
+
+def test_ref_vectors_primitives(orc, vec):
+    v = vec
+    np.testing.assert_array_equal(orc.subm_conv3d(v["conv_coords"], v["conv_feats"], v["conv_w"],
+                                                  v["conv_b"]), v["conv_out"])
+    np.testing.assert_array_equal(orc.linear(v["lin_x"], v["lin_w"], v["lin_b"]), v["lin_out"])
+    np.testing.assert_array_equal(orc.linear(v["lin_x"], v["lin_w"], v["lin_b"]), v["vlin_out"])
+    np.testing.assert_array_equal(orc.layer_norm(v["ln_x"], 1e-6, v["ln_g"], v["ln_b"]),
+                                  v["ln_out_affine"])
+    np.testing.assert_array_equal(orc.layer_norm(v["ln_x"], 1e-5), v["ln_out_plain"])
+    np.testing.assert_array_equal(orc.mh_rms_norm(v["rms_x"], 4, 64, v["rms_g"]), v["rms_out"])
+    np.testing.assert_array_equal(orc.mh_rms_norm(v["rms_x"], 4, 64, v["rms_g"]), v["vrms_out"])
+    np.testing.assert_array_equal(orc.rope(v["rms_coords"], v["rms_x"], 4, 64), v["rope_out"])
+    cu = orc.batch_cu_seqlens(v["attn_coords"], 3)
+    np.testing.assert_array_equal(
+        orc.varlen_attention(v["attn_q"], v["attn_k"], v["attn_v"], cu, cu, 2, 16,
+                             np.float32(0.25)), v["attn_out"])
+    np.testing.assert_array_equal(
+        orc.varlen_attention(v["attn_q"], v["cross_k"], v["cross_v"], cu, v["cross_offsets"], 2,
+                             16, np.float32(0.25)), v["cross_out"])
+    dco, dfo = orc.downsample_mean(v["ds_coords"], v["ds_feats"], 2)
+    np.testing.assert_array_equal(dco, v["ds_out_coords"])
+    np.testing.assert_array_equal(dfo, v["ds_out_feats"])
+    co, cf = orc.channel_to_spatial(v["ds_coords"], v["ds_feats"], 2, v["c2s_sub"])
+    np.testing.assert_array_equal(co, v["c2s_out_coords"])
+    np.testing.assert_array_equal(cf, v["c2s_out_feats"])
+    co, cf = orc.channel_to_spatial(v["ds_coords"], v["ds_feats"], 2)
+    np.testing.assert_array_equal(co, v["c2s_all_coords"])
+    np.testing.assert_array_equal(cf, v["c2s_all_feats"])
+
+
+def test_ref_vectors_block_and_timestep(orc, vec):
+    v = vec
+    ws = [v[f"blk_w{i}"] for i in range(23)]
+    cfg_f = [1e-6, 1.0, 10000.0]
+    out = orc.transformer_block(v["blk_coords"], 2, v["blk_x"], v["blk_tmod"], v["blk_ctx"],
+                                v["blk_ctx_off"], [32, 4, 64, 6, 5, 1, 1, 1, 1], cfg_f, ws,
+                                projected=v["blk_proj"])
+    np.testing.assert_array_equal(out, v["blk_out"])
+    out = orc.transformer_block(v["blk_coords"], 2, v["blk_x"], v["blk_tmod"], v["blk_ctx"],
+                                v["blk_ctx_off"], [32, 4, 64, 6, 5, 1, 1, 1, 0], cfg_f, ws)
+    np.testing.assert_array_equal(out, v["blk_out_noproj"])
+    np.testing.assert_array_equal(orc.timestep_embedding(v["temb_t"], 256), v["temb_freq"])
+    np.testing.assert_array_equal(
+        orc.timestep_embed_mlp(v["temb_t"], 32, 256, v["temb_w0"], v["temb_b0"], v["temb_w2"],
+                               v["temb_b2"]), v["temb_out"])
+
+
+def test_row_sampled_block_matches_full(orc, vec):
+    """Row sampling (the CPU baseline for large configs) is exact per sampled row."""
+    v = vec
+    ws = [v[f"blk_w{i}"] for i in range(23)]
+    rows = np.array([0, 5, 17, v["blk_coords"].shape[0] - 1])
+    out = orc.transformer_block(v["blk_coords"], 2, v["blk_x"], v["blk_tmod"], v["blk_ctx"],
+                                v["blk_ctx_off"], [32, 4, 64, 6, 5, 1, 1, 1, 0],
+                                [1e-6, 1.0, 10000.0], ws, rows=rows)
+    np.testing.assert_array_equal(out[rows], v["blk_out_noproj"][rows])
+
+
+def test_ref_conv_full_size(orc):
+    """The oracle reproduces the reference conv on the 64^3 fp32 workload bit for bit."""
+    import hashlib
+
+    gold = json.loads((GOLD / "ref_conv_64.json").read_text())
+    wl = W.conv_fp32_64()
+    out = orc.subm_conv3d(wl["coords"], wl["feats"], wl["weight"], wl["bias"])
+    assert out.shape[0] == gold["points"]
+    np.testing.assert_array_equal(out[gold["rows"]], np.array(gold["values"], np.float32))
+    assert hashlib.sha256(np.ascontiguousarray(out, "<f4").tobytes()).hexdigest() == gold["sha256"]
+
+
+# --- closed forms / brute force ---------------------------------------------------
+
+def brute_neighbors(coords):
+    index = {tuple(c): i for i, c in enumerate(coords.tolist())}
+    n = len(coords)
+    idx = np.full((27, n), n, np.int32)
+    for p, (b, x, y, z) in enumerate(coords.tolist()):
+        for k in range(27):
+            kd, kh, kw = k // 9, (k // 3) % 3, k % 3
+            idx[k, p] = index.get((b, x + kd - 1, y + kh - 1, z + kw - 1), n)
+    return idx
+
+
+def test_neighbor_map_brute_force_and_invariants(orc):
+    coords = W.shell_coords(16, [[(4.0, 7.0)], [(3.0, 6.0)]], 21)
+    idx = orc.neighbor_map(coords)
+    np.testing.assert_array_equal(idx, brute_neighbors(coords))
+    n = coords.shape[0]
+    np.testing.assert_array_equal(idx[13], np.arange(n))
+    # symmetry: idx[k][p] = q  <=>  idx[26-k][q] = p
+    for k in range(27):
+        present = idx[k] != n
+        p = np.nonzero(present)[0]
+        np.testing.assert_array_equal(idx[26 - k][idx[k][p]], p)
+    pin, pout, offs = orc.neighbor_pairs(idx)
+    assert offs[27] == int((idx != n).sum())
+    for k in range(27):
+        seg = slice(offs[k], offs[k + 1])
+        assert np.all(np.diff(pout[seg]) > 0)
+        np.testing.assert_array_equal(idx[k][pout[seg]], pin[seg])
+
+
+def test_neighbor_map_batches_do_not_mix(orc):
+    coords = np.array([[0, 1, 1, 1], [1, 1, 1, 2], [1, 1, 1, 1]], np.int32)
+    idx = orc.neighbor_map(coords)
+    assert idx[13 + 1][0] == 3  # (0,1,1,2) absent in batch 0
+    assert idx[13 + 1][2] == 1 and idx[13 - 1][1] == 2
+
+
+def test_conv_centre_identity_closed_form(orc):
+    coords = W.shell_coords(16, [[(4.0, 7.0)]], 22)
+    n = coords.shape[0]
+    x = W.normal(22, n * 8, 1).reshape(n, 8)
+    w = np.zeros((27, 8, 8), np.float32)
+    w[13] = np.eye(8, dtype=np.float32)
+    b = W.normal(22, 8, 2)
+    np.testing.assert_array_equal(orc.subm_conv3d(coords, x, w, b), x + b)
+
+
+def test_conv_brute_force_small(orc):
+    coords = W.shell_coords(8, [[(2.0, 3.5)]], 23)
+    n = coords.shape[0]
+    x = W.normal(23, n * 3, 1).reshape(n, 3).astype(np.float64)
+    w = W.normal(23, 27 * 5 * 3, 2).reshape(27, 5, 3).astype(np.float64)
+    b = W.normal(23, 5, 3).astype(np.float64)
+    idx = brute_neighbors(coords)
+    ref = np.tile(b, (n, 1))
+    for k in range(27):
+        for p in range(n):
+            if idx[k, p] != n:
+                ref[p] += w[k] @ x[idx[k, p]]
+    got = orc.subm_conv3d(coords, x, w, b)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_attention_closed_forms(orc):
+    n, H, D = 12, 2, 8
+    q = W.normal(24, n * H * D, 1).reshape(n, H * D)
+    k = np.tile(W.normal(24, H * D, 2), (n, 1))  # identical keys -> uniform weights
+    v = W.normal(24, n * H * D, 3).reshape(n, H * D)
+    cu = np.array([0, n])
+    out = orc.varlen_attention(q, k, v, cu, cu, H, D, 0.3)
+    np.testing.assert_allclose(out, np.tile(v.mean(0), (n, 1)), rtol=1e-5, atol=1e-6)
+    out1 = orc.varlen_attention(q, k[:1], v[:1], cu, np.array([0, 1]), H, D, 0.3)
+    np.testing.assert_allclose(out1, np.tile(v[:1], (n, 1)), rtol=0, atol=0)
+
+
+def test_layer_norm_constant_row_gives_beta(orc):
+    x = np.full((3, 16), 2.5, np.float32)
+    g, b = W.normal(25, 16, 1), W.normal(25, 16, 2)
+    np.testing.assert_array_equal(orc.layer_norm(x, 1e-6, g, b), np.tile(b, (3, 1)))
+
+
+def test_strided_conv_identity_is_count_times_mean(orc):
+    coords = W.shell_coords(16, [[(4.0, 7.0)], [(3.0, 6.0)]], 26)
+    n = coords.shape[0]
+    x = W.normal(26, n * 6, 1).reshape(n, 6)
+    oc, child = orc.downsample_coords_s2(coords)
+    dco, dfo = orc.downsample_mean(coords, x, 2)
+    np.testing.assert_array_equal(oc, dco)
+    w = np.tile(np.eye(6, dtype=np.float32), (8, 1, 1))
+    out = orc.sparse_conv3d_s2(child, x, w, np.zeros(6, np.float32))
+    counts = (child >= 0).sum(1).astype(np.float32)[:, None]
+    np.testing.assert_allclose(out, counts * dfo, rtol=1e-5, atol=1e-5)
+    # every input row is a child of exactly one output row
+    rows = np.sort(child[child >= 0])
+    np.testing.assert_array_equal(rows, np.arange(n))
+
+
+def test_window_partition_brute_force(orc):
+    coords = W.shell_coords(24, [[(6.0, 10.0)], [(5.0, 9.0)]], 27)
+    for shift in (0, 4):
+        fwd, bwd, cu = orc.window_partition(coords, (24, 24, 24), 8, shift)
+        n = coords.shape[0]
+        np.testing.assert_array_equal(np.sort(fwd), np.arange(n))
+        np.testing.assert_array_equal(bwd[fwd], np.arange(n))
+        nw = -(-(24 + shift) // 8)
+        wkey = [(b, (x + shift) // 8, (y + shift) // 8, (z + shift) // 8)
+                for b, x, y, z in coords.tolist()]
+        wid = [((b * nw + a) * nw + c) * nw + d for b, a, c, d in wkey]
+        expect = sorted(range(n), key=lambda i: (wid[i], i))
+        np.testing.assert_array_equal(fwd, expect)
+        for s in range(len(cu) - 1):
+            members = fwd[cu[s]:cu[s + 1]]
+            assert len({wid[i] for i in members}) == 1
+        assert len(cu) - 1 == len(set(wid))
+
+
+def test_validation_first_error_order(orc):
+    coords = np.array([[0, 0, 0, 0], [0, 0, 0, 1], [0, 0, 0, 0], [0, 9, 0, 0]], np.int32)
+    f = np.zeros((4, 2), np.float32)
+    assert orc.sparse_valid(coords, 1, (4, 4, 4), f, 2) == (5, 2)
+    coords2 = coords.copy()
+    coords2[1] = [0, 0, 5, 0]
+    assert orc.sparse_valid(coords2, 1, (4, 4, 4), f, 2) == (4, 1)
+    f2 = f.copy()
+    f2[0, 1] = np.nan
+    assert orc.sparse_valid(coords, 1, (4, 4, 4), f2, 2) == (7, 0)
+    c3 = np.array([[1, 0, 0, 0], [0, 0, 0, 1]], np.int32)
+    assert orc.sparse_valid(c3, 2, (4, 4, 4), np.zeros((2, 2), np.float32), 2) == (6, 1)
+    assert orc.sparse_valid(c3, 0, (4, 4, 4), np.zeros((2, 2), np.float32), 2)[0] == 1
+    assert orc.sparse_valid(c3, 2, (4, 4, 4), np.zeros(3, np.float32), 2)[0] == 3
+
+
+@pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref is built only where /root/reference exists")
+def test_validation_messages_match_compiled_reference(orc):
+    ref = O.Reference()
+    cases = [
+        (np.array([[0, 0, 0, 0], [0, 0, 0, 1], [0, 0, 0, 0]], np.int32), 1, np.zeros((3, 2))),
+        (np.array([[0, 0, 0, 0], [0, 0, 5, 0]], np.int32), 1, np.zeros((2, 2))),
+        (np.array([[1, 0, 0, 0], [0, 0, 0, 1]], np.int32), 2, np.zeros((2, 2))),
+        (np.array([[0, 0, 0, 0], [0, 0, 0, 1]], np.int32), 1, np.array([[0, 1], [np.inf, 0]])),
+    ]
+    for coords, batch, feats in cases:
+        ok, msg = ref.valid(ref.sparse(coords, feats, batch, (4, 4, 4)))
+        code, _ = orc.sparse_valid(coords, batch, (4, 4, 4), feats, 2)
+        assert not ok and code and O.VALID_MESSAGES[code] == msg
