@@ -1,0 +1,349 @@
+// Varlen flash attention on MFMA (sparse self-, cross- and window attention).
+//
+// Work item = (segment, 32*NW-query tile, head).  NW wavefronts each own 32
+// queries and share 64-key K/V tiles staged in LDS.  For every key tile a
+// wave computes S^T = K Q^T (keys x queries) so that each lane owns one query
+// (lane % 32) and 32 of its 64 scores; the online-softmax statistics are then
+// lane-local plus one exchange with the partner lane (lane ^ 32).  The output
+// is accumulated transposed, O^T = V^T P^T, so the running rescale is
+// lane-local too.  P feeds the second MFMA straight from registers (the
+// 32x32 accumulator layout of S^T is the B-operand layout of the next MFMA
+// for the key order it implies); V is staged transposed in LDS so the matching
+// A-operand fragments are two 8-byte reads.
+//
+//   bf16: v_mfma_f32_32x32x16_bf16 (8 for S^T + 8 for O^T per wave per tile)
+//   fp32: v_mfma_f32_32x32x2_f32   (64 + 64 per wave per tile)
+// head_dim and value_dim up to 64 (zero padded to 64 inside the kernel).
+
+#include "pxs_common.h"
+#include "scan.h"
+
+#include <cmath>
+
+namespace pxs {
+namespace {
+
+constexpr int kKeys = 64;  // keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+    const void * q;
+    const void * k;
+    const void * v;
+    int64_t ldq, ldk, ldv;
+    const int64_t * cu_q;
+    const int64_t * cu_k;
+    int nseg;
+    const int64_t * tile_start;  // [nseg + 1]; tile_start[nseg] = total tiles
+    const int32_t * row_map;
+    int hd, vd;
+    float scale_log2;
+    void * o;
+    int64_t ldo;
+    int vec_ok;
+};
+
+template <typename T> struct AttnTraits;
+template <> struct AttnTraits<uint16_t> {
+    static constexpr int kVec = 8;                  // elements per 16 bytes
+    static constexpr int kRowBytes = 64 * 2;        // one padded head row
+    static constexpr int kKPitch = kRowBytes + 16;  // K tile row pitch (bytes)
+    static constexpr int kVPitch = kKeys * 2 + 8;   // V^T row pitch (bytes)
+};
+template <> struct AttnTraits<float> {
+    static constexpr int kVec = 4;
+    static constexpr int kRowBytes = 64 * 4;
+    static constexpr int kKPitch = kRowBytes + 16;
+    static constexpr int kVPitch = kKeys * 4 + 16;
+};
+
+template <typename T>
+__device__ __forceinline__ void load16(const T * base, int64_t row, int64_t ld, int col,
+                                       int limit, bool vec_ok, T (&out)[16 / sizeof(T)]) {
+    constexpr int kVec = 16 / sizeof(T);
+    if (vec_ok && col + kVec <= limit) {
+        *reinterpret_cast<uint4 *>(out) = *reinterpret_cast<const uint4 *>(base + row * ld + col);
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) out[e] = (col + e < limit) ? base[row * ld + col + e] : T(0);
+}
+
+__global__ void attn_tiles_kernel(const int64_t * __restrict__ cu_q, int nseg, int bq,
+                                  int32_t * __restrict__ tiles) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const int64_t len = cu_q[s + 1] - cu_q[s];
+    tiles[s] = static_cast<int32_t>((len + bq - 1) / bq);
+}
+
+template <typename T, int NW>
+__global__ void __launch_bounds__(NW * 64)
+flash_attn_kernel(AttnArgs a) {
+    using Tr = AttnTraits<T>;
+    constexpr int kVec = Tr::kVec;
+    constexpr int kThreads = NW * 64;
+    constexpr int kChunksPerRow = Tr::kRowBytes / 16;
+    __shared__ __align__(16) char k_lds[kKeys * Tr::kKPitch];
+    __shared__ __align__(16) char vt_lds[64 * Tr::kVPitch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, r = lane & 31;
+    const int head = blockIdx.y;
+
+    const int64_t t = blockIdx.x;
+    if (t >= a.tile_start[a.nseg]) return;
+    int lo = 0, hi = a.nseg - 1;
+    while (lo < hi) {  // largest s with tile_start[s] <= t
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.tile_start[mid] <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    const int seg = lo;
+    const int64_t q_begin = a.cu_q[seg] + (t - a.tile_start[seg]) * (32 * NW);
+    const int64_t q_end = a.cu_q[seg + 1];
+    const int64_t k_begin = a.cu_k[seg], k_end = a.cu_k[seg + 1];
+
+    const T * __restrict__ qp = static_cast<const T *>(a.q);
+    const T * __restrict__ kp = static_cast<const T *>(a.k);
+    const T * __restrict__ vp = static_cast<const T *>(a.v);
+
+    // This lane's query and its Q fragment (dims 32h .. 32h+31).
+    const int64_t qi = q_begin + wave * 32 + r;
+    const bool q_valid = qi < q_end;
+    const int64_t q_row = q_valid ? (a.row_map ? a.row_map[qi] : qi) : -1;
+    T qv[32];
+#pragma unroll
+    for (int c = 0; c < 32 / kVec; ++c) {
+        T tmp[kVec];
+        if (q_valid) {
+            load16<T>(qp + head * a.hd, q_row, a.ldq, 32 * h + c * kVec, a.hd, a.vec_ok, tmp);
+        } else {
+#pragma unroll
+            for (int e = 0; e < kVec; ++e) tmp[e] = T(0);
+        }
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) qv[c * kVec + e] = tmp[e];
+    }
+
+    f32x16 oacc[2];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    for (int64_t kt0 = k_begin; kt0 < k_end; kt0 += kKeys) {
+        __syncthreads();
+        // Stage K (row layout) and V (transposed) for keys kt0 .. kt0+63.
+        for (int c = tid; c < kKeys * kChunksPerRow; c += kThreads) {
+            const int key = c / kChunksPerRow, piece = c % kChunksPerRow;
+            const int64_t kidx = kt0 + key;
+            T kk[kVec], vv[kVec];
+            if (kidx < k_end) {
+                const int64_t row = a.row_map ? a.row_map[kidx] : kidx;
+                load16<T>(kp + head * a.hd, row, a.ldk, piece * kVec, a.hd, a.vec_ok, kk);
+                load16<T>(vp + head * a.vd, row, a.ldv, piece * kVec, a.vd, a.vec_ok, vv);
+            } else {
+#pragma unroll
+                for (int e = 0; e < kVec; ++e) kk[e] = vv[e] = T(0);
+            }
+            *reinterpret_cast<uint4 *>(k_lds + key * Tr::kKPitch + piece * 16) =
+                *reinterpret_cast<const uint4 *>(kk);
+#pragma unroll
+            for (int e = 0; e < kVec; ++e) {
+                *reinterpret_cast<T *>(vt_lds + (piece * kVec + e) * Tr::kVPitch +
+                                       key * static_cast<int>(sizeof(T))) = vv[e];
+            }
+        }
+        __syncthreads();
+
+        // S^T for two 32-key sub-tiles.
+        f32x16 sacc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sacc[kt][v] = 0.0f;
+            const char * krow = k_lds + (kt * 32 + r) * Tr::kKPitch;
+            if constexpr (sizeof(T) == 2) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const bf16x8 af = *reinterpret_cast<const bf16x8 *>(krow + h * 64 + s * 16);
+                    bf16x8 bq;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) bq[e] = __builtin_bit_cast(__bf16, qv[s * 8 + e]);
+                    sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bq, sacc[kt], 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const f32x4 af = *reinterpret_cast<const f32x4 *>(krow + (32 * h + 4 * u) * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            af[e], __builtin_bit_cast(float, qv[4 * u + e]), sacc[kt], 0, 0, 0);
+                    }
+                }
+            }
+        }
+
+        // Online softmax (log2 domain).  Register v of sub-tile kt holds key
+        // kt*32 + 8*(v/4) + 4h + v%4.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t key = kt0 + kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                const float sv = key < k_end ? sacc[kt][v] * a.scale_log2 : -INFINITY;
+                sacc[kt][v] = sv;
+                mx = fmaxf(mx, sv);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = (m_new == -INFINITY) ? 1.0f : exp2f(m_run - m_new);
+        float rs = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float p = (m_new == -INFINITY) ? 0.0f : exp2f(sacc[kt][v] - m_new);
+                sacc[kt][v] = p;
+                rs += p;
+            }
+        }
+        rs += __shfl_xor(rs, 32, 64);
+        l_run = l_run * alpha + rs;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+
+        // O^T += V^T P^T.
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            if constexpr (sizeof(T) == 2) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    bf16x8 pb;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) pb[e] = static_cast<__bf16>(sacc[kt][8 * u + e]);
+#pragma unroll
+                    for (int dt = 0; dt < 2; ++dt) {
+                        const char * vrow = vt_lds + (dt * 32 + r) * Tr::kVPitch;
+                        const int key0 = kt * 32 + 16 * u + 4 * h;
+                        const uint2 lo4 = *reinterpret_cast<const uint2 *>(vrow + key0 * 2);
+                        const uint2 hi4 = *reinterpret_cast<const uint2 *>(vrow + (key0 + 8) * 2);
+                        const uint4 packed = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+                        const bf16x8 va = __builtin_bit_cast(bf16x8, packed);
+                        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, oacc[dt], 0, 0, 0);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int dt = 0; dt < 2; ++dt) {
+                        const char * vrow = vt_lds + (dt * 32 + r) * Tr::kVPitch;
+                        const f32x4 va = *reinterpret_cast<const f32x4 *>(
+                            vrow + (kt * 32 + 8 * i + 4 * h) * 4);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                va[j], sacc[kt][4 * i + j], oacc[dt], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    if (!q_valid) return;
+    const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    T * op = static_cast<T *>(a.o) + q_row * a.ldo + head * a.vd;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = dt * 32 + 8 * i + 4 * h + j;
+                if (d < a.vd) store_f32(op + d, oacc[dt][4 * i + j] * inv_l);
+            }
+        }
+    }
+}
+
+template <typename T, int NW>
+int launch_attn(const AttnArgs & args, int64_t total_q, int heads, hipStream_t stream) {
+    const int64_t bound = total_q / (32 * NW) + args.nseg + 1;
+    if (bound > INT32_MAX) return fail(PXS_ERR_ARG, "attention grid too large");
+    hipLaunchKernelGGL((flash_attn_kernel<T, NW>), dim3(static_cast<unsigned>(bound), heads),
+                       dim3(NW * 64), 0, stream, args);
+    return check_launch("flash attention");
+}
+
+bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+} // namespace
+} // namespace pxs
+
+using namespace pxs;
+
+extern "C" {
+
+size_t pxs_attention_workspace_bytes(int nseg) {
+    const int64_t n = std::max(nseg, 1);
+    return static_cast<size_t>(n + 1) * sizeof(int64_t) + static_cast<size_t>(n) * sizeof(int32_t) +
+           scan_workspace_bytes(n) + 64;
+}
+
+int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k, int64_t ld_k,
+                         const void * v, int64_t ld_v, const int64_t * cu_q,
+                         const int64_t * cu_k, int nseg, int64_t total_q,
+                         const int32_t * row_map, int heads, int head_dim, float scale, void * o,
+                         int64_t ld_o, void * workspace, void * stream) {
+    PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_varlen_attention: bad dtype");
+    PXS_CHECK(heads > 0 && head_dim > 0 && head_dim <= 64, PXS_ERR_ARG,
+              "pxs_varlen_attention: head_dim must be in 1..64");
+    PXS_CHECK(heads <= 65535, PXS_ERR_ARG, "pxs_varlen_attention: too many heads");
+    PXS_CHECK(scale > 0.0f && std::isfinite(scale), PXS_ERR_ARG,
+              "sparse attention scale must be finite and positive");
+    PXS_CHECK(nseg >= 0 && total_q >= 0, PXS_ERR_ARG, "pxs_varlen_attention: bad segment count");
+    PXS_CHECK(ld_q >= heads * head_dim && ld_k >= heads * head_dim && ld_v >= heads * head_dim &&
+                  ld_o >= heads * head_dim,
+              PXS_ERR_ARG, "pxs_varlen_attention: row stride smaller than heads * head_dim");
+    if (nseg == 0 || total_q == 0) return PXS_OK;
+    PXS_CHECK(q && k && v && o && cu_q && cu_k && workspace, PXS_ERR_ARG,
+              "pxs_varlen_attention: null pointer");
+    hipStream_t s = as_stream(stream);
+    // Small segments (windows) use one wavefront per workgroup.
+    const int nw = (total_q / nseg >= 256) ? 4 : 1;
+    int64_t * tile_start = static_cast<int64_t *>(workspace);
+    int32_t * tiles = reinterpret_cast<int32_t *>(tile_start + nseg + 1);
+    void * scan_ws = reinterpret_cast<void *>(
+        (reinterpret_cast<uintptr_t>(tiles + nseg) + 7) & ~uintptr_t(7));
+    hipLaunchKernelGGL(attn_tiles_kernel, dim3(grid_for(nseg, 256)), dim3(256), 0, s, cu_q, nseg,
+                       32 * nw, tiles);
+    int rc = exclusive_scan_i32(tiles, tile_start, nseg, tile_start + nseg, scan_ws, s);
+    if (rc) return rc;
+    AttnArgs a{};
+    a.q = q; a.k = k; a.v = v; a.ldq = ld_q; a.ldk = ld_k; a.ldv = ld_v;
+    a.cu_q = cu_q; a.cu_k = cu_k; a.nseg = nseg; a.tile_start = tile_start;
+    a.row_map = row_map; a.hd = head_dim; a.vd = head_dim;
+    a.scale_log2 = scale * kLog2e; a.o = o; a.ldo = ld_o;
+    const int vec = dtype == PXS_BF16 ? 8 : 4;
+    a.vec_ok = (head_dim % vec == 0) && (ld_q % vec == 0) && (ld_k % vec == 0) &&
+               (ld_v % vec == 0) && aligned16(q) && aligned16(k) && aligned16(v);
+    if (dtype == PXS_BF16) {
+        return nw == 4 ? launch_attn<uint16_t, 4>(a, total_q, heads, s)
+                       : launch_attn<uint16_t, 1>(a, total_q, heads, s);
+    }
+    return nw == 4 ? launch_attn<float, 4>(a, total_q, heads, s)
+                   : launch_attn<float, 1>(a, total_q, heads, s);
+}
+
+} // extern "C"

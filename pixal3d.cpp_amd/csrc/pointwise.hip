@@ -1,0 +1,382 @@
+// Row-wise HBM-bound kernels: layer norm (+ adaLN modulation), multi-head RMS
+// norm, 3-D RoPE, the fused QKV prologue, and activations.
+//
+// One wavefront per row; per-row reductions use wavefront shuffles.  These
+// kernels read each row once from HBM (later passes over the same row hit
+// L1/L2), so their bound is HBM bandwidth: bytes = rows * C * (in + out).
+
+#include "pxs_common.h"
+
+#include <cmath>
+#include <vector>
+
+namespace pxs {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // 4 wavefronts of 64 lanes
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+template <typename TX, typename TY, bool kModulate>
+__global__ void __launch_bounds__(64 * kRowsPerBlock)
+layer_norm_kernel(const TX * __restrict__ x, int64_t rows, int channels, float eps,
+                  const float * __restrict__ gamma, const float * __restrict__ beta,
+                  const int32_t * __restrict__ coords, const float * __restrict__ block_mod,
+                  const float * __restrict__ time_mod, int mod_offset, TY * __restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const TX * src = x + row * channels;
+    float s = 0.0f;
+    for (int c = lane; c < channels; c += 64) s += load_f32(src + c);
+    const float mean = wave_sum(s) / static_cast<float>(channels);
+    float v = 0.0f;
+    for (int c = lane; c < channels; c += 64) {
+        const float d = load_f32(src + c) - mean;
+        v += d * d;
+    }
+    const float var = wave_sum(v) / static_cast<float>(channels);
+    const float inv = 1.0f / sqrtf(var + eps);
+    TY * dst = y + row * channels;
+    const float * tm = nullptr;
+    if constexpr (kModulate) tm = time_mod + static_cast<int64_t>(coords[row * 4]) * 6 * channels;
+    for (int c = lane; c < channels; c += 64) {
+        float val = (load_f32(src + c) - mean) * inv;
+        if (gamma) val = val * gamma[c] + beta[c];
+        if constexpr (kModulate) {
+            const float scale = block_mod[mod_offset + channels + c] + tm[mod_offset + channels + c];
+            const float shift = block_mod[mod_offset + c] + tm[mod_offset + c];
+            val = val * (1.0f + scale) + shift;
+        }
+        store_f32(dst + c, val);
+    }
+}
+
+// RoPE frequency table computed on the host exactly as the reference does
+// (std::pow in float), passed by value.
+struct RopeTable {
+    int fdim;
+    float freq[32];
+};
+
+RopeTable make_rope_table(int head_dim, float fmin, float fbase) {
+    RopeTable t{};
+    const int pairs = head_dim / 2;
+    t.fdim = pairs / 3;
+    for (int i = 0; i < t.fdim && i < 32; ++i) {
+        t.freq[i] = fmin / std::pow(fbase, static_cast<float>(i) / static_cast<float>(t.fdim));
+    }
+    return t;
+}
+
+__device__ __forceinline__ void rope_pair(float e, float o, float phase, float & re, float & ro) {
+    const float cs = cosf(phase), sn = sinf(phase);
+    re = e * cs - o * sn;
+    ro = e * sn + o * cs;
+}
+
+// Generic per-(row, head) kernel: optional RMS norm then optional RoPE.
+// Handles any head_dim; used for the standalone entry points.
+template <typename T>
+__global__ void head_norm_rope_kernel(const T * __restrict__ x, int64_t ld_x, int64_t rows,
+                                      int heads, int head_dim, const float * __restrict__ gamma,
+                                      const int32_t * __restrict__ coords, RopeTable rope,
+                                      T * __restrict__ y, int64_t ld_y) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= rows * heads) return;
+    const int64_t row = t / heads;
+    const int head = static_cast<int>(t - row * heads);
+    const T * src = x + row * ld_x + head * head_dim;
+    T * dst = y + row * ld_y + head * head_dim;
+    float inv = 1.0f;
+    const float mult = sqrtf(static_cast<float>(head_dim));
+    if (gamma) {
+        float sq = 0.0f;
+        for (int d = 0; d < head_dim; ++d) {
+            const float v = load_f32(src + d);
+            sq += v * v;
+        }
+        inv = 1.0f / fmaxf(sqrtf(sq), 1e-12f);
+    }
+    const float * g = gamma ? gamma + head * head_dim : nullptr;
+    if (coords) {
+        const int xyz[3] = {coords[row * 4 + 1], coords[row * 4 + 2], coords[row * 4 + 3]};
+        for (int p = 0; p < head_dim / 2; ++p) {
+            float e = load_f32(src + 2 * p), o = load_f32(src + 2 * p + 1);
+            if (g) {
+                e = e * inv * mult * g[2 * p];
+                o = o * inv * mult * g[2 * p + 1];
+            }
+            float phase = 0.0f;
+            if (p < 3 * rope.fdim) phase = static_cast<float>(xyz[p / rope.fdim]) * rope.freq[p % rope.fdim];
+            float re, ro;
+            rope_pair(e, o, phase, re, ro);
+            store_f32(dst + 2 * p, re);
+            store_f32(dst + 2 * p + 1, ro);
+        }
+    } else {
+        for (int d = 0; d < head_dim; ++d) {
+            float v = load_f32(src + d);
+            if (g) v = v * inv * mult * g[d];
+            store_f32(dst + d, v);
+        }
+    }
+}
+
+// Fast path of the QKV prologue for head_dim == 64: one wavefront per row,
+// lane = dimension.  q/k: RMS norm (wave reduction) then RoPE (pair partner
+// via a lane shuffle); v copied.
+template <typename T>
+__global__ void __launch_bounds__(64 * kRowsPerBlock)
+qkv_prepare64_kernel(const T * __restrict__ qkv, int64_t rows, int heads,
+                     const float * __restrict__ q_gamma, const float * __restrict__ k_gamma,
+                     const int32_t * __restrict__ coords, RopeTable rope, T * __restrict__ q,
+                     T * __restrict__ k, T * __restrict__ v) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int C = heads * 64;
+    const T * src = qkv + row * 3 * C;
+    float phase = 0.0f;
+    if (coords) {
+        const int p = lane >> 1;
+        if (p < 3 * rope.fdim) {
+            const int axis = coords[row * 4 + 1 + p / rope.fdim];
+            phase = static_cast<float>(axis) * rope.freq[p % rope.fdim];
+        }
+    }
+    const float cs = cosf(phase), sn = sinf(phase);
+    const bool even = (lane & 1) == 0;
+    for (int part = 0; part < 2; ++part) {
+        const float * gamma = part == 0 ? q_gamma : k_gamma;
+        T * dst = (part == 0 ? q : k) + row * C;
+        for (int h = 0; h < heads; ++h) {
+            float val = load_f32(src + part * C + h * 64 + lane);
+            if (gamma) {
+                const float sq = wave_sum(val * val);
+                const float inv = 1.0f / fmaxf(sqrtf(sq), 1e-12f);
+                val = val * inv * 8.0f * gamma[h * 64 + lane];  // sqrt(64) = 8
+            }
+            if (coords) {
+                const float other = __shfl_xor(val, 1, 64);
+                // even lane: e*cos - o*sin; odd lane: e*sin + o*cos
+                val = even ? (val * cs - other * sn) : (other * sn + val * cs);
+            }
+            store_f32(dst + h * 64 + lane, val);
+        }
+    }
+    T * vd = v + row * C;
+    for (int c = lane; c < C; c += 64) vd[c] = src[2 * C + c];
+}
+
+template <typename T>
+__global__ void split_copy_kernel(const T * __restrict__ qkv, int64_t rows, int C, int part,
+                                  T * __restrict__ out) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows * C;
+         i += stride) {
+        const int64_t r = i / C;
+        out[i] = qkv[r * 3 * C + part * C + (i - r * C)];
+    }
+}
+
+template <typename T>
+__global__ void activation_kernel(T * __restrict__ x, int64_t count, int act) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride) {
+        const float v = load_f32(x + i);
+        store_f32(x + i, act == PXS_ACT_GELU_TANH ? gelu_tanh_f(v) : silu_f(v));
+    }
+}
+
+int check_dtype(int dtype) { return dtype == PXS_F32 || dtype == PXS_BF16; }
+
+template <typename TX, typename TY, bool kMod>
+void launch_ln(const void * x, int64_t rows, int channels, float eps, const float * gamma,
+               const float * beta, const int32_t * coords, const float * bm, const float * tm,
+               int off, void * y, hipStream_t s) {
+    hipLaunchKernelGGL((layer_norm_kernel<TX, TY, kMod>), dim3(grid_for(rows, kRowsPerBlock)),
+                       dim3(64 * kRowsPerBlock), 0, s, static_cast<const TX *>(x), rows, channels,
+                       eps, gamma, beta, coords, bm, tm, off, static_cast<TY *>(y));
+}
+
+template <bool kMod>
+int run_ln(int xd, const void * x, int64_t rows, int channels, float eps, const float * gamma,
+           const float * beta, const int32_t * coords, const float * bm, const float * tm, int off,
+           int yd, void * y, hipStream_t s) {
+    if (xd == PXS_F32 && yd == PXS_F32)
+        launch_ln<float, float, kMod>(x, rows, channels, eps, gamma, beta, coords, bm, tm, off, y, s);
+    else if (xd == PXS_F32 && yd == PXS_BF16)
+        launch_ln<float, uint16_t, kMod>(x, rows, channels, eps, gamma, beta, coords, bm, tm, off, y, s);
+    else if (xd == PXS_BF16 && yd == PXS_F32)
+        launch_ln<uint16_t, float, kMod>(x, rows, channels, eps, gamma, beta, coords, bm, tm, off, y, s);
+    else
+        launch_ln<uint16_t, uint16_t, kMod>(x, rows, channels, eps, gamma, beta, coords, bm, tm, off, y, s);
+    return check_launch("layer norm");
+}
+
+template <typename T>
+int run_head_op(const void * x, int64_t ld_x, int64_t rows, int heads, int head_dim,
+                const float * gamma, const int32_t * coords, const RopeTable & rope, void * y,
+                int64_t ld_y, hipStream_t s) {
+    const int64_t items = rows * heads;
+    hipLaunchKernelGGL(head_norm_rope_kernel<T>, dim3(grid_for(items, 256)), dim3(256), 0, s,
+                       static_cast<const T *>(x), ld_x, rows, heads, head_dim, gamma, coords, rope,
+                       static_cast<T *>(y), ld_y);
+    return check_launch("head norm/rope");
+}
+
+} // namespace
+} // namespace pxs
+
+using namespace pxs;
+
+extern "C" {
+
+int pxs_layer_norm(int x_dtype, const void * x, int64_t rows, int channels, float eps,
+                   const float * gamma, const float * beta, int y_dtype, void * y, void * stream) {
+    PXS_CHECK(check_dtype(x_dtype) && check_dtype(y_dtype), PXS_ERR_ARG, "pxs_layer_norm: bad dtype");
+    PXS_CHECK(rows >= 0 && channels > 0, PXS_ERR_ARG, "pxs_layer_norm: bad shape");
+    PXS_CHECK(eps > 0.0f && std::isfinite(eps), PXS_ERR_ARG,
+              "sparse layer norm epsilon must be finite and positive");
+    PXS_CHECK((gamma == nullptr) == (beta == nullptr), PXS_ERR_ARG,
+              "sparse layer norm affine parameters must be both null or non-null");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x && y, PXS_ERR_ARG, "pxs_layer_norm: null pointer");
+    return run_ln<false>(x_dtype, x, rows, channels, eps, gamma, beta, nullptr, nullptr, nullptr,
+                         0, y_dtype, y, as_stream(stream));
+}
+
+int pxs_layer_norm_modulate(int x_dtype, const void * x, int64_t rows, int channels, float eps,
+                            const int32_t * coords, const float * block_mod,
+                            const float * time_mod, int mod_offset, int y_dtype, void * y,
+                            void * stream) {
+    PXS_CHECK(check_dtype(x_dtype) && check_dtype(y_dtype), PXS_ERR_ARG,
+              "pxs_layer_norm_modulate: bad dtype");
+    PXS_CHECK(rows >= 0 && channels > 0 && mod_offset >= 0, PXS_ERR_ARG,
+              "pxs_layer_norm_modulate: bad shape");
+    PXS_CHECK(eps > 0.0f && std::isfinite(eps), PXS_ERR_ARG,
+              "sparse layer norm epsilon must be finite and positive");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x && y && coords && block_mod && time_mod, PXS_ERR_ARG,
+              "pxs_layer_norm_modulate: null pointer");
+    return run_ln<true>(x_dtype, x, rows, channels, eps, nullptr, nullptr, coords, block_mod,
+                        time_mod, mod_offset, y_dtype, y, as_stream(stream));
+}
+
+int pxs_mh_rms_norm(int dtype, const void * x, int64_t ld_x, int64_t rows, int heads,
+                    int head_dim, const float * gamma, void * y, int64_t ld_y, void * stream) {
+    PXS_CHECK(check_dtype(dtype), PXS_ERR_ARG, "pxs_mh_rms_norm: bad dtype");
+    PXS_CHECK(rows >= 0 && heads > 0 && head_dim > 0 && ld_x >= heads * head_dim &&
+                  ld_y >= heads * head_dim,
+              PXS_ERR_ARG, "sparse RMS norm head dimensions are invalid");
+    PXS_CHECK(gamma, PXS_ERR_ARG, "sparse RMS norm gamma pointer is null");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x && y, PXS_ERR_ARG, "pxs_mh_rms_norm: null pointer");
+    RopeTable none{};
+    return dtype == PXS_F32
+               ? run_head_op<float>(x, ld_x, rows, heads, head_dim, gamma, nullptr, none, y, ld_y,
+                                    as_stream(stream))
+               : run_head_op<uint16_t>(x, ld_x, rows, heads, head_dim, gamma, nullptr, none, y,
+                                       ld_y, as_stream(stream));
+}
+
+int pxs_rope(int dtype, const int32_t * coords, const void * x, int64_t ld_x, int64_t rows,
+             int heads, int head_dim, float freq_min, float freq_base, void * y, int64_t ld_y,
+             void * stream) {
+    PXS_CHECK(check_dtype(dtype), PXS_ERR_ARG, "pxs_rope: bad dtype");
+    PXS_CHECK(rows >= 0 && heads > 0 && head_dim > 0 && head_dim % 2 == 0 &&
+                  ld_x >= heads * head_dim && ld_y >= heads * head_dim,
+              PXS_ERR_ARG, "sparse RoPE head dimensions are invalid");
+    PXS_CHECK(freq_min > 0.0f && std::isfinite(freq_min) && freq_base > 0.0f &&
+                  std::isfinite(freq_base),
+              PXS_ERR_ARG, "sparse RoPE frequencies must be finite and positive");
+    PXS_CHECK(head_dim / 2 / 3 <= 32, PXS_ERR_ARG, "pxs_rope: head_dim above 192 unsupported");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(coords && x && y, PXS_ERR_ARG, "pxs_rope: null pointer");
+    const RopeTable t = make_rope_table(head_dim, freq_min, freq_base);
+    return dtype == PXS_F32
+               ? run_head_op<float>(x, ld_x, rows, heads, head_dim, nullptr, coords, t, y, ld_y,
+                                    as_stream(stream))
+               : run_head_op<uint16_t>(x, ld_x, rows, heads, head_dim, nullptr, coords, t, y,
+                                       ld_y, as_stream(stream));
+}
+
+int pxs_qkv_prepare(int dtype, const void * qkv, int64_t rows, int heads, int head_dim,
+                    const float * q_gamma, const float * k_gamma, const int32_t * coords,
+                    float freq_min, float freq_base, void * q, void * k, void * v,
+                    void * stream) {
+    PXS_CHECK(check_dtype(dtype), PXS_ERR_ARG, "pxs_qkv_prepare: bad dtype");
+    PXS_CHECK(rows >= 0 && heads > 0 && head_dim > 0 && head_dim % 2 == 0, PXS_ERR_ARG,
+              "pxs_qkv_prepare: bad shape");
+    PXS_CHECK((q_gamma == nullptr) == (k_gamma == nullptr), PXS_ERR_ARG,
+              "pxs_qkv_prepare: q_gamma and k_gamma must be both set or both null");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(qkv && q && k && v, PXS_ERR_ARG, "pxs_qkv_prepare: null pointer");
+    hipStream_t s = as_stream(stream);
+    RopeTable t{};
+    if (coords) {
+        PXS_CHECK(freq_min > 0.0f && freq_base > 0.0f, PXS_ERR_ARG,
+                  "sparse RoPE frequencies must be finite and positive");
+        t = make_rope_table(head_dim, freq_min, freq_base);
+    }
+    const int C = heads * head_dim;
+    if (head_dim == 64) {
+        if (dtype == PXS_F32) {
+            hipLaunchKernelGGL(qkv_prepare64_kernel<float>, dim3(grid_for(rows, kRowsPerBlock)),
+                               dim3(64 * kRowsPerBlock), 0, s, static_cast<const float *>(qkv),
+                               rows, heads, q_gamma, k_gamma, coords, t, static_cast<float *>(q),
+                               static_cast<float *>(k), static_cast<float *>(v));
+        } else {
+            hipLaunchKernelGGL(qkv_prepare64_kernel<uint16_t>, dim3(grid_for(rows, kRowsPerBlock)),
+                               dim3(64 * kRowsPerBlock), 0, s, static_cast<const uint16_t *>(qkv),
+                               rows, heads, q_gamma, k_gamma, coords, t,
+                               static_cast<uint16_t *>(q), static_cast<uint16_t *>(k),
+                               static_cast<uint16_t *>(v));
+        }
+        return check_launch("pxs_qkv_prepare");
+    }
+    // Generic head_dim: per-(row, head) kernels reading the interleaved qkv.
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((rows * C + 255) / 256, 16384));
+    int rc;
+    if (dtype == PXS_F32) {
+        rc = run_head_op<float>(qkv, 3 * C, rows, heads, head_dim, q_gamma, coords, t, q, C, s);
+        if (!rc) rc = run_head_op<float>(static_cast<const float *>(qkv) + C, 3 * C, rows, heads,
+                                         head_dim, k_gamma, coords, t, k, C, s);
+        if (!rc) hipLaunchKernelGGL(split_copy_kernel<float>, dim3(blocks), dim3(256), 0, s,
+                                    static_cast<const float *>(qkv), rows, C, 2,
+                                    static_cast<float *>(v));
+    } else {
+        rc = run_head_op<uint16_t>(qkv, 3 * C, rows, heads, head_dim, q_gamma, coords, t, q, C, s);
+        if (!rc) rc = run_head_op<uint16_t>(static_cast<const uint16_t *>(qkv) + C, 3 * C, rows,
+                                            heads, head_dim, k_gamma, coords, t, k, C, s);
+        if (!rc) hipLaunchKernelGGL(split_copy_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s,
+                                    static_cast<const uint16_t *>(qkv), rows, C, 2,
+                                    static_cast<uint16_t *>(v));
+    }
+    return rc ? rc : check_launch("pxs_qkv_prepare");
+}
+
+int pxs_activation(int dtype, void * x, int64_t count, int act, void * stream) {
+    PXS_CHECK(check_dtype(dtype), PXS_ERR_ARG, "pxs_activation: bad dtype");
+    PXS_CHECK(act == PXS_ACT_GELU_TANH || act == PXS_ACT_SILU || act == PXS_ACT_NONE, PXS_ERR_ARG,
+              "pxs_activation: bad activation");
+    if (count <= 0 || act == PXS_ACT_NONE) return PXS_OK;
+    PXS_CHECK(x, PXS_ERR_ARG, "pxs_activation: null pointer");
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
+    if (dtype == PXS_F32) {
+        hipLaunchKernelGGL(activation_kernel<float>, dim3(blocks), dim3(256), 0, as_stream(stream),
+                           static_cast<float *>(x), count, act);
+    } else {
+        hipLaunchKernelGGL(activation_kernel<uint16_t>, dim3(blocks), dim3(256), 0,
+                           as_stream(stream), static_cast<uint16_t *>(x), count, act);
+    }
+    return check_launch("pxs_activation");
+}
+
+} // extern "C"

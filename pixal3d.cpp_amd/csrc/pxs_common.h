@@ -1,0 +1,99 @@
+// Shared device/host helpers for the pxs HIP library (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "pxs.h"
+
+namespace pxs {
+
+// ---- error reporting (thread-local last error, see pxs_last_error) ---------
+void set_error(const std::string & message);
+int fail(int code, const std::string & message);
+int check_hip(hipError_t status, const char * what);
+int check_launch(const char * what);
+
+#define PXS_CHECK(expr, code, msg)            \
+    do {                                      \
+        if (!(expr)) return ::pxs::fail((code), (msg)); \
+    } while (0)
+
+inline hipStream_t as_stream(void * s) { return static_cast<hipStream_t>(s); }
+
+inline unsigned grid_for(int64_t items, int per_block) {
+    return static_cast<unsigned>((items + per_block - 1) / per_block);
+}
+
+// ---- bf16 storage ------------------------------------------------------------
+// bf16 values live in HBM as raw uint16_t bit patterns; device code converts
+// with the hardware round-to-nearest-even conversion.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t bits) {
+    return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) {
+    __bf16 b = static_cast<__bf16>(v);
+    return __builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2 v;
+    v[0] = static_cast<__bf16>(lo);
+    v[1] = static_cast<__bf16>(hi);
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Element load/store helpers templated on storage type (float or uint16_t=bf16).
+template <typename T> __device__ __forceinline__ float load_f32(const T * p);
+template <> __device__ __forceinline__ float load_f32<float>(const float * p) { return *p; }
+template <> __device__ __forceinline__ float load_f32<uint16_t>(const uint16_t * p) {
+    return bf16_to_f32(*p);
+}
+template <typename T> __device__ __forceinline__ void store_f32(T * p, float v);
+template <> __device__ __forceinline__ void store_f32<float>(float * p, float v) { *p = v; }
+template <> __device__ __forceinline__ void store_f32<uint16_t>(uint16_t * p, float v) {
+    *p = f32_to_bf16(v);
+}
+
+// ---- math helpers ------------------------------------------------------------
+__device__ __forceinline__ float gelu_tanh_f(float v) {
+    const float k = 0.7978845608028654f;
+    const float cubic = v * v * v;
+    return 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * cubic)));
+}
+
+__device__ __forceinline__ float silu_f(float v) { return v * (1.0f / (1.0f + expf(-v))); }
+
+// Voxel key packing: (batch, x, y, z) -> 16 bits each.  Lexicographic order
+// of (b, x, y, z) equals numeric order of the key.  All-ones is the empty
+// slot marker; it is unreachable because batch and spatial extents are
+// limited to PXS_MAX_EXTENT (< 0xFFFF).
+__host__ __device__ __forceinline__ uint64_t voxel_key(int32_t b, int32_t x, int32_t y, int32_t z) {
+    return (static_cast<uint64_t>(static_cast<uint32_t>(b) & 0xFFFFu) << 48) |
+           (static_cast<uint64_t>(static_cast<uint32_t>(x) & 0xFFFFu) << 32) |
+           (static_cast<uint64_t>(static_cast<uint32_t>(y) & 0xFFFFu) << 16) |
+           static_cast<uint64_t>(static_cast<uint32_t>(z) & 0xFFFFu);
+}
+
+constexpr uint64_t kEmptyKey = ~0ull;
+
+__device__ __forceinline__ uint64_t mix64(uint64_t k) {
+    // MurmurHash3 fmix64 finalizer.
+    k ^= k >> 33;
+    k *= 0xff51afd7ed558ccdull;
+    k ^= k >> 33;
+    k *= 0xc4ceb9fe1a85ec53ull;
+    k ^= k >> 33;
+    return k;
+}
+
+} // namespace pxs

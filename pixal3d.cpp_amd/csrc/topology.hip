@@ -1,0 +1,668 @@
+// Integer/topology kernels: voxel hash, validation, neighbor maps, pair lists,
+// stride-2 topology, window partition, cu_seqlens, channel-to-spatial.
+//
+// All of these are HBM/latency-bound integer work; they are written for
+// coalesced row-parallel access (one thread per voxel row, offset-major
+// outputs so a wavefront writes 64 consecutive entries of one offset).
+
+#include "pxs_common.h"
+#include "scan.h"
+
+#include <climits>
+
+namespace pxs {
+namespace {
+
+constexpr int kThreads = 256;
+
+int64_t hash_capacity(int64_t n) {
+    int64_t cap = 64;
+    while (cap < 2 * n) cap <<= 1;
+    return cap;
+}
+
+struct HashView {
+    uint64_t * keys;
+    int32_t * vals;
+    uint64_t mask;
+};
+
+HashView hash_view(void * table, int64_t n) {
+    const int64_t cap = hash_capacity(n);
+    HashView h;
+    h.keys = static_cast<uint64_t *>(table);
+    h.vals = reinterpret_cast<int32_t *>(h.keys + cap);
+    h.mask = static_cast<uint64_t>(cap - 1);
+    return h;
+}
+
+__device__ __forceinline__ int32_t hash_find(const uint64_t * __restrict__ keys,
+                                             const int32_t * __restrict__ vals, uint64_t mask,
+                                             uint64_t key) {
+    uint64_t slot = mix64(key) & mask;
+    for (uint64_t probe = 0; probe <= mask; ++probe) {
+        const uint64_t k = keys[slot];
+        if (k == key) return vals[slot];
+        if (k == kEmptyKey) return -1;
+        slot = (slot + 1) & mask;
+    }
+    return -1;
+}
+
+__global__ void hash_init_kernel(uint64_t * keys, int32_t * vals, int64_t cap) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < cap;
+         i += stride) {
+        keys[i] = kEmptyKey;
+        vals[i] = INT_MAX;
+    }
+}
+
+// Lock-free insert: claim a slot with a 64-bit CAS (or find the key already
+// there), then keep the smallest inserting row with atomicMin.  The table has
+// at least 2n slots, so every probe sequence meets an empty slot.
+__global__ void hash_insert_kernel(const int4 * __restrict__ coords, int64_t n,
+                                   uint64_t * keys, int32_t * vals, uint64_t mask) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    const uint64_t key = voxel_key(c.x, c.y, c.z, c.w);
+    uint64_t slot = mix64(key) & mask;
+    for (uint64_t probe = 0; probe <= mask; ++probe) {
+        const unsigned long long prev = atomicCAS(
+            reinterpret_cast<unsigned long long *>(keys + slot),
+            static_cast<unsigned long long>(kEmptyKey), static_cast<unsigned long long>(key));
+        if (prev == kEmptyKey || prev == key) {
+            atomicMin(vals + slot, static_cast<int32_t>(p));
+            return;
+        }
+        slot = (slot + 1) & mask;
+    }
+}
+
+__global__ void status_init_kernel(int64_t * status) { *status = LLONG_MAX; }
+
+// Row checks in the reference's order at one row: outside shape (4),
+// duplicate (5: a smaller row owns the key), not contiguous by batch (6).
+__global__ void validate_coords_kernel(const int4 * __restrict__ coords, int64_t n,
+                                       int batch_size, int sx, int sy, int sz,
+                                       const uint64_t * __restrict__ keys,
+                                       const int32_t * __restrict__ vals, uint64_t mask,
+                                       int64_t * status) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    int code = 0;
+    if (c.x < 0 || c.x >= batch_size || c.y < 0 || c.y >= sx || c.z < 0 || c.z >= sy ||
+        c.w < 0 || c.w >= sz) {
+        code = 4;
+    } else if (hash_find(keys, vals, mask, voxel_key(c.x, c.y, c.z, c.w)) !=
+               static_cast<int32_t>(p)) {
+        code = 5;
+    } else if (p > 0 && coords[p - 1].x > c.x) {
+        code = 6;
+    }
+    if (code) {
+        atomicMin(reinterpret_cast<unsigned long long *>(status),
+                  static_cast<unsigned long long>(p * 8 + code));
+    }
+}
+
+template <typename T>
+__global__ void validate_feats_kernel(const T * __restrict__ feats, int64_t count, int channels,
+                                      int64_t * status) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride) {
+        const float v = load_f32(feats + i);
+        if (!isfinite(v)) {
+            atomicMin(reinterpret_cast<unsigned long long *>(status),
+                      static_cast<unsigned long long>((i / channels) * 8 + 7));
+        }
+    }
+}
+
+// One thread per row, 27 probes; writes offset-major so each offset's
+// entries of a wavefront are contiguous.
+__global__ void __launch_bounds__(kThreads)
+neighbor_map_kernel(const int4 * __restrict__ coords, int64_t n,
+                    const uint64_t * __restrict__ keys, const int32_t * __restrict__ vals,
+                    uint64_t mask, int32_t * __restrict__ nbr, uint32_t * __restrict__ masks) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    uint32_t present = 0;
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const int x = c.y + k / 9 - 1;
+        const int y = c.z + (k / 3) % 3 - 1;
+        const int z = c.w + k % 3 - 1;
+        int32_t row = -1;
+        if (k == 13) {
+            row = static_cast<int32_t>(p);
+        } else if (x >= 0 && y >= 0 && z >= 0) {
+            row = hash_find(keys, vals, mask, voxel_key(c.x, x, y, z));
+        }
+        if (row >= 0) present |= 1u << k;
+        nbr[static_cast<int64_t>(k) * n + p] = row >= 0 ? row : static_cast<int32_t>(n);
+    }
+    if (masks) masks[p] = present;
+}
+
+// Pair lists: counts per (offset, block of kThreads rows).
+__global__ void __launch_bounds__(kThreads)
+pair_count_kernel(const int32_t * __restrict__ nbr, int64_t n, int32_t * __restrict__ counts,
+                  int64_t blocks) {
+    __shared__ int32_t wave_counts[27][kThreads / 64];
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int k = 0; k < 27; ++k) {
+        const bool present = p < n && nbr[static_cast<int64_t>(k) * n + p] != n;
+        const uint64_t ballot = __ballot(present);
+        if (lane == 0) wave_counts[k][wave] = __popcll(ballot);
+    }
+    __syncthreads();
+    if (threadIdx.x < 27) {
+        int32_t s = 0;
+        for (int w = 0; w < kThreads / 64; ++w) s += wave_counts[threadIdx.x][w];
+        counts[static_cast<int64_t>(threadIdx.x) * blocks + blockIdx.x] = s;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+pair_emit_kernel(const int32_t * __restrict__ nbr, int64_t n, const int64_t * __restrict__ base,
+                 int64_t blocks, int32_t * __restrict__ pair_in, int32_t * __restrict__ pair_out) {
+    __shared__ int32_t wave_counts[27][kThreads / 64];
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int32_t in_row[27];
+    uint64_t ballots[27];
+    for (int k = 0; k < 27; ++k) {
+        in_row[k] = p < n ? nbr[static_cast<int64_t>(k) * n + p] : static_cast<int32_t>(n);
+        ballots[k] = __ballot(in_row[k] != n);
+        if (lane == 0) wave_counts[k][wave] = __popcll(ballots[k]);
+    }
+    __syncthreads();
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int k = 0; k < 27; ++k) {
+        if (in_row[k] == n) continue;
+        int64_t pos = base[static_cast<int64_t>(k) * blocks + blockIdx.x];
+        for (int w = 0; w < wave; ++w) pos += wave_counts[k][w];
+        pos += __popcll(ballots[k] & below);
+        pair_in[pos] = in_row[k];
+        pair_out[pos] = static_cast<int32_t>(p);
+    }
+}
+
+__global__ void pair_offsets_kernel(const int64_t * __restrict__ base, int64_t blocks,
+                                    const int64_t * __restrict__ total, int64_t * offsets28) {
+    const int k = threadIdx.x;
+    if (k < 27) offsets28[k] = base[static_cast<int64_t>(k) * blocks];
+    if (k == 27) offsets28[27] = *total;
+}
+
+// ---- stride-2 topology via an occupancy bitmap over the coarse grid -------
+// The dense linearisation ((b*cx + x)*cy + y)*cz + z is lexicographic, so a
+// popcount prefix over the bitmap ranks occupied coarse cells in exactly the
+// order the reference sorts them.
+__global__ void coarse_mark_kernel(const int4 * __restrict__ coords, int64_t n, int cx, int cy,
+                                   int cz, uint32_t * __restrict__ bitmap) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    const int64_t cell = ((static_cast<int64_t>(c.x) * cx + (c.y >> 1)) * cy + (c.z >> 1)) * cz +
+                         (c.w >> 1);
+    atomicOr(bitmap + (cell >> 5), 1u << (cell & 31));
+}
+
+__global__ void coarse_emit_kernel(const int4 * __restrict__ coords, int64_t n, int cx, int cy,
+                                   int cz, const uint32_t * __restrict__ bitmap,
+                                   const int64_t * __restrict__ word_prefix,
+                                   int4 * __restrict__ out_coords, int32_t * __restrict__ child_map) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    const int64_t cell = ((static_cast<int64_t>(c.x) * cx + (c.y >> 1)) * cy + (c.z >> 1)) * cz +
+                         (c.w >> 1);
+    const int64_t w = cell >> 5;
+    const uint32_t bit = static_cast<uint32_t>(cell & 31);
+    const int64_t rank = word_prefix[w] + __popc(bitmap[w] & ((1u << bit) - 1u));
+    const int child = (c.y & 1) + 2 * (c.z & 1) + 4 * (c.w & 1);
+    child_map[static_cast<int64_t>(child) * n + rank] = static_cast<int32_t>(p);
+    // Every child of the cell writes the same coarse coordinate.
+    out_coords[rank] = make_int4(c.x, c.y >> 1, c.z >> 1, c.w >> 1);
+}
+
+// ---- window partition (counting sort by window id, stable per window) -----
+struct WindowGrid {
+    int64_t nx, ny, nz;
+};
+
+__device__ __forceinline__ int64_t window_id(int4 c, int window, int shift, WindowGrid g) {
+    const int64_t wx = (c.y + shift) / window;
+    const int64_t wy = (c.z + shift) / window;
+    const int64_t wz = (c.w + shift) / window;
+    return ((static_cast<int64_t>(c.x) * g.nx + wx) * g.ny + wy) * g.nz + wz;
+}
+
+__global__ void window_count_kernel(const int4 * __restrict__ coords, int64_t n, int window,
+                                    int shift, WindowGrid g, int32_t * __restrict__ counts,
+                                    int32_t * __restrict__ slot) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int64_t wid = window_id(coords[p], window, shift, g);
+    slot[p] = atomicAdd(counts + wid, 1);
+}
+
+__global__ void window_flags_kernel(const int32_t * __restrict__ counts, int64_t windows,
+                                    int32_t * __restrict__ flags) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < windows) flags[i] = counts[i] > 0 ? 1 : 0;
+}
+
+__global__ void window_cu_kernel(const int32_t * __restrict__ counts, int64_t windows,
+                                 const int64_t * __restrict__ start,
+                                 const int64_t * __restrict__ rank, const int64_t * __restrict__ nwin,
+                                 int64_t n, int64_t * __restrict__ cu) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < windows && counts[i] > 0) cu[rank[i]] = start[i];
+    if (i == 0) cu[*nwin] = n;
+}
+
+__global__ void window_place_kernel(const int4 * __restrict__ coords, int64_t n, int window,
+                                    int shift, WindowGrid g, const int64_t * __restrict__ start,
+                                    const int32_t * __restrict__ slot, int32_t * __restrict__ tmp) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int64_t wid = window_id(coords[p], window, shift, g);
+    tmp[start[wid] + slot[p]] = static_cast<int32_t>(p);
+}
+
+// One workgroup per window: rank each member by counting smaller row
+// indices (rows are unique), giving the stable order.  Windows hold at most
+// window^3 rows; larger segments are ranked in LDS chunks.
+__global__ void __launch_bounds__(kThreads)
+window_sort_kernel(const int32_t * __restrict__ tmp, const int64_t * __restrict__ cu,
+                   const int64_t * __restrict__ nwin, int32_t * __restrict__ fwd,
+                   int32_t * __restrict__ bwd) {
+    __shared__ int32_t members[1024];
+    const int64_t w = blockIdx.x;
+    if (w >= *nwin) return;
+    const int64_t begin = cu[w], end = cu[w + 1];
+    const int64_t len = end - begin;
+    for (int64_t i0 = 0; i0 < len; i0 += kThreads) {
+        const int64_t i = i0 + threadIdx.x;
+        const int32_t mine = i < len ? tmp[begin + i] : INT_MAX;
+        int64_t rank = 0;
+        for (int64_t c0 = 0; c0 < len; c0 += 1024) {
+            __syncthreads();
+            for (int64_t j = threadIdx.x; j < 1024 && c0 + j < len; j += kThreads) {
+                members[j] = tmp[begin + c0 + j];
+            }
+            __syncthreads();
+            const int64_t cnt = min<int64_t>(1024, len - c0);
+            for (int64_t j = 0; j < cnt; ++j) rank += members[j] < mine ? 1 : 0;
+        }
+        if (i < len) {
+            fwd[begin + rank] = mine;
+            bwd[mine] = static_cast<int32_t>(begin + rank);
+        }
+    }
+}
+
+// ---- per-batch cu_seqlens ----------------------------------------------------
+__global__ void batch_cu_kernel(const int4 * __restrict__ coords, int64_t n, int batch_size,
+                                int64_t * __restrict__ cu) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (n == 0) {
+        if (p <= batch_size) cu[p] = 0;
+        return;
+    }
+    if (p >= n) return;
+    const int b = coords[p].x;
+    const int prev = p == 0 ? -1 : coords[p - 1].x;
+    for (int bb = prev + 1; bb <= b && bb <= batch_size; ++bb) cu[bb] = p;
+    if (p == n - 1) {
+        for (int bb = b + 1; bb <= batch_size; ++bb) cu[bb] = n;
+    }
+}
+
+// ---- channel to spatial (factor 2) --------------------------------------------
+__global__ void c2s_count_kernel(const float * __restrict__ sub, int64_t n,
+                                 int32_t * __restrict__ counts) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    int c = 0;
+    for (int j = 0; j < 8; ++j) c += sub[p * 8 + j] > 0.0f ? 1 : 0;
+    counts[p] = c;
+}
+
+// One thread per (parent, child); the channel copy is done by the feature
+// kernel below with 16-byte vectors.
+__global__ void c2s_coords_kernel(const int4 * __restrict__ coords, int64_t n,
+                                  const float * __restrict__ sub,
+                                  const int64_t * __restrict__ prefix,
+                                  int4 * __restrict__ out_coords, int64_t * __restrict__ src_of) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n * 8) return;
+    const int64_t p = t >> 3;
+    const int child = static_cast<int>(t & 7);
+    int64_t dst;
+    if (sub) {
+        if (!(sub[p * 8 + child] > 0.0f)) return;
+        int before = 0;
+        for (int j = 0; j < child; ++j) before += sub[p * 8 + j] > 0.0f ? 1 : 0;
+        dst = prefix[p] + before;
+    } else {
+        dst = t;
+    }
+    const int4 c = coords[p];
+    out_coords[dst] = make_int4(c.x, 2 * c.y + (child & 1), 2 * c.z + ((child >> 1) & 1),
+                                2 * c.w + (child >> 2));
+    src_of[dst] = t;  // source (parent * 8 + child)
+}
+
+template <typename T>
+__global__ void c2s_feats_kernel(const T * __restrict__ x, int channels, const int64_t * __restrict__ src_of,
+                                 const int64_t * __restrict__ m_dev, int64_t m_max,
+                                 T * __restrict__ y) {
+    // channels = 8 * c_out; the child slice of parent p is channels / 8 wide.
+    const int c_out = channels / 8;
+    const int64_t m = m_dev ? *m_dev : m_max;
+    const int64_t total = m * c_out;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += stride) {
+        const int64_t r = i / c_out;
+        const int ch = static_cast<int>(i - r * c_out);
+        const int64_t s = src_of[r];
+        y[i] = x[(s >> 3) * channels + (s & 7) * c_out + ch];
+    }
+}
+
+} // namespace
+
+} // namespace pxs
+
+using namespace pxs;
+
+extern "C" {
+
+size_t pxs_voxel_hash_bytes(int64_t n) {
+    const int64_t cap = hash_capacity(n);
+    return static_cast<size_t>(cap) * (sizeof(uint64_t) + sizeof(int32_t));
+}
+
+int pxs_voxel_hash_build(const int32_t * coords, int64_t n, void * table, void * stream) {
+    PXS_CHECK(n >= 0, PXS_ERR_ARG, "pxs_voxel_hash_build: negative row count");
+    PXS_CHECK(n <= INT_MAX, PXS_ERR_ARG, "pxs_voxel_hash_build: row count exceeds int32");
+    PXS_CHECK(table != nullptr, PXS_ERR_ARG, "pxs_voxel_hash_build: null table");
+    PXS_CHECK(n == 0 || coords != nullptr, PXS_ERR_ARG, "pxs_voxel_hash_build: null coords");
+    const HashView h = hash_view(table, n);
+    const int64_t cap = static_cast<int64_t>(h.mask) + 1;
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(hash_init_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((cap + 255) / 256, 8192))),
+                       dim3(256), 0, s, h.keys, h.vals, cap);
+    if (n > 0) {
+        hipLaunchKernelGGL(hash_insert_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                           reinterpret_cast<const int4 *>(coords), n, h.keys, h.vals, h.mask);
+    }
+    return check_launch("pxs_voxel_hash_build");
+}
+
+int pxs_sparse_validate(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                        int sz, int dtype, const void * feats, int channels,
+                        const void * table, int64_t * status, void * stream) {
+    PXS_CHECK(status != nullptr, PXS_ERR_ARG, "pxs_sparse_validate: null status");
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_sparse_validate: bad row count");
+    PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_sparse_validate: bad dtype");
+    PXS_CHECK(batch_size <= PXS_MAX_EXTENT && sx <= PXS_MAX_EXTENT && sy <= PXS_MAX_EXTENT &&
+                  sz <= PXS_MAX_EXTENT,
+              PXS_ERR_ARG, "pxs_sparse_validate: extent exceeds PXS_MAX_EXTENT");
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(status_init_kernel, dim3(1), dim3(1), 0, s, status);
+    if (n > 0) {
+        PXS_CHECK(coords && table, PXS_ERR_ARG, "pxs_sparse_validate: null coords or table");
+        const HashView h = hash_view(const_cast<void *>(table), n);
+        hipLaunchKernelGGL(validate_coords_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+                           s, reinterpret_cast<const int4 *>(coords), n, batch_size, sx, sy, sz,
+                           h.keys, h.vals, h.mask, status);
+        if (feats && channels > 0) {
+            const int64_t count = n * channels;
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 8192));
+            if (dtype == PXS_F32) {
+                hipLaunchKernelGGL(validate_feats_kernel<float>, dim3(blocks), dim3(256), 0, s,
+                                   static_cast<const float *>(feats), count, channels, status);
+            } else {
+                hipLaunchKernelGGL(validate_feats_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s,
+                                   static_cast<const uint16_t *>(feats), count, channels, status);
+            }
+        }
+    }
+    return check_launch("pxs_sparse_validate");
+}
+
+const char * pxs_validation_message(int code) {
+    switch (code) {
+    case 1: return "invalid sparse tensor shape";
+    case 2: return "sparse coordinates must have four columns";
+    case 3: return "sparse feature count does not match coordinates";
+    case 4: return "sparse coordinate is outside its shape";
+    case 5: return "sparse coordinates contain a duplicate point";
+    case 6: return "sparse coordinates must be contiguous by batch";
+    case 7: return "sparse features contain a non-finite value";
+    default: return "";
+    }
+}
+
+int pxs_neighbor_map_k3(const int32_t * coords, int64_t n, const void * table, int32_t * nbr,
+                        uint32_t * masks, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_neighbor_map_k3: bad row count");
+    if (n == 0) return PXS_OK;
+    PXS_CHECK(coords && table && nbr, PXS_ERR_ARG, "pxs_neighbor_map_k3: null pointer");
+    const HashView h = hash_view(const_cast<void *>(table), n);
+    hipLaunchKernelGGL(neighbor_map_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+                       as_stream(stream), reinterpret_cast<const int4 *>(coords), n, h.keys,
+                       h.vals, h.mask, nbr, masks);
+    return check_launch("pxs_neighbor_map_k3");
+}
+
+size_t pxs_neighbor_pairs_workspace_bytes(int64_t n) {
+    const int64_t blocks = std::max<int64_t>((n + kThreads - 1) / kThreads, 1);
+    const int64_t count = 27 * blocks;
+    return static_cast<size_t>(count) * (sizeof(int32_t) + sizeof(int64_t)) + sizeof(int64_t) +
+           scan_workspace_bytes(count) + 64;
+}
+
+int pxs_neighbor_pairs(const int32_t * nbr, int64_t n, int32_t * pair_in, int32_t * pair_out,
+                       int64_t * offsets28, void * workspace, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_neighbor_pairs: bad row count");
+    PXS_CHECK(offsets28 && workspace, PXS_ERR_ARG, "pxs_neighbor_pairs: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) return fill_i64(offsets28, 28, 0, s);
+    PXS_CHECK(nbr && pair_in && pair_out, PXS_ERR_ARG, "pxs_neighbor_pairs: null pointer");
+    const int64_t blocks = (n + kThreads - 1) / kThreads;
+    const int64_t count = 27 * blocks;
+    char * ws = static_cast<char *>(workspace);
+    int64_t * base = reinterpret_cast<int64_t *>(ws);
+    int64_t * total = base + count;
+    int32_t * counts = reinterpret_cast<int32_t *>(total + 1);
+    void * scan_ws = reinterpret_cast<char *>(counts + count) + 8;  // keep 8-byte alignment
+    scan_ws = reinterpret_cast<void *>((reinterpret_cast<uintptr_t>(scan_ws) + 7) & ~uintptr_t(7));
+    hipLaunchKernelGGL(pair_count_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s,
+                       nbr, n, counts, blocks);
+    int rc = exclusive_scan_i32(counts, base, count, total, scan_ws, s);
+    if (rc != PXS_OK) return rc;
+    hipLaunchKernelGGL(pair_emit_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s,
+                       nbr, n, base, blocks, pair_in, pair_out);
+    hipLaunchKernelGGL(pair_offsets_kernel, dim3(1), dim3(64), 0, s, base, blocks, total,
+                       offsets28);
+    return check_launch("pxs_neighbor_pairs");
+}
+
+size_t pxs_downsample_workspace_bytes(int batch_size, int sx, int sy, int sz) {
+    const int64_t cells = static_cast<int64_t>(std::max(batch_size, 1)) * ((sx + 1) / 2) *
+                          ((sy + 1) / 2) * ((sz + 1) / 2);
+    const int64_t words = (cells + 31) / 32;
+    return static_cast<size_t>(words) * (sizeof(uint32_t) + sizeof(int64_t)) +
+           scan_workspace_bytes(words) + 64;
+}
+
+int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size, int sx,
+                               int sy, int sz, int32_t * out_coords, int32_t * child_map,
+                               int64_t * m_out, void * workspace, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_downsample_s2_topology: bad row count");
+    PXS_CHECK(batch_size > 0 && sx > 0 && sy > 0 && sz > 0, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology: invalid shape");
+    PXS_CHECK(m_out && workspace, PXS_ERR_ARG, "pxs_downsample_s2_topology: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) return fill_i64(m_out, 1, 0, s);
+    PXS_CHECK(coords && out_coords && child_map, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology: null pointer");
+    const int cx = (sx + 1) / 2, cy = (sy + 1) / 2, cz = (sz + 1) / 2;
+    const int64_t cells = static_cast<int64_t>(batch_size) * cx * cy * cz;
+    const int64_t words = (cells + 31) / 32;
+    uint32_t * bitmap = static_cast<uint32_t *>(workspace);
+    int64_t * prefix = reinterpret_cast<int64_t *>(
+        (reinterpret_cast<uintptr_t>(bitmap + words) + 7) & ~uintptr_t(7));
+    void * scan_ws = prefix + words;
+    int rc = fill_u32(bitmap, words, 0u, s);
+    if (rc) return rc;
+    rc = fill_i32(child_map, 8 * n, -1, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(coarse_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const int4 *>(coords), n, cx, cy, cz, bitmap);
+    rc = exclusive_scan_popcount(bitmap, prefix, words, m_out, scan_ws, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(coarse_emit_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const int4 *>(coords), n, cx, cy, cz, bitmap, prefix,
+                       reinterpret_cast<int4 *>(out_coords), child_map);
+    return check_launch("pxs_downsample_s2_topology");
+}
+
+size_t pxs_window_partition_workspace_bytes(int batch_size, int sx, int sy, int sz, int window,
+                                            int shift, int64_t n) {
+    if (window <= 0) return 0;
+    const int64_t nx = (sx + shift + window - 1) / window;
+    const int64_t ny = (sy + shift + window - 1) / window;
+    const int64_t nz = (sz + shift + window - 1) / window;
+    const int64_t windows = static_cast<int64_t>(std::max(batch_size, 1)) * nx * ny * nz;
+    // counts + flags (int32), start + rank (int64), slot + tmp (int32 per row), scan.
+    return static_cast<size_t>(windows) * (2 * sizeof(int32_t) + 2 * sizeof(int64_t)) +
+           static_cast<size_t>(std::max<int64_t>(n, 1)) * 2 * sizeof(int32_t) + sizeof(int64_t) +
+           scan_workspace_bytes(windows) + 128;
+}
+
+int pxs_window_partition(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                         int sz, int window, int shift, int32_t * fwd, int32_t * bwd,
+                         int64_t * cu_seqlens, int64_t * nwin_out, void * workspace,
+                         void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_window_partition: bad row count");
+    PXS_CHECK(window > 0 && shift >= 0 && batch_size > 0 && sx > 0 && sy > 0 && sz > 0,
+              PXS_ERR_ARG, "pxs_window_partition: invalid window or shape");
+    PXS_CHECK(cu_seqlens && nwin_out && workspace, PXS_ERR_ARG,
+              "pxs_window_partition: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) {
+        int rc = fill_i64(nwin_out, 1, 0, s);
+        return rc ? rc : fill_i64(cu_seqlens, 1, 0, s);
+    }
+    PXS_CHECK(coords && fwd && bwd, PXS_ERR_ARG, "pxs_window_partition: null pointer");
+    WindowGrid g;
+    g.nx = (sx + shift + window - 1) / window;
+    g.ny = (sy + shift + window - 1) / window;
+    g.nz = (sz + shift + window - 1) / window;
+    const int64_t windows = static_cast<int64_t>(batch_size) * g.nx * g.ny * g.nz;
+    char * ws = static_cast<char *>(workspace);
+    int64_t * start = reinterpret_cast<int64_t *>(ws);
+    int64_t * rank = start + windows;
+    int64_t * nwin_scratch = rank + windows;
+    int32_t * counts = reinterpret_cast<int32_t *>(nwin_scratch + 1);
+    int32_t * flags = counts + windows;
+    int32_t * slot = flags + windows;
+    int32_t * tmp = slot + n;
+    void * scan_ws = reinterpret_cast<void *>(
+        (reinterpret_cast<uintptr_t>(tmp + n) + 7) & ~uintptr_t(7));
+    (void)nwin_scratch;
+    const int4 * c4 = reinterpret_cast<const int4 *>(coords);
+    int rc = fill_i32(counts, windows, 0, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(window_count_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
+                       n, window, shift, g, counts, slot);
+    rc = exclusive_scan_i32(counts, start, windows, nullptr, scan_ws, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(window_flags_kernel, dim3(grid_for(windows, kThreads)), dim3(kThreads), 0, s,
+                       counts, windows, flags);
+    rc = exclusive_scan_i32(flags, rank, windows, nwin_out, scan_ws, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(window_cu_kernel, dim3(grid_for(windows, kThreads)), dim3(kThreads), 0, s,
+                       counts, windows, start, rank, nwin_out, n, cu_seqlens);
+    hipLaunchKernelGGL(window_place_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
+                       n, window, shift, g, start, slot, tmp);
+    // At most n non-empty windows; workgroups past *nwin exit at once.
+    hipLaunchKernelGGL(window_sort_kernel, dim3(static_cast<unsigned>(n)), dim3(kThreads), 0, s,
+                       tmp, cu_seqlens, nwin_out, fwd, bwd);
+    return check_launch("pxs_window_partition");
+}
+
+int pxs_batch_cu_seqlens(const int32_t * coords, int64_t n, int batch_size, int64_t * cu,
+                         void * stream) {
+    PXS_CHECK(n >= 0 && batch_size > 0 && cu, PXS_ERR_ARG, "pxs_batch_cu_seqlens: bad argument");
+    const int64_t items = std::max<int64_t>(n, batch_size + 1);
+    hipLaunchKernelGGL(batch_cu_kernel, dim3(grid_for(items, kThreads)), dim3(kThreads), 0,
+                       as_stream(stream), reinterpret_cast<const int4 *>(coords), n, batch_size,
+                       cu);
+    return check_launch("pxs_batch_cu_seqlens");
+}
+
+size_t pxs_channel_to_spatial_workspace_bytes(int64_t n) {
+    const int64_t rows = std::max<int64_t>(n, 1);
+    return static_cast<size_t>(rows) * (sizeof(int32_t) + sizeof(int64_t)) +
+           static_cast<size_t>(rows) * 8 * sizeof(int64_t) + scan_workspace_bytes(rows) + 64;
+}
+
+int pxs_channel_to_spatial(int dtype, const int32_t * coords, int64_t n, const void * x,
+                           int channels, const float * subdivision, int32_t * out_coords,
+                           void * y, int64_t * m_out, void * workspace, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX / 8, PXS_ERR_ARG, "pxs_channel_to_spatial: bad row count");
+    PXS_CHECK(channels > 0 && channels % 8 == 0, PXS_ERR_ARG,
+              "sparse channel-to-spatial channels are not divisible by factor^3");
+    PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_channel_to_spatial: bad dtype");
+    PXS_CHECK(m_out && workspace, PXS_ERR_ARG, "pxs_channel_to_spatial: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) return fill_i64(m_out, 1, 0, s);
+    PXS_CHECK(coords && x && out_coords && y, PXS_ERR_ARG, "pxs_channel_to_spatial: null pointer");
+    char * ws = static_cast<char *>(workspace);
+    int64_t * prefix = reinterpret_cast<int64_t *>(ws);
+    int64_t * src_of = prefix + n;
+    int32_t * counts = reinterpret_cast<int32_t *>(src_of + 8 * n);
+    void * scan_ws = reinterpret_cast<void *>(
+        (reinterpret_cast<uintptr_t>(counts + n) + 7) & ~uintptr_t(7));
+    int rc;
+    if (subdivision) {
+        hipLaunchKernelGGL(c2s_count_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                           subdivision, n, counts);
+        rc = exclusive_scan_i32(counts, prefix, n, m_out, scan_ws, s);
+        if (rc) return rc;
+    } else {
+        rc = fill_i64(m_out, 1, 8 * n, s);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(c2s_coords_kernel, dim3(grid_for(8 * n, kThreads)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const int4 *>(coords), n, subdivision, prefix,
+                       reinterpret_cast<int4 *>(out_coords), src_of);
+    const int64_t max_elems = 8 * n * (channels / 8);
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((max_elems + 255) / 256, 16384));
+    if (dtype == PXS_F32) {
+        hipLaunchKernelGGL(c2s_feats_kernel<float>, dim3(blocks), dim3(256), 0, s,
+                           static_cast<const float *>(x), channels, src_of, m_out, 8 * n,
+                           static_cast<float *>(y));
+    } else {
+        hipLaunchKernelGGL(c2s_feats_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s,
+                           static_cast<const uint16_t *>(x), channels, src_of, m_out, 8 * n,
+                           static_cast<uint16_t *>(y));
+    }
+    return check_launch("pxs_channel_to_spatial");
+}
+
+} // extern "C"

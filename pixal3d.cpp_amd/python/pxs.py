@@ -1,0 +1,328 @@
+"""ctypes binding of libpxs.so (the C ABI in include/pxs.h) over torch tensors.
+
+torch supplies device memory and the current HIP stream; every computation
+runs in the HIP kernels of libpxs.so.  There is no fallback: if the library
+is missing or a call fails, a PxsError is raised.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import torch
+
+PKG = Path(__file__).resolve().parents[1]
+LIB_PATH = Path(os.environ.get("PXS_LIB", PKG / "lib" / "libpxs.so"))
+
+PXS_F32, PXS_BF16 = 0, 1
+ACT_NONE, ACT_GELU_TANH, ACT_SILU = 0, 1, 2
+
+VALIDATION_MESSAGES = {
+    4: "sparse coordinate is outside its shape",
+    5: "sparse coordinates contain a duplicate point",
+    6: "sparse coordinates must be contiguous by batch",
+    7: "sparse features contain a non-finite value",
+}
+
+
+class PxsError(RuntimeError):
+    pass
+
+
+_vp, _i64, _i32, _f = C.c_void_p, C.c_int64, C.c_int, C.c_float
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "pxs_last_error": (C.c_char_p, []),
+    "pxs_version": (_i32, []),
+    "pxs_voxel_hash_bytes": (C.c_size_t, [_i64]),
+    "pxs_voxel_hash_build": (_i32, [_vp, _i64, _vp, _vp]),
+    "pxs_sparse_validate": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp]),
+    "pxs_validation_message": (C.c_char_p, [_i32]),
+    "pxs_neighbor_map_k3": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp]),
+    "pxs_neighbor_pairs_workspace_bytes": (C.c_size_t, [_i64]),
+    "pxs_neighbor_pairs": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "pxs_subm_conv3d": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "pxs_downsample_workspace_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32]),
+    "pxs_downsample_s2_topology": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "pxs_sparse_conv3d_s2": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _vp, _vp]),
+    "pxs_downsample_mean_s2": (_i32, [_i32, _vp, _i32, _vp, _i64, _i64, _vp, _vp]),
+    "pxs_channel_to_spatial_workspace_bytes": (C.c_size_t, [_i64]),
+    "pxs_channel_to_spatial": (_i32, [_i32, _vp, _i64, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pxs_linear": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "pxs_linear_gate_residual": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
+    "pxs_layer_norm": (_i32, [_i32, _vp, _i64, _i32, _f, _vp, _vp, _i32, _vp, _vp]),
+    "pxs_layer_norm_modulate": (_i32, [_i32, _vp, _i64, _i32, _f, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "pxs_mh_rms_norm": (_i32, [_i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _i64, _vp]),
+    "pxs_rope": (_i32, [_i32, _vp, _vp, _i64, _i64, _i32, _i32, _f, _f, _vp, _i64, _vp]),
+    "pxs_qkv_prepare": (_i32, [_i32, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _f, _f, _vp, _vp, _vp, _vp]),
+    "pxs_activation": (_i32, [_i32, _vp, _i64, _i32, _vp]),
+    "pxs_attention_workspace_bytes": (C.c_size_t, [_i32]),
+    "pxs_varlen_attention": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _i64, _vp,
+                                    _i32, _i32, _f, _vp, _i64, _vp, _vp]),
+    "pxs_batch_cu_seqlens": (_i32, [_vp, _i64, _i32, _vp, _vp]),
+    "pxs_window_partition_workspace_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32, _i32, _i32, _i64]),
+    "pxs_window_partition": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                    _vp, _vp]),
+}
+
+
+def load_library(path: Path = LIB_PATH) -> C.CDLL:
+    if not Path(path).exists():
+        raise PxsError(f"{path} is not built (run __graft_entry__.build())")
+    lib = C.CDLL(str(path))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return PXS_F32
+    if t.dtype == torch.bfloat16:
+        return PXS_BF16
+    raise PxsError(f"unsupported dtype {t.dtype}")
+
+
+class Pxs:
+    """Thin wrappers: allocate outputs with torch, call the C ABI on the current stream."""
+
+    def __init__(self, path: Path = LIB_PATH):
+        self.lib = load_library(path)
+        self.path = Path(path)
+
+    # -- plumbing ---------------------------------------------------------------
+    @staticmethod
+    def stream():
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def _check(self, rc: int, what: str):
+        if rc != 0:
+            raise PxsError(f"{what}: {self.lib.pxs_last_error().decode()} (code {rc})")
+
+    @staticmethod
+    def _ws(nbytes: int, device) -> torch.Tensor:
+        return torch.empty(max(int(nbytes), 8), dtype=torch.uint8, device=device)
+
+    # -- topology -----------------------------------------------------------------
+    def hash_build(self, coords: torch.Tensor) -> torch.Tensor:
+        n = coords.shape[0]
+        table = self._ws(self.lib.pxs_voxel_hash_bytes(n), coords.device)
+        self._check(self.lib.pxs_voxel_hash_build(_ptr(coords), n, _ptr(table), self.stream()),
+                    "pxs_voxel_hash_build")
+        return table
+
+    def validate(self, coords, batch_size, shape, feats=None, table=None):
+        n = coords.shape[0]
+        table = self.hash_build(coords) if table is None else table
+        status = torch.empty(1, dtype=torch.int64, device=coords.device)
+        dt = PXS_F32 if feats is None else _dtype_code(feats)
+        ch = 0 if feats is None else feats.shape[1]
+        self._check(self.lib.pxs_sparse_validate(_ptr(coords), n, batch_size, shape[0], shape[1],
+                                                 shape[2], dt, _ptr(feats), ch, _ptr(table),
+                                                 _ptr(status), self.stream()),
+                    "pxs_sparse_validate")
+        s = int(status.item())
+        if s == (1 << 63) - 1:
+            return 0, -1
+        return s % 8, s // 8
+
+    def neighbor_map(self, coords, table=None, want_masks=True):
+        n = coords.shape[0]
+        table = self.hash_build(coords) if table is None else table
+        nbr = torch.empty((27, n), dtype=torch.int32, device=coords.device)
+        masks = torch.empty(n, dtype=torch.int32, device=coords.device) if want_masks else None
+        self._check(self.lib.pxs_neighbor_map_k3(_ptr(coords), n, _ptr(table), _ptr(nbr),
+                                                 _ptr(masks), self.stream()),
+                    "pxs_neighbor_map_k3")
+        return nbr, masks
+
+    def neighbor_pairs(self, nbr):
+        n = nbr.shape[1]
+        dev = nbr.device
+        pin = torch.empty(max(27 * n, 1), dtype=torch.int32, device=dev)
+        pout = torch.empty(max(27 * n, 1), dtype=torch.int32, device=dev)
+        offs = torch.empty(28, dtype=torch.int64, device=dev)
+        ws = self._ws(self.lib.pxs_neighbor_pairs_workspace_bytes(n), dev)
+        self._check(self.lib.pxs_neighbor_pairs(_ptr(nbr), n, _ptr(pin), _ptr(pout), _ptr(offs),
+                                                _ptr(ws), self.stream()),
+                    "pxs_neighbor_pairs")
+        total = int(offs[27].item())
+        return pin[:total], pout[:total], offs
+
+    def batch_cu_seqlens(self, coords, batch_size):
+        cu = torch.empty(batch_size + 1, dtype=torch.int64, device=coords.device)
+        self._check(self.lib.pxs_batch_cu_seqlens(_ptr(coords), coords.shape[0], batch_size,
+                                                  _ptr(cu), self.stream()),
+                    "pxs_batch_cu_seqlens")
+        return cu
+
+    def downsample_s2(self, coords, batch_size, shape):
+        n = coords.shape[0]
+        dev = coords.device
+        oc = torch.empty((max(n, 1), 4), dtype=torch.int32, device=dev)
+        child = torch.empty((8, max(n, 1)), dtype=torch.int32, device=dev)
+        m = torch.empty(1, dtype=torch.int64, device=dev)
+        ws = self._ws(self.lib.pxs_downsample_workspace_bytes(batch_size, *shape), dev)
+        self._check(self.lib.pxs_downsample_s2_topology(_ptr(coords), n, batch_size, shape[0],
+                                                        shape[1], shape[2], _ptr(oc), _ptr(child),
+                                                        _ptr(m), _ptr(ws), self.stream()),
+                    "pxs_downsample_s2_topology")
+        mm = int(m.item())
+        return oc[:mm], child, mm
+
+    def window_partition(self, coords, batch_size, shape, window, shift):
+        n = coords.shape[0]
+        dev = coords.device
+        fwd = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+        bwd = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+        cu = torch.empty(n + 1, dtype=torch.int64, device=dev)
+        nwin = torch.empty(1, dtype=torch.int64, device=dev)
+        ws = self._ws(self.lib.pxs_window_partition_workspace_bytes(batch_size, *shape, window,
+                                                                    shift, n), dev)
+        self._check(self.lib.pxs_window_partition(_ptr(coords), n, batch_size, shape[0], shape[1],
+                                                  shape[2], window, shift, _ptr(fwd), _ptr(bwd),
+                                                  _ptr(cu), _ptr(nwin), _ptr(ws), self.stream()),
+                    "pxs_window_partition")
+        nw = int(nwin.item())
+        return fwd[:n], bwd[:n], cu[: nw + 1], nw
+
+    def channel_to_spatial(self, coords, x, subdivision=None):
+        n, ch = x.shape
+        dev = x.device
+        oc = torch.empty((max(8 * n, 1), 4), dtype=torch.int32, device=dev)
+        y = torch.empty((max(8 * n, 1), ch // 8), dtype=x.dtype, device=dev)
+        m = torch.empty(1, dtype=torch.int64, device=dev)
+        ws = self._ws(self.lib.pxs_channel_to_spatial_workspace_bytes(n), dev)
+        self._check(self.lib.pxs_channel_to_spatial(_dtype_code(x), _ptr(coords), n, _ptr(x), ch,
+                                                    _ptr(subdivision), _ptr(oc), _ptr(y), _ptr(m),
+                                                    _ptr(ws), self.stream()),
+                    "pxs_channel_to_spatial")
+        mm = int(m.item())
+        return oc[:mm], y[:mm]
+
+    # -- GEMM family ----------------------------------------------------------------
+    def subm_conv3d(self, x, weight, bias, nbr, masks=None, out=None):
+        n, cin = x.shape
+        cout = weight.shape[1]
+        y = torch.empty((n, cout), dtype=x.dtype, device=x.device) if out is None else out
+        self._check(self.lib.pxs_subm_conv3d(_dtype_code(x), _ptr(x), n, cin, _ptr(weight),
+                                             _ptr(bias), cout, _ptr(nbr), _ptr(masks), _ptr(y),
+                                             self.stream()),
+                    "pxs_subm_conv3d")
+        return y
+
+    def sparse_conv3d_s2(self, x, weight, bias, child_map, m, out=None):
+        n, cin = x.shape
+        cout = weight.shape[1]
+        y = torch.empty((m, cout), dtype=x.dtype, device=x.device) if out is None else out
+        self._check(self.lib.pxs_sparse_conv3d_s2(_dtype_code(x), _ptr(x), n, cin, _ptr(weight),
+                                                  _ptr(bias), cout, _ptr(child_map),
+                                                  child_map.shape[1], m, _ptr(y), self.stream()),
+                    "pxs_sparse_conv3d_s2")
+        return y
+
+    def downsample_mean_s2(self, x, child_map, m):
+        y = torch.empty((m, x.shape[1]), dtype=x.dtype, device=x.device)
+        self._check(self.lib.pxs_downsample_mean_s2(_dtype_code(x), _ptr(x), x.shape[1],
+                                                    _ptr(child_map), child_map.shape[1], m,
+                                                    _ptr(y), self.stream()),
+                    "pxs_downsample_mean_s2")
+        return y
+
+    def linear(self, x, weight, bias=None, act=ACT_NONE, out=None):
+        rows, cin = x.shape
+        cout = weight.shape[0]
+        y = torch.empty((rows, cout), dtype=x.dtype, device=x.device) if out is None else out
+        self._check(self.lib.pxs_linear(_dtype_code(x), _ptr(x), rows, cin, _ptr(weight),
+                                        _ptr(bias), cout, act, _ptr(y), self.stream()),
+                    "pxs_linear")
+        return y
+
+    def linear_gate_residual(self, x, weight, bias, coords, block_mod, time_mod, gate_offset,
+                             residual):
+        rows, cin = x.shape
+        cout = weight.shape[0]
+        self._check(self.lib.pxs_linear_gate_residual(_dtype_code(x), _ptr(x), rows, cin,
+                                                      _ptr(weight), _ptr(bias), cout,
+                                                      _ptr(coords), _ptr(block_mod),
+                                                      _ptr(time_mod), gate_offset,
+                                                      _ptr(residual), self.stream()),
+                    "pxs_linear_gate_residual")
+        return residual
+
+    # -- row-wise ---------------------------------------------------------------------
+    def layer_norm(self, x, eps, gamma=None, beta=None, out_dtype=None):
+        out_dtype = out_dtype or x.dtype
+        y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+        self._check(self.lib.pxs_layer_norm(_dtype_code(x), _ptr(x), x.shape[0], x.shape[1], eps,
+                                            _ptr(gamma), _ptr(beta), _dtype_code(y), _ptr(y),
+                                            self.stream()),
+                    "pxs_layer_norm")
+        return y
+
+    def layer_norm_modulate(self, x, eps, coords, block_mod, time_mod, offset, out_dtype=None):
+        out_dtype = out_dtype or x.dtype
+        y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+        self._check(self.lib.pxs_layer_norm_modulate(_dtype_code(x), _ptr(x), x.shape[0],
+                                                     x.shape[1], eps, _ptr(coords),
+                                                     _ptr(block_mod), _ptr(time_mod), offset,
+                                                     _dtype_code(y), _ptr(y), self.stream()),
+                    "pxs_layer_norm_modulate")
+        return y
+
+    def mh_rms_norm(self, x, heads, head_dim, gamma):
+        y = torch.empty_like(x)
+        self._check(self.lib.pxs_mh_rms_norm(_dtype_code(x), _ptr(x), x.stride(0), x.shape[0],
+                                             heads, head_dim, _ptr(gamma), _ptr(y), y.stride(0),
+                                             self.stream()),
+                    "pxs_mh_rms_norm")
+        return y
+
+    def rope(self, coords, x, heads, head_dim, freq_min=1.0, freq_base=10000.0):
+        y = torch.empty_like(x)
+        self._check(self.lib.pxs_rope(_dtype_code(x), _ptr(coords), _ptr(x), x.stride(0),
+                                      x.shape[0], heads, head_dim, freq_min, freq_base, _ptr(y),
+                                      y.stride(0), self.stream()),
+                    "pxs_rope")
+        return y
+
+    def qkv_prepare(self, qkv, heads, head_dim, q_gamma=None, k_gamma=None, coords=None,
+                    freq_min=1.0, freq_base=10000.0):
+        rows = qkv.shape[0]
+        C = heads * head_dim
+        q = torch.empty((rows, C), dtype=qkv.dtype, device=qkv.device)
+        k, v = torch.empty_like(q), torch.empty_like(q)
+        self._check(self.lib.pxs_qkv_prepare(_dtype_code(qkv), _ptr(qkv), rows, heads, head_dim,
+                                             _ptr(q_gamma), _ptr(k_gamma), _ptr(coords), freq_min,
+                                             freq_base, _ptr(q), _ptr(k), _ptr(v), self.stream()),
+                    "pxs_qkv_prepare")
+        return q, k, v
+
+    def activation(self, x, act):
+        self._check(self.lib.pxs_activation(_dtype_code(x), _ptr(x), x.numel(), act, self.stream()),
+                    "pxs_activation")
+        return x
+
+    # -- attention --------------------------------------------------------------------
+    def varlen_attention(self, q, k, v, cu_q, cu_k, heads, head_dim, scale, row_map=None,
+                         out=None, nseg=None):
+        nseg = (cu_q.shape[0] - 1) if nseg is None else nseg
+        o = torch.empty((q.shape[0], heads * head_dim), dtype=q.dtype, device=q.device) \
+            if out is None else out
+        ws = self._ws(self.lib.pxs_attention_workspace_bytes(nseg), q.device)
+        self._check(self.lib.pxs_varlen_attention(_dtype_code(q), _ptr(q), q.stride(0), _ptr(k),
+                                                  k.stride(0), _ptr(v), v.stride(0), _ptr(cu_q),
+                                                  _ptr(cu_k), nseg, q.shape[0], _ptr(row_map),
+                                                  heads, head_dim, scale, _ptr(o), o.stride(0),
+                                                  _ptr(ws), self.stream()),
+                    "pxs_varlen_attention")
+        return o

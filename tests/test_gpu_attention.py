@@ -1,0 +1,121 @@
+"""GPU parity: varlen flash attention (fp32 and bf16), cross attention, window
+attention over the GPU window partition."""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle as O
+import workloads as W
+from gpu_common import assert_bf16, assert_fp32, host, t32, tbf, ti32, ti64
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(scope="module")
+def px():
+    import pxs
+    return pxs.Pxs()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return O.Oracle()
+
+
+def test_attention_reference_kat(px):
+    from test_oracle import kat_inputs
+    gold = json.loads((GOLD / "sparse_numeric_fixture.json").read_text())
+    a = kat_inputs()
+    cu = ti64([0, 5, 10])
+    o = px.varlen_attention(t32(a["q"]), t32(a["k"]), t32(a["v"]), cu, cu, 2, 6, 0.37)
+    assert_fp32(host(o).ravel(), np.array(gold["sparse_attention_output"]), what="KAT sdpa")
+    o = px.varlen_attention(t32(a["q"]), t32(a["ck"]), t32(a["cv"]), cu, ti64([0, 3, 5]), 2, 6, 0.29)
+    assert_fp32(host(o).ravel(), np.array(gold["sparse_cross_output"]), what="KAT cross")
+
+
+def test_attention_reference_vectors(px):
+    v = dict(np.load(GOLD / "ref_vectors.npz"))
+    cu = ti64([0, 37, 101, 106])
+    o = px.varlen_attention(t32(v["attn_q"]), t32(v["attn_k"]), t32(v["attn_v"]), cu, cu, 2, 16, 0.25)
+    assert_fp32(host(o), v["attn_out"], what="sdpa vs reference")
+    o = px.varlen_attention(t32(v["attn_q"]), t32(v["cross_k"]), t32(v["cross_v"]), cu,
+                            ti64(v["cross_offsets"]), 2, 16, 0.25)
+    assert_fp32(host(o), v["cross_out"], what="cross vs reference")
+
+
+@pytest.mark.parametrize("lens,heads,hd", [((100, 300, 7), 3, 64), ((513, 64), 2, 32),
+                                           ((1, 2, 129), 1, 8)])
+def test_attention_fp32_random(px, orc, lens, heads, hd):
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    n = int(cu[-1])
+    C = heads * hd
+    q = W.normal(61, n * C, 1).reshape(n, C)
+    k = W.normal(61, n * C, 2).reshape(n, C)
+    v = W.normal(61, n * C, 3).reshape(n, C)
+    scale = 1.0 / np.sqrt(hd)
+    print(f"[attn fp32] lens={lens} heads={heads} hd={hd}", flush=True)
+    o = host(px.varlen_attention(t32(q), t32(k), t32(v), ti64(cu), ti64(cu), heads, hd, scale))
+    assert_fp32(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(scale)), what="attn")
+
+
+def test_attention_bf16_random(px, orc):
+    lens = (1000, 1536, 77)
+    heads, hd = 4, 64
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    n, C = int(cu[-1]), heads * hd
+    q = W.bf16_round(W.normal(62, n * C, 1).reshape(n, C))
+    k = W.bf16_round(W.normal(62, n * C, 2).reshape(n, C))
+    v = W.bf16_round(W.normal(62, n * C, 3).reshape(n, C))
+    o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, 0.125))
+    assert_bf16(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.125)), what="bf16 attn")
+
+
+def test_attention_bf16_full_size_sampled_rows(px, orc):
+    """Config-3 attention at full size (12,288 + 20,480 tokens, 16 x 64),
+    checked exactly on sampled query rows by the oracle."""
+    wl = W.attn_full()
+    n, C = wl["x"].shape
+    heads, hd = 16, 64
+    # Post-RMS-norm-like inputs: unit-norm heads scaled by sqrt(d).
+    q = W.bf16_round(W.normal(63, n * C, 1).reshape(n, C))
+    k = W.bf16_round(W.normal(63, n * C, 2).reshape(n, C))
+    v = W.bf16_round(W.normal(63, n * C, 3).reshape(n, C))
+    cu = wl["cu_seqlens"]
+    print(f"[attn bf16 full] n={n}", flush=True)
+    o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, 0.125))
+    rows = np.concatenate([np.arange(0, 12288, 97), np.arange(12288, n, 151), [12287, n - 1]])
+    ref = orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.125), rows=rows)
+    assert_bf16(o[rows], ref[rows], what="attn full sampled")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shift", [0, 4])
+def test_window_attention(px, orc, dtype, shift):
+    coords = W.shell_coords(32, [[(8.0, 14.0)], [(6.0, 12.0)]], 64)
+    n = coords.shape[0]
+    heads, hd = 3, 64
+    C = heads * hd
+    q = W.bf16_round(W.normal(64, n * C, 1).reshape(n, C))
+    k = W.bf16_round(W.normal(64, n * C, 2).reshape(n, C))
+    v = W.bf16_round(W.normal(64, n * C, 3).reshape(n, C))
+    fwd, bwd, cu, nwin = px.window_partition(ti32(coords), 2, (32, 32, 32), 8, shift)
+    conv = t32 if dtype == "f32" else tbf
+    o = host(px.varlen_attention(conv(q), conv(k), conv(v), cu, cu, heads, hd, 0.125,
+                                 row_map=fwd, nseg=nwin))
+    # Reference: permute rows by the oracle partition, run reference-order
+    # attention per window, un-permute.
+    rfwd, rbwd, rcu = orc.window_partition(coords, (32, 32, 32), 8, shift)
+    ro = orc.varlen_attention(q[rfwd], k[rfwd], v[rfwd], rcu, rcu, heads, hd, np.float32(0.125))
+    ref = ro[rbwd]
+    (assert_fp32 if dtype == "f32" else assert_bf16)(o, ref, what=f"window {dtype}")
+
+
+def test_attention_empty_key_segment_gives_zeros(px):
+    q = W.normal(65, 10 * 64, 1).reshape(10, 64)
+    k = W.normal(65, 4 * 64, 2).reshape(4, 64)
+    o = host(px.varlen_attention(t32(q), t32(k), t32(k), ti64([0, 6, 10]), ti64([0, 4, 4]), 1, 64, 0.125))
+    assert np.all(o[6:] == 0) and np.all(np.isfinite(o))

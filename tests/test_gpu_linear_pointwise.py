@@ -1,0 +1,149 @@
+"""GPU parity: sparse linear (fp32/bf16, activations, gate-residual epilogue),
+layer norm (+modulation), multi-head RMS norm, RoPE, the QKV prologue."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import workloads as W
+from gpu_common import assert_bf16, assert_fp32, host, t32, tbf, ti32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def px():
+    import pxs
+    return pxs.Pxs()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return O.Oracle()
+
+
+@pytest.mark.parametrize("rows,cin,cout", [(200, 24, 40), (1000, 64, 64), (777, 256, 384),
+                                          (300, 8, 1024), (513, 1024, 8), (5, 3, 4)])
+def test_linear_fp32(px, orc, rows, cin, cout):
+    x = W.normal(51, rows * cin, 1).reshape(rows, cin)
+    w = W.normal(51, cout * cin, 2, std=0.2).reshape(cout, cin)
+    b = W.normal(51, cout, 3)
+    print(f"[linear fp32] {rows}x{cin}->{cout}", flush=True)
+    y = host(px.linear(t32(x), t32(w), t32(b)))
+    assert_fp32(y, orc.linear(x, w, b), what="linear fp32")
+
+
+def test_linear_reference_vectors(px):
+    from pathlib import Path
+    v = dict(np.load(Path(__file__).resolve().parent / "golden" / "ref_vectors.npz"))
+    y = host(px.linear(t32(v["lin_x"]), t32(v["lin_w"]), t32(v["lin_b"])))
+    assert_fp32(y, v["lin_out"], what="linear vs reference")
+
+
+@pytest.mark.parametrize("rows,cin,cout", [(4096, 1024, 3072), (2000, 4096, 1024), (1500, 256, 200)])
+def test_linear_bf16(px, rows, cin, cout):
+    x = W.bf16_round(W.normal(52, rows * cin, 1).reshape(rows, cin))
+    w = W.bf16_round(W.normal(52, cout * cin, 2, std=0.02).reshape(cout, cin))
+    b = W.normal(52, cout, 3, std=0.1)
+    print(f"[linear bf16] {rows}x{cin}->{cout}", flush=True)
+    y = host(px.linear(tbf(x), tbf(w), t32(b)))
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + b
+    assert_bf16(y, ref, what="linear bf16")
+
+
+@pytest.mark.parametrize("act", [1, 2])
+def test_linear_activation_epilogue(px, orc, act):
+    x = W.normal(53, 300 * 48, 1).reshape(300, 48)
+    w = W.normal(53, 96 * 48, 2, std=0.2).reshape(96, 48)
+    b = W.normal(53, 96, 3)
+    y = host(px.linear(t32(x), t32(w), t32(b), act=act))
+    ref = orc.linear(x, w, b)
+    ref = orc.gelu_tanh(ref) if act == 1 else orc.silu(ref)
+    assert_fp32(y, ref, what=f"act {act}")
+
+
+def test_linear_gate_residual(px, orc):
+    coords = np.concatenate([np.zeros((70, 4), np.int32), np.ones((50, 4), np.int32)])
+    coords[:, 1:] = 0
+    x = W.normal(54, 120 * 32, 1).reshape(120, 32)
+    w = W.normal(54, 32 * 32, 2, std=0.2).reshape(32, 32)
+    b = W.normal(54, 32, 3)
+    bmod = W.normal(54, 6 * 32, 4)
+    tmod = W.normal(54, 2 * 6 * 32, 5)
+    res = W.normal(54, 120 * 32, 6).reshape(120, 32)
+    r = t32(res)
+    px.linear_gate_residual(t32(x), t32(w), t32(b), ti32(coords), t32(bmod), t32(tmod), 64, r)
+    lin = orc.gate(coords, orc.linear(x, w, b), bmod, tmod, 64)
+    assert_fp32(host(r), res + lin, what="gate residual")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_layer_norm(px, orc, dtype):
+    x = (W.normal(55, 400 * 1024, 1) * 3 + 0.5).reshape(400, 1024)
+    g, b = W.normal(55, 1024, 2), W.normal(55, 1024, 3)
+    conv = t32 if dtype == "f32" else tbf
+    xr = x if dtype == "f32" else W.bf16_round(x)
+    for gamma, beta, eps in ((g, b, 1e-6), (None, None, 1e-5)):
+        y = host(px.layer_norm(conv(x), eps, None if gamma is None else t32(gamma),
+                               None if beta is None else t32(beta)))
+        ref = orc.layer_norm(xr, eps, gamma, beta)
+        (assert_fp32 if dtype == "f32" else assert_bf16)(y, ref, what=f"ln {dtype}")
+
+
+def test_layer_norm_small_channels_and_kat(px):
+    import json
+    from pathlib import Path
+    from test_oracle import kat_inputs
+    gold = json.loads((Path(__file__).resolve().parent / "golden" /
+                       "sparse_numeric_fixture.json").read_text())
+    a = kat_inputs()
+    y = host(px.layer_norm(t32(a["feats"]), 1e-5, t32(np.array([0.8, 1.1, 1.4])),
+                           t32(np.array([-0.2, 0.03, 0.17]))))
+    assert_fp32(y.ravel(), np.array(gold["sparse_norm_output"]), what="KAT layer norm")
+
+
+def test_layer_norm_modulate_to_bf16(px, orc):
+    coords = np.zeros((300, 4), np.int32)
+    coords[150:, 0] = 1
+    x = W.normal(56, 300 * 256, 1).reshape(300, 256)
+    bmod = W.normal(56, 6 * 256, 2, std=0.1)
+    tmod = W.normal(56, 2 * 6 * 256, 3, std=0.1)
+    y = host(px.layer_norm_modulate(t32(x), 1e-6, ti32(coords), t32(bmod), t32(tmod), 3 * 256,
+                                    out_dtype=__import__("torch").bfloat16))
+    ref = orc.modulate(coords, orc.layer_norm(x, 1e-6), bmod, tmod, 3 * 256)
+    assert_bf16(y, ref, tol=5e-3, what="ln modulate")
+    y32 = host(px.layer_norm_modulate(t32(x), 1e-6, ti32(coords), t32(bmod), t32(tmod), 0))
+    assert_fp32(y32, orc.modulate(coords, orc.layer_norm(x, 1e-6), bmod, tmod, 0), what="ln mod f32")
+
+
+@pytest.mark.parametrize("heads,hd", [(4, 64), (2, 6), (3, 16)])
+def test_rms_and_rope(px, orc, heads, hd):
+    coords = W.shell_coords(64, [[(16.0, 30.0)]], 57)[::50].copy()
+    n = coords.shape[0]
+    x = W.normal(57, n * heads * hd, 1).reshape(n, heads * hd)
+    g = np.abs(W.normal(57, heads * hd, 2)) + 0.5
+    assert_fp32(host(px.mh_rms_norm(t32(x), heads, hd, t32(g))), orc.mh_rms_norm(x, heads, hd, g),
+                what="rms")
+    assert_fp32(host(px.rope(ti32(coords), t32(x), heads, hd)), orc.rope(coords, x, heads, hd),
+                what="rope")
+
+
+@pytest.mark.parametrize("dtype,hd", [("f32", 64), ("bf16", 64), ("f32", 16)])
+def test_qkv_prepare(px, orc, dtype, hd):
+    heads = 4
+    C = heads * hd
+    coords = W.shell_coords(64, [[(16.0, 30.0)]], 58)[::30].copy()
+    n = coords.shape[0]
+    qkv = W.normal(58, n * 3 * C, 1).reshape(n, 3 * C)
+    if dtype == "bf16":
+        qkv = W.bf16_round(qkv)
+    gq = np.abs(W.normal(58, C, 2)) + 0.5
+    gk = np.abs(W.normal(58, C, 3)) + 0.5
+    conv = t32 if dtype == "f32" else tbf
+    q, k, v = px.qkv_prepare(conv(qkv), heads, hd, t32(gq), t32(gk), ti32(coords))
+    rq = orc.rope(coords, orc.mh_rms_norm(qkv[:, :C], heads, hd, gq), heads, hd)
+    rk = orc.rope(coords, orc.mh_rms_norm(qkv[:, C:2 * C], heads, hd, gk), heads, hd)
+    check = assert_fp32 if dtype == "f32" else assert_bf16
+    check(host(q), rq, what="q")
+    check(host(k), rk, what="k")
+    np.testing.assert_array_equal(host(v), qkv[:, 2 * C:])

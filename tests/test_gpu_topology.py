@@ -1,0 +1,124 @@
+"""GPU parity: voxel hash, validation, neighbor maps, pair lists, stride-2
+topology, window partition, cu_seqlens, channel-to-spatial.  All integer
+outputs must match the oracle bit for bit."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import workloads as W
+from gpu_common import dev, host, t32, ti32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def px():
+    import pxs
+    return pxs.Pxs()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return O.Oracle()
+
+
+def coord_cases():
+    return {
+        "conv_fp32_64": (W.conv_fp32_64()["coords"], 1, (64, 64, 64)),
+        "unet_stage_128": (W.shell_coords(128, W.UNET_ITEMS, 2), 2, (128, 128, 128)),
+        "small_2batch": (W.shell_coords(16, [[(4.0, 7.0)], [(3.0, 6.0)]], 31), 2, (16, 16, 16)),
+        "single": (np.array([[0, 3, 3, 3]], np.int32), 1, (8, 8, 8)),
+    }
+
+
+@pytest.mark.parametrize("case", list(coord_cases()))
+def test_neighbor_map_bit_exact(px, orc, case):
+    coords, batch, shape = coord_cases()[case]
+    print(f"[neighbor_map] case={case} n={coords.shape[0]}", flush=True)
+    c = ti32(coords)
+    nbr, masks = px.neighbor_map(c)
+    got = host(nbr).astype(np.int64) if False else nbr.cpu().numpy()
+    ref = orc.neighbor_map(coords)
+    np.testing.assert_array_equal(got, ref)
+    present = (ref != coords.shape[0])
+    ref_masks = (present.astype(np.int64) << np.arange(27)[:, None]).sum(0)
+    np.testing.assert_array_equal(masks.cpu().numpy().astype(np.int64) & 0x7FFFFFF, ref_masks)
+    assert px.validate(c, batch, shape) == (0, -1)
+
+
+@pytest.mark.parametrize("case", ["conv_fp32_64", "small_2batch"])
+def test_neighbor_pairs_bit_exact(px, orc, case):
+    coords, _, _ = coord_cases()[case]
+    print(f"[neighbor_pairs] case={case}", flush=True)
+    nbr, _ = px.neighbor_map(ti32(coords))
+    pin, pout, offs = px.neighbor_pairs(nbr)
+    rin, rout, roffs = orc.neighbor_pairs(orc.neighbor_map(coords))
+    np.testing.assert_array_equal(offs.cpu().numpy(), roffs)
+    np.testing.assert_array_equal(pin.cpu().numpy(), rin)
+    np.testing.assert_array_equal(pout.cpu().numpy(), rout)
+
+
+def test_validation_first_error_matches_oracle(px, orc):
+    base = W.shell_coords(16, [[(4.0, 7.0)], [(3.0, 6.0)]], 32)
+    n = base.shape[0]
+    feats = W.normal(32, n * 5, 1).reshape(n, 5)
+    cases = []
+    dup = base.copy(); dup[n // 2] = dup[n // 3]; cases.append(("duplicate", dup, feats))
+    oob = base.copy(); oob[n // 4, 2] = 16; cases.append(("outside", oob, feats))
+    neg = base.copy(); neg[7, 1] = -1; cases.append(("negative", neg, feats))
+    cont = base.copy(); cont[n - 1, 0] = 0; cases.append(("contiguity", cont, feats))
+    nanf = feats.copy(); nanf[n // 5, 3] = np.nan; cases.append(("nan", base, nanf))
+    inff = feats.copy(); inff[2, 0] = np.inf; cases.append(("inf", base, inff))
+    both = dup.copy(); both[n // 2 + 3, 1] = 99; cases.append(("dup_then_oob", both, nanf))
+    for name, coords, f in cases:
+        print(f"[validate] case={name}", flush=True)
+        got = px.validate(ti32(coords), 2, (16, 16, 16), t32(f))
+        ref = orc.sparse_valid(coords, 2, (16, 16, 16), f, 5)
+        assert got == ref, (name, got, ref)
+
+
+@pytest.mark.parametrize("case", ["unet_stage_128", "small_2batch", "single"])
+def test_downsample_s2_topology(px, orc, case):
+    coords, batch, shape = coord_cases()[case]
+    print(f"[downsample_s2] case={case}", flush=True)
+    oc, child, m = px.downsample_s2(ti32(coords), batch, shape)
+    roc, rchild = orc.downsample_coords_s2(coords)
+    assert m == roc.shape[0]
+    np.testing.assert_array_equal(oc.cpu().numpy(), roc)
+    np.testing.assert_array_equal(child.cpu().numpy()[:, :m], rchild.T)
+
+
+@pytest.mark.parametrize("shift", [0, 4])
+@pytest.mark.parametrize("case", ["swin_64", "small_2batch"])
+def test_window_partition_bit_exact(px, orc, case, shift):
+    if case == "swin_64":
+        coords, batch, shape = W.shell_coords(64, [W.SWIN_SHELLS], 4), 1, (64, 64, 64)
+    else:
+        coords, batch, shape = coord_cases()[case]
+    print(f"[window_partition] case={case} shift={shift}", flush=True)
+    fwd, bwd, cu, nwin = px.window_partition(ti32(coords), batch, shape, 8, shift)
+    rfwd, rbwd, rcu = orc.window_partition(coords, shape, 8, shift)
+    assert nwin == len(rcu) - 1
+    np.testing.assert_array_equal(fwd.cpu().numpy(), rfwd)
+    np.testing.assert_array_equal(bwd.cpu().numpy(), rbwd)
+    np.testing.assert_array_equal(cu.cpu().numpy(), rcu)
+
+
+def test_batch_cu_seqlens(px, orc):
+    coords = W.shell_coords(16, [[(4.0, 7.0)], [], [(3.0, 6.0)]], 33)
+    cu = px.batch_cu_seqlens(ti32(coords), 4).cpu().numpy()
+    np.testing.assert_array_equal(cu, orc.batch_cu_seqlens(coords, 4))
+
+
+@pytest.mark.parametrize("with_sub", [False, True])
+def test_channel_to_spatial(px, orc, with_sub):
+    coords = W.shell_coords(16, [[(4.0, 7.0)], [(3.0, 6.0)]], 34)
+    n = coords.shape[0]
+    x = W.normal(34, n * 24, 1).reshape(n, 24)
+    sub = (W.uniform(34, n * 8, 2) > 0.4).astype(np.float32).reshape(n, 8) if with_sub else None
+    print(f"[c2s] sub={with_sub}", flush=True)
+    oc, y = px.channel_to_spatial(ti32(coords), t32(x), None if sub is None else t32(sub))
+    roc, ry = orc.channel_to_spatial(coords, x, 2, sub)
+    np.testing.assert_array_equal(oc.cpu().numpy(), roc)
+    np.testing.assert_array_equal(host(y), ry)
