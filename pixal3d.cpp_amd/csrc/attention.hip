@@ -26,6 +26,8 @@ namespace {
 constexpr int kKeys = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 struct AttnArgs {
     const void * q;
     const void * k;
@@ -277,6 +279,215 @@ flash_attn_kernel(AttnArgs a) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// bf16, head_dim 64 fast path: K/V tiles stream HBM -> LDS with
+// global_load_lds_dwordx4 into a double buffer (the next tile loads while the
+// current one is consumed), and V stays row-major in LDS: the V^T operand
+// fragments are read with ds_read_b64_tr_b16, whose 16-lane transpose hands
+// lane (G, i) element i%4 of the rows addressed by lanes i/4 + 4t.  Rows are
+// XOR-swizzled in 16-byte pieces (kswz for the K fragment reads, vswz for the
+// transposed V reads) so neither read pattern conflicts on LDS banks.
+
+__device__ __align__(16) uint4 g_attn_zero[8];
+
+__device__ __forceinline__ int kswz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int vswz(int row) { return (2 * (row & 3)) ^ ((row >> 2) & 1); }
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+template <int NW>
+__global__ void __launch_bounds__(NW * 64)
+flash_attn_bf16_kernel(AttnArgs a) {
+    constexpr int kThreads = NW * 64;
+    constexpr int kTileBytes = kKeys * 128;           // one 64-key x 64-dim bf16 tile
+    constexpr int kInstr = 2 * (kKeys / 8) / NW;      // K + V wave instructions per tile
+    __shared__ __align__(16) char lds[2][2 * kTileBytes];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, r = lane & 31;
+    const int head = blockIdx.y;
+
+    const int64_t t = blockIdx.x;
+    if (t >= a.tile_start[a.nseg]) return;
+    int lo = 0, hi = a.nseg - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.tile_start[mid] <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    const int seg = lo;
+    const int64_t q_begin = a.cu_q[seg] + (t - a.tile_start[seg]) * (32 * NW);
+    const int64_t q_end = a.cu_q[seg + 1];
+    const int64_t k_begin = a.cu_k[seg], k_end = a.cu_k[seg + 1];
+
+    const uint16_t * __restrict__ qp = static_cast<const uint16_t *>(a.q);
+    const uint16_t * __restrict__ kp = static_cast<const uint16_t *>(a.k);
+    const uint16_t * __restrict__ vp = static_cast<const uint16_t *>(a.v);
+
+    const int64_t qi = q_begin + wave * 32 + r;
+    const bool q_valid = qi < q_end;
+    const int64_t q_row = q_valid ? (a.row_map ? a.row_map[qi] : qi) : -1;
+    bf16x8 qf[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (q_valid) v = *reinterpret_cast<const uint4 *>(qp + q_row * a.ldq + head * 64 + 32 * h + 8 * s);
+        qf[s] = __builtin_bit_cast(bf16x8, v);
+    }
+
+    const int ntiles = static_cast<int>((k_end - k_begin + kKeys - 1) / kKeys);
+    const int lrow = lane >> 3, lslot = lane & 7;
+    auto issue = [&](int tile) {
+        char * base = lds[tile & 1];
+        const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeys;
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+            const int unit = wave * kInstr + j;           // 0..15: 8 K blocks then 8 V blocks
+            const bool is_v = unit >= kKeys / 8;
+            const int row0 = (unit % (kKeys / 8)) * 8;
+            const int row = row0 + lrow;
+            const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
+            const int64_t kidx = kt0 + row;
+            const void * g = static_cast<const void *>(g_attn_zero);
+            if (kidx < k_end) {
+                const int64_t prow = a.row_map ? a.row_map[kidx] : kidx;
+                g = is_v ? static_cast<const void *>(vp + prow * a.ldv + head * 64 + piece * 8)
+                         : static_cast<const void *>(kp + prow * a.ldk + head * 64 + piece * 8);
+            }
+            __builtin_amdgcn_global_load_lds(
+                g, (__attribute__((address_space(3))) void *)(base + (is_v ? kTileBytes : 0) + row0 * 128),
+                16, 0, 0);
+        }
+    };
+
+    f32x16 oacc[2];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // Lane-constant parts of the transposed V reads: source row t = j / 4 of
+    // the 4-key group and the 4 dims starting at 16*(G%2) + 4*(j%4).
+    const int G = lane >> 4, jl = lane & 15;
+    const int v_key_off = 4 * (G >> 1) + (jl >> 2);
+    const int v_dim_off = 16 * (G & 1) + 4 * (jl & 3);
+
+    if (ntiles > 0) issue(0);
+    for (int tile = 0; tile < ntiles; ++tile) {
+        wait_vmcnt0();
+        __syncthreads();
+        if (tile + 1 < ntiles) issue(tile + 1);
+        const char * kl = lds[tile & 1];
+        const char * vl = kl + kTileBytes;
+        const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeys;
+
+        f32x16 sacc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sacc[kt][v] = 0.0f;
+            const int row = kt * 32 + r;
+            const char * krow = kl + row * 128;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const bf16x8 af = *reinterpret_cast<const bf16x8 *>(
+                    krow + (((4 * h + s) ^ kswz(row)) << 4));
+                sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[s], sacc[kt], 0, 0, 0);
+            }
+        }
+
+        const int valid_keys = static_cast<int>(min<int64_t>(kKeys, k_end - kt0));
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                float sv = sacc[kt][v] * a.scale_log2;
+                if (valid_keys < kKeys) {
+                    const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (key >= valid_keys) sv = -INFINITY;
+                }
+                sacc[kt][v] = sv;
+                mx = fmaxf(mx, sv);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        float rs = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float p = __builtin_amdgcn_exp2f(sacc[kt][v] - m_new);
+                sacc[kt][v] = p;
+                rs += p;
+            }
+        }
+        rs += __shfl_xor(rs, 32, 64);
+        l_run = l_run * alpha + rs;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                bf16x8 pb;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pb[e] = static_cast<__bf16>(sacc[kt][8 * u + e]);
+                const int key_a = kt * 32 + 16 * u + v_key_off;
+                const int key_b = key_a + 8;
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) {
+                    const int dbyte = (dt * 32 + v_dim_off) * 2;
+                    const int piece = dbyte >> 4, within = dbyte & 15;
+                    const char * pa = vl + key_a * 128 + ((piece ^ vswz(key_a)) << 4) + within;
+                    const char * pbp = vl + key_b * 128 + ((piece ^ vswz(key_b)) << 4) + within;
+                    const v4i16 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (v4i16 __attribute__((address_space(3))) *)(pa));
+                    const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (v4i16 __attribute__((address_space(3))) *)(pbp));
+                    const uint2 lo2 = __builtin_bit_cast(uint2, lo4);
+                    const uint2 hi2 = __builtin_bit_cast(uint2, hi4);
+                    const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, oacc[dt], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    if (!q_valid) return;
+    const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    uint16_t * op = static_cast<uint16_t *>(a.o) + q_row * a.ldo + head * 64;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = dt * 32 + 8 * i + 4 * h;
+            uint2 packed;
+            packed.x = pack_bf16x2(oacc[dt][4 * i + 0] * inv_l, oacc[dt][4 * i + 1] * inv_l);
+            packed.y = pack_bf16x2(oacc[dt][4 * i + 2] * inv_l, oacc[dt][4 * i + 3] * inv_l);
+            *reinterpret_cast<uint2 *>(op + d) = packed;
+        }
+    }
+}
+
+template <int NW>
+int launch_attn_bf16(const AttnArgs & args, int64_t total_q, int heads, hipStream_t stream) {
+    const int64_t bound = total_q / (32 * NW) + args.nseg + 1;
+    if (bound > INT32_MAX) return fail(PXS_ERR_ARG, "attention grid too large");
+    hipLaunchKernelGGL((flash_attn_bf16_kernel<NW>), dim3(static_cast<unsigned>(bound), heads),
+                       dim3(NW * 64), 0, stream, args);
+    return check_launch("flash attention (bf16)");
+}
+
 template <typename T, int NW>
 int launch_attn(const AttnArgs & args, int64_t total_q, int heads, hipStream_t stream) {
     const int64_t bound = total_q / (32 * NW) + args.nseg + 1;
@@ -339,6 +550,13 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     a.vec_ok = (head_dim % vec == 0) && (ld_q % vec == 0) && (ld_k % vec == 0) &&
                (ld_v % vec == 0) && aligned16(q) && aligned16(k) && aligned16(v);
     if (dtype == PXS_BF16) {
+        const bool fast = head_dim == 64 && (ld_q % 8 == 0) && (ld_k % 8 == 0) &&
+                          (ld_v % 8 == 0) && (ld_o % 4 == 0) && aligned16(q) && aligned16(k) &&
+                          aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0;
+        if (fast) {
+            return nw == 4 ? launch_attn_bf16<4>(a, total_q, heads, s)
+                           : launch_attn_bf16<1>(a, total_q, heads, s);
+        }
         return nw == 4 ? launch_attn<uint16_t, 4>(a, total_q, heads, s)
                        : launch_attn<uint16_t, 1>(a, total_q, heads, s);
     }

@@ -88,6 +88,40 @@ __device__ __forceinline__ uint4 load_chunk16(const T * base, int64_t row, int64
     return *reinterpret_cast<const uint4 *>(tmp);
 }
 
+// Epilogue.  32x32 accumulator layout: lane (h, r), register v holds row
+// 8*(v/4) + 4*h + v%4, column r of the 32x32 tile.
+template <typename T, int TI, int TJ, int WM, int WN, int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs & a, const f32x16 (&acc)[TI][TJ],
+                                              int64_t p0, int n0, int wm, int wn, int h, int r) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int col = n0 + wn * WN + j * 32 + r;
+            if (col >= a.cout) continue;
+            const float b = a.bias ? a.bias[col] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t row = p0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (row >= a.m) continue;
+                float val = acc[i][j][v] + b;
+                if constexpr (EPI == kEpiStore) {
+                    if (a.act == PXS_ACT_GELU_TANH) val = gelu_tanh_f(val);
+                    else if (a.act == PXS_ACT_SILU) val = silu_f(val);
+                    store_f32(static_cast<T *>(a.y) + row * a.ldy + col, val);
+                } else {
+                    const int batch = a.coords[row * 4];
+                    const float g = a.block_mod[a.gate_offset + col] +
+                                    a.time_mod[static_cast<int64_t>(batch) * 6 * a.cout +
+                                               a.gate_offset + col];
+                    float * res = a.residual + row * a.cout + col;
+                    *res = *res + val * g;
+                }
+            }
+        }
+    }
+}
+
 template <typename T, int BM, int BN, int EPI>
 __global__ void __launch_bounds__(kGemmThreads)
 gather_gemm_kernel(GemmArgs a) {
@@ -256,35 +290,296 @@ gather_gemm_kernel(GemmArgs a) {
         __syncthreads();
     }
 
-    // Epilogue.  32x32 accumulator layout: lane (h, r), register v holds
-    // row 8*(v/4) + 4*h + v%4, column r of the tile.
-#pragma unroll
-    for (int i = 0; i < TI; ++i) {
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int col = n0 + wn * WN + j * 32 + r;
-            if (col >= a.cout) continue;
-            const float b = a.bias ? a.bias[col] : 0.0f;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t row = p0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (row >= a.m) continue;
-                float val = acc[i][j][v] + b;
-                if constexpr (EPI == kEpiStore) {
-                    if (a.act == PXS_ACT_GELU_TANH) val = gelu_tanh_f(val);
-                    else if (a.act == PXS_ACT_SILU) val = silu_f(val);
-                    store_f32(static_cast<T *>(a.y) + row * a.ldy + col, val);
-                } else {
-                    const int batch = a.coords[row * 4];
-                    const float g = a.block_mod[a.gate_offset + col] +
-                                    a.time_mod[static_cast<int64_t>(batch) * 6 * a.cout +
-                                               a.gate_offset + col];
-                    float * res = a.residual + row * a.cout + col;
-                    *res = *res + val * g;
+    gemm_epilogue<T, TI, TJ, WM, WN, EPI>(a, acc, p0, n0, wm, wn, h, r);
+}
+
+
+// ---------------------------------------------------------------------------
+// Pipelined variant for 16-byte-aligned operands: tiles stream from HBM/L2
+// straight into LDS with global_load_lds_dwordx4 (no VGPR staging), NSTAGE
+// stages in flight.  Each wavefront instruction fills 1 KiB of LDS = 8 rows x
+// 128 bytes, lane l landing at offset 16*l; the 16-byte piece a lane fetches
+// is XOR-swizzled so that the MFMA fragment reads (32 rows, one piece) hit
+// distinct banks.  The gathered row indices of the tile (for every present
+// offset) are staged in LDS once at the start, so a stage issues its loads
+// without waiting on an index load.
+
+__device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent rows
+
+// Measured on MI355X (SubMConv3d 128->128 / 256->256, linear 1024->3072):
+// two stages of 128x128 tiles (64 KiB + indices, two workgroups per CU) with
+// the next stage issued before the current one is computed beat deeper
+// pipelines at one workgroup per CU and larger tiles.
+#ifndef PXS_GEMM_STAGES
+#define PXS_GEMM_STAGES 2
+#endif
+#ifndef PXS_GEMM_ISSUE_LATE
+#define PXS_GEMM_ISSUE_LATE 0
+#endif
+// Late issue: queue the next stage's loads after this stage's MFMAs (the
+// buffer they fill was released by the barrier at the top of the iteration).
+constexpr bool kIssueLate = PXS_GEMM_ISSUE_LATE != 0;
+
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    // s_waitcnt with expcnt/lgkmcnt at their maxima: only vmcnt is waited on.
+    switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+    case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+    case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+    case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
+    case 16: __builtin_amdgcn_s_waitcnt(0x4F70); break;
+    case 17: __builtin_amdgcn_s_waitcnt(0x4F71); break;
+    case 18: __builtin_amdgcn_s_waitcnt(0x4F72); break;
+    case 19: __builtin_amdgcn_s_waitcnt(0x4F73); break;
+    case 20: __builtin_amdgcn_s_waitcnt(0x4F74); break;
+    case 21: __builtin_amdgcn_s_waitcnt(0x4F75); break;
+    case 22: __builtin_amdgcn_s_waitcnt(0x4F76); break;
+    case 23: __builtin_amdgcn_s_waitcnt(0x4F77); break;
+    case 24: __builtin_amdgcn_s_waitcnt(0x4F78); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
+}
+
+template <int BM, int BN, int NSTAGE>
+constexpr int lds_gemm_bytes(int noff) {
+    return NSTAGE * (BM + BN) * kChunkBytes + noff * BM * 4;
+}
+
+template <typename T, int BM, int BN, int EPI, int NSTAGE>
+__global__ void __launch_bounds__(kGemmThreads)
+gather_gemm_lds_kernel(GemmArgs a) {
+    constexpr int kVec = Mfma<T>::kVec;
+    constexpr int kChunk = Mfma<T>::kChunk;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TI = WM / 32, TJ = WN / 32;
+    constexpr int kStageBytes = (BM + BN) * kChunkBytes;
+    constexpr int AI = BM / 32;  // A instructions per wave per stage (8 rows each)
+    constexpr int BI = BN / 32;
+    constexpr int kPerStage = AI + BI;
+
+    extern __shared__ __align__(16) char smem[];
+    int32_t * idx_lds = reinterpret_cast<int32_t *>(smem + NSTAGE * kStageBytes);
+    __shared__ uint32_t tile_mask;
+    __shared__ int koff[32];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int h = lane >> 5, r = lane & 31;
+
+    const int tiles_n = (a.cout + BN - 1) / BN;
+    const int logical = remap_xcd(blockIdx.x, gridDim.x);
+    const int64_t p0 = static_cast<int64_t>(logical / tiles_n) * BM;
+    const int n0 = (logical % tiles_n) * BN;
+    const T * __restrict__ x = static_cast<const T *>(a.x);
+    const T * __restrict__ w = static_cast<const T *>(a.w);
+
+    if (tid == 0) tile_mask = 0;
+    __syncthreads();
+    {
+        uint32_t local = 0;
+        for (int row = tid; row < BM; row += kGemmThreads) {
+            const int64_t p = p0 + row;
+            if (p >= a.m) break;
+            if (a.masks) {
+                local |= a.masks[p];
+            } else if (a.rowmap) {
+                for (int k = 0; k < a.noff; ++k) {
+                    const int32_t src = a.rowmap[k * a.ld_map + p];
+                    if (src >= 0 && src < a.rows_in) local |= 1u << k;
                 }
+            } else {
+                local = 1u;
             }
         }
+        if (local) atomicOr(&tile_mask, local);
     }
+    __syncthreads();
+    const uint32_t present = tile_mask & (a.noff >= 32 ? ~0u : ((1u << a.noff) - 1u));
+    const int kcount = __popc(present);
+    if (tid == 0) {
+        uint32_t m = present;
+        for (int i = 0; i < kcount; ++i) {
+            koff[i] = __ffs(m) - 1;
+            m &= m - 1;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < kcount * BM; e += kGemmThreads) {
+        const int i = e / BM, row = e % BM;
+        const int64_t p = p0 + row;
+        int32_t src = -1;
+        if (p < a.m) {
+            const int64_t s = a.rowmap ? static_cast<int64_t>(a.rowmap[koff[i] * a.ld_map + p]) : p;
+            src = (s >= 0 && s < a.rows_in) ? static_cast<int32_t>(s) : -1;
+        }
+        idx_lds[e] = src;
+    }
+    __syncthreads();
+
+    const int chunks = (a.cin + kChunk - 1) / kChunk;
+    const int stages = kcount * chunks;
+    const int lrow = lane >> 3, lslot = lane & 7;
+    const void * zero = static_cast<const void *>(g_zero_chunk);
+
+    // Per-lane constant parts of the load addresses: the row this lane fills
+    // in each of its instructions and the swizzled 16-byte piece it fetches.
+    int a_row[AI], a_piece[AI];
+#pragma unroll
+    for (int j = 0; j < AI; ++j) {
+        a_row[j] = (wave * AI + j) * 8 + lrow;
+        a_piece[j] = lslot ^ swz(a_row[j]);
+    }
+    int64_t b_off[BI];
+    int b_piece[BI];
+    bool b_ok[BI];
+#pragma unroll
+    for (int j = 0; j < BI; ++j) {
+        const int row = (wave * BI + j) * 8 + lrow;
+        b_piece[j] = lslot ^ swz(row);
+        b_ok[j] = n0 + row < a.cout;
+        b_off[j] = static_cast<int64_t>(n0 + row) * a.cin + b_piece[j] * kVec;
+    }
+
+    auto issue = [&](int s) {
+        const int i = s / chunks, chunk = s - i * chunks;
+        const int k = koff[i];
+        char * base = smem + (s % NSTAGE) * kStageBytes;
+        int32_t src[AI];
+#pragma unroll
+        for (int j = 0; j < AI; ++j) src[j] = idx_lds[i * BM + a_row[j]];
+#pragma unroll
+        for (int j = 0; j < AI; ++j) {
+            const int col = chunk * kChunk + a_piece[j] * kVec;
+            const void * g = (src[j] >= 0 && col < a.cin)
+                                 ? static_cast<const void *>(x + static_cast<int64_t>(src[j]) * a.ldx + col)
+                                 : zero;
+            __builtin_amdgcn_global_load_lds(
+                g, (__attribute__((address_space(3))) void *)(base + (wave * AI + j) * 8 * kChunkBytes),
+                16, 0, 0);
+        }
+        const int64_t kbase = static_cast<int64_t>(k) * a.cout * a.cin + chunk * kChunk;
+#pragma unroll
+        for (int j = 0; j < BI; ++j) {
+            const int col = chunk * kChunk + b_piece[j] * kVec;
+            const void * g = (b_ok[j] && col < a.cin) ? static_cast<const void *>(w + kbase + b_off[j]) : zero;
+            __builtin_amdgcn_global_load_lds(
+                g, (__attribute__((address_space(3))) void *)(base + (BM + (wave * BI + j) * 8) * kChunkBytes),
+                16, 0, 0);
+        }
+    };
+
+    f32x16 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+#pragma unroll
+    for (int s = 0; s < NSTAGE - 1; ++s)
+        if (s < stages) issue(s);
+
+    for (int s = 0; s < stages; ++s) {
+        const int after = min(NSTAGE - 2, stages - 1 - s);
+        wait_vmcnt(after * kPerStage);
+        __syncthreads();
+        if constexpr (!kIssueLate) {
+            if (s + NSTAGE - 1 < stages) issue(s + NSTAGE - 1);
+        }
+        const char * sa = smem + (s % NSTAGE) * kStageBytes;
+        const char * sb = sa + BM * kChunkBytes;
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int piece = 4 * h + ks;
+                bf16x8 af[TI], bfr[TJ];
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    const int row = wm * WM + i * 32 + r;
+                    af[i] = *reinterpret_cast<const bf16x8 *>(sa + row * kChunkBytes +
+                                                              ((piece ^ swz(row)) << 4));
+                }
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const int row = wn * WN + j * 32 + r;
+                    bfr[j] = *reinterpret_cast<const bf16x8 *>(sb + row * kChunkBytes +
+                                                               ((piece ^ swz(row)) << 4));
+                }
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j],
+                                                                            acc[i][j], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int piece = 4 * h + u;
+                f32x4 af[TI], bfr[TJ];
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    const int row = wm * WM + i * 32 + r;
+                    af[i] = *reinterpret_cast<const f32x4 *>(sa + row * kChunkBytes +
+                                                             ((piece ^ swz(row)) << 4));
+                }
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const int row = wn * WN + j * 32 + r;
+                    bfr[j] = *reinterpret_cast<const f32x4 *>(sb + row * kChunkBytes +
+                                                              ((piece ^ swz(row)) << 4));
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int i = 0; i < TI; ++i)
+#pragma unroll
+                        for (int j = 0; j < TJ; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][e], bfr[j][e],
+                                                                             acc[i][j], 0, 0, 0);
+            }
+        }
+        if constexpr (kIssueLate) {
+            if (s + NSTAGE - 1 < stages) issue(s + NSTAGE - 1);
+        }
+    }
+    gemm_epilogue<T, TI, TJ, WM, WN, EPI>(a, acc, p0, n0, wm, wn, h, r);
+}
+
+template <typename T, int BM, int BN, int EPI, int NSTAGE>
+int launch_lds_tile(const GemmArgs & args, hipStream_t stream) {
+    const int smem = lds_gemm_bytes<BM, BN, NSTAGE>(args.noff);
+    static int configured = 0;
+    if (configured < smem) {
+        hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, lds_gemm_bytes<BM, BN, NSTAGE>(27));
+        if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(gather_gemm_lds)");
+        configured = lds_gemm_bytes<BM, BN, NSTAGE>(27);
+    }
+    const int64_t tiles_m = (args.m + BM - 1) / BM;
+    const int64_t tiles_n = (args.cout + BN - 1) / BN;
+    const int64_t blocks = tiles_m * tiles_n;
+    if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "gather GEMM grid too large");
+    hipLaunchKernelGGL((gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads), smem, stream, args);
+    return check_launch("gather GEMM (LDS pipeline)");
 }
 
 template <typename T, int BM, int BN, int EPI>
@@ -311,9 +606,14 @@ int launch_tile(const GemmArgs & args, hipStream_t stream) {
 template <typename T, int EPI>
 int dispatch(const GemmArgs & args, hipStream_t stream) {
     if (args.m == 0 || args.cout == 0) return PXS_OK;
+    if (args.noff > 32) return fail(PXS_ERR_ARG, "gather GEMM supports at most 32 offsets");
     const bool narrow = args.cout <= 64;
+    if (args.vec_ok) {
+        // 128-row tiles: the row count only changes the grid, not the tile.
+        return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES>(args, stream)
+                      : launch_lds_tile<T, 128, 128, EPI, PXS_GEMM_STAGES>(args, stream);
+    }
     const int64_t tiles_n = (args.cout + (narrow ? 63 : 127)) / (narrow ? 64 : 128);
-    // Prefer 128-row tiles when they still give every CU two workgroups.
     const bool tall = ((args.m + 127) / 128) * tiles_n >= 512;
     if (narrow) {
         return tall ? launch_tile<T, 128, 64, EPI>(args, stream)
