@@ -123,7 +123,7 @@ def unet_stage(args, torch, px, W):
     oc = torch.empty((n, 4), dtype=torch.int32, device=dev)
     child = torch.empty((8, n), dtype=torch.int32, device=dev)
     m_dev = torch.empty(1, dtype=torch.int64, device=dev)
-    ds_ws = ws(lib.pxs_downsample_workspace_bytes(2, 128, 128, 128))
+    ds_ws = ws(lib.pxs_downsample_workspace_bytes(n, 2, 128, 128, 128, 2))
     # Topology size (deterministic for these coordinates): one sync here,
     # outside the timed region; every step recomputes the topology itself.
     _, _, m = px.downsample_s2(coords, 2, (128, 128, 128))

@@ -69,6 +69,15 @@ int pxs_sparse_validate(const int32_t * coords, int64_t n, int batch_size, int s
 /* The reference's message for a validation code (src/sparse.cpp:249-330). */
 const char * pxs_validation_message(int code);
 
+/* *status = INT64_MAX (no error yet), for calls that min-reduce into it. */
+int pxs_status_reset(int64_t * status, void * stream);
+
+/* Min-reduce into *status row * 8 + 7 for the first row of x ([rows,
+ * channels], row stride ld) holding a non-finite value: the reference's
+ * feature check (src/sparse.cpp:326-331) on a device buffer. */
+int pxs_check_finite(int dtype, const void * x, int64_t rows, int channels, int64_t ld,
+                     int64_t * status, void * stream);
+
 /* Dense 3x3x3 neighbor map (src/slat_decoder.cpp:609-668): nbr[k * n + p] is
  * the row of voxel (b, x+kd-1, y+kh-1, z+kw-1), k = kd*9 + kh*3 + kw, or n
  * when absent.  masks (nullable) receives bit k set when offset k is present. */
@@ -94,7 +103,12 @@ int pxs_subm_conv3d(int dtype, const void * x, int64_t n, int cin, const void * 
                     const float * bias, int cout, const int32_t * nbr, const uint32_t * masks,
                     void * y, void * stream);
 
-/* ---- a4, a15: stride-2 topology, strided conv, mean downsample -------------- */
+/* ---- a4, a15: factor-f topology, strided conv, mean downsample ------------- */
+
+/* Workspace of pxs_downsample_topology / pxs_downsample_s2_topology (factor 2)
+ * for n rows. */
+size_t pxs_downsample_workspace_bytes(int64_t n, int batch_size, int sx, int sy, int sz,
+                                      int factor);
 
 /* Output topology of a factor-2 reduction: the unique (b, x/2, y/2, z/2) in
  * lexicographic order (the coordinates sparse_downsample_mean emits,
@@ -102,10 +116,18 @@ int pxs_subm_conv3d(int dtype, const void * x, int64_t n, int cin, const void * 
  * [8][n] (offset-major, leading dimension n): child c = (x&1) + 2(y&1) +
  * 4(z&1) of output q is input row child_map[c * n + q], or -1.  *m_out
  * (device int64) receives the output row count. */
-size_t pxs_downsample_workspace_bytes(int batch_size, int sx, int sy, int sz);
 int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size, int sx,
                                int sy, int sz, int32_t * out_coords, int32_t * child_map,
                                int64_t * m_out, void * workspace, void * stream);
+
+/* The same topology for any factor f, as groups: output q (coordinates
+ * (b, x/f, y/f, z/f), lexicographic) gathers input rows
+ * group_rows[group_offsets[q] .. group_offsets[q+1]) in ascending order.
+ * out_coords holds up to n rows, group_offsets n + 1 entries, group_rows n. */
+int pxs_downsample_topology(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                            int sz, int factor, int32_t * out_coords, int64_t * group_offsets,
+                            int32_t * group_rows, int64_t * m_out, void * workspace,
+                            void * stream);
 
 /* Stride-2 SparseConv3d with a 2x2x2 kernel (no reference counterpart; the
  * contract is documented with the topology above): y[q] = sum over present
@@ -116,21 +138,23 @@ int pxs_sparse_conv3d_s2(int dtype, const void * x, int64_t n_in, int cin, const
                          const float * bias, int cout, const int32_t * child_map, int64_t ld_map,
                          int64_t m, void * y, void * stream);
 
-/* sparse_downsample_mean features for factor 2 (src/sparse.cpp:536-602):
- * each output is the mean of its children summed in input-row order. */
-int pxs_downsample_mean_s2(int dtype, const void * x, int channels, const int32_t * child_map,
-                           int64_t ld_map, int64_t m, void * y, void * stream);
+/* sparse_downsample_mean features (src/sparse.cpp:536-602): each output is
+ * the sum of its group's rows in ascending row order divided by the count. */
+int pxs_downsample_mean(int dtype, const void * x, int channels, const int64_t * group_offsets,
+                        const int32_t * group_rows, int64_t m, void * y, void * stream);
 
 /* ---- a5: channel to spatial ---------------------------------------------------- */
 
-/* sparse_channel_to_spatial with factor 2 (src/sparse.cpp:604-702).
- * x [n, 8*c_out]; subdivision (nullable, fp32 [n, 8]) selects children > 0.
- * Output rows are parent-major, child ascending; out_coords and y hold up to
- * 8n rows; *m_out (device int64) receives the count. */
-size_t pxs_channel_to_spatial_workspace_bytes(int64_t n);
+/* sparse_channel_to_spatial (src/sparse.cpp:604-702) for factor f (cc = f^3
+ * children): x [n, cc * c_out]; subdivision (nullable, fp32 [n, cc]) selects
+ * children > 0.  Child c lands at (f x + c % f, f y + (c / f) % f,
+ * f z + c / f^2).  Output rows are parent-major, child ascending; out_coords
+ * and y hold up to n * cc rows; *m_out (device int64) receives the count. */
+size_t pxs_channel_to_spatial_workspace_bytes(int64_t n, int factor);
 int pxs_channel_to_spatial(int dtype, const int32_t * coords, int64_t n, const void * x,
-                           int channels, const float * subdivision, int32_t * out_coords,
-                           void * y, int64_t * m_out, void * workspace, void * stream);
+                           int channels, int factor, const float * subdivision,
+                           int32_t * out_coords, void * y, int64_t * m_out, void * workspace,
+                           void * stream);
 
 /* ---- a6: sparse linear --------------------------------------------------------- */
 
@@ -151,6 +175,11 @@ int pxs_linear_gate_residual(int dtype, const void * x, int64_t rows, int cin,
                              const int32_t * coords, const float * block_mod,
                              const float * time_mod, int gate_offset, float * residual,
                              void * stream);
+
+/* Linear whose epilogue adds into an fp32 residual: residual[r, o] +=
+ * (x W^T + bias)[r, o] (add_in_place, src/sparse_transformer.cpp:57-69). */
+int pxs_linear_residual(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+                        const float * bias, int cout, float * residual, void * stream);
 
 /* ---- a10-a12: row-wise normalisation and position embedding ------------------- */
 
@@ -189,6 +218,15 @@ int pxs_qkv_prepare(int dtype, const void * qkv, int64_t rows, int heads, int he
 /* In-place activation (PXS_ACT_*) over count elements. */
 int pxs_activation(int dtype, void * x, int64_t count, int act, void * stream);
 
+/* y = x converted between PXS_F32 and PXS_BF16 (round to nearest even). */
+int pxs_convert(int src_dtype, const void * x, int64_t count, int dst_dtype, void * y,
+                void * stream);
+
+/* timestep_embedding (src/flow.cpp:92-123): out [batch, dim] fp32 from
+ * timesteps (device fp32 [batch]). */
+int pxs_timestep_embedding(const float * timesteps, int64_t batch, int dim, int max_period,
+                           float * out, void * stream);
+
 /* ---- a7, a9: varlen attention ---------------------------------------------------- */
 
 /* sparse_scaled_dot_product_attention / sparse_cross_attention
@@ -198,15 +236,16 @@ int pxs_activation(int dtype, void * x, int64_t count, int act, void * stream);
  * ld_* (elements).  cu_q/cu_k are device int64[nseg + 1]; total_q = cu_q[nseg].
  * row_map (nullable, device int32): logical row i is physical row row_map[i]
  * for q, k, v and o alike (window attention reads the permuted order without
- * moving rows).  head_dim must be 64 for PXS_BF16 (MFMA path) and <= 128 for
- * PXS_F32.  A segment with queries but no keys writes zeros.
+ * moving rows).  head_dim and value_dim (the per-head width of v and o) are
+ * 1..64; head_dim == value_dim == 64 in PXS_BF16 takes the fastest kernel.
+ * A segment with queries but no keys writes zeros.
  * workspace: pxs_attention_workspace_bytes(nseg). */
 size_t pxs_attention_workspace_bytes(int nseg);
 int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k, int64_t ld_k,
                          const void * v, int64_t ld_v, const int64_t * cu_q,
                          const int64_t * cu_k, int nseg, int64_t total_q,
-                         const int32_t * row_map, int heads, int head_dim, float scale, void * o,
-                         int64_t ld_o, void * workspace, void * stream);
+                         const int32_t * row_map, int heads, int head_dim, int value_dim,
+                         float scale, void * o, int64_t ld_o, void * workspace, void * stream);
 
 /* Per-batch cu_seqlens from the batch column (src/sparse.cpp:731-737):
  * cu (device int64[batch_size + 1]). */
@@ -227,6 +266,124 @@ int pxs_window_partition(const int32_t * coords, int64_t n, int batch_size, int 
                          int sz, int window, int shift, int32_t * fwd, int32_t * bwd,
                          int64_t * cu_seqlens, int64_t * nwin_out, void * workspace,
                          void * stream);
+
+/* ---- a13, a14: transformer block and SLat-flow forward, device resident ----------- */
+
+/* SparseTransformerBlockConfig (include/pixal3d/sparse_transformer.h:13-27). */
+typedef struct pxs_block_config {
+    int channels;
+    int num_heads;
+    int mlp_hidden;
+    int context_channels;
+    int proj_in_channels;
+    float norm_eps;
+    float rope_freq_min;
+    float rope_freq_base;
+    int use_rope;
+    int qk_rms_norm;
+    int qk_rms_norm_cross;
+    int use_projection;
+} pxs_block_config;
+
+/* SparseTransformerBlockWeightsF32 (include/pixal3d/sparse_transformer.h:29-53),
+ * as device pointers in the same order.  Linear weights ([out, in]) are in
+ * the call's dtype; modulation, biases, norm affines and RMS gammas are fp32.
+ * Optional members (RMS gammas, projection) may be NULL when the config does
+ * not use them. */
+typedef struct pxs_block_weights {
+    const float * modulation;
+    const void * self_to_qkv_weight;
+    const float * self_to_qkv_bias;
+    const float * self_q_gamma;
+    const float * self_k_gamma;
+    const void * self_to_out_weight;
+    const float * self_to_out_bias;
+    const float * norm2_weight;
+    const float * norm2_bias;
+    const void * cross_to_q_weight;
+    const float * cross_to_q_bias;
+    const void * cross_to_kv_weight;
+    const float * cross_to_kv_bias;
+    const float * cross_q_gamma;
+    const float * cross_k_gamma;
+    const void * cross_to_out_weight;
+    const float * cross_to_out_bias;
+    const void * proj_weight;
+    const float * proj_bias;
+    const void * mlp0_weight;
+    const float * mlp0_bias;
+    const void * mlp2_weight;
+    const float * mlp2_bias;
+} pxs_block_weights;
+
+/* sparse_transformer_cross_block_f32 (src/sparse_transformer.cpp:138-292) on
+ * device buffers.  hidden (fp32 [rows, C]) is the residual stream, updated in
+ * place; coords [rows, 4] contiguous by batch with per-batch bounds cu_rows
+ * (device int64[batch_size + 1]); time_mod fp32 [batch_size, 6C]; context
+ * (dtype [context_tokens, context_channels]) with context_offsets (device
+ * int64[batch_size + 1]); projected (dtype [rows, proj_in_channels]) only when
+ * cfg->use_projection.  Every batch must hold at least one row and one
+ * context token (the reference rejects empty key sequences).  GEMM operands
+ * are in dtype, accumulation and the residual stream in fp32. */
+size_t pxs_transformer_block_workspace_bytes(int dtype, const pxs_block_config * cfg,
+                                             int64_t rows, int64_t context_tokens,
+                                             int batch_size);
+int pxs_transformer_block(int dtype, const pxs_block_config * cfg, const pxs_block_weights * w,
+                          const int32_t * coords, int64_t rows, int batch_size,
+                          const int64_t * cu_rows, float * hidden, const float * time_mod,
+                          const void * context, const int64_t * context_offsets,
+                          int64_t context_tokens, const void * projected, void * workspace,
+                          void * stream);
+
+/* SLatFlowHParams (include/pixal3d/slat_flow.h:12-36) reduced to what the
+ * forward uses; mlp_hidden = model_channels * mlp_ratio. */
+typedef struct pxs_flow_config {
+    int in_channels;
+    int out_channels;
+    int model_channels;
+    int cond_channels;
+    int num_blocks;
+    int num_heads;
+    int proj_in_channels;
+    int mlp_hidden;
+    float norm_eps;
+    float rope_freq_min;
+    float rope_freq_base;
+    int qk_rms_norm;
+    int qk_rms_norm_cross;
+    int use_projection;
+} pxs_flow_config;
+
+/* SLatFlowWeightsF32 (include/pixal3d/slat_flow.h:38-50) as device pointers:
+ * input, timestep-MLP, adaLN and output layers in fp32; blocks is a host
+ * array of num_blocks block weight sets in the call's dtype. */
+typedef struct pxs_flow_weights {
+    const float * input_weight;
+    const float * input_bias;
+    const float * timestep_weight0;
+    const float * timestep_bias0;
+    const float * timestep_weight2;
+    const float * timestep_bias2;
+    const float * modulation_weight;
+    const float * modulation_bias;
+    const float * output_weight;
+    const float * output_bias;
+    const pxs_block_weights * blocks;
+} pxs_flow_weights;
+
+/* slat_flow_forward_f32 (src/slat_flow.cpp:161-249): input linear, 256-wide
+ * sinusoid -> Linear -> SiLU -> Linear -> SiLU -> adaLN Linear, num_blocks
+ * transformer blocks, layer norm (eps 1e-5) and output linear.  x fp32
+ * [rows, in_channels], timesteps device fp32 [batch_size], out fp32
+ * [rows, out_channels]; context / projected as for pxs_transformer_block. */
+size_t pxs_slat_flow_workspace_bytes(int dtype, const pxs_flow_config * cfg, int64_t rows,
+                                     int64_t context_tokens, int batch_size);
+int pxs_slat_flow_forward(int dtype, const pxs_flow_config * cfg, const pxs_flow_weights * w,
+                          const int32_t * coords, int64_t rows, int batch_size,
+                          const int64_t * cu_rows, const float * x, const float * timesteps,
+                          const void * context, const int64_t * context_offsets,
+                          int64_t context_tokens, const void * projected, float * out,
+                          void * workspace, void * stream);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 ORACLE_LIB = HERE / "build" / "liboracle.so"
 REF_LIB = HERE / "_ref" / "libpixal3d_ref.so"
+DROPIN_LIB = HERE / "build" / "libdropin_shim.so"
 
 # Validation codes of orc_sparse_valid -> the reference's messages
 # (src/sparse.cpp:249-330).
@@ -437,8 +438,11 @@ class Reference:
         L.ref_varlen_free.argtypes = [_vp]
         L.ref_varlen_shape.argtypes = [_vp, _i64p]
         L.ref_varlen_read.argtypes = [_vp, _f32p]
-        L.ref_cpu_thread_count.restype = C.c_int
-        L.ref_set_cpu_threads.argtypes = [C.c_int]
+        # The drop-in build of the shim has no thread or timestep entry points.
+        self.has_threads = hasattr(L, "ref_cpu_thread_count")
+        if self.has_threads:
+            L.ref_cpu_thread_count.restype = C.c_int
+            L.ref_set_cpu_threads.argtypes = [C.c_int]
         eb = [C.c_char_p, C.c_int]
         L.ref_sparse_valid.argtypes = [_vp] + eb
         L.ref_varlen_valid.argtypes = [_vp] + eb
@@ -456,9 +460,10 @@ class Reference:
         L.ref_sparse_submanifold_conv3d.argtypes = [_vp, _f32p, _f32p, C.c_int, _vp] + eb
         L.ref_transformer_block.argtypes = [_vp, _f32p, _vp, _vp, _intp, _f32p,
                                             C.POINTER(_f32p), _vp] + eb
-        L.ref_timestep_embedding.argtypes = [_f32p, C.c_int64, C.c_int, C.c_int, _f32p] + eb
-        L.ref_timestep_embed_mlp.argtypes = [_f32p, C.c_int64, C.c_int, C.c_int, _f32p, _f32p,
-                                             _f32p, _f32p, _f32p] + eb
+        if self.has_threads:
+            L.ref_timestep_embedding.argtypes = [_f32p, C.c_int64, C.c_int, C.c_int, _f32p] + eb
+            L.ref_timestep_embed_mlp.argtypes = [_f32p, C.c_int64, C.c_int, C.c_int, _f32p,
+                                                 _f32p, _f32p, _f32p, _f32p] + eb
         for name in ("ref_sparse_valid", "ref_varlen_valid", "ref_sparse_linear",
                      "ref_varlen_linear", "ref_sparse_layer_norm", "ref_sparse_downsample_mean",
                      "ref_sparse_channel_to_spatial", "ref_sparse_sdpa",
@@ -466,7 +471,8 @@ class Reference:
                      "ref_varlen_mh_rms_norm", "ref_sparse_submanifold_conv3d",
                      "ref_transformer_block", "ref_timestep_embedding",
                      "ref_timestep_embed_mlp"):
-            getattr(L, name).restype = C.c_int
+            if hasattr(L, name):
+                getattr(L, name).restype = C.c_int
 
     # -- handles ---------------------------------------------------------------
     def sparse(self, coords, feats, batch_size, shape, channels=None):
@@ -508,9 +514,14 @@ class Reference:
         ok = self.lib.ref_sparse_valid(t.h, err, 512)
         return bool(ok), err.value.decode()
 
-    def linear(self, t, weight, bias):
+    def varlen_valid(self, t: RefVarLen):
+        err = C.create_string_buffer(512)
+        ok = self.lib.ref_varlen_valid(t.h, err, 512)
+        return bool(ok), err.value.decode()
+
+    def linear(self, t, weight, bias, out=None):
         weight, bias = _f32(weight), _f32(bias)
-        out = self.empty()
+        out = self.empty() if out is None else out
         self._call("ref_sparse_linear", t.h, _p(weight, _f32p), _p(bias, _f32p), bias.size, out.h)
         return out
 
@@ -572,13 +583,14 @@ class Reference:
                    bias.size, out.h)
         return out
 
-    def transformer_block(self, t, t_mod, ctx: RefVarLen, cfg_i, cfg_f, weights, projected=None):
+    def transformer_block(self, t, t_mod, ctx: RefVarLen, cfg_i, cfg_f, weights, projected=None,
+                          out=None):
         t_mod = _f32(t_mod)
         cfg_i_a = (C.c_int * 9)(*cfg_i)
         cfg_f_a = (C.c_float * 3)(*cfg_f)
         keep = [None if w is None else _f32(w) for w in weights]
         wp = (_f32p * 23)(*[None if w is None else _p(w, _f32p) for w in keep])
-        out = self.empty()
+        out = self.empty() if out is None else out
         self._call("ref_transformer_block", t.h, _p(t_mod, _f32p), ctx.h,
                    None if projected is None else projected.h, cfg_i_a, cfg_f_a, wp, out.h)
         return out
@@ -597,3 +609,11 @@ class Reference:
         self._call("ref_timestep_embed_mlp", _p(t, _f32p), t.size, hidden, freq_dim,
                    *[_p(a, _f32p) for a in ws], _p(out, _f32p))
         return out
+
+
+class DropIn(Reference):
+    """The MI355X drop-in (libpxs.so) behind the same shim
+    (build/libdropin_shim.so).  Calls need a GPU; loading does not."""
+
+    def __init__(self, path: Path = DROPIN_LIB):
+        super().__init__(path)

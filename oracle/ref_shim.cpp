@@ -1,14 +1,22 @@
-// Test infrastructure only: a C-ABI shim over the reference's own CPU sparse
-// primitives, so the compiled reference (built from its sources under
-// /root/reference by oracle/Makefile, into oracle/_ref/) can be driven from
-// Python tests and timed as the reference CPU baseline.
+// Test infrastructure only: a C-ABI shim over the pixal3d sparse API, so a
+// C++ implementation of include/pixal3d/sparse.h and sparse_transformer.h can
+// be driven from Python tests.  oracle/Makefile builds it twice:
+//   * against the reference's own CPU primitives (compiled from their sources
+//     under /root/reference into oracle/_ref/), the compiled reference that
+//     pins the oracle and is timed as the reference CPU baseline;
+//   * with PXS_DROPIN_SHIM against this repository's drop-in headers and
+//     libpxs.so (into oracle/build/), so the same calls exercise the MI355X
+//     drop-in.  The reference-only entry points (CPU threads, timestep
+//     embedding) are left out of that build.
 //
 // Nothing in the shipped library links this file.  Each entry point forwards
-// to the reference function named in its comment; tensors cross the boundary
-// as opaque handles so a timed call pays no marshalling cost.
+// to the API function named in its comment; tensors cross the boundary as
+// opaque handles so a timed call pays no marshalling cost.
 
+#ifndef PXS_DROPIN_SHIM
 #include "pixal3d/flow.h"
 #include "pixal3d/cpu_threads.h"
+#endif
 #include "pixal3d/sparse.h"
 #include "pixal3d/sparse_transformer.h"
 
@@ -99,6 +107,7 @@ void ref_varlen_read(void * handle, float * feats) {
     std::memcpy(feats, t->feats.data(), t->feats.size() * sizeof(float));
 }
 
+#ifndef PXS_DROPIN_SHIM
 // ---- threads (src/cpu_threads.cpp) ---------------------------------------
 
 int ref_cpu_thread_count() { return pixal3d::cpu_thread_count(); }
@@ -106,6 +115,7 @@ void ref_set_cpu_threads(int threads) {
     if (threads > 0) pixal3d::set_cpu_thread_override(threads);
     else pixal3d::clear_cpu_thread_override();
 }
+#endif
 
 // ---- primitives (src/sparse.cpp) -----------------------------------------
 
@@ -254,6 +264,7 @@ int ref_transformer_block(void * in, const float * timestep_mod, void * context,
                   e, err, errlen);
 }
 
+#ifndef PXS_DROPIN_SHIM
 // ---- timestep embedding (src/flow.cpp) -----------------------------------
 
 int ref_timestep_embedding(const float * t, int64_t batch, int dim, int max_period,
@@ -276,5 +287,7 @@ int ref_timestep_embed_mlp(const float * t, int64_t batch, int hidden, int freq,
     if (ok) std::memcpy(out, v.data(), v.size() * sizeof(float));
     return finish(ok, e, err, errlen);
 }
+
+#endif
 
 } // extern "C"

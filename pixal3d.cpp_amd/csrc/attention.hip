@@ -515,17 +515,17 @@ size_t pxs_attention_workspace_bytes(int nseg) {
 int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k, int64_t ld_k,
                          const void * v, int64_t ld_v, const int64_t * cu_q,
                          const int64_t * cu_k, int nseg, int64_t total_q,
-                         const int32_t * row_map, int heads, int head_dim, float scale, void * o,
-                         int64_t ld_o, void * workspace, void * stream) {
+                         const int32_t * row_map, int heads, int head_dim, int value_dim,
+                         float scale, void * o, int64_t ld_o, void * workspace, void * stream) {
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_varlen_attention: bad dtype");
-    PXS_CHECK(heads > 0 && head_dim > 0 && head_dim <= 64, PXS_ERR_ARG,
-              "pxs_varlen_attention: head_dim must be in 1..64");
+    PXS_CHECK(heads > 0 && head_dim > 0 && head_dim <= 64 && value_dim > 0 && value_dim <= 64,
+              PXS_ERR_ARG, "pxs_varlen_attention: head_dim and value_dim must be in 1..64");
     PXS_CHECK(heads <= 65535, PXS_ERR_ARG, "pxs_varlen_attention: too many heads");
     PXS_CHECK(scale > 0.0f && std::isfinite(scale), PXS_ERR_ARG,
               "sparse attention scale must be finite and positive");
     PXS_CHECK(nseg >= 0 && total_q >= 0, PXS_ERR_ARG, "pxs_varlen_attention: bad segment count");
-    PXS_CHECK(ld_q >= heads * head_dim && ld_k >= heads * head_dim && ld_v >= heads * head_dim &&
-                  ld_o >= heads * head_dim,
+    PXS_CHECK(ld_q >= heads * head_dim && ld_k >= heads * head_dim && ld_v >= heads * value_dim &&
+                  ld_o >= heads * value_dim,
               PXS_ERR_ARG, "pxs_varlen_attention: row stride smaller than heads * head_dim");
     if (nseg == 0 || total_q == 0) return PXS_OK;
     PXS_CHECK(q && k && v && o && cu_q && cu_k && workspace, PXS_ERR_ARG,
@@ -544,13 +544,13 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     AttnArgs a{};
     a.q = q; a.k = k; a.v = v; a.ldq = ld_q; a.ldk = ld_k; a.ldv = ld_v;
     a.cu_q = cu_q; a.cu_k = cu_k; a.nseg = nseg; a.tile_start = tile_start;
-    a.row_map = row_map; a.hd = head_dim; a.vd = head_dim;
+    a.row_map = row_map; a.hd = head_dim; a.vd = value_dim;
     a.scale_log2 = scale * kLog2e; a.o = o; a.ldo = ld_o;
     const int vec = dtype == PXS_BF16 ? 8 : 4;
-    a.vec_ok = (head_dim % vec == 0) && (ld_q % vec == 0) && (ld_k % vec == 0) &&
+    a.vec_ok = (head_dim % vec == 0) && (value_dim % vec == 0) && (ld_q % vec == 0) && (ld_k % vec == 0) &&
                (ld_v % vec == 0) && aligned16(q) && aligned16(k) && aligned16(v);
     if (dtype == PXS_BF16) {
-        const bool fast = head_dim == 64 && (ld_q % 8 == 0) && (ld_k % 8 == 0) &&
+        const bool fast = head_dim == 64 && value_dim == 64 && (ld_q % 8 == 0) && (ld_k % 8 == 0) &&
                           (ld_v % 8 == 0) && (ld_o % 4 == 0) && aligned16(q) && aligned16(k) &&
                           aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0;
         if (fast) {

@@ -27,7 +27,7 @@ constexpr int kGemmThreads = 256;
 constexpr int kChunkBytes = 128;
 constexpr int kPitch = kChunkBytes + 16;
 
-enum Epilogue { kEpiStore = 0, kEpiGateResidual = 1 };
+enum Epilogue { kEpiStore = 0, kEpiGateResidual = 1, kEpiAddResidual = 2 };
 
 struct GemmArgs {
     const void * x;
@@ -109,6 +109,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs & a, const f32x16 (
                     if (a.act == PXS_ACT_GELU_TANH) val = gelu_tanh_f(val);
                     else if (a.act == PXS_ACT_SILU) val = silu_f(val);
                     store_f32(static_cast<T *>(a.y) + row * a.ldy + col, val);
+                } else if constexpr (EPI == kEpiAddResidual) {
+                    float * res = a.residual + row * a.cout + col;
+                    *res = *res + val;
                 } else {
                     const int batch = a.coords[row * 4];
                     const float g = a.block_mod[a.gate_offset + col] +
@@ -637,41 +640,32 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
     args.vec_ok = (args.cin % vec == 0) && (args.ldx % vec == 0) && aligned16(args.x) &&
                   aligned16(args.w);
     if (dtype == PXS_BF16) {
-        return epi == kEpiStore ? dispatch<uint16_t, kEpiStore>(args, stream)
-                                : dispatch<uint16_t, kEpiGateResidual>(args, stream);
+        if (epi == kEpiStore) return dispatch<uint16_t, kEpiStore>(args, stream);
+        if (epi == kEpiAddResidual) return dispatch<uint16_t, kEpiAddResidual>(args, stream);
+        return dispatch<uint16_t, kEpiGateResidual>(args, stream);
     }
-    return epi == kEpiStore ? dispatch<float, kEpiStore>(args, stream)
-                            : dispatch<float, kEpiGateResidual>(args, stream);
+    if (epi == kEpiStore) return dispatch<float, kEpiStore>(args, stream);
+    if (epi == kEpiAddResidual) return dispatch<float, kEpiAddResidual>(args, stream);
+    return dispatch<float, kEpiGateResidual>(args, stream);
 }
 
-// Mean of present children in ascending input-row order (the order the
-// reference's per-group sums visit rows).
+// Mean of each group's rows, summed in the group's (ascending) row order, the
+// order src/sparse.cpp:566-572 accumulates them; then one division
+// (src/sparse.cpp:594-597).
 template <typename T>
 __global__ void downsample_mean_kernel(const T * __restrict__ x, int channels,
-                                       const int32_t * __restrict__ child_map, int64_t ld_map,
-                                       int64_t m, T * __restrict__ y) {
+                                       const int64_t * __restrict__ offsets,
+                                       const int32_t * __restrict__ rows, int64_t m,
+                                       T * __restrict__ y) {
     const int64_t q = blockIdx.x;
     if (q >= m) return;
-    int32_t rows[8];
-    int count = 0;
-    for (int c = 0; c < 8; ++c) {
-        const int32_t r = child_map[c * ld_map + q];
-        if (r >= 0) rows[count++] = r;
-    }
-    // insertion sort (<= 8 entries)
-    for (int i = 1; i < count; ++i) {
-        const int32_t v = rows[i];
-        int j = i - 1;
-        while (j >= 0 && rows[j] > v) {
-            rows[j + 1] = rows[j];
-            --j;
-        }
-        rows[j + 1] = v;
-    }
+    const int64_t begin = offsets[q], end = offsets[q + 1];
     for (int ch = threadIdx.x; ch < channels; ch += blockDim.x) {
         float s = 0.0f;
-        for (int i = 0; i < count; ++i) s += load_f32(x + static_cast<int64_t>(rows[i]) * channels + ch);
-        store_f32(y + q * channels + ch, s / static_cast<float>(count));
+        for (int64_t i = begin; i < end; ++i) {
+            s += load_f32(x + static_cast<int64_t>(rows[i]) * channels + ch);
+        }
+        store_f32(y + q * channels + ch, s / static_cast<float>(end - begin));
     }
 }
 
@@ -745,24 +739,37 @@ int pxs_linear_gate_residual(int dtype, const void * x, int64_t rows, int cin,
     return run_gemm(dtype, a, kEpiGateResidual, as_stream(stream));
 }
 
-int pxs_downsample_mean_s2(int dtype, const void * x, int channels, const int32_t * child_map,
-                           int64_t ld_map, int64_t m, void * y, void * stream) {
-    if (int rc = check_dtype(dtype, "pxs_downsample_mean_s2")) return rc;
-    PXS_CHECK(channels > 0 && m >= 0 && ld_map >= m, PXS_ERR_ARG, "pxs_downsample_mean_s2: bad shape");
+int pxs_linear_residual(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+                        const float * bias, int cout, float * residual, void * stream) {
+    if (int rc = check_dtype(dtype, "pxs_linear_residual")) return rc;
+    PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear_residual: bad shape");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x && weight && residual, PXS_ERR_ARG, "pxs_linear_residual: null pointer");
+    GemmArgs a{};
+    a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
+    a.cout = cout; a.m = rows; a.noff = 1; a.y = nullptr; a.ldy = cout; a.residual = residual;
+    return run_gemm(dtype, a, kEpiAddResidual, as_stream(stream));
+}
+
+int pxs_downsample_mean(int dtype, const void * x, int channels, const int64_t * group_offsets,
+                        const int32_t * group_rows, int64_t m, void * y, void * stream) {
+    if (int rc = check_dtype(dtype, "pxs_downsample_mean")) return rc;
+    PXS_CHECK(channels > 0 && m >= 0 && m <= INT32_MAX, PXS_ERR_ARG,
+              "pxs_downsample_mean: bad shape");
     if (m == 0) return PXS_OK;
-    PXS_CHECK(x && child_map && y, PXS_ERR_ARG, "pxs_downsample_mean_s2: null pointer");
-    PXS_CHECK(m <= INT32_MAX, PXS_ERR_ARG, "pxs_downsample_mean_s2: too many rows");
+    PXS_CHECK(x && group_offsets && group_rows && y, PXS_ERR_ARG,
+              "pxs_downsample_mean: null pointer");
     const int threads = channels >= 256 ? 256 : 64;
     if (dtype == PXS_F32) {
         hipLaunchKernelGGL(downsample_mean_kernel<float>, dim3(static_cast<unsigned>(m)),
                            dim3(threads), 0, as_stream(stream), static_cast<const float *>(x),
-                           channels, child_map, ld_map, m, static_cast<float *>(y));
+                           channels, group_offsets, group_rows, m, static_cast<float *>(y));
     } else {
         hipLaunchKernelGGL(downsample_mean_kernel<uint16_t>, dim3(static_cast<unsigned>(m)),
                            dim3(threads), 0, as_stream(stream), static_cast<const uint16_t *>(x),
-                           channels, child_map, ld_map, m, static_cast<uint16_t *>(y));
+                           channels, group_offsets, group_rows, m, static_cast<uint16_t *>(y));
     }
-    return check_launch("pxs_downsample_mean_s2");
+    return check_launch("pxs_downsample_mean");
 }
 
 } // extern "C"

@@ -194,6 +194,49 @@ __global__ void activation_kernel(T * __restrict__ x, int64_t count, int act) {
     }
 }
 
+// First non-finite element: status = row * 8 + 7 (the code pxs_sparse_validate
+// uses for features), min-reduced over rows.
+template <typename T>
+__global__ void check_finite_kernel(const T * __restrict__ x, int64_t rows, int channels,
+                                    int64_t ld, unsigned long long * __restrict__ status) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    const int64_t count = rows * channels;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride) {
+        const int64_t r = i / channels;
+        const float v = load_f32(x + r * ld + (i - r * channels));
+        if (!isfinite(v)) atomicMin(status, static_cast<unsigned long long>(r * 8 + 7));
+    }
+}
+
+template <typename TS, typename TD>
+__global__ void convert_kernel(const TS * __restrict__ x, int64_t count, TD * __restrict__ y) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride) {
+        store_f32(y + i, load_f32(x + i));
+    }
+}
+
+// Sinusoidal timestep embedding (src/flow.cpp:92-123): cos half then sin
+// half, frequency exp(-ln(max_period) * i / half); a trailing odd column is 0.
+__global__ void timestep_embedding_kernel(const float * __restrict__ t, int64_t batch, int dim,
+                                          float log_period, float * __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int half = dim / 2;
+    if (i >= batch * dim) return;
+    const int64_t row = i / dim;
+    const int col = static_cast<int>(i - row * dim);
+    float v = 0.0f;
+    if (col < 2 * half) {
+        const int idx = col < half ? col : col - half;
+        const float fraction = static_cast<float>(idx) / static_cast<float>(half);
+        const float arg = t[row] * expf(-log_period * fraction);
+        v = col < half ? cosf(arg) : sinf(arg);
+    }
+    out[i] = v;
+}
+
 int check_dtype(int dtype) { return dtype == PXS_F32 || dtype == PXS_BF16; }
 
 template <typename TX, typename TY, bool kMod>
@@ -312,10 +355,11 @@ int pxs_qkv_prepare(int dtype, const void * qkv, int64_t rows, int heads, int he
                     float freq_min, float freq_base, void * q, void * k, void * v,
                     void * stream) {
     PXS_CHECK(check_dtype(dtype), PXS_ERR_ARG, "pxs_qkv_prepare: bad dtype");
-    PXS_CHECK(rows >= 0 && heads > 0 && head_dim > 0 && head_dim % 2 == 0, PXS_ERR_ARG,
-              "pxs_qkv_prepare: bad shape");
+    PXS_CHECK(rows >= 0 && heads > 0 && head_dim > 0 && (head_dim % 2 == 0 || !coords),
+              PXS_ERR_ARG, "pxs_qkv_prepare: bad shape");
     PXS_CHECK((q_gamma == nullptr) == (k_gamma == nullptr), PXS_ERR_ARG,
               "pxs_qkv_prepare: q_gamma and k_gamma must be both set or both null");
+    PXS_CHECK(head_dim / 2 / 3 <= 32, PXS_ERR_ARG, "pxs_qkv_prepare: head_dim above 192 unsupported");
     if (rows == 0) return PXS_OK;
     PXS_CHECK(qkv && q && k && v, PXS_ERR_ARG, "pxs_qkv_prepare: null pointer");
     hipStream_t s = as_stream(stream);
@@ -377,6 +421,65 @@ int pxs_activation(int dtype, void * x, int64_t count, int act, void * stream) {
                            as_stream(stream), static_cast<uint16_t *>(x), count, act);
     }
     return check_launch("pxs_activation");
+}
+
+int pxs_check_finite(int dtype, const void * x, int64_t rows, int channels, int64_t ld,
+                     int64_t * status, void * stream) {
+    PXS_CHECK(check_dtype(dtype), PXS_ERR_ARG, "pxs_check_finite: bad dtype");
+    PXS_CHECK(rows >= 0 && channels > 0 && ld >= channels, PXS_ERR_ARG,
+              "pxs_check_finite: bad shape");
+    PXS_CHECK(status, PXS_ERR_ARG, "pxs_check_finite: null status");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x, PXS_ERR_ARG, "pxs_check_finite: null pointer");
+    const unsigned blocks =
+        static_cast<unsigned>(std::min<int64_t>((rows * channels + 255) / 256, 4096));
+    auto * st = reinterpret_cast<unsigned long long *>(status);
+    if (dtype == PXS_F32) {
+        hipLaunchKernelGGL(check_finite_kernel<float>, dim3(blocks), dim3(256), 0,
+                           as_stream(stream), static_cast<const float *>(x), rows, channels, ld, st);
+    } else {
+        hipLaunchKernelGGL(check_finite_kernel<uint16_t>, dim3(blocks), dim3(256), 0,
+                           as_stream(stream), static_cast<const uint16_t *>(x), rows, channels, ld,
+                           st);
+    }
+    return check_launch("pxs_check_finite");
+}
+
+int pxs_convert(int src_dtype, const void * x, int64_t count, int dst_dtype, void * y,
+                void * stream) {
+    PXS_CHECK(check_dtype(src_dtype) && check_dtype(dst_dtype), PXS_ERR_ARG,
+              "pxs_convert: bad dtype");
+    PXS_CHECK(count >= 0, PXS_ERR_ARG, "pxs_convert: negative count");
+    if (count == 0) return PXS_OK;
+    PXS_CHECK(x && y, PXS_ERR_ARG, "pxs_convert: null pointer");
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
+    hipStream_t s = as_stream(stream);
+    if (src_dtype == PXS_F32 && dst_dtype == PXS_BF16) {
+        hipLaunchKernelGGL((convert_kernel<float, uint16_t>), dim3(blocks), dim3(256), 0, s,
+                           static_cast<const float *>(x), count, static_cast<uint16_t *>(y));
+    } else if (src_dtype == PXS_BF16 && dst_dtype == PXS_F32) {
+        hipLaunchKernelGGL((convert_kernel<uint16_t, float>), dim3(blocks), dim3(256), 0, s,
+                           static_cast<const uint16_t *>(x), count, static_cast<float *>(y));
+    } else if (src_dtype == PXS_F32) {
+        hipLaunchKernelGGL((convert_kernel<float, float>), dim3(blocks), dim3(256), 0, s,
+                           static_cast<const float *>(x), count, static_cast<float *>(y));
+    } else {
+        hipLaunchKernelGGL((convert_kernel<uint16_t, uint16_t>), dim3(blocks), dim3(256), 0, s,
+                           static_cast<const uint16_t *>(x), count, static_cast<uint16_t *>(y));
+    }
+    return check_launch("pxs_convert");
+}
+
+int pxs_timestep_embedding(const float * timesteps, int64_t batch, int dim, int max_period,
+                           float * out, void * stream) {
+    PXS_CHECK(batch >= 0 && dim > 0 && max_period > 0, PXS_ERR_ARG,
+              "pxs_timestep_embedding: bad shape");
+    if (batch == 0) return PXS_OK;
+    PXS_CHECK(timesteps && out, PXS_ERR_ARG, "pxs_timestep_embedding: null pointer");
+    const float log_period = static_cast<float>(std::log(static_cast<double>(max_period)));
+    hipLaunchKernelGGL(timestep_embedding_kernel, dim3(grid_for(batch * dim, 256)), dim3(256), 0,
+                       as_stream(stream), timesteps, batch, dim, log_period, out);
+    return check_launch("pxs_timestep_embedding");
 }
 
 } // extern "C"

@@ -201,20 +201,30 @@ __global__ void pair_offsets_kernel(const int64_t * __restrict__ base, int64_t b
     if (k == 27) offsets28[27] = *total;
 }
 
-// ---- stride-2 topology via an occupancy bitmap over the coarse grid -------
-// The dense linearisation ((b*cx + x)*cy + y)*cz + z is lexicographic, so a
-// popcount prefix over the bitmap ranks occupied coarse cells in exactly the
-// order the reference sorts them.
-__global__ void coarse_mark_kernel(const int4 * __restrict__ coords, int64_t n, int cx, int cy,
-                                   int cz, uint32_t * __restrict__ bitmap) {
+// ---- factor-f topology via an occupancy bitmap over the coarse grid -------
+// The dense linearisation ((b*cx + x/f)*cy + y/f)*cz + z/f is lexicographic,
+// so a popcount prefix over the bitmap ranks occupied coarse cells in exactly
+// the order the reference sorts them (src/sparse.cpp:575-580).
+__device__ __forceinline__ int64_t coarse_cell(int4 c, int f, int cx, int cy, int cz) {
+    return ((static_cast<int64_t>(c.x) * cx + c.y / f) * cy + c.z / f) * cz + c.w / f;
+}
+
+__global__ void coarse_mark_kernel(const int4 * __restrict__ coords, int64_t n, int f, int cx,
+                                   int cy, int cz, uint32_t * __restrict__ bitmap) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= n) return;
-    const int4 c = coords[p];
-    const int64_t cell = ((static_cast<int64_t>(c.x) * cx + (c.y >> 1)) * cy + (c.z >> 1)) * cz +
-                         (c.w >> 1);
+    const int64_t cell = coarse_cell(coords[p], f, cx, cy, cz);
     atomicOr(bitmap + (cell >> 5), 1u << (cell & 31));
 }
 
+__device__ __forceinline__ int64_t coarse_rank(int64_t cell, const uint32_t * __restrict__ bitmap,
+                                               const int64_t * __restrict__ word_prefix) {
+    const int64_t w = cell >> 5;
+    const uint32_t bit = static_cast<uint32_t>(cell & 31);
+    return word_prefix[w] + __popc(bitmap[w] & ((1u << bit) - 1u));
+}
+
+// Factor 2: child c = (x&1) + 2(y&1) + 4(z&1) of output q is row child_map[c*n + q].
 __global__ void coarse_emit_kernel(const int4 * __restrict__ coords, int64_t n, int cx, int cy,
                                    int cz, const uint32_t * __restrict__ bitmap,
                                    const int64_t * __restrict__ word_prefix,
@@ -222,15 +232,55 @@ __global__ void coarse_emit_kernel(const int4 * __restrict__ coords, int64_t n, 
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= n) return;
     const int4 c = coords[p];
-    const int64_t cell = ((static_cast<int64_t>(c.x) * cx + (c.y >> 1)) * cy + (c.z >> 1)) * cz +
-                         (c.w >> 1);
-    const int64_t w = cell >> 5;
-    const uint32_t bit = static_cast<uint32_t>(cell & 31);
-    const int64_t rank = word_prefix[w] + __popc(bitmap[w] & ((1u << bit) - 1u));
+    const int64_t rank = coarse_rank(coarse_cell(c, 2, cx, cy, cz), bitmap, word_prefix);
     const int child = (c.y & 1) + 2 * (c.z & 1) + 4 * (c.w & 1);
     child_map[static_cast<int64_t>(child) * n + rank] = static_cast<int32_t>(p);
     // Every child of the cell writes the same coarse coordinate.
     out_coords[rank] = make_int4(c.x, c.y >> 1, c.z >> 1, c.w >> 1);
+}
+
+// Any factor: group rows by output cell.  Pass 1 ranks each row's cell and
+// takes a slot in its group (atomic, so slot order is arbitrary); pass 2
+// places rows; pass 3 sorts each group by row so a group lists its rows in
+// ascending input order, the order the reference accumulates them
+// (src/sparse.cpp:553-573).
+__global__ void group_assign_kernel(const int4 * __restrict__ coords, int64_t n, int f, int cx,
+                                    int cy, int cz, const uint32_t * __restrict__ bitmap,
+                                    const int64_t * __restrict__ word_prefix,
+                                    int4 * __restrict__ out_coords, int32_t * __restrict__ group_of,
+                                    int32_t * __restrict__ counts, int32_t * __restrict__ slot) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    const int64_t q = coarse_rank(coarse_cell(c, f, cx, cy, cz), bitmap, word_prefix);
+    group_of[p] = static_cast<int32_t>(q);
+    slot[p] = atomicAdd(counts + q, 1);
+    out_coords[q] = make_int4(c.x, c.y / f, c.z / f, c.w / f);
+}
+
+__global__ void group_place_kernel(int64_t n, const int32_t * __restrict__ group_of,
+                                   const int32_t * __restrict__ slot,
+                                   const int64_t * __restrict__ offsets,
+                                   int32_t * __restrict__ rows) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    rows[offsets[group_of[p]] + slot[p]] = static_cast<int32_t>(p);
+}
+
+__global__ void group_sort_kernel(int64_t groups, const int64_t * __restrict__ offsets,
+                                  int32_t * __restrict__ rows) {
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (q >= groups) return;
+    const int64_t begin = offsets[q], end = offsets[q + 1];
+    for (int64_t i = begin + 1; i < end; ++i) {
+        const int32_t v = rows[i];
+        int64_t j = i - 1;
+        while (j >= begin && rows[j] > v) {
+            rows[j + 1] = rows[j];
+            --j;
+        }
+        rows[j + 1] = v;
+    }
 }
 
 // ---- window partition (counting sort by window id, stable per window) -----
@@ -327,47 +377,49 @@ __global__ void batch_cu_kernel(const int4 * __restrict__ coords, int64_t n, int
     }
 }
 
-// ---- channel to spatial (factor 2) --------------------------------------------
-__global__ void c2s_count_kernel(const float * __restrict__ sub, int64_t n,
+// ---- channel to spatial (factor f, cc = f^3 children) --------------------------
+__global__ void c2s_count_kernel(const float * __restrict__ sub, int64_t n, int cc,
                                  int32_t * __restrict__ counts) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= n) return;
     int c = 0;
-    for (int j = 0; j < 8; ++j) c += sub[p * 8 + j] > 0.0f ? 1 : 0;
+    for (int j = 0; j < cc; ++j) c += sub[p * cc + j] > 0.0f ? 1 : 0;
     counts[p] = c;
 }
 
 // One thread per (parent, child); the channel copy is done by the feature
-// kernel below with 16-byte vectors.
-__global__ void c2s_coords_kernel(const int4 * __restrict__ coords, int64_t n,
+// kernel below.  Child c sits at (c % f, (c / f) % f, c / f^2) inside the
+// parent (src/sparse.cpp:682-686).
+__global__ void c2s_coords_kernel(const int4 * __restrict__ coords, int64_t n, int f, int cc,
                                   const float * __restrict__ sub,
                                   const int64_t * __restrict__ prefix,
                                   int4 * __restrict__ out_coords, int64_t * __restrict__ src_of) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t >= n * 8) return;
-    const int64_t p = t >> 3;
-    const int child = static_cast<int>(t & 7);
+    if (t >= n * cc) return;
+    const int64_t p = t / cc;
+    const int child = static_cast<int>(t - p * cc);
     int64_t dst;
     if (sub) {
-        if (!(sub[p * 8 + child] > 0.0f)) return;
+        if (!(sub[p * cc + child] > 0.0f)) return;
         int before = 0;
-        for (int j = 0; j < child; ++j) before += sub[p * 8 + j] > 0.0f ? 1 : 0;
+        for (int j = 0; j < child; ++j) before += sub[p * cc + j] > 0.0f ? 1 : 0;
         dst = prefix[p] + before;
     } else {
         dst = t;
     }
     const int4 c = coords[p];
-    out_coords[dst] = make_int4(c.x, 2 * c.y + (child & 1), 2 * c.z + ((child >> 1) & 1),
-                                2 * c.w + (child >> 2));
-    src_of[dst] = t;  // source (parent * 8 + child)
+    out_coords[dst] = make_int4(c.x, f * c.y + child % f, f * c.z + (child / f) % f,
+                                f * c.w + child / (f * f));
+    src_of[dst] = t;  // source (parent * cc + child)
 }
 
 template <typename T>
-__global__ void c2s_feats_kernel(const T * __restrict__ x, int channels, const int64_t * __restrict__ src_of,
+__global__ void c2s_feats_kernel(const T * __restrict__ x, int channels, int cc,
+                                 const int64_t * __restrict__ src_of,
                                  const int64_t * __restrict__ m_dev, int64_t m_max,
                                  T * __restrict__ y) {
-    // channels = 8 * c_out; the child slice of parent p is channels / 8 wide.
-    const int c_out = channels / 8;
+    // The child slice of parent p is channels / cc wide.
+    const int c_out = channels / cc;
     const int64_t m = m_dev ? *m_dev : m_max;
     const int64_t total = m * c_out;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -376,7 +428,8 @@ __global__ void c2s_feats_kernel(const T * __restrict__ x, int channels, const i
         const int64_t r = i / c_out;
         const int ch = static_cast<int>(i - r * c_out);
         const int64_t s = src_of[r];
-        y[i] = x[(s >> 3) * channels + (s & 7) * c_out + ch];
+        const int64_t parent = s / cc;
+        y[i] = x[parent * channels + (s - parent * cc) * c_out + ch];
     }
 }
 
@@ -442,6 +495,12 @@ int pxs_sparse_validate(const int32_t * coords, int64_t n, int batch_size, int s
     return check_launch("pxs_sparse_validate");
 }
 
+int pxs_status_reset(int64_t * status, void * stream) {
+    PXS_CHECK(status != nullptr, PXS_ERR_ARG, "pxs_status_reset: null status");
+    hipLaunchKernelGGL(status_init_kernel, dim3(1), dim3(1), 0, as_stream(stream), status);
+    return check_launch("pxs_status_reset");
+}
+
 const char * pxs_validation_message(int code) {
     switch (code) {
     case 1: return "invalid sparse tensor shape";
@@ -500,13 +559,41 @@ int pxs_neighbor_pairs(const int32_t * nbr, int64_t n, int32_t * pair_in, int32_
     return check_launch("pxs_neighbor_pairs");
 }
 
-size_t pxs_downsample_workspace_bytes(int batch_size, int sx, int sy, int sz) {
-    const int64_t cells = static_cast<int64_t>(std::max(batch_size, 1)) * ((sx + 1) / 2) *
-                          ((sy + 1) / 2) * ((sz + 1) / 2);
+size_t pxs_downsample_workspace_bytes(int64_t n, int batch_size, int sx, int sy, int sz,
+                                      int factor) {
+    if (factor <= 0) return 0;
+    const int64_t cells = static_cast<int64_t>(std::max(batch_size, 1)) *
+                          ((sx + factor - 1) / factor) * ((sy + factor - 1) / factor) *
+                          ((sz + factor - 1) / factor);
     const int64_t words = (cells + 31) / 32;
+    const int64_t rows = std::max<int64_t>(n, 1);
     return static_cast<size_t>(words) * (sizeof(uint32_t) + sizeof(int64_t)) +
-           scan_workspace_bytes(words) + 64;
+           static_cast<size_t>(rows) * 3 * sizeof(int32_t) +
+           scan_workspace_bytes(std::max(words, rows)) + 128;
 }
+
+namespace {
+struct CoarseGrid {
+    int cx, cy, cz;
+    int64_t words;
+    uint32_t * bitmap;
+    int64_t * prefix;
+    char * rest;  // 8-byte aligned scratch after the bitmap scan
+};
+
+CoarseGrid coarse_grid(void * workspace, int batch_size, int sx, int sy, int sz, int f) {
+    CoarseGrid g;
+    g.cx = (sx + f - 1) / f;
+    g.cy = (sy + f - 1) / f;
+    g.cz = (sz + f - 1) / f;
+    g.words = (static_cast<int64_t>(batch_size) * g.cx * g.cy * g.cz + 31) / 32;
+    g.bitmap = static_cast<uint32_t *>(workspace);
+    g.prefix = reinterpret_cast<int64_t *>(
+        (reinterpret_cast<uintptr_t>(g.bitmap + g.words) + 7) & ~uintptr_t(7));
+    g.rest = reinterpret_cast<char *>(g.prefix + g.words);
+    return g;
+}
+} // namespace
 
 int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size, int sx,
                                int sy, int sz, int32_t * out_coords, int32_t * child_map,
@@ -519,25 +606,64 @@ int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size
     if (n == 0) return fill_i64(m_out, 1, 0, s);
     PXS_CHECK(coords && out_coords && child_map, PXS_ERR_ARG,
               "pxs_downsample_s2_topology: null pointer");
-    const int cx = (sx + 1) / 2, cy = (sy + 1) / 2, cz = (sz + 1) / 2;
-    const int64_t cells = static_cast<int64_t>(batch_size) * cx * cy * cz;
-    const int64_t words = (cells + 31) / 32;
-    uint32_t * bitmap = static_cast<uint32_t *>(workspace);
-    int64_t * prefix = reinterpret_cast<int64_t *>(
-        (reinterpret_cast<uintptr_t>(bitmap + words) + 7) & ~uintptr_t(7));
-    void * scan_ws = prefix + words;
-    int rc = fill_u32(bitmap, words, 0u, s);
+    const CoarseGrid g = coarse_grid(workspace, batch_size, sx, sy, sz, 2);
+    int rc = fill_u32(g.bitmap, g.words, 0u, s);
     if (rc) return rc;
     rc = fill_i32(child_map, 8 * n, -1, s);
     if (rc) return rc;
     hipLaunchKernelGGL(coarse_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
-                       reinterpret_cast<const int4 *>(coords), n, cx, cy, cz, bitmap);
-    rc = exclusive_scan_popcount(bitmap, prefix, words, m_out, scan_ws, s);
+                       reinterpret_cast<const int4 *>(coords), n, 2, g.cx, g.cy, g.cz, g.bitmap);
+    rc = exclusive_scan_popcount(g.bitmap, g.prefix, g.words, m_out, g.rest, s);
     if (rc) return rc;
     hipLaunchKernelGGL(coarse_emit_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
-                       reinterpret_cast<const int4 *>(coords), n, cx, cy, cz, bitmap, prefix,
-                       reinterpret_cast<int4 *>(out_coords), child_map);
+                       reinterpret_cast<const int4 *>(coords), n, g.cx, g.cy, g.cz, g.bitmap,
+                       g.prefix, reinterpret_cast<int4 *>(out_coords), child_map);
     return check_launch("pxs_downsample_s2_topology");
+}
+
+int pxs_downsample_topology(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                            int sz, int factor, int32_t * out_coords, int64_t * group_offsets,
+                            int32_t * group_rows, int64_t * m_out, void * workspace,
+                            void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_downsample_topology: bad row count");
+    PXS_CHECK(factor > 0, PXS_ERR_ARG, "sparse downsample factor must be positive");
+    PXS_CHECK(batch_size > 0 && sx > 0 && sy > 0 && sz > 0, PXS_ERR_ARG,
+              "pxs_downsample_topology: invalid shape");
+    PXS_CHECK(m_out && group_offsets && workspace, PXS_ERR_ARG,
+              "pxs_downsample_topology: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) {
+        int rc = fill_i64(m_out, 1, 0, s);
+        return rc ? rc : fill_i64(group_offsets, 1, 0, s);
+    }
+    PXS_CHECK(coords && out_coords && group_rows, PXS_ERR_ARG,
+              "pxs_downsample_topology: null pointer");
+    const CoarseGrid g = coarse_grid(workspace, batch_size, sx, sy, sz, factor);
+    int32_t * group_of = reinterpret_cast<int32_t *>(g.rest);
+    int32_t * slot = group_of + n;
+    int32_t * counts = slot + n;
+    void * scan_ws = reinterpret_cast<void *>(
+        (reinterpret_cast<uintptr_t>(counts + n) + 7) & ~uintptr_t(7));
+    const int4 * c4 = reinterpret_cast<const int4 *>(coords);
+    int rc = fill_u32(g.bitmap, g.words, 0u, s);
+    if (rc) return rc;
+    rc = fill_i32(counts, n, 0, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(coarse_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
+                       n, factor, g.cx, g.cy, g.cz, g.bitmap);
+    rc = exclusive_scan_popcount(g.bitmap, g.prefix, g.words, m_out, scan_ws, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(group_assign_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
+                       n, factor, g.cx, g.cy, g.cz, g.bitmap, g.prefix,
+                       reinterpret_cast<int4 *>(out_coords), group_of, counts, slot);
+    // counts past the last group are zero, so offsets[m .. n] all equal n.
+    rc = exclusive_scan_i32(counts, group_offsets, n, group_offsets + n, scan_ws, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(group_place_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, n,
+                       group_of, slot, group_offsets, group_rows);
+    hipLaunchKernelGGL(group_sort_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, n,
+                       group_offsets, group_rows);
+    return check_launch("pxs_downsample_topology");
 }
 
 size_t pxs_window_partition_workspace_bytes(int batch_size, int sx, int sy, int sz, int window,
@@ -615,51 +741,58 @@ int pxs_batch_cu_seqlens(const int32_t * coords, int64_t n, int batch_size, int6
     return check_launch("pxs_batch_cu_seqlens");
 }
 
-size_t pxs_channel_to_spatial_workspace_bytes(int64_t n) {
+size_t pxs_channel_to_spatial_workspace_bytes(int64_t n, int factor) {
+    if (factor <= 0 || factor > 1024) return 0;
+    const int64_t cc = static_cast<int64_t>(factor) * factor * factor;
     const int64_t rows = std::max<int64_t>(n, 1);
     return static_cast<size_t>(rows) * (sizeof(int32_t) + sizeof(int64_t)) +
-           static_cast<size_t>(rows) * 8 * sizeof(int64_t) + scan_workspace_bytes(rows) + 64;
+           static_cast<size_t>(rows * cc) * sizeof(int64_t) + scan_workspace_bytes(rows) + 64;
 }
 
 int pxs_channel_to_spatial(int dtype, const int32_t * coords, int64_t n, const void * x,
-                           int channels, const float * subdivision, int32_t * out_coords,
-                           void * y, int64_t * m_out, void * workspace, void * stream) {
-    PXS_CHECK(n >= 0 && n <= INT_MAX / 8, PXS_ERR_ARG, "pxs_channel_to_spatial: bad row count");
-    PXS_CHECK(channels > 0 && channels % 8 == 0, PXS_ERR_ARG,
+                           int channels, int factor, const float * subdivision,
+                           int32_t * out_coords, void * y, int64_t * m_out, void * workspace,
+                           void * stream) {
+    PXS_CHECK(factor > 0 && factor <= 1024, PXS_ERR_ARG,
+              "pxs_channel_to_spatial: factor must be in 1..1024");
+    const int64_t cc = static_cast<int64_t>(factor) * factor * factor;
+    PXS_CHECK(n >= 0 && n * cc <= INT_MAX, PXS_ERR_ARG, "pxs_channel_to_spatial: bad row count");
+    PXS_CHECK(channels > 0 && channels % cc == 0, PXS_ERR_ARG,
               "sparse channel-to-spatial channels are not divisible by factor^3");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_channel_to_spatial: bad dtype");
     PXS_CHECK(m_out && workspace, PXS_ERR_ARG, "pxs_channel_to_spatial: null pointer");
     hipStream_t s = as_stream(stream);
     if (n == 0) return fill_i64(m_out, 1, 0, s);
     PXS_CHECK(coords && x && out_coords && y, PXS_ERR_ARG, "pxs_channel_to_spatial: null pointer");
+    const int icc = static_cast<int>(cc);
     char * ws = static_cast<char *>(workspace);
     int64_t * prefix = reinterpret_cast<int64_t *>(ws);
     int64_t * src_of = prefix + n;
-    int32_t * counts = reinterpret_cast<int32_t *>(src_of + 8 * n);
+    int32_t * counts = reinterpret_cast<int32_t *>(src_of + n * cc);
     void * scan_ws = reinterpret_cast<void *>(
         (reinterpret_cast<uintptr_t>(counts + n) + 7) & ~uintptr_t(7));
     int rc;
     if (subdivision) {
         hipLaunchKernelGGL(c2s_count_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
-                           subdivision, n, counts);
+                           subdivision, n, icc, counts);
         rc = exclusive_scan_i32(counts, prefix, n, m_out, scan_ws, s);
         if (rc) return rc;
     } else {
-        rc = fill_i64(m_out, 1, 8 * n, s);
+        rc = fill_i64(m_out, 1, n * cc, s);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(c2s_coords_kernel, dim3(grid_for(8 * n, kThreads)), dim3(kThreads), 0, s,
-                       reinterpret_cast<const int4 *>(coords), n, subdivision, prefix,
+    hipLaunchKernelGGL(c2s_coords_kernel, dim3(grid_for(n * cc, kThreads)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const int4 *>(coords), n, factor, icc, subdivision, prefix,
                        reinterpret_cast<int4 *>(out_coords), src_of);
-    const int64_t max_elems = 8 * n * (channels / 8);
+    const int64_t max_elems = n * channels;
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((max_elems + 255) / 256, 16384));
     if (dtype == PXS_F32) {
         hipLaunchKernelGGL(c2s_feats_kernel<float>, dim3(blocks), dim3(256), 0, s,
-                           static_cast<const float *>(x), channels, src_of, m_out, 8 * n,
+                           static_cast<const float *>(x), channels, icc, src_of, m_out, n * cc,
                            static_cast<float *>(y));
     } else {
         hipLaunchKernelGGL(c2s_feats_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s,
-                           static_cast<const uint16_t *>(x), channels, src_of, m_out, 8 * n,
+                           static_cast<const uint16_t *>(x), channels, icc, src_of, m_out, n * cc,
                            static_cast<uint16_t *>(y));
     }
     return check_launch("pxs_channel_to_spatial");

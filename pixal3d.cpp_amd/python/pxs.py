@@ -45,12 +45,26 @@ _SIGS = {
     "pxs_neighbor_pairs_workspace_bytes": (C.c_size_t, [_i64]),
     "pxs_neighbor_pairs": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
     "pxs_subm_conv3d": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
-    "pxs_downsample_workspace_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32]),
+    "pxs_status_reset": (_i32, [_vp, _vp]),
+    "pxs_check_finite": (_i32, [_i32, _vp, _i64, _i32, _i64, _vp, _vp]),
+    "pxs_downsample_workspace_bytes": (C.c_size_t, [_i64, _i32, _i32, _i32, _i32, _i32]),
+    "pxs_downsample_topology": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                       _vp, _vp]),
+    "pxs_downsample_mean": (_i32, [_i32, _vp, _i32, _vp, _vp, _i64, _vp, _vp]),
     "pxs_downsample_s2_topology": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "pxs_sparse_conv3d_s2": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _vp, _vp]),
-    "pxs_downsample_mean_s2": (_i32, [_i32, _vp, _i32, _vp, _i64, _i64, _vp, _vp]),
-    "pxs_channel_to_spatial_workspace_bytes": (C.c_size_t, [_i64]),
-    "pxs_channel_to_spatial": (_i32, [_i32, _vp, _i64, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pxs_channel_to_spatial_workspace_bytes": (C.c_size_t, [_i64, _i32]),
+    "pxs_channel_to_spatial": (_i32, [_i32, _vp, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
+                                      _vp]),
+    "pxs_linear_residual": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "pxs_convert": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp]),
+    "pxs_timestep_embedding": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp]),
+    "pxs_transformer_block_workspace_bytes": (C.c_size_t, [_i32, _vp, _i64, _i64, _i32]),
+    "pxs_transformer_block": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
+                                     _i64, _vp, _vp, _vp]),
+    "pxs_slat_flow_workspace_bytes": (C.c_size_t, [_i32, _vp, _i64, _i64, _i32]),
+    "pxs_slat_flow_forward": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
+                                     _i64, _vp, _vp, _vp, _vp]),
     "pxs_linear": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp]),
     "pxs_linear_gate_residual": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "pxs_layer_norm": (_i32, [_i32, _vp, _i64, _i32, _f, _vp, _vp, _i32, _vp, _vp]),
@@ -61,12 +75,55 @@ _SIGS = {
     "pxs_activation": (_i32, [_i32, _vp, _i64, _i32, _vp]),
     "pxs_attention_workspace_bytes": (C.c_size_t, [_i32]),
     "pxs_varlen_attention": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _i64, _vp,
-                                    _i32, _i32, _f, _vp, _i64, _vp, _vp]),
+                                    _i32, _i32, _i32, _f, _vp, _i64, _vp, _vp]),
     "pxs_batch_cu_seqlens": (_i32, [_vp, _i64, _i32, _vp, _vp]),
     "pxs_window_partition_workspace_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32, _i32, _i32, _i64]),
     "pxs_window_partition": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                     _vp, _vp]),
 }
+
+
+BLOCK_WEIGHT_FIELDS = (
+    "modulation", "self_to_qkv_weight", "self_to_qkv_bias", "self_q_gamma", "self_k_gamma",
+    "self_to_out_weight", "self_to_out_bias", "norm2_weight", "norm2_bias", "cross_to_q_weight",
+    "cross_to_q_bias", "cross_to_kv_weight", "cross_to_kv_bias", "cross_q_gamma",
+    "cross_k_gamma", "cross_to_out_weight", "cross_to_out_bias", "proj_weight", "proj_bias",
+    "mlp0_weight", "mlp0_bias", "mlp2_weight", "mlp2_bias")
+# Members that are linear weights (stored in the call's dtype); the rest are fp32.
+BLOCK_LINEAR_WEIGHTS = frozenset({1, 5, 9, 11, 15, 17, 19, 21})
+
+
+class BlockConfig(C.Structure):
+    _fields_ = [("channels", C.c_int), ("num_heads", C.c_int), ("mlp_hidden", C.c_int),
+                ("context_channels", C.c_int), ("proj_in_channels", C.c_int),
+                ("norm_eps", C.c_float), ("rope_freq_min", C.c_float),
+                ("rope_freq_base", C.c_float), ("use_rope", C.c_int), ("qk_rms_norm", C.c_int),
+                ("qk_rms_norm_cross", C.c_int), ("use_projection", C.c_int)]
+
+
+class BlockWeights(C.Structure):
+    _fields_ = [(name, C.c_void_p) for name in BLOCK_WEIGHT_FIELDS]
+
+
+class FlowConfig(C.Structure):
+    _fields_ = [("in_channels", C.c_int), ("out_channels", C.c_int), ("model_channels", C.c_int),
+                ("cond_channels", C.c_int), ("num_blocks", C.c_int), ("num_heads", C.c_int),
+                ("proj_in_channels", C.c_int), ("mlp_hidden", C.c_int), ("norm_eps", C.c_float),
+                ("rope_freq_min", C.c_float), ("rope_freq_base", C.c_float),
+                ("qk_rms_norm", C.c_int), ("qk_rms_norm_cross", C.c_int),
+                ("use_projection", C.c_int)]
+
+
+class FlowWeights(C.Structure):
+    _fields_ = [(name, C.c_void_p) for name in (
+        "input_weight", "input_bias", "timestep_weight0", "timestep_bias0", "timestep_weight2",
+        "timestep_bias2", "modulation_weight", "modulation_bias", "output_weight",
+        "output_bias")] + [("blocks", C.POINTER(BlockWeights))]
+
+
+def block_weights(tensors) -> BlockWeights:
+    """23 device tensors (or None) in BLOCK_WEIGHT_FIELDS order."""
+    return BlockWeights(*[None if t is None else t.data_ptr() for t in tensors])
 
 
 def load_library(path: Path = LIB_PATH) -> C.CDLL:
@@ -171,13 +228,30 @@ class Pxs:
         oc = torch.empty((max(n, 1), 4), dtype=torch.int32, device=dev)
         child = torch.empty((8, max(n, 1)), dtype=torch.int32, device=dev)
         m = torch.empty(1, dtype=torch.int64, device=dev)
-        ws = self._ws(self.lib.pxs_downsample_workspace_bytes(batch_size, *shape), dev)
+        ws = self._ws(self.lib.pxs_downsample_workspace_bytes(n, batch_size, *shape, 2), dev)
         self._check(self.lib.pxs_downsample_s2_topology(_ptr(coords), n, batch_size, shape[0],
                                                         shape[1], shape[2], _ptr(oc), _ptr(child),
                                                         _ptr(m), _ptr(ws), self.stream()),
                     "pxs_downsample_s2_topology")
         mm = int(m.item())
         return oc[:mm], child, mm
+
+    def downsample(self, coords, batch_size, shape, factor):
+        """Factor-f output topology as groups: (coords, offsets, rows, m)."""
+        n = coords.shape[0]
+        dev = coords.device
+        oc = torch.empty((max(n, 1), 4), dtype=torch.int32, device=dev)
+        off = torch.empty(n + 1, dtype=torch.int64, device=dev)
+        rows = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+        m = torch.empty(1, dtype=torch.int64, device=dev)
+        ws = self._ws(self.lib.pxs_downsample_workspace_bytes(n, batch_size, *shape, factor), dev)
+        self._check(self.lib.pxs_downsample_topology(_ptr(coords), n, batch_size, shape[0],
+                                                     shape[1], shape[2], factor, _ptr(oc),
+                                                     _ptr(off), _ptr(rows), _ptr(m), _ptr(ws),
+                                                     self.stream()),
+                    "pxs_downsample_topology")
+        mm = int(m.item())
+        return oc[:mm], off[: mm + 1], rows[:n], mm
 
     def window_partition(self, coords, batch_size, shape, window, shift):
         n = coords.shape[0]
@@ -195,16 +269,17 @@ class Pxs:
         nw = int(nwin.item())
         return fwd[:n], bwd[:n], cu[: nw + 1], nw
 
-    def channel_to_spatial(self, coords, x, subdivision=None):
+    def channel_to_spatial(self, coords, x, subdivision=None, factor=2):
         n, ch = x.shape
+        cc = factor ** 3
         dev = x.device
-        oc = torch.empty((max(8 * n, 1), 4), dtype=torch.int32, device=dev)
-        y = torch.empty((max(8 * n, 1), ch // 8), dtype=x.dtype, device=dev)
+        oc = torch.empty((max(cc * n, 1), 4), dtype=torch.int32, device=dev)
+        y = torch.empty((max(cc * n, 1), ch // cc), dtype=x.dtype, device=dev)
         m = torch.empty(1, dtype=torch.int64, device=dev)
-        ws = self._ws(self.lib.pxs_channel_to_spatial_workspace_bytes(n), dev)
+        ws = self._ws(self.lib.pxs_channel_to_spatial_workspace_bytes(n, factor), dev)
         self._check(self.lib.pxs_channel_to_spatial(_dtype_code(x), _ptr(coords), n, _ptr(x), ch,
-                                                    _ptr(subdivision), _ptr(oc), _ptr(y), _ptr(m),
-                                                    _ptr(ws), self.stream()),
+                                                    factor, _ptr(subdivision), _ptr(oc), _ptr(y),
+                                                    _ptr(m), _ptr(ws), self.stream()),
                     "pxs_channel_to_spatial")
         mm = int(m.item())
         return oc[:mm], y[:mm]
@@ -230,13 +305,21 @@ class Pxs:
                     "pxs_sparse_conv3d_s2")
         return y
 
-    def downsample_mean_s2(self, x, child_map, m):
-        y = torch.empty((m, x.shape[1]), dtype=x.dtype, device=x.device)
-        self._check(self.lib.pxs_downsample_mean_s2(_dtype_code(x), _ptr(x), x.shape[1],
-                                                    _ptr(child_map), child_map.shape[1], m,
-                                                    _ptr(y), self.stream()),
-                    "pxs_downsample_mean_s2")
-        return y
+    def downsample_mean(self, x, offsets, rows, m):
+        y = torch.empty((max(m, 1), x.shape[1]), dtype=x.dtype, device=x.device)
+        self._check(self.lib.pxs_downsample_mean(_dtype_code(x), _ptr(x), x.shape[1],
+                                                 _ptr(offsets), _ptr(rows), m, _ptr(y),
+                                                 self.stream()),
+                    "pxs_downsample_mean")
+        return y[:m]
+
+    def linear_residual(self, x, weight, bias, residual):
+        rows, cin = x.shape
+        self._check(self.lib.pxs_linear_residual(_dtype_code(x), _ptr(x), rows, cin, _ptr(weight),
+                                                 _ptr(bias), weight.shape[0], _ptr(residual),
+                                                 self.stream()),
+                    "pxs_linear_residual")
+        return residual
 
     def linear(self, x, weight, bias=None, act=ACT_NONE, out=None):
         rows, cin = x.shape
@@ -314,15 +397,52 @@ class Pxs:
 
     # -- attention --------------------------------------------------------------------
     def varlen_attention(self, q, k, v, cu_q, cu_k, heads, head_dim, scale, row_map=None,
-                         out=None, nseg=None):
+                         out=None, nseg=None, value_dim=None):
         nseg = (cu_q.shape[0] - 1) if nseg is None else nseg
-        o = torch.empty((q.shape[0], heads * head_dim), dtype=q.dtype, device=q.device) \
+        value_dim = head_dim if value_dim is None else value_dim
+        o = torch.empty((q.shape[0], heads * value_dim), dtype=q.dtype, device=q.device) \
             if out is None else out
         ws = self._ws(self.lib.pxs_attention_workspace_bytes(nseg), q.device)
         self._check(self.lib.pxs_varlen_attention(_dtype_code(q), _ptr(q), q.stride(0), _ptr(k),
                                                   k.stride(0), _ptr(v), v.stride(0), _ptr(cu_q),
                                                   _ptr(cu_k), nseg, q.shape[0], _ptr(row_map),
-                                                  heads, head_dim, scale, _ptr(o), o.stride(0),
+                                                  heads, head_dim, value_dim, scale, _ptr(o),
+                                                  o.stride(0),
                                                   _ptr(ws), self.stream()),
                     "pxs_varlen_attention")
         return o
+
+    # -- compositions ----------------------------------------------------------------------
+    def transformer_block(self, cfg: BlockConfig, weights: BlockWeights, coords, batch_size, cu,
+                          hidden, time_mod, context, ctx_offsets, projected=None, dtype=None):
+        """pxs_transformer_block: hidden (fp32 [rows, C]) is updated in place."""
+        dtype = _dtype_code(context) if dtype is None else dtype
+        rows = coords.shape[0]
+        tokens = context.shape[0]
+        ws = self._ws(self.lib.pxs_transformer_block_workspace_bytes(
+            dtype, C.byref(cfg), rows, tokens, batch_size), hidden.device)
+        self._check(self.lib.pxs_transformer_block(
+            dtype, C.byref(cfg), C.byref(weights), _ptr(coords), rows, batch_size, _ptr(cu),
+            _ptr(hidden), _ptr(time_mod), _ptr(context), _ptr(ctx_offsets), tokens,
+            _ptr(projected), _ptr(ws), self.stream()), "pxs_transformer_block")
+        return hidden
+
+    def slat_flow_forward(self, cfg: FlowConfig, weights: FlowWeights, coords, batch_size, cu, x,
+                          timesteps, context, ctx_offsets, projected=None, dtype=None, out=None,
+                          workspace=None):
+        dtype = _dtype_code(context) if dtype is None else dtype
+        rows = coords.shape[0]
+        tokens = context.shape[0]
+        y = torch.empty((rows, cfg.out_channels), dtype=torch.float32, device=x.device) \
+            if out is None else out
+        ws = workspace if workspace is not None else self._ws(
+            self.flow_workspace_bytes(cfg, rows, tokens, batch_size, dtype), x.device)
+        self._check(self.lib.pxs_slat_flow_forward(
+            dtype, C.byref(cfg), C.byref(weights), _ptr(coords), rows, batch_size, _ptr(cu),
+            _ptr(x), _ptr(timesteps), _ptr(context), _ptr(ctx_offsets), tokens, _ptr(projected),
+            _ptr(y), _ptr(ws), self.stream()), "pxs_slat_flow_forward")
+        return y
+
+    def flow_workspace_bytes(self, cfg: FlowConfig, rows, tokens, batch_size, dtype):
+        return self.lib.pxs_slat_flow_workspace_bytes(dtype, C.byref(cfg), rows, tokens,
+                                                      batch_size)

@@ -146,8 +146,8 @@ def test_strided_conv_identity_invariant(px, orc):
 
 def test_downsample_mean_matches_reference_vectors(px):
     v = dict(np.load(GOLD / "ref_vectors.npz"))
-    oc, child, m = px.downsample_s2(ti32(v["ds_coords"]), 2, (16, 16, 16))
-    y = host(px.downsample_mean_s2(t32(v["ds_feats"]), child, m))
+    oc, off, rows, m = px.downsample(ti32(v["ds_coords"]), 2, (16, 16, 16), 2)
+    y = host(px.downsample_mean(t32(v["ds_feats"]), off, rows, m))
     np.testing.assert_array_equal(oc.cpu().numpy(), v["ds_out_coords"])
     assert_fp32(y, v["ds_out_feats"], what="downsample mean")
 

@@ -122,3 +122,33 @@ def test_channel_to_spatial(px, orc, with_sub):
     roc, ry = orc.channel_to_spatial(coords, x, 2, sub)
     np.testing.assert_array_equal(oc.cpu().numpy(), roc)
     np.testing.assert_array_equal(host(y), ry)
+
+
+@pytest.mark.parametrize("factor", [1, 2, 3])
+def test_downsample_any_factor(px, orc, factor):
+    """Grouped topology and mean for any factor vs the oracle (src/sparse.cpp:536-602)."""
+    coords = W.shell_coords(20, [[(5.0, 8.0)], [(4.0, 7.0)]], 35)
+    n = coords.shape[0]
+    x = W.normal(35, n * 40, 1).reshape(n, 40)
+    print(f"[downsample] factor={factor} n={n}", flush=True)
+    oc, off, rows, m = px.downsample(ti32(coords), 2, (20, 20, 20), factor)
+    y = host(px.downsample_mean(t32(x), off, rows, m))
+    roc, ry = orc.downsample_mean(coords, x, factor)
+    np.testing.assert_array_equal(oc.cpu().numpy(), roc)
+    # Same summation order as the reference: bit-exact.
+    np.testing.assert_array_equal(y, ry)
+    # Groups list their rows in ascending order.
+    o, r = off.cpu().numpy(), rows.cpu().numpy()
+    for q in range(m):
+        assert np.all(np.diff(r[o[q]:o[q + 1]]) > 0)
+
+
+def test_channel_to_spatial_factor3(px, orc):
+    coords = W.shell_coords(12, [[(3.0, 5.0)], [(2.0, 4.0)]], 36)
+    n = coords.shape[0]
+    x = W.normal(36, n * 54, 1).reshape(n, 54)
+    sub = (W.uniform(36, n * 27, 2) > 0.5).astype(np.float32).reshape(n, 27)
+    oc, y = px.channel_to_spatial(ti32(coords), t32(x), t32(sub), factor=3)
+    roc, ry = orc.channel_to_spatial(coords, x, 3, sub)
+    np.testing.assert_array_equal(oc.cpu().numpy(), roc)
+    np.testing.assert_array_equal(host(y), ry)
