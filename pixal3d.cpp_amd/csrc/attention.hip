@@ -19,6 +19,7 @@
 #include "scan.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace pxs {
 namespace {
@@ -27,6 +28,29 @@ constexpr int kKeys = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// s_waitcnt with only vmcnt bounded (n <= 15; expcnt/lgkmcnt at their maxima).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
+}
+
+__device__ __forceinline__ int64_t remap_xcd64(int64_t bid, int64_t blocks) {
+    // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
+    // contiguous range of logical work items.
+    const int64_t q = blocks / 8, rem = blocks % 8;
+    const int64_t xcd = bid % 8, slot = bid / 8;
+    return (xcd < rem) ? xcd * (q + 1) + slot : rem * (q + 1) + (xcd - rem) * q + slot;
+}
 
 struct AttnArgs {
     const void * q;
@@ -296,20 +320,49 @@ __device__ __forceinline__ int vswz(int row) { return (2 * (row & 3)) ^ ((row >>
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
+// Scores are kept in the raw (unscaled) domain; p = exp2(s * c - m * c) with
+// c = scale * log2(e) costs one FMA and one exp per score.  The running max m
+// is only raised when a tile's max exceeds it by more than kLazyLog2 / c
+// (p <= 2^kLazyLog2 meanwhile), so the O rescale runs on few tiles.
+constexpr float kLazyLog2 = 8.0f;
+
+__device__ __forceinline__ float lane_pair_max(float v) {
+    // max over lanes l and l ^ 32 (v_permlane32_swap exchanges the halves).
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                     false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
+__device__ __forceinline__ float lane_pair_sum(float v) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                     false, false);
+    return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
+// Software-pipelined bf16 kernel (head_dim 64).  Each wave owns 32 queries.
+// Iteration j of the key loop issues 16 MFMAs that do not depend on tile j's
+// softmax -- S for tile j+1 (K_{j+1} Q^T) and O += V_{j-1}^T P_{j-1} -- and
+// then runs tile j's softmax on the VALU while they execute, so the matrix
+// cores and the VALU work at the same time.  K/V tiles stream HBM -> LDS with
+// global_load_lds through a ring of 4 stages (tiles j-1 .. j+2 live).
+constexpr int kAttnStages = 4;
+
 template <int NW>
-__global__ void __launch_bounds__(NW * 64)
-flash_attn_bf16_kernel(AttnArgs a) {
-    constexpr int kThreads = NW * 64;
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     constexpr int kTileBytes = kKeys * 128;           // one 64-key x 64-dim bf16 tile
     constexpr int kInstr = 2 * (kKeys / 8) / NW;      // K + V wave instructions per tile
-    __shared__ __align__(16) char lds[2][2 * kTileBytes];
+    __shared__ __align__(16) char lds[kAttnStages][2 * kTileBytes];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, kept in an SGPR
     const int h = lane >> 5, r = lane & 31;
-    const int head = blockIdx.y;
 
-    const int64_t t = blockIdx.x;
+    const int64_t total = tiles_bound * heads;
+    const int64_t logical = remap_xcd64(blockIdx.x, total);
+    const int head = static_cast<int>(logical / tiles_bound);
+    const int64_t t = logical - static_cast<int64_t>(head) * tiles_bound;
     if (t >= a.tile_start[a.nseg]) return;
     int lo = 0, hi = a.nseg - 1;
     while (lo < hi) {
@@ -326,21 +379,22 @@ flash_attn_bf16_kernel(AttnArgs a) {
     const uint16_t * __restrict__ kp = static_cast<const uint16_t *>(a.k);
     const uint16_t * __restrict__ vp = static_cast<const uint16_t *>(a.v);
 
+    // This lane's query and its Q^T fragments (B operand): dims 32h + 8st ..
     const int64_t qi = q_begin + wave * 32 + r;
     const bool q_valid = qi < q_end;
     const int64_t q_row = q_valid ? (a.row_map ? a.row_map[qi] : qi) : -1;
     bf16x8 qf[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int st = 0; st < 4; ++st) {
         uint4 v = make_uint4(0, 0, 0, 0);
-        if (q_valid) v = *reinterpret_cast<const uint4 *>(qp + q_row * a.ldq + head * 64 + 32 * h + 8 * s);
-        qf[s] = __builtin_bit_cast(bf16x8, v);
+        if (q_valid) v = *reinterpret_cast<const uint4 *>(qp + q_row * a.ldq + head * 64 + 32 * h + 8 * st);
+        qf[st] = __builtin_bit_cast(bf16x8, v);
     }
 
     const int ntiles = static_cast<int>((k_end - k_begin + kKeys - 1) / kKeys);
     const int lrow = lane >> 3, lslot = lane & 7;
-    auto issue = [&](int tile) {
-        char * base = lds[tile & 1];
+    auto issue = [&](int tile) __attribute__((always_inline)) {
+        char * base = lds[tile % kAttnStages];
         const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeys;
 #pragma unroll
         for (int j = 0; j < kInstr; ++j) {
@@ -362,12 +416,25 @@ flash_attn_bf16_kernel(AttnArgs a) {
         }
     };
 
-    f32x16 oacc[2];
+    // S^T (keys x queries) for one tile: 2 sub-tiles of 32 keys, 4 K-steps each.
+    auto qk = [&](int tile, f32x16 (&s)[2]) {
+        const char * kl = lds[tile % kAttnStages];
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+        for (int kt = 0; kt < 2; ++kt) {
+            const int row = kt * 32 + r;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
+            for (int st = 0; st < 4; ++st) {
+                const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(
+                    kl + row * 128 + (((4 * h + st) ^ kswz(row)) << 4));
+                if (st == 0) {
+                    const f32x16 zero = {};
+                    s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], zero, 0, 0, 0);
+                } else {
+                    s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kt], 0, 0, 0);
+                }
+            }
+        }
+    };
 
     // Lane-constant parts of the transposed V reads: source row t = j / 4 of
     // the 4-key group and the 4 dims starting at 16*(G%2) + 4*(j%4).
@@ -375,73 +442,19 @@ flash_attn_bf16_kernel(AttnArgs a) {
     const int v_key_off = 4 * (G >> 1) + (jl >> 2);
     const int v_dim_off = 16 * (G & 1) + 4 * (jl & 3);
 
-    if (ntiles > 0) issue(0);
-    for (int tile = 0; tile < ntiles; ++tile) {
-        wait_vmcnt0();
-        __syncthreads();
-        if (tile + 1 < ntiles) issue(tile + 1);
-        const char * kl = lds[tile & 1];
-        const char * vl = kl + kTileBytes;
-        const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeys;
+    f32x16 oacc[2];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
 
-        f32x16 sacc[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) sacc[kt][v] = 0.0f;
-            const int row = kt * 32 + r;
-            const char * krow = kl + row * 128;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const bf16x8 af = *reinterpret_cast<const bf16x8 *>(
-                    krow + (((4 * h + s) ^ kswz(row)) << 4));
-                sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[s], sacc[kt], 0, 0, 0);
-            }
-        }
-
-        const int valid_keys = static_cast<int>(min<int64_t>(kKeys, k_end - kt0));
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                float sv = sacc[kt][v] * a.scale_log2;
-                if (valid_keys < kKeys) {
-                    const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                    if (key >= valid_keys) sv = -INFINITY;
-                }
-                sacc[kt][v] = sv;
-                mx = fmaxf(mx, sv);
-            }
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        float rs = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float p = __builtin_amdgcn_exp2f(sacc[kt][v] - m_new);
-                sacc[kt][v] = p;
-                rs += p;
-            }
-        }
-        rs += __shfl_xor(rs, 32, 64);
-        l_run = l_run * alpha + rs;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
-
+    // O^T += V^T P^T for one tile (P^T fragments pb[kt][u] from softmax).
+    auto pv = [&](int tile, const bf16x8 (&pb)[2][2]) {
+        const char * vl = lds[tile % kAttnStages] + kTileBytes;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                bf16x8 pb;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) pb[e] = static_cast<__bf16>(sacc[kt][8 * u + e]);
                 const int key_a = kt * 32 + 16 * u + v_key_off;
                 const int key_b = key_a + 8;
 #pragma unroll
@@ -457,14 +470,126 @@ flash_attn_bf16_kernel(AttnArgs a) {
                     const uint2 lo2 = __builtin_bit_cast(uint2, lo4);
                     const uint2 hi2 = __builtin_bit_cast(uint2, hi4);
                     const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
-                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, oacc[dt], 0, 0, 0);
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kt][u], oacc[dt], 0, 0, 0);
                 }
             }
         }
+    };
+
+    float m_run = -INFINITY;  // running max of raw scores (lazy, see kLazyLog2)
+    float l_part = 0.0f;      // this lane's half of the row sum
+    const float c = a.scale_log2;
+    const float lazy = kLazyLog2 / c;
+    const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+
+    // Softmax of one tile's scores into bf16 P^T fragments, in two parts so
+    // that independent MFMAs can be interleaved with each: the max (and the
+    // rare lazy rescale of O), then the exponentials and row sums.  valid < 64
+    // masks the keys past the segment end (only the last tile).
+    auto softmax_max = [&](f32x16 (&s)[2], int valid) {
+        if (valid < kKeys) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (key >= valid) s[kt][v] = -INFINITY;
+                }
+        }
+        float mx = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+        for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[0][v]);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[1][v]);
+        return lane_pair_max(mx);
+    };
+    // Raise the running max only when this tile would overflow the lazy
+    // headroom somewhere in the wave (a uniform branch).  O must already hold
+    // every earlier tile's PV product.
+    auto rescale = [&](float mx) __attribute__((always_inline)) {
+        if (__builtin_expect(__ballot(mx > m_run + lazy) != 0, 0)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
+            m_run = m_new;
+            l_part *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+        }
+    };
+    auto softmax_exp = [&](const f32x16 (&s)[2], bf16x8 (&pb)[2][2]) {
+        const float mc = m_run * c;
+        float lsum = l_part;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                bf16x8 p8;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    bf16x2 pp;
+                    pp[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * u + e], c, -mc)));
+                    pp[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * u + e + 1], c, -mc)));
+                    p8[e] = pp[0];
+                    p8[e + 1] = pp[1];
+                    lsum = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, lsum, false);
+                }
+                pb[kt][u] = p8;
+            }
+        }
+        l_part = lsum;
+    };
+
+    // One steady-state step for tile j (full, not the last): PV(j-1) with the
+    // max of S_j, then the rescale, then QK(j+1) with the exponentials of S_j.
+    auto step = [&](int j, f32x16 (&s_cur)[2], f32x16 (&s_next)[2], bf16x8 (&p)[2][2]) {
+        // Tile j+1 has landed (it is the newest load); the barrier also frees
+        // the stage of tile j-2 for tile j+2.
+        wait_vmcnt0();
+        __syncthreads();
+        if (j + 2 < ntiles) issue(j + 2);
+        if (j > 0) pv(j - 1, p);
+        const float mx = softmax_max(s_cur, kKeys);
+        rescale(mx);
+        qk(j + 1, s_next);
+        softmax_exp(s_cur, p);
+    };
+
+    const int64_t klen = k_end - k_begin;
+    if (ntiles > 0) {
+        issue(0);
+        if (ntiles > 1) issue(1);
+        if (ntiles > 1) wait_vmcnt(kInstr);
+        else wait_vmcnt0();
+        __syncthreads();
+        f32x16 s_a[2], s_b[2];
+        bf16x8 p_prev[2][2];
+        qk(0, s_a);
+        // Steady state over tiles 0 .. ntiles-2 (only the last can be
+        // partial), unrolled by two so the S registers alternate roles.
+        int j = 0;
+        for (; j + 2 < ntiles; j += 2) {
+            step(j, s_a, s_b, p_prev);
+            step(j + 1, s_b, s_a, p_prev);
+        }
+        if (j + 1 < ntiles) {
+            step(j, s_a, s_b, p_prev);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) s_a[kt] = s_b[kt];
+        }
+        // Last tile (possibly partial), then the two outstanding PV products.
+        const int last = ntiles - 1;
+        if (last > 0) pv(last - 1, p_prev);
+        const float mx = softmax_max(s_a, static_cast<int>(klen - static_cast<int64_t>(last) * kKeys));
+        rescale(mx);
+        softmax_exp(s_a, p_prev);
+        pv(last, p_prev);
     }
 
+    const float l_tot = lane_pair_sum(l_part);
     if (!q_valid) return;
-    const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     uint16_t * op = static_cast<uint16_t *>(a.o) + q_row * a.ldo + head * 64;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
@@ -482,9 +607,9 @@ flash_attn_bf16_kernel(AttnArgs a) {
 template <int NW>
 int launch_attn_bf16(const AttnArgs & args, int64_t total_q, int heads, hipStream_t stream) {
     const int64_t bound = total_q / (32 * NW) + args.nseg + 1;
-    if (bound > INT32_MAX) return fail(PXS_ERR_ARG, "attention grid too large");
-    hipLaunchKernelGGL((flash_attn_bf16_kernel<NW>), dim3(static_cast<unsigned>(bound), heads),
-                       dim3(NW * 64), 0, stream, args);
+    if (bound * heads > INT32_MAX) return fail(PXS_ERR_ARG, "attention grid too large");
+    hipLaunchKernelGGL((flash_attn_bf16_kernel<NW>), dim3(static_cast<unsigned>(bound * heads)),
+                       dim3(NW * 64), 0, stream, args, heads, bound);
     return check_launch("flash attention (bf16)");
 }
 
@@ -533,12 +658,17 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     hipStream_t s = as_stream(stream);
     // Small segments (windows) use one wavefront per workgroup.
     const int nw = (total_q / nseg >= 256) ? 4 : 1;
+    const bool fast = dtype == PXS_BF16 && head_dim == 64 && value_dim == 64 && (ld_q % 8 == 0) &&
+                      (ld_k % 8 == 0) && (ld_v % 8 == 0) && (ld_o % 4 == 0) && aligned16(q) &&
+                      aligned16(k) && aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0;
+    // Queries per workgroup: the fast kernel runs 64 per wave, the generic one 32.
+    const int q_tile = 32 * nw;  // queries per workgroup: 32 per wave in every kernel
     int64_t * tile_start = static_cast<int64_t *>(workspace);
     int32_t * tiles = reinterpret_cast<int32_t *>(tile_start + nseg + 1);
     void * scan_ws = reinterpret_cast<void *>(
         (reinterpret_cast<uintptr_t>(tiles + nseg) + 7) & ~uintptr_t(7));
     hipLaunchKernelGGL(attn_tiles_kernel, dim3(grid_for(nseg, 256)), dim3(256), 0, s, cu_q, nseg,
-                       32 * nw, tiles);
+                       q_tile, tiles);
     int rc = exclusive_scan_i32(tiles, tile_start, nseg, tile_start + nseg, scan_ws, s);
     if (rc) return rc;
     AttnArgs a{};
@@ -550,9 +680,6 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     a.vec_ok = (head_dim % vec == 0) && (value_dim % vec == 0) && (ld_q % vec == 0) && (ld_k % vec == 0) &&
                (ld_v % vec == 0) && aligned16(q) && aligned16(k) && aligned16(v);
     if (dtype == PXS_BF16) {
-        const bool fast = head_dim == 64 && value_dim == 64 && (ld_q % 8 == 0) && (ld_k % 8 == 0) &&
-                          (ld_v % 8 == 0) && (ld_o % 4 == 0) && aligned16(q) && aligned16(k) &&
-                          aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0;
         if (fast) {
             return nw == 4 ? launch_attn_bf16<4>(a, total_q, heads, s)
                            : launch_attn_bf16<1>(a, total_q, heads, s);

@@ -316,6 +316,12 @@ __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent ro
 #ifndef PXS_GEMM_STAGES
 #define PXS_GEMM_STAGES 2
 #endif
+#ifndef PXS_GEMM_BM
+#define PXS_GEMM_BM 128
+#endif
+#ifndef PXS_GEMM_BN
+#define PXS_GEMM_BN 128
+#endif
 #ifndef PXS_GEMM_ISSUE_LATE
 #define PXS_GEMM_ISSUE_LATE 0
 #endif
@@ -614,7 +620,7 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
     if (args.vec_ok) {
         // 128-row tiles: the row count only changes the grid, not the tile.
         return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES>(args, stream)
-                      : launch_lds_tile<T, 128, 128, EPI, PXS_GEMM_STAGES>(args, stream);
+                      : launch_lds_tile<T, PXS_GEMM_BM, PXS_GEMM_BN, EPI, PXS_GEMM_STAGES>(args, stream);
     }
     const int64_t tiles_n = (args.cout + (narrow ? 63 : 127)) / (narrow ? 64 : 128);
     const bool tall = ((args.m + 127) / 128) * tiles_n >= 512;
