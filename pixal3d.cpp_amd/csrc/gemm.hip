@@ -310,9 +310,10 @@ gather_gemm_kernel(GemmArgs a) {
 __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent rows
 
 // Measured on MI355X (SubMConv3d 128->128 / 256->256, linear 1024->3072):
-// two stages of 128x128 tiles (64 KiB + indices, two workgroups per CU) with
-// the next stage issued before the current one is computed beat deeper
-// pipelines at one workgroup per CU and larger tiles.
+// the kernel is bound by the latency of the gathered loads, so resident waves
+// matter most.  128x128 tiles in two stages (64 KiB + indices, two
+// workgroups per CU) with 8 waves of 64x32 each beat 4 waves of 64x64,
+// 256-row tiles and 3-4 stage pipelines (which fit only one workgroup per CU).
 #ifndef PXS_GEMM_STAGES
 #define PXS_GEMM_STAGES 2
 #endif
@@ -321,6 +322,12 @@ __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent ro
 #endif
 #ifndef PXS_GEMM_BN
 #define PXS_GEMM_BN 128
+#endif
+#ifndef PXS_GEMM_WAVES
+#define PXS_GEMM_WAVES 8
+#endif
+#ifndef PXS_GEMM_WAVES_M
+#define PXS_GEMM_WAVES_M 2
 #endif
 #ifndef PXS_GEMM_ISSUE_LATE
 #define PXS_GEMM_ISSUE_LATE 0
@@ -368,17 +375,22 @@ constexpr int lds_gemm_bytes(int noff) {
     return NSTAGE * (BM + BN) * kChunkBytes + noff * BM * 4;
 }
 
-template <typename T, int BM, int BN, int EPI, int NSTAGE>
-__global__ void __launch_bounds__(kGemmThreads)
+// NW waves per workgroup in a WAVES_M x (NW / WAVES_M) grid; each wave owns
+// a (BM / WAVES_M) x (BN / (NW / WAVES_M)) block of the output tile.
+template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M>
+__global__ void __launch_bounds__(NW * 64)
 gather_gemm_lds_kernel(GemmArgs a) {
     constexpr int kVec = Mfma<T>::kVec;
     constexpr int kChunk = Mfma<T>::kChunk;
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int kThreads = NW * 64;
+    constexpr int WAVES_N = NW / WAVES_M;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int TI = WM / 32, TJ = WN / 32;
     constexpr int kStageBytes = (BM + BN) * kChunkBytes;
-    constexpr int AI = BM / 32;  // A instructions per wave per stage (8 rows each)
-    constexpr int BI = BN / 32;
+    constexpr int AI = BM / (8 * NW);  // A instructions per wave per stage (8 rows each)
+    constexpr int BI = BN / (8 * NW);
     constexpr int kPerStage = AI + BI;
+    static_assert(AI * 8 * NW == BM && BI * 8 * NW == BN, "tile rows must split over the waves");
 
     extern __shared__ __align__(16) char smem[];
     int32_t * idx_lds = reinterpret_cast<int32_t *>(smem + NSTAGE * kStageBytes);
@@ -386,8 +398,9 @@ gather_gemm_lds_kernel(GemmArgs a) {
     __shared__ int koff[32];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int h = lane >> 5, r = lane & 31;
 
     const int tiles_n = (a.cout + BN - 1) / BN;
@@ -401,7 +414,7 @@ gather_gemm_lds_kernel(GemmArgs a) {
     __syncthreads();
     {
         uint32_t local = 0;
-        for (int row = tid; row < BM; row += kGemmThreads) {
+        for (int row = tid; row < BM; row += kThreads) {
             const int64_t p = p0 + row;
             if (p >= a.m) break;
             if (a.masks) {
@@ -428,7 +441,7 @@ gather_gemm_lds_kernel(GemmArgs a) {
         }
     }
     __syncthreads();
-    for (int e = tid; e < kcount * BM; e += kGemmThreads) {
+    for (int e = tid; e < kcount * BM; e += kThreads) {
         const int i = e / BM, row = e % BM;
         const int64_t p = p0 + row;
         int32_t src = -1;
@@ -571,13 +584,13 @@ gather_gemm_lds_kernel(GemmArgs a) {
     gemm_epilogue<T, TI, TJ, WM, WN, EPI>(a, acc, p0, n0, wm, wn, h, r);
 }
 
-template <typename T, int BM, int BN, int EPI, int NSTAGE>
+template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M>
 int launch_lds_tile(const GemmArgs & args, hipStream_t stream) {
     const int smem = lds_gemm_bytes<BM, BN, NSTAGE>(args.noff);
     static int configured = 0;
     if (configured < smem) {
         hipError_t e = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE>),
+            reinterpret_cast<const void *>(&gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE, NW, WAVES_M>),
             hipFuncAttributeMaxDynamicSharedMemorySize, lds_gemm_bytes<BM, BN, NSTAGE>(27));
         if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(gather_gemm_lds)");
         configured = lds_gemm_bytes<BM, BN, NSTAGE>(27);
@@ -586,8 +599,8 @@ int launch_lds_tile(const GemmArgs & args, hipStream_t stream) {
     const int64_t tiles_n = (args.cout + BN - 1) / BN;
     const int64_t blocks = tiles_m * tiles_n;
     if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "gather GEMM grid too large");
-    hipLaunchKernelGGL((gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads), smem, stream, args);
+    hipLaunchKernelGGL((gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE, NW, WAVES_M>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), smem, stream, args);
     return check_launch("gather GEMM (LDS pipeline)");
 }
 
@@ -619,8 +632,9 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
     const bool narrow = args.cout <= 64;
     if (args.vec_ok) {
         // 128-row tiles: the row count only changes the grid, not the tile.
-        return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES>(args, stream)
-                      : launch_lds_tile<T, PXS_GEMM_BM, PXS_GEMM_BN, EPI, PXS_GEMM_STAGES>(args, stream);
+        return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES, 4, 2>(args, stream)
+                      : launch_lds_tile<T, PXS_GEMM_BM, PXS_GEMM_BN, EPI, PXS_GEMM_STAGES,
+                                        PXS_GEMM_WAVES, PXS_GEMM_WAVES_M>(args, stream);
     }
     const int64_t tiles_n = (args.cout + (narrow ? 63 : 127)) / (narrow ? 64 : 128);
     const bool tall = ((args.m + 127) / 128) * tiles_n >= 512;

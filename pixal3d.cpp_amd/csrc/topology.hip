@@ -15,65 +15,102 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// Slots: the next power of two >= PXS_HASH_LOAD_INV * n (load <= 1/that).
+// Measured on MI355X (162k and 32k voxels): load 1/4 with plain mix64 homes
+// halves the neighbor-map time against load 1/2, and grouping consecutive z
+// into shared slot groups loses (shell surfaces have short z runs, so groups
+// mostly add collisions).
+#ifndef PXS_HASH_LOAD_INV
+#define PXS_HASH_LOAD_INV 4
+#endif
 int64_t hash_capacity(int64_t n) {
     int64_t cap = 64;
-    while (cap < 2 * n) cap <<= 1;
+    while (cap < PXS_HASH_LOAD_INV * n) cap <<= 1;
     return cap;
 }
 
+// A slot holds the packed key and the owning row in one 16-byte line piece,
+// so a probe is a single 16-byte load.
+struct __align__(16) HashSlot {
+    unsigned long long key;
+    int32_t val;
+    int32_t pad;
+};
+
 struct HashView {
-    uint64_t * keys;
-    int32_t * vals;
+    HashSlot * slots;
     uint64_t mask;
 };
 
 HashView hash_view(void * table, int64_t n) {
-    const int64_t cap = hash_capacity(n);
     HashView h;
-    h.keys = static_cast<uint64_t *>(table);
-    h.vals = reinterpret_cast<int32_t *>(h.keys + cap);
-    h.mask = static_cast<uint64_t>(cap - 1);
+    h.slots = static_cast<HashSlot *>(table);
+    h.mask = static_cast<uint64_t>(hash_capacity(n) - 1);
     return h;
 }
 
-__device__ __forceinline__ int32_t hash_find(const uint64_t * __restrict__ keys,
-                                             const int32_t * __restrict__ vals, uint64_t mask,
-                                             uint64_t key) {
-    uint64_t slot = mix64(key) & mask;
+#ifndef PXS_HASH_GROUP_BITS
+#define PXS_HASH_GROUP_BITS 0
+#endif
+// Home slot.  With G = PXS_HASH_GROUP_BITS > 0, the 2^G voxels that differ
+// only in the low G bits of z share 2^G consecutive slots.
+__device__ __forceinline__ uint64_t home_slot(uint64_t key, uint64_t mask) {
+    constexpr int G = PXS_HASH_GROUP_BITS;
+    if constexpr (G == 0) return mix64(key) & mask;
+    return ((mix64(key >> G) << G) | (key & ((1u << G) - 1))) & mask;
+}
+
+__device__ __forceinline__ HashSlot load_slot(const HashSlot * slots, uint64_t i) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(slots + i);
+    HashSlot s;
+    s.key = static_cast<unsigned long long>(v.x) | (static_cast<unsigned long long>(v.y) << 32);
+    s.val = static_cast<int32_t>(v.z);
+    s.pad = 0;
+    return s;
+}
+
+// Linear probing from the home slot; the table has at least 2n slots, so
+// every probe sequence meets an empty slot.
+__device__ __forceinline__ int32_t probe_from(const HashSlot * __restrict__ slots, uint64_t mask,
+                                              uint64_t key, uint64_t slot, HashSlot s) {
     for (uint64_t probe = 0; probe <= mask; ++probe) {
-        const uint64_t k = keys[slot];
-        if (k == key) return vals[slot];
-        if (k == kEmptyKey) return -1;
+        if (s.key == key) return s.val;
+        if (s.key == kEmptyKey) return -1;
         slot = (slot + 1) & mask;
+        s = load_slot(slots, slot);
     }
     return -1;
 }
 
-__global__ void hash_init_kernel(uint64_t * keys, int32_t * vals, int64_t cap) {
+__device__ __forceinline__ int32_t hash_find(const HashSlot * __restrict__ slots, uint64_t mask,
+                                             uint64_t key) {
+    const uint64_t slot = home_slot(key, mask);
+    return probe_from(slots, mask, key, slot, load_slot(slots, slot));
+}
+
+__global__ void hash_init_kernel(HashSlot * slots, int64_t cap) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < cap;
          i += stride) {
-        keys[i] = kEmptyKey;
-        vals[i] = INT_MAX;
+        *reinterpret_cast<uint4 *>(slots + i) = make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, INT_MAX, 0u);
     }
 }
 
 // Lock-free insert: claim a slot with a 64-bit CAS (or find the key already
-// there), then keep the smallest inserting row with atomicMin.  The table has
-// at least 2n slots, so every probe sequence meets an empty slot.
-__global__ void hash_insert_kernel(const int4 * __restrict__ coords, int64_t n,
-                                   uint64_t * keys, int32_t * vals, uint64_t mask) {
+// there), then keep the smallest inserting row with atomicMin.
+__global__ void hash_insert_kernel(const int4 * __restrict__ coords, int64_t n, HashSlot * slots,
+                                   uint64_t mask) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= n) return;
     const int4 c = coords[p];
     const uint64_t key = voxel_key(c.x, c.y, c.z, c.w);
-    uint64_t slot = mix64(key) & mask;
+    uint64_t slot = home_slot(key, mask);
     for (uint64_t probe = 0; probe <= mask; ++probe) {
-        const unsigned long long prev = atomicCAS(
-            reinterpret_cast<unsigned long long *>(keys + slot),
-            static_cast<unsigned long long>(kEmptyKey), static_cast<unsigned long long>(key));
+        const unsigned long long prev = atomicCAS(&slots[slot].key,
+                                                  static_cast<unsigned long long>(kEmptyKey),
+                                                  static_cast<unsigned long long>(key));
         if (prev == kEmptyKey || prev == key) {
-            atomicMin(vals + slot, static_cast<int32_t>(p));
+            atomicMin(&slots[slot].val, static_cast<int32_t>(p));
             return;
         }
         slot = (slot + 1) & mask;
@@ -86,8 +123,7 @@ __global__ void status_init_kernel(int64_t * status) { *status = LLONG_MAX; }
 // duplicate (5: a smaller row owns the key), not contiguous by batch (6).
 __global__ void validate_coords_kernel(const int4 * __restrict__ coords, int64_t n,
                                        int batch_size, int sx, int sy, int sz,
-                                       const uint64_t * __restrict__ keys,
-                                       const int32_t * __restrict__ vals, uint64_t mask,
+                                       const HashSlot * __restrict__ slots, uint64_t mask,
                                        int64_t * status) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= n) return;
@@ -96,7 +132,7 @@ __global__ void validate_coords_kernel(const int4 * __restrict__ coords, int64_t
     if (c.x < 0 || c.x >= batch_size || c.y < 0 || c.y >= sx || c.z < 0 || c.z >= sy ||
         c.w < 0 || c.w >= sz) {
         code = 4;
-    } else if (hash_find(keys, vals, mask, voxel_key(c.x, c.y, c.z, c.w)) !=
+    } else if (hash_find(slots, mask, voxel_key(c.x, c.y, c.z, c.w)) !=
                static_cast<int32_t>(p)) {
         code = 5;
     } else if (p > 0 && coords[p - 1].x > c.x) {
@@ -122,31 +158,45 @@ __global__ void validate_feats_kernel(const T * __restrict__ feats, int64_t coun
     }
 }
 
-// One thread per row, 27 probes; writes offset-major so each offset's
-// entries of a wavefront are contiguous.
+// One thread per (row, kd): the 9 neighbours with that x offset.  All 9 home
+// slots are loaded before any is resolved, so a thread keeps 9 probes in
+// flight; the rare collision chains are walked afterwards.  Thread index
+// kd * n + p writes nbr[(9 kd + 3 kh + kw) * n + p], so a wavefront's stores of
+// one offset are contiguous.  masks must be zero on entry (bits are ORed in).
 __global__ void __launch_bounds__(kThreads)
 neighbor_map_kernel(const int4 * __restrict__ coords, int64_t n,
-                    const uint64_t * __restrict__ keys, const int32_t * __restrict__ vals,
-                    uint64_t mask, int32_t * __restrict__ nbr, uint32_t * __restrict__ masks) {
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (p >= n) return;
+                    const HashSlot * __restrict__ slots, uint64_t mask,
+                    int32_t * __restrict__ nbr, uint32_t * __restrict__ masks) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= 3 * n) return;
+    const int kd = static_cast<int>(t / n);
+    const int64_t p = t - static_cast<int64_t>(kd) * n;
     const int4 c = coords[p];
+    const int x = c.y + kd - 1;
+    uint64_t key[9], slot[9];
+    HashSlot first[9];
+    bool probe[9];
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+        const int y = c.z + j / 3 - 1;
+        const int z = c.w + j % 3 - 1;
+        // The centre is the row itself; negative coordinates never exist.
+        probe[j] = !(kd == 1 && j == 4) && x >= 0 && y >= 0 && z >= 0;
+        key[j] = voxel_key(c.x, x, y, z);
+        slot[j] = home_slot(key[j], mask);
+        if (probe[j]) first[j] = load_slot(slots, slot[j]);
+    }
     uint32_t present = 0;
 #pragma unroll
-    for (int k = 0; k < 27; ++k) {
-        const int x = c.y + k / 9 - 1;
-        const int y = c.z + (k / 3) % 3 - 1;
-        const int z = c.w + k % 3 - 1;
+    for (int j = 0; j < 9; ++j) {
         int32_t row = -1;
-        if (k == 13) {
-            row = static_cast<int32_t>(p);
-        } else if (x >= 0 && y >= 0 && z >= 0) {
-            row = hash_find(keys, vals, mask, voxel_key(c.x, x, y, z));
-        }
+        if (kd == 1 && j == 4) row = static_cast<int32_t>(p);
+        else if (probe[j]) row = probe_from(slots, mask, key[j], slot[j], first[j]);
+        const int k = kd * 9 + j;
         if (row >= 0) present |= 1u << k;
         nbr[static_cast<int64_t>(k) * n + p] = row >= 0 ? row : static_cast<int32_t>(n);
     }
-    if (masks) masks[p] = present;
+    if (masks && present) atomicOr(masks + p, present);
 }
 
 // Pair lists: counts per (offset, block of kThreads rows).
@@ -442,8 +492,7 @@ using namespace pxs;
 extern "C" {
 
 size_t pxs_voxel_hash_bytes(int64_t n) {
-    const int64_t cap = hash_capacity(n);
-    return static_cast<size_t>(cap) * (sizeof(uint64_t) + sizeof(int32_t));
+    return static_cast<size_t>(hash_capacity(n)) * sizeof(HashSlot);
 }
 
 int pxs_voxel_hash_build(const int32_t * coords, int64_t n, void * table, void * stream) {
@@ -455,10 +504,10 @@ int pxs_voxel_hash_build(const int32_t * coords, int64_t n, void * table, void *
     const int64_t cap = static_cast<int64_t>(h.mask) + 1;
     hipStream_t s = as_stream(stream);
     hipLaunchKernelGGL(hash_init_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((cap + 255) / 256, 8192))),
-                       dim3(256), 0, s, h.keys, h.vals, cap);
+                       dim3(256), 0, s, h.slots, cap);
     if (n > 0) {
         hipLaunchKernelGGL(hash_insert_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
-                           reinterpret_cast<const int4 *>(coords), n, h.keys, h.vals, h.mask);
+                           reinterpret_cast<const int4 *>(coords), n, h.slots, h.mask);
     }
     return check_launch("pxs_voxel_hash_build");
 }
@@ -479,7 +528,7 @@ int pxs_sparse_validate(const int32_t * coords, int64_t n, int batch_size, int s
         const HashView h = hash_view(const_cast<void *>(table), n);
         hipLaunchKernelGGL(validate_coords_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
                            s, reinterpret_cast<const int4 *>(coords), n, batch_size, sx, sy, sz,
-                           h.keys, h.vals, h.mask, status);
+                           h.slots, h.mask, status);
         if (feats && channels > 0) {
             const int64_t count = n * channels;
             const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 8192));
@@ -520,9 +569,12 @@ int pxs_neighbor_map_k3(const int32_t * coords, int64_t n, const void * table, i
     if (n == 0) return PXS_OK;
     PXS_CHECK(coords && table && nbr, PXS_ERR_ARG, "pxs_neighbor_map_k3: null pointer");
     const HashView h = hash_view(const_cast<void *>(table), n);
-    hipLaunchKernelGGL(neighbor_map_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
-                       as_stream(stream), reinterpret_cast<const int4 *>(coords), n, h.keys,
-                       h.vals, h.mask, nbr, masks);
+    hipStream_t s = as_stream(stream);
+    if (masks) {
+        if (int rc = fill_u32(masks, n, 0u, s)) return rc;
+    }
+    hipLaunchKernelGGL(neighbor_map_kernel, dim3(grid_for(3 * n, kThreads)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const int4 *>(coords), n, h.slots, h.mask, nbr, masks);
     return check_launch("pxs_neighbor_map_k3");
 }
 
