@@ -23,7 +23,8 @@ Also reported on the same line:
   cpu_baseline  - the reference CPU sparse_submanifold_conv3d (compiled from
                   the reference sources, oracle/_ref) on item 0 of the same
                   workload at fp32, all host threads, voxel-GMAC/s
---workload selects another configuration (conv_fp32_64, attn_full, swin_64).
+--workload selects another configuration for profiling (conv_fp32_64,
+attn_block, swin_64, flow_step); their lines are not the headline metric.
 """
 
 from __future__ import annotations
@@ -50,7 +51,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="unet_stage_128",
-                    choices=["unet_stage_128", "conv_fp32_64", "attn_full", "swin_64"])
+                    choices=["unet_stage_128", "conv_fp32_64", "attn_block", "swin_64",
+                             "flow_step"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     return ap.parse_args()
@@ -177,6 +179,7 @@ def unet_stage(args, torch, px, W):
                                          "sparse_conv_b", "hash_map_64", "subm_conv_c")}
     dom = max(macs, key=lambda k: kern[k])
     achieved = 2.0 * macs[dom] / (kern[dom] * 1e-3) / 1e12
+    traffic = measured_traffic(dom)
     per_op = {k: {"ms": round(kern[k], 4),
                   "voxel_gmacs": round(macs[k] / (kern[k] * 1e-3) / 1e9, 1),
                   "tflops": round(2 * macs[k] / (kern[k] * 1e-3) / 1e12, 2)} for k in macs}
@@ -199,9 +202,26 @@ def unet_stage(args, torch, px, W):
                    "per_op": per_op},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic,
+                     "algorithmic_flop": 2 * macs[dom]},
     }
     return result
+
+
+def measured_traffic(op):
+    """HBM bytes per launch of `op` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by the factor
+    the same counter reads for a plain copy of known size), or None when the
+    summary does not cover this kernel."""
+    path = ROOT / "profiles" / "unet_stage_128_traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text()).get(op)
+    if not rec:
+        return None
+    return int(round((rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"])
+                     * 1024))
 
 
 def attention_metric(args, torch, px, W):
@@ -254,16 +274,224 @@ def cpu_baseline_conv():
     idx = orc.neighbor_map(coords)
     pairs = int((idx != coords.shape[0]).sum())
     ref.subm_conv3d(t, wl["w_a"], wl["b_a"])  # warm
+    # A bounded sample: whole calls until at least 10 s of CPU work.
     t0 = time.perf_counter()
-    reps = 2
-    for _ in range(reps):
+    reps = 0
+    while time.perf_counter() - t0 < 10.0 or reps < 2:
         ref.subm_conv3d(t, wl["w_a"], wl["b_a"])
+        reps += 1
     dt = (time.perf_counter() - t0) / reps
     return {"value": round(pairs * 128 * 128 / dt / 1e9, 3), "unit": "voxel-GMAC/s",
             "cores": threads, "kind": "reference",
-            "sample": f"reference sparse_submanifold_conv3d fp32, SubMConv3d 128->128 on batch "
-                      f"item 0 ({coords.shape[0]} voxels, {pairs} pairs) of the same workload, "
-                      f"mean of {reps} calls ({dt:.2f} s each)"}
+            "sample": f"reference sparse_submanifold_conv3d fp32 (compiled from the reference "
+                      f"sources, OpenMP), SubMConv3d 128->128 on batch item 0 ({coords.shape[0]} "
+                      f"voxels, {pairs} pairs) of the same workload, mean of {reps} calls "
+                      f"({dt:.2f} s each, {dt * reps:.1f} s total)"}
+
+
+# ---------------------------------------------------------------------------
+# The other configurations (parity cases; timed here for profiling).
+
+def timed_steps(args, torch, step):
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / args.steps
+
+
+def conv_fp32_64(args, torch, px, W):
+    """One fp32 SubMConv3d 64 -> 64 on ~16k voxels at 64^3: hash, map, conv."""
+    import numpy as np
+
+    dev = torch.device("cuda:0")
+    wl = W.conv_fp32_64()
+    coords = torch.from_numpy(wl["coords"]).to(dev)
+    n = coords.shape[0]
+    x = torch.from_numpy(wl["feats"]).to(dev)
+    w = torch.from_numpy(wl["weight"]).to(dev)
+    b = torch.from_numpy(wl["bias"]).to(dev)
+    y = torch.empty((n, 64), dtype=torch.float32, device=dev)
+    timer = Timer(torch)
+
+    def step():
+        nbr, masks = timer.run("hash_map", lambda: px.neighbor_map(coords))
+        timer.run("conv", lambda: px.subm_conv3d(x, w, b, nbr, masks, out=y))
+
+    nbr, masks = px.neighbor_map(coords)
+    pairs = int(np.unpackbits(masks.cpu().numpy().view(np.uint8)).sum())
+    dt = timed_steps(args, torch, step)
+    macs = pairs * 64 * 64
+    conv_ms = timer.mean_ms("conv")
+    achieved = 2.0 * macs / (conv_ms * 1e-3) / 1e12
+    return {"metric": "SubMConv3d voxel-GMAC/s, fp32 64->64 at 64^3", "value": round(macs / dt / 1e9, 2),
+            "unit": "voxel-GMAC/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "f32",
+            "config": {"workload": f"conv_fp32_64: {n} voxels, {pairs} pairs, hash+map+SubMConv3d",
+                       "hash_map_ms": round(timer.mean_ms("hash_map"), 4),
+                       "conv_ms": round(conv_ms, 4)},
+            "roofline": {"bound": "mfma", "kernel": "conv", "achieved": round(achieved, 2),
+                         "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None}}
+
+
+def attn_block(args, torch, px, W):
+    """Config 3: QKV linear 1024->3072, per-head RMS on q/k, varlen attention on
+    12,288 + 20,480 tokens (16 x 64), output linear 1024->1024, bf16."""
+    dev = torch.device("cuda:0")
+    wl = W.attn_full()
+    n, C, H, D = wl["x"].shape[0], 1024, wl["heads"], wl["head_dim"]
+    bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
+    f32 = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    x, w_qkv, w_out = bf(wl["x"]), bf(wl["w_qkv"]), bf(wl["w_out"])
+    b_qkv, b_out, gq, gk = f32(wl["b_qkv"]), f32(wl["b_out"]), f32(wl["gamma_q"]), f32(wl["gamma_k"])
+    cu = f32(wl["cu_seqlens"])
+    qkv = torch.empty((n, 3 * C), dtype=torch.bfloat16, device=dev)
+    o = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
+    timer = Timer(torch)
+
+    def step():
+        timer.run("qkv", lambda: px.linear(x, w_qkv, b_qkv, out=qkv))
+        q, k, v = timer.run("prepare", lambda: px.qkv_prepare(qkv, H, D, gq, gk))
+        timer.run("attention", lambda: px.varlen_attention(q, k, v, cu, cu, H, D, D ** -0.5, out=o))
+        timer.run("out", lambda: px.linear(o, w_out, b_out, out=y))
+
+    dt = timed_steps(args, torch, step)
+    lens = (wl["cu_seqlens"][1:] - wl["cu_seqlens"][:-1]).tolist()
+    f_attn = 4.0 * sum(L * L for L in lens) * D * H
+    flops = 2.0 * n * C * 3 * C + f_attn + 2.0 * n * C * C
+    a_ms = timer.mean_ms("attention")
+    achieved = f_attn / (a_ms * 1e-3) / 1e12
+    per_op = {k: round(timer.mean_ms(k), 4) for k in ("qkv", "prepare", "attention", "out")}
+    return {"metric": "sparse full-attention block TFLOP/s, bf16", "value": round(flops / dt / 1e12, 2),
+            "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "bf16",
+            "config": {"workload": "attn_block: 12,288 + 20,480 tokens, width 1024, 16 x 64",
+                       "per_op_ms": per_op, "flop_per_step": flops},
+            "roofline": {"bound": "mfma", "kernel": "attention", "achieved": round(achieved, 2),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}}
+
+
+def swin_64(args, torch, px, W):
+    """Config 4: two shifted-window attention blocks (window 8, shift 0 then 4,
+    12 x 64, width 768) on ~28k voxels at 64^3, then the channel-to-spatial
+    upsample: SubMConv3d 768 -> 8*192 at 64^3 and subdivision to 128^3."""
+    dev = torch.device("cuda:0")
+    wl = W.swin_64()
+    coords = torch.from_numpy(wl["coords"]).to(dev)
+    n, C, H, D = wl["x"].shape[0], 768, wl["heads"], wl["head_dim"]
+    bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
+    f32 = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    x, w_qkv, w_out, w_up = bf(wl["x"]), bf(wl["w_qkv"]), bf(wl["w_out"]), bf(wl["w_up"])
+    b_qkv, b_out, b_up = f32(wl["b_qkv"]), f32(wl["b_out"]), f32(wl["b_up"])
+    h = x.clone()
+    qkv = torch.empty((n, 3 * C), dtype=torch.bfloat16, device=dev)
+    o = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
+    packed = torch.empty((n, 8 * 192), dtype=torch.bfloat16, device=dev)
+    timer = Timer(torch)
+    win_flops = []
+
+    def step():
+        for shift in wl["shifts"]:
+            fwd, bwd, cu, nw = timer.run(f"partition_{shift}", lambda: px.window_partition(
+                coords, 1, wl["shape"], wl["window"], shift))
+            if len(win_flops) < len(wl["shifts"]):
+                lens = (cu[1:] - cu[:-1]).cpu().double()
+                win_flops.append(float(4.0 * (lens * lens).sum() * D * H))
+            timer.run("qkv", lambda: px.linear(h, w_qkv, b_qkv, out=qkv))
+            q, k, v = qkv[:, :C], qkv[:, C:2 * C], qkv[:, 2 * C:]
+            timer.run("window_attention", lambda: px.varlen_attention(
+                q, k, v, cu, cu, H, D, D ** -0.5, row_map=fwd, out=o, nseg=nw))
+            timer.run("out", lambda: px.linear(o, w_out, b_out, out=h))
+        nbr, masks = timer.run("hash_map", lambda: px.neighbor_map(coords))
+        timer.run("up_conv", lambda: px.subm_conv3d(h, w_up, b_up, nbr, masks, out=packed))
+        timer.run("c2s", lambda: px.channel_to_spatial(coords, packed))
+
+    dt = timed_steps(args, torch, step)
+    nbr, masks = px.neighbor_map(coords)
+    import numpy as np
+    pairs = int(np.unpackbits(masks.cpu().numpy().view(np.uint8)).sum())
+    f_win = sum(win_flops)
+    f_lin = len(wl["shifts"]) * (2.0 * n * C * 3 * C + 2.0 * n * C * C)
+    f_up = 2.0 * pairs * C * 8 * 192
+    flops = f_win + f_lin + f_up
+    per_op = {k: round(timer.mean_ms(k), 4) for k in ("qkv", "window_attention", "out", "hash_map",
+                                                      "up_conv", "c2s", "partition_0", "partition_4")}
+    up_tf = f_up / (timer.mean_ms("up_conv") * 1e-3) / 1e12
+    return {"metric": "shifted-window attention + C2S upsample TFLOP/s, bf16",
+            "value": round(flops / dt / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4),
+            "dtype": "bf16",
+            "config": {"workload": f"swin_64: {n} voxels, window 8 shift 0/4, 12 x 64, "
+                                   f"up-conv 768->1536 ({pairs} pairs) + C2S to 128^3",
+                       "per_op_ms": per_op,
+                       "window_attention_tflops": round(
+                           f_win / len(wl["shifts"]) / (timer.mean_ms("window_attention") * 1e-3) / 1e12, 2)},
+            "roofline": {"bound": "mfma", "kernel": "up_conv", "achieved": round(up_tf, 2),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(up_tf / PEAK_BF16_TFLOPS, 4), "traffic": None}}
+
+
+def flow_step(args, torch, px, W):
+    """Config 5: one SLat-flow forward (24 blocks, width 1024) on ~42k voxels,
+    device resident (pxs_slat_flow_forward), random N(0, 0.02) weights."""
+    import pxs as P
+
+    dev = torch.device("cuda:0")
+    wl = W.flow_step_64()
+    coords = torch.from_numpy(wl["coords"]).to(dev)
+    n, C, H, M, T = coords.shape[0], wl["width"], wl["heads"], wl["mlp_hidden"], wl["context_tokens"]
+    nb = wl["blocks"]
+    g = torch.Generator(device=dev).manual_seed(5)
+    rnd = lambda *s, std=0.02, dt=torch.bfloat16: (torch.randn(*s, generator=g, device=dev) * std).to(dt)  # noqa: E731
+    one = lambda c: torch.ones(c, device=dev)  # noqa: E731
+    zero = lambda c: torch.zeros(c, device=dev)  # noqa: E731
+    keep = []
+    blocks = []
+    for _ in range(nb):
+        ws = [rnd(6 * C, dt=torch.float32), rnd(3 * C, C), zero(3 * C), one(C), one(C), rnd(C, C),
+              zero(C), one(C), zero(C), rnd(C, C), zero(C), rnd(2 * C, C), zero(2 * C), one(C),
+              one(C), rnd(C, C), zero(C), None, None, rnd(M, C), zero(M), rnd(C, M), zero(C)]
+        keep.append(ws)
+        blocks.append(P.block_weights(ws))
+    fw = [rnd(C, 8, dt=torch.float32), zero(C), rnd(C, 256, dt=torch.float32), zero(C),
+          rnd(C, C, dt=torch.float32), zero(C), rnd(6 * C, C, dt=torch.float32), zero(6 * C),
+          rnd(8, C, dt=torch.float32), zero(8)]
+    arr = (P.BlockWeights * nb)(*blocks)
+    weights = P.FlowWeights(*[t.data_ptr() for t in fw], arr)
+    cfg = P.FlowConfig(8, 8, C, C, nb, H, 0, M, 1e-6, 1.0, 10000.0, 1, 1, 0)
+    x = torch.randn(n, 8, generator=g, device=dev)
+    tsteps = torch.rand(1, generator=g, device=dev) * 1000.0
+    ctx = torch.randn(T, C, generator=g, device=dev).to(torch.bfloat16)
+    ctx_off = torch.tensor([0, T], dtype=torch.int64, device=dev)
+    cu = px.batch_cu_seqlens(coords, 1)
+    out = torch.empty((n, 8), dtype=torch.float32, device=dev)
+    ws = torch.empty(px.flow_workspace_bytes(cfg, n, T, 1, P.PXS_BF16), dtype=torch.uint8, device=dev)
+
+    def step():
+        px.slat_flow_forward(cfg, weights, coords, 1, cu, x, tsteps, ctx, ctx_off, out=out,
+                             workspace=ws, dtype=P.PXS_BF16)
+
+    dt = timed_steps(args, torch, step)
+    f_self = 4.0 * n * n * 64 * H
+    f_lin = 2.0 * n * C * (3 * C + C + C + C + 2 * M)
+    f_cross = 4.0 * n * T * 64 * H + 2.0 * T * C * 2 * C
+    flops = nb * (f_self + f_lin + f_cross) + 2.0 * n * (8 * C + C * 8)
+    assert torch.isfinite(out).all().item()
+    return {"metric": "SLat-flow step TFLOP/s, bf16", "value": round(flops / dt / 1e12, 2),
+            "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "bf16",
+            "config": {"workload": f"flow_step: {n} voxels at 64^3, 24 blocks width 1024 "
+                                   f"(16 x 64, MLP 4096), 1,370 context tokens",
+                       "flop_per_step": flops},
+            "roofline": {"bound": "mfma", "kernel": "whole forward", "achieved": round(flops / dt / 1e12, 2),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(flops / dt / 1e12 / PEAK_BF16_TFLOPS, 4), "traffic": None}}
+
+
+OTHER_WORKLOADS = {"conv_fp32_64": conv_fp32_64, "attn_block": attn_block, "swin_64": swin_64,
+                   "flow_step": flow_step}
 
 
 def main():
@@ -280,8 +508,7 @@ def main():
 
     px = pxs.Pxs()
     if args.workload != "unet_stage_128":
-        from bench_workloads import run_workload
-        result = run_workload(args, torch, px, W)
+        result = OTHER_WORKLOADS[args.workload](args, torch, px, W)
     else:
         result = unet_stage(args, torch, px, W)
         if not args.no_attention:

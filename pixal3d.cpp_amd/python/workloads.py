@@ -186,3 +186,15 @@ def swin_64(seed: int = 4, width: int = 768, heads: int = 12, up_out: int = 192)
                 b_out=np.zeros(width, np.float32), w_up=w_up,
                 b_up=np.zeros(8 * up_out, np.float32), heads=heads, head_dim=width // heads,
                 window=8, shifts=(0, 4))
+
+
+FLOW_SHELLS = [(24.0, 31.0), (18.0, 30.0), (12.0, 24.0)]
+
+
+def flow_step_64(seed: int = 5):
+    """One SLat-flow denoising step: ~42k voxels on 64^3 (three nested shells),
+    24 blocks of width 1024 (16 heads x 64, MLP 4096), cross-attention to 1,370
+    condition tokens of width 1024, input/output linears 8 -> 1024 -> 8."""
+    coords = shell_coords(64, [FLOW_SHELLS], seed)
+    return dict(coords=coords, batch_size=1, shape=(64, 64, 64), in_channels=8, out_channels=8,
+                width=1024, heads=16, mlp_hidden=4096, blocks=24, context_tokens=1370)
