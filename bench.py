@@ -397,7 +397,7 @@ def swin_64(args, torch, px, W):
     def step():
         for shift in wl["shifts"]:
             fwd, bwd, cu, nw = timer.run(f"partition_{shift}", lambda: px.window_partition(
-                coords, 1, wl["shape"], wl["window"], shift))
+                coords, 1, wl["shape"], wl["window"], shift, sync=False))
             if len(win_flops) < len(wl["shifts"]):
                 lens = (cu[1:] - cu[:-1]).cpu().double()
                 win_flops.append(float(4.0 * (lens * lens).sum() * D * H))

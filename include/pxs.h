@@ -259,7 +259,10 @@ int pxs_batch_cu_seqlens(const int32_t * coords, int64_t n, int batch_size, int6
  * ceil((S + shift) / window), wid = ((b*nx + wx)*ny + wy)*nz + wz.
  * fwd = stable sort of rows by wid, bwd = its inverse; cu_seqlens
  * (capacity n + 1) bounds the non-empty windows in ascending wid and
- * *nwin_out (device int64) receives their count. */
+ * *nwin_out (device int64) receives their count.  Entries nwin .. cap, with
+ * cap = min(n, batch_size * nx * ny * nz) known on the host, hold n: passing
+ * nseg = cap to pxs_varlen_attention (empty trailing segments) needs no read
+ * of *nwin_out. */
 size_t pxs_window_partition_workspace_bytes(int batch_size, int sx, int sy, int sz, int window,
                                             int shift, int64_t n);
 int pxs_window_partition(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
@@ -384,6 +387,67 @@ int pxs_slat_flow_forward(int dtype, const pxs_flow_config * cfg, const pxs_flow
                           const void * context, const int64_t * context_offsets,
                           int64_t context_tokens, const void * projected, float * out,
                           void * workspace, void * stream);
+
+/* ---- a16: SLat-decoder blocks, device resident ------------------------------------ */
+
+/* SLatDecoderBlockWeightsF32 (include/pixal3d/slat_decoder.h:18-41) as device
+ * pointers in the same order.  Convolution weights ([27, out, in]) and the
+ * ConvNeXt MLP weights ([out, in]) are in the call's dtype; norms and biases
+ * are fp32, and so is to_subdiv_weight (the subdivision logits select
+ * children by sign, so they are computed in fp32 in every dtype).  Members a
+ * block kind does not use may be NULL. */
+typedef struct pxs_decoder_block_weights {
+    const float * norm_weight;
+    const float * norm_bias;
+    const float * norm1_weight;
+    const float * norm1_bias;
+    const void * conv1_weight;
+    const float * conv1_bias;
+    const float * norm2_weight;
+    const float * norm2_bias;
+    const void * conv2_weight;
+    const float * conv2_bias;
+    const void * mlp0_weight;
+    const float * mlp0_bias;
+    const void * mlp2_weight;
+    const float * mlp2_bias;
+    const float * to_subdiv_weight;
+    const float * to_subdiv_bias;
+} pxs_decoder_block_weights;
+
+/* sparse_convnext_block_f32 (src/slat_decoder.cpp:185-224): y = x +
+ * MLP2(SiLU(MLP0(LN_affine(SubMConv3d(x))))) with MLP0 channels -> mlp_hidden.
+ * x, y fp32 [rows, channels] and may be the same buffer.  nbr/masks: the
+ * level's neighbor map (pxs_neighbor_map_k3), or both NULL to build it in the
+ * workspace (have_map = 0 in the size query). */
+size_t pxs_convnext_block_workspace_bytes(int dtype, int64_t rows, int channels, int mlp_hidden,
+                                          int have_map);
+int pxs_convnext_block(int dtype, const int32_t * coords, int64_t rows, const float * x,
+                       int channels, int mlp_hidden, float eps,
+                       const pxs_decoder_block_weights * w, const int32_t * nbr,
+                       const uint32_t * masks, float * y, void * workspace, void * stream);
+
+/* sparse_resblock_c2s_f32 (src/slat_decoder.cpp:226-288): subdivide x
+ * [rows, channels] (channels % 8 == 0) to the 2x grid.  Children are selected
+ * by subdivision (fp32 [rows, 8], > 0), by the block's own to_subdiv logits
+ * when pred_subdiv (written to predicted_subdiv [rows, 8] if non-NULL), or all
+ * kept when neither is given.  Output: out_coords [m, 4] and y fp32
+ * [m, out_channels] with m <= 8 * rows; *rows_out (host) receives m.  When
+ * children are selected the call waits once on the stream to read m.
+ * out_channels must be a multiple of channels / 8 (the repeated skip). */
+size_t pxs_resblock_c2s_workspace_bytes(int dtype, int64_t rows, int channels,
+                                        int out_channels);
+int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const float * x,
+                     int channels, int out_channels, float eps,
+                     const pxs_decoder_block_weights * w, int pred_subdiv,
+                     const float * subdivision, float * predicted_subdiv, int32_t * out_coords,
+                     float * y, int64_t * rows_out, void * workspace, void * stream);
+
+/* repeat_channels + add_in_place (src/slat_decoder.cpp:44-107):
+ * y[r, j] = a[r, j] + skip[r, j / (channels / skip_channels)], y fp32; a in
+ * a_dtype (may be y itself when PXS_F32). */
+int pxs_add_repeat(int a_dtype, const void * a, int64_t rows, int channels, const float * skip,
+                   int skip_channels, float * y, void * stream);
 
 #ifdef __cplusplus
 }

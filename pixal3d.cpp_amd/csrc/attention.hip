@@ -52,6 +52,30 @@ __device__ __forceinline__ int64_t remap_xcd64(int64_t bid, int64_t blocks) {
     return (xcd < rem) ? xcd * (q + 1) + slot : rem * (q + 1) + (xcd - rem) * q + slot;
 }
 
+// The segment owning query tile t: the largest s with tile_start[s] <= t
+// (tile_start is non-decreasing; empty segments repeat a value).  The wave
+// samples 64 evenly spaced entries per round and keeps the last interval whose
+// start is <= t, so nseg <= 64 takes one dependent load and nseg <= 4096 two.
+__device__ __forceinline__ int find_segment(const int64_t * __restrict__ tile_start, int nseg,
+                                            int64_t t, int lane) {
+    int lo = 0, len = nseg;
+    while (len > 1) {
+        const int stride = (len + 63) >> 6;
+        const int off = lane * stride;
+        const bool le = off < len && tile_start[lo + off] <= t;
+        const int cnt = __popcll(__ballot(le));  // >= 1: tile_start[lo] <= t
+        lo += (cnt - 1) * stride;
+        len = min(stride, len - (cnt - 1) * stride);
+    }
+    return __builtin_amdgcn_readfirstlane(lo);
+}
+
+// Mean segment length from which the generic kernel runs 4 waves per
+// workgroup instead of one.
+#ifndef PXS_ATTN_NW4_MIN
+#define PXS_ATTN_NW4_MIN 256
+#endif
+
 struct AttnArgs {
     const void * q;
     const void * k;
@@ -120,13 +144,7 @@ flash_attn_kernel(AttnArgs a) {
 
     const int64_t t = blockIdx.x;
     if (t >= a.tile_start[a.nseg]) return;
-    int lo = 0, hi = a.nseg - 1;
-    while (lo < hi) {  // largest s with tile_start[s] <= t
-        const int mid = (lo + hi + 1) >> 1;
-        if (a.tile_start[mid] <= t) lo = mid;
-        else hi = mid - 1;
-    }
-    const int seg = lo;
+    const int seg = find_segment(a.tile_start, a.nseg, t, lane);
     const int64_t q_begin = a.cu_q[seg] + (t - a.tile_start[seg]) * (32 * NW);
     const int64_t q_end = a.cu_q[seg + 1];
     const int64_t k_begin = a.cu_k[seg], k_end = a.cu_k[seg + 1];
@@ -364,13 +382,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     const int head = static_cast<int>(logical / tiles_bound);
     const int64_t t = logical - static_cast<int64_t>(head) * tiles_bound;
     if (t >= a.tile_start[a.nseg]) return;
-    int lo = 0, hi = a.nseg - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (a.tile_start[mid] <= t) lo = mid;
-        else hi = mid - 1;
-    }
-    const int seg = lo;
+    const int seg = find_segment(a.tile_start, a.nseg, t, lane);
     const int64_t q_begin = a.cu_q[seg] + (t - a.tile_start[seg]) * (32 * NW);
     const int64_t q_end = a.cu_q[seg + 1];
     const int64_t k_begin = a.cu_k[seg], k_end = a.cu_k[seg + 1];
@@ -656,13 +668,16 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     PXS_CHECK(q && k && v && o && cu_q && cu_k && workspace, PXS_ERR_ARG,
               "pxs_varlen_attention: null pointer");
     hipStream_t s = as_stream(stream);
-    // Small segments (windows) use one wavefront per workgroup.
-    const int nw = (total_q / nseg >= 256) ? 4 : 1;
     const bool fast = dtype == PXS_BF16 && head_dim == 64 && value_dim == 64 && (ld_q % 8 == 0) &&
                       (ld_k % 8 == 0) && (ld_v % 8 == 0) && (ld_o % 4 == 0) && aligned16(q) &&
                       aligned16(k) && aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0;
-    // Queries per workgroup: the fast kernel runs 64 per wave, the generic one 32.
-    const int q_tile = 32 * nw;  // queries per workgroup: 32 per wave in every kernel
+    // Waves per workgroup (32 queries each, sharing the K/V tiles).  The bf16
+    // kernel always runs 4: its 4-stage K/V ring takes 64 KB of LDS per
+    // workgroup whatever the wave count, so fewer waves only lower occupancy
+    // (windows of ~100 rows run 3.6x faster with 4 waves than with 1).  The
+    // generic kernel drops to one wave for short segments.
+    const int nw = (fast || total_q / nseg >= PXS_ATTN_NW4_MIN) ? 4 : 1;
+    const int q_tile = 32 * nw;
     int64_t * tile_start = static_cast<int64_t *>(workspace);
     int32_t * tiles = reinterpret_cast<int32_t *>(tile_start + nseg + 1);
     void * scan_ws = reinterpret_cast<void *>(
@@ -680,10 +695,7 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     a.vec_ok = (head_dim % vec == 0) && (value_dim % vec == 0) && (ld_q % vec == 0) && (ld_k % vec == 0) &&
                (ld_v % vec == 0) && aligned16(q) && aligned16(k) && aligned16(v);
     if (dtype == PXS_BF16) {
-        if (fast) {
-            return nw == 4 ? launch_attn_bf16<4>(a, total_q, heads, s)
-                           : launch_attn_bf16<1>(a, total_q, heads, s);
-        }
+        if (fast) return launch_attn_bf16<4>(a, total_q, heads, s);
         return nw == 4 ? launch_attn<uint16_t, 4>(a, total_q, heads, s)
                        : launch_attn<uint16_t, 1>(a, total_q, heads, s);
     }

@@ -10,6 +10,7 @@
 // The adaLN modulate and the gates are fused into the layer-norm kernel and
 // the GEMM epilogues; RMS norm and RoPE are fused into one QKV prologue.
 
+#include "carve.h"
 #include "pxs_common.h"
 #include "scan.h"
 
@@ -17,29 +18,6 @@
 
 namespace pxs {
 namespace {
-
-constexpr size_t kAlign = 256;
-
-size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
-
-size_t dtype_bytes(int dtype) { return dtype == PXS_BF16 ? 2 : 4; }
-
-// Carves aligned sub-buffers out of a caller workspace, in a fixed order, so
-// the size query and the call agree by construction.
-class Carver {
-public:
-    explicit Carver(void * base) : base_(static_cast<char *>(base)) {}
-    void * take(size_t bytes) {
-        void * p = base_ ? base_ + used_ : nullptr;
-        used_ += align_up(bytes);
-        return p;
-    }
-    size_t used() const { return used_; }
-
-private:
-    char * base_;
-    size_t used_ = 0;
-};
 
 struct BlockBuffers {
     void * xm;    // [rows, C]       LN output fed to a GEMM
@@ -99,10 +77,6 @@ int check_block_args(const pxs_block_config * cfg, const pxs_block_weights * w) 
     return PXS_OK;
 }
 
-#define PXS_TRY(expr)              \
-    do {                           \
-        if (int rc_ = (expr)) return rc_; \
-    } while (0)
 
 int run_block(int dtype, const pxs_block_config & cfg, const pxs_block_weights & w,
               const int32_t * coords, int64_t rows, int batch_size, const int64_t * cu_rows,

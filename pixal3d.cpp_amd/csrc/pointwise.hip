@@ -218,6 +218,23 @@ __global__ void convert_kernel(const TS * __restrict__ x, int64_t count, TD * __
     }
 }
 
+// repeat_channels followed by add_in_place (src/slat_decoder.cpp:44-107):
+// y[r, j] = a[r, j] + skip[r, j / repeats].  a and y may be the same fp32
+// buffer: each element is read and written by one thread.
+template <typename T>
+__global__ void add_repeat_kernel(const T * a, int64_t rows, int channels,
+                                  const float * __restrict__ skip, int skip_channels, int repeats,
+                                  float * y) {
+    const int64_t count = rows * channels;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride) {
+        const int64_t r = i / channels;
+        const int j = static_cast<int>(i - r * channels);
+        y[i] = load_f32(a + i) + skip[r * skip_channels + j / repeats];
+    }
+}
+
 // Sinusoidal timestep embedding (src/flow.cpp:92-123): cos half then sin
 // half, frequency exp(-ln(max_period) * i / half); a trailing odd column is 0.
 __global__ void timestep_embedding_kernel(const float * __restrict__ t, int64_t batch, int dim,
@@ -468,6 +485,28 @@ int pxs_convert(int src_dtype, const void * x, int64_t count, int dst_dtype, voi
                            static_cast<const uint16_t *>(x), count, static_cast<uint16_t *>(y));
     }
     return check_launch("pxs_convert");
+}
+
+int pxs_add_repeat(int a_dtype, const void * a, int64_t rows, int channels, const float * skip,
+                   int skip_channels, float * y, void * stream) {
+    PXS_CHECK(check_dtype(a_dtype), PXS_ERR_ARG, "pxs_add_repeat: bad dtype");
+    PXS_CHECK(rows >= 0 && channels > 0 && skip_channels > 0 && channels % skip_channels == 0,
+              PXS_ERR_ARG, "SLat decoder skip channels are not repeatable");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(a && skip && y, PXS_ERR_ARG, "pxs_add_repeat: null pointer");
+    const int64_t count = rows * channels;
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
+    const int repeats = channels / skip_channels;
+    if (a_dtype == PXS_F32) {
+        hipLaunchKernelGGL(add_repeat_kernel<float>, dim3(blocks), dim3(256), 0, as_stream(stream),
+                           static_cast<const float *>(a), rows, channels, skip, skip_channels,
+                           repeats, y);
+    } else {
+        hipLaunchKernelGGL(add_repeat_kernel<uint16_t>, dim3(blocks), dim3(256), 0,
+                           as_stream(stream), static_cast<const uint16_t *>(a), rows, channels,
+                           skip, skip_channels, repeats, y);
+    }
+    return check_launch("pxs_add_repeat");
 }
 
 int pxs_timestep_embedding(const float * timesteps, int64_t batch, int dim, int max_period,

@@ -360,13 +360,17 @@ __global__ void window_flags_kernel(const int32_t * __restrict__ counts, int64_t
     if (i < windows) flags[i] = counts[i] > 0 ? 1 : 0;
 }
 
+// cu[rank] = start of each non-empty window; cu[nwin .. cap] = n, so that
+// any segment count between nwin and cap = min(n, windows) describes the same
+// partition (the extra segments are empty).
 __global__ void window_cu_kernel(const int32_t * __restrict__ counts, int64_t windows,
                                  const int64_t * __restrict__ start,
                                  const int64_t * __restrict__ rank, const int64_t * __restrict__ nwin,
-                                 int64_t n, int64_t * __restrict__ cu) {
+                                 int64_t n, int64_t cap, int64_t * __restrict__ cu) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < windows && counts[i] > 0) cu[rank[i]] = start[i];
-    if (i == 0) cu[*nwin] = n;
+    const int64_t nw = *nwin;
+    if (i >= nw && i <= cap) cu[i] = n;
 }
 
 __global__ void window_place_kernel(const int4 * __restrict__ coords, int64_t n, int window,
@@ -773,12 +777,13 @@ int pxs_window_partition(const int32_t * coords, int64_t n, int batch_size, int 
                        counts, windows, flags);
     rc = exclusive_scan_i32(flags, rank, windows, nwin_out, scan_ws, s);
     if (rc) return rc;
-    hipLaunchKernelGGL(window_cu_kernel, dim3(grid_for(windows, kThreads)), dim3(kThreads), 0, s,
-                       counts, windows, start, rank, nwin_out, n, cu_seqlens);
+    const int64_t cap = std::min<int64_t>(n, windows);
+    hipLaunchKernelGGL(window_cu_kernel, dim3(grid_for(windows + 1, kThreads)), dim3(kThreads), 0,
+                       s, counts, windows, start, rank, nwin_out, n, cap, cu_seqlens);
     hipLaunchKernelGGL(window_place_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
                        n, window, shift, g, start, slot, tmp);
-    // At most n non-empty windows; workgroups past *nwin exit at once.
-    hipLaunchKernelGGL(window_sort_kernel, dim3(static_cast<unsigned>(n)), dim3(kThreads), 0, s,
+    // At most cap non-empty windows; workgroups past *nwin exit at once.
+    hipLaunchKernelGGL(window_sort_kernel, dim3(static_cast<unsigned>(cap)), dim3(kThreads), 0, s,
                        tmp, cu_seqlens, nwin_out, fwd, bwd);
     return check_launch("pxs_window_partition");
 }

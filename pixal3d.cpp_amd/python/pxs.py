@@ -80,6 +80,13 @@ _SIGS = {
     "pxs_window_partition_workspace_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32, _i32, _i32, _i64]),
     "pxs_window_partition": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                     _vp, _vp]),
+    "pxs_convnext_block_workspace_bytes": (C.c_size_t, [_i32, _i64, _i32, _i32, _i32]),
+    "pxs_convnext_block": (_i32, [_i32, _vp, _i64, _vp, _i32, _i32, _f, _vp, _vp, _vp, _vp, _vp,
+                                  _vp]),
+    "pxs_resblock_c2s_workspace_bytes": (C.c_size_t, [_i32, _i64, _i32, _i32]),
+    "pxs_resblock_c2s": (_i32, [_i32, _vp, _i64, _vp, _i32, _i32, _f, _vp, _i32, _vp, _vp, _vp,
+                                _vp, _vp, _vp, _vp]),
+    "pxs_add_repeat": (_i32, [_i32, _vp, _i64, _i32, _vp, _i32, _vp, _vp]),
 }
 
 
@@ -119,6 +126,24 @@ class FlowWeights(C.Structure):
         "input_weight", "input_bias", "timestep_weight0", "timestep_bias0", "timestep_weight2",
         "timestep_bias2", "modulation_weight", "modulation_bias", "output_weight",
         "output_bias")] + [("blocks", C.POINTER(BlockWeights))]
+
+
+DECODER_WEIGHT_FIELDS = (
+    "norm_weight", "norm_bias", "norm1_weight", "norm1_bias", "conv1_weight", "conv1_bias",
+    "norm2_weight", "norm2_bias", "conv2_weight", "conv2_bias", "mlp0_weight", "mlp0_bias",
+    "mlp2_weight", "mlp2_bias", "to_subdiv_weight", "to_subdiv_bias")
+# Members stored in the call's dtype (convolution and ConvNeXt MLP weights).
+DECODER_DTYPE_WEIGHTS = frozenset({"conv1_weight", "conv2_weight", "mlp0_weight", "mlp2_weight"})
+
+
+class DecoderBlockWeights(C.Structure):
+    _fields_ = [(name, C.c_void_p) for name in DECODER_WEIGHT_FIELDS]
+
+
+def decoder_block_weights(tensors: dict) -> DecoderBlockWeights:
+    """Device tensors by DECODER_WEIGHT_FIELDS name; missing names are NULL."""
+    return DecoderBlockWeights(*[tensors[k].data_ptr() if tensors.get(k) is not None else None
+                                 for k in DECODER_WEIGHT_FIELDS])
 
 
 def block_weights(tensors) -> BlockWeights:
@@ -253,7 +278,10 @@ class Pxs:
         mm = int(m.item())
         return oc[:mm], off[: mm + 1], rows[:n], mm
 
-    def window_partition(self, coords, batch_size, shape, window, shift):
+    def window_partition(self, coords, batch_size, shape, window, shift, sync=True):
+        """-> (fwd, bwd, cu, nseg).  sync=False skips reading the window count:
+        nseg is then the host bound min(n, windows) and cu ends in empty
+        segments."""
         n = coords.shape[0]
         dev = coords.device
         fwd = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
@@ -266,6 +294,10 @@ class Pxs:
                                                   shape[2], window, shift, _ptr(fwd), _ptr(bwd),
                                                   _ptr(cu), _ptr(nwin), _ptr(ws), self.stream()),
                     "pxs_window_partition")
+        if not sync:
+            grid = [(e + shift + window - 1) // window for e in shape]
+            cap = min(n, batch_size * grid[0] * grid[1] * grid[2])
+            return fwd[:n], bwd[:n], cu[: cap + 1], cap
         nw = int(nwin.item())
         return fwd[:n], bwd[:n], cu[: nw + 1], nw
 
@@ -441,6 +473,44 @@ class Pxs:
             dtype, C.byref(cfg), C.byref(weights), _ptr(coords), rows, batch_size, _ptr(cu),
             _ptr(x), _ptr(timesteps), _ptr(context), _ptr(ctx_offsets), tokens, _ptr(projected),
             _ptr(y), _ptr(ws), self.stream()), "pxs_slat_flow_forward")
+        return y
+
+    def convnext_block(self, coords, x, mlp_hidden, eps, weights: DecoderBlockWeights, dtype,
+                       nbr=None, masks=None, out=None):
+        """pxs_convnext_block: x fp32 [rows, C] -> fp32 [rows, C] (out may be x)."""
+        rows, ch = x.shape
+        y = torch.empty_like(x) if out is None else out
+        ws = self._ws(self.lib.pxs_convnext_block_workspace_bytes(
+            dtype, rows, ch, mlp_hidden, int(nbr is not None)), x.device)
+        self._check(self.lib.pxs_convnext_block(
+            dtype, _ptr(coords), rows, _ptr(x), ch, mlp_hidden, eps, C.byref(weights), _ptr(nbr),
+            _ptr(masks), _ptr(y), _ptr(ws), self.stream()), "pxs_convnext_block")
+        return y
+
+    def resblock_c2s(self, coords, x, out_channels, eps, weights: DecoderBlockWeights, dtype,
+                     subdivision=None, pred_subdiv=False):
+        """pxs_resblock_c2s -> (out_coords [m, 4], y fp32 [m, out], predicted [rows, 8] or None)."""
+        rows, ch = x.shape
+        dev = x.device
+        oc = torch.empty((max(8 * rows, 1), 4), dtype=torch.int32, device=dev)
+        y = torch.empty((max(8 * rows, 1), out_channels), dtype=torch.float32, device=dev)
+        pred = torch.empty((max(rows, 1), 8), dtype=torch.float32, device=dev) if pred_subdiv \
+            else None
+        m = C.c_int64(0)
+        ws = self._ws(self.lib.pxs_resblock_c2s_workspace_bytes(dtype, rows, ch, out_channels),
+                      dev)
+        self._check(self.lib.pxs_resblock_c2s(
+            dtype, _ptr(coords), rows, _ptr(x), ch, out_channels, eps, C.byref(weights),
+            int(pred_subdiv), _ptr(subdivision), _ptr(pred), _ptr(oc), _ptr(y), C.byref(m),
+            _ptr(ws), self.stream()), "pxs_resblock_c2s")
+        return oc[:m.value], y[:m.value], (pred[:rows] if pred is not None else None)
+
+    def add_repeat(self, a, skip, out=None):
+        rows, ch = a.shape
+        y = torch.empty((rows, ch), dtype=torch.float32, device=a.device) if out is None else out
+        self._check(self.lib.pxs_add_repeat(_dtype_code(a), _ptr(a), rows, ch, _ptr(skip),
+                                            skip.shape[1], _ptr(y), self.stream()),
+                    "pxs_add_repeat")
         return y
 
     def flow_workspace_bytes(self, cfg: FlowConfig, rows, tokens, batch_size, dtype):

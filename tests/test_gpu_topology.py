@@ -3,6 +3,7 @@ topology, window partition, cu_seqlens, channel-to-spatial.  All integer
 outputs must match the oracle bit for bit."""
 
 import numpy as np
+import torch
 import pytest
 
 import oracle as O
@@ -103,6 +104,28 @@ def test_window_partition_bit_exact(px, orc, case, shift):
     np.testing.assert_array_equal(fwd.cpu().numpy(), rfwd)
     np.testing.assert_array_equal(bwd.cpu().numpy(), rbwd)
     np.testing.assert_array_equal(cu.cpu().numpy(), rcu)
+
+
+def test_window_partition_padded_segments(px, orc):
+    """Without reading the window count, cu_seqlens up to min(n, windows) ends
+    in empty segments, and attention over that bound equals attention over
+    the exact count."""
+    coords = W.shell_coords(64, [W.SWIN_SHELLS], 4)
+    n = coords.shape[0]
+    c = ti32(coords)
+    fwd, bwd, cu, nwin = px.window_partition(c, 1, (64, 64, 64), 8, 4)
+    _, _, cu_b, cap = px.window_partition(c, 1, (64, 64, 64), 8, 4, sync=False)
+    assert cap == min(n, 9 ** 3) and cap >= nwin
+    cb = cu_b.cpu().numpy()
+    np.testing.assert_array_equal(cb[: nwin + 1], cu.cpu().numpy())
+    assert (cb[nwin:] == n).all()
+    H, D = 2, 64
+    g = torch.Generator().manual_seed(5)
+    q, k, v = [torch.randn(n, H * D, generator=g).to("cuda").to(torch.bfloat16) for _ in range(3)]
+    o1 = px.varlen_attention(q, k, v, cu, cu, H, D, 0.125, row_map=fwd, nseg=nwin)
+    o2 = px.varlen_attention(q, k, v, cu_b, cu_b, H, D, 0.125, row_map=fwd, nseg=cap)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(o1.float().cpu().numpy(), o2.float().cpu().numpy())
 
 
 def test_batch_cu_seqlens(px, orc):

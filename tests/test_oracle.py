@@ -296,3 +296,85 @@ def test_validation_messages_match_compiled_reference(orc):
         ok, msg = ref.valid(ref.sparse(coords, feats, batch, (4, 4, 4)))
         code, _ = orc.sparse_valid(coords, batch, (4, 4, 4), feats, 2)
         assert not ok and code and O.VALID_MESSAGES[code] == msg
+
+
+# --- decoder blocks: compositions of compiled reference primitives ---------------
+
+def _silu(v):
+    """silu_in_place (src/slat_decoder.cpp:68-78)."""
+    v = np.asarray(v, np.float32)
+    return v * (np.float32(1.0) / (np.float32(1.0) + np.exp(-v)))
+
+
+@pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref is built only where /root/reference exists")
+def test_decoder_blocks_compose_reference_primitives(orc):
+    """orc_convnext_block and orc_resblock_c2s against the compiled reference's
+    conv / layer norm / linear / channel_to_spatial chained in the order of
+    src/slat_decoder.cpp:185-288, with SiLU and repeat_channels
+    (src/slat_decoder.cpp:68-107) applied between the calls."""
+    ref = O.Reference()
+    seed, G, C, M, O_ = 51, 12, 16, 32, 8
+    coords = W.shell_coords(G, [[(3.0, 4.5)], [(2.5, 4.0)]], seed)
+    n = coords.shape[0]
+    x = W.normal(seed, n * C, 1).reshape(n, C)
+    g, b = 1.0 + W.normal(seed, C, 2, std=0.1), W.normal(seed, C, 3, std=0.1)
+    cw = W.normal(seed, 27 * C * C, 4, std=0.05).reshape(27, C, C)
+    cb = W.normal(seed, C, 5, std=0.1)
+    w0, b0 = W.normal(seed, M * C, 6, std=0.2).reshape(M, C), W.normal(seed, M, 7, std=0.1)
+    w2, b2 = W.normal(seed, C * M, 8, std=0.2).reshape(C, M), W.normal(seed, C, 9, std=0.1)
+    sp = lambda c, f, shape=(G, G, G): ref.sparse(c, f, 2, shape)
+
+    # ConvNeXt.
+    conv = ref.subm_conv3d(sp(coords, x), cw, cb)
+    h = ref.linear(ref.layer_norm(conv, 1e-6, g, b), w0, b0).read()[1]
+    r = ref.linear(sp(coords, _silu(h)), w2, b2).read()[1]
+    expect = r + x
+    got = orc.convnext_block(coords, x, M, 1e-6, [g, b, cw, cb, w0, b0, w2, b2])
+    assert np.max(np.abs(got - expect)) <= 1e-6 * np.max(np.abs(expect))
+
+    # Channel-to-spatial residual block with a given subdivision.
+    P = 8 * O_
+    c1w = W.normal(seed, 27 * P * C, 10, std=0.05).reshape(27, P, C)
+    c1b = W.normal(seed, P, 11, std=0.1)
+    c2w = W.normal(seed, 27 * O_ * O_, 12, std=0.1).reshape(27, O_, O_)
+    c2b = W.normal(seed, O_, 13, std=0.1)
+    sub = W.normal(seed, n * 8, 14).reshape(n, 8)
+    sub_t = sp(coords, sub)
+    normed = _silu(ref.layer_norm(sp(coords, x), 1e-6, g, b).read()[1])
+    packed = ref.subm_conv3d(sp(coords, normed), c1w, c1b)
+    oc, hidden = ref.channel_to_spatial(packed, 2, sub_t).read()
+    _, skip = ref.channel_to_spatial(sp(coords, x), 2, sub_t).read()
+    S2 = (2 * G,) * 3
+    hn = _silu(ref.layer_norm(sp(oc, hidden, S2), 1e-6).read()[1])
+    y = ref.subm_conv3d(sp(oc, hn, S2), c2w, c2b).read()[1]
+    expect = y + np.repeat(skip, O_ // (C // 8), axis=1)
+    got_c, got = orc.resblock_c2s(coords, x, O_, 1e-6, [g, b, c1w, c1b, c2w, c2b],
+                                  subdivision=sub)
+    np.testing.assert_array_equal(got_c, oc)
+    assert np.max(np.abs(got - expect)) <= 1e-6 * np.max(np.abs(expect))
+
+
+def test_decoder_block_closed_forms(orc):
+    """mlp2 = 0 makes the ConvNeXt block the identity; conv2 = 0 leaves the C2S
+    block's output equal to the repeated subdivided input."""
+    seed, C, M, O_ = 52, 16, 32, 8
+    coords = W.shell_coords(12, [[(3.0, 4.5)]], seed)
+    n = coords.shape[0]
+    x = W.normal(seed, n * C, 1).reshape(n, C)
+    ones, zeros = np.ones(C, np.float32), np.zeros(C, np.float32)
+    cw = W.normal(seed, 27 * C * C, 4, std=0.05).reshape(27, C, C)
+    w0 = W.normal(seed, M * C, 6, std=0.2).reshape(M, C)
+    out = orc.convnext_block(coords, x, M, 1e-6, [ones, zeros, cw, zeros, w0, np.zeros(M),
+                                                  np.zeros((C, M)), zeros])
+    np.testing.assert_array_equal(out, x)
+    P = 8 * O_
+    c1w = W.normal(seed, 27 * P * C, 10, std=0.05).reshape(27, P, C)
+    oc, y = orc.resblock_c2s(coords, x, O_, 1e-6, [ones, zeros, c1w, np.zeros(P),
+                                                   np.zeros((27, O_, O_)), np.zeros(O_)])
+    assert oc.shape[0] == 8 * n
+    sc, skip = orc.channel_to_spatial(coords, x, 2)
+    np.testing.assert_array_equal(oc, sc)
+    # repeat_channels repeats each source channel consecutively.
+    expect = np.repeat(skip, O_ // (C // 8), axis=1)
+    np.testing.assert_array_equal(y, expect)
+    assert y[0, 0] == y[0, 1] == skip[0, 0] and y[0, O_ // (C // 8)] == skip[0, 1]
