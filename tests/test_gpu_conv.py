@@ -102,6 +102,44 @@ def test_conv_bf16_unet_full_size_sampled_rows(px):
     np.testing.assert_array_equal(host(yi), host(xb))
 
 
+def plane_spans(idx, n, bm=128):
+    """Per (tile of bm rows, x-plane) span of the input rows the plane's nine
+    offsets read: the bf16 kernel stages runs of at most 256 rows and gathers
+    per offset above that."""
+    spans = []
+    for t in range(0, n, bm):
+        sub = idx[:, t:t + bm]
+        for kd in range(3):
+            v = sub[9 * kd:9 * kd + 9].ravel()
+            v = v[v != n]
+            spans.append(int(v.max() - v.min() + 1) if v.size else 0)
+    return np.array(spans)
+
+
+@pytest.mark.parametrize("masks", [True, False])
+def test_conv_bf16_staged_and_gathered_planes(px, orc, masks):
+    """A 3 x 72 x 72 slab plus a shell in a second batch: y lines of 72 rows
+    push some planes past the 256-row staging limit (gathered per offset),
+    the rest are staged; both must agree with the oracle."""
+    slab = np.array([(0, x, y, z) for x in range(3) for y in range(72) for z in range(72)],
+                    np.int32)
+    shell = W.shell_coords(24, [[(6.0, 10.0)]], 45)
+    shell[:, 0] = 1
+    coords = np.concatenate([slab, shell])
+    n = coords.shape[0]
+    spans = plane_spans(orc.neighbor_map(coords), n)
+    assert (spans > 256).any() and ((spans > 0) & (spans <= 256)).any()
+    cin, cout = 64, 128
+    x = W.bf16_round(W.normal(45, n * cin, 1).reshape(n, cin))
+    w = W.bf16_round(W.normal(45, 27 * cout * cin, 2, std=float(np.sqrt(2 / (27 * cin))))
+                     .reshape(27, cout, cin))
+    b = W.normal(45, cout, 3, std=0.1)
+    print(f"[conv bf16 slab] n={n} masks={masks}", flush=True)
+    nbr, mk = px.neighbor_map(ti32(coords))
+    y = px.subm_conv3d(tbf(x), tbf(w), t32(b), nbr, mk if masks else None)
+    assert_bf16(host(y), orc.subm_conv3d(coords, x, w, b), what="bf16 conv slab")
+
+
 def test_conv_masks_optional(px, orc):
     coords = W.shell_coords(16, [[(4.0, 7.0)]], 43)
     n = coords.shape[0]
