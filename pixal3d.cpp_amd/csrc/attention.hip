@@ -364,6 +364,7 @@ __device__ __forceinline__ float lane_pair_sum(float v) {
 // cores and the VALU work at the same time.  K/V tiles stream HBM -> LDS with
 // global_load_lds through a ring of 4 stages (tiles j-1 .. j+2 live).
 constexpr int kAttnStages = 4;
+constexpr int kKeyRowsLds = 1024;  // longest permuted segment whose key rows are staged in LDS
 
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
@@ -371,6 +372,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     constexpr int kTileBytes = kKeys * 128;           // one 64-key x 64-dim bf16 tile
     constexpr int kInstr = 2 * (kKeys / 8) / NW;      // K + V wave instructions per tile
     __shared__ __align__(16) char lds[kAttnStages][2 * kTileBytes];
+    __shared__ int32_t key_rows[kKeyRowsLds];  // row_map of the segment's keys
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -405,26 +407,63 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 
     const int ntiles = static_cast<int>((k_end - k_begin + kKeys - 1) / kKeys);
     const int lrow = lane >> 3, lslot = lane & 7;
+    // Permuted keys (windows): stage the segment's row indices in LDS, so the
+    // tile loads below need no global index load (whose wait would also wait
+    // for the K/V prefetches in flight).  Longer segments read row_map
+    // directly.
+    const int64_t klen_all = k_end - k_begin;
+    const bool keys_in_lds = a.row_map != nullptr && klen_all <= kKeyRowsLds;
+    if (keys_in_lds) {
+        for (int64_t i = tid; i < klen_all; i += NW * 64) key_rows[i] = a.row_map[k_begin + i];
+        __syncthreads();
+    }
+    const uint32_t lds_base = lds_offset(&lds[0][0]);
+    // The zero source of masked rows, kept in registers across the loop.
+    uint64_t zero_addr = reinterpret_cast<uint64_t>(&g_attn_zero[0]);
+    asm volatile("" : "+s"(zero_addr));
+    // Per-lane source pointers of this wave's kInstr load units for tile 0;
+    // a full tile of unpermuted keys advances them by 64 rows.
+    const uint16_t * src0[kInstr];
+    int64_t src_step[kInstr];
+#pragma unroll
+    for (int j = 0; j < kInstr; ++j) {
+        const int unit = wave * kInstr + j;           // 0..15: 8 K blocks then 8 V blocks
+        const bool is_v = unit >= kKeys / 8;
+        const int row = (unit % (kKeys / 8)) * 8 + lrow;
+        const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
+        const int64_t ld = is_v ? a.ldv : a.ldk;
+        src0[j] = (is_v ? vp : kp) + (k_begin + row) * ld + head * 64 + piece * 8;
+        src_step[j] = kKeys * ld;
+    }
     auto issue = [&](int tile) __attribute__((always_inline)) {
-        char * base = lds[tile % kAttnStages];
+        const uint32_t base = lds_base + (tile % kAttnStages) * (2 * kTileBytes);
         const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeys;
+        if (a.row_map == nullptr && kt0 + kKeys <= k_end) {
+#pragma unroll
+            for (int j = 0; j < kInstr; ++j) {
+                const int unit = wave * kInstr + j;
+                const bool is_v = unit >= kKeys / 8;
+                const int row0 = (unit % (kKeys / 8)) * 8;
+                lds_dma16(src0[j] + tile * src_step[j], base + (is_v ? kTileBytes : 0) + row0 * 128);
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < kInstr; ++j) {
-            const int unit = wave * kInstr + j;           // 0..15: 8 K blocks then 8 V blocks
+            const int unit = wave * kInstr + j;
             const bool is_v = unit >= kKeys / 8;
             const int row0 = (unit % (kKeys / 8)) * 8;
             const int row = row0 + lrow;
             const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
             const int64_t kidx = kt0 + row;
-            const void * g = static_cast<const void *>(g_attn_zero);
+            const void * g = reinterpret_cast<const void *>(zero_addr);
             if (kidx < k_end) {
-                const int64_t prow = a.row_map ? a.row_map[kidx] : kidx;
+                const int64_t prow = keys_in_lds ? key_rows[kidx - k_begin]
+                                                 : (a.row_map ? a.row_map[kidx] : kidx);
                 g = is_v ? static_cast<const void *>(vp + prow * a.ldv + head * 64 + piece * 8)
                          : static_cast<const void *>(kp + prow * a.ldk + head * 64 + piece * 8);
             }
-            __builtin_amdgcn_global_load_lds(
-                g, (__attribute__((address_space(3))) void *)(base + (is_v ? kTileBytes : 0) + row0 * 128),
-                16, 0, 0);
+            lds_dma16(g, base + (is_v ? kTileBytes : 0) + row0 * 128);
         }
     };
 
@@ -532,7 +571,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     };
     auto softmax_exp = [&](const f32x16 (&s)[2], bf16x8 (&pb)[2][2]) {
         const float mc = m_run * c;
-        float lsum = l_part;
+        float lsum = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
@@ -550,7 +589,29 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
                 pb[kt][u] = p8;
             }
         }
-        l_part = lsum;
+        return lsum;  // this lane's share of the tile's row sum
+    };
+    // Full tiles after the first skip the max: m_run (the first tile's max,
+    // raised only by the lazy rescale of a partial last tile) stays in place,
+    // and a tile whose scores exceed it by enough to push a row sum past
+    // kTileSumLimit (or to inf) is redone with its true max.  p then stays
+    // below 2^40, far from fp32 and bf16 overflow in O and l.
+    constexpr float kTileSumLimit = 1099511627776.0f;  // 2^40
+    auto softmax_exp_checked = [&](f32x16 (&s)[2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+        float ts = softmax_exp(s, pb);
+        if (__builtin_expect(__ballot(!(ts <= kTileSumLimit)) != 0, 0)) {
+            const float mx = softmax_max(s, kKeys);
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
+            m_run = m_new;
+            l_part *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+            ts = softmax_exp(s, pb);
+        }
+        l_part += ts;
     };
 
     // One steady-state step for tile j (full, not the last): PV(j-1) with the
@@ -559,13 +620,12 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         // Tile j+1 has landed (it is the newest load); the barrier also frees
         // the stage of tile j-2 for tile j+2.
         wait_vmcnt0();
-        __syncthreads();
+        barrier_no_fence();
         if (j + 2 < ntiles) issue(j + 2);
         if (j > 0) pv(j - 1, p);
-        const float mx = softmax_max(s_cur, kKeys);
-        rescale(mx);
+        if (j == 0) rescale(softmax_max(s_cur, kKeys));
         qk(j + 1, s_next);
-        softmax_exp(s_cur, p);
+        softmax_exp_checked(s_cur, p);
     };
 
     const int64_t klen = k_end - k_begin;
@@ -574,7 +634,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         if (ntiles > 1) issue(1);
         if (ntiles > 1) wait_vmcnt(kInstr);
         else wait_vmcnt0();
-        __syncthreads();
+        barrier_no_fence();
         f32x16 s_a[2], s_b[2];
         bf16x8 p_prev[2][2];
         qk(0, s_a);
@@ -595,7 +655,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         if (last > 0) pv(last - 1, p_prev);
         const float mx = softmax_max(s_a, static_cast<int>(klen - static_cast<int64_t>(last) * kKeys));
         rescale(mx);
-        softmax_exp(s_a, p_prev);
+        l_part += softmax_exp(s_a, p_prev);
         pv(last, p_prev);
     }
 

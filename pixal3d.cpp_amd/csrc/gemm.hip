@@ -490,18 +490,14 @@ gather_gemm_lds_kernel(GemmArgs a) {
             const void * g = (src[j] >= 0 && col < a.cin)
                                  ? static_cast<const void *>(x + static_cast<int64_t>(src[j]) * a.ldx + col)
                                  : zero;
-            __builtin_amdgcn_global_load_lds(
-                g, (__attribute__((address_space(3))) void *)(base + (wave * AI + j) * 8 * kChunkBytes),
-                16, 0, 0);
+            lds_dma16(g, lds_offset(base + (wave * AI + j) * 8 * kChunkBytes));
         }
         const int64_t kbase = static_cast<int64_t>(k) * a.cout * a.cin + chunk * kChunk;
 #pragma unroll
         for (int j = 0; j < BI; ++j) {
             const int col = chunk * kChunk + b_piece[j] * kVec;
             const void * g = (b_ok[j] && col < a.cin) ? static_cast<const void *>(w + kbase + b_off[j]) : zero;
-            __builtin_amdgcn_global_load_lds(
-                g, (__attribute__((address_space(3))) void *)(base + (BM + (wave * BI + j) * 8) * kChunkBytes),
-                16, 0, 0);
+            lds_dma16(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
         }
     };
 
@@ -520,7 +516,7 @@ gather_gemm_lds_kernel(GemmArgs a) {
     for (int s = 0; s < stages; ++s) {
         const int after = min(NSTAGE - 2, stages - 1 - s);
         wait_vmcnt(after * kPerStage);
-        __syncthreads();
+        barrier_no_fence();
         if constexpr (!kIssueLate) {
             if (s + NSTAGE - 1 < stages) issue(s + NSTAGE - 1);
         }
@@ -691,11 +687,15 @@ gather_gemm_rega_kernel(GemmArgs a) {
     }
 
     // Issue step s: this lane's 64 A bytes into regs, and the wave's share of
-    // the weight chunk into LDS slot s % DEPTH.
+    // the weight chunk into LDS slot s % DEPTH.  Steps past the end load the
+    // zero chunk: issuing every step keeps the control flow straight, so the
+    // compiler's own waits for the A registers count exactly the groups in
+    // flight instead of draining them all.
     auto issue = [&](int s, uint4 (&areg)[4]) __attribute__((always_inline)) {
-        const int i = s / chunks, chunk = s - i * chunks;
-        const int k = koff[i];
-        const int32_t src = idx_lds[i * BM + my_row];
+        const bool live = s < steps;
+        const int i = live ? s / chunks : 0, chunk = live ? s - i * chunks : 0;
+        const int k = live ? koff[i] : 0;
+        const int32_t src = live ? idx_lds[i * BM + my_row] : -1;
         const int col0 = chunk * kChunk + 32 * h;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -710,7 +710,7 @@ gather_gemm_rega_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < BI; ++j) {
             const int col = chunk * kChunk + b_piece[j] * kVec;
-            const void * g = (b_ok[j] && col < a.cin) ? static_cast<const void *>(w + kbase + b_off[j]) : zero;
+            const void * g = (live && b_ok[j] && col < a.cin) ? static_cast<const void *>(w + kbase + b_off[j]) : zero;
             __builtin_amdgcn_global_load_lds(
                 g, (__attribute__((address_space(3))) void *)(base + (wave * BI + j) * 8 * kChunkBytes),
                 16, 0, 0);
@@ -741,22 +741,18 @@ gather_gemm_rega_kernel(GemmArgs a) {
 
     uint4 ar[DEPTH][4];
 #pragma unroll
-    for (int d = 0; d < DEPTH - 1; ++d)
-        if (d < steps) issue(d, ar[d]);
+    for (int d = 0; d < DEPTH - 1; ++d) issue(d, ar[d]);
 
     for (int s0 = 0; s0 < steps; s0 += DEPTH) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             const int s = s0 + d;
-            if (s < steps) {
-                // Step s's group has landed when at most the groups of
-                // s+1 .. s+DEPTH-2 are still outstanding.
-                const int after = min(DEPTH - 2, steps - 1 - s);
-                wait_vmcnt(after * kGroup);
-                __syncthreads();
-                if (s + DEPTH - 1 < steps) issue(s + DEPTH - 1, ar[(d + DEPTH - 1) % DEPTH]);
-                compute(s, ar[d]);
-            }
+            // Step s's group has landed when only the groups of
+            // s+1 .. s+DEPTH-2 are still outstanding.
+            wait_vmcnt((DEPTH - 2) * kGroup);
+            barrier_no_fence();
+            issue(s + DEPTH - 1, ar[(d + DEPTH - 1) % DEPTH]);
+            if (s < steps) compute(s, ar[d]);
         }
     }
     gemm_epilogue<T, 1, TJ, 32, BN, EPI>(a, reinterpret_cast<const f32x16 (&)[1][TJ]>(acc), p0, n0,

@@ -64,6 +64,41 @@ template <> __device__ __forceinline__ void store_f32<uint16_t>(uint16_t * p, fl
     *p = f32_to_bf16(v);
 }
 
+// ---- LDS DMA pipelines ----------------------------------------------------------
+// LDS byte offset of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_offset(const void * p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+        (const __attribute__((address_space(3))) char *)(p)));
+}
+
+// 16 bytes per lane from global memory into LDS (global_load_lds_dwordx4):
+// lane l writes lds_base + 16 l, lds_base wave-uniform.  Written as inline
+// asm: the compiler then neither counts it nor makes later LDS reads wait for
+// it (it cannot prove that a read of one ring stage misses the stage being
+// filled, and would drain the whole pipeline); the caller waits with
+// s_waitcnt vmcnt and a workgroup barrier before reading the data.
+// No "memory" clobber: the stage it fills was released by a barrier_no_fence
+// (whose clobbers keep earlier LDS reads before it), and the source is never
+// written by the kernels that use it.
+__device__ __forceinline__ void lds_dma16(const void * g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(g), "s"(lds_base)
+                 : "m0");
+}
+
+// Workgroup barrier without __syncthreads' release/acquire fences (which wait
+// for every outstanding global load, prefetches included).  It waits for the
+// wave's own LDS accesses (lgkmcnt 0), so no wave refills a stage another is
+// still reading; callers wait for their LDS DMA (vmcnt) first.  The empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void barrier_no_fence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt unbounded
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ---- math helpers ------------------------------------------------------------
 __device__ __forceinline__ float gelu_tanh_f(float v) {
     const float k = 0.7978845608028654f;

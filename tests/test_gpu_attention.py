@@ -74,6 +74,28 @@ def test_attention_bf16_random(px, orc):
     assert_bf16(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.125)), what="bf16 attn")
 
 
+@pytest.mark.parametrize("jump", [4.0, 40.0, 400.0])
+def test_attention_bf16_late_score_jump(px, orc, jump):
+    """Keys after the first 64 score far above the first tile's maximum
+    (scores scaled by `jump`): the kernel keeps the first tile's max as its
+    reference and must renormalize when a later tile would overflow."""
+    lens = (700, 260)
+    heads, hd = 2, 64
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    n, C = int(cu[-1]), heads * hd
+    q = W.bf16_round(W.normal(64, n * C, 1).reshape(n, C))
+    k = W.normal(64, n * C, 2).reshape(n, C)
+    for b in range(len(lens)):
+        k[cu[b] + 64:cu[b + 1]] *= jump
+    k = W.bf16_round(k)
+    v = W.bf16_round(W.normal(64, n * C, 3).reshape(n, C))
+    print(f"[attn bf16 jump] jump={jump}", flush=True)
+    o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, 0.125))
+    assert np.isfinite(o).all()
+    assert_bf16(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.125)),
+                what=f"bf16 attn jump {jump}")
+
+
 def test_attention_bf16_full_size_sampled_rows(px, orc):
     """Config-3 attention at full size (12,288 + 20,480 tokens, 16 x 64),
     checked exactly on sampled query rows by the oracle."""
