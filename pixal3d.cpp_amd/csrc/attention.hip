@@ -616,15 +616,25 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 
     // One steady-state step for tile j (full, not the last): PV(j-1) with the
     // max of S_j, then the rescale, then QK(j+1) with the exponentials of S_j.
+    // One steady-state step for full tile j > 0: PV(j-1), QK(j+1), then tile
+    // j's exponentials (overflow-checked) while those MFMAs run.  The first
+    // tile (step_first) takes its max to set m_run.
     auto step = [&](int j, f32x16 (&s_cur)[2], f32x16 (&s_next)[2], bf16x8 (&p)[2][2]) {
         // Tile j+1 has landed (it is the newest load); the barrier also frees
         // the stage of tile j-2 for tile j+2.
         wait_vmcnt0();
         barrier_no_fence();
         if (j + 2 < ntiles) issue(j + 2);
-        if (j > 0) pv(j - 1, p);
-        if (j == 0) rescale(softmax_max(s_cur, kKeys));
+        pv(j - 1, p);
         qk(j + 1, s_next);
+        softmax_exp_checked(s_cur, p);
+    };
+    auto step_first = [&](f32x16 (&s_cur)[2], f32x16 (&s_next)[2], bf16x8 (&p)[2][2]) {
+        wait_vmcnt0();
+        barrier_no_fence();
+        if (2 < ntiles) issue(2);
+        rescale(softmax_max(s_cur, kKeys));
+        qk(1, s_next);
         softmax_exp_checked(s_cur, p);
     };
 
@@ -639,8 +649,14 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         bf16x8 p_prev[2][2];
         qk(0, s_a);
         // Steady state over tiles 0 .. ntiles-2 (only the last can be
-        // partial), unrolled by two so the S registers alternate roles.
-        int j = 0;
+        // partial): the first tile peeled, the rest unrolled by two so the S
+        // registers alternate roles.
+        int j = 1;
+        if (ntiles > 1) {
+            step_first(s_a, s_b, p_prev);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) s_a[kt] = s_b[kt];
+        }
         for (; j + 2 < ntiles; j += 2) {
             step(j, s_a, s_b, p_prev);
             step(j + 1, s_b, s_a, p_prev);
