@@ -292,10 +292,14 @@ def cpu_baseline_conv():
 # ---------------------------------------------------------------------------
 # The other configurations (parity cases; timed here for profiling).
 
-def timed_steps(args, torch, step):
+def timed_steps(args, torch, step, timer=None):
+    """Mean wall time of one step over args.steps after args.warmup untimed
+    steps; the per-kernel timer restarts after the warmup."""
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    if timer is not None:
+        timer.reset()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
@@ -323,7 +327,7 @@ def conv_fp32_64(args, torch, px, W):
 
     nbr, masks = px.neighbor_map(coords)
     pairs = int(np.unpackbits(masks.cpu().numpy().view(np.uint8)).sum())
-    dt = timed_steps(args, torch, step)
+    dt = timed_steps(args, torch, step, timer)
     macs = pairs * 64 * 64
     conv_ms = timer.mean_ms("conv")
     achieved = 2.0 * macs / (conv_ms * 1e-3) / 1e12
@@ -359,7 +363,7 @@ def attn_block(args, torch, px, W):
         timer.run("attention", lambda: px.varlen_attention(q, k, v, cu, cu, H, D, D ** -0.5, out=o))
         timer.run("out", lambda: px.linear(o, w_out, b_out, out=y))
 
-    dt = timed_steps(args, torch, step)
+    dt = timed_steps(args, torch, step, timer)
     lens = (wl["cu_seqlens"][1:] - wl["cu_seqlens"][:-1]).tolist()
     f_attn = 4.0 * sum(L * L for L in lens) * D * H
     flops = 2.0 * n * C * 3 * C + f_attn + 2.0 * n * C * C
@@ -410,7 +414,7 @@ def swin_64(args, torch, px, W):
         timer.run("up_conv", lambda: px.subm_conv3d(h, w_up, b_up, nbr, masks, out=packed))
         timer.run("c2s", lambda: px.channel_to_spatial(coords, packed))
 
-    dt = timed_steps(args, torch, step)
+    dt = timed_steps(args, torch, step, timer)
     nbr, masks = px.neighbor_map(coords)
     import numpy as np
     pairs = int(np.unpackbits(masks.cpu().numpy().view(np.uint8)).sum())

@@ -759,6 +759,177 @@ gather_gemm_rega_kernel(GemmArgs a) {
                                          wave, 0, h, r);
 }
 
+// ---------------------------------------------------------------------------
+// fp32 split-K gather GEMM for small and medium problems (config-1 sized
+// convolutions, fp32 linears).  A workgroup owns 32 output rows x 64 output
+// channels; its (offset, 32-channel chunk) steps are dealt round-robin to
+// the 4 waves, so even a few hundred tiles keep every CU busy.  Each wave
+// loads its operands straight into VGPRs -- lane (h, r) takes the 64
+// contiguous bytes k = 16h .. 16h+15 of A row r and of weight row r, the
+// same K permutation on both sides of v_mfma_f32_32x32x2_f32 -- with the
+// next step's loads in flight during the current step's 32 MFMAs, and no
+// barrier until the end, where waves 1-3 hand their partial sums to wave 0
+// through LDS (a fixed summation order: deterministic).
+
+template <int EPI>
+__global__ void __launch_bounds__(256)
+split_gemm_f32_kernel(GemmArgs a) {
+    constexpr int BM = 32, BN = 64, NW = 4;
+    __shared__ float red[NW - 1][2][16][64];
+    __shared__ int32_t idx_lds[32 * BM];
+    __shared__ uint32_t tile_mask;
+    __shared__ int koff[32];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, r = lane & 31;
+
+    const int tiles_n = (a.cout + BN - 1) / BN;
+    const int logical = remap_xcd(blockIdx.x, gridDim.x);
+    const int64_t p0 = static_cast<int64_t>(logical / tiles_n) * BM;
+    const int n0 = (logical % tiles_n) * BN;
+    const float * __restrict__ x = static_cast<const float *>(a.x);
+    const float * __restrict__ w = static_cast<const float *>(a.w);
+
+    if (tid == 0) tile_mask = 0;
+    __syncthreads();
+    if (tid < BM && p0 + tid < a.m) {
+        const int64_t p = p0 + tid;
+        uint32_t local = 0;
+        if (a.masks) {
+            local = a.masks[p];
+        } else if (a.rowmap) {
+            for (int k = 0; k < a.noff; ++k) {
+                const int32_t src = a.rowmap[k * a.ld_map + p];
+                if (src >= 0 && src < a.rows_in) local |= 1u << k;
+            }
+        } else {
+            local = 1u;
+        }
+        if (local) atomicOr(&tile_mask, local);
+    }
+    __syncthreads();
+    const uint32_t present = tile_mask & (a.noff >= 32 ? ~0u : ((1u << a.noff) - 1u));
+    const int kcount = __popc(present);
+    if (tid == 0) {
+        uint32_t m = present;
+        for (int i = 0; i < kcount; ++i) {
+            koff[i] = __ffs(m) - 1;
+            m &= m - 1;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < kcount * BM; e += NW * 64) {
+        const int i = e / BM, row = e % BM;
+        const int64_t p = p0 + row;
+        int32_t src = -1;
+        if (p < a.m) {
+            const int64_t s = a.rowmap ? static_cast<int64_t>(a.rowmap[koff[i] * a.ld_map + p]) : p;
+            src = (s >= 0 && s < a.rows_in) ? static_cast<int32_t>(s) : -1;
+        }
+        idx_lds[e] = src;
+    }
+    __syncthreads();
+
+    const int chunks = (a.cin + 31) / 32;
+    const int steps = kcount * chunks;
+    const int my_steps = steps > wave ? (steps - wave + NW - 1) / NW : 0;
+    const float4 * zero4 = reinterpret_cast<const float4 *>(g_zero_chunk);
+
+    // Operands of one step: A (16 floats of row r) and B (16 floats of each
+    // of the two 32-column weight tiles).  Steps past the end load zeros, so
+    // every iteration issues the same loads and the compiler's waits count
+    // exactly one step in flight.
+    struct Ops {
+        float4 av[4];
+        float4 bv[2][4];
+    };
+    auto load = [&](int t, Ops & o) __attribute__((always_inline)) {
+        const int s = wave + t * NW;
+        const bool live = t < my_steps;
+        const int i = live ? s / chunks : 0, chunk = live ? s - i * chunks : 0;
+        const int k = live ? koff[i] : 0;
+        const int32_t src = live ? idx_lds[i * BM + r] : -1;
+        const int col0 = chunk * 32 + 16 * h;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int col = col0 + 4 * q;
+            o.av[q] = (src >= 0 && col < a.cin)
+                          ? *reinterpret_cast<const float4 *>(x + static_cast<int64_t>(src) * a.ldx + col)
+                          : *zero4;
+        }
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const int c = n0 + ct * 32 + r;
+            const bool ok = live && c < a.cout;
+            const float * wrow = w + (static_cast<int64_t>(k) * a.cout + c) * a.cin;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int col = col0 + 4 * q;
+                o.bv[ct][q] = (ok && col < a.cin) ? *reinterpret_cast<const float4 *>(wrow + col) : *zero4;
+            }
+        }
+    };
+
+    f32x16 acc[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[ct][v] = 0.0f;
+    auto compute = [&](const Ops & o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+                    acc[ct] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.av[q][e], o.bv[ct][q][e],
+                                                                   acc[ct], 0, 0, 0);
+    };
+
+    Ops o0, o1;
+    load(0, o0);
+    for (int t = 0; t < my_steps; t += 2) {
+        load(t + 1, o1);
+        compute(o0);
+        load(t + 2, o0);
+        if (t + 1 < my_steps) compute(o1);
+    }
+
+    if (wave > 0) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) red[wave - 1][ct][v][lane] = acc[ct][v];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int wv = 0; wv < NW - 1; ++wv)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[ct][v] += red[wv][ct][v][lane];
+    f32x16 (&acc2)[1][2] = reinterpret_cast<f32x16 (&)[1][2]>(acc);
+    gemm_epilogue<float, 1, 2, 32, 64, EPI>(a, acc2, p0, n0, 0, 0, h, r);
+}
+
+#ifndef PXS_SPLIT_F32
+#define PXS_SPLIT_F32 1
+#endif
+
+template <int EPI>
+int launch_split_f32(const GemmArgs & args, hipStream_t stream) {
+    const int64_t tiles_m = (args.m + 31) / 32;
+    const int64_t tiles_n = (args.cout + 63) / 64;
+    const int64_t blocks = tiles_m * tiles_n;
+    if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "gather GEMM grid too large");
+    hipLaunchKernelGGL((split_gemm_f32_kernel<EPI>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                       0, stream, args);
+    return check_launch("gather GEMM (fp32 split-K)");
+}
+
 #ifndef PXS_REGA_DEPTH
 #define PXS_REGA_DEPTH 3
 #endif
@@ -872,6 +1043,12 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
                           : launch_rega_tile<4, kEpiAddResidual, PXS_REGA_DEPTH>(args, stream);
         return narrow ? launch_rega_tile<2, kEpiGateResidual, PXS_REGA_DEPTH>(args, stream)
                       : launch_rega_tile<4, kEpiGateResidual, PXS_REGA_DEPTH>(args, stream);
+    }
+    if (dtype == PXS_F32 && args.vec_ok && PXS_SPLIT_F32 && args.m > 0 && args.cout > 0 &&
+        args.noff <= 32 && (args.ldx % 4 == 0)) {
+        if (epi == kEpiStore) return launch_split_f32<kEpiStore>(args, stream);
+        if (epi == kEpiAddResidual) return launch_split_f32<kEpiAddResidual>(args, stream);
+        return launch_split_f32<kEpiGateResidual>(args, stream);
     }
     if (dtype == PXS_BF16) {
         if (epi == kEpiStore) return dispatch<uint16_t, kEpiStore>(args, stream);

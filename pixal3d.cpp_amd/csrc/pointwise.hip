@@ -127,9 +127,52 @@ __global__ void head_norm_rope_kernel(const T * __restrict__ x, int64_t ld_x, in
     }
 }
 
-// Fast path of the QKV prologue for head_dim == 64: one wavefront per row,
-// lane = dimension.  q/k: RMS norm (wave reduction) then RoPE (pair partner
-// via a lane shuffle); v copied.
+// Fast path of the QKV prologue for head_dim == 64: one wavefront per row;
+// each lane owns 8 consecutive dimensions (one 16-byte bf16 load, two for
+// fp32), so 8 lanes hold a head and a wave covers 8 heads per pass.  The RMS
+// norm reduces over the head's 8 lanes; RoPE pairs (2i, 2i+1) sit inside a
+// lane, and the lane's 4 pair phases depend only on the row, so their
+// sin/cos are computed once per row for every head of q and k.
+template <typename T> struct Vec8;
+template <> struct Vec8<uint16_t> {
+    static __device__ __forceinline__ void load(const uint16_t * p, float (&v)[8]) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+    }
+    static __device__ __forceinline__ void store(uint16_t * p, const float (&v)[8]) {
+        uint4 u;
+        u.x = pack_bf16x2(v[0], v[1]);
+        u.y = pack_bf16x2(v[2], v[3]);
+        u.z = pack_bf16x2(v[4], v[5]);
+        u.w = pack_bf16x2(v[6], v[7]);
+        *reinterpret_cast<uint4 *>(p) = u;
+    }
+    static __device__ __forceinline__ void copy(const uint16_t * src, uint16_t * dst) {
+        *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
+    }
+};
+template <> struct Vec8<float> {
+    static __device__ __forceinline__ void load(const float * p, float (&v)[8]) {
+        const float4 a = *reinterpret_cast<const float4 *>(p);
+        const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    static __device__ __forceinline__ void store(float * p, const float (&v)[8]) {
+        *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4 *>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    static __device__ __forceinline__ void copy(const float * src, float * dst) {
+        *reinterpret_cast<float4 *>(dst) = *reinterpret_cast<const float4 *>(src);
+        *reinterpret_cast<float4 *>(dst + 4) = *reinterpret_cast<const float4 *>(src + 4);
+    }
+};
+
 template <typename T>
 __global__ void __launch_bounds__(64 * kRowsPerBlock)
 qkv_prepare64_kernel(const T * __restrict__ qkv, int64_t rows, int heads,
@@ -141,36 +184,55 @@ qkv_prepare64_kernel(const T * __restrict__ qkv, int64_t rows, int heads,
     if (row >= rows) return;
     const int C = heads * 64;
     const T * src = qkv + row * 3 * C;
-    float phase = 0.0f;
+    const int sub = lane & 7;       // 8-dim slice of the head
+    const int hl = lane >> 3;       // head within the pass
+    float cs[4] = {1.0f, 1.0f, 1.0f, 1.0f}, sn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (coords) {
-        const int p = lane >> 1;
-        if (p < 3 * rope.fdim) {
-            const int axis = coords[row * 4 + 1 + p / rope.fdim];
-            phase = static_cast<float>(axis) * rope.freq[p % rope.fdim];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int p = sub * 4 + i;
+            if (p < 3 * rope.fdim) {
+                const float phase = static_cast<float>(coords[row * 4 + 1 + p / rope.fdim]) *
+                                    rope.freq[p % rope.fdim];
+                cs[i] = cosf(phase);
+                sn[i] = sinf(phase);
+            }
         }
     }
-    const float cs = cosf(phase), sn = sinf(phase);
-    const bool even = (lane & 1) == 0;
     for (int part = 0; part < 2; ++part) {
         const float * gamma = part == 0 ? q_gamma : k_gamma;
         T * dst = (part == 0 ? q : k) + row * C;
-        for (int h = 0; h < heads; ++h) {
-            float val = load_f32(src + part * C + h * 64 + lane);
+        for (int hb = 0; hb < heads; hb += 8) {
+            const int h = hb + hl;
+            // Heads past the end idle their lanes but still join the shuffles.
+            const bool on = h < heads;
+            const int d0 = (on ? h : 0) * 64 + sub * 8;
+            float val[8];
+            Vec8<T>::load(src + part * C + d0, val);
             if (gamma) {
-                const float sq = wave_sum(val * val);
+                float sq = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sq += val[i] * val[i];
+                sq += __shfl_xor(sq, 1, 64);
+                sq += __shfl_xor(sq, 2, 64);
+                sq += __shfl_xor(sq, 4, 64);
                 const float inv = 1.0f / fmaxf(sqrtf(sq), 1e-12f);
-                val = val * inv * 8.0f * gamma[h * 64 + lane];  // sqrt(64) = 8
+#pragma unroll
+                for (int i = 0; i < 8; ++i) val[i] = val[i] * inv * 8.0f * gamma[d0 + i];  // sqrt(64) = 8
             }
             if (coords) {
-                const float other = __shfl_xor(val, 1, 64);
-                // even lane: e*cos - o*sin; odd lane: e*sin + o*cos
-                val = even ? (val * cs - other * sn) : (other * sn + val * cs);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = val[2 * i], o = val[2 * i + 1];
+                    val[2 * i] = e * cs[i] - o * sn[i];
+                    val[2 * i + 1] = e * sn[i] + o * cs[i];
+                }
             }
-            store_f32(dst + h * 64 + lane, val);
+            if (on) Vec8<T>::store(dst + d0, val);
         }
     }
     T * vd = v + row * C;
-    for (int c = lane; c < C; c += 64) vd[c] = src[2 * C + c];
+    for (int c = lane * 8; c < C; c += 512) Vec8<T>::copy(src + 2 * C + c, vd + c);
 }
 
 template <typename T>
@@ -387,7 +449,11 @@ int pxs_qkv_prepare(int dtype, const void * qkv, int64_t rows, int heads, int he
         t = make_rope_table(head_dim, freq_min, freq_base);
     }
     const int C = heads * head_dim;
-    if (head_dim == 64) {
+    const bool aligned = (reinterpret_cast<uintptr_t>(qkv) & 15u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(q) & 15u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(k) & 15u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(v) & 15u) == 0;
+    if (head_dim == 64 && aligned) {
         if (dtype == PXS_F32) {
             hipLaunchKernelGGL(qkv_prepare64_kernel<float>, dim3(grid_for(rows, kRowsPerBlock)),
                                dim3(64 * kRowsPerBlock), 0, s, static_cast<const float *>(qkv),

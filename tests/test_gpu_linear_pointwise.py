@@ -128,9 +128,9 @@ def test_rms_and_rope(px, orc, heads, hd):
                 what="rope")
 
 
-@pytest.mark.parametrize("dtype,hd", [("f32", 64), ("bf16", 64), ("f32", 16)])
-def test_qkv_prepare(px, orc, dtype, hd):
-    heads = 4
+@pytest.mark.parametrize("dtype,hd,heads", [("f32", 64, 4), ("bf16", 64, 4), ("f32", 16, 4),
+                                            ("bf16", 64, 12), ("f32", 64, 16)])
+def test_qkv_prepare(px, orc, dtype, hd, heads):
     C = heads * hd
     coords = W.shell_coords(64, [[(16.0, 30.0)]], 58)[::30].copy()
     n = coords.shape[0]
