@@ -314,6 +314,9 @@ __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent ro
 // matter most.  128x128 tiles in two stages (64 KiB + indices, two
 // workgroups per CU) with 8 waves of 64x32 each beat 4 waves of 64x64,
 // 256-row tiles and 3-4 stage pipelines (which fit only one workgroup per CU).
+// Loading gathered rows straight into VGPRs (64 bytes per lane, weights alone
+// through LDS) lost 15-20% in the U-Net stage: its 32-byte row pieces per
+// instruction coalesce worse than these 8 full 128-byte row chunks.
 #ifndef PXS_GEMM_STAGES
 #define PXS_GEMM_STAGES 2
 #endif
@@ -581,185 +584,6 @@ gather_gemm_lds_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Register-A gather GEMM (bf16).  Each wave owns 32 output rows x BN output
-// channels (BN / 32 accumulators) and loads its own gathered A rows straight
-// into VGPRs: lane (h, r) fetches the 64 contiguous bytes of row r that its
-// four K-steps consume (k = 32h .. 32h+31 of the 64-channel chunk, the same K
-// permutation as the weight fragments).  Only the weight chunk (shared by
-// every wave of the workgroup) goes through an LDS ring.  A and B loads run
-// DEPTH steps ahead, so DEPTH - 1 steps of gathered rows are in flight per
-// wave without spending LDS on them.  Measured on MI355X against the LDS-A
-// kernel below: SubMConv3d 256->256 at 64^3 180 -> 151 us, 128->128 at 128^3
-// and linear 1024->3072 unchanged (results bit-identical: same K order);
-// DEPTH 3 and 4 tie, DEPTH 5 (one workgroup per CU) is 35% slower.
-
-template <int TJ, int DEPTH>
-constexpr int lds_rega_bytes(int noff) {
-    return DEPTH * 32 * TJ * kChunkBytes + noff * 128 * 4;
-}
-
-template <int TJ, int EPI, int DEPTH>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-gather_gemm_rega_kernel(GemmArgs a) {
-    using T = uint16_t;
-    constexpr int NW = 4, BM = 32 * NW, BN = 32 * TJ;
-    constexpr int kVec = 8, kChunk = 64;
-    constexpr int BI = BN / (8 * NW);       // weight rows: 8 per wave instruction
-    constexpr int kGroup = 4 + BI;          // VMEM instructions per wave per step
-    static_assert(BI * 8 * NW == BN, "weight rows must split over the waves");
-
-    extern __shared__ __align__(16) char smem[];
-    char * b_lds = smem;                                                     // DEPTH x [BN][128 B]
-    int32_t * idx_lds = reinterpret_cast<int32_t *>(smem + DEPTH * BN * kChunkBytes);  // [noff][BM]
-    __shared__ uint32_t tile_mask;
-    __shared__ int koff[32];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane >> 5, r = lane & 31;
-
-    const int tiles_n = (a.cout + BN - 1) / BN;
-    const int logical = remap_xcd(blockIdx.x, gridDim.x);
-    const int64_t p0 = static_cast<int64_t>(logical / tiles_n) * BM;
-    const int n0 = (logical % tiles_n) * BN;
-    const T * __restrict__ x = static_cast<const T *>(a.x);
-    const T * __restrict__ w = static_cast<const T *>(a.w);
-
-    if (tid == 0) tile_mask = 0;
-    __syncthreads();
-    {
-        uint32_t local = 0;
-        for (int row = tid; row < BM; row += NW * 64) {
-            const int64_t p = p0 + row;
-            if (p >= a.m) break;
-            if (a.masks) {
-                local |= a.masks[p];
-            } else if (a.rowmap) {
-                for (int k = 0; k < a.noff; ++k) {
-                    const int32_t src = a.rowmap[k * a.ld_map + p];
-                    if (src >= 0 && src < a.rows_in) local |= 1u << k;
-                }
-            } else {
-                local = 1u;
-            }
-        }
-        if (local) atomicOr(&tile_mask, local);
-    }
-    __syncthreads();
-    const uint32_t present = tile_mask & (a.noff >= 32 ? ~0u : ((1u << a.noff) - 1u));
-    const int kcount = __popc(present);
-    if (tid == 0) {
-        uint32_t m = present;
-        for (int i = 0; i < kcount; ++i) {
-            koff[i] = __ffs(m) - 1;
-            m &= m - 1;
-        }
-    }
-    __syncthreads();
-    for (int e = tid; e < kcount * BM; e += NW * 64) {
-        const int i = e / BM, row = e % BM;
-        const int64_t p = p0 + row;
-        int32_t src = -1;
-        if (p < a.m) {
-            const int64_t s = a.rowmap ? static_cast<int64_t>(a.rowmap[koff[i] * a.ld_map + p]) : p;
-            src = (s >= 0 && s < a.rows_in) ? static_cast<int32_t>(s) : -1;
-        }
-        idx_lds[e] = src;
-    }
-    __syncthreads();
-
-    const int chunks = (a.cin + kChunk - 1) / kChunk;
-    const int steps = kcount * chunks;
-    const int lrow = lane >> 3, lslot = lane & 7;
-    const void * zero = static_cast<const void *>(g_zero_chunk);
-    const int my_row = wave * 32 + r;
-
-    int b_piece[BI];
-    bool b_ok[BI];
-    int64_t b_off[BI];
-#pragma unroll
-    for (int j = 0; j < BI; ++j) {
-        const int row = (wave * BI + j) * 8 + lrow;
-        b_piece[j] = lslot ^ swz(row);
-        b_ok[j] = n0 + row < a.cout;
-        b_off[j] = static_cast<int64_t>(n0 + row) * a.cin + b_piece[j] * kVec;
-    }
-
-    // Issue step s: this lane's 64 A bytes into regs, and the wave's share of
-    // the weight chunk into LDS slot s % DEPTH.  Steps past the end load the
-    // zero chunk: issuing every step keeps the control flow straight, so the
-    // compiler's own waits for the A registers count exactly the groups in
-    // flight instead of draining them all.
-    auto issue = [&](int s, uint4 (&areg)[4]) __attribute__((always_inline)) {
-        const bool live = s < steps;
-        const int i = live ? s / chunks : 0, chunk = live ? s - i * chunks : 0;
-        const int k = live ? koff[i] : 0;
-        const int32_t src = live ? idx_lds[i * BM + my_row] : -1;
-        const int col0 = chunk * kChunk + 32 * h;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int col = col0 + q * kVec;
-            const uint4 * g = (src >= 0 && col < a.cin)
-                                  ? reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(src) * a.ldx + col)
-                                  : reinterpret_cast<const uint4 *>(zero);
-            areg[q] = *g;
-        }
-        char * base = b_lds + (s % DEPTH) * BN * kChunkBytes;
-        const int64_t kbase = static_cast<int64_t>(k) * a.cout * a.cin + chunk * kChunk;
-#pragma unroll
-        for (int j = 0; j < BI; ++j) {
-            const int col = chunk * kChunk + b_piece[j] * kVec;
-            const void * g = (live && b_ok[j] && col < a.cin) ? static_cast<const void *>(w + kbase + b_off[j]) : zero;
-            __builtin_amdgcn_global_load_lds(
-                g, (__attribute__((address_space(3))) void *)(base + (wave * BI + j) * 8 * kChunkBytes),
-                16, 0, 0);
-        }
-    };
-
-    f32x16 acc[TJ];
-#pragma unroll
-    for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
-
-    auto compute = [&](int s, const uint4 (&areg)[4]) __attribute__((always_inline)) {
-        const char * sb = b_lds + (s % DEPTH) * BN * kChunkBytes;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const bf16x8 af = __builtin_bit_cast(bf16x8, areg[ks]);
-            const int piece = 4 * h + ks;
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const int row = j * 32 + r;
-                const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(
-                    sb + row * kChunkBytes + ((piece ^ swz(row)) << 4));
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bfr, acc[j], 0, 0, 0);
-            }
-        }
-    };
-
-    uint4 ar[DEPTH][4];
-#pragma unroll
-    for (int d = 0; d < DEPTH - 1; ++d) issue(d, ar[d]);
-
-    for (int s0 = 0; s0 < steps; s0 += DEPTH) {
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d) {
-            const int s = s0 + d;
-            // Step s's group has landed when only the groups of
-            // s+1 .. s+DEPTH-2 are still outstanding.
-            wait_vmcnt((DEPTH - 2) * kGroup);
-            barrier_no_fence();
-            issue(s + DEPTH - 1, ar[(d + DEPTH - 1) % DEPTH]);
-            if (s < steps) compute(s, ar[d]);
-        }
-    }
-    gemm_epilogue<T, 1, TJ, 32, BN, EPI>(a, reinterpret_cast<const f32x16 (&)[1][TJ]>(acc), p0, n0,
-                                         wave, 0, h, r);
-}
-
-// ---------------------------------------------------------------------------
 // fp32 split-K gather GEMM for small and medium problems (config-1 sized
 // convolutions, fp32 linears).  A workgroup owns 32 output rows x 64 output
 // channels; its (offset, 32-channel chunk) steps are dealt round-robin to
@@ -930,33 +754,6 @@ int launch_split_f32(const GemmArgs & args, hipStream_t stream) {
     return check_launch("gather GEMM (fp32 split-K)");
 }
 
-#ifndef PXS_REGA_DEPTH
-#define PXS_REGA_DEPTH 3
-#endif
-#ifndef PXS_REGA
-#define PXS_REGA 1
-#endif
-
-template <int TJ, int EPI, int DEPTH>
-int launch_rega_tile(const GemmArgs & args, hipStream_t stream) {
-    const int smem = lds_rega_bytes<TJ, DEPTH>(args.noff);
-    static int configured = 0;
-    if (configured < smem) {
-        hipError_t e = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&gather_gemm_rega_kernel<TJ, EPI, DEPTH>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, lds_rega_bytes<TJ, DEPTH>(32));
-        if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(gather_gemm_rega)");
-        configured = lds_rega_bytes<TJ, DEPTH>(32);
-    }
-    const int64_t tiles_m = (args.m + 127) / 128;
-    const int64_t tiles_n = (args.cout + 32 * TJ - 1) / (32 * TJ);
-    const int64_t blocks = tiles_m * tiles_n;
-    if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "gather GEMM grid too large");
-    hipLaunchKernelGGL((gather_gemm_rega_kernel<TJ, EPI, DEPTH>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(256), smem, stream, args);
-    return check_launch("gather GEMM (register A)");
-}
-
 template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M>
 int launch_lds_tile(const GemmArgs & args, hipStream_t stream) {
     const int smem = lds_gemm_bytes<BM, BN, NSTAGE>(args.noff);
@@ -1032,18 +829,6 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
     const int vec = dtype == PXS_BF16 ? 8 : 4;
     args.vec_ok = (args.cin % vec == 0) && (args.ldx % vec == 0) && aligned16(args.x) &&
                   aligned16(args.w);
-    if (dtype == PXS_BF16 && args.vec_ok && PXS_REGA && args.m > 0 && args.cout > 0 &&
-        args.noff <= 32) {
-        const bool narrow = args.cout <= 64;
-        if (epi == kEpiStore)
-            return narrow ? launch_rega_tile<2, kEpiStore, PXS_REGA_DEPTH>(args, stream)
-                          : launch_rega_tile<4, kEpiStore, PXS_REGA_DEPTH>(args, stream);
-        if (epi == kEpiAddResidual)
-            return narrow ? launch_rega_tile<2, kEpiAddResidual, PXS_REGA_DEPTH>(args, stream)
-                          : launch_rega_tile<4, kEpiAddResidual, PXS_REGA_DEPTH>(args, stream);
-        return narrow ? launch_rega_tile<2, kEpiGateResidual, PXS_REGA_DEPTH>(args, stream)
-                      : launch_rega_tile<4, kEpiGateResidual, PXS_REGA_DEPTH>(args, stream);
-    }
     if (dtype == PXS_F32 && args.vec_ok && PXS_SPLIT_F32 && args.m > 0 && args.cout > 0 &&
         args.noff <= 32 && (args.ldx % 4 == 0)) {
         if (epi == kEpiStore) return launch_split_f32<kEpiStore>(args, stream);
