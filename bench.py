@@ -118,7 +118,7 @@ def unet_stage(args, torch, px, W):
         return torch.empty(max(int(nbytes), 8), dtype=torch.uint8, device=dev)
 
     # Buffers sized once.
-    table1 = ws(lib.pxs_voxel_hash_bytes(n))
+    grid1 = ws(lib.pxs_voxel_grid_bytes(2, 128, 128, 128))
     nbr1 = torch.empty((27, n), dtype=torch.int32, device=dev)
     mask1 = torch.empty(n, dtype=torch.int32, device=dev)
     y_a = torch.empty((n, 128), dtype=torch.bfloat16, device=dev)
@@ -130,7 +130,7 @@ def unet_stage(args, torch, px, W):
     # outside the timed region; every step recomputes the topology itself.
     _, _, m = px.downsample_s2(coords, 2, (128, 128, 128))
     y_b = torch.empty((m, 256), dtype=torch.bfloat16, device=dev)
-    table2 = ws(lib.pxs_voxel_hash_bytes(m))
+    grid2 = ws(lib.pxs_voxel_grid_bytes(2, 64, 64, 64))
     nbr2 = torch.empty((27, m), dtype=torch.int32, device=dev)
     mask2 = torch.empty(m, dtype=torch.int32, device=dev)
     y_c = torch.empty((m, 256), dtype=torch.bfloat16, device=dev)
@@ -142,18 +142,20 @@ def unet_stage(args, torch, px, W):
 
     def step():
         s = S()
-        timer.run("hash_map_128", lambda: (
-            chk(lib.pxs_voxel_hash_build(P(coords), n, P(table1), s), "hash"),
-            chk(lib.pxs_neighbor_map_k3(P(coords), n, P(table1), P(nbr1), P(mask1), s), "map")))
+        timer.run("neighbor_map_128", lambda: (
+            chk(lib.pxs_voxel_grid_build(P(coords), n, 2, 128, 128, 128, P(grid1), s), "grid"),
+            chk(lib.pxs_neighbor_map_k3_grid(P(coords), n, 2, 128, 128, 128, P(grid1), P(nbr1),
+                                             P(mask1), s), "map")))
         timer.run("subm_conv_a", lambda: chk(lib.pxs_subm_conv3d(
             1, P(x), n, 128, P(w_a), P(b_a), 128, P(nbr1), P(mask1), P(y_a), s), "conv a"))
         timer.run("downsample_s2", lambda: chk(lib.pxs_downsample_s2_topology(
             P(coords), n, 2, 128, 128, 128, P(oc), P(child), P(m_dev), P(ds_ws), s), "ds"))
         timer.run("sparse_conv_b", lambda: chk(lib.pxs_sparse_conv3d_s2(
             1, P(y_a), n, 128, P(w_b), P(b_b), 256, P(child), n, m, P(y_b), s), "conv b"))
-        timer.run("hash_map_64", lambda: (
-            chk(lib.pxs_voxel_hash_build(P(oc), m, P(table2), s), "hash2"),
-            chk(lib.pxs_neighbor_map_k3(P(oc), m, P(table2), P(nbr2), P(mask2), s), "map2")))
+        timer.run("neighbor_map_64", lambda: (
+            chk(lib.pxs_voxel_grid_build(P(oc), m, 2, 64, 64, 64, P(grid2), s), "grid2"),
+            chk(lib.pxs_neighbor_map_k3_grid(P(oc), m, 2, 64, 64, 64, P(grid2), P(nbr2), P(mask2),
+                                             s), "map2")))
         timer.run("subm_conv_c", lambda: chk(lib.pxs_subm_conv3d(
             1, P(y_b), m, 256, P(w_c), P(b_c), 256, P(nbr2), P(mask2), P(y_c), s), "conv c"))
 
@@ -175,20 +177,21 @@ def unet_stage(args, torch, px, W):
     ms = dt * 1e3 / args.steps
     total_macs = sum(macs.values())
     value = total_macs / (dt / args.steps) / 1e9
-    kern = {k: timer.mean_ms(k) for k in ("hash_map_128", "subm_conv_a", "downsample_s2",
-                                         "sparse_conv_b", "hash_map_64", "subm_conv_c")}
+    kern = {k: timer.mean_ms(k) for k in ("neighbor_map_128", "subm_conv_a", "downsample_s2",
+                                         "sparse_conv_b", "neighbor_map_64", "subm_conv_c")}
     dom = max(macs, key=lambda k: kern[k])
     achieved = 2.0 * macs[dom] / (kern[dom] * 1e-3) / 1e12
     traffic = measured_traffic(dom)
     per_op = {k: {"ms": round(kern[k], 4),
                   "voxel_gmacs": round(macs[k] / (kern[k] * 1e-3) / 1e9, 1),
                   "tflops": round(2 * macs[k] / (kern[k] * 1e-3) / 1e12, 2)} for k in macs}
-    # Map kernels are HBM-bound: coords in (16 B/row) + 27 int32 out + mask out.
-    map_bytes = n * (16 + 27 * 4 + 4)
-    per_op["hash_map_128"] = {"ms": round(kern["hash_map_128"], 4),
-                              "gbs": round(map_bytes / (kern["hash_map_128"] * 1e-3) / 1e9, 1)}
+    # Map kernels are HBM-bound: the grid fill (4 B per cell), coords in
+    # (16 B/row, read twice) and 27 int32 + a mask out per row.
+    map_bytes = lib.pxs_voxel_grid_bytes(2, 128, 128, 128) + n * (2 * 16 + 27 * 4 + 4)
+    per_op["neighbor_map_128"] = {"ms": round(kern["neighbor_map_128"], 4),
+                              "gbs": round(map_bytes / (kern["neighbor_map_128"] * 1e-3) / 1e9, 1)}
     per_op["downsample_s2"] = {"ms": round(kern["downsample_s2"], 4)}
-    per_op["hash_map_64"] = {"ms": round(kern["hash_map_64"], 4)}
+    per_op["neighbor_map_64"] = {"ms": round(kern["neighbor_map_64"], 4)}
     result = {
         "metric": "SubMConv3d voxel-GMAC/s & sparse-attn TFLOP/s vs roofline, 1 MI355X",
         "value": round(value, 2),
@@ -196,8 +199,8 @@ def unet_stage(args, torch, px, W):
         "ms_per_step": round(ms, 4),
         "dtype": "bf16",
         "config": {"workload": "unet_stage_128: batch 2 on 128^3 (61,056 + 101,207 voxels, "
-                               "3 ellipsoid shells each); hash+map, SubMConv3d 128->128, "
-                               "s2 SparseConv3d 128->256, hash+map at 64^3, SubMConv3d 256->256",
+                               "3 ellipsoid shells each); voxel grid + neighbour map, SubMConv3d 128->128, "
+                               "s2 SparseConv3d 128->256, grid + map at 64^3, SubMConv3d 256->256",
                    "voxels": n, "voxels_64": m, "pairs_a": pa, "pairs_c": pc,
                    "per_op": per_op},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
@@ -322,7 +325,7 @@ def conv_fp32_64(args, torch, px, W):
     timer = Timer(torch)
 
     def step():
-        nbr, masks = timer.run("hash_map", lambda: px.neighbor_map(coords))
+        nbr, masks = timer.run("neighbor_map", lambda: px.neighbor_map_grid(coords, 1, (64, 64, 64)))
         timer.run("conv", lambda: px.subm_conv3d(x, w, b, nbr, masks, out=y))
 
     nbr, masks = px.neighbor_map(coords)
@@ -333,8 +336,8 @@ def conv_fp32_64(args, torch, px, W):
     achieved = 2.0 * macs / (conv_ms * 1e-3) / 1e12
     return {"metric": "SubMConv3d voxel-GMAC/s, fp32 64->64 at 64^3", "value": round(macs / dt / 1e9, 2),
             "unit": "voxel-GMAC/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "f32",
-            "config": {"workload": f"conv_fp32_64: {n} voxels, {pairs} pairs, hash+map+SubMConv3d",
-                       "hash_map_ms": round(timer.mean_ms("hash_map"), 4),
+            "config": {"workload": f"conv_fp32_64: {n} voxels, {pairs} pairs, voxel grid + neighbour map + SubMConv3d",
+                       "neighbor_map_ms": round(timer.mean_ms("neighbor_map"), 4),
                        "conv_ms": round(conv_ms, 4)},
             "roofline": {"bound": "mfma", "kernel": "conv", "achieved": round(achieved, 2),
                          "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
@@ -410,7 +413,7 @@ def swin_64(args, torch, px, W):
             timer.run("window_attention", lambda: px.varlen_attention(
                 q, k, v, cu, cu, H, D, D ** -0.5, row_map=fwd, out=o, nseg=nw))
             timer.run("out", lambda: px.linear(o, w_out, b_out, out=h))
-        nbr, masks = timer.run("hash_map", lambda: px.neighbor_map(coords))
+        nbr, masks = timer.run("neighbor_map", lambda: px.neighbor_map_grid(coords, 1, wl["shape"]))
         timer.run("up_conv", lambda: px.subm_conv3d(h, w_up, b_up, nbr, masks, out=packed))
         timer.run("c2s", lambda: px.channel_to_spatial(coords, packed))
 
@@ -422,7 +425,7 @@ def swin_64(args, torch, px, W):
     f_lin = len(wl["shifts"]) * (2.0 * n * C * 3 * C + 2.0 * n * C * C)
     f_up = 2.0 * pairs * C * 8 * 192
     flops = f_win + f_lin + f_up
-    per_op = {k: round(timer.mean_ms(k), 4) for k in ("qkv", "window_attention", "out", "hash_map",
+    per_op = {k: round(timer.mean_ms(k), 4) for k in ("qkv", "window_attention", "out", "neighbor_map",
                                                       "up_conv", "c2s", "partition_0", "partition_4")}
     up_tf = f_up / (timer.mean_ms("up_conv") * 1e-3) / 1e12
     return {"metric": "shifted-window attention + C2S upsample TFLOP/s, bf16",

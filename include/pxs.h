@@ -84,6 +84,22 @@ int pxs_check_finite(int dtype, const void * x, int64_t rows, int channels, int6
 int pxs_neighbor_map_k3(const int32_t * coords, int64_t n, const void * table, int32_t * nbr,
                         uint32_t * masks, void * stream);
 
+/* Dense voxel grid: one int32 cell per (b, x, y, z) of the extents
+ * [batch_size, sx, sy, sz] (batch_size * sx * sy * sz * 4 bytes; 0 when the
+ * extents are invalid) holding the smallest row with that coordinate.  Rows
+ * outside the extents are left out.  Where the grid fits comfortably in HBM
+ * (17 MB for two 128^3 items) it replaces the hash for neighbour maps: one
+ * load per neighbour and no probe chains. */
+size_t pxs_voxel_grid_bytes(int batch_size, int sx, int sy, int sz);
+int pxs_voxel_grid_build(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                         int sz, void * grid, void * stream);
+
+/* pxs_neighbor_map_k3 over a dense voxel grid of the same coords and
+ * extents: identical nbr and masks. */
+int pxs_neighbor_map_k3_grid(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                             int sz, const void * grid, int32_t * nbr, uint32_t * masks,
+                             void * stream);
+
 /* Compacted per-offset pair lists from a dense map: for each k ascending,
  * (input row, output row) pairs with output rows ascending; offsets28
  * (device int64[28]) bounds the lists.  pair_in/pair_out hold up to 27*n. */

@@ -199,6 +199,64 @@ neighbor_map_kernel(const int4 * __restrict__ coords, int64_t n,
     if (masks && present) atomicOr(masks + p, present);
 }
 
+// ---- dense voxel grid -----------------------------------------------------------
+// An int32 cell per (b, x, y, z) of the extents, holding the smallest row at
+// that coordinate or kGridEmpty.  Building it is a fill and a scatter; a
+// neighbour lookup is one load from a cell next to the row's own (z
+// neighbours are adjacent words, y neighbours sz words away), with no probe
+// chain.  Rows outside the extents are not entered.
+constexpr int32_t kGridEmpty = INT_MAX;
+
+struct GridDims {
+    int b, x, y, z;
+};
+
+__device__ __forceinline__ bool grid_inside(const GridDims & g, int b, int x, int y, int z) {
+    return static_cast<unsigned>(b) < static_cast<unsigned>(g.b) &&
+           static_cast<unsigned>(x) < static_cast<unsigned>(g.x) &&
+           static_cast<unsigned>(y) < static_cast<unsigned>(g.y) &&
+           static_cast<unsigned>(z) < static_cast<unsigned>(g.z);
+}
+
+__device__ __forceinline__ int64_t grid_cell(const GridDims & g, int b, int x, int y, int z) {
+    return ((static_cast<int64_t>(b) * g.x + x) * g.y + y) * g.z + z;
+}
+
+__global__ void grid_scatter_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
+                                    int32_t * __restrict__ grid) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    if (grid_inside(g, c.x, c.y, c.z, c.w)) atomicMin(grid + grid_cell(g, c.x, c.y, c.z, c.w), static_cast<int32_t>(p));
+}
+
+// One thread per row: all 27 lookups in flight at once; nbr[k * n + p] is
+// written with a wavefront's rows contiguous for each k, and the row's mask
+// is stored whole (no atomics, no zero fill).
+__global__ void __launch_bounds__(kThreads)
+neighbor_map_grid_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
+                         const int32_t * __restrict__ grid, int32_t * __restrict__ nbr,
+                         uint32_t * __restrict__ masks) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    int32_t row[27];
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const int x = c.y + k / 9 - 1, y = c.z + (k / 3) % 3 - 1, z = c.w + k % 3 - 1;
+        row[k] = grid_inside(g, c.x, x, y, z) ? grid[grid_cell(g, c.x, x, y, z)] : kGridEmpty;
+    }
+    row[13] = static_cast<int32_t>(p);  // the centre is the row itself
+    uint32_t present = 0;
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const bool hit = row[k] != kGridEmpty;
+        if (hit) present |= 1u << k;
+        nbr[static_cast<int64_t>(k) * n + p] = hit ? row[k] : static_cast<int32_t>(n);
+    }
+    if (masks) masks[p] = present;
+}
+
 // Pair lists: counts per (offset, block of kThreads rows).
 __global__ void __launch_bounds__(kThreads)
 pair_count_kernel(const int32_t * __restrict__ nbr, int64_t n, int32_t * __restrict__ counts,
@@ -580,6 +638,46 @@ int pxs_neighbor_map_k3(const int32_t * coords, int64_t n, const void * table, i
     hipLaunchKernelGGL(neighbor_map_kernel, dim3(grid_for(3 * n, kThreads)), dim3(kThreads), 0, s,
                        reinterpret_cast<const int4 *>(coords), n, h.slots, h.mask, nbr, masks);
     return check_launch("pxs_neighbor_map_k3");
+}
+
+size_t pxs_voxel_grid_bytes(int batch_size, int sx, int sy, int sz) {
+    if (batch_size <= 0 || sx <= 0 || sy <= 0 || sz <= 0) return 0;
+    const double cells = static_cast<double>(batch_size) * sx * sy * sz;
+    if (cells * 4.0 > 9.0e18) return 0;
+    return static_cast<size_t>(batch_size) * sx * sy * sz * sizeof(int32_t);
+}
+
+int pxs_voxel_grid_build(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                         int sz, void * grid, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_voxel_grid_build: bad row count");
+    const size_t bytes = pxs_voxel_grid_bytes(batch_size, sx, sy, sz);
+    PXS_CHECK(bytes > 0, PXS_ERR_ARG, "pxs_voxel_grid_build: invalid extents");
+    PXS_CHECK(grid != nullptr && (n == 0 || coords != nullptr), PXS_ERR_ARG,
+              "pxs_voxel_grid_build: null pointer");
+    hipStream_t s = as_stream(stream);
+    int32_t * cells = static_cast<int32_t *>(grid);
+    if (int rc = fill_i32(cells, static_cast<int64_t>(bytes / sizeof(int32_t)), kGridEmpty, s)) return rc;
+    if (n > 0) {
+        hipLaunchKernelGGL(grid_scatter_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                           reinterpret_cast<const int4 *>(coords), n,
+                           GridDims{batch_size, sx, sy, sz}, cells);
+    }
+    return check_launch("pxs_voxel_grid_build");
+}
+
+int pxs_neighbor_map_k3_grid(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                             int sz, const void * grid, int32_t * nbr, uint32_t * masks,
+                             void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_neighbor_map_k3_grid: bad row count");
+    PXS_CHECK(pxs_voxel_grid_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              "pxs_neighbor_map_k3_grid: invalid extents");
+    if (n == 0) return PXS_OK;
+    PXS_CHECK(coords && grid && nbr, PXS_ERR_ARG, "pxs_neighbor_map_k3_grid: null pointer");
+    hipLaunchKernelGGL(neighbor_map_grid_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+                       as_stream(stream), reinterpret_cast<const int4 *>(coords), n,
+                       GridDims{batch_size, sx, sy, sz}, static_cast<const int32_t *>(grid), nbr,
+                       masks);
+    return check_launch("pxs_neighbor_map_k3_grid");
 }
 
 size_t pxs_neighbor_pairs_workspace_bytes(int64_t n) {

@@ -80,6 +80,9 @@ _SIGS = {
     "pxs_window_partition_workspace_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32, _i32, _i32, _i64]),
     "pxs_window_partition": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                     _vp, _vp]),
+    "pxs_voxel_grid_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32]),
+    "pxs_voxel_grid_build": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "pxs_neighbor_map_k3_grid": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "pxs_convnext_block_workspace_bytes": (C.c_size_t, [_i32, _i64, _i32, _i32, _i32]),
     "pxs_convnext_block": (_i32, [_i32, _vp, _i64, _vp, _i32, _i32, _f, _vp, _vp, _vp, _vp, _vp,
                                   _vp]),
@@ -226,6 +229,27 @@ class Pxs:
                                                  _ptr(masks), self.stream()),
                     "pxs_neighbor_map_k3")
         return nbr, masks
+
+    def grid_build(self, coords, batch_size, shape):
+        nbytes = self.lib.pxs_voxel_grid_bytes(batch_size, *shape)
+        grid = torch.empty(max(nbytes // 4, 1), dtype=torch.int32, device=coords.device)
+        self._check(self.lib.pxs_voxel_grid_build(_ptr(coords), coords.shape[0], batch_size,
+                                                  *shape, _ptr(grid), self.stream()),
+                    "pxs_voxel_grid_build")
+        return grid
+
+    def neighbor_map_grid(self, coords, batch_size, shape, grid=None, want_masks=True):
+        """pxs_voxel_grid_build + pxs_neighbor_map_k3_grid -> (nbr [27, n], masks [n])."""
+        n = coords.shape[0]
+        grid = self.grid_build(coords, batch_size, shape) if grid is None else grid
+        nbr = torch.empty((27, max(n, 1)), dtype=torch.int32, device=coords.device)
+        masks = torch.empty(max(n, 1), dtype=torch.int32, device=coords.device) if want_masks \
+            else None
+        self._check(self.lib.pxs_neighbor_map_k3_grid(_ptr(coords), n, batch_size, *shape,
+                                                      _ptr(grid), _ptr(nbr), _ptr(masks),
+                                                      self.stream()),
+                    "pxs_neighbor_map_k3_grid")
+        return nbr[:, :n], (masks[:n] if masks is not None else None)
 
     def neighbor_pairs(self, nbr):
         n = nbr.shape[1]

@@ -48,6 +48,35 @@ def test_neighbor_map_bit_exact(px, orc, case):
     assert px.validate(c, batch, shape) == (0, -1)
 
 
+@pytest.mark.parametrize("case", list(coord_cases()) + ["edges"])
+def test_neighbor_map_grid_bit_exact(px, orc, case):
+    """The dense-grid map equals the oracle's (and so the hash map's) bit for
+    bit, including voxels on the grid faces and a coordinate outside the
+    extents (never entered; its own row is still its centre)."""
+    if case == "edges":
+        coords = np.array([[0, 0, 0, 0], [0, 0, 0, 1], [0, 0, 1, 0], [0, 7, 7, 7], [0, 7, 7, 6],
+                           [1, 0, 0, 0], [1, 7, 0, 7]], np.int32)
+        batch, shape = 2, (8, 8, 8)
+    else:
+        coords, batch, shape = coord_cases()[case]
+    print(f"[neighbor_map_grid] case={case} n={coords.shape[0]}", flush=True)
+    nbr, masks = px.neighbor_map_grid(ti32(coords), batch, shape)
+    ref = orc.neighbor_map(coords)
+    np.testing.assert_array_equal(nbr.cpu().numpy(), ref)
+    present = (ref != coords.shape[0])
+    ref_masks = (present.astype(np.int64) << np.arange(27)[:, None]).sum(0)
+    np.testing.assert_array_equal(masks.cpu().numpy().astype(np.int64) & 0x7FFFFFF, ref_masks)
+
+
+def test_neighbor_map_grid_skips_out_of_extent_rows(px):
+    coords = np.array([[0, 1, 1, 1], [0, 1, 1, 2], [0, 9, 1, 1]], np.int32)  # x = 9 >= 8
+    nbr, masks = px.neighbor_map_grid(ti32(coords), 1, (8, 8, 8))
+    nb = nbr.cpu().numpy()
+    assert nb[13].tolist() == [0, 1, 2]          # centres
+    assert nb[14, 0] == 1 and nb[12, 1] == 0     # z neighbours inside the extents
+    assert (np.delete(nb[:, 2], 13) == 3).all()  # the outside row sees no neighbour
+
+
 @pytest.mark.parametrize("case", ["conv_fp32_64", "small_2batch"])
 def test_neighbor_pairs_bit_exact(px, orc, case):
     coords, _, _ = coord_cases()[case]
