@@ -317,12 +317,32 @@ __device__ __forceinline__ int64_t coarse_cell(int4 c, int f, int cx, int cy, in
     return ((static_cast<int64_t>(c.x) * cx + c.y / f) * cy + c.z / f) * cz + c.w / f;
 }
 
+// Rows that share a bitmap word (the f^3 children of a cell and their
+// neighbours along z) are merged inside the wavefront first: one atomic per
+// distinct word instead of one per row.  Sorted input gives a handful of
+// words per wavefront.
 __global__ void coarse_mark_kernel(const int4 * __restrict__ coords, int64_t n, int f, int cx,
                                    int cy, int cz, uint32_t * __restrict__ bitmap) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (p >= n) return;
-    const int64_t cell = coarse_cell(coords[p], f, cx, cy, cz);
-    atomicOr(bitmap + (cell >> 5), 1u << (cell & 31));
+    const bool live = p < n;
+    int64_t word = -1;
+    uint32_t bit = 0;
+    if (live) {
+        const int64_t cell = coarse_cell(coords[p], f, cx, cy, cz);
+        word = cell >> 5;
+        bit = 1u << (cell & 31);
+    }
+    uint64_t pending = __ballot(live);
+    while (pending) {
+        const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+        const int64_t w0 = __shfl(word, leader, 64);
+        const bool mine = live && word == w0;
+        uint32_t v = mine ? bit : 0u;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) v |= __shfl_xor(v, d, 64);
+        if ((threadIdx.x & 63) == leader) atomicOr(bitmap + w0, v);
+        pending &= ~__ballot(mine);
+    }
 }
 
 __device__ __forceinline__ int64_t coarse_rank(int64_t cell, const uint32_t * __restrict__ bitmap,

@@ -3,12 +3,16 @@
 * kat_inputs: tests/sparse_numeric_fixture.cpp:23-156 (10 points, 2 batches,
   affine sequences);
 * block_kat: tests/sparse_transformer_numeric_fixture.cpp:36-135 (one cross
-  block, C=12, 2 heads x 6, MLP 18, context 5, projection 7).
+  block, C=12, 2 heads x 6, MLP 18, context 5, projection 7);
+* flow_case: seeded SLat-flow inputs and weights (this build's, for the
+  oracle-vs-reference and GPU-vs-oracle flow checks).
 The expected outputs are the reference binaries' printed values, committed as
 tests/golden/*.json.
 """
 
 import numpy as np
+
+import workloads as W
 
 
 def kat_inputs():
@@ -72,3 +76,38 @@ def block_kat():
     tmod = seq(2 * 6 * C, 0.07, -0.009)
     return dict(coords=coords, x=x, proj=proj, ctx=ctx, tmod=tmod, weights=ws,
                 cfg_i=[C, H, M, CC, PC, 1, 1, 1, 1], cfg_f=[1e-6, 1.0, 10000.0])
+
+
+def flow_case(seed, n_items, grid, C, H, nblocks, ctx_tokens, in_ch=8, out_ch=8, mlp_ratio=4):
+    coords = W.shell_coords(grid, n_items, seed)
+    n = coords.shape[0]
+    M, CC = C * mlp_ratio, C
+    rng_std = 0.02
+    x = W.normal(seed, n * in_ch, 1).reshape(n, in_ch)
+    t = (W.uniform(seed, len(n_items), 2) * 1000.0).astype(np.float32)
+    ctx = W.normal(seed, ctx_tokens * len(n_items) * CC, 3).reshape(-1, CC)
+    ctx_off = np.arange(len(n_items) + 1, dtype=np.int64) * ctx_tokens
+    fw = [W.normal(seed, C * in_ch, 10, std=rng_std).reshape(C, in_ch), np.zeros(C, np.float32),
+          W.normal(seed, C * 256, 11, std=rng_std).reshape(C, 256), np.zeros(C, np.float32),
+          W.normal(seed, C * C, 12, std=rng_std).reshape(C, C), np.zeros(C, np.float32),
+          W.normal(seed, 6 * C * C, 13, std=rng_std).reshape(6 * C, C),
+          np.zeros(6 * C, np.float32),
+          W.normal(seed, out_ch * C, 14, std=rng_std).reshape(out_ch, C),
+          np.zeros(out_ch, np.float32)]
+    shapes = [6 * C, 3 * C * C, 3 * C, C, C, C * C, C, C, C, C * C, C, 2 * C * CC, 2 * C, C, C,
+              C * C, C, None, None, M * C, M, C * M, C]
+    blocks = []
+    for b in range(nblocks):
+        ws = []
+        for i, s in enumerate(shapes):
+            if s is None:
+                ws.append(None)
+                continue
+            w = W.normal(seed + 100 * (b + 1), s, i, std=rng_std)
+            if i in (3, 4, 7, 13, 14):  # RMS gammas and the norm2 weight
+                w = np.ones(s, np.float32)
+            ws.append(w)
+        blocks.append(ws)
+    dims = [in_ch, C, out_ch, nblocks, H, M, CC, 1, 1]
+    return dict(coords=coords, x=x, t=t, ctx=ctx, ctx_off=ctx_off, fw=fw, blocks=blocks,
+                dims=dims, C=C, H=H, M=M, CC=CC, n=n)

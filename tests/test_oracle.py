@@ -378,3 +378,37 @@ def test_decoder_block_closed_forms(orc):
     expect = np.repeat(skip, O_ // (C // 8), axis=1)
     np.testing.assert_array_equal(y, expect)
     assert y[0, 0] == y[0, 1] == skip[0, 0] and y[0, O_ // (C // 8)] == skip[0, 1]
+
+
+def _silu_branch(v):
+    """silu (src/slat_flow.cpp:79-83): the two-branch form."""
+    v = np.asarray(v, np.float32)
+    pos = v / (np.float32(1.0) + np.exp(-np.maximum(v, 0)))
+    e = np.exp(np.minimum(v, 0))
+    neg = v * e / (np.float32(1.0) + e)
+    return np.where(v >= 0, pos, neg).astype(np.float32)
+
+
+@pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref is built only where /root/reference exists")
+def test_flow_composes_reference_primitives(orc):
+    """orc_slat_flow_forward against the compiled reference's sparse_linear,
+    timestep_embed_mlp (src/flow.cpp:125-180), the row linear's arithmetic
+    (varlen_linear: bias first, inputs ascending), the transformer block and
+    sparse_layer_norm, chained as src/slat_flow.cpp:201-248 does."""
+    from fixtures import flow_case
+
+    ref = O.Reference()
+    C, H, B, G = 32, 2, 2, 12
+    case = flow_case(33, [[(3.0, 4.5)], [(2.5, 4.0)]], G, C, H, 2, 5)
+    fw, blocks = case["fw"], case["blocks"]
+    h = ref.linear(ref.sparse(case["coords"], case["x"], B, (G, G, G)), fw[0], fw[1])
+    temb = _silu_branch(ref.timestep_embed_mlp(case["t"], C, 256, fw[2], fw[3], fw[4], fw[5]))
+    tmod = ref.varlen_linear(ref.varlen([0, B], temb), fw[6], fw[7]).read()
+    ctx = ref.varlen(case["ctx_off"], case["ctx"])
+    cfg_i = [C, H, case["M"], case["CC"], 0, 1, 1, 1, 0]
+    for ws in blocks:
+        h = ref.transformer_block(h, tmod, ctx, cfg_i, [1e-6, 1.0, 10000.0], ws)
+    expect = ref.linear(ref.layer_norm(h, 1e-5), fw[8], fw[9]).read()[1]
+    got = orc.slat_flow_forward(case["coords"], B, case["x"], case["t"], case["ctx"],
+                                case["ctx_off"], case["dims"], [1e-6, 1.0, 10000.0], fw, blocks)
+    assert np.max(np.abs(got - expect)) <= 1e-6 * np.max(np.abs(expect))
