@@ -316,7 +316,11 @@ __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent ro
 // 256-row tiles and 3-4 stage pipelines (which fit only one workgroup per CU).
 // Loading gathered rows straight into VGPRs (64 bytes per lane, weights alone
 // through LDS) lost 15-20% in the U-Net stage: its 32-byte row pieces per
-// instruction coalesce worse than these 8 full 128-byte row chunks.
+// instruction coalesce worse than these 8 full 128-byte row chunks.  Staging
+// them through VGPRs with this kernel's own load pattern, two steps ahead of
+// the LDS ring (twice the gathers in flight), lost 10%: the kernel is not
+// bound by load latency; each stage moves 128 KiB through LDS per workgroup
+// (fragment reads plus DMA writes) with the matrix cores about a third busy.
 #ifndef PXS_GEMM_STAGES
 #define PXS_GEMM_STAGES 2
 #endif
