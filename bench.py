@@ -48,8 +48,8 @@ PEAK_HBM_GBS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="unet_stage_128",
                     choices=["unet_stage_128", "conv_fp32_64", "attn_block", "swin_64",
                              "flow_step"])
@@ -82,6 +82,28 @@ class Timer:
 
     def reset(self):
         self.events = {}
+
+
+# Untimed warmup: the requested steps, continued until the GPU has run for
+# at least this long (its clocks take a few hundred ms to settle).
+MIN_WARMUP_S = 0.5
+
+
+def warm_up(args, torch, step):
+    """args.warmup untimed steps, then more until MIN_WARMUP_S has passed;
+    returns the number of steps run."""
+    t0 = time.perf_counter()
+    done = 0
+    for _ in range(args.warmup):
+        step()
+        done += 1
+    torch.cuda.synchronize()
+    while time.perf_counter() - t0 < MIN_WARMUP_S:
+        for _ in range(10):
+            step()
+        done += 10
+        torch.cuda.synchronize()
+    return done
 
 
 def cpu_threads():
@@ -159,9 +181,7 @@ def unet_stage(args, torch, px, W):
         timer.run("subm_conv_c", lambda: chk(lib.pxs_subm_conv3d(
             1, P(y_b), m, 256, P(w_c), P(b_c), 256, P(nbr2), P(mask2), P(y_c), s), "conv c"))
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm = warm_up(args, torch, step)
     # Active pair counts (algorithmic work) from the neighbor masks.
     pa = int(np.unpackbits(mask1.cpu().numpy().view(np.uint8)).sum())
     pc = int(np.unpackbits(mask2.cpu().numpy().view(np.uint8)).sum())
@@ -202,7 +222,7 @@ def unet_stage(args, torch, px, W):
                                "3 ellipsoid shells each); voxel grid + neighbour map, SubMConv3d 128->128, "
                                "s2 SparseConv3d 128->256, grid + map at 64^3, SubMConv3d 256->256",
                    "voxels": n, "voxels_64": m, "pairs_a": pa, "pairs_c": pc,
-                   "per_op": per_op},
+                   "warmup_steps_run": warm, "per_op": per_op},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
@@ -241,9 +261,7 @@ def attention_metric(args, torch, px, W):
     cu = torch.tensor([0, lens[0], n], dtype=torch.int64, device=dev)
     o = torch.empty_like(q)
     timer = Timer(torch)
-    for _ in range(args.warmup):
-        px.varlen_attention(q, k, v, cu, cu, heads, hd, 0.125, out=o)
-    torch.cuda.synchronize()
+    warm_up(args, torch, lambda: px.varlen_attention(q, k, v, cu, cu, heads, hd, 0.125, out=o))
     steps = max(args.steps, 5)
     for _ in range(steps):
         timer.run("attn", lambda: px.varlen_attention(q, k, v, cu, cu, heads, hd, 0.125, out=o))
@@ -298,9 +316,7 @@ def cpu_baseline_conv():
 def timed_steps(args, torch, step, timer=None):
     """Mean wall time of one step over args.steps after args.warmup untimed
     steps; the per-kernel timer restarts after the warmup."""
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_up(args, torch, step)
     if timer is not None:
         timer.reset()
     t0 = time.perf_counter()

@@ -20,6 +20,8 @@
 
 #include "pxs_common.h"
 
+#include <type_traits>
+
 namespace pxs {
 namespace {
 
@@ -321,6 +323,11 @@ __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent ro
 // the LDS ring (twice the gathers in flight), lost 10%: the kernel is not
 // bound by load latency; each stage moves 128 KiB through LDS per workgroup
 // (fragment reads plus DMA writes) with the matrix cores about a third busy.
+// Splitting each stage's four K steps between two groups of 4 waves with
+// 64x64 blocks (KSPLIT = 2) cuts that to 96 KiB: U-Net stage +3.5%.
+// Reordering rows so that 128-row tiles share neighbour masks (buckets of the
+// face offsets, or of the x-1/x+1 planes: up to 20% fewer offset stages)
+// lost 2-15% to the lost locality of the gathered rows.
 #ifndef PXS_GEMM_STAGES
 #define PXS_GEMM_STAGES 2
 #endif
@@ -335,6 +342,9 @@ __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent ro
 #endif
 #ifndef PXS_GEMM_WAVES_M
 #define PXS_GEMM_WAVES_M 2
+#endif
+#ifndef PXS_GEMM_KSPLIT
+#define PXS_GEMM_KSPLIT 2
 #endif
 #ifndef PXS_GEMM_ISSUE_LATE
 #define PXS_GEMM_ISSUE_LATE 0
@@ -382,17 +392,24 @@ constexpr int lds_gemm_bytes(int noff) {
     return NSTAGE * (BM + BN) * kChunkBytes + noff * BM * 4;
 }
 
-// NW waves per workgroup in a WAVES_M x (NW / WAVES_M) grid; each wave owns
-// a (BM / WAVES_M) x (BN / (NW / WAVES_M)) block of the output tile.
-template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M>
+// NW waves per workgroup in KSPLIT groups; the waves of a group form a
+// WAVES_M x (NW / KSPLIT / WAVES_M) grid, each owning a block of the output
+// tile.  With KSPLIT = 2 the two groups take alternate 16-element K steps
+// of every stage and add their partial sums once at the end: 8 waves of
+// 64x64 blocks read each LDS fragment for two MFMAs instead of 1.5.
+template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M, int KSPLIT>
 __global__ void __launch_bounds__(NW * 64)
 gather_gemm_lds_kernel(GemmArgs a) {
     constexpr int kVec = Mfma<T>::kVec;
     constexpr int kChunk = Mfma<T>::kChunk;
     constexpr int kThreads = NW * 64;
-    constexpr int WAVES_N = NW / WAVES_M;
+    constexpr int NWG = NW / KSPLIT;
+    constexpr int WAVES_N = NWG / WAVES_M;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int TI = WM / 32, TJ = WN / 32;
+    constexpr int KSTEPS = 4 / KSPLIT;  // 16-element K steps per stage and group
+    static_assert(KSPLIT == 1 || (KSPLIT == 2 && sizeof(T) == 2 && TI % 2 == 0),
+                  "K split: bf16 only, an even number of 32-row blocks per wave");
     constexpr int kStageBytes = (BM + BN) * kChunkBytes;
     constexpr int AI = BM / (8 * NW);  // A instructions per wave per stage (8 rows each)
     constexpr int BI = BN / (8 * NW);
@@ -407,7 +424,8 @@ gather_gemm_lds_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int kg = wave / NWG, wl = wave % NWG;
+    const int wm = wl / WAVES_N, wn = wl % WAVES_N;
     const int h = lane >> 5, r = lane & 31;
 
     const int tiles_n = (a.cout + BN - 1) / BN;
@@ -422,8 +440,8 @@ gather_gemm_lds_kernel(GemmArgs a) {
     {
         uint32_t local = 0;
         for (int row = tid; row < BM; row += kThreads) {
+            if (p0 + row >= a.m) break;
             const int64_t p = p0 + row;
-            if (p >= a.m) break;
             if (a.masks) {
                 local |= a.masks[p];
             } else if (a.rowmap) {
@@ -450,9 +468,9 @@ gather_gemm_lds_kernel(GemmArgs a) {
     __syncthreads();
     for (int e = tid; e < kcount * BM; e += kThreads) {
         const int i = e / BM, row = e % BM;
-        const int64_t p = p0 + row;
         int32_t src = -1;
-        if (p < a.m) {
+        if (p0 + row < a.m) {
+            const int64_t p = p0 + row;
             const int64_t s = a.rowmap ? static_cast<int64_t>(a.rowmap[koff[i] * a.ld_map + p]) : p;
             src = (s >= 0 && s < a.rows_in) ? static_cast<int32_t>(s) : -1;
         }
@@ -531,8 +549,8 @@ gather_gemm_lds_kernel(GemmArgs a) {
         const char * sb = sa + BM * kChunkBytes;
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const int piece = 4 * h + ks;
+            for (int kk = 0; kk < KSTEPS; ++kk) {
+                const int piece = 4 * h + kg * KSTEPS + kk;
                 bf16x8 af[TI], bfr[TJ];
 #pragma unroll
                 for (int i = 0; i < TI; ++i) {
@@ -584,7 +602,44 @@ gather_gemm_lds_kernel(GemmArgs a) {
             if (s + NSTAGE - 1 < stages) issue(s + NSTAGE - 1);
         }
     }
-    gemm_epilogue<T, TI, TJ, WM, WN, EPI>(a, acc, p0, n0, wm, wn, h, r);
+    if constexpr (KSPLIT == 1) {
+        gemm_epilogue<T, TI, TJ, WM, WN, EPI>(a, acc, p0, n0, wm, wn, h, r);
+    } else {
+        // Group 0 finishes the upper 32-row blocks of each wave's tile and
+        // group 1 the lower ones; each hands the other half of its partial
+        // sums over through the (now idle) stage buffers.  A lane's slot is
+        // its own register index, so the exchange is conflict-free, and the
+        // sum a + b is the same whichever group adds it.
+        constexpr int HI = TI / 2;
+        static_assert(NW * HI * TJ * 16 * 64 * 4 <= NSTAGE * kStageBytes,
+                      "exchange must fit in the stage buffers");
+        float * xch = reinterpret_cast<float *>(smem);
+        auto slot = [&](int group, int i, int j, int v) {
+            return ((((group * NWG + wl) * HI + i) * TJ + j) * 16 + v) * 64 + lane;
+        };
+        auto finish = [&](auto keep_tag) {
+            constexpr int KEEP = decltype(keep_tag)::value, GIVE = HI - KEEP;
+#pragma unroll
+            for (int i = 0; i < HI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) xch[slot(kg, i, j, v)] = acc[GIVE + i][j][v];
+            barrier_no_fence();
+            f32x16 fin[HI][TJ];
+#pragma unroll
+            for (int i = 0; i < HI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        fin[i][j][v] = acc[KEEP + i][j][v] + xch[slot(1 - kg, i, j, v)];
+            gemm_epilogue<T, HI, TJ, WM, WN, EPI>(a, fin, p0 + KEEP * 32, n0, wm, wn, h, r);
+        };
+        barrier_no_fence();  // every wave is done reading the stage buffers
+        if (kg == 0) finish(std::integral_constant<int, 0>{});
+        else finish(std::integral_constant<int, HI>{});
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -650,9 +705,9 @@ split_gemm_f32_kernel(GemmArgs a) {
     __syncthreads();
     for (int e = tid; e < kcount * BM; e += NW * 64) {
         const int i = e / BM, row = e % BM;
-        const int64_t p = p0 + row;
         int32_t src = -1;
-        if (p < a.m) {
+        if (p0 + row < a.m) {
+            const int64_t p = p0 + row;
             const int64_t s = a.rowmap ? static_cast<int64_t>(a.rowmap[koff[i] * a.ld_map + p]) : p;
             src = (s >= 0 && s < a.rows_in) ? static_cast<int32_t>(s) : -1;
         }
@@ -758,13 +813,13 @@ int launch_split_f32(const GemmArgs & args, hipStream_t stream) {
     return check_launch("gather GEMM (fp32 split-K)");
 }
 
-template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M>
+template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M, int KSPLIT>
 int launch_lds_tile(const GemmArgs & args, hipStream_t stream) {
     const int smem = lds_gemm_bytes<BM, BN, NSTAGE>(args.noff);
     static int configured = 0;
     if (configured < smem) {
         hipError_t e = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE, NW, WAVES_M>),
+            reinterpret_cast<const void *>(&gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE, NW, WAVES_M, KSPLIT>),
             hipFuncAttributeMaxDynamicSharedMemorySize, lds_gemm_bytes<BM, BN, NSTAGE>(27));
         if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(gather_gemm_lds)");
         configured = lds_gemm_bytes<BM, BN, NSTAGE>(27);
@@ -773,7 +828,7 @@ int launch_lds_tile(const GemmArgs & args, hipStream_t stream) {
     const int64_t tiles_n = (args.cout + BN - 1) / BN;
     const int64_t blocks = tiles_m * tiles_n;
     if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "gather GEMM grid too large");
-    hipLaunchKernelGGL((gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE, NW, WAVES_M>),
+    hipLaunchKernelGGL((gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE, NW, WAVES_M, KSPLIT>),
                        dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), smem, stream, args);
     return check_launch("gather GEMM (LDS pipeline)");
 }
@@ -806,9 +861,11 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
     const bool narrow = args.cout <= 64;
     if (args.vec_ok) {
         // 128-row tiles: the row count only changes the grid, not the tile.
-        return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES, 4, 2>(args, stream)
+        constexpr int ksplit = sizeof(T) == 2 ? PXS_GEMM_KSPLIT : 1;
+        constexpr int waves_m = ksplit == 2 ? 2 : PXS_GEMM_WAVES_M;
+        return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES, 4, 2, 1>(args, stream)
                       : launch_lds_tile<T, PXS_GEMM_BM, PXS_GEMM_BN, EPI, PXS_GEMM_STAGES,
-                                        PXS_GEMM_WAVES, PXS_GEMM_WAVES_M>(args, stream);
+                                        PXS_GEMM_WAVES, waves_m, ksplit>(args, stream);
     }
     const int64_t tiles_n = (args.cout + (narrow ? 63 : 127)) / (narrow ? 64 : 128);
     const bool tall = ((args.m + 127) / 128) * tiles_n >= 512;

@@ -34,7 +34,7 @@ def run_conv(px, coords, x, w, b, dtype):
 
 def test_conv_fp32_reference_kat(px):
     """The reference's own KAT (tests/sparse_numeric_fixture.cpp): 10 points, 3 -> 4."""
-    from test_oracle import kat_inputs
+    from fixtures import kat_inputs
 
     a = kat_inputs()
     gold = np.array(json.loads((GOLD / "sparse_numeric_fixture.json").read_text())
@@ -104,8 +104,7 @@ def test_conv_bf16_unet_full_size_sampled_rows(px):
 
 def plane_spans(idx, n, bm=128):
     """Per (tile of bm rows, x-plane) span of the input rows the plane's nine
-    offsets read: the bf16 kernel stages runs of at most 256 rows and gathers
-    per offset above that."""
+    offsets read."""
     spans = []
     for t in range(0, n, bm):
         sub = idx[:, t:t + bm]
@@ -118,9 +117,9 @@ def plane_spans(idx, n, bm=128):
 
 @pytest.mark.parametrize("masks", [True, False])
 def test_conv_bf16_staged_and_gathered_planes(px, orc, masks):
-    """A 3 x 72 x 72 slab plus a shell in a second batch: y lines of 72 rows
-    push some planes past the 256-row staging limit (gathered per offset),
-    the rest are staged; both must agree with the oracle."""
+    """A 3 x 72 x 72 slab plus a shell in a second batch: dense tiles whose
+    planes read rows hundreds apart next to thin shell tiles; both must agree
+    with the oracle, with and without the neighbour masks."""
     slab = np.array([(0, x, y, z) for x in range(3) for y in range(72) for z in range(72)],
                     np.int32)
     shell = W.shell_coords(24, [[(6.0, 10.0)]], 45)
