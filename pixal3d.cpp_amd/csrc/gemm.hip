@@ -346,6 +346,9 @@ __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent ro
 #ifndef PXS_GEMM_KSPLIT
 #define PXS_GEMM_KSPLIT 2
 #endif
+#ifndef PXS_GEMM_WIDE
+#define PXS_GEMM_WIDE 1
+#endif
 #ifndef PXS_GEMM_ISSUE_LATE
 #define PXS_GEMM_ISSUE_LATE 0
 #endif
@@ -863,6 +866,16 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
         // 128-row tiles: the row count only changes the grid, not the tile.
         constexpr int ksplit = sizeof(T) == 2 ? PXS_GEMM_KSPLIT : 1;
         constexpr int waves_m = ksplit == 2 ? 2 : PXS_GEMM_WAVES_M;
+        if constexpr (sizeof(T) == 2) {
+            // Long gathers wider than 128 channels: one 256-channel tile
+            // gathers each row chunk once instead of once per 128-channel
+            // tile (one workgroup per CU; SubMConv3d 256->256 at 64^3 -6%).
+            // Short ones (the 8-offset stride-2 conv, 16 K stages) lose 6%:
+            // with one workgroup per CU nothing hides a tile's prologue.
+            const int64_t kstages = static_cast<int64_t>(args.noff) * ((args.cin + 63) / 64);
+            if (PXS_GEMM_WIDE && args.rowmap && args.cout > 128 && kstages >= 32)
+                return launch_lds_tile<T, 128, 256, EPI, 2, 8, 2, 1>(args, stream);
+        }
         return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES, 4, 2, 1>(args, stream)
                       : launch_lds_tile<T, PXS_GEMM_BM, PXS_GEMM_BN, EPI, PXS_GEMM_STAGES,
                                         PXS_GEMM_WAVES, waves_m, ksplit>(args, stream);
