@@ -15,7 +15,8 @@ size_t scan_workspace_bytes(int64_t count);
 
 // out[i] = sum_{j<i} value(i) for i < count, and *total = sum of all, where
 // value(i) = in[i] (int32 input) or popcount(in[i]) when popcount is set.
-// out may alias nothing; total is a device int64.  Three launches:
+// out may alias nothing; total is a device int64.  Up to 16384 items: one
+// single-workgroup launch.  Above that, three launches:
 // per-tile sums, a single-block scan of the tile sums, per-tile scans.
 int exclusive_scan_i32(const int32_t * in, int64_t * out, int64_t count, int64_t * total,
                        void * workspace, hipStream_t stream);

@@ -99,6 +99,81 @@ scan_tiles(const void * in, int64_t count, const int64_t * partials, int64_t * o
     }
 }
 
+// Counts up to kSingleItems: one workgroup of 1024 threads scans everything
+// in a single launch (the three-phase scan costs three launches even for a
+// few thousand items).  The items are read coalesced into LDS (one pad word
+// per 16, so that thread t's 16 consecutive items at 17t.. hit distinct
+// banks), then each thread scans its own 16.
+constexpr int kSingleThreads = 1024;
+constexpr int kSinglePer = 16;
+constexpr int64_t kSingleItems = static_cast<int64_t>(kSinglePer) * kSingleThreads;
+constexpr int kSingleLdsBytes = static_cast<int>((kSingleItems + kSingleItems / 16) * 4);
+
+template <bool kPopcount>
+__global__ void __launch_bounds__(kSingleThreads)
+scan_single(const void * in, int64_t count, int64_t * out, int64_t * total) {
+    extern __shared__ int32_t stage[];
+    __shared__ int64_t wave_sums[kSingleThreads / 64];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    {
+        // All 16 loads in flight at once, then the LDS stores.
+        int32_t v[kSinglePer];
+#pragma unroll
+        for (int j = 0; j < kSinglePer; ++j) {
+            const int i = j * kSingleThreads + t;
+            v[j] = i < count ? static_cast<int32_t>(scan_value<kPopcount>(in, i)) : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < kSinglePer; ++j) {
+            const int i = j * kSingleThreads + t;
+            stage[i + (i >> 4)] = v[j];
+        }
+    }
+    __syncthreads();
+    const int base = t * kSinglePer;
+    int64_t vals[kSinglePer];
+    int64_t s = 0;
+#pragma unroll
+    for (int j = 0; j < kSinglePer; ++j) {
+        vals[j] = base + j < count ? stage[t * (kSinglePer + 1) + j] : 0;
+        s += vals[j];
+    }
+    int64_t inc = s;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t o = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) wave_sums[wave] = inc;
+    __syncthreads();
+    if (wave == 0) {
+        int64_t w = lane < kSingleThreads / 64 ? wave_sums[lane] : 0;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int64_t o = __shfl_up(w, d, 64);
+            if (lane >= d) w += o;
+        }
+        if (lane < kSingleThreads / 64) wave_sums[lane] = w;  // inclusive over waves
+    }
+    __syncthreads();
+    // Thread t's exclusive base in LDS; its items become their offsets from
+    // it (a partial sum of 16 items fits in int32, the total does too).
+    __shared__ int64_t thread_base[kSingleThreads];
+    thread_base[t] = inc - s + (wave > 0 ? wave_sums[wave - 1] : 0);
+    int32_t part = 0;
+#pragma unroll
+    for (int j = 0; j < kSinglePer; ++j) {
+        stage[t * (kSinglePer + 1) + j] = part;
+        part += static_cast<int32_t>(vals[j]);
+    }
+    __syncthreads();
+    // Coalesced stores: item i = j * 1024 + t.
+#pragma unroll
+    for (int j = 0; j < kSinglePer; ++j) {
+        const int i = j * kSingleThreads + t;
+        if (i < count) out[i] = thread_base[i >> 4] + stage[i + (i >> 4)];
+    }
+    if (t == kSingleThreads - 1 && total) *total = wave_sums[kSingleThreads / 64 - 1];
+}
+
 template <typename T>
 __global__ void fill_kernel(T * p, int64_t count, T value) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -116,6 +191,19 @@ int run_scan(const void * in, int64_t * out, int64_t count, int64_t * total, voi
     if (count <= 0) {
         if (total) return fill_i64(total, 1, 0, stream);
         return PXS_OK;
+    }
+    if (count <= kSingleItems) {
+        static bool configured = false;
+        if (!configured) {
+            hipError_t e = hipFuncSetAttribute(
+                reinterpret_cast<const void *>(&scan_single<kPopcount>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, kSingleLdsBytes);
+            if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(scan_single)");
+            configured = true;
+        }
+        hipLaunchKernelGGL(scan_single<kPopcount>, dim3(1), dim3(kSingleThreads), kSingleLdsBytes,
+                           stream, in, count, out, total);
+        return check_launch("exclusive scan (single workgroup)");
     }
     hipLaunchKernelGGL(scan_tile_sums<kPopcount>, dim3(static_cast<unsigned>(tiles)),
                        dim3(kScanBlock), 0, stream, in, count, partials);

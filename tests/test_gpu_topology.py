@@ -135,6 +135,19 @@ def test_window_partition_bit_exact(px, orc, case, shift):
     np.testing.assert_array_equal(cu.cpu().numpy(), rcu)
 
 
+def test_window_partition_many_windows(px, orc):
+    """Window 4 at 128^3, batch 2: 65,536 windows, past the single-workgroup
+    scan (16,384 items), so the three-phase scan runs."""
+    coords = W.shell_coords(128, W.UNET_ITEMS, 2)
+    print(f"[window_partition] unet_stage_128 window=4 n={coords.shape[0]}", flush=True)
+    fwd, bwd, cu, nwin = px.window_partition(ti32(coords), 2, (128, 128, 128), 4, 2)
+    rfwd, rbwd, rcu = orc.window_partition(coords, (128, 128, 128), 4, 2)
+    assert nwin == len(rcu) - 1
+    np.testing.assert_array_equal(fwd.cpu().numpy(), rfwd)
+    np.testing.assert_array_equal(bwd.cpu().numpy(), rbwd)
+    np.testing.assert_array_equal(cu.cpu().numpy(), rcu)
+
+
 def test_window_partition_padded_segments(px, orc):
     """Without reading the window count, cu_seqlens up to min(n, windows) ends
     in empty segments, and attention over that bound equals attention over
@@ -193,6 +206,20 @@ def test_downsample_any_factor(px, orc, factor):
     o, r = off.cpu().numpy(), rows.cpu().numpy()
     for q in range(m):
         assert np.all(np.diff(r[o[q]:o[q + 1]]) > 0)
+
+
+def test_downsample_factor2_full_size(px, orc):
+    """Factor-2 grouping and mean over the 162,263-row U-Net coordinates
+    (group offsets scanned over more rows than one workgroup takes)."""
+    coords = W.shell_coords(128, W.UNET_ITEMS, 2)
+    n = coords.shape[0]
+    x = W.normal(37, n * 8, 1).reshape(n, 8)
+    print(f"[downsample] factor=2 n={n}", flush=True)
+    oc, off, rows, m = px.downsample(ti32(coords), 2, (128, 128, 128), 2)
+    y = host(px.downsample_mean(t32(x), off, rows, m))
+    roc, ry = orc.downsample_mean(coords, x, 2)
+    np.testing.assert_array_equal(oc.cpu().numpy(), roc)
+    np.testing.assert_array_equal(y, ry)
 
 
 def test_channel_to_spatial_factor3(px, orc):
