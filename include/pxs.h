@@ -404,6 +404,77 @@ int pxs_slat_flow_forward(int dtype, const pxs_flow_config * cfg, const pxs_flow
                           int64_t context_tokens, const void * projected, float * out,
                           void * workspace, void * stream);
 
+/* ---- f4: flow-matching Euler sampler with classifier-free guidance ---------------- */
+
+/* FlowEulerSamplerConfig (include/pixal3d/flow_sampler.h:14-23) without the
+ * trajectory flag. */
+typedef struct pxs_flow_sampler_config {
+    int steps;
+    float sigma_min;
+    float rescale_t;
+    float guidance_strength;
+    float guidance_rescale;
+    float guidance_interval_min;
+    float guidance_interval_max;
+} pxs_flow_sampler_config;
+
+/* Host function: the schedule of step `step` of flow_euler_sample_f32
+ * (src/flow_sampler.cpp:268-285): the model time t in [0, 1] (the model is
+ * called with 1000 t), the next step's t, and the guidance weight (the
+ * configured strength inside the guidance interval, else 1).  Rejects the
+ * configurations valid_config rejects (src/flow_sampler.cpp:111-124) with its
+ * message. */
+int pxs_flow_sampler_schedule(const pxs_flow_sampler_config * cfg, int step, float * timestep,
+                              float * next_timestep, float * guidance);
+
+/* The guided prediction of one step (src/flow_sampler.cpp:192-235, 304-318):
+ * prediction = g * positive + (1 - g) * negative, then, when
+ * guidance_rescale > 0, the CFG rescale: x0 = (1 - sigma_min) state -
+ * (sigma_min + (1 - sigma_min) t) pred for pred = positive and the blend, the
+ * population standard deviation of each batch item's x0 values (rows
+ * cu_rows[b] .. cu_rows[b+1]), x0_cfg scaled by std_pos / std_cfg (1 when
+ * std_cfg is 0) and mixed with weight guidance_rescale, converted back to a
+ * prediction.  All fp32 [rows, channels] device buffers; results equal the
+ * reference bit for bit.  coords, cu_rows and the workspace are used by the
+ * rescale only.  An item without rows keeps a zero deviation (the reference
+ * rejects such input before this step). */
+size_t pxs_flow_guidance_workspace_bytes(int batch_size);
+int pxs_flow_guidance(const float * state, const float * positive, const float * negative,
+                      const int32_t * coords, const int64_t * cu_rows, int64_t rows, int channels,
+                      int batch_size, float timestep, float sigma_min, float guidance,
+                      float guidance_rescale, float * prediction, void * workspace, void * stream);
+
+/* pred_to_xstart (src/flow_sampler.cpp:138-146): x0 = (1 - sigma_min) state
+ * - (sigma_min + (1 - sigma_min) t) prediction, over count fp32 values. */
+int pxs_flow_pred_to_xstart(const float * state, const float * prediction, int64_t count,
+                            float timestep, float sigma_min, float * x0, void * stream);
+
+/* The Euler step state -= delta * prediction (src/flow_sampler.cpp:330-333),
+ * delta = t - t_next. */
+int pxs_flow_euler_update(float * state, const float * prediction, int64_t count, float delta,
+                          void * stream);
+
+/* flow_euler_sample_f32 (src/flow_sampler.cpp:237-345) with the SLat-flow
+ * model of pxs_slat_flow_forward as the velocity, device resident: from
+ * noise (fp32 [rows, in_channels]) at t = 1 to samples at t = 0.  Guided
+ * steps run the conditional and unconditional forwards as ONE varlen batch
+ * of 2 * batch_size items (the rows twice, cond then uncond context), so
+ * every launch of the forward carries twice the tokens; a step whose
+ * guidance weight is 1 (or 0) runs the conditional (or unconditional)
+ * forward alone, as the reference does.  cond / uncond: context tokens in the
+ * call's dtype with per-item offsets, as for pxs_slat_flow_forward.  Requires
+ * in_channels == out_channels.  samples may alias noise. */
+size_t pxs_flow_euler_sample_workspace_bytes(int dtype, const pxs_flow_config * cfg,
+                                             int64_t rows, int64_t cond_tokens,
+                                             int64_t uncond_tokens, int batch_size);
+int pxs_flow_euler_sample(int dtype, const pxs_flow_config * cfg, const pxs_flow_weights * w,
+                          const pxs_flow_sampler_config * scfg, const int32_t * coords,
+                          int64_t rows, int batch_size, const int64_t * cu_rows,
+                          const float * noise, const void * cond, const int64_t * cond_offsets,
+                          int64_t cond_tokens, const void * uncond,
+                          const int64_t * uncond_offsets, int64_t uncond_tokens,
+                          float * samples, void * workspace, void * stream);
+
 /* ---- a16: SLat-decoder blocks, device resident ------------------------------------ */
 
 /* SLatDecoderBlockWeightsF32 (include/pixal3d/slat_decoder.h:18-41) as device

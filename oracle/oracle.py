@@ -60,6 +60,27 @@ def _i64(a):
     return np.ascontiguousarray(a, dtype=np.int64)
 
 
+# velocity(state*, rows, channels, 1000 t, conditional, velocity*, user) -> nonzero ok
+VELOCITY_FN = C.CFUNCTYPE(C.c_int, _f32p, C.c_int64, C.c_int, C.c_float, C.c_int, _f32p, _vp)
+
+
+def velocity_callback(fn):
+    """Wrap fn(state [rows, ch] float32, t_model, conditional) -> velocity array
+    as a C callback (keep the returned object alive while it is used)."""
+
+    def cb(state_p, rows, channels, t_model, cond, out_p, _user):
+        try:
+            n = int(rows) * int(channels)
+            state = np.ctypeslib.as_array(state_p, shape=(n,)).reshape(int(rows), int(channels))
+            out = np.ctypeslib.as_array(out_p, shape=(n,)).reshape(int(rows), int(channels))
+            out[...] = np.asarray(fn(state.copy(), np.float32(t_model), bool(cond)), np.float32)
+            return 1
+        except Exception:  # reported to the caller as a failed callback
+            return 0
+
+    return VELOCITY_FN(cb)
+
+
 def build_oracle() -> None:
     """Compile build/liboracle.so (and _ref/ when /root/reference exists)."""
     import subprocess
@@ -124,6 +145,14 @@ class Oracle:
         L.orc_resblock_c2s.argtypes = [_i32p, C.c_int64, _f32p, C.c_int, C.c_int, C.c_float,
                                        _f32p, C.POINTER(_f32p), _i32p, _f32p]
         L.orc_thread_count.restype = C.c_int
+        L.orc_flow_schedule.restype = C.c_int
+        L.orc_flow_schedule.argtypes = [C.c_int, _f32p, C.c_int, _f32p, _f32p, _f32p]
+        L.orc_flow_guidance.restype = C.c_int
+        L.orc_flow_guidance.argtypes = [_f32p, _f32p, _f32p, _i32p, C.c_int64, C.c_int, C.c_int,
+                                        C.c_float, C.c_float, C.c_float, C.c_float, _f32p]
+        L.orc_flow_euler_sample.restype = C.c_int
+        L.orc_flow_euler_sample.argtypes = [_i32p, C.c_int64, C.c_int, C.c_int, _f32p, C.c_int,
+                                            _f32p, VELOCITY_FN, _vp, _f32p, _f32p, _f32p]
 
     # -- validation and topology -------------------------------------------
     def sparse_valid(self, coords, batch_size, shape, feats, channels):
@@ -369,6 +398,43 @@ class Oracle:
     def thread_count(self) -> int:
         return int(self.lib.orc_thread_count())
 
+    # -- flow Euler sampler ------------------------------------------------------
+    def flow_schedule(self, steps, cfg_f, step):
+        """(code, t, t_next, guidance); cfg_f = [sigma_min, rescale_t, strength,
+        rescale, interval_min, interval_max]."""
+        cf = _f32(cfg_f)
+        t, tn, g = (np.zeros(1, np.float32) for _ in range(3))
+        rc = self.lib.orc_flow_schedule(steps, _p(cf, _f32p), step, _p(t, _f32p), _p(tn, _f32p),
+                                        _p(g, _f32p))
+        return int(rc), t[0], tn[0], g[0]
+
+    def flow_guidance(self, state, pos, neg, coords, batch_size, t, sigma_min, guidance, rescale):
+        state, pos, neg = _f32(state), _f32(pos), _f32(neg)
+        coords = _i32(coords).reshape(-1, 4)
+        pred = np.empty_like(state)
+        rc = self.lib.orc_flow_guidance(_p(state, _f32p), _p(pos, _f32p), _p(neg, _f32p),
+                                        _p(coords, _i32p), coords.shape[0], state.shape[1],
+                                        batch_size, t, sigma_min, guidance, rescale,
+                                        _p(pred, _f32p))
+        if rc:
+            raise ValueError(f"orc_flow_guidance failed with code {rc}")
+        return pred
+
+    def flow_euler_sample(self, coords, batch_size, noise, steps, cfg_f, fn, record=False):
+        """-> (samples, traj_xt or None, traj_x0 or None); fn as for velocity_callback."""
+        coords, noise, cf = _i32(coords).reshape(-1, 4), _f32(noise), _f32(cfg_f)
+        rows, ch = noise.shape
+        out = np.empty_like(noise)
+        xt = np.empty((steps, rows, ch), np.float32) if record else None
+        x0 = np.empty((steps, rows, ch), np.float32) if record else None
+        cb = velocity_callback(fn)
+        rc = self.lib.orc_flow_euler_sample(_p(coords, _i32p), rows, ch, batch_size,
+                                            _p(noise, _f32p), steps, _p(cf, _f32p), cb, None,
+                                            _p(out, _f32p), _p(xt, _f32p), _p(x0, _f32p))
+        if rc:
+            raise ValueError(f"orc_flow_euler_sample failed with code {rc}")
+        return out, xt, x0
+
 
 class RefSparse:
     """An owned reference SparseTensorF32 handle."""
@@ -460,6 +526,8 @@ class Reference:
         L.ref_sparse_submanifold_conv3d.argtypes = [_vp, _f32p, _f32p, C.c_int, _vp] + eb
         L.ref_transformer_block.argtypes = [_vp, _f32p, _vp, _vp, _intp, _f32p,
                                             C.POINTER(_f32p), _vp] + eb
+        L.ref_flow_euler_sample.argtypes = [_vp, _intp, _f32p, VELOCITY_FN, _vp, _vp, _f32p,
+                                            _f32p] + eb
         if self.has_threads:
             L.ref_timestep_embedding.argtypes = [_f32p, C.c_int64, C.c_int, C.c_int, _f32p] + eb
             L.ref_timestep_embed_mlp.argtypes = [_f32p, C.c_int64, C.c_int, C.c_int, _f32p,
@@ -470,7 +538,7 @@ class Reference:
                      "ref_sparse_cross_attention", "ref_sparse_rope", "ref_sparse_mh_rms_norm",
                      "ref_varlen_mh_rms_norm", "ref_sparse_submanifold_conv3d",
                      "ref_transformer_block", "ref_timestep_embedding",
-                     "ref_timestep_embed_mlp"):
+                     "ref_timestep_embed_mlp", "ref_flow_euler_sample"):
             if hasattr(L, name):
                 getattr(L, name).restype = C.c_int
 
@@ -594,6 +662,21 @@ class Reference:
         self._call("ref_transformer_block", t.h, _p(t_mod, _f32p), ctx.h,
                    None if projected is None else projected.h, cfg_i_a, cfg_f_a, wp, out.h)
         return out
+
+    def flow_euler_sample(self, noise: "RefSparse", steps, cfg_f, fn, record=False):
+        """flow_euler_sample_f32 with fn as the velocity (see velocity_callback);
+        -> (samples RefSparse, traj_xt or None, traj_x0 or None)."""
+        shape = noise.shape()
+        rows, ch = int(shape[0]), int(shape[1])
+        cfg_i = (C.c_int * 2)(steps, 1 if record else 0)
+        cf = _f32(cfg_f)
+        xt = np.empty((max(steps, 1), rows, ch), np.float32) if record else None
+        x0 = np.empty((max(steps, 1), rows, ch), np.float32) if record else None
+        out = self.empty()
+        cb = velocity_callback(fn) if fn is not None else VELOCITY_FN()
+        self._call("ref_flow_euler_sample", noise.h, cfg_i, _p(cf, _f32p), cb, None, out.h,
+                   _p(xt, _f32p), _p(x0, _f32p))
+        return out, xt, x0
 
     def timestep_embedding(self, t, dim, max_period=10000):
         t = _f32(t)

@@ -36,6 +36,13 @@
 //                              bias = 0 => out = count * mean-pool
 //   orc_window_partition       contract; pinned by brute-force invariants in tests
 //                              (window membership, stable order, permutation)
+//   orc_flow_schedule, orc_flow_guidance, orc_flow_euler_sample
+//                              bit-exact vs oracle/_ref (the reference's
+//                              src/flow_sampler.cpp compiled where it lies, driven
+//                              with the same velocity callback); closed forms in
+//                              tests (zero velocity keeps the state; guidance 1 or
+//                              0 selects one branch; constant velocity v moves the
+//                              state by -v in total)
 
 #include <algorithm>
 #include <cmath>
@@ -846,6 +853,142 @@ int64_t orc_resblock_c2s(const int32_t * coords, int64_t n, const float * x, int
     }
     std::memcpy(out_coords, sc.data(), static_cast<size_t>(m) * 4 * sizeof(int32_t));
     return m;
+}
+
+// ---- flow Euler sampler (src/flow_sampler.cpp) -----------------------------
+
+// Step schedule (src/flow_sampler.cpp:268-285) and configuration checks
+// (111-124).  cfg = {sigma_min, rescale_t, guidance_strength, guidance_rescale,
+// interval_min, interval_max}.  Returns 0, 1 (invalid configuration) or 2
+// (non-finite schedule).
+int orc_flow_schedule(int steps, const float * cfg, int step, float * t, float * t_next,
+                      float * guidance) {
+    const float sigma_min = cfg[0], rescale_t = cfg[1], strength = cfg[2], rescale = cfg[3];
+    const float lo = cfg[4], hi = cfg[5];
+    const bool bad = steps <= 0 || !(sigma_min >= 0.0f) || !(sigma_min < 1.0f) ||
+                     !std::isfinite(sigma_min) || !(rescale_t > 0.0f) || !std::isfinite(rescale_t) ||
+                     !std::isfinite(strength) || !std::isfinite(rescale) || rescale < 0.0f ||
+                     !std::isfinite(lo) || !std::isfinite(hi) || lo > hi;
+    if (bad) return 1;
+    const float fsteps = static_cast<float>(steps);
+    const float lin = 1.0f - static_cast<float>(step) / fsteps;
+    const float den = 1.0f + (rescale_t - 1.0f) * lin;
+    if (!(den > 0.0f) || !std::isfinite(den)) return 2;
+    const float now = rescale_t * lin / den;
+    const float lin_next = 1.0f - static_cast<float>(step + 1) / fsteps;
+    const float den_next = 1.0f + (rescale_t - 1.0f) * lin_next;
+    if (!(den_next > 0.0f) || !std::isfinite(den_next)) return 2;
+    *t = now;
+    *t_next = rescale_t * lin_next / den_next;
+    *guidance = (now >= lo && now <= hi) ? strength : 1.0f;
+    return 0;
+}
+
+// x0 = a * state - b * pred (src/flow_sampler.cpp:138-146).
+static void flow_x0(const float * state, const float * pred, int64_t count, float t,
+                    float sigma_min, float * x0) {
+    const float a = 1.0f - sigma_min;
+    const float b = sigma_min + a * t;
+    for (int64_t i = 0; i < count; ++i) x0[i] = a * state[i] - b * pred[i];
+}
+
+// Population standard deviation per batch item, summed in row order
+// (src/flow_sampler.cpp:158-190).  Returns false for an item without points.
+static bool flow_batch_std(const int32_t * coords, const float * x, int64_t rows, int channels,
+                           int batch, std::vector<float> & out) {
+    std::vector<float> sum(batch, 0.0f), sum_sq(batch, 0.0f);
+    std::vector<size_t> count(batch, 0);
+    for (int64_t p = 0; p < rows; ++p) {
+        const int b = coords[p * 4];
+        for (int c = 0; c < channels; ++c) {
+            const float v = x[p * channels + c];
+            sum[b] += v;
+            sum_sq[b] += v * v;
+            ++count[b];
+        }
+    }
+    out.assign(batch, 0.0f);
+    for (int b = 0; b < batch; ++b) {
+        if (count[b] == 0) return false;
+        const float mean = sum[b] / static_cast<float>(count[b]);
+        const float mean_sq = sum_sq[b] / static_cast<float>(count[b]);
+        out[b] = std::sqrt(std::max(mean_sq - mean * mean, 0.0f));
+    }
+    return true;
+}
+
+// Guided prediction: the blend (src/flow_sampler.cpp:192-200), then the CFG
+// rescale when rescale > 0 (202-235).  Returns 0, or 3 for an item without
+// points.
+int orc_flow_guidance(const float * state, const float * pos, const float * neg,
+                      const int32_t * coords, int64_t rows, int channels, int batch, float t,
+                      float sigma_min, float guidance, float rescale, float * pred) {
+    const int64_t count = rows * channels;
+    const float wn = 1.0f - guidance;
+    for (int64_t i = 0; i < count; ++i) pred[i] = guidance * pos[i] + wn * neg[i];
+    if (!(rescale > 0.0f)) return 0;
+    std::vector<float> x0_pos(count), x0_cfg(count), sd_pos, sd_cfg;
+    flow_x0(state, pos, count, t, sigma_min, x0_pos.data());
+    flow_x0(state, pred, count, t, sigma_min, x0_cfg.data());
+    if (!flow_batch_std(coords, x0_pos.data(), rows, channels, batch, sd_pos) ||
+        !flow_batch_std(coords, x0_cfg.data(), rows, channels, batch, sd_cfg)) {
+        return 3;
+    }
+    for (int64_t p = 0; p < rows; ++p) {
+        const int b = coords[p * 4];
+        const float ratio = sd_cfg[b] != 0.0f ? sd_pos[b] / sd_cfg[b] : 1.0f;
+        for (int c = 0; c < channels; ++c) {
+            float & v = x0_cfg[p * channels + c];
+            const float scaled = v * ratio;
+            v = rescale * scaled + (1.0f - rescale) * v;
+        }
+    }
+    const float a = 1.0f - sigma_min;
+    const float b = sigma_min + a * t;
+    for (int64_t i = 0; i < count; ++i) pred[i] = (a * state[i] - x0_cfg[i]) / b;
+    return 0;
+}
+
+// velocity(state, rows, channels, 1000 t, conditional, out, user): nonzero = ok.
+typedef int (*orc_velocity_fn)(const float *, int64_t, int, float, int, float *, void *);
+
+// flow_euler_sample_f32 (src/flow_sampler.cpp:237-345) without diagnostics.
+// traj_xt / traj_x0 (nullable) receive steps x [rows, channels] each.
+// Returns 0, the orc_flow_schedule / orc_flow_guidance codes, or 4 when the
+// callback fails.
+int orc_flow_euler_sample(const int32_t * coords, int64_t rows, int channels, int batch,
+                          const float * noise, int steps, const float * cfg,
+                          orc_velocity_fn model, void * user, float * samples, float * traj_xt,
+                          float * traj_x0) {
+    const int64_t count = rows * channels;
+    float t0 = 0.0f, t1 = 0.0f, g0 = 0.0f;
+    if (orc_flow_schedule(steps, cfg, 0, &t0, &t1, &g0) == 1) return 1;
+    std::vector<float> state(noise, noise + count), pos(count), neg(count), pred(count);
+    for (int step = 0; step < steps; ++step) {
+        float t = 0.0f, t_next = 0.0f, g = 1.0f;
+        if (int rc = orc_flow_schedule(steps, cfg, step, &t, &t_next, &g)) return rc;
+        if (g == 1.0f || g == 0.0f) {
+            if (!model(state.data(), rows, channels, 1000.0f * t, g == 1.0f ? 1 : 0, pred.data(),
+                       user)) {
+                return 4;
+            }
+        } else {
+            if (!model(state.data(), rows, channels, 1000.0f * t, 1, pos.data(), user) ||
+                !model(state.data(), rows, channels, 1000.0f * t, 0, neg.data(), user)) {
+                return 4;
+            }
+            if (int rc = orc_flow_guidance(state.data(), pos.data(), neg.data(), coords, rows,
+                                           channels, batch, t, cfg[0], g, cfg[3], pred.data())) {
+                return rc;
+            }
+        }
+        if (traj_x0) flow_x0(state.data(), pred.data(), count, t, cfg[0], traj_x0 + step * count);
+        const float delta = t - t_next;
+        for (int64_t i = 0; i < count; ++i) state[i] -= delta * pred[i];
+        if (traj_xt) std::copy(state.begin(), state.end(), traj_xt + step * count);
+    }
+    std::copy(state.begin(), state.end(), samples);
+    return 0;
 }
 
 int orc_thread_count() {

@@ -17,6 +17,7 @@
 #include "pixal3d/flow.h"
 #include "pixal3d/cpu_threads.h"
 #endif
+#include "pixal3d/flow_sampler.h"
 #include "pixal3d/sparse.h"
 #include "pixal3d/sparse_transformer.h"
 
@@ -262,6 +263,53 @@ int ref_transformer_block(void * in, const float * timestep_mod, void * context,
                       *as_sparse(in), timestep_mod, *as_varlen(context),
                       projected ? as_sparse(projected) : nullptr, c, w, *as_sparse(out), &e),
                   e, err, errlen);
+}
+
+// ---- flow Euler sampler (src/flow_sampler.cpp) ---------------------------
+// model(state feats, rows, channels, 1000 t, conditional, velocity feats, user)
+// returns nonzero on success; the velocity keeps the state's shape.
+// cfg_i = {steps, record_trajectory}; cfg_f = {sigma_min, rescale_t,
+// guidance_strength, guidance_rescale, interval_min, interval_max}.
+// traj_xt / traj_x0 (nullable) receive steps x feats each.
+typedef int (*ref_velocity_fn)(const float *, int64_t, int, float, int, float *, void *);
+
+int ref_flow_euler_sample(void * noise, const int * cfg_i, const float * cfg_f,
+                          ref_velocity_fn fn, void * user, void * out, float * traj_xt,
+                          float * traj_x0, char * err, int errlen) {
+    pixal3d::FlowEulerSamplerConfig c;
+    c.steps = cfg_i[0];
+    c.record_trajectory = cfg_i[1] != 0;
+    c.sigma_min = cfg_f[0];
+    c.rescale_t = cfg_f[1];
+    c.guidance_strength = cfg_f[2];
+    c.guidance_rescale = cfg_f[3];
+    c.guidance_interval_min = cfg_f[4];
+    c.guidance_interval_max = cfg_f[5];
+    pixal3d::FlowVelocityFn model;
+    if (fn) {
+        model = [fn, user](const SparseTensorF32 & state, float t, bool cond,
+                           SparseTensorF32 & velocity, std::string * error) {
+            velocity = state;
+            if (!fn(state.feats.data(), static_cast<int64_t>(state.points()), state.channels, t,
+                    cond ? 1 : 0, velocity.feats.data(), user)) {
+                if (error) *error = "velocity callback failed";
+                return false;
+            }
+            return true;
+        };
+    }
+    pixal3d::FlowEulerSampleF32 result;
+    std::string e;
+    const bool ok = pixal3d::flow_euler_sample_f32(*as_sparse(noise), c, model, result, &e);
+    if (ok) {
+        *as_sparse(out) = result.samples;
+        const size_t count = result.samples.feats.size();
+        for (size_t i = 0; traj_xt && i < result.pred_x_t.size(); ++i)
+            std::memcpy(traj_xt + i * count, result.pred_x_t[i].feats.data(), count * sizeof(float));
+        for (size_t i = 0; traj_x0 && i < result.pred_x_0.size(); ++i)
+            std::memcpy(traj_x0 + i * count, result.pred_x_0[i].feats.data(), count * sizeof(float));
+    }
+    return finish(ok, e, err, errlen);
 }
 
 #ifndef PXS_DROPIN_SHIM

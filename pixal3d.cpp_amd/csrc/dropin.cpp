@@ -14,6 +14,7 @@
 // grow-only device buffers that later calls on that thread reuse; nothing is
 // shared between threads, so calls are reentrant like the reference's.
 
+#include "pixal3d/flow_sampler.h"
 #include "pixal3d/sparse.h"
 #include "pixal3d/sparse_transformer.h"
 #include "pxs.h"
@@ -23,7 +24,9 @@
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
+#include <iostream>
 #include <limits>
 #include <string>
 #include <vector>
@@ -40,7 +43,8 @@ void set_error(std::string * error, const std::string & message) {
 enum Slot {
     kInCoords, kInFeats, kTable, kStatus, kNbr, kMasks, kWeight, kBias, kOut, kOutCoords,
     kWork, kAuxCoords, kAuxFeats, kAux2Feats, kCuQ, kCuK, kOffsets, kRows, kGamma, kBeta,
-    kCount, kSlotCount
+    kCount, kFlowState, kFlowPos, kFlowNeg, kFlowPred, kFlowX0, kFlowCu, kFlowWork,
+    kSlotCount
 };
 
 class Device {
@@ -1035,6 +1039,282 @@ bool sparse_transformer_cross_block_f32(const SparseTensorF32 & input,
     result.feats.resize(input.feats.size());
     if (!download(result.feats.data(), hidden, result.feats.size(), error)) return false;
     output = std::move(result);
+    return true;
+}
+
+// ---- flow Euler sampler (src/flow_sampler.cpp) ------------------------------
+//
+// The reference control flow, error checks and messages, with the model as a
+// host callback; the blend, CFG rescale, x0 and Euler update run on the
+// device (pxs_flow_guidance and friends), so the state is uploaded once,
+// updated in HBM, and copied back each step for the next callback.
+
+namespace {
+
+// PIXAL3D_FLOW_NONFINITE_TRACE diagnostics (src/flow_sampler.cpp:20-83):
+// host statistics of a host tensor, printed to stderr, failing on a
+// non-finite value.
+bool flow_diagnostics_enabled() {
+    const char * value = std::getenv("PIXAL3D_FLOW_NONFINITE_TRACE");
+    return value && *value && std::string(value) != "0";
+}
+
+bool trace_features(const SparseTensorF32 & tensor, const char * label, const char * branch,
+                    int step, float timestep, std::string * error) {
+    std::size_t nonfinite = 0, first_bad = 0;
+    float first_value = 0.0f;
+    float lo = std::numeric_limits<float>::infinity();
+    float hi = -std::numeric_limits<float>::infinity();
+    float max_abs = 0.0f;
+    long double sum = 0.0L;
+    for (std::size_t i = 0; i < tensor.feats.size(); ++i) {
+        const float v = tensor.feats[i];
+        if (!std::isfinite(v)) {
+            if (nonfinite == 0) {
+                first_bad = i;
+                first_value = v;
+            }
+            ++nonfinite;
+            continue;
+        }
+        lo = std::min(lo, v);
+        hi = std::max(hi, v);
+        max_abs = std::max(max_abs, std::fabs(v));
+        sum += static_cast<long double>(v);
+    }
+    const double mean = tensor.feats.empty()
+                            ? 0.0
+                            : static_cast<double>(sum / static_cast<long double>(tensor.feats.size()));
+    const char * lab = label && *label ? label : "features";
+    const char * br = branch && *branch ? branch : "unknown";
+    std::cerr << "pixal3d: flow trace step=" << step << " timestep=" << timestep << " branch=" << br
+              << " tensor=" << lab << " points=" << tensor.points()
+              << " values=" << tensor.feats.size() << " min=" << (tensor.feats.empty() ? 0.0f : lo)
+              << " max=" << (tensor.feats.empty() ? 0.0f : hi) << " max_abs=" << max_abs
+              << " mean=" << mean << " nonfinite=" << nonfinite;
+    if (nonfinite != 0) std::cerr << " first_bad_index=" << first_bad << " first_bad_value=" << first_value;
+    std::cerr << std::endl;
+    if (nonfinite != 0) {
+        set_error(error, std::string("flow ") + lab + " contains non-finite values at step " +
+                             std::to_string(step) + " (branch=" + br +
+                             ", first index=" + std::to_string(first_bad) + ")");
+        return false;
+    }
+    return true;
+}
+
+bool same_shape(const SparseTensorF32 & a, const SparseTensorF32 & b) {
+    return a.batch_size == b.batch_size && a.channels == b.channels &&
+           a.spatial_x == b.spatial_x && a.spatial_y == b.spatial_y &&
+           a.spatial_z == b.spatial_z && a.coords == b.coords && a.feats.size() == b.feats.size();
+}
+
+void clear_for_callback(SparseTensorF32 & t) {
+    t.batch_size = t.channels = t.spatial_x = t.spatial_y = t.spatial_z = 0;
+    t.coords.clear();
+    t.feats.clear();
+}
+
+bool check_model_output(const SparseTensorF32 & state, const SparseTensorF32 & velocity,
+                        std::string * error) {
+    if (!velocity.valid(error)) return false;
+    if (!same_shape(state, velocity)) {
+        set_error(error, "flow model velocity shape or coordinates changed during sampling");
+        return false;
+    }
+    return true;
+}
+
+pxs_flow_sampler_config sampler_config(const FlowEulerSamplerConfig & c) {
+    pxs_flow_sampler_config s{};
+    s.steps = c.steps;
+    s.sigma_min = c.sigma_min;
+    s.rescale_t = c.rescale_t;
+    s.guidance_strength = c.guidance_strength;
+    s.guidance_rescale = c.guidance_rescale;
+    s.guidance_interval_min = c.guidance_interval_min;
+    s.guidance_interval_max = c.guidance_interval_max;
+    return s;
+}
+
+// The first failing check of sparse_batch_std's input on an x0 computed in
+// HBM (src/flow_sampler.cpp:162-182): finiteness (SparseTensorF32::valid;
+// the coordinates are the state's, already valid), then a point per item.
+bool x0_checks(const float * state, const float * pred, int64_t count, float t, float sigma_min,
+               int64_t rows, int channels, bool empty_item, std::string * error) {
+    Device & d = device();
+    float * x0 = scratch<float>(kFlowX0, static_cast<std::size_t>(count), error);
+    int64_t * status = scratch<int64_t>(kStatus, 1, error);
+    if (!x0 || !status) return false;
+    if (!pxs_ok(pxs_flow_pred_to_xstart(state, pred, count, t, sigma_min, x0, d.stream()), error) ||
+        !pxs_ok(pxs_status_reset(status, d.stream()), error) ||
+        !pxs_ok(pxs_check_finite(PXS_F32, x0, rows, channels, channels, status, d.stream()), error)) {
+        return false;
+    }
+    int64_t host_status = 0;
+    if (!download(&host_status, status, 1, error)) return false;
+    if (host_status != std::numeric_limits<int64_t>::max()) {
+        set_error(error, "sparse features contain a non-finite value");
+        return false;
+    }
+    if (empty_item) {
+        set_error(error, "flow CFG rescale requires at least one point per batch");
+        return false;
+    }
+    return true;
+}
+
+} // namespace
+
+bool flow_euler_sample_f32(const SparseTensorF32 & noise, const FlowEulerSamplerConfig & config,
+                           const FlowVelocityFn & model, FlowEulerSampleF32 & output,
+                           std::string * error) {
+    output = FlowEulerSampleF32{};
+    if (!noise.valid(error)) return false;
+    const pxs_flow_sampler_config scfg = sampler_config(config);
+    {
+        float t0 = 0.0f, t1 = 0.0f, g = 0.0f;
+        // Configuration checks of valid_config (src/flow_sampler.cpp:111-124).
+        if (pxs_flow_sampler_schedule(&scfg, 0, &t0, &t1, &g) != PXS_OK &&
+            std::string(pxs_last_error()) == "invalid flow Euler sampler configuration") {
+            set_error(error, "invalid flow Euler sampler configuration");
+            return false;
+        }
+    }
+    if (!model) {
+        set_error(error, "flow Euler sampler model callback is empty");
+        return false;
+    }
+    SparseTensorF32 state = noise;
+    const bool diagnostics = flow_diagnostics_enabled();
+    if (diagnostics && !trace_features(state, "state_before", "initial", -1, 1.0f, error)) return false;
+    if (config.record_trajectory) {
+        output.pred_x_t.reserve(static_cast<std::size_t>(config.steps));
+        output.pred_x_0.reserve(static_cast<std::size_t>(config.steps));
+    }
+    Device & d = device();
+    if (!d.ready(error)) return false;
+    const int64_t rows = static_cast<int64_t>(state.points());
+    const int channels = state.channels;
+    const int64_t count = rows * channels;
+    const std::size_t ucount = static_cast<std::size_t>(count);
+    float * dstate = upload(kFlowState, state.feats.data(), ucount, error);
+    if (!dstate) return false;
+    const std::vector<int64_t> cu = batch_bounds(state);
+    bool empty_item = false;
+    for (int b = 0; b < state.batch_size; ++b) empty_item |= cu[b + 1] == cu[b];
+    SparseTensorF32 prediction, positive, negative;
+    for (int step = 0; step < config.steps; ++step) {
+        float t = 0.0f, t_next = 0.0f, guidance = 1.0f;
+        if (pxs_flow_sampler_schedule(&scfg, step, &t, &t_next, &guidance) != PXS_OK) {
+            set_error(error, pxs_last_error());
+            return false;
+        }
+        const float * dpred = nullptr;
+        clear_for_callback(prediction);
+        if (guidance == 1.0f || guidance == 0.0f) {
+            const bool cond = guidance == 1.0f;
+            if (!model(state, 1000.0f * t, cond, prediction, error) ||
+                !check_model_output(state, prediction, error)) {
+                return false;
+            }
+            if (diagnostics && !trace_features(prediction, "prediction",
+                                               cond ? "conditional" : "unconditional", step, t,
+                                               error)) {
+                return false;
+            }
+            dpred = upload(kFlowPred, prediction.feats.data(), ucount, error);
+            if (!dpred) return false;
+        } else {
+            clear_for_callback(positive);
+            clear_for_callback(negative);
+            if (!model(state, 1000.0f * t, true, positive, error) ||
+                !check_model_output(state, positive, error)) {
+                return false;
+            }
+            if (diagnostics && !trace_features(positive, "prediction", "conditional", step, t, error))
+                return false;
+            if (!model(state, 1000.0f * t, false, negative, error) ||
+                !check_model_output(state, negative, error)) {
+                return false;
+            }
+            if (diagnostics && !trace_features(negative, "prediction", "unconditional", step, t, error))
+                return false;
+            const float * dpos = upload(kFlowPos, positive.feats.data(), ucount, error);
+            const float * dneg = upload(kFlowNeg, negative.feats.data(), ucount, error);
+            float * dout = scratch<float>(kFlowPred, ucount, error);
+            if (!dpos || !dneg || !dout) return false;
+            if (!pxs_ok(pxs_flow_guidance(dstate, dpos, dneg, nullptr, nullptr, rows, channels,
+                                          state.batch_size, t, config.sigma_min, guidance, 0.0f,
+                                          dout, nullptr, d.stream()),
+                        error)) {
+                return false;
+            }
+            dpred = dout;
+            if (diagnostics) {
+                SparseTensorF32 blend = positive;
+                if (!download(blend.feats.data(), dout, ucount, error) ||
+                    !trace_features(blend, "cfg_blend", "guided", step, t, error)) {
+                    return false;
+                }
+            }
+            if (config.guidance_rescale > 0.0f) {
+                if (!x0_checks(dstate, dpos, count, t, config.sigma_min, rows, channels, empty_item,
+                               error) ||
+                    !x0_checks(dstate, dout, count, t, config.sigma_min, rows, channels, empty_item,
+                               error)) {
+                    return false;
+                }
+                const int64_t * dcu = upload(kFlowCu, cu.data(), cu.size(), error);
+                void * ws = device().buffer(kFlowWork,
+                                            pxs_flow_guidance_workspace_bytes(state.batch_size),
+                                            error);
+                if (!dcu || !ws) return false;
+                const int32_t * dcoords = upload(kInCoords, state.coords.data(), state.coords.size(),
+                                                 error);
+                if (!dcoords) return false;
+                if (!pxs_ok(pxs_flow_guidance(dstate, dpos, dneg, dcoords, dcu, rows, channels,
+                                              state.batch_size, t, config.sigma_min, guidance,
+                                              config.guidance_rescale, dout, ws, d.stream()),
+                            error)) {
+                    return false;
+                }
+                if (diagnostics) {
+                    SparseTensorF32 rescaled = positive;
+                    if (!download(rescaled.feats.data(), dout, ucount, error) ||
+                        !trace_features(rescaled, "guidance_rescale", "guided", step, t, error)) {
+                        return false;
+                    }
+                }
+            }
+        }
+        SparseTensorF32 x0;
+        if (config.record_trajectory) {
+            float * dx0 = scratch<float>(kFlowX0, ucount, error);
+            if (!dx0 ||
+                !pxs_ok(pxs_flow_pred_to_xstart(dstate, dpred, count, t, config.sigma_min, dx0,
+                                                d.stream()),
+                        error)) {
+                return false;
+            }
+            copy_shape(state, channels, x0);
+            x0.feats.resize(ucount);
+            if (!download(x0.feats.data(), dx0, ucount, error)) return false;
+            if (diagnostics && !trace_features(x0, "x0", "guided", step, t, error)) return false;
+        }
+        const float delta = t - t_next;
+        if (!pxs_ok(pxs_flow_euler_update(dstate, dpred, count, delta, d.stream()), error) ||
+            !download(state.feats.data(), dstate, ucount, error)) {
+            return false;
+        }
+        if (diagnostics && !trace_features(state, "state_after", "euler", step, t_next, error))
+            return false;
+        if (config.record_trajectory) {
+            output.pred_x_t.push_back(state);
+            output.pred_x_0.push_back(std::move(x0));
+        }
+    }
+    output.samples = std::move(state);
     return true;
 }
 

@@ -321,10 +321,16 @@ __device__ __forceinline__ int64_t coarse_cell(int4 c, int f, int cx, int cy, in
 // neighbours along z) are merged inside the wavefront first: one atomic per
 // distinct word instead of one per row.  Sorted input gives a handful of
 // words per wavefront.
+// It also sets clear[k * n + p] = value for k < clear_rows (the child map or
+// the group counts the next kernels fill in), saving a fill launch.
 __global__ void coarse_mark_kernel(const int4 * __restrict__ coords, int64_t n, int f, int cx,
-                                   int cy, int cz, uint32_t * __restrict__ bitmap) {
+                                   int cy, int cz, uint32_t * __restrict__ bitmap,
+                                   int32_t * __restrict__ clear, int clear_rows, int32_t value) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const bool live = p < n;
+    if (live) {
+        for (int k = 0; k < clear_rows; ++k) clear[k * n + p] = value;
+    }
     int64_t word = -1;
     uint32_t bit = 0;
     if (live) {
@@ -783,10 +789,9 @@ int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size
     const CoarseGrid g = coarse_grid(workspace, batch_size, sx, sy, sz, 2);
     int rc = fill_u32(g.bitmap, g.words, 0u, s);
     if (rc) return rc;
-    rc = fill_i32(child_map, 8 * n, -1, s);
-    if (rc) return rc;
     hipLaunchKernelGGL(coarse_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
-                       reinterpret_cast<const int4 *>(coords), n, 2, g.cx, g.cy, g.cz, g.bitmap);
+                       reinterpret_cast<const int4 *>(coords), n, 2, g.cx, g.cy, g.cz, g.bitmap,
+                       child_map, 8, -1);
     rc = exclusive_scan_popcount(g.bitmap, g.prefix, g.words, m_out, g.rest, s);
     if (rc) return rc;
     hipLaunchKernelGGL(coarse_emit_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
@@ -821,10 +826,8 @@ int pxs_downsample_topology(const int32_t * coords, int64_t n, int batch_size, i
     const int4 * c4 = reinterpret_cast<const int4 *>(coords);
     int rc = fill_u32(g.bitmap, g.words, 0u, s);
     if (rc) return rc;
-    rc = fill_i32(counts, n, 0, s);
-    if (rc) return rc;
     hipLaunchKernelGGL(coarse_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
-                       n, factor, g.cx, g.cy, g.cz, g.bitmap);
+                       n, factor, g.cx, g.cy, g.cz, g.bitmap, counts, 1, 0);
     rc = exclusive_scan_popcount(g.bitmap, g.prefix, g.words, m_out, scan_ws, s);
     if (rc) return rc;
     hipLaunchKernelGGL(group_assign_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,

@@ -63,6 +63,15 @@ _SIGS = {
     "pxs_transformer_block": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                                      _i64, _vp, _vp, _vp]),
     "pxs_slat_flow_workspace_bytes": (C.c_size_t, [_i32, _vp, _i64, _i64, _i32]),
+    "pxs_flow_sampler_schedule": (_i32, [_vp, _i32, _vp, _vp, _vp]),
+    "pxs_flow_guidance_workspace_bytes": (C.c_size_t, [_i32]),
+    "pxs_flow_guidance": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _f, _f, _f, _f, _vp,
+                                 _vp, _vp]),
+    "pxs_flow_pred_to_xstart": (_i32, [_vp, _vp, _i64, _f, _f, _vp, _vp]),
+    "pxs_flow_euler_update": (_i32, [_vp, _vp, _i64, _f, _vp]),
+    "pxs_flow_euler_sample_workspace_bytes": (C.c_size_t, [_i32, _vp, _i64, _i64, _i64, _i32]),
+    "pxs_flow_euler_sample": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp,
+                                     _i64, _vp, _vp, _i64, _vp, _vp, _vp]),
     "pxs_slat_flow_forward": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                                      _i64, _vp, _vp, _vp, _vp]),
     "pxs_linear": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp]),
@@ -122,6 +131,13 @@ class FlowConfig(C.Structure):
                 ("rope_freq_min", C.c_float), ("rope_freq_base", C.c_float),
                 ("qk_rms_norm", C.c_int), ("qk_rms_norm_cross", C.c_int),
                 ("use_projection", C.c_int)]
+
+
+class SamplerConfig(C.Structure):
+    """pxs_flow_sampler_config (FlowEulerSamplerConfig without the trajectory flag)."""
+    _fields_ = [("steps", C.c_int), ("sigma_min", C.c_float), ("rescale_t", C.c_float),
+                ("guidance_strength", C.c_float), ("guidance_rescale", C.c_float),
+                ("guidance_interval_min", C.c_float), ("guidance_interval_max", C.c_float)]
 
 
 class FlowWeights(C.Structure):
@@ -535,6 +551,54 @@ class Pxs:
         self._check(self.lib.pxs_add_repeat(_dtype_code(a), _ptr(a), rows, ch, _ptr(skip),
                                             skip.shape[1], _ptr(y), self.stream()),
                     "pxs_add_repeat")
+        return y
+
+    # -- flow Euler sampler -----------------------------------------------------
+    def flow_sampler_schedule(self, scfg: SamplerConfig, step):
+        """-> (t, t_next, guidance) of one step (host computation)."""
+        t, tn, g = C.c_float(), C.c_float(), C.c_float()
+        self._check(self.lib.pxs_flow_sampler_schedule(C.byref(scfg), step, C.byref(t),
+                                                       C.byref(tn), C.byref(g)),
+                    "pxs_flow_sampler_schedule")
+        return t.value, tn.value, g.value
+
+    def flow_guidance(self, state, positive, negative, coords, cu, batch_size, t, sigma_min,
+                      guidance, rescale, out=None):
+        rows, ch = state.shape
+        y = torch.empty_like(state) if out is None else out
+        ws = self._ws(self.lib.pxs_flow_guidance_workspace_bytes(batch_size), state.device)
+        self._check(self.lib.pxs_flow_guidance(_ptr(state), _ptr(positive), _ptr(negative),
+                                               _ptr(coords), _ptr(cu), rows, ch, batch_size, t,
+                                               sigma_min, guidance, rescale, _ptr(y), _ptr(ws),
+                                               self.stream()), "pxs_flow_guidance")
+        return y
+
+    def flow_pred_to_xstart(self, state, prediction, t, sigma_min):
+        y = torch.empty_like(state)
+        self._check(self.lib.pxs_flow_pred_to_xstart(_ptr(state), _ptr(prediction), state.numel(),
+                                                     t, sigma_min, _ptr(y), self.stream()),
+                    "pxs_flow_pred_to_xstart")
+        return y
+
+    def flow_euler_update(self, state, prediction, delta):
+        """In place: state -= delta * prediction."""
+        self._check(self.lib.pxs_flow_euler_update(_ptr(state), _ptr(prediction), state.numel(),
+                                                   delta, self.stream()), "pxs_flow_euler_update")
+        return state
+
+    def flow_euler_sample(self, cfg: FlowConfig, weights: FlowWeights, scfg: SamplerConfig, coords,
+                          batch_size, cu, noise, cond, cond_offsets, uncond, uncond_offsets,
+                          dtype=None, out=None):
+        dtype = _dtype_code(cond) if dtype is None else dtype
+        rows = coords.shape[0]
+        y = torch.empty_like(noise) if out is None else out
+        ws = self._ws(self.lib.pxs_flow_euler_sample_workspace_bytes(
+            dtype, C.byref(cfg), rows, cond.shape[0], uncond.shape[0], batch_size), noise.device)
+        self._check(self.lib.pxs_flow_euler_sample(
+            dtype, C.byref(cfg), C.byref(weights), C.byref(scfg), _ptr(coords), rows, batch_size,
+            _ptr(cu), _ptr(noise), _ptr(cond), _ptr(cond_offsets), cond.shape[0], _ptr(uncond),
+            _ptr(uncond_offsets), uncond.shape[0], _ptr(y), _ptr(ws), self.stream()),
+            "pxs_flow_euler_sample")
         return y
 
     def flow_workspace_bytes(self, cfg: FlowConfig, rows, tokens, batch_size, dtype):

@@ -111,3 +111,24 @@ def flow_case(seed, n_items, grid, C, H, nblocks, ctx_tokens, in_ch=8, out_ch=8,
     dims = [in_ch, C, out_ch, nblocks, H, M, CC, 1, 1]
     return dict(coords=coords, x=x, t=t, ctx=ctx, ctx_off=ctx_off, fw=fw, blocks=blocks,
                 dims=dims, C=C, H=H, M=M, CC=CC, n=n)
+
+
+def flow_velocity(coords, channels, seed=5):
+    """A deterministic stand-in for the flow model (numpy float32): the
+    velocity of state s at model time T for condition c is
+    tanh(s * a_c) * (T / 1000 + 0.5) + m_c[item] + 0.01 * x-coordinate,
+    with different a_c, m_c for the conditional and unconditional branch."""
+    coords = np.asarray(coords, np.int32).reshape(-1, 4)
+    items = coords[:, 0]
+    nb = int(items.max()) + 1 if items.size else 1
+    m = {True: W.normal(seed, nb * channels, 1, std=0.3).reshape(nb, channels),
+         False: W.normal(seed, nb * channels, 2, std=0.3).reshape(nb, channels)}
+    a = {True: np.float32(0.9), False: np.float32(-0.4)}
+    xo = (np.float32(0.01) * coords[:, 1].astype(np.float32))[:, None]
+
+    def fn(state, t_model, conditional):
+        s = np.asarray(state, np.float32)
+        scale = np.float32(t_model) / np.float32(1000.0) + np.float32(0.5)
+        return (np.tanh(s * a[conditional]) * scale + m[conditional][items] + xo).astype(np.float32)
+
+    return fn

@@ -412,3 +412,77 @@ def test_flow_composes_reference_primitives(orc):
     got = orc.slat_flow_forward(case["coords"], B, case["x"], case["t"], case["ctx"],
                                 case["ctx_off"], case["dims"], [1e-6, 1.0, 10000.0], fw, blocks)
     assert np.max(np.abs(got - expect)) <= 1e-6 * np.max(np.abs(expect))
+
+
+# --- flow Euler sampler (src/flow_sampler.cpp) -------------------------------------
+
+SAMPLER_CASES = {
+    # name: (steps, [sigma_min, rescale_t, strength, rescale, interval_min, interval_max])
+    "unguided": (6, [1e-5, 1.0, 1.0, 0.0, 0.0, 1.0]),
+    "guided": (5, [1e-5, 3.0, 3.0, 0.0, 0.0, 1.0]),
+    "guided_rescale_interval": (7, [1e-5, 3.0, 7.5, 0.7, 0.2, 0.8]),
+    "unconditional": (4, [1e-3, 1.0, 0.0, 0.0, 0.0, 1.0]),
+    "full_rescale": (3, [1e-5, 1.0, 4.0, 1.0, 0.0, 1.0]),
+}
+
+
+def sampler_inputs(seed=61):
+    from fixtures import flow_velocity
+    coords = W.shell_coords(12, [[(3.0, 4.5)], [(2.5, 4.0)]], seed)
+    noise = W.normal(seed, coords.shape[0] * 8, 1).reshape(-1, 8)
+    return coords, noise, flow_velocity(coords, 8, seed)
+
+
+@pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref is built only where /root/reference exists")
+@pytest.mark.parametrize("case", list(SAMPLER_CASES))
+def test_flow_sampler_matches_compiled_reference(orc, case):
+    """orc_flow_euler_sample against the reference's flow_euler_sample_f32
+    compiled from src/flow_sampler.cpp, both driven by the same velocity
+    callback: samples and both trajectories bit for bit."""
+    steps, cfg = SAMPLER_CASES[case]
+    coords, noise, fn = sampler_inputs()
+    ref = O.Reference()
+    out, rxt, rx0 = ref.flow_euler_sample(ref.sparse(coords, noise, 2, (12, 12, 12)), steps, cfg,
+                                          fn, record=True)
+    got, xt, x0 = orc.flow_euler_sample(coords, 2, noise, steps, cfg, fn, record=True)
+    np.testing.assert_array_equal(got, out.read()[1])
+    np.testing.assert_array_equal(xt, rxt)
+    np.testing.assert_array_equal(x0, rx0)
+
+
+@pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref is built only where /root/reference exists")
+def test_flow_sampler_errors_match_compiled_reference(orc):
+    coords, noise, fn = sampler_inputs()
+    ref = O.Reference()
+    t = ref.sparse(coords, noise, 2, (12, 12, 12))
+    for steps, cfg, msg in [
+            (0, [1e-5, 1.0, 1.0, 0.0, 0.0, 1.0], "invalid flow Euler sampler configuration"),
+            (3, [1e-5, 1.0, 1.0, -0.5, 0.0, 1.0], "invalid flow Euler sampler configuration"),
+            (3, [1e-5, 1.0, 1.0, 0.0, 0.9, 0.1], "invalid flow Euler sampler configuration"),
+            (3, [1.0, 1.0, 1.0, 0.0, 0.0, 1.0], "invalid flow Euler sampler configuration")]:
+        with pytest.raises(O.ReferenceError, match=msg):
+            ref.flow_euler_sample(t, steps, cfg, fn)
+        assert orc.flow_schedule(steps, cfg, 0)[0] == 1
+    with pytest.raises(O.ReferenceError, match="model callback is empty"):
+        ref.flow_euler_sample(t, 3, [1e-5, 1.0, 1.0, 0.0, 0.0, 1.0], None)
+
+
+def test_flow_sampler_closed_forms(orc):
+    """Zero velocity keeps the noise; a constant velocity v moves the state by
+    sum(t_i - t_{i+1}) v = (1 - 0) v; a unit guidance interval that excludes
+    every step runs the conditional branch only."""
+    coords, noise, fn = sampler_inputs()
+    zero = lambda s, t, c: np.zeros_like(s)  # noqa: E731
+    got, _, _ = orc.flow_euler_sample(coords, 2, noise, 5, [1e-5, 2.0, 3.0, 0.5, 0.0, 1.0], zero)
+    np.testing.assert_array_equal(got, noise)
+    v = W.normal(62, noise.size, 1).reshape(noise.shape)
+    const = lambda s, t, c: v  # noqa: E731
+    got, _, _ = orc.flow_euler_sample(coords, 2, noise, 8, [1e-5, 1.0, 1.0, 0.0, 0.0, 1.0], const)
+    np.testing.assert_allclose(got, noise - v, rtol=0, atol=1e-5)
+    a, _, _ = orc.flow_euler_sample(coords, 2, noise, 4, [1e-5, 1.0, 5.0, 0.7, 2.0, 3.0], fn)
+    b, _, _ = orc.flow_euler_sample(coords, 2, noise, 4, [1e-5, 1.0, 1.0, 0.0, 0.0, 1.0], fn)
+    np.testing.assert_array_equal(a, b)
+    # Schedule with rescale_t = 1: t_i = 1 - i / steps.
+    for i in range(4):
+        rc, t, tn, g = orc.flow_schedule(4, [1e-5, 1.0, 2.0, 0.0, 0.0, 1.0], i)
+        assert rc == 0 and t == np.float32(1.0) - np.float32(i) / np.float32(4.0) and g == 2.0
