@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="unet_stage_128",
                     choices=["unet_stage_128", "conv_fp32_64", "attn_block", "swin_64",
-                             "flow_step"])
+                             "flow_step", "flow_sample"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     return ap.parse_args()
@@ -477,9 +477,9 @@ def swin_64(args, torch, px, W):
                          "frac": round(up_tf / PEAK_BF16_TFLOPS, 4), "traffic": None}}
 
 
-def flow_step(args, torch, px, W):
-    """Config 5: one SLat-flow forward (24 blocks, width 1024) on ~42k voxels,
-    device resident (pxs_slat_flow_forward), random N(0, 0.02) weights."""
+def flow_model(torch, px, W):
+    """Config 5's SLat-flow model (24 blocks, width 1024, 16 x 64, MLP 4096) on
+    ~42k voxels at 64^3 with random N(0, 0.02) weights, bf16 GEMM operands."""
     import pxs as P
 
     dev = torch.device("cuda:0")
@@ -505,23 +505,36 @@ def flow_step(args, torch, px, W):
     arr = (P.BlockWeights * nb)(*blocks)
     weights = P.FlowWeights(*[t.data_ptr() for t in fw], arr)
     cfg = P.FlowConfig(8, 8, C, C, nb, H, 0, M, 1e-6, 1.0, 10000.0, 1, 1, 0)
-    x = torch.randn(n, 8, generator=g, device=dev)
-    tsteps = torch.rand(1, generator=g, device=dev) * 1000.0
     ctx = torch.randn(T, C, generator=g, device=dev).to(torch.bfloat16)
     ctx_off = torch.tensor([0, T], dtype=torch.int64, device=dev)
     cu = px.batch_cu_seqlens(coords, 1)
-    out = torch.empty((n, 8), dtype=torch.float32, device=dev)
-    ws = torch.empty(px.flow_workspace_bytes(cfg, n, T, 1, P.PXS_BF16), dtype=torch.uint8, device=dev)
-
-    def step():
-        px.slat_flow_forward(cfg, weights, coords, 1, cu, x, tsteps, ctx, ctx_off, out=out,
-                             workspace=ws, dtype=P.PXS_BF16)
-
-    dt = timed_steps(args, torch, step)
     f_self = 4.0 * n * n * 64 * H
     f_lin = 2.0 * n * C * (3 * C + C + C + C + 2 * M)
     f_cross = 4.0 * n * T * 64 * H + 2.0 * T * C * 2 * C
     flops = nb * (f_self + f_lin + f_cross) + 2.0 * n * (8 * C + C * 8)
+    return dict(cfg=cfg, weights=weights, keep=(keep, fw, arr), coords=coords, cu=cu, ctx=ctx,
+                ctx_off=ctx_off, n=n, T=T, flops=flops, g=g, dev=dev)
+
+
+def flow_step(args, torch, px, W):
+    """Config 5: one SLat-flow forward (24 blocks, width 1024) on ~42k voxels,
+    device resident (pxs_slat_flow_forward), random N(0, 0.02) weights."""
+    import pxs as P
+
+    m = flow_model(torch, px, W)
+    n, T, dev, g = m["n"], m["T"], m["dev"], m["g"]
+    x = torch.randn(n, 8, generator=g, device=dev)
+    tsteps = torch.rand(1, generator=g, device=dev) * 1000.0
+    out = torch.empty((n, 8), dtype=torch.float32, device=dev)
+    ws = torch.empty(px.flow_workspace_bytes(m["cfg"], n, T, 1, P.PXS_BF16), dtype=torch.uint8,
+                     device=dev)
+
+    def step():
+        px.slat_flow_forward(m["cfg"], m["weights"], m["coords"], 1, m["cu"], x, tsteps, m["ctx"],
+                             m["ctx_off"], out=out, workspace=ws, dtype=P.PXS_BF16)
+
+    dt = timed_steps(args, torch, step)
+    flops = m["flops"]
     assert torch.isfinite(out).all().item()
     return {"metric": "SLat-flow step TFLOP/s, bf16", "value": round(flops / dt / 1e12, 2),
             "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "bf16",
@@ -533,7 +546,61 @@ def flow_step(args, torch, px, W):
                          "frac": round(flops / dt / 1e12 / PEAK_BF16_TFLOPS, 4), "traffic": None}}
 
 
+def flow_sample(args, torch, px, W):
+    """Guided flow-Euler sampling with config 5's model (pxs_flow_euler_sample):
+    2 Euler steps at guidance 7.5 with CFG rescale 0.7, each step ONE forward
+    over the doubled batch (conditional + unconditional, ~84k tokens); the same
+    steps composed from two separate forwards are timed beside it."""
+    import pxs as P
+
+    m = flow_model(torch, px, W)
+    n, T, dev, g = m["n"], m["T"], m["dev"], m["g"]
+    noise = torch.randn(n, 8, generator=g, device=dev)
+    uncond = torch.zeros_like(m["ctx"])
+    out = torch.empty_like(noise)
+    steps = 2
+    scfg = P.SamplerConfig(steps, 1e-5, 3.0, 7.5, 0.7, 0.0, 1.0)
+
+    def sample():
+        px.flow_euler_sample(m["cfg"], m["weights"], scfg, m["coords"], 1, m["cu"], noise, m["ctx"],
+                             m["ctx_off"], uncond, m["ctx_off"], dtype=P.PXS_BF16, out=out)
+
+    state = torch.empty_like(noise)
+    ws = torch.empty(px.flow_workspace_bytes(m["cfg"], n, T, 1, P.PXS_BF16), dtype=torch.uint8,
+                     device=dev)
+    sched = [px.flow_sampler_schedule(scfg, i) for i in range(steps)]
+    tts = [torch.full((1,), 1000.0 * t, device=dev) for t, _, _ in sched]
+
+    def separate():
+        state.copy_(noise)
+        for (t, tn, gd), tt in zip(sched, tts):
+            pos = px.slat_flow_forward(m["cfg"], m["weights"], m["coords"], 1, m["cu"], state, tt,
+                                       m["ctx"], m["ctx_off"], workspace=ws, dtype=P.PXS_BF16)
+            neg = px.slat_flow_forward(m["cfg"], m["weights"], m["coords"], 1, m["cu"], state, tt,
+                                       uncond, m["ctx_off"], workspace=ws, dtype=P.PXS_BF16)
+            pred = px.flow_guidance(state, pos, neg, m["coords"], m["cu"], 1, t, 1e-5, gd, 0.7)
+            px.flow_euler_update(state, pred, t - tn)
+
+    dt = timed_steps(args, torch, sample)
+    dt_sep = timed_steps(args, torch, separate)
+    flops = 2 * steps * m["flops"]
+    assert torch.isfinite(out).all().item()
+    tf = flops / dt / 1e12
+    return {"metric": "SLat-flow guided sampling TFLOP/s, bf16", "value": round(tf, 2),
+            "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "bf16",
+            "config": {"workload": f"flow_sample: {n} voxels at 64^3, config-5 model, {steps} "
+                                   f"Euler steps, guidance 7.5, CFG rescale 0.7, 1,370 context "
+                                   f"tokens (uncond: zeros)",
+                       "ms_per_euler_step": round(dt * 1e3 / steps, 3),
+                       "separate_forwards_ms": round(dt_sep * 1e3, 4),
+                       "flop_per_call": flops},
+            "roofline": {"bound": "mfma", "kernel": "whole sampler", "achieved": round(tf, 2),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None}}
+
+
 OTHER_WORKLOADS = {"conv_fp32_64": conv_fp32_64, "attn_block": attn_block, "swin_64": swin_64,
+                   "flow_sample": flow_sample,
                    "flow_step": flow_step}
 
 
