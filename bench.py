@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="unet_stage_128",
                     choices=["unet_stage_128", "conv_fp32_64", "attn_block", "swin_64",
-                             "flow_step", "flow_sample"])
+                             "flow_step", "flow_sample", "decoder"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     return ap.parse_args()
@@ -599,8 +599,90 @@ def flow_sample(args, torch, px, W):
                          "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None}}
 
 
+def decoder(args, torch, px, W):
+    """The SLat shape-decoder stack on the device (pxs_slat_decoder_forward):
+    ~10.6k latent voxels at 64^3, 5 levels (1024 -> 64 channels), predicted
+    subdivisions up to 1024^3, bf16 convolution and MLP operands."""
+    import numpy as np
+
+    import pxs as P
+
+    dev = torch.device("cuda:0")
+    wl = W.decoder_64()
+    coords = torch.from_numpy(wl["coords"]).to(dev)
+    n = coords.shape[0]
+    chans, nblk = wl["model_channels"], wl["num_blocks"]
+    g = torch.Generator(device=dev).manual_seed(7)
+    rnd = lambda *s, std=0.02, dt=torch.float32: (torch.randn(*s, generator=g, device=dev) * std).to(dt)  # noqa: E731
+    keep, blocks = [], []
+    for level, C in enumerate(chans):
+        for _ in range(nblk[level]):
+            w = {"norm_weight": torch.ones(C, device=dev), "norm_bias": rnd(C),
+                 "conv1_weight": rnd(27, C, C, std=(27 * C) ** -0.5, dt=torch.bfloat16),
+                 "conv1_bias": rnd(C), "mlp0_weight": rnd(4 * C, C, std=C ** -0.5, dt=torch.bfloat16),
+                 "mlp0_bias": rnd(4 * C), "mlp2_weight": rnd(C, 4 * C, std=0.02, dt=torch.bfloat16),
+                 "mlp2_bias": rnd(C)}
+            keep.append(w)
+            blocks.append(P.DecoderBlock(P.PXS_DECODER_CONVNEXT, C, C, 4 * C,
+                                         P.decoder_block_weights(w)))
+        if level + 1 < len(chans):
+            O_ = chans[level + 1]
+            w = {"norm1_weight": torch.ones(C, device=dev), "norm1_bias": rnd(C),
+                 "conv1_weight": rnd(27, 8 * O_, C, std=(27 * C) ** -0.5, dt=torch.bfloat16),
+                 "conv1_bias": rnd(8 * O_),
+                 "conv2_weight": rnd(27, O_, O_, std=(27 * O_) ** -0.5, dt=torch.bfloat16),
+                 "conv2_bias": rnd(O_), "to_subdiv_weight": rnd(8, C, std=C ** -0.5),
+                 "to_subdiv_bias": rnd(8, std=0.0)}
+            keep.append(w)
+            blocks.append(P.DecoderBlock(P.PXS_DECODER_C2S, C, O_, 0, P.decoder_block_weights(w)))
+    cfg = P.decoder_config(wl["latent_channels"], wl["out_channels"], 1e-6, True, chans, nblk)
+    fl_w, fl_b = rnd(chans[0], wl["latent_channels"], std=0.2), rnd(chans[0])
+    out_w, out_b = rnd(wl["out_channels"], chans[-1], std=0.1), rnd(wl["out_channels"])
+    x = torch.randn(n, wl["latent_channels"], generator=g, device=dev)
+    # Capacity of every level: 8 x the largest pre-final level (about 4x
+    # growth per predicted level here); the call fails loudly past it.
+    max_rows = 8_000_000
+    res = {}
+
+    def step():
+        res["out"] = px.slat_decoder_forward(P.PXS_BF16, cfg, fl_w, fl_b, out_w, out_b, blocks,
+                                             coords, x, predict=False, max_rows=max_rows)
+
+    dt = timed_steps(args, torch, step)
+    oc, y, level_rows, _ = res["out"]
+    assert torch.isfinite(y).all().item()
+    # Algorithmic work: active conv pairs per level (from each level's map),
+    # ConvNeXt MLPs, C2S convolutions, output linear.
+    lvl_coords = [coords] + [px.slat_decoder_forward(P.PXS_BF16, cfg, fl_w, fl_b, out_w, out_b,
+                                                     blocks, coords, x, upsample_times=u,
+                                                     max_rows=max_rows)[0]
+                             for u in range(1, len(chans))]
+    macs = 0
+    for level, (c, C) in enumerate(zip(lvl_coords, chans)):
+        _, masks = px.neighbor_map(c)
+        pairs = int(np.unpackbits(masks.cpu().numpy().view(np.uint8)).sum())
+        macs += nblk[level] * (pairs * C * C + 2 * c.shape[0] * C * 4 * C)
+        if level + 1 < len(chans):
+            O_ = chans[level + 1]
+            _, m_next = px.neighbor_map(lvl_coords[level + 1])
+            pairs_next = int(np.unpackbits(m_next.cpu().numpy().view(np.uint8)).sum())
+            macs += pairs * C * 8 * O_ + pairs_next * O_ * O_
+    macs += n * wl["latent_channels"] * chans[0] + level_rows[-1] * chans[-1] * wl["out_channels"]
+    tf = 2.0 * macs / dt / 1e12
+    return {"metric": "SLat decoder stack TFLOP/s, bf16", "value": round(tf, 2), "unit": "TFLOP/s",
+            "ms_per_step": round(dt * 1e3, 4), "dtype": "bf16",
+            "config": {"workload": f"decoder: {n} latent voxels at 64^3, channels {chans}, "
+                                   f"one ConvNeXt block per level, predicted subdivisions",
+                       "level_rows": level_rows,
+                       "output_voxels_per_s": round(level_rows[-1] / dt, 1),
+                       "flop_per_step": 2.0 * macs},
+            "roofline": {"bound": "mfma", "kernel": "whole decoder", "achieved": round(tf, 2),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None}}
+
+
 OTHER_WORKLOADS = {"conv_fp32_64": conv_fp32_64, "attn_block": attn_block, "swin_64": swin_64,
-                   "flow_sample": flow_sample,
+                   "flow_sample": flow_sample, "decoder": decoder,
                    "flow_step": flow_step}
 
 

@@ -181,6 +181,14 @@ int pxs_channel_to_spatial(int dtype, const int32_t * coords, int64_t n, const v
 int pxs_linear(int dtype, const void * x, int64_t rows, int cin, const void * weight,
                const float * bias, int cout, int act, void * y, void * stream);
 
+/* fp32 sparse_linear in the reference's own operation order (bias, then
+ * inputs ascending, each product and sum rounded alone): bit-equal to
+ * src/sparse.cpp:436-446.  One thread per output value, so meant for few
+ * outputs where exact signs matter: the decoder's subdivision logits
+ * (to_subdiv, 8 outputs), whose sign decides the next level's topology. */
+int pxs_linear_ordered(const float * x, int64_t rows, int cin, const float * weight,
+                       const float * bias, int cout, float * y, void * stream);
+
 /* Linear whose epilogue applies the adaLN gate and the residual add of
  * src/sparse_transformer.cpp:229-235 (gate_in_place + add_in_place):
  * residual[r, o] += (block_mod[off + o] + time_mod[b(r) * 6 * cout + off + o])
@@ -529,6 +537,60 @@ int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const floa
                      const pxs_decoder_block_weights * w, int pred_subdiv,
                      const float * subdivision, float * predicted_subdiv, int32_t * out_coords,
                      float * y, int64_t * rows_out, void * workspace, void * stream);
+
+/* One entry of SLatDecoderWeightsF32::blocks (include/pixal3d/slat_decoder.h:
+ * 18-41): kind 0 = ConvNeXt, 1 = channel-to-spatial. */
+#define PXS_DECODER_CONVNEXT 0
+#define PXS_DECODER_C2S 1
+typedef struct pxs_decoder_block {
+    int kind;
+    int channels;
+    int out_channels;
+    int mlp_hidden;
+    pxs_decoder_block_weights w;
+} pxs_decoder_block;
+
+/* SLatDecoderConfig (include/pixal3d/slat_decoder.h:46-53); model_channels
+ * and num_blocks are host arrays of `levels` entries. */
+typedef struct pxs_decoder_config {
+    int latent_channels;
+    int out_channels;
+    float norm_eps;
+    int pred_subdiv;
+    int levels;
+    const int * model_channels;
+    const int * num_blocks;
+} pxs_decoder_config;
+
+/* slat_decoder_forward_f32 (src/slat_decoder.cpp:290-375) on the device:
+ * from_latent linear, then per level num_blocks[l] ConvNeXt blocks (sharing
+ * one neighbour map per level) and, except at the last level, the
+ * channel-to-spatial block that makes the next level's coordinates; final
+ * layer norm (eps 1e-5, no affine) and output linear.  blocks: host array of
+ * n_blocks entries in level order.  With upsample_times >= 0 the call is
+ * slat_decoder_upsample_coords_f32 (src/slat_decoder.cpp:377-440) instead: it
+ * stops after upsample_times C2S levels and returns that level's hidden
+ * state (y [m, model_channels[upsample_times]]) with its coordinates.
+ * guide (nullable): host array of levels - 1 device fp32 [rows_l, 8]
+ * subdivision guides; predicted (nullable, pred_subdiv only): host array of
+ * levels - 1 device fp32 buffers of max_rows x 8 that receive each C2S
+ * block's logits.  max_rows bounds every level: each C2S needs
+ * 8 * rows_l <= max_rows (rows * 8^(levels-1) always suffices).  *rows_out
+ * (host) receives the output rows m; level_rows (host, nullable) the rows of
+ * each level.  The call waits on the stream once per C2S level to read its
+ * row count. */
+size_t pxs_slat_decoder_workspace_bytes(int dtype, const pxs_decoder_config * cfg,
+                                        const pxs_decoder_block * blocks, int n_blocks,
+                                        int64_t rows, int64_t max_rows);
+int pxs_slat_decoder_forward(int dtype, const pxs_decoder_config * cfg,
+                             const float * from_latent_weight, const float * from_latent_bias,
+                             const float * output_weight, const float * output_bias,
+                             const pxs_decoder_block * blocks, int n_blocks,
+                             const int32_t * coords, int64_t rows, const float * x,
+                             const float * const * guide, float * const * predicted,
+                             int upsample_times, int64_t max_rows, int32_t * out_coords,
+                             float * y, int64_t * rows_out, int64_t * level_rows,
+                             void * workspace, void * stream);
 
 /* repeat_channels + add_in_place (src/slat_decoder.cpp:44-107):
  * y[r, j] = a[r, j] + skip[r, j / (channels / skip_channels)], y fp32; a in

@@ -11,6 +11,7 @@
 #include "carve.h"
 #include "pxs_common.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace pxs {
@@ -88,6 +89,50 @@ C2SBuffers carve_c2s(Carver & c, int dtype, int64_t rows, int channels, int out_
     b.c2s_ws = c.take(pxs_channel_to_spatial_workspace_bytes(rows, 2));
     b.map1 = carve_map(c, rows);
     b.map2 = carve_map(c, 8 * std::max<int64_t>(rows, 1));
+    return b;
+}
+
+struct DecoderBuffers {
+    float * hid[2];
+    int32_t * crd[2];
+    MapBuffers map;
+    void * block_ws;
+};
+
+int64_t grow8(int64_t n, int64_t cap) { return n > cap / 8 ? cap : 8 * n; }
+
+// Buffers sized for each level's capacity min(max_rows, rows * 8^l): two
+// hidden-state and two coordinate buffers (ping-pong across C2S levels), one
+// neighbour map, and the largest block workspace.  Blocks past n_blocks are
+// not sized (the forward rejects such a configuration).
+DecoderBuffers carve_decoder(Carver & c, int dtype, const pxs_decoder_config & cfg,
+                             const pxs_decoder_block * blocks, int n_blocks, int64_t rows,
+                             int64_t max_rows) {
+    size_t hid = 0, ws = 0;
+    int64_t cap = rows, cap_max = rows;
+    int bi = 0;
+    for (int l = 0; l < cfg.levels; ++l) {
+        if (l > 0) cap = grow8(cap, max_rows);
+        cap_max = std::max(cap_max, cap);
+        const int C = cfg.model_channels[l];
+        hid = std::max(hid, static_cast<size_t>(cap) * static_cast<size_t>(std::max(C, 1)));
+        for (int k = 0; k < cfg.num_blocks[l] && bi < n_blocks; ++k, ++bi)
+            ws = std::max(ws, pxs_convnext_block_workspace_bytes(dtype, cap, C, blocks[bi].mlp_hidden, 1));
+        if (l + 1 < cfg.levels && bi < n_blocks) {
+            ws = std::max(ws, pxs_resblock_c2s_workspace_bytes(dtype, cap, blocks[bi].channels,
+                                                              blocks[bi].out_channels));
+            ++bi;
+        }
+    }
+    hid = std::max(hid, static_cast<size_t>(std::max<int64_t>(rows, 1)) *
+                            static_cast<size_t>(std::max(cfg.latent_channels, 1)));
+    DecoderBuffers b{};
+    b.hid[0] = static_cast<float *>(c.take(hid * 4));
+    b.hid[1] = static_cast<float *>(c.take(hid * 4));
+    b.crd[0] = static_cast<int32_t *>(c.take(static_cast<size_t>(cap_max) * 16));
+    b.crd[1] = static_cast<int32_t *>(c.take(static_cast<size_t>(cap_max) * 16));
+    b.map = carve_map(c, cap_max);
+    b.block_ws = c.take(ws);
     return b;
 }
 
@@ -203,8 +248,9 @@ int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const floa
     const float * selected = subdivision;
     if (pred_subdiv) {
         float * pred = predicted_subdiv ? predicted_subdiv : b.pred;
-        PXS_TRY(pxs_linear(PXS_F32, x, rows, channels, w->to_subdiv_weight, w->to_subdiv_bias, 8,
-                           PXS_ACT_NONE, pred, stream));
+        // In sparse_linear's own order: a logit's sign picks the children.
+        PXS_TRY(pxs_linear_ordered(x, rows, channels, w->to_subdiv_weight, w->to_subdiv_bias, 8,
+                                   pred, stream));
         selected = pred;
     }
     PXS_TRY(pxs_layer_norm(PXS_F32, x, rows, channels, eps, w->norm1_weight, w->norm1_bias, dtype,
@@ -235,6 +281,133 @@ int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const floa
     PXS_TRY(pxs_subm_conv3d(dtype, b.hnorm, m, out_channels, w->conv2_weight, w->conv2_bias,
                             out_channels, b.map2.nbr, b.map2.masks, conv_out, stream));
     return pxs_add_repeat(dtype, conv_out, m, out_channels, b.skip, channels / 8, y, stream);
+}
+
+size_t pxs_slat_decoder_workspace_bytes(int dtype, const pxs_decoder_config * cfg,
+                                        const pxs_decoder_block * blocks, int n_blocks,
+                                        int64_t rows, int64_t max_rows) {
+    if (!cfg || !blocks || cfg->levels <= 0 || !cfg->model_channels || !cfg->num_blocks ||
+        rows < 0 || max_rows < rows) {
+        return 0;
+    }
+    Carver c(nullptr);
+    carve_decoder(c, dtype, *cfg, blocks, n_blocks, rows, max_rows);
+    return c.used();
+}
+
+int pxs_slat_decoder_forward(int dtype, const pxs_decoder_config * cfg,
+                             const float * from_latent_weight, const float * from_latent_bias,
+                             const float * output_weight, const float * output_bias,
+                             const pxs_decoder_block * blocks, int n_blocks,
+                             const int32_t * coords, int64_t rows, const float * x,
+                             const float * const * guide, float * const * predicted,
+                             int upsample_times, int64_t max_rows, int32_t * out_coords,
+                             float * y, int64_t * rows_out, int64_t * level_rows,
+                             void * workspace, void * stream) {
+    PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG,
+              "pxs_slat_decoder_forward: bad dtype");
+    PXS_CHECK(cfg && rows_out, PXS_ERR_ARG, "pxs_slat_decoder_forward: null config");
+    const bool upsample = upsample_times >= 0;
+    // Configuration checks in the reference's order (src/slat_decoder.cpp:298-330, 385-410).
+    PXS_CHECK(cfg->norm_eps > 0.0f && std::isfinite(cfg->norm_eps), PXS_ERR_ARG,
+              "SLat decoder norm epsilon must be finite and positive");
+    const bool shape_ok = cfg->latent_channels > 0 && cfg->out_channels > 0 && cfg->levels > 0 &&
+                          cfg->model_channels && cfg->num_blocks;
+    if (upsample) {
+        PXS_CHECK(shape_ok && cfg->pred_subdiv && upsample_times < cfg->levels, PXS_ERR_ARG,
+                  "invalid SLat decoder coordinate-upsample configuration");
+    } else {
+        PXS_CHECK(shape_ok, PXS_ERR_ARG, "invalid SLat decoder configuration");
+    }
+    const int levels = cfg->levels;
+    int64_t expected = levels - 1;
+    for (int l = 0; l < levels; ++l) {
+        PXS_CHECK(cfg->num_blocks[l] >= 0, PXS_ERR_ARG, "invalid SLat decoder block count");
+        expected += cfg->num_blocks[l];
+    }
+    PXS_CHECK(blocks && n_blocks == expected, PXS_ERR_ARG,
+              "SLat decoder weight block count does not match configuration");
+    PXS_CHECK(from_latent_weight, PXS_ERR_ARG, "missing SLat decoder tensor: from_latent.weight");
+    PXS_CHECK(from_latent_bias, PXS_ERR_ARG, "missing SLat decoder tensor: from_latent.bias");
+    if (!upsample) {
+        PXS_CHECK(output_weight, PXS_ERR_ARG, "missing SLat decoder tensor: output_layer.weight");
+        PXS_CHECK(output_bias, PXS_ERR_ARG, "missing SLat decoder tensor: output_layer.bias");
+    }
+    PXS_CHECK(!predicted || cfg->pred_subdiv, PXS_ERR_ARG,
+              "pxs_slat_decoder_forward: predicted logits need pred_subdiv");
+    PXS_CHECK(rows >= 0 && max_rows >= rows, PXS_ERR_ARG, "pxs_slat_decoder_forward: bad shape");
+    PXS_CHECK(rows == 0 || (coords && x && out_coords && y && workspace), PXS_ERR_ARG,
+              "pxs_slat_decoder_forward: null pointer");
+    if (level_rows) level_rows[0] = rows;
+    *rows_out = 0;
+    if (rows == 0) return PXS_OK;
+    hipStream_t s = as_stream(stream);
+    Carver c(workspace);
+    const DecoderBuffers b = carve_decoder(c, dtype, *cfg, blocks, n_blocks, rows, max_rows);
+    const float eps = cfg->norm_eps;
+    int cur = 0;
+    int64_t n = rows;
+    const int32_t * ccur = coords;
+    PXS_TRY(pxs_linear(PXS_F32, x, rows, cfg->latent_channels, from_latent_weight, from_latent_bias,
+                       cfg->model_channels[0], PXS_ACT_NONE, b.hid[0], stream));
+    int bi = 0;
+    for (int l = 0; l < levels; ++l) {
+        const int C = cfg->model_channels[l];
+        if (upsample && l == upsample_times) {
+            // slat_decoder_upsample_coords_f32 returns the hidden state here.
+            PXS_TRY(check_hip(hipMemcpyAsync(y, b.hid[cur], n * C * sizeof(float),
+                                             hipMemcpyDeviceToDevice, s), "decoder output copy"));
+            PXS_TRY(check_hip(hipMemcpyAsync(out_coords, ccur, n * 16, hipMemcpyDeviceToDevice, s),
+                              "decoder coordinate copy"));
+            *rows_out = n;
+            return check_launch("pxs_slat_decoder_forward");
+        }
+        if (cfg->num_blocks[l] > 0) PXS_TRY(build_map(ccur, n, b.map, stream));
+        for (int k = 0; k < cfg->num_blocks[l]; ++k, ++bi) {
+            const pxs_decoder_block & blk = blocks[bi];
+            PXS_CHECK(blk.kind == PXS_DECODER_CONVNEXT, PXS_ERR_ARG,
+                      upsample ? "SLat decoder coordinate-upsample expected ConvNeXt block"
+                               : "SLat decoder expected ConvNeXt block");
+            PXS_CHECK(blk.channels == C, PXS_ERR_ARG,
+                      "pxs_slat_decoder_forward: block channels do not match the level");
+            PXS_TRY(pxs_convnext_block(dtype, ccur, n, b.hid[cur], C, blk.mlp_hidden, eps, &blk.w,
+                                       b.map.nbr, b.map.masks, b.hid[cur], b.block_ws, stream));
+        }
+        if (l + 1 == levels) break;
+        const pxs_decoder_block & blk = blocks[bi++];
+        PXS_CHECK(blk.kind == PXS_DECODER_C2S, PXS_ERR_ARG,
+                  upsample ? "SLat decoder coordinate-upsample expected C2S block"
+                           : "SLat decoder expected channel-to-spatial block");
+        PXS_CHECK(blk.channels == C && blk.out_channels == cfg->model_channels[l + 1], PXS_ERR_ARG,
+                  "pxs_slat_decoder_forward: block channels do not match the level");
+        PXS_CHECK(n <= max_rows / 8, PXS_ERR_ARG,
+                  "pxs_slat_decoder_forward: a level may exceed max_rows (needs 8 * rows)");
+        const int nxt = 1 - cur;
+        const bool pred = upsample ? true : cfg->pred_subdiv != 0;
+        const float * g = (!upsample && guide) ? guide[l] : nullptr;
+        float * logits = (!upsample && predicted) ? predicted[l] : nullptr;
+        int64_t m = 0;
+        PXS_TRY(pxs_resblock_c2s(dtype, ccur, n, b.hid[cur], C, blk.out_channels, eps, &blk.w,
+                                 pred ? 1 : 0, g, logits, b.crd[nxt], b.hid[nxt], &m, b.block_ws,
+                                 stream));
+        ccur = b.crd[nxt];
+        cur = nxt;
+        n = m;
+        if (level_rows) level_rows[l + 1] = n;
+    }
+    // Final layer norm (eps 1e-5, no affine) and output linear
+    // (src/slat_decoder.cpp:367-372).
+    const int C = cfg->model_channels[levels - 1];
+    PXS_TRY(pxs_layer_norm(PXS_F32, b.hid[cur], n, C, 1e-5f, nullptr, nullptr, PXS_F32,
+                           b.hid[1 - cur], stream));
+    PXS_TRY(pxs_linear(PXS_F32, b.hid[1 - cur], n, C, output_weight, output_bias, cfg->out_channels,
+                       PXS_ACT_NONE, y, stream));
+    if (n > 0 && ccur != out_coords) {
+        PXS_TRY(check_hip(hipMemcpyAsync(out_coords, ccur, n * 16, hipMemcpyDeviceToDevice, s),
+                          "decoder coordinate copy"));
+    }
+    *rows_out = n;
+    return check_launch("pxs_slat_decoder_forward");
 }
 
 } // extern "C"

@@ -939,6 +939,82 @@ __global__ void downsample_mean_kernel(const T * __restrict__ x, int channels,
     }
 }
 
+// fp32 linear in sparse_linear's own operation order (src/sparse.cpp:436-446):
+// value = bias[o], then value += w[o][i] * x[i] for i ascending, every product
+// and sum rounded alone.  One thread per (row, output); the x row is read in
+// 16-byte pieces.  For a handful of outputs whose signs decide a topology
+// (the subdivision logits), where the MFMA linear's different summation
+// order could flip a logit within rounding of zero.
+__global__ void ordered_linear_kernel(const float * __restrict__ x, int64_t rows, int cin,
+                                      const float * __restrict__ weight,
+                                      const float * __restrict__ bias, int cout,
+                                      float * __restrict__ y) {
+#pragma clang fp contract(off)
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= rows * cout) return;
+    const int64_t row = t / cout;
+    const int o = static_cast<int>(t - row * cout);
+    const float * xr = x + row * cin;
+    const float * wr = weight + static_cast<int64_t>(o) * cin;
+    float value = bias ? bias[o] : 0.0f;
+    int i = 0;
+    if ((cin & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(weight) & 15) == 0) {
+        for (; i < cin; i += 4) {
+            const float4 xv = *reinterpret_cast<const float4 *>(xr + i);
+            const float4 wv = *reinterpret_cast<const float4 *>(wr + i);
+            value += wv.x * xv.x;
+            value += wv.y * xv.y;
+            value += wv.z * xv.z;
+            value += wv.w * xv.w;
+        }
+    }
+    for (; i < cin; ++i) value += wr[i] * xr[i];
+    y[t] = value;
+}
+
+// The same order with one thread per row for up to 8 outputs: the row is
+// read once and each output keeps its own running sum (interleaving the
+// outputs does not change any one sum's order).  Weights come from LDS.
+constexpr int kOrderedRowOut = 8;
+constexpr int kOrderedRowCin = 2048;
+
+__global__ void __launch_bounds__(256)
+ordered_linear_rows_kernel(const float * __restrict__ x, int64_t rows, int cin,
+                           const float * __restrict__ weight, const float * __restrict__ bias,
+                           int cout, float * __restrict__ y) {
+#pragma clang fp contract(off)
+    __shared__ float w_lds[kOrderedRowOut * kOrderedRowCin];
+    for (int e = threadIdx.x; e < cout * cin; e += blockDim.x) w_lds[e] = weight[e];
+    __syncthreads();
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const float * xr = x + row * cin;
+    float acc[kOrderedRowOut];
+#pragma unroll
+    for (int o = 0; o < kOrderedRowOut; ++o) acc[o] = (o < cout && bias) ? bias[o] : 0.0f;
+    for (int i = 0; i < cin; i += 4) {
+        float xv[4];
+        if (i + 4 <= cin && (reinterpret_cast<uintptr_t>(xr + i) & 15) == 0) {
+            const float4 v = *reinterpret_cast<const float4 *>(xr + i);
+            xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[j] = i + j < cin ? xr[i + j] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (i + j >= cin) break;
+#pragma unroll
+            for (int o = 0; o < kOrderedRowOut; ++o)
+                if (o < cout) acc[o] += w_lds[o * cin + i + j] * xv[j];
+        }
+    }
+#pragma unroll
+    for (int o = 0; o < kOrderedRowOut; ++o)
+        if (o < cout) y[row * cout + o] = acc[o];
+}
+
 } // namespace
 } // namespace pxs
 
@@ -1040,6 +1116,22 @@ int pxs_downsample_mean(int dtype, const void * x, int channels, const int64_t *
                            channels, group_offsets, group_rows, m, static_cast<uint16_t *>(y));
     }
     return check_launch("pxs_downsample_mean");
+}
+
+int pxs_linear_ordered(const float * x, int64_t rows, int cin, const float * weight,
+                       const float * bias, int cout, float * y, void * stream) {
+    PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear_ordered: bad shape");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x && weight && y, PXS_ERR_ARG, "pxs_linear_ordered: null pointer");
+    if (cout <= kOrderedRowOut && cin <= kOrderedRowCin) {
+        hipLaunchKernelGGL(ordered_linear_rows_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)),
+                           dim3(256), 0, as_stream(stream), x, rows, cin, weight, bias, cout, y);
+        return check_launch("pxs_linear_ordered");
+    }
+    const int64_t count = rows * cout;
+    hipLaunchKernelGGL(ordered_linear_kernel, dim3(static_cast<unsigned>((count + 255) / 256)),
+                       dim3(256), 0, as_stream(stream), x, rows, cin, weight, bias, cout, y);
+    return check_launch("pxs_linear_ordered");
 }
 
 } // extern "C"

@@ -63,6 +63,10 @@ _SIGS = {
     "pxs_transformer_block": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                                      _i64, _vp, _vp, _vp]),
     "pxs_slat_flow_workspace_bytes": (C.c_size_t, [_i32, _vp, _i64, _i64, _i32]),
+    "pxs_linear_ordered": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "pxs_slat_decoder_workspace_bytes": (C.c_size_t, [_i32, _vp, _vp, _i32, _i64, _i64]),
+    "pxs_slat_decoder_forward": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _vp,
+                                        _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "pxs_flow_sampler_schedule": (_i32, [_vp, _i32, _vp, _vp, _vp]),
     "pxs_flow_guidance_workspace_bytes": (C.c_size_t, [_i32]),
     "pxs_flow_guidance": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _f, _f, _f, _f, _vp,
@@ -157,6 +161,31 @@ DECODER_DTYPE_WEIGHTS = frozenset({"conv1_weight", "conv2_weight", "mlp0_weight"
 
 class DecoderBlockWeights(C.Structure):
     _fields_ = [(name, C.c_void_p) for name in DECODER_WEIGHT_FIELDS]
+
+
+PXS_DECODER_CONVNEXT = 0
+PXS_DECODER_C2S = 1
+
+
+class DecoderBlock(C.Structure):
+    """pxs_decoder_block: one entry of SLatDecoderWeightsF32::blocks."""
+    _fields_ = [("kind", C.c_int), ("channels", C.c_int), ("out_channels", C.c_int),
+                ("mlp_hidden", C.c_int), ("w", DecoderBlockWeights)]
+
+
+class DecoderConfig(C.Structure):
+    """pxs_decoder_config (SLatDecoderConfig); keep the channel arrays alive."""
+    _fields_ = [("latent_channels", C.c_int), ("out_channels", C.c_int), ("norm_eps", C.c_float),
+                ("pred_subdiv", C.c_int), ("levels", C.c_int),
+                ("model_channels", C.POINTER(C.c_int)), ("num_blocks", C.POINTER(C.c_int))]
+
+
+def decoder_config(latent, out, eps, pred_subdiv, model_channels, num_blocks):
+    mc = (C.c_int * len(model_channels))(*model_channels)
+    nb = (C.c_int * len(num_blocks))(*num_blocks)
+    cfg = DecoderConfig(latent, out, eps, int(pred_subdiv), len(model_channels), mc, nb)
+    cfg._keep = (mc, nb)
+    return cfg
 
 
 def decoder_block_weights(tensors: dict) -> DecoderBlockWeights:
@@ -552,6 +581,51 @@ class Pxs:
                                             skip.shape[1], _ptr(y), self.stream()),
                     "pxs_add_repeat")
         return y
+
+    def linear_ordered(self, x, weight, bias=None, out=None):
+        """pxs_linear_ordered: fp32, the reference's summation order (bit-equal)."""
+        rows, cin = x.shape
+        cout = weight.shape[0]
+        y = torch.empty((rows, cout), dtype=torch.float32, device=x.device) if out is None else out
+        self._check(self.lib.pxs_linear_ordered(_ptr(x), rows, cin, _ptr(weight), _ptr(bias), cout,
+                                                _ptr(y), self.stream()), "pxs_linear_ordered")
+        return y
+
+    def slat_decoder_forward(self, dtype, cfg: DecoderConfig, from_latent_w, from_latent_b,
+                             output_w, output_b, blocks, coords, x, guide=None, predict=False,
+                             upsample_times=-1, max_rows=None):
+        """pxs_slat_decoder_forward -> (out_coords [m, 4], y [m, ch], level_rows list,
+        predicted logits list or None)."""
+        rows = coords.shape[0]
+        levels = cfg.levels
+        max_rows = rows * 8 ** (levels - 1) if max_rows is None else max_rows
+        arr = (DecoderBlock * len(blocks))(*blocks)
+        ws = self._ws(self.lib.pxs_slat_decoder_workspace_bytes(dtype, C.byref(cfg), arr,
+                                                               len(blocks), rows, max_rows),
+                      x.device)
+        out_ch = cfg.out_channels if upsample_times < 0 else cfg.model_channels[upsample_times]
+        out_coords = torch.empty((max_rows, 4), dtype=torch.int32, device=x.device)
+        y = torch.empty((max_rows, out_ch), dtype=torch.float32, device=x.device)
+        guide_arr = None
+        if guide is not None:
+            guide_arr = (C.c_void_p * (levels - 1))(*[g.data_ptr() for g in guide])
+        preds = None
+        pred_arr = None
+        if predict:
+            preds = [torch.empty((max_rows, 8), dtype=torch.float32, device=x.device)
+                     for _ in range(levels - 1)]
+            pred_arr = (C.c_void_p * (levels - 1))(*[t.data_ptr() for t in preds])
+        m = C.c_int64()
+        lvl = (C.c_int64 * levels)()
+        self._check(self.lib.pxs_slat_decoder_forward(
+            dtype, C.byref(cfg), _ptr(from_latent_w), _ptr(from_latent_b), _ptr(output_w),
+            _ptr(output_b), arr, len(blocks), _ptr(coords), rows, _ptr(x), guide_arr, pred_arr,
+            upsample_times, max_rows, _ptr(out_coords), _ptr(y), C.byref(m), lvl, _ptr(ws),
+            self.stream()), "pxs_slat_decoder_forward")
+        level_rows = list(lvl)
+        if preds is not None:
+            preds = [p[:level_rows[i]] for i, p in enumerate(preds)]
+        return out_coords[:m.value], y[:m.value], level_rows, preds
 
     # -- flow Euler sampler -----------------------------------------------------
     def flow_sampler_schedule(self, scfg: SamplerConfig, step):

@@ -198,3 +198,18 @@ def flow_step_64(seed: int = 5):
     coords = shell_coords(64, [FLOW_SHELLS], seed)
     return dict(coords=coords, batch_size=1, shape=(64, 64, 64), in_channels=8, out_channels=8,
                 width=1024, heads=16, mlp_hidden=4096, blocks=24, context_tokens=1370)
+
+
+DECODER_SHELLS = [(18.0, 22.0)]
+
+
+def decoder_64(seed: int = 7):
+    """A shape-decoder stack at the reference's decode scale: ~10.6k voxels at
+    64^3, five levels of 1024, 512, 256, 128, 64 channels (the decoder shapes
+    of tests/sparse_linear_cuda_benchmark.cpp:42-52: MLP 4C per level, output
+    linear 64 -> 7), one ConvNeXt block per level, four predicted
+    channel-to-spatial levels up to 1024^3."""
+    coords = shell_coords(64, [DECODER_SHELLS], seed)
+    return dict(coords=coords, latent_channels=32, out_channels=7,
+                model_channels=[1024, 512, 256, 128, 64], num_blocks=[1, 1, 1, 1, 1])
+

@@ -123,8 +123,9 @@ def test_resblock_c2s(px, orc, dtype, mode):
                                   pred_subdiv=(mode == "predicted"))
     torch.cuda.synchronize()
     if mode == "predicted":
+        # to_subdiv runs in sparse_linear's own order: the logits are bit-equal.
         ref_pred = orc.linear(x, w["to_subdiv_weight"], w["to_subdiv_bias"])
-        assert_fp32(host(pred), ref_pred, what="to_subdiv logits")
+        np.testing.assert_array_equal(host(pred), ref_pred)
         # The oracle selects children with the device's own logits, so a logit
         # within rounding of zero cannot split the two topologies.
         sub = host(pred)
@@ -161,3 +162,152 @@ def test_add_repeat(px):
     got = px.add_repeat(ab, skip)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(got), host(ab) + np.repeat(host(skip), 4, axis=1))
+
+
+# --- the decoder stack (slat_decoder_forward_f32, src/slat_decoder.cpp:290-440) -----
+
+def convnext_weights(seed, C, M):
+    return convnext_case(seed, C, M)[2]
+
+
+def c2s_weights(seed, C, O_):
+    return c2s_case(seed, C, O_)[2]
+
+
+def decoder_case(seed, latent=8, out=24, channels=(64, 32, 16), nblocks=(1, 1, 1)):
+    coords = W.shell_coords(12, [[(3.0, 4.5)], [(2.5, 4.0)]], seed)
+    n = coords.shape[0]
+    x = W.normal(seed, n * latent, 1).reshape(n, latent)
+    fl_w = W.normal(seed, channels[0] * latent, 2, std=latent ** -0.5).reshape(channels[0], latent)
+    fl_b = W.normal(seed, channels[0], 3, std=0.1)
+    out_w = W.normal(seed, out * channels[-1], 4, std=channels[-1] ** -0.5).reshape(out, channels[-1])
+    out_b = W.normal(seed, out, 5, std=0.1)
+    blocks = []  # (kind, C, out, mlp, weights)
+    k = 0
+    for level, C in enumerate(channels):
+        for _ in range(nblocks[level]):
+            k += 1
+            blocks.append((pxs.PXS_DECODER_CONVNEXT, C, C, 4 * C, convnext_weights(seed + k, C, 4 * C)))
+        if level + 1 < len(channels):
+            k += 1
+            blocks.append((pxs.PXS_DECODER_C2S, C, channels[level + 1], 0,
+                           c2s_weights(seed + k, C, channels[level + 1])))
+    return dict(coords=coords, x=x, fl=(fl_w, fl_b), out=(out_w, out_b), blocks=blocks,
+                channels=channels, nblocks=nblocks, latent=latent, out_ch=out)
+
+
+def run_decoder(px, case, dtype, pred_subdiv, guide=None, upsample_times=-1):
+    keep = []
+    blocks = []
+    for kind, C, O_, M, w in case["blocks"]:
+        dev, dw = device_decoder_weights(w, dtype)
+        keep.append(dev)
+        blocks.append(pxs.DecoderBlock(kind, C, O_, M, dw))
+    cfg = pxs.decoder_config(case["latent"], case["out_ch"], 1e-6, pred_subdiv,
+                             list(case["channels"]), list(case["nblocks"]))
+    fl = [t32(a) for a in case["fl"]]
+    ow = [t32(a) for a in case["out"]]
+    res = px.slat_decoder_forward(dtype, cfg, fl[0], fl[1], ow[0], ow[1], blocks,
+                                  ti32(case["coords"]), t32(case["x"]),
+                                  guide=None if guide is None else [t32(g) for g in guide],
+                                  predict=pred_subdiv and upsample_times < 0,
+                                  upsample_times=upsample_times)
+    torch.cuda.synchronize()
+    return res
+
+
+def oracle_decoder(orc, case, dtype, select, stop=None):
+    """slat_decoder_forward_f32 composed from the oracle's pieces in the
+    reference's order (src/slat_decoder.cpp:332-372): select(level, hidden) gives
+    the subdivision of each C2S; stop = upsample_times returns the hidden
+    state of that level (src/slat_decoder.cpp:419-423)."""
+    coords = case["coords"]
+    h = orc.linear(case["x"], *case["fl"])
+    bi = 0
+    for level, C in enumerate(case["channels"]):
+        if stop is not None and level == stop:
+            return coords, h
+        for _ in range(case["nblocks"][level]):
+            kind, C_, O_, M, w = case["blocks"][bi]
+            wr = rounded(w, dtype)
+            h = orc.convnext_block(coords, h, M, 1e-6, [wr[k] for k in ORC_CONVNEXT])
+            bi += 1
+        if level + 1 < len(case["channels"]):
+            kind, C_, O_, M, w = case["blocks"][bi]
+            wr = rounded(w, dtype)
+            coords, h = orc.resblock_c2s(coords, h, O_, 1e-6, [wr[k] for k in ORC_C2S],
+                                         subdivision=select(level, h, w))
+            bi += 1
+    return coords, orc.linear(orc.layer_norm(h, 1e-5), *case["out"])
+
+
+def test_decoder_stack_predicted_fp32(px, orc):
+    """Three levels (64 -> 32 -> 16 channels, one ConvNeXt block each) with
+    predicted subdivisions.  The oracle subdivides with the device's logits
+    (a logit within rounding of zero could otherwise split the topologies),
+    and those logits must equal the oracle's to_subdiv linear of the oracle's
+    own hidden state to the fp32 bar."""
+    case = decoder_case(81)
+    oc, y, level_rows, preds = run_decoder(px, case, pxs.PXS_F32, True)
+    print(f"[decoder stack fp32] level rows {level_rows}", flush=True)
+    got_logits = [host(p) for p in preds]
+
+    def select(level, h, w):
+        ref = orc.linear(h, w["to_subdiv_weight"], w["to_subdiv_bias"])
+        assert_fp32(got_logits[level], ref, what=f"level {level} logits")
+        return got_logits[level]
+
+    rc, ry = oracle_decoder(orc, case, pxs.PXS_F32, select)
+    assert level_rows[-1] == rc.shape[0] and 0 < level_rows[1] < 8 * level_rows[0]
+    np.testing.assert_array_equal(host(oc).astype(np.int32), rc)
+    assert_fp32(host(y), ry, what="decoder stack fp32")
+
+
+@pytest.mark.parametrize("dtype", [pxs.PXS_F32, pxs.PXS_BF16])
+def test_decoder_stack_guided(px, orc, dtype):
+    """Guide subdivisions fix the topology, so bf16 compares too."""
+    case = decoder_case(82, nblocks=(2, 1, 1))
+    n0 = case["coords"].shape[0]
+    g0 = W.normal(83, n0 * 8, 1).reshape(n0, 8)
+    guides = [g0]
+    # The second level's guide needs its row count: the children g0 keeps.
+    n1 = int((g0 > 0).sum())
+    guides.append(W.normal(84, n1 * 8, 1).reshape(n1, 8))
+    oc, y, level_rows, _ = run_decoder(px, case, dtype, False, guide=guides)
+    print(f"[decoder stack guided] dtype={dtype} level rows {level_rows}", flush=True)
+    rc, ry = oracle_decoder(orc, case, dtype, lambda level, h, w: guides[level])
+    assert level_rows[1] == n1
+    np.testing.assert_array_equal(host(oc).astype(np.int32), rc)
+    if dtype == pxs.PXS_F32:
+        assert_fp32(host(y), ry, what="decoder stack guided fp32")
+    else:
+        assert_bf16(host(y), ry, what="decoder stack guided bf16")
+
+
+def test_decoder_upsample_coords(px, orc):
+    """upsample_times = 1: the coordinates and hidden state after one C2S
+    level (slat_decoder_upsample_coords_f32); upsample_times = 0 returns the
+    latent projection on the input coordinates."""
+    case = decoder_case(85)
+    oc, y, _, _ = run_decoder(px, case, pxs.PXS_F32, True, upsample_times=0)
+    np.testing.assert_array_equal(host(oc).astype(np.int32), case["coords"])
+    assert_fp32(host(y), orc.linear(case["x"], *case["fl"]), what="upsample 0")
+    oc1, y1, _, _ = run_decoder(px, case, pxs.PXS_F32, True, upsample_times=1)
+    full_c, _, _, preds = run_decoder(px, case, pxs.PXS_F32, True)
+    logits = host(preds[0])
+    rc, rh = oracle_decoder(orc, case, pxs.PXS_F32, lambda level, h, w: logits, stop=1)
+    np.testing.assert_array_equal(host(oc1).astype(np.int32), rc)
+    assert_fp32(host(y1), rh, what="upsample 1")
+
+
+def test_decoder_stack_errors(px):
+    case = decoder_case(86)
+    with pytest.raises(pxs.PxsError, match="weight block count"):
+        bad = dict(case, blocks=case["blocks"][:-1])
+        run_decoder(px, bad, pxs.PXS_F32, True)
+    with pytest.raises(pxs.PxsError, match="coordinate-upsample configuration"):
+        run_decoder(px, case, pxs.PXS_F32, False, upsample_times=1)
+    with pytest.raises(pxs.PxsError, match="expected ConvNeXt block"):
+        swapped = list(case["blocks"])
+        swapped[0], swapped[1] = swapped[1], swapped[0]
+        run_decoder(px, dict(case, blocks=swapped), pxs.PXS_F32, True)

@@ -147,3 +147,15 @@ def test_qkv_prepare(px, orc, dtype, hd, heads):
     check(host(q), rq, what="q")
     check(host(k), rk, what="k")
     np.testing.assert_array_equal(host(v), qkv[:, 2 * C:])
+
+
+@pytest.mark.parametrize("cin,cout", [(64, 8), (37, 8), (128, 3), (96, 24)])
+def test_linear_ordered_bit_exact(px, orc, cin, cout):
+    """pxs_linear_ordered reproduces sparse_linear's operation order: bit-equal
+    to the oracle (itself bit-equal to the compiled reference)."""
+    rows = 1000
+    x = W.normal(91, rows * cin, 1).reshape(rows, cin)
+    w = W.normal(91, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin)
+    b = W.normal(91, cout, 3)
+    got = px.linear_ordered(t32(x), t32(w), t32(b))
+    np.testing.assert_array_equal(host(got), orc.linear(x, w, b))
