@@ -349,6 +349,7 @@ __device__ __align__(16) uint4 g_zero_chunk[8];  // 128 zero bytes for absent ro
 #ifndef PXS_GEMM_WIDE
 #define PXS_GEMM_WIDE 1
 #endif
+
 #ifndef PXS_GEMM_ISSUE_LATE
 #define PXS_GEMM_ISSUE_LATE 0
 #endif
@@ -873,6 +874,9 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
             // Short ones (the 8-offset stride-2 conv, 16 K stages) lose 6%:
             // with one workgroup per CU nothing hides a tile's prologue.
             const int64_t kstages = static_cast<int64_t>(args.noff) * ((args.cin + 63) / 64);
+            // (192-row tiles, which put SubMConv3d 256->256 on ~40k rows in
+            // one round of tiles instead of 1.2, measured the same: the
+            // chip-wide operand rate bounds it, not the last round.)
             if (PXS_GEMM_WIDE && args.rowmap && args.cout > 128 && kstages >= 32)
                 return launch_lds_tile<T, 128, 256, EPI, 2, 8, 2, 1>(args, stream);
         }

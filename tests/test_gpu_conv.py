@@ -203,3 +203,30 @@ def test_unet_stage_strided_full_size(px):
         ok = src >= 0
         ref[ok] += x[src[ok]].astype(np.float64) @ w[c].astype(np.float64).T
     assert_bf16(y[rows], ref, what="unet B sampled")
+
+
+def test_unet_stage_conv_c_full_size(px):
+    """Config-2 op C at full size (SubMConv3d 256 -> 256 on the ~40k coarse
+    voxels, 128 x 256 tiles): sampled rows in float64, plus the exact centre
+    identity on every row."""
+    wl = W.unet_stage_128()
+    oc, _, m = px.downsample_s2(ti32(wl["coords"]), 2, (128, 128, 128))
+    coords = oc[:m].contiguous()
+    print(f"[conv bf16 unet C] m={m}", flush=True)
+    x = W.bf16_round(W.normal(95, m * 256, 1).reshape(m, 256))
+    w = wl["w_c"]
+    nbr, masks = px.neighbor_map(coords)
+    xb = tbf(x)
+    y = host(px.subm_conv3d(xb, tbf(w), t32(wl["b_c"]), nbr, masks))
+    idx = nbr.cpu().numpy()
+    rows = np.linspace(0, m - 1, 1500).astype(np.int64)
+    ref = np.tile(wl["b_c"].astype(np.float64), (rows.size, 1))
+    for k in range(27):
+        src = idx[k, rows]
+        ok = src != m
+        ref[ok] += x[src[ok]].astype(np.float64) @ w[k].astype(np.float64).T
+    assert_bf16(y[rows], ref, what="unet C sampled")
+    eye = np.zeros((27, 256, 256), np.float32)
+    eye[13] = np.eye(256, dtype=np.float32)
+    yi = px.subm_conv3d(xb, tbf(eye), t32(np.zeros(256)), nbr, masks)
+    np.testing.assert_array_equal(host(yi), host(xb))
