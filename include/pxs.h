@@ -598,6 +598,98 @@ int pxs_slat_decoder_forward(int dtype, const pxs_decoder_config * cfg,
 int pxs_add_repeat(int a_dtype, const void * a, int64_t rows, int channels, const float * skip,
                    int skip_channels, float * y, void * stream);
 
+/* ---- f3: GGUF pack ingestion ------------------------------------------------------- */
+
+/* An open Pixal3D GGUF pack (host object).  The C++ drop-in of the
+ * reference reader is include/pixal3d/pack.h. */
+typedef struct pxs_pack pxs_pack;
+
+/* load_pack_info + Pixal3DPackReader::open (src/pack.cpp:127-311): parse the
+ * GGUF v3 header, metadata and tensor table (no payload) and apply the
+ * reference's checks and messages. */
+int pxs_pack_open(const char * path, pxs_pack ** pack);
+void pxs_pack_close(pxs_pack * pack);
+
+/* Pixal3DPackInfo (include/pixal3d/pack.h:16-47) as a JSON object written to
+ * buf (NUL-terminated) when len suffices; returns the length it needs
+ * (NUL included), 0 for a NULL pack. */
+size_t pxs_pack_describe(const pxs_pack * pack, char * buf, size_t len);
+
+/* Pixal3DPackReader::metadata_* (src/pack.cpp:387-462): the reference's type
+ * rules, defaults for a missing optional key (0, 0.0, false, "") and
+ * messages. */
+int pxs_pack_metadata_u32(const pxs_pack * pack, const char * key, int required,
+                          uint32_t * value);
+int pxs_pack_metadata_f32(const pxs_pack * pack, const char * key, int required, float * value);
+int pxs_pack_metadata_bool(const pxs_pack * pack, const char * key, int required, int * value);
+int pxs_pack_metadata_string(const pxs_pack * pack, const char * key, int required, char * buf,
+                             size_t len);
+
+/* Pixal3DPackReader::read_tensor (src/pack.cpp:331-385): the payload bytes
+ * into host memory dst (capacity bytes); *n_bytes receives the size. */
+int pxs_pack_read_tensor(const pxs_pack * pack, const char * name, void * dst, size_t capacity,
+                         size_t * n_bytes);
+
+/* Device workspace of the upload calls below (two 16 MiB staging chunks and
+ * one flag per tensor of the pack). */
+size_t pxs_pack_upload_workspace_bytes(const pxs_pack * pack);
+
+/* read_tensor_f32 (src/slat_flow.cpp:360-395) onto the device: an F32, F16
+ * or BF16 tensor converted to dtype (PXS_F32 exactly; PXS_BF16 rounded to
+ * nearest even) at dst (device, 16-byte aligned, count = the tensor's
+ * elements).  The payload streams file -> pinned staging -> HBM in chunks
+ * with the next read overlapping the copy and conversion.  A non-finite
+ * value fails with PXS_ERR_DATA.  Waits for `stream`.  Calls on one pack
+ * must not overlap (they share its pinned staging). */
+int pxs_pack_upload(pxs_pack * pack, const char * name, int dtype, void * dst, int64_t count,
+                    void * workspace, void * stream);
+
+/* SLatFlowModel::load (src/slat_flow.cpp:1239-1281) for one component
+ * (shape_flow_512, shape_flow_1024, texture_flow_1024): plan reads and checks
+ * the hyperparameters (read_hparams / valid_hparams, src/slat_flow.cpp:
+ * 397-429, 113-138) into *cfg and sizes the device arena; load converts
+ * every tensor of the component into the arena (block linear weights in
+ * dtype, everything else fp32, each 256-byte aligned) and binds *w and
+ * blocks[0 .. num_blocks) (SLatFlowModel::forward, src/slat_flow.cpp:
+ * 1348-1395) for pxs_slat_flow_forward / pxs_flow_euler_sample with the same
+ * dtype.  A missing tensor or one whose shape disagrees with the
+ * hyperparameters fails the load.  Waits for `stream`. */
+int pxs_slat_flow_pack_plan(const pxs_pack * pack, const char * component, int dtype,
+                            pxs_flow_config * cfg, size_t * arena_bytes);
+int pxs_slat_flow_pack_load(pxs_pack * pack, const char * component, int dtype, void * arena,
+                            size_t arena_bytes, void * workspace, pxs_flow_weights * w,
+                            pxs_block_weights * blocks, int max_blocks, void * stream);
+
+/* SLatDecoderHParams (include/pixal3d/slat_decoder.h:108-118); n_blocks =
+ * sum(num_blocks) + levels - 1 entries of pxs_decoder_block. */
+#define PXS_DECODER_MAX_LEVELS 16
+typedef struct pxs_decoder_hparams {
+    int resolution;
+    int latent_channels;
+    int out_channels;
+    int levels;
+    int pred_subdiv;
+    int n_blocks;
+    float norm_eps;
+    int model_channels[PXS_DECODER_MAX_LEVELS];
+    int num_blocks[PXS_DECODER_MAX_LEVELS];
+} pxs_decoder_hparams;
+
+/* SLatDecoderModel::load (src/slat_decoder.cpp:3392-3467) and make_weights
+ * (2911-2970) for one component: plan reads the metadata into *hp and sizes
+ * the arena; load converts the component's tensors into the arena
+ * (convolution and ConvNeXt MLP weights in dtype, everything else fp32) and
+ * fills blocks[0 .. n_blocks) in level order and io_weights[4] =
+ * {from_latent weight, bias, output_layer weight, bias} for
+ * pxs_slat_decoder_forward (whose config is latent_channels, out_channels,
+ * norm_eps, pred_subdiv, levels, model_channels, num_blocks of *hp).  Waits
+ * for `stream`. */
+int pxs_slat_decoder_pack_plan(const pxs_pack * pack, const char * component, int dtype,
+                               pxs_decoder_hparams * hp, size_t * arena_bytes);
+int pxs_slat_decoder_pack_load(pxs_pack * pack, const char * component, int dtype, void * arena,
+                               size_t arena_bytes, void * workspace, pxs_decoder_block * blocks,
+                               int max_blocks, const float ** io_weights, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -700,3 +700,22 @@ class DropIn(Reference):
 
     def __init__(self, path: Path = DROPIN_LIB):
         super().__init__(path)
+
+    def pack_reader_case(self, path, tensor, u32_key, capacity=1 << 20):
+        """dropin_pack_reader_case (host only, no GPU): the drop-in
+        Pixal3DPackReader driven as tests/test_pack_reader.cpp drives the
+        reference's -> ({key: (flag, text) or value}, tensor bytes)."""
+        fn = self.lib.dropin_pack_reader_case
+        fn.restype = C.c_int
+        fn.argtypes = [C.c_char_p, C.c_char_p, C.c_char_p, _vp, C.c_size_t, C.c_char_p, C.c_int]
+        out = C.create_string_buffer(capacity)
+        report = C.create_string_buffer(1 << 16)
+        fn(str(path).encode(), tensor.encode(), u32_key.encode(), out, capacity, report,
+           len(report))
+        result = {}
+        for line in report.value.decode().splitlines():
+            key, _, value = line.partition("=")
+            flag, colon, text = value.partition(":")
+            result[key] = (int(flag), text) if colon else int(value)
+        n = result.get("bytes", 0)
+        return result, out.raw[:n]

@@ -18,6 +18,9 @@
 #include "pixal3d/cpu_threads.h"
 #endif
 #include "pixal3d/flow_sampler.h"
+#ifdef PXS_DROPIN_SHIM
+#include "pixal3d/pack.h"
+#endif
 #include "pixal3d/sparse.h"
 #include "pixal3d/sparse_transformer.h"
 
@@ -336,6 +339,60 @@ int ref_timestep_embed_mlp(const float * t, int64_t batch, int hidden, int freq,
     return finish(ok, e, err, errlen);
 }
 
+#endif
+
+#ifdef PXS_DROPIN_SHIM
+// ---- pack reader (include/pixal3d/pack.h) -------------------------------------
+
+// Drives pixal3d::load_pack_info and Pixal3DPackReader the way the
+// reference's tests/test_pack_reader.cpp:53-69 drives them: open, inspect,
+// read one tensor into out, read a missing tensor, read a u32 key, close,
+// read after close.  Each result is one "key=value" line of report.
+int dropin_pack_reader_case(const char * path, const char * tensor, const char * u32_key,
+                            unsigned char * out, size_t cap, char * report, int reportlen) {
+    std::string r, e;
+    pixal3d::Pixal3DPackInfo info;
+    const bool listed = pixal3d::load_pack_info(path, info, &e);
+    r += "load_pack_info=" + std::to_string(listed) + ":" + (listed ? "" : e) + "\n";
+    pixal3d::Pixal3DPackReader reader;
+    e.clear();
+    const bool opened = reader.open(path, &e);
+    r += "open=" + std::to_string(opened) + ":" + (opened ? "" : e) + "\n";
+    r += "is_open=" + std::to_string(reader.is_open()) + "\n";
+    if (opened) {
+        const pixal3d::Pixal3DPackInfo & in = reader.info();
+        r += "tensors=" + std::to_string(in.tensors.size()) + "\n";
+        r += "tensor_bytes=" + std::to_string(in.tensor_bytes()) + "\n";
+        r += "has_tensor=" + std::to_string(in.has_tensor(tensor)) + "\n";
+        for (const auto & t : in.tensors) {
+            if (t.name == tensor) r += "offset=" + std::to_string(t.offset) + "\n";
+        }
+        std::vector<std::uint8_t> raw;
+        e.clear();
+        const bool read = reader.read_tensor(tensor, raw, &e);
+        r += "read=" + std::to_string(read) + ":" + (read ? "" : e) + "\n";
+        r += "bytes=" + std::to_string(raw.size()) + "\n";
+        if (read && raw.size() <= cap) std::memcpy(out, raw.data(), raw.size());
+        e.clear();
+        const bool missing = reader.read_tensor("missing", raw, &e);
+        r += "missing=" + std::to_string(missing) + ":" + e + "\n";
+        std::uint32_t v = 0;
+        e.clear();
+        const bool meta = reader.metadata_u32(u32_key, v, true, &e);
+        r += "meta=" + std::to_string(meta) + ":" + (meta ? std::to_string(v) : e) + "\n";
+        reader.close();
+        r += "closed_is_open=" + std::to_string(reader.is_open()) + "\n";
+        e.clear();
+        const bool after = reader.read_tensor(tensor, raw, &e);
+        r += "closed_read=" + std::to_string(after) + ":" + e + "\n";
+        e.clear();
+        const bool meta_after = reader.metadata_u32(u32_key, v, true, &e);
+        r += "closed_meta=" + std::to_string(meta_after) + ":" + e + "\n";
+    }
+    std::strncpy(report, r.c_str(), static_cast<std::size_t>(reportlen - 1));
+    report[reportlen - 1] = '\0';
+    return opened ? 1 : 0;
+}
 #endif
 
 } // extern "C"

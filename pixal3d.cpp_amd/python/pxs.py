@@ -103,6 +103,22 @@ _SIGS = {
     "pxs_resblock_c2s": (_i32, [_i32, _vp, _i64, _vp, _i32, _i32, _f, _vp, _i32, _vp, _vp, _vp,
                                 _vp, _vp, _vp, _vp]),
     "pxs_add_repeat": (_i32, [_i32, _vp, _i64, _i32, _vp, _i32, _vp, _vp]),
+    "pxs_pack_open": (_i32, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "pxs_pack_close": (None, [_vp]),
+    "pxs_pack_describe": (C.c_size_t, [_vp, C.c_char_p, C.c_size_t]),
+    "pxs_pack_metadata_u32": (_i32, [_vp, C.c_char_p, _i32, C.POINTER(C.c_uint32)]),
+    "pxs_pack_metadata_f32": (_i32, [_vp, C.c_char_p, _i32, C.POINTER(C.c_float)]),
+    "pxs_pack_metadata_bool": (_i32, [_vp, C.c_char_p, _i32, C.POINTER(C.c_int)]),
+    "pxs_pack_metadata_string": (_i32, [_vp, C.c_char_p, _i32, C.c_char_p, C.c_size_t]),
+    "pxs_pack_read_tensor": (_i32, [_vp, C.c_char_p, _vp, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "pxs_pack_upload_workspace_bytes": (C.c_size_t, [_vp]),
+    "pxs_pack_upload": (_i32, [_vp, C.c_char_p, _i32, _vp, _i64, _vp, _vp]),
+    "pxs_slat_flow_pack_plan": (_i32, [_vp, C.c_char_p, _i32, _vp, _vp]),
+    "pxs_slat_flow_pack_load": (_i32, [_vp, C.c_char_p, _i32, _vp, C.c_size_t, _vp, _vp, _vp,
+                                       _i32, _vp]),
+    "pxs_slat_decoder_pack_plan": (_i32, [_vp, C.c_char_p, _i32, _vp, _vp]),
+    "pxs_slat_decoder_pack_load": (_i32, [_vp, C.c_char_p, _i32, _vp, C.c_size_t, _vp, _vp,
+                                          _i32, _vp, _vp]),
 }
 
 
@@ -199,6 +215,18 @@ def block_weights(tensors) -> BlockWeights:
     return BlockWeights(*[None if t is None else t.data_ptr() for t in tensors])
 
 
+PXS_DECODER_MAX_LEVELS = 16
+
+
+class DecoderHParams(C.Structure):
+    """pxs_decoder_hparams (SLatDecoderHParams)."""
+    _fields_ = [("resolution", C.c_int), ("latent_channels", C.c_int),
+                ("out_channels", C.c_int), ("levels", C.c_int), ("pred_subdiv", C.c_int),
+                ("n_blocks", C.c_int), ("norm_eps", C.c_float),
+                ("model_channels", C.c_int * PXS_DECODER_MAX_LEVELS),
+                ("num_blocks", C.c_int * PXS_DECODER_MAX_LEVELS)]
+
+
 def load_library(path: Path = LIB_PATH) -> C.CDLL:
     if not Path(path).exists():
         raise PxsError(f"{path} is not built (run __graft_entry__.build())")
@@ -211,7 +239,10 @@ def load_library(path: Path = LIB_PATH) -> C.CDLL:
 
 
 def _ptr(t):
-    return None if t is None else C.c_void_p(t.data_ptr())
+    """A device pointer argument: a tensor, a raw address (int) or None."""
+    if t is None:
+        return None
+    return C.c_void_p(t if isinstance(t, int) else t.data_ptr())
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -678,3 +709,131 @@ class Pxs:
     def flow_workspace_bytes(self, cfg: FlowConfig, rows, tokens, batch_size, dtype):
         return self.lib.pxs_slat_flow_workspace_bytes(dtype, C.byref(cfg), rows, tokens,
                                                       batch_size)
+
+    # -- GGUF packs (f3) ----------------------------------------------------------
+    def pack_open(self, path) -> "Pack":
+        return Pack(self, path)
+
+    def slat_flow_pack_load(self, pack: "Pack", component, dtype, device="cuda"):
+        """pxs_slat_flow_pack_plan + _load -> PackedFlow (config, weights, arena)."""
+        cfg, need = FlowConfig(), C.c_size_t()
+        name = component.encode()
+        self._check(self.lib.pxs_slat_flow_pack_plan(pack.handle, name, dtype, C.byref(cfg),
+                                                     C.byref(need)), "pxs_slat_flow_pack_plan")
+        arena = self._ws(need.value, device)
+        ws = self._ws(self.lib.pxs_pack_upload_workspace_bytes(pack.handle), device)
+        blocks = (BlockWeights * cfg.num_blocks)()
+        weights = FlowWeights()
+        self._check(self.lib.pxs_slat_flow_pack_load(
+            pack.handle, name, dtype, _ptr(arena), C.c_size_t(arena.numel()), _ptr(ws),
+            C.byref(weights), blocks, cfg.num_blocks, self.stream()), "pxs_slat_flow_pack_load")
+        return PackedFlow(cfg, weights, blocks, arena, dtype)
+
+    def slat_decoder_pack_load(self, pack: "Pack", component, dtype, device="cuda"):
+        """pxs_slat_decoder_pack_plan + _load -> PackedDecoder."""
+        hp, need = DecoderHParams(), C.c_size_t()
+        name = component.encode()
+        self._check(self.lib.pxs_slat_decoder_pack_plan(pack.handle, name, dtype, C.byref(hp),
+                                                        C.byref(need)),
+                    "pxs_slat_decoder_pack_plan")
+        arena = self._ws(need.value, device)
+        ws = self._ws(self.lib.pxs_pack_upload_workspace_bytes(pack.handle), device)
+        blocks = (DecoderBlock * max(hp.n_blocks, 1))()
+        io = (C.c_void_p * 4)()
+        self._check(self.lib.pxs_slat_decoder_pack_load(
+            pack.handle, name, dtype, _ptr(arena), C.c_size_t(arena.numel()), _ptr(ws), blocks,
+            hp.n_blocks, io, self.stream()), "pxs_slat_decoder_pack_load")
+        return PackedDecoder(hp, list(blocks)[:hp.n_blocks], [int(a) for a in io], arena, dtype)
+
+
+class Pack:
+    """An open GGUF pack (pxs_pack_open); close() it, or use it in a with."""
+
+    def __init__(self, px: Pxs, path):
+        self.px, self.lib = px, px.lib
+        h = C.c_void_p()
+        px._check(self.lib.pxs_pack_open(str(path).encode(), C.byref(h)), "pxs_pack_open")
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            self.lib.pxs_pack_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def describe(self) -> dict:
+        import json
+        n = self.lib.pxs_pack_describe(self.handle, None, 0)
+        buf = C.create_string_buffer(n)
+        self.lib.pxs_pack_describe(self.handle, buf, n)
+        return json.loads(buf.value.decode("utf-8"))
+
+    def metadata(self, key, kind, required=True):
+        """kind: "u32", "f32", "bool" or "string"."""
+        k = key.encode()
+        if kind == "string":
+            need = 1 << 16
+            buf = C.create_string_buffer(need)
+            self.px._check(self.lib.pxs_pack_metadata_string(self.handle, k, int(required), buf,
+                                                             need), "pxs_pack_metadata_string")
+            return buf.value.decode("utf-8")
+        ctype = {"u32": C.c_uint32, "f32": C.c_float, "bool": C.c_int}[kind]
+        v = ctype()
+        fn = getattr(self.lib, f"pxs_pack_metadata_{kind}")
+        self.px._check(fn(self.handle, k, int(required), C.byref(v)), f"pxs_pack_metadata_{kind}")
+        return bool(v.value) if kind == "bool" else v.value
+
+    def read_tensor(self, name) -> bytes:
+        n = C.c_size_t()
+        k = name.encode()
+        info = {t["name"]: t for t in self.describe()["tensors"]}.get(name)
+        size = info["n_bytes"] if info else 0
+        buf = C.create_string_buffer(max(size, 1))
+        self.px._check(self.lib.pxs_pack_read_tensor(self.handle, k, buf, size, C.byref(n)),
+                       "pxs_pack_read_tensor")
+        return buf.raw[:n.value]
+
+    def upload(self, name, dtype, count, device="cuda", out=None):
+        """pxs_pack_upload -> a 1-D device tensor of count elements in dtype."""
+        tdt = torch.float32 if dtype == PXS_F32 else torch.bfloat16
+        y = torch.empty(count, dtype=tdt, device=device) if out is None else out
+        ws = self.px._ws(self.lib.pxs_pack_upload_workspace_bytes(self.handle), device)
+        self.px._check(self.lib.pxs_pack_upload(self.handle, name.encode(), dtype, _ptr(y), count,
+                                                _ptr(ws), self.px.stream()), "pxs_pack_upload")
+        return y
+
+
+class PackedFlow:
+    """A SLat-flow component loaded into one device arena: cfg (FlowConfig),
+    weights (FlowWeights over blocks) for slat_flow_forward / flow_euler_sample
+    in `dtype`.  Keep this object alive while the weights are used."""
+
+    def __init__(self, cfg, weights, blocks, arena, dtype):
+        self.cfg, self.weights, self.blocks, self.arena, self.dtype = (cfg, weights, blocks,
+                                                                         arena, dtype)
+
+
+class PackedDecoder:
+    """A SLat-decoder component in one device arena: hp (DecoderHParams),
+    blocks (DecoderBlock list), io = [from_latent w, b, output w, b] device
+    addresses; config() gives the DecoderConfig for slat_decoder_forward."""
+
+    def __init__(self, hp, blocks, io, arena, dtype):
+        self.hp, self.blocks, self.io, self.arena, self.dtype = hp, blocks, io, arena, dtype
+
+    def config(self):
+        L = self.hp.levels
+        return decoder_config(self.hp.latent_channels, self.hp.out_channels, self.hp.norm_eps,
+                              self.hp.pred_subdiv, list(self.hp.model_channels[:L]),
+                              list(self.hp.num_blocks[:L]))

@@ -45,7 +45,12 @@ DROPIN_SYMBOLS = [
     "pixal3d::sparse_rotary_position_embedding(", "pixal3d::sparse_multihead_rms_norm(",
     "pixal3d::varlen_multihead_rms_norm(", "pixal3d::sparse_submanifold_conv3d(",
     "pixal3d::SparseTensorF32::valid(", "pixal3d::VarLenTensorF32::valid(",
-    "pixal3d::sparse_transformer_cross_block_f32(",
+    "pixal3d::sparse_transformer_cross_block_f32(", "pixal3d::flow_euler_sample_f32(",
+    "pixal3d::load_pack_info(", "pixal3d::Pixal3DPackReader::open(",
+    "pixal3d::Pixal3DPackReader::close(", "pixal3d::Pixal3DPackReader::read_tensor(",
+    "pixal3d::Pixal3DPackReader::metadata_u32(", "pixal3d::Pixal3DPackReader::metadata_f32(",
+    "pixal3d::Pixal3DPackReader::metadata_bool(", "pixal3d::Pixal3DPackReader::metadata_string(",
+    "pixal3d::Pixal3DPackInfo::tensor_bytes(", "pixal3d::Pixal3DPackInfo::has_tensor(",
 ]
 
 
