@@ -3,11 +3,12 @@
 // src/slat_decoder.cpp:3392-3467, whose read_tensor_f32 widens F16 / BF16
 // payloads on the host: src/slat_flow.cpp:360-395).
 //
-// A payload streams in 16 MiB chunks: pread into pinned host staging, one
-// DMA to HBM staging, one conversion kernel into the destination, with the
-// next chunk's file read overlapping the previous chunk's copy and
-// conversion (two chunks in flight).  The kernel is HBM-bound elementwise
-// work: 8 elements per thread, 16-byte loads and stores.
+// Payloads stream in 16 MiB chunks that consecutive tensors share: one file
+// read into pinned host staging (split over four reader threads when large),
+// one DMA to HBM staging, one conversion launch per tensor piece, with the
+// next chunk's read overlapping the previous chunk's DMA and conversions
+// (two chunks in flight).  The kernel is HBM-bound elementwise work: 8
+// elements per thread, 16-byte loads and stores.
 //
 // Conversions are exact or round to nearest even, independent of the
 // device's denormal modes: F16 is widened with integer operations (a
@@ -18,7 +19,11 @@
 
 #include "ingest.h"
 
+#include <unistd.h>
+
 #include <algorithm>
+#include <cerrno>
+#include <thread>
 
 #pragma clang fp contract(off)
 
@@ -165,46 +170,130 @@ int Ingest::begin() {
                      "hipMemsetAsync(pack flags)");
 }
 
-int Ingest::upload(const GgufTensor & t, int dtype, void * dst, size_t flag) {
-    PXS_CHECK(t.type == kGgmlF32 || t.type == kGgmlF16 || t.type == kGgmlBf16, PXS_ERR_ARG,
-              "pack upload: unsupported tensor type: " + t.name);
-    PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pack upload: bad dtype");
-    PXS_CHECK(flag < flags_, PXS_ERR_ARG, "pack upload: flag slot out of range");
-    PXS_CHECK(reinterpret_cast<uintptr_t>(dst) % 16 == 0, PXS_ERR_ARG,
-              "pack upload: destination must be 16-byte aligned: " + t.name);
-    const size_t esize = t.type == kGgmlF32 ? 4 : 2;
-    const size_t osize = dtype == PXS_F32 ? 4 : 2;
-    PXS_CHECK(t.n_bytes % esize == 0, PXS_ERR_ARG, "pack upload: misaligned payload: " + t.name);
-    auto * dev_stage = static_cast<uint8_t *>(workspace_);
-    auto * host_stage = static_cast<uint8_t *>(pack_->host_stage);
-    int32_t * flag_ptr =
-        reinterpret_cast<int32_t *>(dev_stage + stage_bytes()) + static_cast<int64_t>(flag);
-    for (uint64_t off = 0; off < t.n_bytes; off += kIngestChunk) {
-        const size_t bytes = static_cast<size_t>(std::min<uint64_t>(kIngestChunk, t.n_bytes - off));
-        const int s = slot_;
-        slot_ ^= 1;
-        if (pending_[s]) {
-            int rc = check_hip(hipEventSynchronize(done_[s]), "hipEventSynchronize(pack staging)");
-            if (rc != PXS_OK) return rc;
-            pending_[s] = false;
-        }
-        uint8_t * host = host_stage + s * kIngestChunk;
-        uint8_t * dev = dev_stage + s * kIngestChunk;
-        PXS_CHECK(read_payload(pack_->fd, pack_->file, t, off, host, bytes), PXS_ERR_ARG,
-                  "short read for tensor: " + t.name);
-        int rc = check_hip(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, stream_),
-                           "hipMemcpyAsync(pack staging)");
-        if (rc != PXS_OK) return rc;
-        const int64_t n = static_cast<int64_t>(bytes / esize);
-        void * out = static_cast<uint8_t *>(dst) + (off / esize) * osize;
-        rc = t.type == kGgmlF32   ? launch_convert<kGgmlF32>(dev, n, dtype, out, flag_ptr, stream_)
-             : t.type == kGgmlF16 ? launch_convert<kGgmlF16>(dev, n, dtype, out, flag_ptr, stream_)
-                                  : launch_convert<kGgmlBf16>(dev, n, dtype, out, flag_ptr, stream_);
-        if (rc != PXS_OK) return rc;
-        rc = check_hip(hipEventRecord(done_[s], stream_), "hipEventRecord(pack staging)");
-        if (rc != PXS_OK) return rc;
-        pending_[s] = true;
+namespace {
+
+// pread of [offset, offset + n) into dst, retried on short reads.
+bool read_range(int fd, uint64_t offset, uint8_t * dst, size_t n) {
+    while (n > 0) {
+        const ssize_t got = ::pread(fd, dst, n, static_cast<off_t>(offset));
+        if (got < 0 && errno == EINTR) continue;
+        if (got <= 0) return false;
+        dst += got;
+        offset += static_cast<uint64_t>(got);
+        n -= static_cast<size_t>(got);
     }
+    return true;
+}
+
+// A large read is split over reader threads: one thread copying out of the
+// page cache tops out well below the host link's DMA rate.
+constexpr int kReaders = 4;
+constexpr size_t kSplitBytes = size_t(4) << 20;
+
+bool read_parallel(int fd, uint64_t offset, uint8_t * dst, size_t n) {
+    if (n < kSplitBytes) return read_range(fd, offset, dst, n);
+    const size_t part = (n / kReaders + 4095) / 4096 * 4096;
+    bool ok[kReaders] = {};
+    std::thread workers[kReaders - 1];
+    for (int r = 1; r < kReaders; ++r) {
+        const size_t a = std::min(n, r * part), b = std::min(n, (r + 1) * part);
+        workers[r - 1] = std::thread([&, r, a, b] { ok[r] = read_range(fd, offset + a, dst + a, b - a); });
+    }
+    ok[0] = read_range(fd, offset, dst, std::min(n, part));
+    for (auto & w : workers) w.join();
+    for (bool v : ok) {
+        if (!v) return false;
+    }
+    return true;
+}
+
+size_t elem_size(uint32_t type) { return type == kGgmlF32 ? 4 : 2; }
+
+} // namespace
+
+int Ingest::run(const std::vector<IngestItem> & items) {
+    for (const IngestItem & it : items) {
+        const GgufTensor & t = *it.tensor;
+        PXS_CHECK(t.type == kGgmlF32 || t.type == kGgmlF16 || t.type == kGgmlBf16, PXS_ERR_ARG,
+                  "pack upload: unsupported tensor type: " + t.name);
+        PXS_CHECK(it.dtype == PXS_F32 || it.dtype == PXS_BF16, PXS_ERR_ARG,
+                  "pack upload: bad dtype");
+        PXS_CHECK(it.flag < flags_, PXS_ERR_ARG, "pack upload: flag slot out of range");
+        PXS_CHECK(reinterpret_cast<uintptr_t>(it.dst) % 16 == 0, PXS_ERR_ARG,
+                  "pack upload: destination must be 16-byte aligned: " + t.name);
+        PXS_CHECK(t.n_bytes % elem_size(t.type) == 0, PXS_ERR_ARG,
+                  "pack upload: misaligned payload: " + t.name);
+    }
+    const uint64_t base = pack_->file.data_offset;
+    std::vector<Segment> segs;
+    uint64_t chunk_begin = 0, chunk_end = 0;
+    for (size_t i = 0; i < items.size(); ++i) {
+        const GgufTensor & t = *items[i].tensor;
+        const uint64_t es = elem_size(t.type);
+        uint64_t done = 0;
+        while (done < t.n_bytes) {
+            const uint64_t at = base + t.offset + done;
+            // Pieces keep the kernel's 16-byte accesses aligned: each starts
+            // 16-byte aligned in the chunk (the chunk's first piece at 0) and
+            // every split falls on a multiple of 8 elements.  A piece opens a
+            // new chunk when it is misaligned in the current one, would not
+            // fit, or lies before its end (an out-of-order table).
+            const uint64_t step = 8 * es;
+            if (!segs.empty() &&
+                (at < chunk_end || (at - chunk_begin) % 16 != 0 ||
+                 (chunk_begin + kIngestChunk - at) / step * step == 0 ||
+                 at + std::min<uint64_t>(t.n_bytes - done, step) > chunk_begin + kIngestChunk)) {
+                const int rc = flush(chunk_begin, chunk_end, items, segs);
+                if (rc != PXS_OK) return rc;
+                segs.clear();
+            }
+            if (segs.empty()) chunk_begin = at;
+            const uint64_t room = (chunk_begin + kIngestChunk - at) / step * step;
+            const uint64_t take = std::min<uint64_t>(t.n_bytes - done, room);
+            segs.push_back({i, at - chunk_begin, done / es, static_cast<int64_t>(take / es)});
+            chunk_end = at + take;
+            done += take;
+        }
+    }
+    if (!segs.empty()) return flush(chunk_begin, chunk_end, items, segs);
+    return PXS_OK;
+}
+
+int Ingest::flush(uint64_t begin, uint64_t end, const std::vector<IngestItem> & items,
+                  const std::vector<Segment> & segs) {
+    const int s = slot_;
+    slot_ ^= 1;
+    if (pending_[s]) {
+        int rc = check_hip(hipEventSynchronize(done_[s]), "hipEventSynchronize(pack staging)");
+        if (rc != PXS_OK) return rc;
+        pending_[s] = false;
+    }
+    const size_t bytes = static_cast<size_t>(end - begin);
+    auto * host = static_cast<uint8_t *>(pack_->host_stage) + s * kIngestChunk;
+    auto * dev = static_cast<uint8_t *>(workspace_) + s * kIngestChunk;
+    if (!read_parallel(pack_->fd, begin, host, bytes)) {
+        // Name the first tensor the failed range covers.
+        return fail(PXS_ERR_ARG, "short read for tensor: " + items[segs.front().item].tensor->name);
+    }
+    int rc = check_hip(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, stream_),
+                       "hipMemcpyAsync(pack staging)");
+    if (rc != PXS_OK) return rc;
+    auto * flags = reinterpret_cast<int32_t *>(static_cast<uint8_t *>(workspace_) + stage_bytes());
+    for (const Segment & g : segs) {
+        const IngestItem & it = items[g.item];
+        const uint32_t type = it.tensor->type;
+        const uint8_t * src = dev + g.chunk_offset;
+        void * out = static_cast<uint8_t *>(it.dst) +
+                     g.first_element * (it.dtype == PXS_F32 ? 4 : 2);
+        int32_t * flag = flags + it.flag;
+        rc = type == kGgmlF32   ? launch_convert<kGgmlF32>(src, g.elements, it.dtype, out, flag, stream_)
+             : type == kGgmlF16 ? launch_convert<kGgmlF16>(src, g.elements, it.dtype, out, flag, stream_)
+                                : launch_convert<kGgmlBf16>(src, g.elements, it.dtype, out, flag, stream_);
+        if (rc != PXS_OK) return rc;
+    }
+    rc = check_hip(hipEventRecord(done_[s], stream_), "hipEventRecord(pack staging)");
+    if (rc != PXS_OK) return rc;
+    pending_[s] = true;
     return PXS_OK;
 }
 
@@ -246,7 +335,7 @@ int pxs_pack_upload(pxs_pack * pack, const char * name, int dtype, void * dst, i
     if (elements == 0) return PXS_OK;
     Ingest ingest(pack, workspace, 1, as_stream(stream));
     int rc = ingest.begin();
-    if (rc == PXS_OK) rc = ingest.upload(*t, dtype, dst, 0);
+    if (rc == PXS_OK) rc = ingest.run({IngestItem{t, dtype, dst, 0}});
     std::vector<int32_t> flags;
     const int frc = ingest.finish(flags);
     if (rc != PXS_OK) return rc;

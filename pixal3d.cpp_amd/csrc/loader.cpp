@@ -87,11 +87,11 @@ void place(const GgufFile & f, const std::string & prefix, int dtype, IsOperand 
 // misaligned, unreadable or non-finite fails the load.
 int upload_all(pxs_pack * pack, const Layout & layout, void * arena, void * workspace,
                hipStream_t stream, bool flow) {
-    Ingest ingest(pack, workspace, layout.items.size(), stream);
-    int rc = ingest.begin();
-    if (rc != PXS_OK) return rc;
+    // Host checks in table order; the items before the first failing tensor
+    // are uploaded, so a non-finite value in an earlier tensor still wins.
     int host_rc = PXS_OK;
     std::string host_msg;
+    std::vector<IngestItem> items;
     size_t k = 0;
     for (; k < layout.items.size(); ++k) {
         const Placement & p = layout.items[k];
@@ -112,17 +112,21 @@ int upload_all(pxs_pack * pack, const Layout & layout, void * arena, void * work
             host_msg = "SLat decoder tensor payload is not element aligned: " + t.name;
             break;
         }
-        if (p.bytes == 0) continue;
-        rc = ingest.upload(t, p.dtype, static_cast<uint8_t *>(arena) + p.offset, k);
-        if (rc != PXS_OK) {
-            host_rc = rc;
-            host_msg = pxs_last_error();
-            break;
-        }
+        if (p.bytes > 0) items.push_back({&t, p.dtype, static_cast<uint8_t *>(arena) + p.offset, k});
+    }
+    Ingest ingest(pack, workspace, layout.items.size(), stream);
+    int rc = ingest.begin();
+    if (rc != PXS_OK) return rc;
+    rc = ingest.run(items);
+    if (rc != PXS_OK) {
+        // An I/O or runtime failure: still report an earlier non-finite
+        // tensor first when the stream got that far.
+        host_rc = rc;
+        host_msg = pxs_last_error();
     }
     std::vector<int32_t> nonfinite;
-    rc = ingest.finish(nonfinite);
-    if (rc != PXS_OK) return rc;
+    const int frc = ingest.finish(nonfinite);
+    if (frc != PXS_OK) return frc;
     for (size_t j = 0; j < k; ++j) {
         if (nonfinite[j]) {
             return fail(PXS_ERR_DATA, std::string(flow ? "SLat flow" : "SLat decoder") +

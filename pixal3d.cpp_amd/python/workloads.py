@@ -213,3 +213,91 @@ def decoder_64(seed: int = 7):
     return dict(coords=coords, latent_channels=32, out_channels=7,
                 model_channels=[1024, 512, 256, 128, 64], num_blocks=[1, 1, 1, 1, 1])
 
+
+
+def write_flow_pack(path, width=1024, blocks=24, heads=16, mlp_ratio=4, cond=1024,
+                    in_ch=8, out_ch=8, seed=11, f16_matrices=False):
+    """Write a synthetic SLat-flow component pack (shape_flow_1024, compact-v1
+    names) in the converter's GGUF v3 layout: general / pixal3d keys, the
+    flow hyperparameters, tensors in sorted name order, 32-byte alignment.
+    Values are N(0, 0.02) (ones for norms and gammas); matrices are F16 when
+    f16_matrices (the converter's ftype 1), else everything is F32 (the
+    deployed flow policy).  Returns the payload bytes."""
+    import struct
+
+    C, M = width, width * mlp_ratio
+    D = C // heads
+    shapes = {"input_layer.weight": (C, in_ch), "input_layer.bias": (C,),
+              "t_embedder.mlp.0.weight": (C, 256), "t_embedder.mlp.0.bias": (C,),
+              "t_embedder.mlp.2.weight": (C, C), "t_embedder.mlp.2.bias": (C,),
+              "adaLN_modulation.1.weight": (6 * C, C), "adaLN_modulation.1.bias": (6 * C,),
+              "out_layer.weight": (out_ch, C), "out_layer.bias": (out_ch,)}
+    for b in range(blocks):
+        p, x = f"blocks.{b}.", f"blocks.{b}.cross_attn.cross_attn_block."
+        shapes.update({p + "modulation": (6 * C,), p + "self_attn.to_qkv.weight": (3 * C, C),
+                       p + "self_attn.to_qkv.bias": (3 * C,),
+                       p + "self_attn.q_rms_norm.gamma": (heads, D),
+                       p + "self_attn.k_rms_norm.gamma": (heads, D),
+                       p + "self_attn.to_out.weight": (C, C), p + "self_attn.to_out.bias": (C,),
+                       p + "norm2.weight": (C,), p + "norm2.bias": (C,),
+                       x + "to_q.weight": (C, C), x + "to_q.bias": (C,),
+                       x + "to_kv.weight": (2 * C, cond), x + "to_kv.bias": (2 * C,),
+                       x + "q_rms_norm.gamma": (heads, D), x + "k_rms_norm.gamma": (heads, D),
+                       x + "to_out.weight": (C, C), x + "to_out.bias": (C,),
+                       p + "mlp.mlp.0.weight": (M, C), p + "mlp.mlp.0.bias": (M,),
+                       p + "mlp.mlp.2.weight": (C, M), p + "mlp.mlp.2.bias": (C,)})
+
+    def s(v):
+        raw = v.encode()
+        return struct.pack("<Q", len(raw)) + raw
+
+    pre = "pixal3d.shape_flow_1024."
+    kv = [(k, 8, s(v)) for k, v in (("general.architecture", "pixal3d"),
+                                     ("general.name", "synthetic-flow"))]
+    kv += [("general.file_type", 4, struct.pack("<I", 1 if f16_matrices else 0)),
+           ("general.alignment", 4, struct.pack("<I", 32)),
+           ("pixal3d.bundle_format", 4, struct.pack("<I", 1)),
+           ("pixal3d.tensor_name_scheme", 8, s("compact-v1")),
+           ("pixal3d.component.0", 8, s("shape_flow_1024")),
+           (pre + "model_class", 8, s("ElasticSLatFlowModel"))]
+    kv += [(pre + k, 4, struct.pack("<I", v)) for k, v in (
+        ("resolution", 64), ("in_channels", in_ch), ("out_channels", out_ch),
+        ("model_channels", C), ("cond_channels", cond), ("num_blocks", blocks),
+        ("num_heads", heads))]
+    kv += [(pre + "mlp_ratio", 6, struct.pack("<f", mlp_ratio)),
+           (pre + "share_mod", 7, b"\x01"), (pre + "qk_rms_norm", 7, b"\x01"),
+           (pre + "qk_rms_norm_cross", 7, b"\x01"),
+           (pre + "rope_freq_min", 6, struct.pack("<f", 1.0)),
+           (pre + "rope_freq_base", 6, struct.pack("<f", 10000.0))]
+    names = sorted(shapes)
+    types = {}
+    for n in names:
+        small = len(shapes[n]) < 2 or any(t in n for t in ("gamma", "modulation", "norm"))
+        types[n] = 0 if (small or not f16_matrices) else 1
+    align = lambda v: (v + 31) // 32 * 32  # noqa: E731
+    head = bytearray(b"GGUF") + struct.pack("<IQQ", 3, len(names), len(kv))
+    for k, t, v in kv:
+        head += s(k) + struct.pack("<I", t) + v
+    off, offsets = 0, []
+    for n in names:
+        offsets.append(off)
+        off = align(off + int(np.prod(shapes[n])) * (2 if types[n] else 4))
+    for n, o in zip(names, offsets):
+        dims = tuple(reversed(shapes[n]))
+        head += s("sh1024." + n) + struct.pack("<I", len(dims))
+        head += b"".join(struct.pack("<Q", d) for d in dims) + struct.pack("<IQ", types[n], o)
+    head += b"\0" * (align(len(head)) - len(head))
+    rng = np.random.default_rng(seed)
+    total = 0
+    with open(path, "wb") as f:
+        f.write(head)
+        for n in names:
+            count = int(np.prod(shapes[n]))
+            if "gamma" in n or n.endswith("norm2.weight"):
+                v = np.ones(count, np.float32)
+            else:
+                v = (rng.standard_normal(count, dtype=np.float32) * np.float32(0.02))
+            raw = (v.astype(np.float16) if types[n] else v).tobytes()
+            f.write(raw + b"\0" * (align(len(raw)) - len(raw)))
+            total += len(raw)
+    return total

@@ -348,3 +348,59 @@ def test_decoder_pack_load_errors(px, tmp_path):
         with pytest.raises(pxs.PxsError, match="unsupported SLat decoder tensor type: "
                                                "texture_decoder.zz_quant"):
             px.slat_decoder_pack_load(pack, "texture_decoder", pxs.PXS_F32)
+
+
+def check_flow_arena(packed, info, alias, dtype):
+    """Every weight pxs_slat_flow_pack_load bound holds the pack's value in
+    its role's dtype."""
+    tdt = torch.bfloat16 if dtype == pxs.PXS_BF16 else torch.float32
+    for i, name in enumerate(FLOW_TOP):
+        ref = decoded(info, f"{alias}.{name}")
+        got = arena_slice(packed, getattr(packed.weights, pxs.FlowWeights._fields_[i][0]),
+                          ref.size, torch.float32)
+        np.testing.assert_array_equal(bits_of(got), ref.view(np.uint32), err_msg=name)
+    for b in range(packed.cfg.num_blocks):
+        blk = packed.blocks[b]
+        for i, field in enumerate(pxs.BLOCK_WEIGHT_FIELDS):
+            name = f"{alias}.blocks.{b}.{FLOW_FIELDS[field]}"
+            if info.tensor(name) is None:
+                continue
+            ref = torch.from_numpy(decoded(info, name))
+            want = ref.to(tdt) if i in pxs.BLOCK_LINEAR_WEIGHTS else ref
+            got = arena_slice(packed, getattr(blk, field), ref.numel(), want.dtype)
+            np.testing.assert_array_equal(bits_of(got), bits_of(want), err_msg=name)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_flow_pack_load_multichunk(px, tmp_path, f16):
+    """Width 512, 3 blocks (~50 MB F32): tensors share and straddle the 16 MiB
+    staging chunks; every bound weight is checked."""
+    path = tmp_path / "wide.gguf"
+    W.write_flow_pack(path, width=512, blocks=3, heads=8, cond=512, f16_matrices=f16)
+    info = G.load_pack_info(path)
+    for dtype in (pxs.PXS_F32, pxs.PXS_BF16):
+        print(f"[flow pack multichunk] f16={f16} dtype={dtype}", flush=True)
+        with px.pack_open(path) as pack:
+            packed = px.slat_flow_pack_load(pack, "shape_flow_1024", dtype)
+        torch.cuda.synchronize()
+        check_flow_arena(packed, info, "sh1024", dtype)
+
+
+def test_flow_pack_load_alignment_8(px, tmp_path):
+    """general.alignment 8: payloads sit at 8-byte offsets, so pieces that are
+    not 16-byte aligned in a chunk open a chunk of their own."""
+    info = G.load_pack_info(golden("pack_flow_f16"))
+    kvs = [(k, vt, (8 if k == "general.alignment" else v)) for k, (vt, v) in info.kv.items()]
+    tensors = [G.Tensor(t.name, t.ggml_type, t.ne[:max(t.n_dims, 1)], G.read_tensor(info, t.name))
+               for t in info.tensors]
+    # a 2-byte tensor first shifts every later payload by 8 bytes
+    tensors.insert(0, G.Tensor("sh1024.aaa_extra", G.GGML_F16, (1,), np.float16(0.5).tobytes()))
+    path = tmp_path / "a8.gguf"
+    G.write_pack(path, kvs, tensors, alignment=8)
+    info8 = G.load_pack_info(path)
+    assert any(t.offset % 16 for t in info8.tensors)
+    for dtype in (pxs.PXS_F32, pxs.PXS_BF16):
+        with px.pack_open(path) as pack:
+            packed = px.slat_flow_pack_load(pack, "shape_flow_1024", dtype)
+        torch.cuda.synchronize()
+        check_flow_arena(packed, info8, "sh1024", dtype)
