@@ -9,7 +9,8 @@
  *     are reported before anything is enqueued.
  *   - Calls are asynchronous on `stream` unless stated; none of them allocate
  *     device memory: scratch comes from a caller-provided workspace sized by
- *     the matching *_workspace_bytes query.
+ *     the matching *_workspace_bytes query.  (A pack's first upload allocates
+ *     its 32 MiB of pinned host staging, freed by pxs_pack_close.)
  *   - Coordinates are int32 rows (batch, x, y, z).  Features are row-major
  *     [rows, channels].  PXS_BF16 data is stored as raw bfloat16 bit
  *     patterns (uint16); arithmetic accumulates in fp32.
