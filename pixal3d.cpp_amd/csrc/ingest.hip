@@ -195,12 +195,21 @@ bool read_parallel(int fd, uint64_t offset, uint8_t * dst, size_t n) {
     const size_t part = (n / kReaders + 4095) / 4096 * 4096;
     bool ok[kReaders] = {};
     std::thread workers[kReaders - 1];
-    for (int r = 1; r < kReaders; ++r) {
-        const size_t a = std::min(n, r * part), b = std::min(n, (r + 1) * part);
-        workers[r - 1] = std::thread([&, r, a, b] { ok[r] = read_range(fd, offset + a, dst + a, b - a); });
+    int started = 1;  // parts [0, started) have a reader; the rest are read here
+    try {
+        for (int r = 1; r < kReaders; ++r, ++started) {
+            const size_t a = std::min(n, r * part), b = std::min(n, (r + 1) * part);
+            workers[r - 1] = std::thread([&, r, a, b] { ok[r] = read_range(fd, offset + a, dst + a, b - a); });
+        }
+    } catch (...) {
+        // No thread to be had: the parts without one are read on this thread.
     }
     ok[0] = read_range(fd, offset, dst, std::min(n, part));
-    for (auto & w : workers) w.join();
+    for (int r = started; r < kReaders; ++r) {
+        const size_t a = std::min(n, r * part), b = std::min(n, (r + 1) * part);
+        ok[r] = read_range(fd, offset + a, dst + a, b - a);
+    }
+    for (int r = 1; r < started; ++r) workers[r - 1].join();
     for (bool v : ok) {
         if (!v) return false;
     }
@@ -319,29 +328,31 @@ size_t pxs_pack_upload_workspace_bytes(const pxs_pack * pack) {
 
 int pxs_pack_upload(pxs_pack * pack, const char * name, int dtype, void * dst, int64_t count,
                     void * workspace, void * stream) {
-    PXS_CHECK(pack && name && workspace, PXS_ERR_ARG, "pxs_pack_upload: null argument");
-    const GgufTensor * t = pack->file.tensor(name);
-    PXS_CHECK(t, PXS_ERR_ARG, std::string("tensor not found: ") + name);
-    PXS_CHECK(t->type == kGgmlF32 || t->type == kGgmlF16 || t->type == kGgmlBf16, PXS_ERR_ARG,
-              std::string("pxs_pack_upload: tensor ") + name + " has type " +
-                  ggml_type_name(t->type) + ", not f32, f16 or bf16");
-    PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_pack_upload: bad dtype");
-    const uint64_t esize = t->type == kGgmlF32 ? 4 : 2;
-    const int64_t elements = static_cast<int64_t>(t->n_bytes / esize);
-    PXS_CHECK(count == elements, PXS_ERR_ARG,
-              std::string("pxs_pack_upload: ") + name + " holds " + std::to_string(elements) +
-                  " elements, not " + std::to_string(count));
-    PXS_CHECK(dst || elements == 0, PXS_ERR_ARG, "pxs_pack_upload: null destination");
-    if (elements == 0) return PXS_OK;
-    Ingest ingest(pack, workspace, 1, as_stream(stream));
-    int rc = ingest.begin();
-    if (rc == PXS_OK) rc = ingest.run({IngestItem{t, dtype, dst, 0}});
-    std::vector<int32_t> flags;
-    const int frc = ingest.finish(flags);
-    if (rc != PXS_OK) return rc;
-    if (frc != PXS_OK) return frc;
-    PXS_CHECK(!flags[0], PXS_ERR_DATA, std::string("tensor contains a non-finite value: ") + name);
-    return PXS_OK;
+    return pxs::guarded("pxs_pack_upload", [&]() -> int {
+        PXS_CHECK(pack && name && workspace, PXS_ERR_ARG, "pxs_pack_upload: null argument");
+        const GgufTensor * t = pack->file.tensor(name);
+        PXS_CHECK(t, PXS_ERR_ARG, std::string("tensor not found: ") + name);
+        PXS_CHECK(t->type == kGgmlF32 || t->type == kGgmlF16 || t->type == kGgmlBf16, PXS_ERR_ARG,
+                  std::string("pxs_pack_upload: tensor ") + name + " has type " +
+                      ggml_type_name(t->type) + ", not f32, f16 or bf16");
+        PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_pack_upload: bad dtype");
+        const uint64_t esize = t->type == kGgmlF32 ? 4 : 2;
+        const int64_t elements = static_cast<int64_t>(t->n_bytes / esize);
+        PXS_CHECK(count == elements, PXS_ERR_ARG,
+                  std::string("pxs_pack_upload: ") + name + " holds " + std::to_string(elements) +
+                      " elements, not " + std::to_string(count));
+        PXS_CHECK(dst || elements == 0, PXS_ERR_ARG, "pxs_pack_upload: null destination");
+        if (elements == 0) return PXS_OK;
+        Ingest ingest(pack, workspace, 1, as_stream(stream));
+        int rc = ingest.begin();
+        if (rc == PXS_OK) rc = ingest.run({IngestItem{t, dtype, dst, 0}});
+        std::vector<int32_t> flags;
+        const int frc = ingest.finish(flags);
+        if (rc != PXS_OK) return rc;
+        if (frc != PXS_OK) return frc;
+        PXS_CHECK(!flags[0], PXS_ERR_DATA, std::string("tensor contains a non-finite value: ") + name);
+        return PXS_OK;
+    });
 }
 
 } // extern "C"

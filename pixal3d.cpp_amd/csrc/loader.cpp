@@ -393,160 +393,168 @@ extern "C" {
 
 int pxs_slat_flow_pack_plan(const pxs_pack * pack, const char * component, int dtype,
                             pxs_flow_config * cfg, size_t * arena_bytes) {
-    PXS_CHECK(pack && component && cfg && arena_bytes, PXS_ERR_ARG,
-              "pxs_slat_flow_pack_plan: null argument");
-    Layout layout;
-    int rc = flow_plan(pack, component, dtype, *cfg, layout);
-    if (rc != PXS_OK) return rc;
-    *arena_bytes = layout.arena_bytes;
-    return PXS_OK;
+    return pxs::guarded("pxs_slat_flow_pack_plan", [&]() -> int {
+        PXS_CHECK(pack && component && cfg && arena_bytes, PXS_ERR_ARG,
+                  "pxs_slat_flow_pack_plan: null argument");
+        Layout layout;
+        int rc = flow_plan(pack, component, dtype, *cfg, layout);
+        if (rc != PXS_OK) return rc;
+        *arena_bytes = layout.arena_bytes;
+        return PXS_OK;
+    });
 }
 
 int pxs_slat_flow_pack_load(pxs_pack * pack, const char * component, int dtype, void * arena,
                             size_t arena_bytes, void * workspace, pxs_flow_weights * w,
                             pxs_block_weights * blocks, int max_blocks, void * stream) {
-    PXS_CHECK(pack && component && w && blocks, PXS_ERR_ARG,
-              "pxs_slat_flow_pack_load: null argument");
-    pxs_flow_config cfg;
-    Layout layout;
-    int rc = flow_plan(pack, component, dtype, cfg, layout);
-    if (rc != PXS_OK) return rc;
-    rc = check_arena(arena, arena_bytes, layout.arena_bytes, workspace, "pxs_slat_flow_pack_load");
-    if (rc != PXS_OK) return rc;
-    PXS_CHECK(max_blocks >= cfg.num_blocks, PXS_ERR_ARG,
-              "pxs_slat_flow_pack_load: blocks holds " + std::to_string(max_blocks) +
-                  " entries, the model has " + std::to_string(cfg.num_blocks));
-    rc = upload_all(pack, layout, arena, workspace, as_stream(stream), true);
-    if (rc != PXS_OK) return rc;
-    const int64_t C = cfg.model_channels, CC = cfg.cond_channels, M = cfg.mlp_hidden;
-    Binder b(layout, arena, "SLat flow");
-    std::memset(w, 0, sizeof(*w));
-    w->input_weight = b.mat32("input_layer.weight", C, cfg.in_channels);
-    w->input_bias = b.vec("input_layer.bias", C);
-    w->timestep_weight0 = b.mat32("t_embedder.mlp.0.weight", C, 256);
-    w->timestep_bias0 = b.vec("t_embedder.mlp.0.bias", C);
-    w->timestep_weight2 = b.mat32("t_embedder.mlp.2.weight", C, C);
-    w->timestep_bias2 = b.vec("t_embedder.mlp.2.bias", C);
-    w->modulation_weight = b.mat32("adaLN_modulation.1.weight", 6 * C, C);
-    w->modulation_bias = b.vec("adaLN_modulation.1.bias", 6 * C);
-    w->output_weight = b.mat32("out_layer.weight", cfg.out_channels, C);
-    w->output_bias = b.vec("out_layer.bias", cfg.out_channels);
-    for (int i = 0; i < cfg.num_blocks; ++i) {
-        const std::string p = "blocks." + std::to_string(i);
-        const std::string cross = p + ".cross_attn.cross_attn_block";
-        pxs_block_weights & k = blocks[i];
-        std::memset(&k, 0, sizeof(k));
-        k.modulation = b.vec(p + ".modulation", 6 * C);
-        k.self_to_qkv_weight = b.get(p + ".self_attn.to_qkv.weight", 3 * C, C);
-        k.self_to_qkv_bias = b.vec(p + ".self_attn.to_qkv.bias", 3 * C);
-        if (cfg.qk_rms_norm) {
-            k.self_q_gamma = b.vec(p + ".self_attn.q_rms_norm.gamma", C);
-            k.self_k_gamma = b.vec(p + ".self_attn.k_rms_norm.gamma", C);
+    return pxs::guarded("pxs_slat_flow_pack_load", [&]() -> int {
+        PXS_CHECK(pack && component && w && blocks, PXS_ERR_ARG,
+                  "pxs_slat_flow_pack_load: null argument");
+        pxs_flow_config cfg;
+        Layout layout;
+        int rc = flow_plan(pack, component, dtype, cfg, layout);
+        if (rc != PXS_OK) return rc;
+        rc = check_arena(arena, arena_bytes, layout.arena_bytes, workspace, "pxs_slat_flow_pack_load");
+        if (rc != PXS_OK) return rc;
+        PXS_CHECK(max_blocks >= cfg.num_blocks, PXS_ERR_ARG,
+                  "pxs_slat_flow_pack_load: blocks holds " + std::to_string(max_blocks) +
+                      " entries, the model has " + std::to_string(cfg.num_blocks));
+        rc = upload_all(pack, layout, arena, workspace, as_stream(stream), true);
+        if (rc != PXS_OK) return rc;
+        const int64_t C = cfg.model_channels, CC = cfg.cond_channels, M = cfg.mlp_hidden;
+        Binder b(layout, arena, "SLat flow");
+        std::memset(w, 0, sizeof(*w));
+        w->input_weight = b.mat32("input_layer.weight", C, cfg.in_channels);
+        w->input_bias = b.vec("input_layer.bias", C);
+        w->timestep_weight0 = b.mat32("t_embedder.mlp.0.weight", C, 256);
+        w->timestep_bias0 = b.vec("t_embedder.mlp.0.bias", C);
+        w->timestep_weight2 = b.mat32("t_embedder.mlp.2.weight", C, C);
+        w->timestep_bias2 = b.vec("t_embedder.mlp.2.bias", C);
+        w->modulation_weight = b.mat32("adaLN_modulation.1.weight", 6 * C, C);
+        w->modulation_bias = b.vec("adaLN_modulation.1.bias", 6 * C);
+        w->output_weight = b.mat32("out_layer.weight", cfg.out_channels, C);
+        w->output_bias = b.vec("out_layer.bias", cfg.out_channels);
+        for (int i = 0; i < cfg.num_blocks; ++i) {
+            const std::string p = "blocks." + std::to_string(i);
+            const std::string cross = p + ".cross_attn.cross_attn_block";
+            pxs_block_weights & k = blocks[i];
+            std::memset(&k, 0, sizeof(k));
+            k.modulation = b.vec(p + ".modulation", 6 * C);
+            k.self_to_qkv_weight = b.get(p + ".self_attn.to_qkv.weight", 3 * C, C);
+            k.self_to_qkv_bias = b.vec(p + ".self_attn.to_qkv.bias", 3 * C);
+            if (cfg.qk_rms_norm) {
+                k.self_q_gamma = b.vec(p + ".self_attn.q_rms_norm.gamma", C);
+                k.self_k_gamma = b.vec(p + ".self_attn.k_rms_norm.gamma", C);
+            }
+            k.self_to_out_weight = b.get(p + ".self_attn.to_out.weight", C, C);
+            k.self_to_out_bias = b.vec(p + ".self_attn.to_out.bias", C);
+            k.norm2_weight = b.vec(p + ".norm2.weight", C);
+            k.norm2_bias = b.vec(p + ".norm2.bias", C);
+            k.cross_to_q_weight = b.get(cross + ".to_q.weight", C, C);
+            k.cross_to_q_bias = b.vec(cross + ".to_q.bias", C);
+            k.cross_to_kv_weight = b.get(cross + ".to_kv.weight", 2 * C, CC);
+            k.cross_to_kv_bias = b.vec(cross + ".to_kv.bias", 2 * C);
+            if (cfg.qk_rms_norm_cross) {
+                k.cross_q_gamma = b.vec(cross + ".q_rms_norm.gamma", C);
+                k.cross_k_gamma = b.vec(cross + ".k_rms_norm.gamma", C);
+            }
+            k.cross_to_out_weight = b.get(cross + ".to_out.weight", C, C);
+            k.cross_to_out_bias = b.vec(cross + ".to_out.bias", C);
+            if (cfg.use_projection) {
+                k.proj_weight = b.get(p + ".cross_attn.proj_linear.weight", C, cfg.proj_in_channels);
+                k.proj_bias = b.vec(p + ".cross_attn.proj_linear.bias", C);
+            }
+            k.mlp0_weight = b.get(p + ".mlp.mlp.0.weight", M, C);
+            k.mlp0_bias = b.vec(p + ".mlp.mlp.0.bias", M);
+            k.mlp2_weight = b.get(p + ".mlp.mlp.2.weight", C, M);
+            k.mlp2_bias = b.vec(p + ".mlp.mlp.2.bias", C);
         }
-        k.self_to_out_weight = b.get(p + ".self_attn.to_out.weight", C, C);
-        k.self_to_out_bias = b.vec(p + ".self_attn.to_out.bias", C);
-        k.norm2_weight = b.vec(p + ".norm2.weight", C);
-        k.norm2_bias = b.vec(p + ".norm2.bias", C);
-        k.cross_to_q_weight = b.get(cross + ".to_q.weight", C, C);
-        k.cross_to_q_bias = b.vec(cross + ".to_q.bias", C);
-        k.cross_to_kv_weight = b.get(cross + ".to_kv.weight", 2 * C, CC);
-        k.cross_to_kv_bias = b.vec(cross + ".to_kv.bias", 2 * C);
-        if (cfg.qk_rms_norm_cross) {
-            k.cross_q_gamma = b.vec(cross + ".q_rms_norm.gamma", C);
-            k.cross_k_gamma = b.vec(cross + ".k_rms_norm.gamma", C);
-        }
-        k.cross_to_out_weight = b.get(cross + ".to_out.weight", C, C);
-        k.cross_to_out_bias = b.vec(cross + ".to_out.bias", C);
-        if (cfg.use_projection) {
-            k.proj_weight = b.get(p + ".cross_attn.proj_linear.weight", C, cfg.proj_in_channels);
-            k.proj_bias = b.vec(p + ".cross_attn.proj_linear.bias", C);
-        }
-        k.mlp0_weight = b.get(p + ".mlp.mlp.0.weight", M, C);
-        k.mlp0_bias = b.vec(p + ".mlp.mlp.0.bias", M);
-        k.mlp2_weight = b.get(p + ".mlp.mlp.2.weight", C, M);
-        k.mlp2_bias = b.vec(p + ".mlp.mlp.2.bias", C);
-    }
-    w->blocks = blocks;
-    return b.rc();
+        w->blocks = blocks;
+        return b.rc();
+    });
 }
 
 int pxs_slat_decoder_pack_plan(const pxs_pack * pack, const char * component, int dtype,
                                pxs_decoder_hparams * hp, size_t * arena_bytes) {
-    PXS_CHECK(pack && component && hp && arena_bytes, PXS_ERR_ARG,
-              "pxs_slat_decoder_pack_plan: null argument");
-    Layout layout;
-    int rc = decoder_plan(pack, component, dtype, *hp, layout);
-    if (rc != PXS_OK) return rc;
-    *arena_bytes = layout.arena_bytes;
-    return PXS_OK;
+    return pxs::guarded("pxs_slat_decoder_pack_plan", [&]() -> int {
+        PXS_CHECK(pack && component && hp && arena_bytes, PXS_ERR_ARG,
+                  "pxs_slat_decoder_pack_plan: null argument");
+        Layout layout;
+        int rc = decoder_plan(pack, component, dtype, *hp, layout);
+        if (rc != PXS_OK) return rc;
+        *arena_bytes = layout.arena_bytes;
+        return PXS_OK;
+    });
 }
 
 int pxs_slat_decoder_pack_load(pxs_pack * pack, const char * component, int dtype, void * arena,
                                size_t arena_bytes, void * workspace, pxs_decoder_block * blocks,
                                int max_blocks, const float ** io_weights, void * stream) {
-    PXS_CHECK(pack && component && blocks && io_weights, PXS_ERR_ARG,
-              "pxs_slat_decoder_pack_load: null argument");
-    pxs_decoder_hparams hp;
-    Layout layout;
-    int rc = decoder_plan(pack, component, dtype, hp, layout);
-    if (rc != PXS_OK) return rc;
-    rc = check_arena(arena, arena_bytes, layout.arena_bytes, workspace,
-                     "pxs_slat_decoder_pack_load");
-    if (rc != PXS_OK) return rc;
-    PXS_CHECK(max_blocks >= hp.n_blocks, PXS_ERR_ARG,
-              "pxs_slat_decoder_pack_load: blocks holds " + std::to_string(max_blocks) +
-                  " entries, the model has " + std::to_string(hp.n_blocks));
-    rc = upload_all(pack, layout, arena, workspace, as_stream(stream), false);
-    if (rc != PXS_OK) return rc;
-    // make_weights (src/slat_decoder.cpp:2911-2970).
-    Binder b(layout, arena, "SLat decoder");
-    const int L = hp.levels;
-    io_weights[0] = b.mat32("from_latent.weight", hp.model_channels[0], hp.latent_channels);
-    io_weights[1] = b.vec("from_latent.bias", hp.model_channels[0]);
-    io_weights[2] = b.mat32("output_layer.weight", hp.out_channels, hp.model_channels[L - 1]);
-    io_weights[3] = b.vec("output_layer.bias", hp.out_channels);
-    int n = 0;
-    for (int l = 0; l < L; ++l) {
-        const int64_t C = hp.model_channels[l];
-        for (int i = 0; i < hp.num_blocks[l]; ++i) {
-            const std::string p = "blocks." + std::to_string(l) + "." + std::to_string(i);
-            pxs_decoder_block & k = blocks[n++];
-            std::memset(&k, 0, sizeof(k));
-            k.kind = PXS_DECODER_CONVNEXT;
-            k.channels = static_cast<int>(C);
-            k.out_channels = static_cast<int>(C);
-            k.mlp_hidden = static_cast<int>(4 * C);
-            k.w.norm_weight = b.vec(p + ".norm.weight", C);
-            k.w.norm_bias = b.vec(p + ".norm.bias", C);
-            k.w.conv1_weight = b.get(p + ".conv.weight", C, C, 27);
-            k.w.conv1_bias = b.vec(p + ".conv.bias", C);
-            k.w.mlp0_weight = b.get(p + ".mlp.0.weight", 4 * C, C);
-            k.w.mlp0_bias = b.vec(p + ".mlp.0.bias", 4 * C);
-            k.w.mlp2_weight = b.get(p + ".mlp.2.weight", C, 4 * C);
-            k.w.mlp2_bias = b.vec(p + ".mlp.2.bias", C);
-        }
-        if (l + 1 < L) {
-            const int64_t O = hp.model_channels[l + 1];
-            const std::string p =
-                "blocks." + std::to_string(l) + "." + std::to_string(hp.num_blocks[l]);
-            pxs_decoder_block & k = blocks[n++];
-            std::memset(&k, 0, sizeof(k));
-            k.kind = PXS_DECODER_C2S;
-            k.channels = static_cast<int>(C);
-            k.out_channels = static_cast<int>(O);
-            k.w.norm1_weight = b.vec(p + ".norm1.weight", C);
-            k.w.norm1_bias = b.vec(p + ".norm1.bias", C);
-            k.w.conv1_weight = b.get(p + ".conv1.weight", 8 * O, C, 27);
-            k.w.conv1_bias = b.vec(p + ".conv1.bias", 8 * O);
-            k.w.conv2_weight = b.get(p + ".conv2.weight", O, O, 27);
-            k.w.conv2_bias = b.vec(p + ".conv2.bias", O);
-            if (hp.pred_subdiv) {
-                k.w.to_subdiv_weight = b.mat32(p + ".to_subdiv.weight", 8, C);
-                k.w.to_subdiv_bias = b.vec(p + ".to_subdiv.bias", 8);
+    return pxs::guarded("pxs_slat_decoder_pack_load", [&]() -> int {
+        PXS_CHECK(pack && component && blocks && io_weights, PXS_ERR_ARG,
+                  "pxs_slat_decoder_pack_load: null argument");
+        pxs_decoder_hparams hp;
+        Layout layout;
+        int rc = decoder_plan(pack, component, dtype, hp, layout);
+        if (rc != PXS_OK) return rc;
+        rc = check_arena(arena, arena_bytes, layout.arena_bytes, workspace,
+                         "pxs_slat_decoder_pack_load");
+        if (rc != PXS_OK) return rc;
+        PXS_CHECK(max_blocks >= hp.n_blocks, PXS_ERR_ARG,
+                  "pxs_slat_decoder_pack_load: blocks holds " + std::to_string(max_blocks) +
+                      " entries, the model has " + std::to_string(hp.n_blocks));
+        rc = upload_all(pack, layout, arena, workspace, as_stream(stream), false);
+        if (rc != PXS_OK) return rc;
+        // make_weights (src/slat_decoder.cpp:2911-2970).
+        Binder b(layout, arena, "SLat decoder");
+        const int L = hp.levels;
+        io_weights[0] = b.mat32("from_latent.weight", hp.model_channels[0], hp.latent_channels);
+        io_weights[1] = b.vec("from_latent.bias", hp.model_channels[0]);
+        io_weights[2] = b.mat32("output_layer.weight", hp.out_channels, hp.model_channels[L - 1]);
+        io_weights[3] = b.vec("output_layer.bias", hp.out_channels);
+        int n = 0;
+        for (int l = 0; l < L; ++l) {
+            const int64_t C = hp.model_channels[l];
+            for (int i = 0; i < hp.num_blocks[l]; ++i) {
+                const std::string p = "blocks." + std::to_string(l) + "." + std::to_string(i);
+                pxs_decoder_block & k = blocks[n++];
+                std::memset(&k, 0, sizeof(k));
+                k.kind = PXS_DECODER_CONVNEXT;
+                k.channels = static_cast<int>(C);
+                k.out_channels = static_cast<int>(C);
+                k.mlp_hidden = static_cast<int>(4 * C);
+                k.w.norm_weight = b.vec(p + ".norm.weight", C);
+                k.w.norm_bias = b.vec(p + ".norm.bias", C);
+                k.w.conv1_weight = b.get(p + ".conv.weight", C, C, 27);
+                k.w.conv1_bias = b.vec(p + ".conv.bias", C);
+                k.w.mlp0_weight = b.get(p + ".mlp.0.weight", 4 * C, C);
+                k.w.mlp0_bias = b.vec(p + ".mlp.0.bias", 4 * C);
+                k.w.mlp2_weight = b.get(p + ".mlp.2.weight", C, 4 * C);
+                k.w.mlp2_bias = b.vec(p + ".mlp.2.bias", C);
+            }
+            if (l + 1 < L) {
+                const int64_t O = hp.model_channels[l + 1];
+                const std::string p =
+                    "blocks." + std::to_string(l) + "." + std::to_string(hp.num_blocks[l]);
+                pxs_decoder_block & k = blocks[n++];
+                std::memset(&k, 0, sizeof(k));
+                k.kind = PXS_DECODER_C2S;
+                k.channels = static_cast<int>(C);
+                k.out_channels = static_cast<int>(O);
+                k.w.norm1_weight = b.vec(p + ".norm1.weight", C);
+                k.w.norm1_bias = b.vec(p + ".norm1.bias", C);
+                k.w.conv1_weight = b.get(p + ".conv1.weight", 8 * O, C, 27);
+                k.w.conv1_bias = b.vec(p + ".conv1.bias", 8 * O);
+                k.w.conv2_weight = b.get(p + ".conv2.weight", O, O, 27);
+                k.w.conv2_bias = b.vec(p + ".conv2.bias", O);
+                if (hp.pred_subdiv) {
+                    k.w.to_subdiv_weight = b.mat32(p + ".to_subdiv.weight", 8, C);
+                    k.w.to_subdiv_bias = b.vec(p + ".to_subdiv.bias", 8);
+                }
             }
         }
-    }
-    return b.rc();
+        return b.rc();
+    });
 }
 
 } // extern "C"

@@ -424,6 +424,14 @@ bool read_payload(int fd, const GgufFile & f, const GgufTensor & t, uint64_t off
     return true;
 }
 
+int guarded_fail(const char * what, const char * why) noexcept {
+    try {
+        return fail(PXS_ERR_ARG, std::string(what) + ": " + why);
+    } catch (...) {
+        return PXS_ERR_ARG;
+    }
+}
+
 } // namespace pxs
 
 // ---- drop-in pixal3d::load_pack_info / Pixal3DPackReader ------------------------
@@ -582,25 +590,27 @@ int copy_out(const std::string & s, char * buf, size_t len, const char * what) {
 extern "C" {
 
 int pxs_pack_open(const char * path, pxs_pack ** pack) {
-    PXS_CHECK(path && pack, PXS_ERR_ARG, "pxs_pack_open: null argument");
-    *pack = nullptr;
-    auto * p = new pxs_pack();
-    if (!pxs::parse_gguf(path, p->file)) {
-        delete p;
-        return pxs::fail(PXS_ERR_ARG, std::string("gguf_init_from_file failed: ") + path);
-    }
-    std::string error;
-    if (!pxs::validate_pack(p->file, p->info, &error)) {
-        delete p;
-        return pxs::fail(PXS_ERR_ARG, error);
-    }
-    p->fd = ::open(path, O_RDONLY | O_CLOEXEC);
-    if (p->fd < 0) {
-        delete p;
-        return pxs::fail(PXS_ERR_ARG, std::string("cannot open GGUF file: ") + path);
-    }
-    *pack = p;
-    return PXS_OK;
+    return pxs::guarded("pxs_pack_open", [&]() -> int {
+        PXS_CHECK(path && pack, PXS_ERR_ARG, "pxs_pack_open: null argument");
+        *pack = nullptr;
+        auto * p = new pxs_pack();
+        if (!pxs::parse_gguf(path, p->file)) {
+            delete p;
+            return pxs::fail(PXS_ERR_ARG, std::string("gguf_init_from_file failed: ") + path);
+        }
+        std::string error;
+        if (!pxs::validate_pack(p->file, p->info, &error)) {
+            delete p;
+            return pxs::fail(PXS_ERR_ARG, error);
+        }
+        p->fd = ::open(path, O_RDONLY | O_CLOEXEC);
+        if (p->fd < 0) {
+            delete p;
+            return pxs::fail(PXS_ERR_ARG, std::string("cannot open GGUF file: ") + path);
+        }
+        *pack = p;
+        return PXS_OK;
+    });
 }
 
 void pxs_pack_close(pxs_pack * pack) {
@@ -612,6 +622,7 @@ void pxs_pack_close(pxs_pack * pack) {
 
 size_t pxs_pack_describe(const pxs_pack * pack, char * buf, size_t len) {
     if (!pack) return 0;
+    try {
     const pixal3d::Pixal3DPackInfo & in = pack->info;
     std::string s = "{\"gguf_version\":" + std::to_string(in.gguf_version) +
                     ",\"alignment\":" + std::to_string(in.alignment) +
@@ -651,60 +662,74 @@ size_t pxs_pack_describe(const pxs_pack * pack, char * buf, size_t len) {
     s += "]}";
     if (buf && len > s.size()) std::memcpy(buf, s.c_str(), s.size() + 1);
     return s.size() + 1;
+    } catch (...) {
+        pxs::guarded_fail("pxs_pack_describe", "out of host memory");
+        return 0;
+    }
 }
 
 int pxs_pack_metadata_u32(const pxs_pack * pack, const char * key, int required,
                           uint32_t * value) {
-    PXS_CHECK(pack && key && value, PXS_ERR_ARG, "pxs_pack_metadata_u32: null argument");
-    std::string error;
-    if (!pxs::metadata_u32(pack->file, key, *value, required != 0, &error)) {
-        return pxs::fail(PXS_ERR_ARG, error);
-    }
-    return PXS_OK;
+    return pxs::guarded("pxs_pack_metadata_u32", [&]() -> int {
+        PXS_CHECK(pack && key && value, PXS_ERR_ARG, "pxs_pack_metadata_u32: null argument");
+        std::string error;
+        if (!pxs::metadata_u32(pack->file, key, *value, required != 0, &error)) {
+            return pxs::fail(PXS_ERR_ARG, error);
+        }
+        return PXS_OK;
+    });
 }
 
 int pxs_pack_metadata_f32(const pxs_pack * pack, const char * key, int required, float * value) {
-    PXS_CHECK(pack && key && value, PXS_ERR_ARG, "pxs_pack_metadata_f32: null argument");
-    std::string error;
-    if (!pxs::metadata_f32(pack->file, key, *value, required != 0, &error)) {
-        return pxs::fail(PXS_ERR_ARG, error);
-    }
-    return PXS_OK;
+    return pxs::guarded("pxs_pack_metadata_f32", [&]() -> int {
+        PXS_CHECK(pack && key && value, PXS_ERR_ARG, "pxs_pack_metadata_f32: null argument");
+        std::string error;
+        if (!pxs::metadata_f32(pack->file, key, *value, required != 0, &error)) {
+            return pxs::fail(PXS_ERR_ARG, error);
+        }
+        return PXS_OK;
+    });
 }
 
 int pxs_pack_metadata_bool(const pxs_pack * pack, const char * key, int required, int * value) {
-    PXS_CHECK(pack && key && value, PXS_ERR_ARG, "pxs_pack_metadata_bool: null argument");
-    std::string error;
-    bool v = false;
-    if (!pxs::metadata_bool(pack->file, key, v, required != 0, &error)) {
-        return pxs::fail(PXS_ERR_ARG, error);
-    }
-    *value = v ? 1 : 0;
-    return PXS_OK;
+    return pxs::guarded("pxs_pack_metadata_bool", [&]() -> int {
+        PXS_CHECK(pack && key && value, PXS_ERR_ARG, "pxs_pack_metadata_bool: null argument");
+        std::string error;
+        bool v = false;
+        if (!pxs::metadata_bool(pack->file, key, v, required != 0, &error)) {
+            return pxs::fail(PXS_ERR_ARG, error);
+        }
+        *value = v ? 1 : 0;
+        return PXS_OK;
+    });
 }
 
 int pxs_pack_metadata_string(const pxs_pack * pack, const char * key, int required, char * buf,
                              size_t len) {
-    PXS_CHECK(pack && key, PXS_ERR_ARG, "pxs_pack_metadata_string: null argument");
-    std::string error, v;
-    if (!pxs::metadata_string(pack->file, key, v, required != 0, &error)) {
-        return pxs::fail(PXS_ERR_ARG, error);
-    }
-    return copy_out(v, buf, len, "pxs_pack_metadata_string");
+    return pxs::guarded("pxs_pack_metadata_string", [&]() -> int {
+        PXS_CHECK(pack && key, PXS_ERR_ARG, "pxs_pack_metadata_string: null argument");
+        std::string error, v;
+        if (!pxs::metadata_string(pack->file, key, v, required != 0, &error)) {
+            return pxs::fail(PXS_ERR_ARG, error);
+        }
+        return copy_out(v, buf, len, "pxs_pack_metadata_string");
+    });
 }
 
 int pxs_pack_read_tensor(const pxs_pack * pack, const char * name, void * dst, size_t capacity,
                          size_t * n_bytes) {
-    PXS_CHECK(pack && name, PXS_ERR_ARG, "pxs_pack_read_tensor: null argument");
-    const pxs::GgufTensor * t = pack->file.tensor(name);
-    PXS_CHECK(t, PXS_ERR_ARG, std::string("tensor not found: ") + name);
-    if (n_bytes) *n_bytes = t->n_bytes;
-    PXS_CHECK(dst || t->n_bytes == 0, PXS_ERR_ARG, "pxs_pack_read_tensor: null destination");
-    PXS_CHECK(capacity >= t->n_bytes, PXS_ERR_ARG,
-              std::string("pxs_pack_read_tensor: destination too small for ") + name);
-    PXS_CHECK(t->n_bytes == 0 || pxs::read_payload(pack->fd, pack->file, *t, 0, dst, t->n_bytes),
-              PXS_ERR_ARG, std::string("short read for tensor: ") + name);
-    return PXS_OK;
+    return pxs::guarded("pxs_pack_read_tensor", [&]() -> int {
+        PXS_CHECK(pack && name, PXS_ERR_ARG, "pxs_pack_read_tensor: null argument");
+        const pxs::GgufTensor * t = pack->file.tensor(name);
+        PXS_CHECK(t, PXS_ERR_ARG, std::string("tensor not found: ") + name);
+        if (n_bytes) *n_bytes = t->n_bytes;
+        PXS_CHECK(dst || t->n_bytes == 0, PXS_ERR_ARG, "pxs_pack_read_tensor: null destination");
+        PXS_CHECK(capacity >= t->n_bytes, PXS_ERR_ARG,
+                  std::string("pxs_pack_read_tensor: destination too small for ") + name);
+        PXS_CHECK(t->n_bytes == 0 || pxs::read_payload(pack->fd, pack->file, *t, 0, dst, t->n_bytes),
+                  PXS_ERR_ARG, std::string("short read for tensor: ") + name);
+        return PXS_OK;
+    });
 }
 
 } // extern "C"

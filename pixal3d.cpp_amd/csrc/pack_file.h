@@ -6,6 +6,7 @@
 #include "pixal3d/pack.h"
 
 #include <cstdint>
+#include <new>
 #include <string>
 #include <unordered_map>
 #include <utility>
@@ -67,6 +68,19 @@ struct GgufFile {
 // Parse the container at `path` (header, metadata, tensor table; no payload)
 // with the checks of ggml's GGUF parser.  False for anything it rejects.
 bool parse_gguf(const std::string & path, GgufFile & out);
+
+// Runs a C-ABI body so that no C++ exception (an allocation failure) crosses
+// the C boundary: it becomes an error code with a message.
+int guarded_fail(const char * what, const char * why) noexcept;
+template <typename F> int guarded(const char * what, F && body) noexcept {
+    try {
+        return body();
+    } catch (const std::bad_alloc &) {
+        return guarded_fail(what, "out of host memory");
+    } catch (...) {
+        return guarded_fail(what, "unexpected host error");
+    }
+}
 
 // The Pixal3D checks on top of the container (src/pack.cpp:127-288), with
 // the reference's messages.

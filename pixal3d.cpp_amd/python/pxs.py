@@ -777,7 +777,8 @@ class Pack:
         n = self.lib.pxs_pack_describe(self.handle, None, 0)
         buf = C.create_string_buffer(n)
         self.lib.pxs_pack_describe(self.handle, buf, n)
-        return json.loads(buf.value.decode("utf-8"))
+        # Tensor names are bytes; keep ones that are not UTF-8 round-trippable.
+        return json.loads(buf.value.decode("utf-8", errors="surrogateescape"))
 
     def metadata(self, key, kind, required=True):
         """kind: "u32", "f32", "bool" or "string"."""
