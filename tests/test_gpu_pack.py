@@ -404,3 +404,69 @@ def test_flow_pack_load_alignment_8(px, tmp_path):
             packed = px.slat_flow_pack_load(pack, "shape_flow_1024", dtype)
         torch.cuda.synchronize()
         check_flow_arena(packed, info8, "sh1024", dtype)
+
+
+def test_flow_pack_load_projection_mode(px, tmp_path):
+    """image_attn_mode proj: the block's proj_linear weights are bound (in
+    the GEMM dtype) and the forward with a projection input equals the
+    forward over the same weights uploaded directly."""
+    info = G.load_pack_info(golden("pack_flow_f16"))
+    C, PC = 16, 12
+    rng = np.random.default_rng(31)
+    pw = (rng.standard_normal((C, PC)) * 0.2).astype(np.float32)
+    pb = (rng.standard_normal(C) * 0.1).astype(np.float32)
+    kvs = [(k, vt, v) for k, (vt, v) in info.kv.items()
+           if k != "pixal3d.shape_flow_1024.image_attn_mode"]
+    kvs += [("pixal3d.shape_flow_1024.image_attn_mode", G.VT_STRING, "proj"),
+            ("pixal3d.shape_flow_1024.proj_in_channels", G.VT_U32, PC)]
+    tensors = [G.Tensor(t.name, t.ggml_type, t.ne[:max(t.n_dims, 1)], G.read_tensor(info, t.name))
+               for t in info.tensors]
+    tensors += [G.f32_tensor("sh1024.blocks.0.cross_attn.proj_linear.weight", pw, G.GGML_F16),
+                G.f32_tensor("sh1024.blocks.0.cross_attn.proj_linear.bias", pb)]
+    path = tmp_path / "proj.gguf"
+    G.write_pack(path, kvs, tensors)
+    info_p = G.load_pack_info(path)
+    for dtype in (pxs.PXS_F32, pxs.PXS_BF16):
+        tdt = torch.bfloat16 if dtype == pxs.PXS_BF16 else torch.float32
+        with px.pack_open(path) as pack:
+            packed = px.slat_flow_pack_load(pack, "shape_flow_1024", dtype)
+        cfg = packed.cfg
+        assert (cfg.use_projection, cfg.proj_in_channels) == (1, PC)
+        check_flow_arena(packed, info_p, "sh1024", dtype)
+        direct, keep = direct_flow(info_p, "sh1024", cfg.num_blocks, dtype)
+        coords, x, t, ctx, ctx_off = flow_inputs(cfg, tdt)
+        proj = t32(W.normal(5, coords.shape[0] * PC, 9).reshape(-1, PC)).to(tdt)
+        cu = px.batch_cu_seqlens(coords, 2)
+        a = px.slat_flow_forward(cfg, packed.weights, coords, 2, cu, x, t, ctx, ctx_off,
+                                 projected=proj, dtype=dtype)
+        b = px.slat_flow_forward(cfg, direct, coords, 2, cu, x, t, ctx, ctx_off, projected=proj,
+                                 dtype=dtype)
+        torch.cuda.synchronize()
+        assert torch.isfinite(a).all()
+        np.testing.assert_array_equal(bits_of(a), bits_of(b))
+
+
+def test_decoder_pack_load_without_subdivision_head(px, tmp_path):
+    """pred_subdiv false: the C2S block binds no to_subdiv tensors (the pack
+    may omit them) and the decoder runs with given subdivisions."""
+    info = G.load_pack_info(golden("pack_decoder_f16"))
+    kvs = [(k, vt, (False if k == "pixal3d.texture_decoder.pred_subdiv" else v))
+           for k, (vt, v) in info.kv.items()]
+    tensors = [G.Tensor(t.name, t.ggml_type, t.ne[:max(t.n_dims, 1)], G.read_tensor(info, t.name))
+               for t in info.tensors if "to_subdiv" not in t.name]
+    path = tmp_path / "nosub.gguf"
+    G.write_pack(path, kvs, tensors)
+    with px.pack_open(path) as pack:
+        packed = px.slat_decoder_pack_load(pack, "texture_decoder", pxs.PXS_F32)
+    assert packed.hp.pred_subdiv == 0
+    c2s = packed.blocks[1]
+    assert not c2s.w.to_subdiv_weight and not c2s.w.to_subdiv_bias
+    coords = W.shell_coords(12, [[(3.0, 4.5)], [(2.5, 4.0)]], 22)
+    n = coords.shape[0]
+    x = t32(W.normal(22, n * 8, 1).reshape(-1, 8))
+    guide = t32((W.uniform(22, n * 8, 2).reshape(n, 8) > 0.5).astype(np.float32))
+    out_coords, y, level_rows, _ = px.slat_decoder_forward(
+        pxs.PXS_F32, packed.config(), *packed.io, packed.blocks, ti32(coords), x, guide=[guide])
+    torch.cuda.synchronize()
+    assert level_rows[0] == n and level_rows[1] == int(host(guide).sum())
+    assert torch.isfinite(y).all() and y.shape[1] == packed.hp.out_channels
