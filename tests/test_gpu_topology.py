@@ -231,3 +231,39 @@ def test_channel_to_spatial_factor3(px, orc):
     roc, ry = orc.channel_to_spatial(coords, x, 3, sub)
     np.testing.assert_array_equal(oc.cpu().numpy(), roc)
     np.testing.assert_array_equal(host(y), ry)
+
+
+def max_extent_coords():
+    """Rows at the edges of the largest extents the voxel key holds
+    (PXS_MAX_EXTENT = 32768 per axis and for the batch): neighbours across
+    x = 32767 / z = 32767 and in the last batch item."""
+    M = 32767
+    rows = [(0, 0, 0, 0), (0, 0, 0, 1), (0, 0, M, M - 1), (0, 0, M, M), (0, 1, M, M),
+            (0, M, 0, 0), (0, M, M, M - 1), (0, M, M, M), (M, M - 1, M, M), (M, M, M, M)]
+    return np.array(sorted(rows), np.int32)
+
+
+def test_max_extent_coordinates(px, orc):
+    coords = max_extent_coords()
+    c = ti32(coords)
+    nbr, masks = px.neighbor_map(c)
+    ref = orc.neighbor_map(coords)
+    np.testing.assert_array_equal(nbr.cpu().numpy(), ref)
+    n = coords.shape[0]
+    assert (ref != n).sum() > n  # the neighbours across the far faces are found
+    shape = (32768, 32768, 32768)
+    assert px.validate(c, 32768, shape) == (0, -1)
+    f = W.normal(3, n * 2, 1).reshape(n, 2)
+    assert orc.sparse_valid(coords, 32768, shape, f, 2) == (0, -1)
+    # a z extent of 32767 puts the rows at z = 32767 outside the shape: the
+    # first of them is reported, as the reference does
+    got = px.validate(c, 32768, (32768, 32768, 32767), t32(f))
+    assert got == orc.sparse_valid(coords, 32768, (32768, 32768, 32767), f, 2) == (4, 3)
+
+
+@pytest.mark.parametrize("dims", [(32769, 8, 8, 8), (1, 8, 32769, 8), (1, 8, 8, 40000)])
+def test_extents_beyond_the_key_are_rejected(px, dims):
+    import pxs
+    coords = ti32(np.array([[0, 1, 1, 1]], np.int32))
+    with pytest.raises(pxs.PxsError, match="extent exceeds PXS_MAX_EXTENT"):
+        px.validate(coords, dims[0], dims[1:])
