@@ -71,8 +71,12 @@ def align(value, alignment):
 
 # --- writer ------------------------------------------------------------------------
 
+def _utf8(value):
+    return value.encode("utf-8", errors="surrogateescape")
+
+
 def gguf_string(value):
-    raw = value.encode("utf-8") if isinstance(value, str) else bytes(value)
+    raw = _utf8(value) if isinstance(value, str) else bytes(value)
     return struct.pack("<Q", len(raw)) + raw
 
 
@@ -217,7 +221,9 @@ class _Cursor:
         return struct.unpack(fmt, self.take(struct.calcsize(fmt)))[0]
 
     def string(self):
-        return self.take(self.unpack("<Q")).decode("utf-8")
+        # GGUF strings are bytes (ggml does not check their encoding); keep
+        # them round-trippable.
+        return self.take(self.unpack("<Q")).decode("utf-8", errors="surrogateescape")
 
 
 def _value(cur, vtype, nested=False):
@@ -271,7 +277,7 @@ def parse_container(data):
         tensors, names = [], set()
         for _ in range(n_tensors):
             name = cur.string()
-            if len(name.encode("utf-8")) >= GGML_MAX_NAME or name in names:
+            if len(_utf8(name)) >= GGML_MAX_NAME or name in names:
                 raise ValueError("name")
             names.add(name)
             n_dims = cur.unpack("<I")
@@ -296,7 +302,7 @@ def parse_container(data):
             if offset != running:
                 raise ValueError("offset")
             running += align(tensor_nbytes(gtype, ne), alignment)
-    except (EOFError, UnicodeDecodeError, struct.error):
+    except (EOFError, struct.error):
         raise ValueError("truncated")
     return version, kv, tensors, alignment, data_offset
 
@@ -374,7 +380,7 @@ def load_pack_info(path):
         raise PackError("GGUF tensor data offset is beyond end of file")
     names = set()
     for name, ne, gtype, offset in table:
-        if not name or len(name.encode("utf-8")) >= GGML_MAX_NAME or name in names:
+        if not name or len(_utf8(name)) >= GGML_MAX_NAME or name in names:
             raise PackError("GGUF tensor names must be non-empty, unique, and <64 bytes")
         names.add(name)
         nbytes = tensor_nbytes(gtype, ne)

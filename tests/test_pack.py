@@ -397,7 +397,7 @@ def library_open(px, path):
     h = C.c_void_p()
     rc = px.lib.pxs_pack_open(str(path).encode(), C.byref(h))
     if rc != 0:
-        return None, px.lib.pxs_last_error().decode()
+        return None, px.lib.pxs_last_error().decode("utf-8", errors="surrogateescape")
     return h, None
 
 
@@ -622,3 +622,66 @@ def test_decoder_plan_errors(px, tmp_path, case):
     with pytest.raises(pxs.PxsError) as e:
         decoder_plan(px, path, "texture_decoder" if component is None else component)
     assert str(e.value) == want
+
+
+# --- fuzzing the parser ------------------------------------------------------------
+
+from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import strategies as st  # noqa: E402
+
+_FUZZ_BASE = {stem: golden(stem).read_bytes() for stem in ("pack_flow_f16", "pack_decoder_f16")}
+
+
+@st.composite
+def mutated_pack(draw):
+    """A golden pack with a few random edits: byte overwrites (biased to the
+    header and tensor table, where the parser decides), a truncation, or a
+    spliced run of bytes."""
+    stem = draw(st.sampled_from(sorted(_FUZZ_BASE)))
+    data = bytearray(_FUZZ_BASE[stem])
+    head = G.load_pack_info(golden(stem)).data_offset
+    for _ in range(draw(st.integers(1, 4))):
+        kind = draw(st.sampled_from(["byte", "byte", "byte", "truncate", "splice", "u64"]))
+        lim = min(head, len(data))
+        if kind == "byte":
+            at = draw(st.integers(0, lim - 1))
+            data[at] = draw(st.integers(0, 255))
+        elif kind == "u64":
+            if lim < 8:
+                continue
+            at = draw(st.integers(0, lim - 8))
+            data[at:at + 8] = draw(st.sampled_from([
+                (2 ** 63 - 1).to_bytes(8, "little"), (2 ** 64 - 1).to_bytes(8, "little"),
+                (1 << 40).to_bytes(8, "little"), (0).to_bytes(8, "little")]))
+        elif kind == "truncate":
+            del data[draw(st.integers(0, len(data) - 1)):]
+        else:
+            at = draw(st.integers(0, lim))
+            data[at:at] = draw(st.binary(min_size=1, max_size=24))
+        if not data:
+            break
+    return bytes(data)
+
+
+@settings(max_examples=400, derandomize=True, deadline=None,
+          suppress_health_check=[HealthCheck.function_scoped_fixture, HealthCheck.too_slow])
+@given(data=mutated_pack())
+def test_parser_fuzz_matches_oracle(px, tmp_path, data):
+    """Random damage to a real pack: the library neither crashes nor reads
+    past the file, and its verdict (and message) equals the oracle's."""
+    path = tmp_path / "fuzz.gguf"
+    path.write_bytes(data)
+    try:
+        info, want = G.load_pack_info(path), None
+    except G.PackError as e:
+        info, want = None, str(e)
+    h, got = library_open(px, path)
+    assert got == want
+    if h is not None:
+        n = px.lib.pxs_pack_describe(h, None, 0)
+        buf = C.create_string_buffer(n)
+        px.lib.pxs_pack_describe(h, buf, n)
+        d = json.loads(buf.value.decode("utf-8", errors="surrogateescape"))
+        px.lib.pxs_pack_close(h)
+        assert [t["name"] for t in d["tensors"]] == [t.name for t in info.tensors]
+        assert [t["offset"] for t in d["tensors"]] == [t.offset for t in info.tensors]
