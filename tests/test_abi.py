@@ -71,3 +71,38 @@ def test_fp32_gemm_path_never_falls_back_to_cpu():
                          text=True).stdout
     assert "libamdhip64" in out
     assert "liboracle" not in out and "pixal3d_ref" not in out
+
+
+C_PROGRAM = r"""
+#include "pxs.h"
+#include <stdio.h>
+#include <string.h>
+int main(void) {
+    pxs_pack * pack = NULL;
+    pxs_flow_config cfg;
+    pxs_decoder_hparams hp;
+    pxs_block_weights bw;
+    pxs_decoder_block db;
+    memset(&cfg, 0, sizeof cfg);
+    memset(&hp, 0, sizeof hp);
+    memset(&bw, 0, sizeof bw);
+    memset(&db, 0, sizeof db);
+    if (pxs_pack_open("/nonexistent/pack.gguf", &pack) == PXS_OK) return 1;
+    printf("%s|%d\n", pxs_last_error(), pxs_version());
+    return 0;
+}
+"""
+
+
+def test_c_abi_header_is_plain_c(tmp_path):
+    """include/pxs.h compiles as strict C99 (no C++ in the C ABI) and a C
+    program links against libpxs.so and calls it (a host-only call)."""
+    src = tmp_path / "abi.c"
+    src.write_text(C_PROGRAM)
+    exe = tmp_path / "abi"
+    lib_dir = str(pxs.LIB_PATH.parent)
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror",
+                    "-I", str(ROOT / "include"), str(src), "-L", lib_dir, "-lpxs",
+                    f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    assert out.strip() == "gguf_init_from_file failed: /nonexistent/pack.gguf|1"
