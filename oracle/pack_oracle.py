@@ -1,8 +1,8 @@
 """GGUF v3 pack restatement: writer, validating reader and payload decoding.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/ and bench.py's cpu_baseline leg
-as the checker of the pack ingestion path; the shipped library never imports
-it.
+TEST INFRASTRUCTURE ONLY: imported by tests/ and __graft_entry__.smoke() as
+the checker of the pack ingestion path; the shipped library and the measured
+path never import it.
 
 What it restates:
 
