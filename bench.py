@@ -381,7 +381,7 @@ def conv_fp32_64(args, torch, px, W):
 
 
 def attn_block(args, torch, px, W):
-    """Config 3: QKV linear 1024->3072, per-head RMS on q/k, varlen attention on
+    """Attention block: QKV linear 1024->3072, per-head RMS on q/k, varlen attention on
     12,288 + 20,480 tokens (16 x 64), output linear 1024->1024, bf16."""
     dev = torch.device("cuda:0")
     wl = W.attn_full()
@@ -419,7 +419,7 @@ def attn_block(args, torch, px, W):
 
 
 def swin_64(args, torch, px, W):
-    """Config 4: two shifted-window attention blocks (window 8, shift 0 then 4,
+    """Two shifted-window attention blocks (window 8, shift 0 then 4,
     12 x 64, width 768) on ~28k voxels at 64^3, then the channel-to-spatial
     upsample: SubMConv3d 768 -> 8*192 at 64^3 and subdivision to 128^3."""
     dev = torch.device("cuda:0")
@@ -478,7 +478,7 @@ def swin_64(args, torch, px, W):
 
 
 def flow_model(torch, px, W):
-    """Config 5's SLat-flow model (24 blocks, width 1024, 16 x 64, MLP 4096) on
+    """The 24-block SLat-flow model (width 1024, 16 x 64 heads, MLP 4096) on
     ~42k voxels at 64^3 with random N(0, 0.02) weights, bf16 GEMM operands."""
     import pxs as P
 
@@ -517,7 +517,7 @@ def flow_model(torch, px, W):
 
 
 def flow_step(args, torch, px, W):
-    """Config 5: one SLat-flow forward (24 blocks, width 1024) on ~42k voxels,
+    """One SLat-flow forward (24 blocks, width 1024) on ~42k voxels,
     device resident (pxs_slat_flow_forward), random N(0, 0.02) weights."""
     import pxs as P
 
@@ -547,7 +547,7 @@ def flow_step(args, torch, px, W):
 
 
 def flow_sample(args, torch, px, W):
-    """Guided flow-Euler sampling with config 5's model (pxs_flow_euler_sample):
+    """Guided flow-Euler sampling with the 24-block width-1024 SLat-flow model (pxs_flow_euler_sample):
     2 Euler steps at guidance 7.5 with CFG rescale 0.7, each step ONE forward
     over the doubled batch (conditional + unconditional, ~84k tokens); the same
     steps composed from two separate forwards are timed beside it."""
@@ -588,7 +588,7 @@ def flow_sample(args, torch, px, W):
     tf = flops / dt / 1e12
     return {"metric": "SLat-flow guided sampling TFLOP/s, bf16", "value": round(tf, 2),
             "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "bf16",
-            "config": {"workload": f"flow_sample: {n} voxels at 64^3, config-5 model, {steps} "
+            "config": {"workload": f"flow_sample: {n} voxels at 64^3, 24-block width-1024 model, {steps} "
                                    f"Euler steps, guidance 7.5, CFG rescale 0.7, 1,370 context "
                                    f"tokens (uncond: zeros)",
                        "ms_per_euler_step": round(dt * 1e3 / steps, 3),
@@ -600,7 +600,7 @@ def flow_sample(args, torch, px, W):
 
 
 def pack_load(args, torch, px, W):
-    """GGUF ingestion of config 5's SLat-flow component (width 1024, 24
+    """GGUF ingestion of a SLat-flow component (width 1024, 24
     blocks, F32 storage as the deployed flow packs hold it, 1.6 GB):
     pxs_slat_flow_pack_load from a pack in the page cache into an HBM arena,
     block linears converted to bf16.  A step is one whole load; the pack is
@@ -765,7 +765,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              f"(the sparse path shards by segment and by spatial slab; see DESIGN.md)",
+              f"(the sparse path would shard by segment and by spatial slab)",
               file=sys.stderr)
         sys.exit(2)
     import torch

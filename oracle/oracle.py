@@ -1,8 +1,8 @@
 """ctypes bindings for the CPU oracle and the compiled reference.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker.  The shipped library never
-imports this module.
+cpu_baseline leg of bench.py, to check and time against.  The shipped
+library never imports this module.
 
 * ``Oracle`` wraps build/liboracle.so, this repository's C++ restatement of
   the reference CPU path (pxs_oracle.cpp, with per-function citations).

@@ -1,7 +1,7 @@
 """GGUF v3 pack restatement: writer, validating reader and payload decoding.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/ and __graft_entry__.smoke() as
-the checker of the pack ingestion path; the shipped library and the measured
+TEST INFRASTRUCTURE ONLY: imported by tests/ and __graft_entry__.smoke() to
+check the pack ingestion path against; the shipped library and the measured
 path never import it.
 
 What it restates:

@@ -1,7 +1,8 @@
 // pxs oracle: a CPU restatement of the reference sparse-voxel path.
 //
 // TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
-// cpu_baseline leg of bench.py load this library, and only as the checker.
+// cpu_baseline leg of bench.py load this library, and only as the reference
+// that results are compared with.
 // The shipped library (pixal3d.cpp_amd/) never links, loads or calls it.
 //
 // Every function restates the reference algorithm with the reference's loop

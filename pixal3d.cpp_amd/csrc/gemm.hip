@@ -647,7 +647,7 @@ gather_gemm_lds_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// fp32 split-K gather GEMM for small and medium problems (config-1 sized
+// fp32 split-K gather GEMM for small and medium problems (16k-voxel, 64-channel
 // convolutions, fp32 linears).  A workgroup owns 32 output rows x 64 output
 // channels; its (offset, 32-channel chunk) steps are dealt round-robin to
 // the 4 waves, so even a few hundred tiles keep every CU busy.  Each wave

@@ -7,7 +7,7 @@ axis-aligned ellipsoids of two-voxel thickness: a voxel v is active when
 |rho - 1| * min(a) < 1 with rho = ||(v + 0.5 - c) / a||.  Rows are sorted
 lexicographically by (batch, x, y, z).
 
-Workloads (sizes are the BASELINE configurations of the sparse path):
+Workloads (the sizes of the sparse path's benchmark workloads):
   conv_fp32_64     one 3x3x3 submanifold conv, fp32, 64^3 grid, one shell with
                    semi-axes U[16,30], C 64 -> 64
   unet_stage_128   batch 2 on a 128^3 grid, each item a union of 3 shells;

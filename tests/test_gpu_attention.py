@@ -97,7 +97,7 @@ def test_attention_bf16_late_score_jump(px, orc, jump):
 
 
 def test_attention_bf16_full_size_sampled_rows(px, orc):
-    """Config-3 attention at full size (12,288 + 20,480 tokens, 16 x 64),
+    """Full attention at full size (12,288 + 20,480 tokens, 16 x 64),
     checked exactly on sampled query rows by the oracle."""
     wl = W.attn_full()
     n, C = wl["x"].shape

@@ -76,7 +76,7 @@ def test_conv_bf16_vs_oracle(px, orc, cin, cout):
 
 
 def test_conv_bf16_unet_full_size_sampled_rows(px):
-    """Config-2 op A at full size (~160k voxels, 128 -> 128): sampled output rows
+    """The U-Net stage's op A at full size (~160k voxels, 128 -> 128): sampled output rows
     recomputed in float64 from the GPU neighbor map (itself bit-exact vs the
     oracle), plus the centre-identity property on every row."""
     wl = W.unet_stage_128()
@@ -190,7 +190,7 @@ def test_downsample_mean_matches_reference_vectors(px):
 
 
 def test_unet_stage_strided_full_size(px):
-    """Config-2 op B at full size, sampled outputs in float64."""
+    """The U-Net stage's op B (stride-2 conv 128 -> 256) at full size, sampled outputs in float64."""
     wl = W.unet_stage_128()
     coords, x, w = wl["coords"], wl["feats"], wl["w_b"]
     oc, child, m = px.downsample_s2(ti32(coords), 2, (128, 128, 128))
@@ -206,7 +206,7 @@ def test_unet_stage_strided_full_size(px):
 
 
 def test_unet_stage_conv_c_full_size(px):
-    """Config-2 op C at full size (SubMConv3d 256 -> 256 on the ~40k coarse
+    """The U-Net stage's op C at full size (SubMConv3d 256 -> 256 on the ~40k coarse
     voxels, 128 x 256 tiles): sampled rows in float64, plus the exact centre
     identity on every row."""
     wl = W.unet_stage_128()
