@@ -632,7 +632,7 @@ int pxs_pack_read_tensor(const pxs_pack * pack, const char * name, void * dst, s
                          size_t * n_bytes);
 
 /* Device workspace of the upload calls below (two 16 MiB staging chunks and
- * one flag per tensor of the pack). */
+ * one flag per tensor of the pack); it must be 16-byte aligned. */
 size_t pxs_pack_upload_workspace_bytes(const pxs_pack * pack);
 
 /* read_tensor_f32 (src/slat_flow.cpp:360-395) onto the device: an F32, F16

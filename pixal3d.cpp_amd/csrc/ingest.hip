@@ -150,6 +150,9 @@ Ingest::~Ingest() {
 }
 
 int Ingest::begin() {
+    // The conversion kernel reads the staging chunks with 16-byte loads.
+    PXS_CHECK(reinterpret_cast<uintptr_t>(workspace_) % 16 == 0, PXS_ERR_ARG,
+              "pack upload: workspace must be 16-byte aligned");
     if (!pack_->host_stage) {
         int rc = check_hip(hipHostMalloc(&pack_->host_stage, stage_bytes(), hipHostMallocDefault),
                            "hipHostMalloc(pack staging)");
@@ -345,7 +348,8 @@ int pxs_pack_upload(pxs_pack * pack, const char * name, int dtype, void * dst, i
         if (elements == 0) return PXS_OK;
         Ingest ingest(pack, workspace, 1, as_stream(stream));
         int rc = ingest.begin();
-        if (rc == PXS_OK) rc = ingest.run({IngestItem{t, dtype, dst, 0}});
+        if (rc != PXS_OK) return rc;  // nothing enqueued
+        rc = ingest.run({IngestItem{t, dtype, dst, 0}});
         std::vector<int32_t> flags;
         const int frc = ingest.finish(flags);
         if (rc != PXS_OK) return rc;

@@ -16,6 +16,7 @@ import torch
 PKG = Path(__file__).resolve().parents[1]
 LIB_PATH = Path(os.environ.get("PXS_LIB", PKG / "lib" / "libpxs.so"))
 
+PXS_OK, PXS_ERR_ARG, PXS_ERR_HIP, PXS_ERR_DATA = 0, 1, 2, 3
 PXS_F32, PXS_BF16 = 0, 1
 ACT_NONE, ACT_GELU_TANH, ACT_SILU = 0, 1, 2
 

@@ -101,6 +101,13 @@ def test_upload_errors(px, tmp_path):
             pack.upload("f32_mix", pxs.PXS_F32, 1048)
         with pytest.raises(pxs.PxsError, match="tensor not found: nope"):
             pack.upload("nope", pxs.PXS_F32, 1)
+        ws = torch.empty(px.lib.pxs_pack_upload_workspace_bytes(pack.handle) + 16,
+                         dtype=torch.uint8, device="cuda")
+        y = torch.empty(777, dtype=torch.float32, device="cuda")
+        rc = px.lib.pxs_pack_upload(pack.handle, b"bf16_rand", pxs.PXS_F32, y.data_ptr(), 777,
+                                    ws.data_ptr() + 8, px.stream())
+        assert rc == pxs.PXS_ERR_ARG
+        assert px.lib.pxs_last_error().decode() == "pack upload: workspace must be 16-byte aligned"
         # the pack stays usable after an error
         got = pack.upload("bf16_rand", pxs.PXS_F32, 777)
         assert torch.isfinite(got).all()

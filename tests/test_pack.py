@@ -147,6 +147,23 @@ def test_library_reader_matches_oracle(px, stem):
         assert pack.metadata(prefix + "absent", "string", required=False) == ""
 
 
+def test_upload_rejects_misaligned_workspace(px):
+    """The staging workspace is read with 16-byte loads: a workspace that is
+    not 16-byte aligned is an argument error, raised before any device work
+    (so the call runs here without a device; the pointers are never
+    dereferenced)."""
+    path = golden("pack_flow_f16")
+    info = G.load_pack_info(path)
+    t = next(t for t in info.tensors if t.ggml_type == G.GGML_F32)
+    count = t.n_bytes // 4
+    with px.pack_open(path) as pack:
+        rc = px.lib.pxs_pack_upload(pack.handle, t.name.encode(), pxs.PXS_F32, 1 << 20, count,
+                                    (1 << 20) + 8, None)
+        assert rc == pxs.PXS_ERR_ARG
+        assert px.lib.pxs_last_error().decode() == \
+            "pack upload: workspace must be 16-byte aligned"
+
+
 def reference_case_pack(path):
     """The pack tests/test_pack_reader.cpp:29-49 writes: one F32 [2, 3]
     tensor ss.input_layer.bias in an otherwise empty compact-v1 pack."""
