@@ -9,8 +9,10 @@
  *     are reported before anything is enqueued.
  *   - Calls are asynchronous on `stream` unless stated; none of them allocate
  *     device memory: scratch comes from a caller-provided workspace sized by
- *     the matching *_workspace_bytes query.  (A pack's first upload allocates
- *     its 32 MiB of pinned host staging, freed by pxs_pack_close.)
+ *     the matching *_workspace_bytes query, 256-byte aligned (as hipMalloc
+ *     returns; a misaligned one is an argument error).  (A pack's first
+ *     upload allocates its 32 MiB of pinned host staging, freed by
+ *     pxs_pack_close.)
  *   - Coordinates are int32 rows (batch, x, y, z).  Features are row-major
  *     [rows, channels].  PXS_BF16 data is stored as raw bfloat16 bit
  *     patterns (uint16); arithmetic accumulates in fp32.
@@ -632,7 +634,7 @@ int pxs_pack_read_tensor(const pxs_pack * pack, const char * name, void * dst, s
                          size_t * n_bytes);
 
 /* Device workspace of the upload calls below (two 16 MiB staging chunks and
- * one flag per tensor of the pack); it must be 16-byte aligned. */
+ * one flag per tensor of the pack). */
 size_t pxs_pack_upload_workspace_bytes(const pxs_pack * pack);
 
 /* read_tensor_f32 (src/slat_flow.cpp:360-395) onto the device: an F32, F16

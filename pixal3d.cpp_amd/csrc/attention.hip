@@ -730,6 +730,7 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
                          const int64_t * cu_k, int nseg, int64_t total_q,
                          const int32_t * row_map, int heads, int head_dim, int value_dim,
                          float scale, void * o, int64_t ld_o, void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_varlen_attention");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_varlen_attention: bad dtype");
     PXS_CHECK(heads > 0 && head_dim > 0 && head_dim <= 64 && value_dim > 0 && value_dim <= 64,
               PXS_ERR_ARG, "pxs_varlen_attention: head_dim and value_dim must be in 1..64");

@@ -210,6 +210,7 @@ int pxs_transformer_block(int dtype, const pxs_block_config * cfg, const pxs_blo
                           const void * context, const int64_t * context_offsets,
                           int64_t context_tokens, const void * projected, void * workspace,
                           void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_transformer_block");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG,
               "pxs_transformer_block: bad dtype");
     PXS_TRY(check_block_args(cfg, w));
@@ -240,6 +241,7 @@ int pxs_slat_flow_forward(int dtype, const pxs_flow_config * cfg, const pxs_flow
                           const void * context, const int64_t * context_offsets,
                           int64_t context_tokens, const void * projected, float * out,
                           void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_slat_flow_forward");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG,
               "pxs_slat_flow_forward: bad dtype");
     PXS_CHECK(cfg && w, PXS_ERR_ARG, "pxs_slat_flow_forward: null config or weights");

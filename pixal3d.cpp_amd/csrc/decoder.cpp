@@ -155,6 +155,7 @@ int pxs_convnext_block(int dtype, const int32_t * coords, int64_t rows, const fl
                        int channels, int mlp_hidden, float eps,
                        const pxs_decoder_block_weights * w, const int32_t * nbr,
                        const uint32_t * masks, float * y, void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_convnext_block");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_convnext_block: bad dtype");
     PXS_CHECK(eps > 0.0f && std::isfinite(eps), PXS_ERR_ARG,
               "SLat decoder norm epsilon must be finite and positive");
@@ -217,6 +218,7 @@ int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const floa
                      const pxs_decoder_block_weights * w, int pred_subdiv,
                      const float * subdivision, float * predicted_subdiv, int32_t * out_coords,
                      float * y, int64_t * rows_out, void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_resblock_c2s");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_resblock_c2s: bad dtype");
     PXS_CHECK(eps > 0.0f && std::isfinite(eps), PXS_ERR_ARG,
               "SLat decoder norm epsilon must be finite and positive");
@@ -304,6 +306,7 @@ int pxs_slat_decoder_forward(int dtype, const pxs_decoder_config * cfg,
                              int upsample_times, int64_t max_rows, int32_t * out_coords,
                              float * y, int64_t * rows_out, int64_t * level_rows,
                              void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_slat_decoder_forward");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG,
               "pxs_slat_decoder_forward: bad dtype");
     PXS_CHECK(cfg && rows_out, PXS_ERR_ARG, "pxs_slat_decoder_forward: null config");

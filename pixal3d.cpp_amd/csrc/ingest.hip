@@ -150,9 +150,6 @@ Ingest::~Ingest() {
 }
 
 int Ingest::begin() {
-    // The conversion kernel reads the staging chunks with 16-byte loads.
-    PXS_CHECK(reinterpret_cast<uintptr_t>(workspace_) % 16 == 0, PXS_ERR_ARG,
-              "pack upload: workspace must be 16-byte aligned");
     if (!pack_->host_stage) {
         int rc = check_hip(hipHostMalloc(&pack_->host_stage, stage_bytes(), hipHostMallocDefault),
                            "hipHostMalloc(pack staging)");
@@ -331,6 +328,7 @@ size_t pxs_pack_upload_workspace_bytes(const pxs_pack * pack) {
 
 int pxs_pack_upload(pxs_pack * pack, const char * name, int dtype, void * dst, int64_t count,
                     void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_pack_upload");
     return pxs::guarded("pxs_pack_upload", [&]() -> int {
         PXS_CHECK(pack && name && workspace, PXS_ERR_ARG, "pxs_pack_upload: null argument");
         const GgufTensor * t = pack->file.tensor(name);

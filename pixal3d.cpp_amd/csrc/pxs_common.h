@@ -22,6 +22,14 @@ int check_launch(const char * what);
         if (!(expr)) return ::pxs::fail((code), (msg)); \
     } while (0)
 
+// Caller workspaces are carved into 256-byte-aligned sub-buffers that hold
+// 16-byte vectors and 64-bit counters, so a workspace must start 256-byte
+// aligned (as hipMalloc returns); a null workspace passes, for calls that
+// need none.
+#define PXS_CHECK_WORKSPACE(ws, what)                                       \
+    PXS_CHECK(reinterpret_cast<uintptr_t>(ws) % 256 == 0, PXS_ERR_ARG,     \
+              std::string(what) + ": workspace must be 256-byte aligned")
+
 inline hipStream_t as_stream(void * s) { return static_cast<hipStream_t>(s); }
 
 inline unsigned grid_for(int64_t items, int per_block) {

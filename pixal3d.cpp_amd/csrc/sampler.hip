@@ -221,6 +221,7 @@ int pxs_flow_guidance(const float * state, const float * positive, const float *
                       const int32_t * coords, const int64_t * cu_rows, int64_t rows, int channels,
                       int batch_size, float timestep, float sigma_min, float guidance,
                       float guidance_rescale, float * prediction, void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_flow_guidance");
     PXS_CHECK(rows >= 0 && channels > 0 && batch_size > 0, PXS_ERR_ARG,
               "pxs_flow_guidance: bad shape");
     if (rows == 0) return PXS_OK;
@@ -283,6 +284,7 @@ int pxs_flow_euler_sample(int dtype, const pxs_flow_config * cfg, const pxs_flow
                           int64_t cond_tokens, const void * uncond,
                           const int64_t * uncond_offsets, int64_t uncond_tokens,
                           float * samples, void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_flow_euler_sample");
     PXS_CHECK(cfg && w && scfg, PXS_ERR_ARG, "pxs_flow_euler_sample: null config or weights");
     PXS_CHECK(rows >= 0 && batch_size > 0 && cond_tokens >= 0 && uncond_tokens >= 0, PXS_ERR_ARG,
               "pxs_flow_euler_sample: bad shape");

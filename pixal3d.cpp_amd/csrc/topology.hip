@@ -715,6 +715,7 @@ size_t pxs_neighbor_pairs_workspace_bytes(int64_t n) {
 
 int pxs_neighbor_pairs(const int32_t * nbr, int64_t n, int32_t * pair_in, int32_t * pair_out,
                        int64_t * offsets28, void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_neighbor_pairs");
     PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_neighbor_pairs: bad row count");
     PXS_CHECK(offsets28 && workspace, PXS_ERR_ARG, "pxs_neighbor_pairs: null pointer");
     hipStream_t s = as_stream(stream);
@@ -778,6 +779,7 @@ CoarseGrid coarse_grid(void * workspace, int batch_size, int sx, int sy, int sz,
 int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size, int sx,
                                int sy, int sz, int32_t * out_coords, int32_t * child_map,
                                int64_t * m_out, void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_downsample_s2_topology");
     PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_downsample_s2_topology: bad row count");
     PXS_CHECK(batch_size > 0 && sx > 0 && sy > 0 && sz > 0, PXS_ERR_ARG,
               "pxs_downsample_s2_topology: invalid shape");
@@ -804,6 +806,7 @@ int pxs_downsample_topology(const int32_t * coords, int64_t n, int batch_size, i
                             int sz, int factor, int32_t * out_coords, int64_t * group_offsets,
                             int32_t * group_rows, int64_t * m_out, void * workspace,
                             void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_downsample_topology");
     PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_downsample_topology: bad row count");
     PXS_CHECK(factor > 0, PXS_ERR_ARG, "sparse downsample factor must be positive");
     PXS_CHECK(batch_size > 0 && sx > 0 && sy > 0 && sz > 0, PXS_ERR_ARG,
@@ -860,6 +863,7 @@ int pxs_window_partition(const int32_t * coords, int64_t n, int batch_size, int 
                          int sz, int window, int shift, int32_t * fwd, int32_t * bwd,
                          int64_t * cu_seqlens, int64_t * nwin_out, void * workspace,
                          void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_window_partition");
     PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_window_partition: bad row count");
     PXS_CHECK(window > 0 && shift >= 0 && batch_size > 0 && sx > 0 && sy > 0 && sz > 0,
               PXS_ERR_ARG, "pxs_window_partition: invalid window or shape");
@@ -931,6 +935,7 @@ int pxs_channel_to_spatial(int dtype, const int32_t * coords, int64_t n, const v
                            int channels, int factor, const float * subdivision,
                            int32_t * out_coords, void * y, int64_t * m_out, void * workspace,
                            void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_channel_to_spatial");
     PXS_CHECK(factor > 0 && factor <= 1024, PXS_ERR_ARG,
               "pxs_channel_to_spatial: factor must be in 1..1024");
     const int64_t cc = static_cast<int64_t>(factor) * factor * factor;

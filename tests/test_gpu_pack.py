@@ -107,7 +107,8 @@ def test_upload_errors(px, tmp_path):
         rc = px.lib.pxs_pack_upload(pack.handle, b"bf16_rand", pxs.PXS_F32, y.data_ptr(), 777,
                                     ws.data_ptr() + 8, px.stream())
         assert rc == pxs.PXS_ERR_ARG
-        assert px.lib.pxs_last_error().decode() == "pack upload: workspace must be 16-byte aligned"
+        assert px.lib.pxs_last_error().decode() == \
+            "pxs_pack_upload: workspace must be 256-byte aligned"
         # the pack stays usable after an error
         got = pack.upload("bf16_rand", pxs.PXS_F32, 777)
         assert torch.isfinite(got).all()

@@ -148,10 +148,10 @@ def test_library_reader_matches_oracle(px, stem):
 
 
 def test_upload_rejects_misaligned_workspace(px):
-    """The staging workspace is read with 16-byte loads: a workspace that is
-    not 16-byte aligned is an argument error, raised before any device work
-    (so the call runs here without a device; the pointers are never
-    dereferenced)."""
+    """Workspaces must be 256-byte aligned (the staging chunks are read with
+    16-byte loads): a misaligned one is an argument error, raised before any
+    device work (so the call runs here without a device; the pointers are
+    never dereferenced)."""
     path = golden("pack_flow_f16")
     info = G.load_pack_info(path)
     t = next(t for t in info.tensors if t.ggml_type == G.GGML_F32)
@@ -161,7 +161,7 @@ def test_upload_rejects_misaligned_workspace(px):
                                     (1 << 20) + 8, None)
         assert rc == pxs.PXS_ERR_ARG
         assert px.lib.pxs_last_error().decode() == \
-            "pack upload: workspace must be 16-byte aligned"
+            "pxs_pack_upload: workspace must be 256-byte aligned"
 
 
 def reference_case_pack(path):
