@@ -13,9 +13,11 @@
  *     returns; a misaligned one is an argument error).  (A pack's first
  *     upload allocates its 32 MiB of pinned host staging, freed by
  *     pxs_pack_close.)
- *   - Coordinates are int32 rows (batch, x, y, z).  Features are row-major
- *     [rows, channels].  PXS_BF16 data is stored as raw bfloat16 bit
- *     patterns (uint16); arithmetic accumulates in fp32.
+ *   - Coordinates are int32 rows (batch, x, y, z), read as 16-byte rows, so
+ *     a coordinate array starts 16-byte aligned (as any [rows, 4] int32
+ *     allocation does).  Features are row-major [rows, channels].
+ *     PXS_BF16 data is stored as raw bfloat16 bit patterns (uint16);
+ *     arithmetic accumulates in fp32.
  *
  * Each entry point names the reference interface it replaces; paths are
  * relative to the Pixal3D.cpp tree.
