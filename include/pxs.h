@@ -83,6 +83,26 @@ int pxs_status_reset(int64_t * status, void * stream);
 int pxs_check_finite(int dtype, const void * x, int64_t rows, int channels, int64_t ld,
                      int64_t * status, void * stream);
 
+/* Summary of count fp32 device values, the figures the flow sampler's
+ * PIXAL3D_FLOW_NONFINITE_TRACE line prints (trace_features,
+ * src/flow_sampler.cpp:25-83): how many values are non-finite, the first
+ * one's index (count when none) and value, and min, max, max |v| and the sum
+ * over the finite values (+inf, -inf, 0 and 0 when none is finite).  The sum
+ * is accumulated in double in a fixed tree order (the reference sums serially
+ * in long double).  stats points to device memory. */
+typedef struct pxs_value_stats {
+    int64_t nonfinite;
+    int64_t first_bad;
+    double sum;
+    float first_bad_value;
+    float min;
+    float max;
+    float max_abs;
+} pxs_value_stats;
+size_t pxs_value_stats_workspace_bytes(int64_t count);
+int pxs_value_stats_f32(const float * x, int64_t count, pxs_value_stats * stats, void * workspace,
+                        void * stream);
+
 /* Dense 3x3x3 neighbor map (src/slat_decoder.cpp:609-668): nbr[k * n + p] is
  * the row of voxel (b, x+kd-1, y+kh-1, z+kw-1), k = kd*9 + kh*3 + kw, or n
  * when absent.  masks (nullable) receives bit k set when offset k is present. */
@@ -266,7 +286,9 @@ int pxs_timestep_embedding(const float * timesteps, int64_t batch, int dim, int 
  * row_map (nullable, device int32): logical row i is physical row row_map[i]
  * for q, k, v and o alike (window attention reads the permuted order without
  * moving rows).  head_dim and value_dim (the per-head width of v and o) are
- * 1..64; head_dim == value_dim == 64 in PXS_BF16 takes the fastest kernel.
+ * 1..512; head_dim == value_dim == 64 in PXS_BF16 takes the fastest kernel,
+ * dims up to 64 the tiled MFMA kernels, wider heads a wavefront-per-query
+ * kernel (one online-softmax pass over the keys, no head-size limit below 512).
  * A segment with queries but no keys writes zeros.
  * workspace: pxs_attention_workspace_bytes(nseg). */
 size_t pxs_attention_workspace_bytes(int nseg);
@@ -476,7 +498,16 @@ int pxs_flow_euler_update(float * state, const float * prediction, int64_t count
  * guidance weight is 1 (or 0) runs the conditional (or unconditional)
  * forward alone, as the reference does.  cond / uncond: context tokens in the
  * call's dtype with per-item offsets, as for pxs_slat_flow_forward.  Requires
- * in_channels == out_channels.  samples may alias noise. */
+ * in_channels == out_channels.  samples may alias noise.
+ * The reference's finiteness checks run on the device: every step's velocity
+ * (check_model_output, src/flow_sampler.cpp:126-136) and, when
+ * guidance_rescale > 0, the x0 of the conditional prediction and of the CFG
+ * blend (sparse_batch_std, src/flow_sampler.cpp:168).  They collect into one
+ * status word that is read after the last step (the call synchronizes
+ * `stream` once there); a non-finite value fails the call with PXS_ERR_DATA and
+ * the reference's message "sparse features contain a non-finite value", and
+ * samples is then undefined (the reference stops at the failing step; the
+ * device runs every step and reports at the end). */
 size_t pxs_flow_euler_sample_workspace_bytes(int dtype, const pxs_flow_config * cfg,
                                              int64_t rows, int64_t cond_tokens,
                                              int64_t uncond_tokens, int batch_size);

@@ -379,20 +379,41 @@ int64_t orc_channel_to_spatial(const int32_t * coords, int64_t n, const float * 
 // ---------------------------------------------------------------------------
 // a6: sparse_linear / varlen_linear / row_linear (src/sparse.cpp:434-447,
 // 476-486; src/slat_flow.cpp:85-111).  Bias first, then in ascending.
+namespace {
+inline void linear_row(const float * src, int cin, const float * weight, const float * bias,
+                       int cout, float * dst) {
+    for (int o = 0; o < cout; ++o) {
+        float acc = bias[o];
+        const float * wrow = weight + static_cast<int64_t>(o) * cin;
+        for (int i = 0; i < cin; ++i) acc += wrow[i] * src[i];
+        dst[o] = acc;
+    }
+}
+}  // namespace
+
 void orc_linear(const float * x, int64_t rows, int cin, const float * weight, const float * bias,
                 int cout, float * y) {
 #pragma omp parallel for schedule(static)
-    for (int64_t r = 0; r < rows; ++r) {
-        const float * src = x + r * cin;
-        float * dst = y + r * cout;
-        for (int o = 0; o < cout; ++o) {
-            float acc = bias[o];
-            const float * wrow = weight + static_cast<int64_t>(o) * cin;
-            for (int i = 0; i < cin; ++i) acc += wrow[i] * src[i];
-            dst[o] = acc;
-        }
+    for (int64_t r = 0; r < rows; ++r) linear_row(x + r * cin, cin, weight, bias, cout, y + r * cout);
+}
+
+namespace {
+// orc_linear on the listed rows only (all rows when `rows` is null).  Every
+// output element is computed alone, in the same order, so a listed row equals
+// orc_linear's bit for bit; unlisted rows of y are left as they are.
+void linear_on_rows(const float * x, int64_t n, int cin, const float * weight, const float * bias,
+                    int cout, float * y, const int64_t * rows, int64_t row_count) {
+    if (!rows) {
+        orc_linear(x, n, cin, weight, bias, cout, y);
+        return;
+    }
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < row_count; ++i) {
+        const int64_t r = rows[i];
+        linear_row(x + r * cin, cin, weight, bias, cout, y + r * cout);
     }
 }
+}  // namespace
 
 // ---------------------------------------------------------------------------
 // a12: sparse_layer_norm (src/sparse.cpp:490-534): two-pass mean/variance.
@@ -634,9 +655,12 @@ void orc_silu(float * x, int64_t count) {
 // cfg_i = {channels, heads, mlp_hidden, context_channels, proj_in_channels,
 // use_rope, qk_rms_norm, qk_rms_norm_cross, use_projection};
 // cfg_f = {norm_eps, rope_freq_min, rope_freq_base}.  ctx_offsets has
-// batch_size + 1 entries.  out may alias x.  rows restricts the two
-// attentions to sampled query rows when non-null (every other stage runs
-// in full); only those rows of out are meaningful then.
+// batch_size + 1 entries.  out may alias x.  rows, when non-null, restricts
+// the block to sampled rows: the keys and values of the self-attention are
+// computed for every row (each sampled query attends to all of its batch),
+// every other linear and both attentions only for the sampled rows, and the
+// row-local elementwise stages run over all rows.  Each sampled row of out
+// then equals the full block's bit for bit; the other rows are meaningless.
 void orc_transformer_block(const int32_t * coords, int64_t n, int batch_size, const float * x,
                            const float * t_mod, const float * ctx, const int64_t * ctx_offsets,
                            const float * projected, const int * cfg_i, const float * cfg_f,
@@ -660,13 +684,18 @@ void orc_transformer_block(const int32_t * coords, int64_t n, int batch_size, co
     std::vector<float> a(NC), b(NC);
     orc_layer_norm(h.data(), n, C, eps, nullptr, nullptr, a.data());
     orc_modulate(coords, a.data(), n, C, mod, t_mod, 0, b.data());
-    std::vector<float> qkv(static_cast<size_t>(n) * 3 * C);
-    orc_linear(b.data(), n, C, qkv_w, qkv_b, 3 * C, qkv.data());
+    // The fused QKV linear as its two halves: q (weight rows [0, C)) for the
+    // query rows, k and v (weight rows [C, 3C)) for every row.
     std::vector<float> q(NC), k(NC), v(NC);
-    for (int64_t r = 0; r < n; ++r) {
-        std::memcpy(&q[r * C], &qkv[r * 3 * C], sizeof(float) * C);
-        std::memcpy(&k[r * C], &qkv[r * 3 * C + C], sizeof(float) * C);
-        std::memcpy(&v[r * C], &qkv[r * 3 * C + 2 * C], sizeof(float) * C);
+    linear_on_rows(b.data(), n, C, qkv_w, qkv_b, C, q.data(), rows, row_count);
+    {
+        std::vector<float> kv(static_cast<size_t>(n) * 2 * C);
+        orc_linear(b.data(), n, C, qkv_w + static_cast<int64_t>(C) * C, qkv_b + C, 2 * C,
+                   kv.data());
+        for (int64_t r = 0; r < n; ++r) {
+            std::memcpy(&k[r * C], &kv[r * 2 * C], sizeof(float) * C);
+            std::memcpy(&v[r * C], &kv[r * 2 * C + C], sizeof(float) * C);
+        }
     }
     if (qk_rms) {
         orc_mh_rms_norm(q.data(), n, H, D, q_g, a.data());
@@ -685,13 +714,13 @@ void orc_transformer_block(const int32_t * coords, int64_t n, int batch_size, co
     std::vector<float> att(NC, 0.0f);
     orc_varlen_attention(q.data(), k.data(), v.data(), cu.data(), cu.data(), batch_size, H, D, D,
                          scale, att.data(), rows, row_count);
-    orc_linear(att.data(), n, C, out_w, out_b, C, a.data());
+    linear_on_rows(att.data(), n, C, out_w, out_b, C, a.data(), rows, row_count);
     orc_gate(coords, a.data(), n, C, mod, t_mod, 2 * C);
     for (size_t i = 0; i < NC; ++i) h[i] += a[i];
 
     orc_layer_norm(h.data(), n, C, eps, n2_w, n2_b, b.data());
     std::vector<float> cq(NC);
-    orc_linear(b.data(), n, C, cq_w, cq_b, C, cq.data());
+    linear_on_rows(b.data(), n, C, cq_w, cq_b, C, cq.data(), rows, row_count);
     if (qk_rms_cross) {
         orc_mh_rms_norm(cq.data(), n, H, D, cq_g, a.data());
         cq.swap(a);
@@ -712,9 +741,9 @@ void orc_transformer_block(const int32_t * coords, int64_t n, int batch_size, co
     std::fill(att.begin(), att.end(), 0.0f);
     orc_varlen_attention(cq.data(), ck.data(), cv.data(), cu.data(), ctx_offsets, batch_size, H,
                          D, D, scale, att.data(), rows, row_count);
-    orc_linear(att.data(), n, C, co_w, co_b, C, a.data());
+    linear_on_rows(att.data(), n, C, co_w, co_b, C, a.data(), rows, row_count);
     if (use_proj) {
-        orc_linear(projected, n, PC, pj_w, pj_b, C, b.data());
+        linear_on_rows(projected, n, PC, pj_w, pj_b, C, b.data(), rows, row_count);
         for (size_t i = 0; i < NC; ++i) a[i] += b[i];
     }
     for (size_t i = 0; i < NC; ++i) h[i] += a[i];
@@ -722,9 +751,9 @@ void orc_transformer_block(const int32_t * coords, int64_t n, int batch_size, co
     orc_layer_norm(h.data(), n, C, eps, nullptr, nullptr, a.data());
     orc_modulate(coords, a.data(), n, C, mod, t_mod, 3 * C, b.data());
     std::vector<float> hid(static_cast<size_t>(n) * M);
-    orc_linear(b.data(), n, C, m0_w, m0_b, M, hid.data());
+    linear_on_rows(b.data(), n, C, m0_w, m0_b, M, hid.data(), rows, row_count);
     orc_gelu_tanh(hid.data(), static_cast<int64_t>(hid.size()));
-    orc_linear(hid.data(), n, M, m2_w, m2_b, C, a.data());
+    linear_on_rows(hid.data(), n, M, m2_w, m2_b, C, a.data(), rows, row_count);
     orc_gate(coords, a.data(), n, C, mod, t_mod, 5 * C);
     for (size_t i = 0; i < NC; ++i) h[i] += a[i];
     std::memcpy(out, h.data(), NC * sizeof(float));

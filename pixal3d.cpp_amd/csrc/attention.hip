@@ -712,6 +712,76 @@ int launch_attn(const AttnArgs & args, int64_t total_q, int heads, hipStream_t s
 
 bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Heads wider than the tiled kernels take (head_dim or value_dim above 64, up
+// to kWideMaxDim): one wavefront per (query row, head) walks the segment's
+// keys in order with an online softmax.  Lane l owns dims l, l + 64, ... of
+// q, k and the output; a key's score is the wavefront sum of the lanes'
+// partial dot products.  Latency-bound (every key costs a 6-step shuffle
+// reduction), but it keeps the drop-in's attention free of a head-size limit.
+constexpr int kWideMaxDim = 512;
+constexpr int kWidePerLane = kWideMaxDim / 64;
+
+template <typename T>
+__global__ void __launch_bounds__(64)
+attn_wide_kernel(AttnArgs a, int64_t total_q, float scale) {
+    const int64_t qi = blockIdx.x;
+    const int head = blockIdx.y;
+    const int lane = threadIdx.x;
+    if (qi >= total_q) return;
+    // segment of query qi: the last s with cu_q[s] <= qi
+    int lo = 0, hi = a.nseg;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (a.cu_q[mid] <= qi) lo = mid; else hi = mid;
+    }
+    const int64_t k_begin = a.cu_k[lo], k_end = a.cu_k[lo + 1];
+    const T * q = static_cast<const T *>(a.q);
+    const T * k = static_cast<const T *>(a.k);
+    const T * v = static_cast<const T *>(a.v);
+    const int64_t q_row = a.row_map ? a.row_map[qi] : qi;
+    float qv[kWidePerLane];
+#pragma unroll
+    for (int c = 0; c < kWidePerLane; ++c) {
+        const int d = lane + 64 * c;
+        qv[c] = d < a.hd ? load_f32(q + q_row * a.ldq + static_cast<int64_t>(head) * a.hd + d) : 0.0f;
+    }
+    float acc[kWidePerLane];
+#pragma unroll
+    for (int c = 0; c < kWidePerLane; ++c) acc[c] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    for (int64_t j = k_begin; j < k_end; ++j) {
+        const int64_t row = a.row_map ? a.row_map[j] : j;
+        const T * kr = k + row * a.ldk + static_cast<int64_t>(head) * a.hd;
+        float part = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kWidePerLane; ++c) {
+            const int d = lane + 64 * c;
+            if (d < a.hd) part += qv[c] * load_f32(kr + d);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+        const float sc = part * scale;
+        const float m_new = fmaxf(m, sc);
+        const float corr = expf(m - m_new);  // 0 on the first key (m = -inf)
+        const float p = expf(sc - m_new);
+        l = l * corr + p;
+        const T * vr = v + row * a.ldv + static_cast<int64_t>(head) * a.vd;
+#pragma unroll
+        for (int c = 0; c < kWidePerLane; ++c) {
+            const int d = lane + 64 * c;
+            if (d < a.vd) acc[c] = acc[c] * corr + p * load_f32(vr + d);
+        }
+        m = m_new;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;  // no keys: zeros
+    T * o = static_cast<T *>(a.o);
+#pragma unroll
+    for (int c = 0; c < kWidePerLane; ++c) {
+        const int d = lane + 64 * c;
+        if (d < a.vd) store_f32(o + q_row * a.ldo + static_cast<int64_t>(head) * a.vd + d, acc[c] * inv);
+    }
+}
+
 } // namespace
 } // namespace pxs
 
@@ -732,8 +802,9 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
                          float scale, void * o, int64_t ld_o, void * workspace, void * stream) {
     PXS_CHECK_WORKSPACE(workspace, "pxs_varlen_attention");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_varlen_attention: bad dtype");
-    PXS_CHECK(heads > 0 && head_dim > 0 && head_dim <= 64 && value_dim > 0 && value_dim <= 64,
-              PXS_ERR_ARG, "pxs_varlen_attention: head_dim and value_dim must be in 1..64");
+    PXS_CHECK(heads > 0 && head_dim > 0 && head_dim <= kWideMaxDim && value_dim > 0 &&
+                  value_dim <= kWideMaxDim,
+              PXS_ERR_ARG, "pxs_varlen_attention: head_dim and value_dim must be in 1..512");
     PXS_CHECK(heads <= 65535, PXS_ERR_ARG, "pxs_varlen_attention: too many heads");
     PXS_CHECK(scale > 0.0f && std::isfinite(scale), PXS_ERR_ARG,
               "sparse attention scale must be finite and positive");
@@ -745,6 +816,20 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     PXS_CHECK(q && k && v && o && cu_q && cu_k && workspace, PXS_ERR_ARG,
               "pxs_varlen_attention: null pointer");
     hipStream_t s = as_stream(stream);
+    if (head_dim > 64 || value_dim > 64) {
+        PXS_CHECK(total_q <= INT32_MAX, PXS_ERR_ARG, "attention grid too large");
+        AttnArgs a{};
+        a.q = q; a.k = k; a.v = v; a.ldq = ld_q; a.ldk = ld_k; a.ldv = ld_v;
+        a.cu_q = cu_q; a.cu_k = cu_k; a.nseg = nseg; a.row_map = row_map;
+        a.hd = head_dim; a.vd = value_dim; a.o = o; a.ldo = ld_o;
+        const dim3 grid(static_cast<unsigned>(total_q), heads);
+        if (dtype == PXS_BF16) {
+            hipLaunchKernelGGL(attn_wide_kernel<uint16_t>, grid, dim3(64), 0, s, a, total_q, scale);
+        } else {
+            hipLaunchKernelGGL(attn_wide_kernel<float>, grid, dim3(64), 0, s, a, total_q, scale);
+        }
+        return check_launch("flash attention (wide heads)");
+    }
     const bool fast = dtype == PXS_BF16 && head_dim == 64 && value_dim == 64 && (ld_q % 8 == 0) &&
                       (ld_k % 8 == 0) && (ld_v % 8 == 0) && (ld_o % 4 == 0) && aligned16(q) &&
                       aligned16(k) && aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0;

@@ -57,8 +57,8 @@ int check_block_args(const pxs_block_config * cfg, const pxs_block_weights * w) 
                   cfg->context_channels > 0 && cfg->channels % cfg->num_heads == 0 &&
                   cfg->norm_eps > 0.0f && std::isfinite(cfg->norm_eps),
               PXS_ERR_ARG, "invalid sparse transformer block configuration");
-    PXS_CHECK(cfg->channels / cfg->num_heads <= 64, PXS_ERR_ARG,
-              "pxs_transformer_block: head_dim above 64 unsupported");
+    PXS_CHECK(cfg->channels / cfg->num_heads <= 192, PXS_ERR_ARG,
+              "pxs_transformer_block: head_dim above 192 unsupported");
     PXS_CHECK(!cfg->use_projection || cfg->proj_in_channels > 0, PXS_ERR_ARG,
               "sparse transformer projection shape does not match query");
     PXS_CHECK(w->modulation && w->self_to_qkv_weight && w->self_to_qkv_bias &&

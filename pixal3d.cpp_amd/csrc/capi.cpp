@@ -11,9 +11,21 @@ thread_local std::string g_last_error;
 
 void set_error(const std::string & message) { g_last_error = message; }
 
-int fail(int code, const std::string & message) {
-    g_last_error = message;
+int fail(int code, const std::string & message) noexcept {
+    try {
+        g_last_error = message;
+    } catch (...) {
+        g_last_error.clear();  // out of host memory: the code alone reports it
+    }
     return code;
+}
+
+int fail_workspace(const char * what) noexcept {
+    try {
+        return fail(PXS_ERR_ARG, std::string(what) + ": workspace must be 256-byte aligned");
+    } catch (...) {
+        return fail(PXS_ERR_ARG, std::string());
+    }
 }
 
 int check_hip(hipError_t status, const char * what) {

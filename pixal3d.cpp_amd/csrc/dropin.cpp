@@ -28,6 +28,7 @@
 #include <cstring>
 #include <iostream>
 #include <limits>
+#include <sstream>
 #include <string>
 #include <vector>
 
@@ -44,7 +45,7 @@ enum Slot {
     kInCoords, kInFeats, kTable, kStatus, kNbr, kMasks, kWeight, kBias, kOut, kOutCoords,
     kWork, kAuxCoords, kAuxFeats, kAux2Feats, kCuQ, kCuK, kOffsets, kRows, kGamma, kBeta,
     kCount, kFlowState, kFlowPos, kFlowNeg, kFlowPred, kFlowX0, kFlowCu, kFlowWork,
-    kSlotCount
+    kTraceStats, kTraceWork, kSlotCount
 };
 
 class Device {
@@ -1051,78 +1052,73 @@ bool sparse_transformer_cross_block_f32(const SparseTensorF32 & input,
 
 namespace {
 
-// PIXAL3D_FLOW_NONFINITE_TRACE diagnostics (src/flow_sampler.cpp:20-83):
-// host statistics of a host tensor, printed to stderr, failing on a
-// non-finite value.
-bool flow_diagnostics_enabled() {
-    const char * value = std::getenv("PIXAL3D_FLOW_NONFINITE_TRACE");
-    return value && *value && std::string(value) != "0";
+// PIXAL3D_FLOW_NONFINITE_TRACE (src/flow_sampler.cpp:20-83).  Every tensor
+// the reference traces is in HBM here when it is traced, so the figures come
+// from one device reduction over that copy (pxs_value_stats_f32) and only a
+// 48-byte summary crosses to the host.  The printed line and the error text
+// are the reference's; its mean is a serial long-double sum divided by the
+// value count, the device's a double tree sum, which the six printed digits
+// do not tell apart.
+bool trace_requested() {
+    const char * v = std::getenv("PIXAL3D_FLOW_NONFINITE_TRACE");
+    if (v == nullptr || v[0] == '\0') return false;
+    return std::strcmp(v, "0") != 0;
 }
 
-bool trace_features(const SparseTensorF32 & tensor, const char * label, const char * branch,
-                    int step, float timestep, std::string * error) {
-    std::size_t nonfinite = 0, first_bad = 0;
-    float first_value = 0.0f;
-    float lo = std::numeric_limits<float>::infinity();
-    float hi = -std::numeric_limits<float>::infinity();
-    float max_abs = 0.0f;
-    long double sum = 0.0L;
-    for (std::size_t i = 0; i < tensor.feats.size(); ++i) {
-        const float v = tensor.feats[i];
-        if (!std::isfinite(v)) {
-            if (nonfinite == 0) {
-                first_bad = i;
-                first_value = v;
-            }
-            ++nonfinite;
-            continue;
-        }
-        lo = std::min(lo, v);
-        hi = std::max(hi, v);
-        max_abs = std::max(max_abs, std::fabs(v));
-        sum += static_cast<long double>(v);
-    }
-    const double mean = tensor.feats.empty()
-                            ? 0.0
-                            : static_cast<double>(sum / static_cast<long double>(tensor.feats.size()));
-    const char * lab = label && *label ? label : "features";
-    const char * br = branch && *branch ? branch : "unknown";
-    std::cerr << "pixal3d: flow trace step=" << step << " timestep=" << timestep << " branch=" << br
-              << " tensor=" << lab << " points=" << tensor.points()
-              << " values=" << tensor.feats.size() << " min=" << (tensor.feats.empty() ? 0.0f : lo)
-              << " max=" << (tensor.feats.empty() ? 0.0f : hi) << " max_abs=" << max_abs
-              << " mean=" << mean << " nonfinite=" << nonfinite;
-    if (nonfinite != 0) std::cerr << " first_bad_index=" << first_bad << " first_bad_value=" << first_value;
-    std::cerr << std::endl;
-    if (nonfinite != 0) {
-        set_error(error, std::string("flow ") + lab + " contains non-finite values at step " +
-                             std::to_string(step) + " (branch=" + br +
-                             ", first index=" + std::to_string(first_bad) + ")");
+struct TracePoint {
+    int step;
+    float timestep;
+    const char * branch;
+};
+
+bool trace_on_device(const float * values, int64_t points, int channels, const char * tensor,
+                     const TracePoint & at, std::string * error) {
+    Device & d = device();
+    const int64_t count = points * channels;
+    auto * summary = static_cast<pxs_value_stats *>(
+        d.buffer(kTraceStats, sizeof(pxs_value_stats), error));
+    void * work = d.buffer(kTraceWork, pxs_value_stats_workspace_bytes(count), error);
+    if (!summary || !work ||
+        !pxs_ok(pxs_value_stats_f32(values, count, summary, work, d.stream()), error)) {
         return false;
     }
-    return true;
+    pxs_value_stats st{};
+    if (!download(&st, summary, 1, error)) return false;
+    const bool has_values = count > 0;
+    std::ostringstream line;
+    line << "pixal3d: flow trace step=" << at.step << " timestep=" << at.timestep
+         << " branch=" << at.branch << " tensor=" << tensor << " points=" << points
+         << " values=" << count << " min=" << (has_values ? st.min : 0.0f)
+         << " max=" << (has_values ? st.max : 0.0f) << " max_abs=" << st.max_abs
+         << " mean=" << (has_values ? st.sum / static_cast<double>(count) : 0.0)
+         << " nonfinite=" << st.nonfinite;
+    if (st.nonfinite > 0) {
+        line << " first_bad_index=" << st.first_bad << " first_bad_value=" << st.first_bad_value;
+    }
+    std::cerr << line.str() << std::endl;
+    if (st.nonfinite == 0) return true;
+    std::ostringstream msg;
+    msg << "flow " << tensor << " contains non-finite values at step " << at.step
+        << " (branch=" << at.branch << ", first index=" << st.first_bad << ")";
+    set_error(error, msg.str());
+    return false;
 }
 
-bool same_shape(const SparseTensorF32 & a, const SparseTensorF32 & b) {
-    return a.batch_size == b.batch_size && a.channels == b.channels &&
-           a.spatial_x == b.spatial_x && a.spatial_y == b.spatial_y &&
-           a.spatial_z == b.spatial_z && a.coords == b.coords && a.feats.size() == b.feats.size();
-}
-
-void clear_for_callback(SparseTensorF32 & t) {
-    t.batch_size = t.channels = t.spatial_x = t.spatial_y = t.spatial_z = 0;
-    t.coords.clear();
-    t.feats.clear();
-}
-
-bool check_model_output(const SparseTensorF32 & state, const SparseTensorF32 & velocity,
-                        std::string * error) {
+// check_model_output (src/flow_sampler.cpp:126-136): a velocity must be a
+// valid tensor over exactly the state's voxels, shape and channel count.
+bool accept_velocity(const SparseTensorF32 & state, const SparseTensorF32 & velocity,
+                     std::string * error) {
     if (!velocity.valid(error)) return false;
-    if (!same_shape(state, velocity)) {
-        set_error(error, "flow model velocity shape or coordinates changed during sampling");
-        return false;
+    const int want[5] = {state.batch_size, state.channels, state.spatial_x, state.spatial_y,
+                         state.spatial_z};
+    const int got[5] = {velocity.batch_size, velocity.channels, velocity.spatial_x,
+                        velocity.spatial_y, velocity.spatial_z};
+    if (std::equal(want, want + 5, got) && velocity.feats.size() == state.feats.size() &&
+        velocity.coords == state.coords) {
+        return true;
     }
-    return true;
+    set_error(error, "flow model velocity shape or coordinates changed during sampling");
+    return false;
 }
 
 pxs_flow_sampler_config sampler_config(const FlowEulerSamplerConfig & c) {
@@ -1186,8 +1182,7 @@ bool flow_euler_sample_f32(const SparseTensorF32 & noise, const FlowEulerSampler
         return false;
     }
     SparseTensorF32 state = noise;
-    const bool diagnostics = flow_diagnostics_enabled();
-    if (diagnostics && !trace_features(state, "state_before", "initial", -1, 1.0f, error)) return false;
+    const bool diagnostics = trace_requested();
     if (config.record_trajectory) {
         output.pred_x_t.reserve(static_cast<std::size_t>(config.steps));
         output.pred_x_0.reserve(static_cast<std::size_t>(config.steps));
@@ -1200,10 +1195,31 @@ bool flow_euler_sample_f32(const SparseTensorF32 & noise, const FlowEulerSampler
     const std::size_t ucount = static_cast<std::size_t>(count);
     float * dstate = upload(kFlowState, state.feats.data(), ucount, error);
     if (!dstate) return false;
+    // A traced tensor: trace_on_device over its HBM copy, when requested.
+    auto traced = [&](const float * values, const char * tensor, int step, float t,
+                      const char * branch) {
+        return !diagnostics ||
+               trace_on_device(values, rows, channels, tensor, TracePoint{step, t, branch}, error);
+    };
+    if (!traced(dstate, "state_before", -1, 1.0f, "initial")) return false;
     const std::vector<int64_t> cu = batch_bounds(state);
     bool empty_item = false;
     for (int b = 0; b < state.batch_size; ++b) empty_item |= cu[b + 1] == cu[b];
-    SparseTensorF32 prediction, positive, negative;
+    // One model call: the velocity lands in a fresh host tensor (as the
+    // reference clears its workspace tensor before each callback), is checked,
+    // then copied to the device slot and traced there.
+    SparseTensorF32 velocity;
+    auto evaluate = [&](bool conditional, float t, int step, std::size_t slot) -> const float * {
+        velocity = SparseTensorF32{};
+        if (!model(state, 1000.0f * t, conditional, velocity, error) ||
+            !accept_velocity(state, velocity, error)) {
+            return nullptr;
+        }
+        const float * dv = upload(slot, velocity.feats.data(), ucount, error);
+        if (!dv || !traced(dv, "prediction", step, t, conditional ? "conditional" : "unconditional"))
+            return nullptr;
+        return dv;
+    };
     for (int step = 0; step < config.steps; ++step) {
         float t = 0.0f, t_next = 0.0f, guidance = 1.0f;
         if (pxs_flow_sampler_schedule(&scfg, step, &t, &t_next, &guidance) != PXS_OK) {
@@ -1211,82 +1227,46 @@ bool flow_euler_sample_f32(const SparseTensorF32 & noise, const FlowEulerSampler
             return false;
         }
         const float * dpred = nullptr;
-        clear_for_callback(prediction);
         if (guidance == 1.0f || guidance == 0.0f) {
-            const bool cond = guidance == 1.0f;
-            if (!model(state, 1000.0f * t, cond, prediction, error) ||
-                !check_model_output(state, prediction, error)) {
-                return false;
-            }
-            if (diagnostics && !trace_features(prediction, "prediction",
-                                               cond ? "conditional" : "unconditional", step, t,
-                                               error)) {
-                return false;
-            }
-            dpred = upload(kFlowPred, prediction.feats.data(), ucount, error);
+            dpred = evaluate(guidance == 1.0f, t, step, kFlowPred);
             if (!dpred) return false;
         } else {
-            clear_for_callback(positive);
-            clear_for_callback(negative);
-            if (!model(state, 1000.0f * t, true, positive, error) ||
-                !check_model_output(state, positive, error)) {
-                return false;
-            }
-            if (diagnostics && !trace_features(positive, "prediction", "conditional", step, t, error))
-                return false;
-            if (!model(state, 1000.0f * t, false, negative, error) ||
-                !check_model_output(state, negative, error)) {
-                return false;
-            }
-            if (diagnostics && !trace_features(negative, "prediction", "unconditional", step, t, error))
-                return false;
-            const float * dpos = upload(kFlowPos, positive.feats.data(), ucount, error);
-            const float * dneg = upload(kFlowNeg, negative.feats.data(), ucount, error);
-            float * dout = scratch<float>(kFlowPred, ucount, error);
-            if (!dpos || !dneg || !dout) return false;
-            if (!pxs_ok(pxs_flow_guidance(dstate, dpos, dneg, nullptr, nullptr, rows, channels,
+            const float * dpos = evaluate(true, t, step, kFlowPos);
+            if (!dpos) return false;
+            const float * dneg = evaluate(false, t, step, kFlowNeg);
+            if (!dneg) return false;
+            float * blend = scratch<float>(kFlowPred, ucount, error);
+            if (!blend ||
+                !pxs_ok(pxs_flow_guidance(dstate, dpos, dneg, nullptr, nullptr, rows, channels,
                                           state.batch_size, t, config.sigma_min, guidance, 0.0f,
-                                          dout, nullptr, d.stream()),
-                        error)) {
+                                          blend, nullptr, d.stream()),
+                        error) ||
+                !traced(blend, "cfg_blend", step, t, "guided")) {
                 return false;
-            }
-            dpred = dout;
-            if (diagnostics) {
-                SparseTensorF32 blend = positive;
-                if (!download(blend.feats.data(), dout, ucount, error) ||
-                    !trace_features(blend, "cfg_blend", "guided", step, t, error)) {
-                    return false;
-                }
             }
             if (config.guidance_rescale > 0.0f) {
                 if (!x0_checks(dstate, dpos, count, t, config.sigma_min, rows, channels, empty_item,
                                error) ||
-                    !x0_checks(dstate, dout, count, t, config.sigma_min, rows, channels, empty_item,
-                               error)) {
+                    !x0_checks(dstate, blend, count, t, config.sigma_min, rows, channels,
+                               empty_item, error)) {
                     return false;
                 }
                 const int64_t * dcu = upload(kFlowCu, cu.data(), cu.size(), error);
-                void * ws = device().buffer(kFlowWork,
-                                            pxs_flow_guidance_workspace_bytes(state.batch_size),
-                                            error);
-                if (!dcu || !ws) return false;
-                const int32_t * dcoords = upload(kInCoords, state.coords.data(), state.coords.size(),
-                                                 error);
-                if (!dcoords) return false;
-                if (!pxs_ok(pxs_flow_guidance(dstate, dpos, dneg, dcoords, dcu, rows, channels,
+                void * ws = d.buffer(kFlowWork, pxs_flow_guidance_workspace_bytes(state.batch_size),
+                                     error);
+                const int32_t * dcoords =
+                    dcu && ws ? upload(kInCoords, state.coords.data(), state.coords.size(), error)
+                              : nullptr;
+                if (!dcoords ||
+                    !pxs_ok(pxs_flow_guidance(dstate, dpos, dneg, dcoords, dcu, rows, channels,
                                               state.batch_size, t, config.sigma_min, guidance,
-                                              config.guidance_rescale, dout, ws, d.stream()),
-                            error)) {
+                                              config.guidance_rescale, blend, ws, d.stream()),
+                            error) ||
+                    !traced(blend, "guidance_rescale", step, t, "guided")) {
                     return false;
                 }
-                if (diagnostics) {
-                    SparseTensorF32 rescaled = positive;
-                    if (!download(rescaled.feats.data(), dout, ucount, error) ||
-                        !trace_features(rescaled, "guidance_rescale", "guided", step, t, error)) {
-                        return false;
-                    }
-                }
             }
+            dpred = blend;
         }
         SparseTensorF32 x0;
         if (config.record_trajectory) {
@@ -1294,21 +1274,19 @@ bool flow_euler_sample_f32(const SparseTensorF32 & noise, const FlowEulerSampler
             if (!dx0 ||
                 !pxs_ok(pxs_flow_pred_to_xstart(dstate, dpred, count, t, config.sigma_min, dx0,
                                                 d.stream()),
-                        error)) {
+                        error) ||
+                !traced(dx0, "x0", step, t, "guided")) {
                 return false;
             }
             copy_shape(state, channels, x0);
             x0.feats.resize(ucount);
             if (!download(x0.feats.data(), dx0, ucount, error)) return false;
-            if (diagnostics && !trace_features(x0, "x0", "guided", step, t, error)) return false;
         }
-        const float delta = t - t_next;
-        if (!pxs_ok(pxs_flow_euler_update(dstate, dpred, count, delta, d.stream()), error) ||
+        if (!pxs_ok(pxs_flow_euler_update(dstate, dpred, count, t - t_next, d.stream()), error) ||
+            !traced(dstate, "state_after", step, t_next, "euler") ||
             !download(state.feats.data(), dstate, ucount, error)) {
             return false;
         }
-        if (diagnostics && !trace_features(state, "state_after", "euler", step, t_next, error))
-            return false;
         if (config.record_trajectory) {
             output.pred_x_t.push_back(state);
             output.pred_x_0.push_back(std::move(x0));

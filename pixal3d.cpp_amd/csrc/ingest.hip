@@ -107,6 +107,8 @@ ingest_convert_kernel(const uint8_t * __restrict__ src, int64_t n, void * __rest
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             h[k] = SRC == kGgmlBf16 ? (v[k] >> 16) : f32_bits_to_bf16(v[k]);
+            // a finite F32 above the bf16 range rounds to infinity
+            bad = bad || (k < cnt && (h[k] & 0x7f80u) == 0x7f80u);
         }
         if (cnt == 8) {
             *reinterpret_cast<uint4 *>(out) =
@@ -328,9 +330,9 @@ size_t pxs_pack_upload_workspace_bytes(const pxs_pack * pack) {
 
 int pxs_pack_upload(pxs_pack * pack, const char * name, int dtype, void * dst, int64_t count,
                     void * workspace, void * stream) {
-    PXS_CHECK_WORKSPACE(workspace, "pxs_pack_upload");
     return pxs::guarded("pxs_pack_upload", [&]() -> int {
         PXS_CHECK(pack && name && workspace, PXS_ERR_ARG, "pxs_pack_upload: null argument");
+        PXS_CHECK_WORKSPACE(workspace, "pxs_pack_upload");
         const GgufTensor * t = pack->file.tensor(name);
         PXS_CHECK(t, PXS_ERR_ARG, std::string("tensor not found: ") + name);
         PXS_CHECK(t->type == kGgmlF32 || t->type == kGgmlF16 || t->type == kGgmlBf16, PXS_ERR_ARG,

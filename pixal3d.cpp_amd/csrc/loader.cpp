@@ -407,10 +407,10 @@ int pxs_slat_flow_pack_plan(const pxs_pack * pack, const char * component, int d
 int pxs_slat_flow_pack_load(pxs_pack * pack, const char * component, int dtype, void * arena,
                             size_t arena_bytes, void * workspace, pxs_flow_weights * w,
                             pxs_block_weights * blocks, int max_blocks, void * stream) {
-    PXS_CHECK_WORKSPACE(workspace, "pxs_slat_flow_pack_load");
     return pxs::guarded("pxs_slat_flow_pack_load", [&]() -> int {
         PXS_CHECK(pack && component && w && blocks, PXS_ERR_ARG,
                   "pxs_slat_flow_pack_load: null argument");
+        PXS_CHECK_WORKSPACE(workspace, "pxs_slat_flow_pack_load");
         pxs_flow_config cfg;
         Layout layout;
         int rc = flow_plan(pack, component, dtype, cfg, layout);
@@ -491,10 +491,10 @@ int pxs_slat_decoder_pack_plan(const pxs_pack * pack, const char * component, in
 int pxs_slat_decoder_pack_load(pxs_pack * pack, const char * component, int dtype, void * arena,
                                size_t arena_bytes, void * workspace, pxs_decoder_block * blocks,
                                int max_blocks, const float ** io_weights, void * stream) {
-    PXS_CHECK_WORKSPACE(workspace, "pxs_slat_decoder_pack_load");
     return pxs::guarded("pxs_slat_decoder_pack_load", [&]() -> int {
         PXS_CHECK(pack && component && blocks && io_weights, PXS_ERR_ARG,
                   "pxs_slat_decoder_pack_load: null argument");
+        PXS_CHECK_WORKSPACE(workspace, "pxs_slat_decoder_pack_load");
         pxs_decoder_hparams hp;
         Layout layout;
         int rc = decoder_plan(pack, component, dtype, hp, layout);

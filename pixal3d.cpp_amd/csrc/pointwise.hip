@@ -271,6 +271,96 @@ __global__ void check_finite_kernel(const T * __restrict__ x, int64_t rows, int 
     }
 }
 
+// Value statistics (pxs_value_stats_f32): each workgroup folds a grid-stride
+// slice into one partial, a single workgroup then folds the partials in
+// workgroup order, so the result does not depend on scheduling.
+struct StatsPartial {
+    double sum;
+    long long nonfinite;
+    long long first_bad;
+    float lo, hi, max_abs, pad;
+};
+
+__device__ __forceinline__ void stats_fold(StatsPartial & a, const StatsPartial & b) {
+    a.sum += b.sum;
+    a.nonfinite += b.nonfinite;
+    a.first_bad = b.first_bad < a.first_bad ? b.first_bad : a.first_bad;
+    a.lo = fminf(a.lo, b.lo);
+    a.hi = fmaxf(a.hi, b.hi);
+    a.max_abs = fmaxf(a.max_abs, b.max_abs);
+}
+
+constexpr int kStatsThreads = 256;
+
+// Tree over the workgroup's 256 partials in LDS; thread 0 holds the result.
+__device__ void stats_block_fold(StatsPartial & mine, StatsPartial * lds) {
+    lds[threadIdx.x] = mine;
+    __syncthreads();
+    for (int span = kStatsThreads / 2; span >= 1; span >>= 1) {
+        if (static_cast<int>(threadIdx.x) < span) {
+            stats_fold(lds[threadIdx.x], lds[threadIdx.x + span]);
+        }
+        __syncthreads();
+    }
+    mine = lds[0];
+}
+
+__device__ __forceinline__ StatsPartial stats_empty(long long count) {
+    StatsPartial p;
+    p.sum = 0.0;
+    p.nonfinite = 0;
+    p.first_bad = count;
+    p.lo = INFINITY;
+    p.hi = -INFINITY;
+    p.max_abs = 0.0f;
+    p.pad = 0.0f;
+    return p;
+}
+
+__global__ void __launch_bounds__(kStatsThreads)
+value_stats_partial_kernel(const float * __restrict__ x, int64_t count,
+                           StatsPartial * __restrict__ partials) {
+    __shared__ StatsPartial lds[kStatsThreads];
+    StatsPartial p = stats_empty(count);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride) {
+        const float v = x[i];
+        if (!isfinite(v)) {
+            ++p.nonfinite;
+            if (i < p.first_bad) p.first_bad = i;
+            continue;
+        }
+        p.sum += static_cast<double>(v);
+        p.lo = fminf(p.lo, v);
+        p.hi = fmaxf(p.hi, v);
+        p.max_abs = fmaxf(p.max_abs, fabsf(v));
+    }
+    stats_block_fold(p, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = p;
+}
+
+__global__ void __launch_bounds__(kStatsThreads)
+value_stats_final_kernel(const float * __restrict__ x, int64_t count,
+                         const StatsPartial * __restrict__ partials, int nparts,
+                         pxs_value_stats * __restrict__ out) {
+    __shared__ StatsPartial lds[kStatsThreads];
+    StatsPartial p = stats_empty(count);
+    for (int i = threadIdx.x; i < nparts; i += kStatsThreads) stats_fold(p, partials[i]);
+    stats_block_fold(p, lds);
+    if (threadIdx.x == 0) {
+        out->nonfinite = p.nonfinite;
+        out->first_bad = p.first_bad;
+        out->sum = p.sum;
+        out->first_bad_value = p.first_bad < count ? x[p.first_bad] : 0.0f;
+        out->min = p.lo;
+        out->max = p.hi;
+        out->max_abs = p.max_abs;
+    }
+}
+
+constexpr int kStatsMaxParts = 1024;
+
 template <typename TS, typename TD>
 __global__ void convert_kernel(const TS * __restrict__ x, int64_t count, TD * __restrict__ y) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -526,6 +616,29 @@ int pxs_check_finite(int dtype, const void * x, int64_t rows, int channels, int6
                            st);
     }
     return check_launch("pxs_check_finite");
+}
+
+size_t pxs_value_stats_workspace_bytes(int64_t count) {
+    (void)count;
+    return kStatsMaxParts * sizeof(StatsPartial);
+}
+
+int pxs_value_stats_f32(const float * x, int64_t count, pxs_value_stats * stats, void * workspace,
+                        void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_value_stats_f32");
+    PXS_CHECK(count >= 0, PXS_ERR_ARG, "pxs_value_stats_f32: negative count");
+    PXS_CHECK(stats && workspace && (x || count == 0), PXS_ERR_ARG,
+              "pxs_value_stats_f32: null pointer");
+    const int parts = static_cast<int>(
+        std::max<int64_t>(1, std::min<int64_t>((count + 4 * kStatsThreads - 1) / (4 * kStatsThreads),
+                                               kStatsMaxParts)));
+    auto * partials = static_cast<StatsPartial *>(workspace);
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(value_stats_partial_kernel, dim3(parts), dim3(kStatsThreads), 0, s, x, count,
+                       partials);
+    hipLaunchKernelGGL(value_stats_final_kernel, dim3(1), dim3(kStatsThreads), 0, s, x, count,
+                       partials, parts, stats);
+    return check_launch("pxs_value_stats_f32");
 }
 
 int pxs_convert(int src_dtype, const void * x, int64_t count, int dst_dtype, void * y,

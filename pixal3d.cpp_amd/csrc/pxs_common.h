@@ -13,7 +13,8 @@ namespace pxs {
 
 // ---- error reporting (thread-local last error, see pxs_last_error) ---------
 void set_error(const std::string & message);
-int fail(int code, const std::string & message);
+int fail(int code, const std::string & message) noexcept;
+int fail_workspace(const char * what) noexcept;
 int check_hip(hipError_t status, const char * what);
 int check_launch(const char * what);
 
@@ -26,9 +27,12 @@ int check_launch(const char * what);
 // 16-byte vectors and 64-bit counters, so a workspace must start 256-byte
 // aligned (as hipMalloc returns); a null workspace passes, for calls that
 // need none.
-#define PXS_CHECK_WORKSPACE(ws, what)                                       \
-    PXS_CHECK(reinterpret_cast<uintptr_t>(ws) % 256 == 0, PXS_ERR_ARG,     \
-              std::string(what) + ": workspace must be 256-byte aligned")
+// The message is composed inside fail_workspace, which cannot throw.
+#define PXS_CHECK_WORKSPACE(ws, what)                                   \
+    do {                                                                \
+        if (reinterpret_cast<uintptr_t>(ws) % 256 != 0)                 \
+            return ::pxs::fail_workspace(what);                         \
+    } while (0)
 
 inline hipStream_t as_stream(void * s) { return static_cast<hipStream_t>(s); }
 

@@ -15,6 +15,7 @@
 #include "pxs_common.h"
 
 #include <algorithm>
+#include <limits>
 #include <cmath>
 
 #pragma clang fp contract(off)
@@ -151,6 +152,8 @@ struct SamplerBuffers {
     void * ctx2;
     float * velocity;
     float * prediction;
+    float * x0;
+    int64_t * status;
     void * guide_ws;
     void * flow_ws;
 };
@@ -168,6 +171,8 @@ SamplerBuffers carve_sampler(Carver & c, int dtype, const pxs_flow_config & f, i
     b.ctx2 = c.take(std::max<size_t>(tokens2, 1) * f.cond_channels * dtype_bytes(dtype));
     b.velocity = static_cast<float *>(c.take(r2 * f.out_channels * sizeof(float)));
     b.prediction = static_cast<float *>(c.take(static_cast<size_t>(rows) * f.out_channels * sizeof(float)));
+    b.x0 = static_cast<float *>(c.take(static_cast<size_t>(rows) * f.out_channels * sizeof(float)));
+    b.status = static_cast<int64_t *>(c.take(sizeof(int64_t)));
     b.guide_ws = c.take(pxs_flow_guidance_workspace_bytes(batch));
     b.flow_ws = c.take(pxs_slat_flow_workspace_bytes(dtype, &f, 2 * rows,
                                                      std::max<int64_t>(cond_tokens + uncond_tokens, 1),
@@ -331,6 +336,12 @@ int pxs_flow_euler_sample(int dtype, const pxs_flow_config * cfg, const pxs_flow
                           "pxs_flow_euler_sample: context copy"));
     }
     PXS_TRY(check_launch("pxs_flow_euler_sample setup"));
+    // One status word collects the reference's finiteness checks of every
+    // step: the model velocity (check_model_output -> valid(),
+    // src/flow_sampler.cpp:126-136) and, under CFG rescale, both x0 inputs of
+    // sparse_batch_std (src/flow_sampler.cpp:168).  It is read once, after the
+    // last step.
+    PXS_TRY(pxs_status_reset(b.status, stream));
 
     for (int step = 0; step < scfg->steps; ++step) {
         float t = 0.0f, t_next = 0.0f, guidance = 1.0f;
@@ -347,6 +358,7 @@ int pxs_flow_euler_sample(int dtype, const pxs_flow_config * cfg, const pxs_flow
                                           conditional ? cond_offsets : uncond_offsets,
                                           conditional ? cond_tokens : uncond_tokens, nullptr,
                                           b.velocity, b.flow_ws, stream));
+            PXS_TRY(pxs_check_finite(PXS_F32, b.velocity, rows, C, C, b.status, stream));
             pred = b.velocity;
         } else {
             // Both branches in one forward over the doubled batch.
@@ -362,6 +374,19 @@ int pxs_flow_euler_sample(int dtype, const pxs_flow_config * cfg, const pxs_flow
                                           b.x2, b.t2, b.ctx2, b.ctx_off2,
                                           cond_tokens + uncond_tokens, nullptr, b.velocity,
                                           b.flow_ws, stream));
+            PXS_TRY(pxs_check_finite(PXS_F32, b.velocity, 2 * rows, C, C, b.status, stream));
+            if (scfg->guidance_rescale > 0.0f) {
+                // x0 of the conditional prediction, then of the plain CFG blend.
+                PXS_TRY(pxs_flow_pred_to_xstart(samples, b.velocity, count, t, scfg->sigma_min,
+                                                b.x0, stream));
+                PXS_TRY(pxs_check_finite(PXS_F32, b.x0, rows, C, C, b.status, stream));
+                PXS_TRY(pxs_flow_guidance(samples, b.velocity, b.velocity + count, nullptr,
+                                          nullptr, rows, C, batch_size, t, scfg->sigma_min,
+                                          guidance, 0.0f, b.prediction, nullptr, stream));
+                PXS_TRY(pxs_flow_pred_to_xstart(samples, b.prediction, count, t, scfg->sigma_min,
+                                                b.x0, stream));
+                PXS_TRY(pxs_check_finite(PXS_F32, b.x0, rows, C, C, b.status, stream));
+            }
             PXS_TRY(pxs_flow_guidance(samples, b.velocity, b.velocity + count, coords, cu_rows, rows,
                                       C, batch_size, t, scfg->sigma_min, guidance,
                                       scfg->guidance_rescale, b.prediction, b.guide_ws, stream));
@@ -369,7 +394,14 @@ int pxs_flow_euler_sample(int dtype, const pxs_flow_config * cfg, const pxs_flow
         }
         PXS_TRY(pxs_flow_euler_update(samples, pred, count, t - t_next, stream));
     }
-    return check_launch("pxs_flow_euler_sample");
+    PXS_TRY(check_launch("pxs_flow_euler_sample"));
+    int64_t status = 0;
+    PXS_TRY(check_hip(hipMemcpyAsync(&status, b.status, sizeof(status), hipMemcpyDeviceToHost, s),
+                      "pxs_flow_euler_sample: status read"));
+    PXS_TRY(check_hip(hipStreamSynchronize(s), "pxs_flow_euler_sample: status read"));
+    PXS_CHECK(status == std::numeric_limits<int64_t>::max(), PXS_ERR_DATA,
+              "sparse features contain a non-finite value");
+    return PXS_OK;
 }
 
 } // extern "C"

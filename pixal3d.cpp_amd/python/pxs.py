@@ -11,6 +11,7 @@ import ctypes as C
 import os
 from pathlib import Path
 
+import numpy as np
 import torch
 
 PKG = Path(__file__).resolve().parents[1]
@@ -48,6 +49,8 @@ _SIGS = {
     "pxs_subm_conv3d": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "pxs_status_reset": (_i32, [_vp, _vp]),
     "pxs_check_finite": (_i32, [_i32, _vp, _i64, _i32, _i64, _vp, _vp]),
+    "pxs_value_stats_workspace_bytes": (C.c_size_t, [_i64]),
+    "pxs_value_stats_f32": (_i32, [_vp, _i64, _vp, _vp, _vp]),
     "pxs_downsample_workspace_bytes": (C.c_size_t, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "pxs_downsample_topology": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                        _vp, _vp]),
@@ -522,6 +525,19 @@ class Pxs:
                                              freq_base, _ptr(q), _ptr(k), _ptr(v), self.stream()),
                     "pxs_qkv_prepare")
         return q, k, v
+
+    def value_stats(self, x):
+        """pxs_value_stats_f32 over an fp32 tensor -> dict of the summary."""
+        count = x.numel()
+        raw = torch.empty(40, dtype=torch.uint8, device=x.device)
+        ws = self._ws(self.lib.pxs_value_stats_workspace_bytes(count), x.device)
+        self._check(self.lib.pxs_value_stats_f32(_ptr(x), count, _ptr(raw), _ptr(ws),
+                                                 self.stream()), "pxs_value_stats_f32")
+        b = raw.cpu().numpy()
+        i64, f64, f32 = b[:16].view(np.int64), b[16:24].view(np.float64), b[24:40].view(np.float32)
+        return {"nonfinite": int(i64[0]), "first_bad": int(i64[1]), "sum": float(f64[0]),
+                "first_bad_value": float(f32[0]), "min": float(f32[1]), "max": float(f32[2]),
+                "max_abs": float(f32[3])}
 
     def activation(self, x, act):
         self._check(self.lib.pxs_activation(_dtype_code(x), _ptr(x), x.numel(), act, self.stream()),

@@ -10,6 +10,10 @@ The expected outputs are the reference binaries' printed values, committed as
 tests/golden/*.json.
 """
 
+import os
+import sys
+import tempfile
+
 import numpy as np
 
 import workloads as W
@@ -132,3 +136,60 @@ def flow_velocity(coords, channels, seed=5):
         return (np.tanh(s * a[conditional]) * scale + m[conditional][items] + xo).astype(np.float32)
 
     return fn
+
+
+def child_slots_brute_force(coords, out_coords):
+    """Slot c of output (b, X, Y, Z) holds the input row at
+    (b, 2X + (c & 1), 2Y + ((c >> 1) & 1), 2Z + (c >> 2)), or -1: the
+    little-endian child order of the reference's factor-2 subdivision
+    (src/sparse.cpp:676-690), found by dictionary lookup."""
+    where = {tuple(r): i for i, r in enumerate(coords.tolist())}
+    expect = np.full((out_coords.shape[0], 8), -1, np.int32)
+    for q, (b, x, y, z) in enumerate(out_coords.tolist()):
+        for c in range(8):
+            expect[q, c] = where.get((b, 2 * x + (c & 1), 2 * y + ((c >> 1) & 1),
+                                      2 * z + (c >> 2)), -1)
+    return expect
+
+
+def subdivided_parents(seed, channels, masked):
+    """Parents on a 10^3 grid (two batch items) with 8*channels features and,
+    when masked, a +-1 subdivision mask with at least one child per parent."""
+    parents = W.shell_coords(10, [[(2.0, 4.0)], [(1.5, 3.5)]], seed)
+    m = parents.shape[0]
+    pf = W.normal(seed, m * 8 * channels, 1).reshape(m, 8 * channels)
+    sub = None
+    if masked:
+        sub = np.where(W.uniform(seed, m * 8, 2).reshape(m, 8) < 0.5, 1.0, -1.0).astype(np.float32)
+        sub[np.arange(m), np.arange(m) % 8] = 1.0
+    return parents, pf, sub
+
+
+# Flow-sampler runs whose PIXAL3D_FLOW_NONFINITE_TRACE lines the compiled
+# reference wrote to tests/golden/flow_trace_lines.json (make_trace_golden.py).
+# name: (steps, [sigma_min, rescale_t, strength, rescale, interval_min, interval_max], record)
+TRACE_CASES = {
+    "guided_rescale": (2, [1e-5, 3.0, 7.5, 0.7, 0.0, 1.0], True),
+    "unguided": (2, [1e-5, 1.0, 1.0, 0.0, 0.0, 1.0], True),
+    "blend_overflow": (2, [1e-5, 1.0, 3.0, 0.0, 0.0, 1.0], False),
+}
+
+
+def overflow_velocity(state, t_model, conditional):
+    """+-3e38 velocities: their CFG blend overflows to infinity."""
+    return np.full_like(state, 3e38 if conditional else -3e38)
+
+
+def capture_stderr(fn):
+    """Run fn with file descriptor 2 redirected to a file; -> (result, text)."""
+    sys.stderr.flush()
+    saved = os.dup(2)
+    with tempfile.TemporaryFile(mode="w+b") as tmp:
+        os.dup2(tmp.fileno(), 2)
+        try:
+            result = fn()
+        finally:
+            os.dup2(saved, 2)
+            os.close(saved)
+        tmp.seek(0)
+        return result, tmp.read().decode()

@@ -141,3 +141,36 @@ def test_attention_empty_key_segment_gives_zeros(px):
     k = W.normal(65, 4 * 64, 2).reshape(4, 64)
     o = host(px.varlen_attention(t32(q), t32(k), t32(k), ti64([0, 6, 10]), ti64([0, 4, 4]), 1, 64, 0.125))
     assert np.all(o[6:] == 0) and np.all(np.isfinite(o))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("hd,vd", [(128, 128), (96, 160), (200, 40)])
+def test_attention_wide_heads(px, orc, dtype, hd, vd):
+    """Heads wider than 64 (the drop-in's reference API allows any width):
+    self-attention over three segments, cross-attention with one empty key
+    segment, and a permuted row order, against the oracle."""
+    lens, klens = (300, 77, 1), (50, 0, 130)
+    heads = 2
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    cuk = np.concatenate([[0], np.cumsum(klens)]).astype(np.int64)
+    n, nk = int(cu[-1]), int(cuk[-1])
+    rnd = lambda rows, w, s: W.bf16_round(W.normal(66, rows * w, s).reshape(rows, w))  # noqa: E731
+    q, k, v = rnd(n, heads * hd, 1), rnd(n, heads * hd, 2), rnd(n, heads * vd, 3)
+    ck, cv = rnd(nk, heads * hd, 4), rnd(nk, heads * vd, 5)
+    conv = t32 if dtype == "f32" else tbf
+    check = assert_fp32 if dtype == "f32" else assert_bf16
+    scale = float(hd) ** -0.5
+    print(f"[attn wide] dtype={dtype} hd={hd} vd={vd}", flush=True)
+    o = host(px.varlen_attention(conv(q), conv(k), conv(v), ti64(cu), ti64(cu), heads, hd, scale,
+                                 value_dim=vd))
+    check(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(scale)), what="wide self")
+    o = host(px.varlen_attention(conv(q), conv(ck), conv(cv), ti64(cu), ti64(cuk), heads, hd,
+                                 scale, value_dim=vd))
+    ref = orc.varlen_attention(q, ck, cv, cu, cuk, heads, hd, np.float32(scale))
+    assert np.all(o[cu[1]:cu[2]] == 0)
+    check(o, ref, what="wide cross")
+    perm = np.random.default_rng(7).permutation(n).astype(np.int32)
+    o = host(px.varlen_attention(conv(q), conv(k), conv(v), ti64(cu), ti64(cu), heads, hd, scale,
+                                 row_map=ti32(perm), value_dim=vd))
+    ref = orc.varlen_attention(q[perm], k[perm], v[perm], cu, cu, heads, hd, np.float32(scale))
+    check(o[perm], ref, what="wide permuted")

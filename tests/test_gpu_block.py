@@ -116,3 +116,27 @@ def test_flow_bf16_reduced_config(px, orc):
     ref = oracle_flow(orc, case, bf16=True)
     assert np.isfinite(got).all()
     assert_bf16(got, ref, what="flow bf16 reduced")
+
+
+def test_block_fp32_wide_heads(px, orc):
+    """A block with 128-wide heads (C = 256, 2 heads; RoPE, q/k RMS norms,
+    cross-attention), fp32, against the oracle block
+    (src/sparse_transformer.cpp:138-292); the reference allows any head width."""
+    from test_gpu_configs import flow_block_weights, normal
+    rng = np.random.default_rng(94)
+    coords = W.shell_coords(12, [[(3.0, 5.0)], [(2.0, 4.0)]], 94)
+    n, C, H, M, CC, T = coords.shape[0], 256, 2, 512, 64, 9
+    ws = flow_block_weights(rng, C, M, CC)
+    x = normal(rng, (n, C))
+    tmod = normal(rng, (2, 6 * C), 0.3)
+    ctx = normal(rng, (2 * T, CC))
+    off = np.array([0, T, 2 * T], np.int64)
+    print(f"[block wide heads] n={n} head_dim={C // H}", flush=True)
+    c = ti32(coords)
+    hidden = t32(x).clone()
+    dws = device_weights(ws, torch.float32)  # kept alive: the struct holds raw pointers
+    px.transformer_block(block_cfg(C, H, M, CC, 0, False), pxs.block_weights(dws), c, 2,
+                         px.batch_cu_seqlens(c, 2), hidden, t32(tmod), t32(ctx), ti64(off))
+    ref = orc.transformer_block(coords, 2, x, tmod, ctx, off, [C, H, M, CC, 0, 1, 1, 1, 0],
+                                [1e-6, 1.0, 10000.0], ws)
+    assert_fp32(host(hidden), ref, what="block wide heads")

@@ -181,6 +181,35 @@ def test_strided_conv_identity_invariant(px, orc):
     assert_fp32(y, counts * mean, what="identity s2")
 
 
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_strided_conv_one_hot_inverts_subdivision(px, orc, dtype, masked):
+    """Children from the oracle's sparse_channel_to_spatial (factor 2, pinned to
+    the reference's child order c = cx + 2cy + 4cz): the device child map equals
+    the brute-force slots, and the device stride-2 conv with W_c0 = I, every other
+    W_c = 0, bias 0 hands back slice c0 of every parent (0 where the mask dropped
+    child c0), exactly, for each of the 8 slots."""
+    from fixtures import child_slots_brute_force, subdivided_parents
+
+    cp = 16
+    parents, pf, sub = subdivided_parents(30, cp, masked)
+    if dtype == "bf16":
+        pf = W.bf16_round(pf)
+    cc, cf = orc.channel_to_spatial(parents, pf, 2, sub)
+    print(f"[s2 one-hot] dtype={dtype} masked={masked} children={cc.shape[0]}", flush=True)
+    oc, child, m = px.downsample_s2(ti32(cc), 2, (20, 20, 20))
+    np.testing.assert_array_equal(oc.cpu().numpy(), parents)
+    cm = child.cpu().numpy()[:, :m].T
+    np.testing.assert_array_equal(cm, child_slots_brute_force(cc, parents))
+    conv = tbf if dtype == "bf16" else t32
+    keep = np.ones((m, 8), np.float32) if sub is None else (sub > 0).astype(np.float32)
+    for c0 in range(8):
+        w = np.zeros((8, cp, cp), np.float32)
+        w[c0] = np.eye(cp, dtype=np.float32)
+        y = host(px.sparse_conv3d_s2(conv(cf), conv(w), t32(np.zeros(cp)), child, m))
+        np.testing.assert_array_equal(y, pf[:, c0 * cp:(c0 + 1) * cp] * keep[:, c0:c0 + 1])
+
+
 def test_downsample_mean_matches_reference_vectors(px):
     v = dict(np.load(GOLD / "ref_vectors.npz"))
     oc, off, rows, m = px.downsample(ti32(v["ds_coords"]), 2, (16, 16, 16), 2)

@@ -264,3 +264,26 @@ def test_dropin_argument_errors(di):
                  "sparse cross-attention scale must be finite and positive")
     expect_error(lambda: di.mh_rms_norm(t, 3, 2, np.ones(4, np.float32)),
                  "sparse RMS norm head dimensions are invalid")
+
+
+def test_dropin_attention_wide_heads(di, orc):
+    """sparse_scaled_dot_product_attention and sparse_cross_attention with
+    heads wider than 64 (128-wide q/k, 96-wide v) against the oracle, which
+    follows src/sparse.cpp:704-859."""
+    coords = W.shell_coords(12, [[(3.0, 5.0)], [(2.0, 4.0)]], 67)
+    n = coords.shape[0]
+    heads, hd, vd = 2, 128, 96
+    q = W.normal(67, n * heads * hd, 1).reshape(n, heads * hd)
+    k = W.normal(67, n * heads * hd, 2).reshape(n, heads * hd)
+    v = W.normal(67, n * heads * vd, 3).reshape(n, heads * vd)
+    shp = (12, 12, 12)
+    out = di.sdpa(di.sparse(coords, q, 2, shp), di.sparse(coords, k, 2, shp),
+                  di.sparse(coords, v, 2, shp), heads, hd, 0.09).read()[1]
+    cu = orc.batch_cu_seqlens(coords, 2)
+    close(out, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.09)), "sdpa wide")
+    off = np.array([0, 7, 20], np.int64)
+    ck = W.normal(67, 20 * heads * hd, 4).reshape(20, heads * hd)
+    cv = W.normal(67, 20 * heads * vd, 5).reshape(20, heads * vd)
+    out = di.cross_attention(di.sparse(coords, q, 2, shp), di.varlen(off, ck), di.varlen(off, cv),
+                             heads, hd, 0.09).read()[1]
+    close(out, orc.varlen_attention(q, ck, cv, cu, off, heads, hd, np.float32(0.09)), "cross wide")

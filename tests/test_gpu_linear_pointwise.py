@@ -159,3 +159,26 @@ def test_linear_ordered_bit_exact(px, orc, cin, cout):
     b = W.normal(91, cout, 3)
     got = px.linear_ordered(t32(x), t32(w), t32(b))
     np.testing.assert_array_equal(host(got), orc.linear(x, w, b))
+
+
+@pytest.mark.parametrize("count", [0, 1, 777, 1_000_003])
+def test_value_stats(px, count):
+    """pxs_value_stats_f32 against numpy: finite min / max / max |v| exactly,
+    the sum to double rounding, the non-finite count and the first one."""
+    x = W.normal(68, count, 1) * np.float32(3.0)
+    if count > 100:
+        x[count // 3] = np.inf
+        x[count // 2] = np.nan
+        x[count - 1] = -np.inf
+    print(f"[value stats] count={count}", flush=True)
+    got = px.value_stats(t32(x))
+    fin = x[np.isfinite(x)]
+    bad = np.flatnonzero(~np.isfinite(x))
+    assert got["nonfinite"] == bad.size
+    assert got["first_bad"] == (bad[0] if bad.size else count)
+    if bad.size:
+        assert got["first_bad_value"] == x[bad[0]]
+    assert got["min"] == (fin.min() if fin.size else np.inf)
+    assert got["max"] == (fin.max() if fin.size else -np.inf)
+    assert got["max_abs"] == (np.abs(fin).max() if fin.size else 0.0)
+    assert abs(got["sum"] - fin.astype(np.float64).sum()) <= 1e-9 * max(1.0, np.abs(fin).sum())

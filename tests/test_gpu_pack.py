@@ -49,7 +49,7 @@ def upload_pack(tmp_path):
     finite = halves[(halves & 0x7C00) != 0x7C00]           # every finite half
     rng = np.random.default_rng(9)
     f32 = np.concatenate([rng.standard_normal(1003).astype(np.float32) * 5,
-                          np.array([0.0, -0.0, 1e-40, -3e-39, 3.4e38, -1.17549435e-38],
+                          np.array([0.0, -0.0, 1e-40, -3e-39, 3.38e38, -1.17549435e-38],
                                    np.float32),
                           ((np.arange(40, dtype=np.uint32) << 16) | 0x8000).view(np.float32)])
     bf = G.bf16_bits(rng.standard_normal(777).astype(np.float32) * 100)
@@ -59,6 +59,7 @@ def upload_pack(tmp_path):
                G.Tensor("bf16_rand", G.GGML_BF16, (bf.size,), bf.tobytes()),
                G.Tensor("f16_big", G.GGML_F16, (big.size,), big.tobytes()),
                G.f32_tensor("f32_inf", np.array([1.0, 2.0, np.inf, 3.0], np.float32)),
+               G.f32_tensor("f32_over_bf16", np.array([1.0, -3.4e38, 2.0], np.float32)),
                G.Tensor("f16_nan", G.GGML_F16, (3,), np.array([0x3C00, 0x7E00, 0], np.uint16)
                         .tobytes()),
                G.Tensor("q4", 2, (32,), bytes(18))]
@@ -95,6 +96,12 @@ def test_upload_errors(px, tmp_path):
             pack.upload("f32_inf", pxs.PXS_F32, 4)
         with pytest.raises(pxs.PxsError, match=r"non-finite value: f16_nan \(code 3\)"):
             pack.upload("f16_nan", pxs.PXS_BF16, 3)
+        # a finite F32 beyond the bf16 range loads as fp32, but as bf16 it would
+        # become an infinity: that load fails like a non-finite payload
+        got = pack.upload("f32_over_bf16", pxs.PXS_F32, 3)
+        assert float(got[1]) == float(np.float32(-3.4e38))
+        with pytest.raises(pxs.PxsError, match=r"non-finite value: f32_over_bf16"):
+            pack.upload("f32_over_bf16", pxs.PXS_BF16, 3)
         with pytest.raises(pxs.PxsError, match="has type q4_0, not f32, f16 or bf16"):
             pack.upload("q4", pxs.PXS_F32, 32)
         with pytest.raises(pxs.PxsError, match="holds 1049 elements, not 1048"):

@@ -157,3 +157,77 @@ def test_device_sampler_matches_oracle(px, orc):
     e = max_rel(got, ref)
     print(f"[device sampler vs oracle] max rel {e:.2e}", flush=True)
     assert e <= FP32_TOL, f"device sampler: max rel error {e:.3e}"
+
+
+@pytest.mark.parametrize("guidance,rescale", [(1.0, 0.0), (5.0, 0.0), (5.0, 0.7)])
+def test_device_sampler_rejects_nonfinite_velocity(px, guidance, rescale):
+    """A NaN output bias makes every velocity non-finite: the device sampler
+    reports the reference's check (check_model_output -> valid(),
+    src/flow_sampler.cpp:126-136) as PXS_ERR_DATA with its message, on the
+    single-branch and the batched CFG paths; the same call with a finite bias
+    succeeds."""
+    case, cfg, weights, keep, uncond = flow_setup(px, torch.float32)
+    coords = ti32(case["coords"])
+    cu = px.batch_cu_seqlens(coords, 2)
+    noise = t32(np.random.default_rng(5).standard_normal((case["n"], 8)).astype(np.float32))
+    scfg = pxs.SamplerConfig(2, 1e-5, 3.0, guidance, rescale, 0.0, 1.0)
+    args = (cfg, weights, scfg, coords, 2, cu, noise, t32(case["ctx"]), ti64(case["ctx_off"]),
+            t32(uncond), ti64(np.array([0, 3, 6], np.int64)))
+    print(f"[device sampler nan] guidance={guidance} rescale={rescale}", flush=True)
+    assert np.isfinite(host(px.flow_euler_sample(*args))).all()
+    out_bias = keep[0][9]
+    out_bias[3] = float("nan")
+    with pytest.raises(pxs.PxsError, match="sparse features contain a non-finite value"):
+        px.flow_euler_sample(*args)
+    out_bias[3] = 0.0
+    assert np.isfinite(host(px.flow_euler_sample(*args))).all()
+
+
+def trace_fields(line):
+    head, _, rest = line.partition("pixal3d: flow trace ")
+    return dict(kv.split("=", 1) for kv in rest.split())
+
+
+@pytest.mark.parametrize("case", ["guided_rescale", "unguided", "blend_overflow"])
+def test_dropin_sampler_trace_matches_reference(case, monkeypatch):
+    """PIXAL3D_FLOW_NONFINITE_TRACE: the drop-in's stderr lines (figures from
+    one device reduction per traced tensor) against the lines the compiled
+    reference printed for the same run (tests/golden/flow_trace_lines.json):
+    the same tensors in the same order with the same step, timestep, branch,
+    counts, min, max, max_abs and first bad value, the mean within 1e-5
+    (a double tree sum against a serial long-double sum), and the same error."""
+    import json
+    from pathlib import Path
+
+    from fixtures import TRACE_CASES, capture_stderr, overflow_velocity
+
+    gold = json.loads((Path(__file__).resolve().parent / "golden" / "flow_trace_lines.json")
+                      .read_text())[case]
+    steps, cfg, record = TRACE_CASES[case]
+    coords, noise, fn = sampler_inputs()
+    velocity = overflow_velocity if case == "blend_overflow" else fn
+    d = O.DropIn()
+    monkeypatch.setenv("PIXAL3D_FLOW_NONFINITE_TRACE", "1")
+    print(f"[drop-in trace] case={case}", flush=True)
+
+    def run():
+        try:
+            d.flow_euler_sample(d.sparse(coords, noise, 2, (12, 12, 12)), steps, cfg, velocity,
+                                record=record)
+            return None
+        except O.ReferenceError as e:
+            return str(e)
+
+    error, text = capture_stderr(run)
+    lines = [ln for ln in text.splitlines() if ln.startswith("pixal3d: flow trace")]
+    assert error == gold["error"]
+    assert len(lines) == len(gold["lines"])
+    for got, want in zip(lines, gold["lines"]):
+        g, w = trace_fields(got), trace_fields(want)
+        assert g.keys() == w.keys(), (got, want)
+        for key in g:
+            if key == "mean":
+                gm, wm = float(g[key]), float(w[key])
+                assert abs(gm - wm) <= 1e-5 * max(abs(wm), 1e-3), (got, want)
+            else:
+                assert g[key] == w[key], (key, got, want)

@@ -18,7 +18,7 @@ import pytest
 
 import oracle as O
 import workloads as W
-from fixtures import block_kat, kat_inputs
+from fixtures import block_kat, child_slots_brute_force, kat_inputs, subdivided_parents
 
 GOLD = Path(__file__).resolve().parent / "golden"
 
@@ -126,15 +126,20 @@ def test_ref_vectors_block_and_timestep(orc, vec):
                                v["temb_b2"]), v["temb_out"])
 
 
-def test_row_sampled_block_matches_full(orc, vec):
-    """Row sampling (the CPU baseline for large configs) is exact per sampled row."""
+@pytest.mark.parametrize("proj", [True, False])
+def test_row_sampled_block_matches_full(orc, vec, proj):
+    """Row sampling (the CPU baseline and the parity check for large configs:
+    linears and attentions on the sampled rows, keys and values on all rows)
+    is exact per sampled row, against the compiled reference's block."""
     v = vec
     ws = [v[f"blk_w{i}"] for i in range(23)]
-    rows = np.array([0, 5, 17, v["blk_coords"].shape[0] - 1])
+    rows = np.array([0, 5, 17, 40, v["blk_coords"].shape[0] - 1])
     out = orc.transformer_block(v["blk_coords"], 2, v["blk_x"], v["blk_tmod"], v["blk_ctx"],
-                                v["blk_ctx_off"], [32, 4, 64, 6, 5, 1, 1, 1, 0],
-                                [1e-6, 1.0, 10000.0], ws, rows=rows)
-    np.testing.assert_array_equal(out[rows], v["blk_out_noproj"][rows])
+                                v["blk_ctx_off"], [32, 4, 64, 6, 5, 1, 1, 1, int(proj)],
+                                [1e-6, 1.0, 10000.0], ws, rows=rows,
+                                projected=v["blk_proj"] if proj else None)
+    want = v["blk_out"] if proj else v["blk_out_noproj"]
+    np.testing.assert_array_equal(out[rows], want[rows])
 
 
 def test_ref_conv_full_size(orc):
@@ -246,6 +251,38 @@ def test_strided_conv_identity_is_count_times_mean(orc):
     # every input row is a child of exactly one output row
     rows = np.sort(child[child >= 0])
     np.testing.assert_array_equal(rows, np.arange(n))
+
+
+def test_strided_conv_child_slots_brute_force(orc):
+    coords = W.shell_coords(16, [[(4.0, 7.0)], [(3.0, 6.0)]], 28)
+    oc, child = orc.downsample_coords_s2(coords)
+    np.testing.assert_array_equal(child, child_slots_brute_force(coords, oc))
+    # a big-endian or axis-swapped order would differ on this input
+    assert (child[:, 1] != child[:, 4]).any() and (child[:, 2] != child[:, 4]).any()
+
+
+@pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref is built only where /root/reference exists")
+@pytest.mark.parametrize("masked", [False, True])
+def test_strided_conv_one_hot_inverts_reference_subdivision(orc, masked):
+    """The compiled reference's sparse_channel_to_spatial (factor 2) moves parent
+    channel slice c to child c = cx + 2cy + 4cz (src/sparse.cpp:676-690).  A
+    stride-2 conv over those children with W_c0 = I, every other W_c = 0 and
+    bias 0 must hand back slice c0 of every parent, or 0 where the mask dropped
+    child c0, for each of the 8 slots: any other child order fails."""
+    ref = O.Reference()
+    cp = 5
+    parents, pf, sub = subdivided_parents(29, cp, masked)
+    sub_h = None if sub is None else ref.sparse(parents, sub, 2, (10, 10, 10))
+    cc, cf = ref.channel_to_spatial(ref.sparse(parents, pf, 2, (10, 10, 10)), 2, sub_h).read()
+    oc, child = orc.downsample_coords_s2(cc)
+    np.testing.assert_array_equal(oc, parents)
+    np.testing.assert_array_equal(child, child_slots_brute_force(cc, oc))
+    keep = np.ones((parents.shape[0], 8), np.float32) if sub is None else (sub > 0)
+    for c0 in range(8):
+        w = np.zeros((8, cp, cp), np.float32)
+        w[c0] = np.eye(cp, dtype=np.float32)
+        out = orc.sparse_conv3d_s2(child, cf, w, np.zeros(cp, np.float32))
+        np.testing.assert_array_equal(out, pf[:, c0 * cp:(c0 + 1) * cp] * keep[:, c0:c0 + 1])
 
 
 def test_window_partition_brute_force(orc):

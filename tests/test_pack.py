@@ -162,6 +162,11 @@ def test_upload_rejects_misaligned_workspace(px):
         assert rc == pxs.PXS_ERR_ARG
         assert px.lib.pxs_last_error().decode() == \
             "pxs_pack_upload: workspace must be 256-byte aligned"
+        # a null argument is reported before the alignment
+        rc = px.lib.pxs_pack_upload(None, t.name.encode(), pxs.PXS_F32, 1 << 20, count,
+                                    (1 << 20) + 8, None)
+        assert rc == pxs.PXS_ERR_ARG
+        assert px.lib.pxs_last_error().decode() == "pxs_pack_upload: null argument"
 
 
 def reference_case_pack(path):
