@@ -298,6 +298,23 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
                          const int32_t * row_map, int heads, int head_dim, int value_dim,
                          float scale, void * o, int64_t ld_o, void * workspace, void * stream);
 
+/* pxs_varlen_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * Its scratch (segment tile counts and their prefix sums) lives in a 1 MiB
+ * array in the library's device image, one per GPU, held until the process
+ * ends; nseg is limited to PXS_ATTN_NOALLOC_MAX_SEGMENTS (a larger count is
+ * an argument error).  It allocates nothing and otherwise behaves exactly as
+ * pxs_varlen_attention (same kernels, same results).  All calls on one GPU
+ * share that array: calls that overlap on one GPU (several streams or host
+ * threads) race and must be ordered by the caller. */
+#define PXS_ATTN_NOALLOC_MAX_SEGMENTS 65536
+int pxs_varlen_attention_noalloc(int dtype, const void * q, int64_t ld_q, const void * k,
+                                 int64_t ld_k, const void * v, int64_t ld_v, const int64_t * cu_q,
+                                 const int64_t * cu_k, int nseg, int64_t total_q,
+                                 const int32_t * row_map, int heads, int head_dim, int value_dim,
+                                 float scale, void * o, int64_t ld_o, void * stream);
+
 /* Per-batch cu_seqlens from the batch column (src/sparse.cpp:731-737):
  * cu (device int64[batch_size + 1]). */
 int pxs_batch_cu_seqlens(const int32_t * coords, int64_t n, int batch_size, int64_t * cu,

@@ -19,6 +19,7 @@
 #include "scan.h"
 
 #include <cmath>
+#include <atomic>
 #include <type_traits>
 
 namespace pxs {
@@ -712,6 +713,40 @@ int launch_attn(const AttnArgs & args, int64_t total_q, int heads, hipStream_t s
 
 bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Scratch of pxs_varlen_attention_noalloc: the segment tile counts, their
+// prefix sums and the scan partials of up to PXS_ATTN_NOALLOC_MAX_SEGMENTS
+// segments.  Each device holds its own copy for the life of the process.
+constexpr size_t kNoAllocScratchBytes = 1u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the host-side symbol is only a stand-in and must never reach a
+// kernel).
+int noalloc_scratch(void ** out) {
+    int dev = 0;
+    if (int rc = check_hip(hipGetDevice(&dev), "pxs_varlen_attention_noalloc: hipGetDevice"))
+        return rc;
+    PXS_CHECK(dev >= 0 && dev < kMaxDevices, PXS_ERR_ARG,
+              "pxs_varlen_attention_noalloc: device index out of range");
+    // Racing first calls look up the same address and store the same value.
+    void * cached = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!cached) {
+        void * ptr = nullptr;
+        if (int rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
+                               "pxs_varlen_attention_noalloc: hipGetSymbolAddress"))
+            return rc;
+        PXS_CHECK(ptr != nullptr, PXS_ERR_HIP,
+                  "pxs_varlen_attention_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+        cached = ptr;
+    }
+    *out = cached;
+    return PXS_OK;
+}
+
 // Heads wider than the tiled kernels take (head_dim or value_dim above 64, up
 // to kWideMaxDim): one wavefront per (query row, head) walks the segment's
 // keys in order with an online softmax.  Lane l owns dims l, l + 64, ... of
@@ -863,6 +898,22 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     }
     return nw == 4 ? launch_attn<float, 4>(a, total_q, heads, s)
                    : launch_attn<float, 1>(a, total_q, heads, s);
+}
+
+int pxs_varlen_attention_noalloc(int dtype, const void * q, int64_t ld_q, const void * k,
+                                 int64_t ld_k, const void * v, int64_t ld_v, const int64_t * cu_q,
+                                 const int64_t * cu_k, int nseg, int64_t total_q,
+                                 const int32_t * row_map, int heads, int head_dim, int value_dim,
+                                 float scale, void * o, int64_t ld_o, void * stream) {
+    PXS_CHECK(nseg <= PXS_ATTN_NOALLOC_MAX_SEGMENTS, PXS_ERR_ARG,
+              "pxs_varlen_attention_noalloc: more than PXS_ATTN_NOALLOC_MAX_SEGMENTS (65536) "
+              "segments; use pxs_varlen_attention with a workspace");
+    PXS_CHECK(pxs_attention_workspace_bytes(nseg) <= kNoAllocScratchBytes, PXS_ERR_ARG,
+              "pxs_varlen_attention_noalloc: scratch too small for this segment count");
+    void * ws = nullptr;
+    if (int rc = noalloc_scratch(&ws)) return rc;
+    return pxs_varlen_attention(dtype, q, ld_q, k, ld_k, v, ld_v, cu_q, cu_k, nseg, total_q,
+                                row_map, heads, head_dim, value_dim, scale, o, ld_o, ws, stream);
 }
 
 } // extern "C"

@@ -19,6 +19,7 @@ LIB_PATH = Path(os.environ.get("PXS_LIB", PKG / "lib" / "libpxs.so"))
 
 PXS_OK, PXS_ERR_ARG, PXS_ERR_HIP, PXS_ERR_DATA = 0, 1, 2, 3
 PXS_F32, PXS_BF16 = 0, 1
+PXS_ATTN_NOALLOC_MAX_SEGMENTS = 65536
 ACT_NONE, ACT_GELU_TANH, ACT_SILU = 0, 1, 2
 
 VALIDATION_MESSAGES = {
@@ -93,6 +94,8 @@ _SIGS = {
     "pxs_attention_workspace_bytes": (C.c_size_t, [_i32]),
     "pxs_varlen_attention": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _i64, _vp,
                                     _i32, _i32, _i32, _f, _vp, _i64, _vp, _vp]),
+    "pxs_varlen_attention_noalloc": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32,
+                                            _i64, _vp, _i32, _i32, _i32, _f, _vp, _i64, _vp]),
     "pxs_batch_cu_seqlens": (_i32, [_vp, _i64, _i32, _vp, _vp]),
     "pxs_window_partition_workspace_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32, _i32, _i32, _i64]),
     "pxs_window_partition": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
