@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="unet_stage_128",
                     choices=["unet_stage_128", "conv_fp32_64", "attn_block", "swin_64",
-                             "flow_step", "flow_sample", "decoder", "pack_load"])
+                             "flow_step", "flow_sample", "decoder", "pack_load", "hash_map_128"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     return ap.parse_args()
@@ -112,11 +112,40 @@ def warm_up(args, torch, step):
 
 
 def cpu_threads():
+    """OpenMP threads for the CPU baseline and how they were chosen: the
+    process's CPU affinity, capped by a cgroup CPU quota and by
+    OMP_NUM_THREADS when either is set (a GPU box's CPU share can be smaller
+    than the CPUs its affinity mask lists)."""
     try:
-        n = len(os.sched_getaffinity(0))
+        affinity = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        affinity = os.cpu_count() or 1
+    limits = {"affinity": affinity}
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if quota != "max":
+            limits["cgroup_quota"] = max(1, int(int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        limits["OMP_NUM_THREADS"] = int(omp)
+    return max(1, min(limits.values())), limits
+
+
+def cpu_timing(fn, warmup=2, iterations=3):
+    """The reference benchmark's method (tests/sparse_linear_cuda_benchmark.cpp:
+    717-731): `warmup` untimed calls, then `iterations` timed ones; -> (median s,
+    min s)."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(iterations):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], times[0]
 
 
 # ---------------------------------------------------------------------------
@@ -144,24 +173,27 @@ def unet_stage(args, torch, px, W):
     def ws(nbytes):
         return torch.empty(max(int(nbytes), 8), dtype=torch.uint8, device=dev)
 
-    # Buffers sized once.
-    grid1 = ws(lib.pxs_voxel_grid_bytes(2, 128, 128, 128))
+    # Buffers sized once.  The voxel grids are generation-tagged: reset once
+    # here, then every step inserts its rows under a new generation, so no
+    # step refills a grid (O(rows) per build, not O(cells)).
+    grid1 = px.tagged_grid(2, (128, 128, 128))
+    grid2 = ws(lib.pxs_voxel_grid_bytes(2, 64, 64, 64))  # rewritten whole by the s2 topology
+    ds_ws = px.s2_tagged_workspace(2, (128, 128, 128))
     nbr1 = torch.empty((27, n), dtype=torch.int32, device=dev)
     mask1 = torch.empty(n, dtype=torch.int32, device=dev)
     y_a = torch.empty((n, 128), dtype=torch.bfloat16, device=dev)
     oc = torch.empty((n, 4), dtype=torch.int32, device=dev)
     child = torch.empty((8, n), dtype=torch.int32, device=dev)
     m_dev = torch.empty(1, dtype=torch.int64, device=dev)
-    ds_ws = ws(lib.pxs_downsample_workspace_bytes(n, 2, 128, 128, 128, 2))
     # Topology size (deterministic for these coordinates): one sync here,
     # outside the timed region; every step recomputes the topology itself.
     _, _, m = px.downsample_s2(coords, 2, (128, 128, 128))
     y_b = torch.empty((m, 256), dtype=torch.bfloat16, device=dev)
-    grid2 = ws(lib.pxs_voxel_grid_bytes(2, 64, 64, 64))
     nbr2 = torch.empty((27, m), dtype=torch.int32, device=dev)
     mask2 = torch.empty(m, dtype=torch.int32, device=dev)
     y_c = torch.empty((m, 256), dtype=torch.bfloat16, device=dev)
     timer = Timer(torch)
+    gen = [0]
 
     def chk(rc, what):
         if rc != 0:
@@ -169,20 +201,22 @@ def unet_stage(args, torch, px, W):
 
     def step():
         s = S()
+        gen[0] += 1
+        g = C.c_uint32(gen[0])
         timer.run("neighbor_map_128", lambda: (
-            chk(lib.pxs_voxel_grid_build(P(coords), n, 2, 128, 128, 128, P(grid1), s), "grid"),
-            chk(lib.pxs_neighbor_map_k3_grid(P(coords), n, 2, 128, 128, 128, P(grid1), P(nbr1),
-                                             P(mask1), s), "map")))
+            chk(lib.pxs_voxel_grid_tagged_insert(P(coords), n, 2, 128, 128, 128, P(grid1), g, s),
+                "grid"),
+            chk(lib.pxs_neighbor_map_k3_grid_tagged(P(coords), n, 2, 128, 128, 128, P(grid1), g,
+                                                    P(nbr1), P(mask1), s), "map")))
         timer.run("subm_conv_a", lambda: chk(lib.pxs_subm_conv3d(
             1, P(x), n, 128, P(w_a), P(b_a), 128, P(nbr1), P(mask1), P(y_a), s), "conv a"))
-        timer.run("downsample_s2", lambda: chk(lib.pxs_downsample_s2_topology(
-            P(coords), n, 2, 128, 128, 128, P(oc), P(child), P(m_dev), P(ds_ws), s), "ds"))
+        timer.run("downsample_s2", lambda: chk(lib.pxs_downsample_s2_topology_tagged(
+            P(coords), n, 2, 128, 128, 128, P(grid1), g, P(oc), P(child), n, P(m_dev), P(grid2),
+            P(ds_ws), s), "ds"))
         timer.run("sparse_conv_b", lambda: chk(lib.pxs_sparse_conv3d_s2(
             1, P(y_a), n, 128, P(w_b), P(b_b), 256, P(child), n, m, P(y_b), s), "conv b"))
-        timer.run("neighbor_map_64", lambda: (
-            chk(lib.pxs_voxel_grid_build(P(oc), m, 2, 64, 64, 64, P(grid2), s), "grid2"),
-            chk(lib.pxs_neighbor_map_k3_grid(P(oc), m, 2, 64, 64, 64, P(grid2), P(nbr2), P(mask2),
-                                             s), "map2")))
+        timer.run("neighbor_map_64", lambda: chk(lib.pxs_neighbor_map_k3_grid(
+            P(oc), m, 2, 64, 64, 64, P(grid2), P(nbr2), P(mask2), s), "map2"))
         timer.run("subm_conv_c", lambda: chk(lib.pxs_subm_conv3d(
             1, P(y_b), m, 256, P(w_c), P(b_c), 256, P(nbr2), P(mask2), P(y_c), s), "conv c"))
 
@@ -221,9 +255,10 @@ def unet_stage(args, torch, px, W):
     per_op = {k: {"ms": round(kern[k], 4),
                   "voxel_gmacs": round(macs[k] / (kern[k] * 1e-3) / 1e9, 1),
                   "tflops": round(2 * macs[k] / (kern[k] * 1e-3) / 1e12, 2)} for k in macs}
-    # Map kernels are HBM-bound: the grid fill (4 B per cell), coords in
-    # (16 B/row, read twice) and 27 int32 + a mask out per row.
-    map_bytes = lib.pxs_voxel_grid_bytes(2, 128, 128, 128) + n * (2 * 16 + 27 * 4 + 4)
+    # Map kernels are HBM-bound: coords in (16 B/row, read twice), one 8-byte
+    # tagged cell written per row, 27 int32 + a mask out per row (the 27 cell
+    # reads per row hit cache lines shared with neighbouring rows).
+    map_bytes = n * (2 * 16 + 8 + 27 * 4 + 4)
     per_op["neighbor_map_128"] = {"ms": round(kern["neighbor_map_128"], 4),
                               "gbs": round(map_bytes / (kern["neighbor_map_128"] * 1e-3) / 1e9, 1)}
     per_op["downsample_s2"] = {"ms": round(kern["downsample_s2"], 4)}
@@ -235,8 +270,9 @@ def unet_stage(args, torch, px, W):
         "ms_per_step": round(ms, 4),
         "dtype": "bf16",
         "config": {"workload": "unet_stage_128: batch 2 on 128^3 (61,056 + 101,207 voxels, "
-                               "3 ellipsoid shells each); voxel grid + neighbour map, SubMConv3d 128->128, "
-                               "s2 SparseConv3d 128->256, grid + map at 64^3, SubMConv3d 256->256",
+                               "3 ellipsoid shells each); tagged voxel grid + neighbour map, "
+                               "SubMConv3d 128->128, s2 topology (+ 64^3 grid), SparseConv3d "
+                               "128->256, map at 64^3, SubMConv3d 256->256",
                    "voxels": n, "voxels_64": m, "pairs_a": pa, "pairs_c": pc,
                    "warmup_steps_run": warm,
                    "per_op_note": "per-op times from a pass of args.steps steps with every op "
@@ -295,7 +331,59 @@ def attention_metric(args, torch, px, W):
 
 
 def cpu_baseline_conv():
-    """Reference sparse_submanifold_conv3d (oracle/_ref) on item 0, fp32."""
+    """The U-Net stage on the host cores: SubMConv3d A (128 -> 128 at 128^3) and
+    C (256 -> 256 at 64^3) by the reference's sparse_submanifold_conv3d compiled
+    from its sources (oracle/_ref, OpenMP), the stride-2 conv B (which the
+    reference does not have) by the oracle's restatement; the same inputs as the
+    device stage, fp32."""
+    import numpy as np
+
+    import oracle as O
+    import workloads as W
+
+    if not O.REF_LIB.exists():
+        return None
+    ref, orc = O.Reference(), O.Oracle()
+    threads, limits = cpu_threads()
+    ref.set_threads(threads)
+    wl = W.unet_stage_128()
+    coords, feats = wl["coords"], wl["feats"]
+    n = coords.shape[0]
+    oc, child = orc.downsample_coords_s2(coords)
+    m = oc.shape[0]
+    pa = int((orc.neighbor_map(coords) != n).sum())
+    pc = int((orc.neighbor_map(oc) != m).sum())
+    t_a = ref.sparse(coords, feats, 2, (128, 128, 128))
+    x_c = W.normal(95, m * 256, 1).reshape(m, 256)
+    t_c = ref.sparse(oc, x_c, 2, (64, 64, 64))
+
+    def stage():
+        ref.subm_conv3d(t_a, wl["w_a"], wl["b_a"])
+        orc.sparse_conv3d_s2(child, feats, wl["w_b"], wl["b_b"])
+        ref.subm_conv3d(t_c, wl["w_c"], wl["b_c"])
+
+    med, best = cpu_timing(stage)
+    macs = pa * 128 * 128 + n * 128 * 256 + pc * 256 * 256
+    return {"value": round(macs / med / 1e9, 3), "unit": "voxel-GMAC/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"the whole stage on the host, fp32: SubMConv3d A ({n} voxels, {pa} pairs) "
+                      f"and C ({m} voxels, {pc} pairs) by the reference sparse_submanifold_conv3d "
+                      f"(compiled from its sources, OpenMP, {threads} threads; CPU limits "
+                      f"{limits}), the stride-2 conv B by the oracle (no reference exists); "
+                      f"warmup 2, iterations 3: median {med:.3f} s, min {best:.3f} s per stage",
+            "median_s": round(med, 4), "min_s": round(best, 4)}
+
+
+ATTN_CPU_ROWS = 32  # sampled query rows per segment
+
+
+def cpu_baseline_attention():
+    """The reference's sparse_scaled_dot_product_attention (single-threaded,
+    src/sparse.cpp:704-783, compiled from its sources into oracle/_ref) on the
+    12,288 + 20,480-token workload: ATTN_CPU_ROWS evenly spaced query rows per
+    segment against every key of it, all 16 heads; the full-call time is
+    extrapolated linearly in the queries (each row costs its segment's key
+    count)."""
     import numpy as np
 
     import oracle as O
@@ -304,30 +392,29 @@ def cpu_baseline_conv():
     if not O.REF_LIB.exists():
         return None
     ref = O.Reference()
-    threads = cpu_threads()
-    ref.set_threads(threads)
-    wl = W.unet_stage_128()
-    item0 = wl["coords"][:, 0] == 0
-    coords = wl["coords"][item0]
-    feats = wl["feats"][item0]
-    t = ref.sparse(coords, feats, 1, (128, 128, 128))
-    orc = O.Oracle()
-    idx = orc.neighbor_map(coords)
-    pairs = int((idx != coords.shape[0]).sum())
-    ref.subm_conv3d(t, wl["w_a"], wl["b_a"])  # warm
-    # A bounded sample: whole calls until at least 10 s of CPU work.
-    t0 = time.perf_counter()
-    reps = 0
-    while time.perf_counter() - t0 < 10.0 or reps < 2:
-        ref.subm_conv3d(t, wl["w_a"], wl["b_a"])
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    return {"value": round(pairs * 128 * 128 / dt / 1e9, 3), "unit": "voxel-GMAC/s",
-            "cores": threads, "kind": "reference",
-            "sample": f"reference sparse_submanifold_conv3d fp32 (compiled from the reference "
-                      f"sources, OpenMP), SubMConv3d 128->128 on batch item 0 ({coords.shape[0]} "
-                      f"voxels, {pairs} pairs) of the same workload, mean of {reps} calls "
-                      f"({dt:.2f} s each, {dt * reps:.1f} s total)"}
+    lens, heads, hd = (12288, 20480), 16, 64
+    n, c = sum(lens), heads * hd
+    coords = W.attn_full()["coords"]
+    q = W.normal(71, n * c, 1).reshape(n, c)
+    k = W.normal(71, n * c, 2).reshape(n, c)
+    v = W.normal(71, n * c, 3).reshape(n, c)
+    starts = np.cumsum((0,) + lens[:-1])
+    rows = np.concatenate([s + np.linspace(0, L - 1, ATTN_CPU_ROWS).astype(np.int64)
+                           for s, L in zip(starts, lens)])
+    tq = ref.sparse(coords[rows], q[rows], 2, (32, 32, 32))
+    tk, tv = ref.sparse(coords, k, 2, (32, 32, 32)), ref.sparse(coords, v, 2, (32, 32, 32))
+    med, best = cpu_timing(lambda: ref.sdpa(tq, tk, tv, heads, hd, 0.125))
+    scale = sum(L * L for L in lens) / (ATTN_CPU_ROWS * sum(lens))
+    flops = 4.0 * sum(L * L for L in lens) * hd * heads
+    full = med * scale
+    return {"value": round(flops / full / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+            "kind": "reference",
+            "sample": f"extrapolated: reference sparse_scaled_dot_product_attention (compiled "
+                      f"from its sources; single-threaded, as the reference is) on "
+                      f"{ATTN_CPU_ROWS} query rows per segment against all keys, 16 heads x 64; "
+                      f"warmup 2, iterations 3: median {med:.3f} s, min {best:.3f} s per sample; "
+                      f"the full call ({n} queries) extrapolated x{scale:.1f} to {full:.1f} s",
+            "median_s": round(med, 4), "min_s": round(best, 4), "extrapolated_s": round(full, 2)}
 
 
 # ---------------------------------------------------------------------------
@@ -756,9 +843,62 @@ def decoder(args, torch, px, W):
                          "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None}}
 
 
+def hash_map_128(args, torch, px, W):
+    """The hash path of the neighbour map on the U-Net stage's coordinates
+    (162,263 voxels at 128^3, batch 2): open-addressing voxel hash build
+    (pxs_voxel_hash_build: table init + insert) and the 3x3x3 map over it
+    (pxs_neighbor_map_k3: mask fill + lookups), the path for coordinates
+    without known extents.  Also one 256 MiB device copy, the plain-copy
+    reference for the FETCH_SIZE / WRITE_SIZE counters."""
+    dev = torch.device("cuda:0")
+    coords = torch.from_numpy(W.unet_stage_128()["coords"]).to(dev)
+    n = coords.shape[0]
+    table = torch.empty(px.lib.pxs_voxel_hash_bytes(n), dtype=torch.uint8, device=dev)
+    nbr = torch.empty((27, n), dtype=torch.int32, device=dev)
+    masks = torch.empty(n, dtype=torch.int32, device=dev)
+    timer = Timer(torch)
+    src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)  # the calibration copy (copyBuffer, 2^28 bytes each way)
+
+    import ctypes as C
+
+    lib = px.lib
+
+    def step():
+        s = px.stream()
+        timer.run("hash_build", lambda: px._check(lib.pxs_voxel_hash_build(
+            C.c_void_p(coords.data_ptr()), n, C.c_void_p(table.data_ptr()), s),
+            "pxs_voxel_hash_build"))
+        timer.run("neighbor_map", lambda: px._check(lib.pxs_neighbor_map_k3(
+            C.c_void_p(coords.data_ptr()), n, C.c_void_p(table.data_ptr()),
+            C.c_void_p(nbr.data_ptr()), C.c_void_p(masks.data_ptr()), s), "pxs_neighbor_map_k3"))
+
+    dt = timed_steps(args, torch, step, timer)
+    hb, nm = timer.mean_ms("hash_build"), timer.mean_ms("neighbor_map")
+    slots = px.lib.pxs_voxel_hash_bytes(n)
+    # algorithmic bytes: build = slot init (table bytes) + coords 16 B/row + one
+    # 16-byte slot written per row; map = coords 16 B/row, 27 slot probes of
+    # 16 B (at least one each), 27 int32 out + a mask per row
+    b_build = slots + n * (16 + 16)
+    b_map = n * (16 + 27 * 16 + 27 * 4 + 4)
+    return {"metric": "voxel hash + neighbour map GB/s (algorithmic bytes)",
+            "value": round((b_build + b_map) / dt / 1e9, 1), "unit": "GB/s",
+            "ms_per_step": round(dt * 1e3, 4), "dtype": "int32",
+            "config": {"workload": f"hash_map_128: {n} voxels at 128^3 (batch 2), hash build + 3x3x3 map",
+                       "hash_build_ms": round(hb, 4), "neighbor_map_ms": round(nm, 4),
+                       "hash_build_gbs": round(b_build / (hb * 1e-3) / 1e9, 1),
+                       "neighbor_map_gbs": round(b_map / (nm * 1e-3) / 1e9, 1),
+                       "table_bytes": slots},
+            "roofline": {"bound": "hbm", "kernel": "neighbor_map",
+                         "achieved": round(b_map / (nm * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(b_map / (nm * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                         "traffic": None}}
+
+
 OTHER_WORKLOADS = {"conv_fp32_64": conv_fp32_64, "attn_block": attn_block, "swin_64": swin_64,
                    "flow_sample": flow_sample, "decoder": decoder, "pack_load": pack_load,
-                   "flow_step": flow_step}
+                   "flow_step": flow_step, "hash_map_128": hash_map_128}
 
 
 def main():
@@ -789,6 +929,8 @@ def main():
     base.update(result)
     if not args.no_cpu_baseline and args.workload == "unet_stage_128":
         base["cpu_baseline"] = cpu_baseline_conv()
+        if "attention" in base:
+            base["attention"]["cpu_baseline"] = cpu_baseline_attention()
     print(json.dumps(base), flush=True)
 
 

@@ -125,6 +125,28 @@ int pxs_neighbor_map_k3_grid(const int32_t * coords, int64_t n, int batch_size, 
                              int sz, const void * grid, int32_t * nbr, uint32_t * masks,
                              void * stream);
 
+/* Generation-tagged voxel grid: one uint64 cell per (b, x, y, z) of the
+ * extents (twice pxs_voxel_grid_bytes), holding ~generation in its high word
+ * and a row in its low word.  It is reset (all ones) once per allocation;
+ * after that every insert takes a generation larger than any earlier one
+ * since the reset, and lookups with that generation see only its rows, so the
+ * grid is never refilled: a build costs O(rows) instead of O(cells).  Within
+ * a generation the smallest row of a coordinate wins, as in
+ * pxs_voxel_grid_build.  Generation 0 is the reset state and is rejected.
+ * A replacement, for hot loops that rebuild maps over fixed extents, of the
+ * per-build std::unordered_map of src/slat_decoder.cpp:630-635. */
+size_t pxs_voxel_grid_tagged_bytes(int batch_size, int sx, int sy, int sz);
+int pxs_voxel_grid_tagged_reset(void * grid, int batch_size, int sx, int sy, int sz,
+                                void * stream);
+int pxs_voxel_grid_tagged_insert(const int32_t * coords, int64_t n, int batch_size, int sx,
+                                 int sy, int sz, void * grid, uint32_t generation, void * stream);
+
+/* pxs_neighbor_map_k3 over a tagged grid built with the same coords and
+ * generation: identical nbr and masks (src/slat_decoder.cpp:609-668). */
+int pxs_neighbor_map_k3_grid_tagged(const int32_t * coords, int64_t n, int batch_size, int sx,
+                                    int sy, int sz, const void * grid, uint32_t generation,
+                                    int32_t * nbr, uint32_t * masks, void * stream);
+
 /* Compacted per-offset pair lists from a dense map: for each k ascending,
  * (input row, output row) pairs with output rows ascending; offsets28
  * (device int64[28]) bounds the lists.  pair_in/pair_out hold up to 27*n. */
@@ -160,6 +182,27 @@ size_t pxs_downsample_workspace_bytes(int64_t n, int batch_size, int sx, int sy,
 int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size, int sx,
                                int sy, int sz, int32_t * out_coords, int32_t * child_map,
                                int64_t * m_out, void * workspace, void * stream);
+
+/* pxs_downsample_s2_topology for a pipeline that keeps a tagged fine grid:
+ * the same out_coords, *m_out and child map (leading dimension ld_map >= n,
+ * all 8 slots of the m outputs written, -1 when absent), with the children
+ * read from fine_grid (coords inserted with fine_generation), and the whole
+ * dense coarse grid written: coarse_grid (pxs_voxel_grid_bytes of the extents
+ * ceil(s/2)) ends holding each output row at its cell and INT_MAX elsewhere,
+ * ready for pxs_neighbor_map_k3_grid over out_coords with no build of its
+ * own.  Three launches: occupancy bits, a blocked scan of their counts, one
+ * thread per coarse cell emitting in lexicographic order.  The workspace
+ * (pxs_downsample_s2_tagged_workspace_bytes) carries the occupancy bitmap,
+ * which must be zero before the first call
+ * (pxs_downsample_s2_tagged_workspace_reset) and which every call leaves zero. */
+size_t pxs_downsample_s2_tagged_workspace_bytes(int batch_size, int sx, int sy, int sz);
+int pxs_downsample_s2_tagged_workspace_reset(void * workspace, int batch_size, int sx, int sy,
+                                             int sz, void * stream);
+int pxs_downsample_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size, int sx,
+                                      int sy, int sz, const void * fine_grid,
+                                      uint32_t fine_generation, int32_t * out_coords,
+                                      int32_t * child_map, int64_t ld_map, int64_t * m_out,
+                                      void * coarse_grid, void * workspace, void * stream);
 
 /* The same topology for any factor f, as groups: output q (coordinates
  * (b, x/f, y/f, z/f), lexicographic) gathers input rows

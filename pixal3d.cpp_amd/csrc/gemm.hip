@@ -359,6 +359,15 @@ constexpr bool kIssueLate = PXS_GEMM_ISSUE_LATE != 0;
 
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
+// Absent gathered rows (a neighbour missing for this output row, or a row
+// past the tile end): with PXS_GEMM_MASK_ABSENT their lanes are left out of
+// the LDS DMA, and the fragment reads replace their stale LDS bytes with
+// zeros in registers, so no bytes travel for them.
+#ifndef PXS_GEMM_MASK_ABSENT
+#define PXS_GEMM_MASK_ABSENT 0
+#endif
+constexpr bool kMaskAbsent = PXS_GEMM_MASK_ABSENT != 0;
+
 __device__ __forceinline__ void wait_vmcnt(int n) {
     // s_waitcnt with expcnt/lgkmcnt at their maxima: only vmcnt is waited on.
     switch (n) {
@@ -519,7 +528,13 @@ gather_gemm_lds_kernel(GemmArgs a) {
             const void * g = (src[j] >= 0 && col < a.cin)
                                  ? static_cast<const void *>(x + static_cast<int64_t>(src[j]) * a.ldx + col)
                                  : zero;
-            lds_dma16(g, lds_offset(base + (wave * AI + j) * 8 * kChunkBytes));
+            if constexpr (kMaskAbsent) {
+                // lane 0 always issues (zero line when its row is absent)
+                const uint64_t lanes = __ballot(src[j] >= 0) | 1ull;
+                lds_dma16_masked(g, lds_offset(base + (wave * AI + j) * 8 * kChunkBytes), lanes);
+            } else {
+                lds_dma16(g, lds_offset(base + (wave * AI + j) * 8 * kChunkBytes));
+            }
         }
         const int64_t kbase = static_cast<int64_t>(k) * a.cout * a.cin + chunk * kChunk;
 #pragma unroll
@@ -551,6 +566,12 @@ gather_gemm_lds_kernel(GemmArgs a) {
         }
         const char * sa = smem + (s % NSTAGE) * kStageBytes;
         const char * sb = sa + BM * kChunkBytes;
+        bool row_ok[TI];
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            row_ok[i] = true;
+            if constexpr (kMaskAbsent) row_ok[i] = idx_lds[(s / chunks) * BM + wm * WM + i * 32 + r] >= 0;
+        }
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
             for (int kk = 0; kk < KSTEPS; ++kk) {
@@ -559,8 +580,12 @@ gather_gemm_lds_kernel(GemmArgs a) {
 #pragma unroll
                 for (int i = 0; i < TI; ++i) {
                     const int row = wm * WM + i * 32 + r;
-                    af[i] = *reinterpret_cast<const bf16x8 *>(sa + row * kChunkBytes +
-                                                              ((piece ^ swz(row)) << 4));
+                    uint4 raw = *reinterpret_cast<const uint4 *>(sa + row * kChunkBytes +
+                                                                 ((piece ^ swz(row)) << 4));
+                    if constexpr (kMaskAbsent) {
+                        if (!row_ok[i]) raw = make_uint4(0, 0, 0, 0);
+                    }
+                    af[i] = __builtin_bit_cast(bf16x8, raw);
                 }
 #pragma unroll
                 for (int j = 0; j < TJ; ++j) {
@@ -583,8 +608,12 @@ gather_gemm_lds_kernel(GemmArgs a) {
 #pragma unroll
                 for (int i = 0; i < TI; ++i) {
                     const int row = wm * WM + i * 32 + r;
-                    af[i] = *reinterpret_cast<const f32x4 *>(sa + row * kChunkBytes +
-                                                             ((piece ^ swz(row)) << 4));
+                    uint4 raw = *reinterpret_cast<const uint4 *>(sa + row * kChunkBytes +
+                                                                 ((piece ^ swz(row)) << 4));
+                    if constexpr (kMaskAbsent) {
+                        if (!row_ok[i]) raw = make_uint4(0, 0, 0, 0);
+                    }
+                    af[i] = __builtin_bit_cast(f32x4, raw);
                 }
 #pragma unroll
                 for (int j = 0; j < TJ; ++j) {

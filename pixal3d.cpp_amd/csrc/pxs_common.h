@@ -99,6 +99,20 @@ __device__ __forceinline__ void lds_dma16(const void * g, uint32_t lds_base) {
                  : "m0");
 }
 
+// lds_dma16 for the lanes set in `lanes` only (EXEC narrowed inside the asm
+// and restored after it); the other lanes leave their 16 LDS bytes as they
+// were.  `lanes` must not be empty: the instruction is then always issued, so
+// the caller's vmcnt bookkeeping holds.
+__device__ __forceinline__ void lds_dma16_masked(const void * g, uint32_t lds_base,
+                                                 uint64_t lanes) {
+    uint64_t saved;
+    asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, exec, %3\n\ts_mov_b32 m0, %2\n\t"
+                 "s_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b64 exec, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(lds_base), "s"(lanes)
+                 : "m0", "scc");
+}
+
 // Workgroup barrier without __syncthreads' release/acquire fences (which wait
 // for every outstanding global load, prefetches included).  It waits for the
 // wave's own LDS accesses (lgkmcnt 0), so no wave refills a stage another is

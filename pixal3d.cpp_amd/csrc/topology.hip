@@ -8,6 +8,7 @@
 #include "pxs_common.h"
 #include "scan.h"
 
+#include <algorithm>
 #include <climits>
 
 namespace pxs {
@@ -257,6 +258,71 @@ neighbor_map_grid_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g
     if (masks) masks[p] = present;
 }
 
+// ---- generation-tagged voxel grid ---------------------------------------------
+// One uint64 cell per (b, x, y, z): the high word holds ~generation, the low
+// word the row.  A cell belongs to the current build only when its high word
+// is ~generation, so the grid is never refilled: a reset (all ones) once per
+// allocation, then every build passes a larger generation and old entries
+// simply stop matching.  Insertion is an atomicMin, so within a generation the
+// smallest row wins (a newer generation has a smaller ~generation and always
+// replaces an older entry).
+__device__ __forceinline__ unsigned long long tag_cell(uint32_t generation, uint32_t row) {
+    return (static_cast<unsigned long long>(~generation) << 32) | row;
+}
+
+__device__ __forceinline__ int32_t tag_lookup(unsigned long long cell, uint32_t generation) {
+    return static_cast<uint32_t>(cell >> 32) == ~generation ? static_cast<int32_t>(cell)
+                                                            : kGridEmpty;
+}
+
+__global__ void tagged_scatter_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
+                                      unsigned long long * __restrict__ grid,
+                                      uint32_t generation) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    if (grid_inside(g, c.x, c.y, c.z, c.w)) {
+        atomicMin(grid + grid_cell(g, c.x, c.y, c.z, c.w),
+                  tag_cell(generation, static_cast<uint32_t>(p)));
+    }
+}
+
+// neighbor_map_grid_kernel over a tagged grid: the same map and masks.
+__global__ void __launch_bounds__(kThreads)
+neighbor_map_tagged_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
+                           const unsigned long long * __restrict__ grid, uint32_t generation,
+                           int32_t * __restrict__ nbr, uint32_t * __restrict__ masks) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    int32_t row[27];
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const int x = c.y + k / 9 - 1, y = c.z + (k / 3) % 3 - 1, z = c.w + k % 3 - 1;
+        row[k] = grid_inside(g, c.x, x, y, z)
+                     ? tag_lookup(grid[grid_cell(g, c.x, x, y, z)], generation)
+                     : kGridEmpty;
+    }
+    row[13] = static_cast<int32_t>(p);
+    uint32_t present = 0;
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const bool hit = row[k] != kGridEmpty;
+        if (hit) present |= 1u << k;
+        nbr[static_cast<int64_t>(k) * n + p] = hit ? row[k] : static_cast<int32_t>(n);
+    }
+    if (masks) masks[p] = present;
+}
+
+template <typename T>
+__global__ void fill_value_kernel(T * p, int64_t count, T value) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride) {
+        p[i] = value;
+    }
+}
+
 // Pair lists: counts per (offset, block of kThreads rows).
 __global__ void __launch_bounds__(kThreads)
 pair_count_kernel(const int32_t * __restrict__ nbr, int64_t n, int32_t * __restrict__ counts,
@@ -324,18 +390,21 @@ __device__ __forceinline__ int64_t coarse_cell(int4 c, int f, int cx, int cy, in
 // It also sets clear[k * n + p] = value for k < clear_rows (the child map or
 // the group counts the next kernels fill in), saving a fill launch.
 __global__ void coarse_mark_kernel(const int4 * __restrict__ coords, int64_t n, int f, int cx,
-                                   int cy, int cz, uint32_t * __restrict__ bitmap,
+                                   int cy, int cz, int64_t words, uint32_t * __restrict__ bitmap,
                                    int32_t * __restrict__ clear, int clear_rows, int32_t value) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const bool live = p < n;
+    bool live = p < n;
     if (live) {
         for (int k = 0; k < clear_rows; ++k) clear[k * n + p] = value;
     }
     int64_t word = -1;
     uint32_t bit = 0;
     if (live) {
-        const int64_t cell = coarse_cell(coords[p], f, cx, cy, cz);
-        word = cell >> 5;
+        const int4 c = coords[p];
+        const int64_t cell = coarse_cell(c, f, cx, cy, cz);
+        // a row outside the extents (invalid input) marks nothing
+        live = c.x >= 0 && c.y >= 0 && c.z >= 0 && c.w >= 0 && cell >= 0 && (cell >> 5) < words;
+        word = live ? cell >> 5 : -1;
         bit = 1u << (cell & 31);
     }
     uint64_t pending = __ballot(live);
@@ -371,6 +440,109 @@ __global__ void coarse_emit_kernel(const int4 * __restrict__ coords, int64_t n, 
     child_map[static_cast<int64_t>(child) * n + rank] = static_cast<int32_t>(p);
     // Every child of the cell writes the same coarse coordinate.
     out_coords[rank] = make_int4(c.x, c.y >> 1, c.z >> 1, c.w >> 1);
+}
+
+// ---- stride-2 topology from the fine tagged grid ---------------------------------
+// Bitmap words are scanned in blocks of kWordBlock: block-local exclusive
+// prefixes plus one total per block, which the emit adds up (at most a few
+// dozen totals per block of words).
+constexpr int kWordBlock = 1024;
+
+__global__ void __launch_bounds__(kThreads)
+word_block_scan_kernel(const uint32_t * __restrict__ bitmap, int64_t words,
+                       int32_t * __restrict__ local_prefix, int32_t * __restrict__ block_totals) {
+    constexpr int kPer = kWordBlock / kThreads;  // 4 words per thread
+    __shared__ int32_t wave_sums[kThreads / 64];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kWordBlock;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    int32_t cnt[kPer];
+    int32_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int64_t w = base + t * kPer + j;
+        cnt[j] = w < words ? __popc(bitmap[w]) : 0;
+        mine += cnt[j];
+    }
+    int32_t inc = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int32_t o = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) wave_sums[wave] = inc;
+    __syncthreads();
+    int32_t before = inc - mine;
+    for (int w = 0; w < wave; ++w) before += wave_sums[w];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int64_t w = base + t * kPer + j;
+        if (w < words) local_prefix[w] = before;
+        before += cnt[j];
+    }
+    if (t == kThreads - 1) block_totals[blockIdx.x] = before;
+}
+
+// One thread per coarse cell (32 per bitmap word).  Every cell writes its
+// entry of the dense coarse grid (its rank, or kGridEmpty), so that grid needs
+// no fill and is freshly cached for the coarse neighbour map that follows.  An
+// occupied cell also writes its rank's coordinate and its 8 children looked
+// up in the fine tagged grid (child c = (x&1) + 2(y&1) + 4(z&1), -1 when
+// absent).  Lane 0 of each word's 32 clears the word once the wavefront has
+// read it, so the bitmap is zero again for the next call.
+__global__ void __launch_bounds__(kThreads)
+coarse_emit_grid_kernel(uint32_t * __restrict__ bitmap, int64_t words, int64_t cells,
+                        const int32_t * __restrict__ local_prefix,
+                        const int32_t * __restrict__ block_totals, int nblocks, GridDims fine,
+                        GridDims coarse, const unsigned long long * __restrict__ fine_grid,
+                        uint32_t fine_gen, int32_t * __restrict__ coarse_grid,
+                        int4 * __restrict__ out_coords, int32_t * __restrict__ child_map,
+                        int64_t ld_map, int64_t * m_out) {
+    __shared__ int64_t partial[kThreads];
+    const int64_t cell = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t w = cell >> 5;
+    // The workgroup's 8 words lie in one scan block (kWordBlock words, a
+    // multiple of 8); its base is the sum of the earlier blocks' totals
+    // (workgroup 0 sums all of them, for m_out).
+    const int64_t first_word = static_cast<int64_t>(blockIdx.x) * (kThreads / 32);
+    const int64_t sb = blockIdx.x == 0 ? nblocks : first_word / kWordBlock;
+    int64_t acc = 0;
+    for (int64_t b = threadIdx.x; b < sb; b += kThreads) acc += block_totals[b];
+    partial[threadIdx.x] = acc;
+    __syncthreads();
+    for (int span = kThreads / 2; span >= 1; span >>= 1) {
+        if (static_cast<int>(threadIdx.x) < span) partial[threadIdx.x] += partial[threadIdx.x + span];
+        __syncthreads();
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) *m_out = partial[0];
+    const int64_t block_base = blockIdx.x == 0 ? 0 : partial[0];
+    if (w >= words) return;
+    const uint32_t bits = bitmap[w];
+    const int bit = static_cast<int>(cell & 31);
+    // every lane of the word has read it (wavefront-wide loads precede this)
+    __builtin_amdgcn_wave_barrier();
+    if (bit == 0 && bits) bitmap[w] = 0u;
+    const bool occupied = (bits >> bit) & 1u;
+    const int64_t rank = block_base + local_prefix[w] + __popc(bits & ((1u << bit) - 1u));
+    if (cell < cells) coarse_grid[cell] = occupied ? static_cast<int32_t>(rank) : kGridEmpty;
+    if (!occupied) return;
+    const int64_t per_item = static_cast<int64_t>(coarse.x) * coarse.y * coarse.z;
+    const int b = static_cast<int>(cell / per_item);
+    int64_t rem = cell - static_cast<int64_t>(b) * per_item;
+    const int X = static_cast<int>(rem / (static_cast<int64_t>(coarse.y) * coarse.z));
+    rem -= static_cast<int64_t>(X) * coarse.y * coarse.z;
+    const int Y = static_cast<int>(rem / coarse.z);
+    const int Z = static_cast<int>(rem - static_cast<int64_t>(Y) * coarse.z);
+    out_coords[rank] = make_int4(b, X, Y, Z);
+    int32_t child[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int x = 2 * X + (c & 1), y = 2 * Y + ((c >> 1) & 1), z = 2 * Z + (c >> 2);
+        child[c] = grid_inside(fine, b, x, y, z)
+                       ? tag_lookup(fine_grid[grid_cell(fine, b, x, y, z)], fine_gen)
+                       : kGridEmpty;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) child_map[c * ld_map + rank] = child[c] == kGridEmpty ? -1 : child[c];
 }
 
 // Any factor: group rows by output cell.  Pass 1 ranks each row's cell and
@@ -706,6 +878,57 @@ int pxs_neighbor_map_k3_grid(const int32_t * coords, int64_t n, int batch_size, 
     return check_launch("pxs_neighbor_map_k3_grid");
 }
 
+size_t pxs_voxel_grid_tagged_bytes(int batch_size, int sx, int sy, int sz) {
+    return 2 * pxs_voxel_grid_bytes(batch_size, sx, sy, sz);
+}
+
+int pxs_voxel_grid_tagged_reset(void * grid, int batch_size, int sx, int sy, int sz,
+                                void * stream) {
+    const size_t bytes = pxs_voxel_grid_tagged_bytes(batch_size, sx, sy, sz);
+    PXS_CHECK(bytes > 0, PXS_ERR_ARG, "pxs_voxel_grid_tagged_reset: invalid extents");
+    PXS_CHECK(grid, PXS_ERR_ARG, "pxs_voxel_grid_tagged_reset: null pointer");
+    const int64_t cells = static_cast<int64_t>(bytes / 8);
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((cells + kThreads - 1) / kThreads, 16384));
+    hipLaunchKernelGGL(fill_value_kernel<unsigned long long>, dim3(blocks), dim3(kThreads), 0,
+                       as_stream(stream), static_cast<unsigned long long *>(grid), cells,
+                       ~0ull);
+    return check_launch("pxs_voxel_grid_tagged_reset");
+}
+
+int pxs_voxel_grid_tagged_insert(const int32_t * coords, int64_t n, int batch_size, int sx,
+                                 int sy, int sz, void * grid, uint32_t generation, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_voxel_grid_tagged_insert: bad row count");
+    PXS_CHECK(pxs_voxel_grid_tagged_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              "pxs_voxel_grid_tagged_insert: invalid extents");
+    PXS_CHECK(generation != 0, PXS_ERR_ARG,
+              "pxs_voxel_grid_tagged_insert: generation 0 is the reset state");
+    if (n == 0) return PXS_OK;
+    PXS_CHECK(grid && coords, PXS_ERR_ARG, "pxs_voxel_grid_tagged_insert: null pointer");
+    hipLaunchKernelGGL(tagged_scatter_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+                       as_stream(stream), reinterpret_cast<const int4 *>(coords), n,
+                       GridDims{batch_size, sx, sy, sz},
+                       static_cast<unsigned long long *>(grid), generation);
+    return check_launch("pxs_voxel_grid_tagged_insert");
+}
+
+int pxs_neighbor_map_k3_grid_tagged(const int32_t * coords, int64_t n, int batch_size, int sx,
+                                    int sy, int sz, const void * grid, uint32_t generation,
+                                    int32_t * nbr, uint32_t * masks, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG,
+              "pxs_neighbor_map_k3_grid_tagged: bad row count");
+    PXS_CHECK(pxs_voxel_grid_tagged_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              "pxs_neighbor_map_k3_grid_tagged: invalid extents");
+    PXS_CHECK(generation != 0, PXS_ERR_ARG,
+              "pxs_neighbor_map_k3_grid_tagged: generation 0 is the reset state");
+    if (n == 0) return PXS_OK;
+    PXS_CHECK(coords && grid && nbr, PXS_ERR_ARG, "pxs_neighbor_map_k3_grid_tagged: null pointer");
+    hipLaunchKernelGGL(neighbor_map_tagged_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+                       as_stream(stream), reinterpret_cast<const int4 *>(coords), n,
+                       GridDims{batch_size, sx, sy, sz},
+                       static_cast<const unsigned long long *>(grid), generation, nbr, masks);
+    return check_launch("pxs_neighbor_map_k3_grid_tagged");
+}
+
 size_t pxs_neighbor_pairs_workspace_bytes(int64_t n) {
     const int64_t blocks = std::max<int64_t>((n + kThreads - 1) / kThreads, 1);
     const int64_t count = 27 * blocks;
@@ -792,14 +1015,77 @@ int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size
     int rc = fill_u32(g.bitmap, g.words, 0u, s);
     if (rc) return rc;
     hipLaunchKernelGGL(coarse_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
-                       reinterpret_cast<const int4 *>(coords), n, 2, g.cx, g.cy, g.cz, g.bitmap,
-                       child_map, 8, -1);
+                       reinterpret_cast<const int4 *>(coords), n, 2, g.cx, g.cy, g.cz, g.words,
+                       g.bitmap, child_map, 8, -1);
     rc = exclusive_scan_popcount(g.bitmap, g.prefix, g.words, m_out, g.rest, s);
     if (rc) return rc;
     hipLaunchKernelGGL(coarse_emit_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
                        reinterpret_cast<const int4 *>(coords), n, g.cx, g.cy, g.cz, g.bitmap,
                        g.prefix, reinterpret_cast<int4 *>(out_coords), child_map);
     return check_launch("pxs_downsample_s2_topology");
+}
+
+size_t pxs_downsample_s2_tagged_workspace_bytes(int batch_size, int sx, int sy, int sz) {
+    if (batch_size <= 0 || sx <= 0 || sy <= 0 || sz <= 0) return 0;
+    const int64_t cells = static_cast<int64_t>(batch_size) * ((sx + 1) / 2) * ((sy + 1) / 2) *
+                          ((sz + 1) / 2);
+    const int64_t words = (cells + 31) / 32;
+    const int64_t blocks = (words + kWordBlock - 1) / kWordBlock;
+    auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
+    return static_cast<size_t>(up(words * 4) + up(words * 4) + up(blocks * 4));
+}
+
+int pxs_downsample_s2_tagged_workspace_reset(void * workspace, int batch_size, int sx, int sy,
+                                             int sz, void * stream) {
+    const size_t bytes = pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz);
+    PXS_CHECK(bytes > 0, PXS_ERR_ARG, "pxs_downsample_s2_tagged_workspace_reset: invalid shape");
+    PXS_CHECK_WORKSPACE(workspace, "pxs_downsample_s2_tagged_workspace_reset");
+    PXS_CHECK(workspace, PXS_ERR_ARG, "pxs_downsample_s2_tagged_workspace_reset: null pointer");
+    return fill_u32(static_cast<uint32_t *>(workspace), static_cast<int64_t>(bytes / 4), 0u,
+                    as_stream(stream));
+}
+
+int pxs_downsample_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size, int sx,
+                                      int sy, int sz, const void * fine_grid,
+                                      uint32_t fine_generation, int32_t * out_coords,
+                                      int32_t * child_map, int64_t ld_map, int64_t * m_out,
+                                      void * coarse_grid, void * workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_downsample_s2_topology_tagged");
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology_tagged: bad row count");
+    PXS_CHECK(pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology_tagged: invalid shape");
+    PXS_CHECK(fine_generation != 0, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology_tagged: generation 0 is the reset state");
+    PXS_CHECK(ld_map >= n, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology_tagged: child map stride below the row count");
+    PXS_CHECK(m_out && workspace, PXS_ERR_ARG, "pxs_downsample_s2_topology_tagged: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) return fill_i64(m_out, 1, 0, s);
+    PXS_CHECK(coords && fine_grid && out_coords && child_map && coarse_grid, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology_tagged: null pointer");
+    const int cx = (sx + 1) / 2, cy = (sy + 1) / 2, cz = (sz + 1) / 2;
+    const int64_t cells = static_cast<int64_t>(batch_size) * cx * cy * cz;
+    const int64_t words = (cells + 31) / 32;
+    const int64_t blocks = (words + kWordBlock - 1) / kWordBlock;
+    char * ws = static_cast<char *>(workspace);
+    auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
+    uint32_t * bitmap = reinterpret_cast<uint32_t *>(ws);
+    int32_t * local_prefix = reinterpret_cast<int32_t *>(ws + up(words * 4));
+    int32_t * totals = reinterpret_cast<int32_t *>(ws + 2 * up(words * 4));
+    PXS_CHECK(blocks <= INT_MAX, PXS_ERR_ARG, "pxs_downsample_s2_topology_tagged: grid too large");
+    hipLaunchKernelGGL(coarse_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const int4 *>(coords), n, 2, cx, cy, cz, words, bitmap,
+                       nullptr, 0, 0);
+    hipLaunchKernelGGL(word_block_scan_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
+                       0, s, bitmap, words, local_prefix, totals);
+    hipLaunchKernelGGL(coarse_emit_grid_kernel, dim3(grid_for(words * 32, kThreads)), dim3(kThreads), 0,
+                       s, bitmap, words, cells, local_prefix, totals, static_cast<int>(blocks),
+                       GridDims{batch_size, sx, sy, sz}, GridDims{batch_size, cx, cy, cz},
+                       static_cast<const unsigned long long *>(fine_grid), fine_generation,
+                       static_cast<int32_t *>(coarse_grid), reinterpret_cast<int4 *>(out_coords),
+                       child_map, ld_map, m_out);
+    return check_launch("pxs_downsample_s2_topology_tagged");
 }
 
 int pxs_downsample_topology(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
@@ -830,7 +1116,7 @@ int pxs_downsample_topology(const int32_t * coords, int64_t n, int batch_size, i
     int rc = fill_u32(g.bitmap, g.words, 0u, s);
     if (rc) return rc;
     hipLaunchKernelGGL(coarse_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
-                       n, factor, g.cx, g.cy, g.cz, g.bitmap, counts, 1, 0);
+                       n, factor, g.cx, g.cy, g.cz, g.words, g.bitmap, counts, 1, 0);
     rc = exclusive_scan_popcount(g.bitmap, g.prefix, g.words, m_out, scan_ws, s);
     if (rc) return rc;
     hipLaunchKernelGGL(group_assign_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,

@@ -101,6 +101,16 @@ _SIGS = {
     "pxs_window_partition": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                     _vp, _vp]),
     "pxs_voxel_grid_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32]),
+    "pxs_voxel_grid_tagged_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32]),
+    "pxs_voxel_grid_tagged_reset": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
+    "pxs_voxel_grid_tagged_insert": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, C.c_uint32,
+                                            _vp]),
+    "pxs_neighbor_map_k3_grid_tagged": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, C.c_uint32,
+                                               _vp, _vp, _vp]),
+    "pxs_downsample_s2_tagged_workspace_bytes": (C.c_size_t, [_i32, _i32, _i32, _i32]),
+    "pxs_downsample_s2_tagged_workspace_reset": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
+    "pxs_downsample_s2_topology_tagged": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp,
+                                                 C.c_uint32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "pxs_voxel_grid_build": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
     "pxs_neighbor_map_k3_grid": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "pxs_convnext_block_workspace_bytes": (C.c_size_t, [_i32, _i64, _i32, _i32, _i32]),
@@ -320,6 +330,60 @@ class Pxs:
                                                   *shape, _ptr(grid), self.stream()),
                     "pxs_voxel_grid_build")
         return grid
+
+    # -- generation-tagged grids ---------------------------------------------------
+    def tagged_grid(self, batch_size, shape, device="cuda"):
+        """A reset tagged voxel grid for these extents."""
+        nbytes = self.lib.pxs_voxel_grid_tagged_bytes(batch_size, *shape)
+        grid = torch.empty(max(nbytes // 8, 1), dtype=torch.int64, device=device)
+        self._check(self.lib.pxs_voxel_grid_tagged_reset(_ptr(grid), batch_size, *shape,
+                                                         self.stream()),
+                    "pxs_voxel_grid_tagged_reset")
+        return grid
+
+    def tagged_insert(self, coords, batch_size, shape, grid, generation):
+        self._check(self.lib.pxs_voxel_grid_tagged_insert(_ptr(coords), coords.shape[0],
+                                                          batch_size, *shape, _ptr(grid),
+                                                          generation, self.stream()),
+                    "pxs_voxel_grid_tagged_insert")
+
+    def neighbor_map_tagged(self, coords, batch_size, shape, grid, generation):
+        n = coords.shape[0]
+        nbr = torch.empty((27, max(n, 1)), dtype=torch.int32, device=coords.device)
+        masks = torch.empty(max(n, 1), dtype=torch.int32, device=coords.device)
+        self._check(self.lib.pxs_neighbor_map_k3_grid_tagged(_ptr(coords), n, batch_size, *shape,
+                                                             _ptr(grid), generation, _ptr(nbr),
+                                                             _ptr(masks), self.stream()),
+                    "pxs_neighbor_map_k3_grid_tagged")
+        return nbr[:, :n], masks[:n]
+
+    def s2_tagged_workspace(self, batch_size, shape, device="cuda"):
+        """A workspace for pxs_downsample_s2_topology_tagged with its bitmap zeroed."""
+        nbytes = self.lib.pxs_downsample_s2_tagged_workspace_bytes(batch_size, *shape)
+        ws = self._ws(nbytes, device)
+        self._check(self.lib.pxs_downsample_s2_tagged_workspace_reset(_ptr(ws), batch_size, *shape,
+                                                                      self.stream()),
+                    "pxs_downsample_s2_tagged_workspace_reset")
+        return ws
+
+    def downsample_s2_tagged(self, coords, batch_size, shape, fine_grid, fine_gen, coarse_grid,
+                             workspace, sync=True):
+        """-> (out_coords, child_map [8, n], m); m is the host count when sync
+        (else the device int64).  coarse_grid (a plain voxel grid of the
+        halved extents) is rewritten whole."""
+        n = coords.shape[0]
+        dev = coords.device
+        oc = torch.empty((max(n, 1), 4), dtype=torch.int32, device=dev)
+        child = torch.empty((8, max(n, 1)), dtype=torch.int32, device=dev)
+        m = torch.empty(1, dtype=torch.int64, device=dev)
+        self._check(self.lib.pxs_downsample_s2_topology_tagged(
+            _ptr(coords), n, batch_size, *shape, _ptr(fine_grid), fine_gen, _ptr(oc), _ptr(child),
+            child.shape[1], _ptr(m), _ptr(coarse_grid), _ptr(workspace),
+            self.stream()), "pxs_downsample_s2_topology_tagged")
+        if not sync:
+            return oc, child, m
+        mm = int(m.item())
+        return oc[:mm], child, mm
 
     def neighbor_map_grid(self, coords, batch_size, shape, grid=None, want_masks=True):
         """pxs_voxel_grid_build + pxs_neighbor_map_k3_grid -> (nbr [27, n], masks [n])."""

@@ -267,3 +267,59 @@ def test_extents_beyond_the_key_are_rejected(px, dims):
     coords = ti32(np.array([[0, 1, 1, 1]], np.int32))
     with pytest.raises(pxs.PxsError, match="extent exceeds PXS_MAX_EXTENT"):
         px.validate(coords, dims[0], dims[1:])
+
+
+# --- generation-tagged grids ---------------------------------------------------------
+
+def test_tagged_grid_map_across_generations(px, orc):
+    """One tagged grid, four builds with increasing generations over different
+    coordinate sets (each a superset, a subset or a disjoint set of the last):
+    each map equals the oracle's, so stale cells of earlier generations never
+    leak into a later map."""
+    shape, batch = (24, 24, 24), 2
+    sets = [W.shell_coords(24, [[(6.0, 10.0)], [(5.0, 9.0)]], 51),
+            W.shell_coords(24, [[(4.0, 11.0)], [(3.0, 10.0)]], 52),
+            W.shell_coords(24, [[(8.0, 9.0)], [(2.0, 3.0)]], 53),
+            W.shell_coords(24, [[(6.0, 10.0)], [(5.0, 9.0)]], 51)]
+    grid = px.tagged_grid(batch, shape)
+    for gen, coords in enumerate(sets, start=1):
+        print(f"[tagged map] generation={gen} n={coords.shape[0]}", flush=True)
+        c = ti32(coords)
+        px.tagged_insert(c, batch, shape, grid, gen)
+        nbr, masks = px.neighbor_map_tagged(c, batch, shape, grid, gen)
+        ref = orc.neighbor_map(coords)
+        np.testing.assert_array_equal(nbr.cpu().numpy(), ref)
+        ref_masks = ((ref != coords.shape[0]).astype(np.int64) << np.arange(27)[:, None]).sum(0)
+        np.testing.assert_array_equal(masks.cpu().numpy().astype(np.int64) & 0x7FFFFFF, ref_masks)
+
+
+@pytest.mark.parametrize("case", ["unet_stage_128", "small_2batch", "single", "odd"])
+def test_downsample_s2_tagged_bit_exact(px, orc, case):
+    """The tagged stride-2 topology equals the oracle's (coordinates, count,
+    all 8 child slots), the coarse grid it writes gives the oracle's map over
+    the output coordinates, and later calls on the same workspace and grids
+    with other coordinates are exact too (the occupancy bitmap is left zero,
+    stale fine-grid entries do not match, the coarse grid is rewritten whole)."""
+    if case == "odd":
+        coords, batch, shape = (W.shell_coords(23, [[(5.0, 9.0)], [(4.0, 8.0)]], 54), 2,
+                                (23, 23, 23))
+    else:
+        coords, batch, shape = coord_cases()[case]
+    cshape = tuple((s + 1) // 2 for s in shape)
+    fine = px.tagged_grid(batch, shape)
+    coarse = torch.full((px.lib.pxs_voxel_grid_bytes(batch, *cshape) // 4,), 12345,
+                        dtype=torch.int32, device=dev())  # garbage: every cell is written
+    ws = px.s2_tagged_workspace(batch, shape)
+    other = coords[::2].copy()
+    for gen, cc in ((1, coords), (2, other), (3, coords)):
+        print(f"[s2 tagged] case={case} generation={gen} n={cc.shape[0]}", flush=True)
+        c = ti32(cc)
+        px.tagged_insert(c, batch, shape, fine, gen)
+        oc, child, m = px.downsample_s2_tagged(c, batch, shape, fine, gen, coarse, ws)
+        roc, rchild = orc.downsample_coords_s2(cc)
+        assert m == roc.shape[0]
+        np.testing.assert_array_equal(oc.cpu().numpy(), roc)
+        np.testing.assert_array_equal(child.cpu().numpy()[:, :m], rchild.T)
+        nbr, _ = px.neighbor_map_grid(oc.contiguous(), batch, cshape, grid=coarse)
+        np.testing.assert_array_equal(nbr.cpu().numpy(), orc.neighbor_map(roc))
+    assert not ws[:px.lib.pxs_downsample_s2_tagged_workspace_bytes(batch, *shape) // 3].any()
