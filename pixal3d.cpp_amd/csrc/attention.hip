@@ -365,6 +365,12 @@ __device__ __forceinline__ float lane_pair_sum(float v) {
 // cores and the VALU work at the same time.  K/V tiles stream HBM -> LDS with
 // global_load_lds through a ring of 4 stages (tiles j-1 .. j+2 live).
 constexpr int kAttnStages = 4;
+// Raise the wave's issue priority while it queues a tile's MFMAs, so the
+// SIMD's other wave fills the matrix core's shadow with its VALU softmax.
+#ifndef PXS_ATTN_SETPRIO
+#define PXS_ATTN_SETPRIO 0
+#endif
+constexpr bool kSetPrio = PXS_ATTN_SETPRIO != 0;
 constexpr int kKeyRowsLds = 1024;  // longest permuted segment whose key rows are staged in LDS
 
 template <int NW>
@@ -626,8 +632,10 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         wait_vmcnt0();
         barrier_no_fence();
         if (j + 2 < ntiles) issue(j + 2);
+        if constexpr (kSetPrio) __builtin_amdgcn_s_setprio(1);
         pv(j - 1, p);
         qk(j + 1, s_next);
+        if constexpr (kSetPrio) __builtin_amdgcn_s_setprio(0);
         softmax_exp_checked(s_cur, p);
     };
     auto step_first = [&](f32x16 (&s_cur)[2], f32x16 (&s_next)[2], bf16x8 (&p)[2][2]) {
