@@ -71,6 +71,19 @@ __device__ __forceinline__ int find_segment(const int64_t * __restrict__ tile_st
     return __builtin_amdgcn_readfirstlane(lo);
 }
 
+// Mean segment length (queries per segment, from the host-known total and
+// segment count) up to which bf16 head_dim-64 attention runs the per-segment
+// window kernel, and that kernel's waves per workgroup.
+#ifndef PXS_ATTN_WINDOW_MEAN
+#define PXS_ATTN_WINDOW_MEAN 512
+#endif
+#ifndef PXS_ATTN_WINDOW_WAVES
+#define PXS_ATTN_WINDOW_WAVES 4
+#endif
+#ifndef PXS_ATTN_WINDOW_HPG
+#define PXS_ATTN_WINDOW_HPG 1  // heads per workgroup; 0 = from the segment count
+#endif
+
 // Mean segment length from which the generic kernel runs 4 waves per
 // workgroup instead of one.
 #ifndef PXS_ATTN_NW4_MIN
@@ -701,6 +714,290 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Short segments (windows of a few hundred rows, bf16, head_dim 64): one
+// workgroup owns a segment and a group of heads and walks its (head, query
+// pass, 64-key chunk) items with one continuous K/V DMA pipeline, so the
+// segment's setup (bounds, row-map staging) and the pipeline fill are paid
+// once per segment and head group, not once per head; each item is an exact
+// online-softmax step (the chunk's own max).  A pass covers 32 * NW queries.
+#ifndef PXS_ATTN_WINDOW_STAGES
+#define PXS_ATTN_WINDOW_STAGES 2
+#endif
+// K/V ring depth; chunk t+kWinStages-1 is issued while chunk t is computed.
+constexpr int kWinStages = PXS_ATTN_WINDOW_STAGES;
+constexpr int kWinAhead = kWinStages - 1;
+constexpr int kWinRowsLds = 512;  // longest segment whose row map is staged in LDS (8^3)
+
+#ifndef PXS_ATTN_WINDOW_WAVES_PER_EU
+#define PXS_ATTN_WINDOW_WAVES_PER_EU 2
+#endif
+
+template <int NW>
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(PXS_ATTN_WINDOW_WAVES_PER_EU)))
+window_attn_bf16_kernel(AttnArgs a, int heads, int heads_per_group, int groups) {
+    constexpr int kTileBytes = kKeys * 128;       // 64 keys x 64 dims, bf16
+    constexpr int kInstr = 2 * (kKeys / 8) / NW;  // K + V DMA instructions per wave per chunk
+    static_assert(kInstr >= 1 && kInstr * NW * 8 == 2 * kKeys, "chunk rows must split over waves");
+    __shared__ __align__(16) char lds[kWinStages][2 * kTileBytes];
+    __shared__ int32_t q_rows[kWinRowsLds];
+    __shared__ int32_t k_rows[kWinRowsLds];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, r = lane & 31;
+    // Consecutive workgroups land on different XCDs, which spreads the
+    // segments (and the empty ones a window partition's bound appends) evenly;
+    // segments share no rows, so there is no L2 locality to keep.
+    const int64_t logical = blockIdx.x;
+    const int seg = static_cast<int>(logical / groups);
+    const int grp = static_cast<int>(logical - static_cast<int64_t>(seg) * groups);
+    const int head0 = grp * heads_per_group;
+    const int nheads = min(heads_per_group, heads - head0);
+    const int64_t q0 = a.cu_q[seg], k0 = a.cu_k[seg];
+    const int64_t nq = a.cu_q[seg + 1] - q0, nk = a.cu_k[seg + 1] - k0;
+    if (nq <= 0 || nheads <= 0) return;  // uniform over the workgroup
+
+    const uint16_t * __restrict__ qp = static_cast<const uint16_t *>(a.q);
+    const uint16_t * __restrict__ kp = static_cast<const uint16_t *>(a.k);
+    const uint16_t * __restrict__ vp = static_cast<const uint16_t *>(a.v);
+    uint16_t * __restrict__ op = static_cast<uint16_t *>(a.o);
+
+    // Physical rows of the segment's queries and keys.
+    const bool q_lds = nq <= kWinRowsLds, k_lds = nk <= kWinRowsLds;
+    for (int64_t i = tid; i < nq && q_lds; i += NW * 64)
+        q_rows[i] = static_cast<int32_t>(a.row_map ? a.row_map[q0 + i] : q0 + i);
+    for (int64_t i = tid; i < nk && k_lds; i += NW * 64)
+        k_rows[i] = static_cast<int32_t>(a.row_map ? a.row_map[k0 + i] : k0 + i);
+    __syncthreads();
+    auto q_row_of = [&](int64_t i) -> int64_t {
+        return q_lds ? q_rows[i] : (a.row_map ? a.row_map[q0 + i] : q0 + i);
+    };
+    auto k_row_of = [&](int64_t i) -> int64_t {
+        return k_lds ? k_rows[i] : (a.row_map ? a.row_map[k0 + i] : k0 + i);
+    };
+
+    const int passes = static_cast<int>((nq + 32 * NW - 1) / (32 * NW));
+    const int chunks = static_cast<int>((nk + kKeys - 1) / kKeys);
+    if (chunks == 0) {
+        // queries without keys: zeros, as the tiled kernels write
+        for (int hh = 0; hh < nheads; ++hh)
+            for (int64_t i = wave * 32 + r; i < nq; i += 32 * NW) {
+                if (h) continue;
+                uint4 * dst = reinterpret_cast<uint4 *>(op + q_row_of(i) * a.ldo + (head0 + hh) * 64);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[j] = make_uint4(0, 0, 0, 0);
+            }
+        return;
+    }
+    const int per_head = passes * chunks;
+    const int items = nheads * per_head;
+    const int lrow = lane >> 3, lslot = lane & 7;
+    const uint32_t lds_base = lds_offset(&lds[0][0]);
+    uint64_t zero_addr = reinterpret_cast<uint64_t>(&g_attn_zero[0]);
+    asm volatile("" : "+s"(zero_addr));
+
+    auto issue = [&](int t) __attribute__((always_inline)) {
+        const int hh = t / per_head;
+        const int kc = (t - hh * per_head) % chunks;
+        const int head = head0 + hh;
+        const uint32_t base = lds_base + (t % kWinStages) * (2 * kTileBytes);
+#pragma unroll
+        for (int j = 0; j < kInstr; ++j) {
+            const int unit = wave * kInstr + j;  // 0..15: 8 K blocks then 8 V blocks
+            const bool is_v = unit >= kKeys / 8;
+            const int row0 = (unit % (kKeys / 8)) * 8;
+            const int row = row0 + lrow;
+            const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
+            const int64_t kidx = static_cast<int64_t>(kc) * kKeys + row;
+            const void * g = reinterpret_cast<const void *>(zero_addr);
+            if (kidx < nk) {
+                const int64_t prow = k_row_of(kidx);
+                g = is_v ? static_cast<const void *>(vp + prow * a.ldv + head * 64 + piece * 8)
+                         : static_cast<const void *>(kp + prow * a.ldk + head * 64 + piece * 8);
+            }
+            lds_dma16(g, base + (is_v ? kTileBytes : 0) + row0 * 128);
+        }
+    };
+
+    // Q^T fragments (B operand) of one (head, pass): dims 32h + 8st ..
+    auto load_q = [&](int hh, int pass, bf16x8 (&dst)[4]) __attribute__((always_inline)) {
+        const int64_t qi = static_cast<int64_t>(pass) * 32 * NW + wave * 32 + r;
+        const int64_t prow = qi < nq ? q_row_of(qi) : -1;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (prow >= 0)
+                v = *reinterpret_cast<const uint4 *>(qp + prow * a.ldq + (head0 + hh) * 64 + 32 * h + 8 * st);
+            dst[st] = __builtin_bit_cast(bf16x8, v);
+        }
+    };
+
+    const int G = lane >> 4, jl = lane & 15;
+    const int v_key_off = 4 * (G >> 1) + (jl >> 2);
+    const int v_dim_off = 16 * (G & 1) + 4 * (jl & 3);
+    const float c = a.scale_log2;
+
+    bf16x8 qf[4], qn[4];
+    load_q(0, 0, qn);
+#pragma unroll
+    for (int t = 0; t < kWinAhead; ++t)
+        if (t < items) issue(t);
+
+    f32x16 oacc[2];
+    float m_run = -INFINITY, l_part = 0.0f;
+    for (int t = 0; t < items; ++t) {
+        const int hh = t / per_head;
+        const int rem = t - hh * per_head;
+        const int pass = rem / chunks, kc = rem - (rem / chunks) * chunks;
+        // Item t's chunk has landed: only the DMAs of the items after it may
+        // be in flight (loads return in order, so anything issued before
+        // them is in too).
+        wait_vmcnt(min(kWinAhead - 1, items - 1 - t) * kInstr);
+        barrier_no_fence();
+        if (kc == 0) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st) qf[st] = qn[st];
+            // the next (head, pass) group's Q, loaded one group ahead and
+            // issued before the next DMA issue
+            const int nxt = t + chunks;
+            if (nxt < items) {
+                const int nh = nxt / per_head;
+                load_q(nh, (nxt - nh * per_head) / chunks, qn);
+            }
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
+            m_run = -INFINITY;
+            l_part = 0.0f;
+        }
+        asm volatile("" ::: "memory");
+        if (t + kWinAhead < items) issue(t + kWinAhead);
+
+        const char * kl = lds[t % kWinStages];
+        const char * vl = kl + kTileBytes;
+        f32x16 sc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int row = kt * 32 + r;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(
+                    kl + row * 128 + (((4 * h + st) ^ kswz(row)) << 4));
+                if (st == 0) {
+                    const f32x16 zero = {};
+                    sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], zero, 0, 0, 0);
+                } else {
+                    sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], sc[kt], 0, 0, 0);
+                }
+            }
+        }
+        const int64_t valid = nk - static_cast<int64_t>(kc) * kKeys;
+        if (valid < kKeys) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (key >= valid) sc[kt][v] = -INFINITY;
+                }
+        }
+        float mx = sc[0][0];
+#pragma unroll
+        for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sc[0][v]);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[1][v]);
+        mx = lane_pair_max(mx);
+        const float m_new = fmaxf(m_run, mx);  // finite: every chunk has a valid key
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
+        m_run = m_new;
+        l_part *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+        const float mc = m_run * c;
+        const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+        bf16x8 pb[2][2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                bf16x8 p8;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    bf16x2 pp;
+                    pp[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][8 * u + e], c, -mc)));
+                    pp[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][8 * u + e + 1], c, -mc)));
+                    p8[e] = pp[0];
+                    p8[e + 1] = pp[1];
+                    l_part = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, l_part, false);
+                }
+                pb[kt][u] = p8;
+            }
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int key_a = kt * 32 + 16 * u + v_key_off;
+                const int key_b = key_a + 8;
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) {
+                    const int dbyte = (dt * 32 + v_dim_off) * 2;
+                    const int piece = dbyte >> 4, within = dbyte & 15;
+                    const char * pa = vl + key_a * 128 + ((piece ^ vswz(key_a)) << 4) + within;
+                    const char * pbp = vl + key_b * 128 + ((piece ^ vswz(key_b)) << 4) + within;
+                    const v4i16 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (v4i16 __attribute__((address_space(3))) *)(pa));
+                    const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (v4i16 __attribute__((address_space(3))) *)(pbp));
+                    const uint2 lo2 = __builtin_bit_cast(uint2, lo4);
+                    const uint2 hi2 = __builtin_bit_cast(uint2, hi4);
+                    const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kt][u], oacc[dt], 0, 0, 0);
+                }
+            }
+        }
+        if (kc == chunks - 1) {
+            const float l_tot = lane_pair_sum(l_part);
+            const int64_t qi = static_cast<int64_t>(pass) * 32 * NW + wave * 32 + r;
+            if (qi < nq) {
+                const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+                uint16_t * dst = op + q_row_of(qi) * a.ldo + (head0 + hh) * 64;
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int d = dt * 32 + 8 * i + 4 * h;
+                        uint2 packed;
+                        packed.x = pack_bf16x2(oacc[dt][4 * i + 0] * inv_l, oacc[dt][4 * i + 1] * inv_l);
+                        packed.y = pack_bf16x2(oacc[dt][4 * i + 2] * inv_l, oacc[dt][4 * i + 3] * inv_l);
+                        *reinterpret_cast<uint2 *>(dst + d) = packed;
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int NW>
+int launch_attn_window(const AttnArgs & args, int heads, hipStream_t stream) {
+    // Head groups: enough workgroups to give every CU a few (256 CUs).
+    const int64_t want = (4 * 256 + args.nseg - 1) / std::max(args.nseg, 1);
+    const int groups0 = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(heads, want)));
+    const int hpg = PXS_ATTN_WINDOW_HPG > 0 ? std::min(heads, PXS_ATTN_WINDOW_HPG)
+                                            : (heads + groups0 - 1) / groups0;
+    const int groups = (heads + hpg - 1) / hpg;
+    const int64_t blocks = static_cast<int64_t>(args.nseg) * groups;
+    if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "attention grid too large");
+    hipLaunchKernelGGL((window_attn_bf16_kernel<NW>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(NW * 64), 0, stream, args, heads, hpg, groups);
+    return check_launch("window attention (bf16)");
+}
+
 template <int NW>
 int launch_attn_bf16(const AttnArgs & args, int64_t total_q, int heads, hipStream_t stream) {
     const int64_t bound = total_q / (32 * NW) + args.nseg + 1;
@@ -876,6 +1173,13 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     const bool fast = dtype == PXS_BF16 && head_dim == 64 && value_dim == 64 && (ld_q % 8 == 0) &&
                       (ld_k % 8 == 0) && (ld_v % 8 == 0) && (ld_o % 4 == 0) && aligned16(q) &&
                       aligned16(k) && aligned16(v) && (reinterpret_cast<uintptr_t>(o) & 7u) == 0;
+    if (fast && total_q <= static_cast<int64_t>(PXS_ATTN_WINDOW_MEAN) * nseg) {
+        AttnArgs a{};
+        a.q = q; a.k = k; a.v = v; a.ldq = ld_q; a.ldk = ld_k; a.ldv = ld_v;
+        a.cu_q = cu_q; a.cu_k = cu_k; a.nseg = nseg; a.row_map = row_map;
+        a.hd = head_dim; a.vd = value_dim; a.scale_log2 = scale * kLog2e; a.o = o; a.ldo = ld_o;
+        return launch_attn_window<PXS_ATTN_WINDOW_WAVES>(a, heads, s);
+    }
     // Waves per workgroup (32 queries each, sharing the K/V tiles).  The bf16
     // kernel always runs 4: its 4-stage K/V ring takes 64 KB of LDS per
     // workgroup whatever the wave count, so fewer waves only lower occupancy

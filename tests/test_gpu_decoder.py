@@ -311,3 +311,58 @@ def test_decoder_stack_errors(px):
         swapped = list(case["blocks"])
         swapped[0], swapped[1] = swapped[1], swapped[0]
         run_decoder(px, dict(case, blocks=swapped), pxs.PXS_F32, True)
+
+
+def without_residual_branches(case):
+    """Every ConvNeXt MLP-2 and every C2S conv2 (weight and bias) set to zero:
+    each ConvNeXt block becomes the identity and each C2S block its
+    subdivided, channel-repeated skip (src/slat_decoder.cpp:210-222, 262-287)."""
+    blocks = []
+    for kind, C, O_, M, w in case["blocks"]:
+        w = dict(w)
+        names = ("mlp2_weight", "mlp2_bias") if kind == pxs.PXS_DECODER_CONVNEXT else \
+            ("conv2_weight", "conv2_bias")
+        for k in names:
+            w[k] = np.zeros_like(w[k])
+        blocks.append((kind, C, O_, M, w))
+    return dict(case, blocks=blocks)
+
+
+def closed_form_decoder(orc, case, guides):
+    """slat_decoder_forward_f32 (src/slat_decoder.cpp:332-376) with the residual
+    branches zeroed: out_linear(LN_1e-5(R_L( ... R_1(from_latent(x)) ... ))),
+    R_l = repeat each channel of channel_to_spatial(h, guide_l) to the next
+    level's width.  Built from the pinned primitives only, not from the
+    decoder composition."""
+    coords, h = case["coords"], orc.linear(case["x"], *case["fl"])
+    ch = case["channels"]
+    for level in range(len(ch) - 1):
+        coords, sub = orc.channel_to_spatial(coords, h, 2, guides[level])
+        h = np.repeat(sub, ch[level + 1] // (ch[level] // 8), axis=1)
+    return coords, orc.linear(orc.layer_norm(h, 1e-5), *case["out"])
+
+
+@pytest.mark.parametrize("dtype", [pxs.PXS_F32, pxs.PXS_BF16])
+def test_decoder_stack_closed_form(px, orc, dtype):
+    """The device stack and the oracle's chained blocks both reduce to the
+    closed form when the residual branches are zero: this pins the chain (the
+    latent projection first, the levels' subdivisions in order, the skip's
+    channel repeat, the final affine-free layer norm at eps 1e-5 and the
+    output linear) independently of the chained restatement.  256 -> 32 -> 16
+    channels: a level-1 child's 4 channels come from 4 different level-0
+    channels, so the final norm sees 4 distinct values per row (with 64 -> 32
+    every child would hold one value repeated, a zero-variance norm input whose
+    output is rounding noise times 1/sqrt(eps))."""
+    case = without_residual_branches(decoder_case(87, channels=(256, 32, 16), nblocks=(2, 1, 1)))
+    n0 = case["coords"].shape[0]
+    g0 = W.normal(88, n0 * 8, 1).reshape(n0, 8)
+    n1 = int((g0 > 0).sum())
+    guides = [g0, W.normal(89, n1 * 8, 1).reshape(n1, 8)]
+    rc, ry = closed_form_decoder(orc, case, guides)
+    print(f"[decoder closed form] dtype={dtype} rows={rc.shape[0]}", flush=True)
+    oc, y, _, _ = run_decoder(px, case, dtype, False, guide=guides)
+    np.testing.assert_array_equal(host(oc).astype(np.int32), rc)
+    assert_fp32(host(y), ry, what=f"decoder closed form dtype={dtype}")
+    oc2, oy = oracle_decoder(orc, case, pxs.PXS_F32, lambda level, h, w: guides[level])
+    np.testing.assert_array_equal(oc2, rc)
+    assert_fp32(oy, ry, what="chained oracle blocks vs closed form")

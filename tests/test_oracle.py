@@ -523,3 +523,41 @@ def test_flow_sampler_closed_forms(orc):
     for i in range(4):
         rc, t, tn, g = orc.flow_schedule(4, [1e-5, 1.0, 2.0, 0.0, 0.0, 1.0], i)
         assert rc == 0 and t == np.float32(1.0) - np.float32(i) / np.float32(4.0) and g == 2.0
+
+
+@pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref is built only where /root/reference exists")
+def test_decoder_closed_form_helper_matches_compiled_reference(orc):
+    """The decoder closed form (residual branches zero) built from the oracle's
+    primitives equals the same chain built from the compiled reference's
+    primitives (sparse_linear, sparse_channel_to_spatial, sparse_layer_norm)
+    bit for bit; the channel repeat is repeat_channels (src/slat_decoder.cpp:
+    84-107: each channel `repeats` times in a row)."""
+    ref = O.Reference()
+    coords = W.shell_coords(12, [[(3.0, 4.5)], [(2.5, 4.0)]], 90)
+    n, latent, ch = coords.shape[0], 8, (256, 32, 16)  # 4 distinct values per final row
+    x = W.normal(90, n * latent, 1).reshape(n, latent)
+    fl_w = W.normal(90, ch[0] * latent, 2).reshape(ch[0], latent)
+    fl_b = W.normal(90, ch[0], 3)
+    ow = W.normal(90, 24 * ch[-1], 4).reshape(24, ch[-1])
+    ob = W.normal(90, 24, 5)
+    g0 = W.normal(91, n * 8, 1).reshape(n, 8)
+    n1 = int((g0 > 0).sum())
+    guides = [g0, W.normal(92, n1 * 8, 1).reshape(n1, 8)]
+    # oracle primitives
+    c, h = coords, orc.linear(x, fl_w, fl_b)
+    for lv in range(2):
+        c, sub = orc.channel_to_spatial(c, h, 2, guides[lv])
+        h = np.repeat(sub, ch[lv + 1] // (ch[lv] // 8), axis=1)
+    want = orc.linear(orc.layer_norm(h, 1e-5), ow, ob)
+    # reference primitives
+    shape = 12
+    t = ref.linear(ref.sparse(coords, x, 2, (shape,) * 3), fl_w, fl_b)
+    for lv in range(2):
+        cc, _ = t.read()
+        t = ref.channel_to_spatial(t, 2, ref.sparse(cc, guides[lv], 2, (shape,) * 3))
+        shape *= 2
+        rc, rf = t.read()
+        t = ref.sparse(rc, np.repeat(rf, ch[lv + 1] // (ch[lv] // 8), axis=1), 2, (shape,) * 3)
+    got = ref.linear(ref.layer_norm(t, 1e-5), ow, ob).read()
+    np.testing.assert_array_equal(got[0], c)
+    np.testing.assert_array_equal(got[1], want)
