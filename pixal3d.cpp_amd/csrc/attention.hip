@@ -30,7 +30,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// s_waitcnt with only vmcnt bounded (n <= 15; expcnt/lgkmcnt at their maxima).
+// s_waitcnt with only vmcnt bounded (expcnt/lgkmcnt at their maxima); n above
+// 15 waits for everything.
 __device__ __forceinline__ void wait_vmcnt(int n) {
     switch (n) {
     case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
@@ -41,6 +42,13 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
     case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
     case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
     case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+    case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+    case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+    case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
     default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
     }
 }
@@ -717,20 +725,31 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 // ---------------------------------------------------------------------------
 // Short segments (windows of a few hundred rows, bf16, head_dim 64): one
 // workgroup owns a segment and a group of heads and walks its (head, query
-// pass, 64-key chunk) items with one continuous K/V DMA pipeline, so the
+// pass, 64-key chunk) items with one continuous DMA pipeline, so the
 // segment's setup (bounds, row-map staging) and the pipeline fill are paid
 // once per segment and head group, not once per head; each item is an exact
 // online-softmax step (the chunk's own max).  A pass covers 32 * NW queries.
+//
+// Every global read in the item loop is an LDS DMA whose completion the
+// kernel counts itself: the K/V chunks go through a ring of kWinStages
+// stages shared by the waves, and each wave DMAs its own 32 query rows into
+// a private slot (kWinStages slots per wave) with the first chunk of each
+// (head, pass), and reads its fragments from there at every item of it.
+// Chunk t + kWinStages is issued at the end of item t, once a barrier shows
+// every wave has finished reading stage t % kWinStages.  The kernel is
+// latency bound (a workgroup's chain is segment bounds -> row map -> DMA ->
+// compute -> store), so what it is tuned for is workgroups per CU: one stage
+// and re-read query fragments keep it at 36 KB of LDS and 128 VGPRs, four
+// workgroups per CU.
 #ifndef PXS_ATTN_WINDOW_STAGES
-#define PXS_ATTN_WINDOW_STAGES 2
+#define PXS_ATTN_WINDOW_STAGES 1
 #endif
-// K/V ring depth; chunk t+kWinStages-1 is issued while chunk t is computed.
 constexpr int kWinStages = PXS_ATTN_WINDOW_STAGES;
-constexpr int kWinAhead = kWinStages - 1;
+static_assert(kWinStages >= 1 && kWinStages <= 3, "window ring depth");
 constexpr int kWinRowsLds = 512;  // longest segment whose row map is staged in LDS (8^3)
 
 #ifndef PXS_ATTN_WINDOW_WAVES_PER_EU
-#define PXS_ATTN_WINDOW_WAVES_PER_EU 2
+#define PXS_ATTN_WINDOW_WAVES_PER_EU 4
 #endif
 
 template <int NW>
@@ -739,8 +758,12 @@ __attribute__((amdgpu_waves_per_eu(PXS_ATTN_WINDOW_WAVES_PER_EU)))
 window_attn_bf16_kernel(AttnArgs a, int heads, int heads_per_group, int groups) {
     constexpr int kTileBytes = kKeys * 128;       // 64 keys x 64 dims, bf16
     constexpr int kInstr = 2 * (kKeys / 8) / NW;  // K + V DMA instructions per wave per chunk
+    constexpr int kQInstr = 4;                    // 32 query rows x 8 pieces / 64 lanes
+    constexpr int kQSlotBytes = 32 * 128;
     static_assert(kInstr >= 1 && kInstr * NW * 8 == 2 * kKeys, "chunk rows must split over waves");
+    static_assert((kWinStages - 1) * (kInstr + kQInstr) <= 15, "vmcnt bookkeeping range");
     __shared__ __align__(16) char lds[kWinStages][2 * kTileBytes];
+    __shared__ __align__(16) char qlds[kWinStages][NW][kQSlotBytes];
     __shared__ int32_t q_rows[kWinRowsLds];
     __shared__ int32_t k_rows[kWinRowsLds];
 
@@ -759,227 +782,285 @@ window_attn_bf16_kernel(AttnArgs a, int heads, int heads_per_group, int groups) 
     const int64_t nq = a.cu_q[seg + 1] - q0, nk = a.cu_k[seg + 1] - k0;
     if (nq <= 0 || nheads <= 0) return;  // uniform over the workgroup
 
-    const uint16_t * __restrict__ qp = static_cast<const uint16_t *>(a.q);
-    const uint16_t * __restrict__ kp = static_cast<const uint16_t *>(a.k);
-    const uint16_t * __restrict__ vp = static_cast<const uint16_t *>(a.v);
+    const char * __restrict__ qp = static_cast<const char *>(a.q);
+    const char * __restrict__ kp = static_cast<const char *>(a.k);
+    const char * __restrict__ vp = static_cast<const char *>(a.v);
     uint16_t * __restrict__ op = static_cast<uint16_t *>(a.o);
-
-    // Physical rows of the segment's queries and keys.
-    const bool q_lds = nq <= kWinRowsLds, k_lds = nk <= kWinRowsLds;
-    for (int64_t i = tid; i < nq && q_lds; i += NW * 64)
-        q_rows[i] = static_cast<int32_t>(a.row_map ? a.row_map[q0 + i] : q0 + i);
-    for (int64_t i = tid; i < nk && k_lds; i += NW * 64)
-        k_rows[i] = static_cast<int32_t>(a.row_map ? a.row_map[k0 + i] : k0 + i);
-    __syncthreads();
-    auto q_row_of = [&](int64_t i) -> int64_t {
-        return q_lds ? q_rows[i] : (a.row_map ? a.row_map[q0 + i] : q0 + i);
-    };
-    auto k_row_of = [&](int64_t i) -> int64_t {
-        return k_lds ? k_rows[i] : (a.row_map ? a.row_map[k0 + i] : k0 + i);
-    };
+    // Row strides in bytes; the drop-in's strides are far below 2^32 bytes.
+    const uint32_t ldq_b = static_cast<uint32_t>(a.ldq) * 2u;
+    const uint32_t ldk_b = static_cast<uint32_t>(a.ldk) * 2u;
+    const uint32_t ldv_b = static_cast<uint32_t>(a.ldv) * 2u;
+    const uint64_t q_addr = reinterpret_cast<uint64_t>(qp);
+    // Each wave DMAs only K rows or only V rows of a chunk (NW >= 2): its
+    // source and stride are chosen once here, as values.
+    static_assert(NW >= 2, "a wave's chunk DMAs must be all K or all V");
+    const bool dma_v = wave * kInstr >= kKeys / 8;
+    const uint32_t dma_ld = dma_v ? ldv_b : ldk_b;
+    const uint64_t dma_base = dma_v ? reinterpret_cast<uint64_t>(vp) : reinterpret_cast<uint64_t>(kp);
 
     const int passes = static_cast<int>((nq + 32 * NW - 1) / (32 * NW));
     const int chunks = static_cast<int>((nk + kKeys - 1) / kKeys);
-    if (chunks == 0) {
-        // queries without keys: zeros, as the tiled kernels write
-        for (int hh = 0; hh < nheads; ++hh)
-            for (int64_t i = wave * 32 + r; i < nq; i += 32 * NW) {
-                if (h) continue;
-                uint4 * dst = reinterpret_cast<uint4 *>(op + q_row_of(i) * a.ldo + (head0 + hh) * 64);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) dst[j] = make_uint4(0, 0, 0, 0);
-            }
-        return;
-    }
     const int per_head = passes * chunks;
     const int items = nheads * per_head;
     const int lrow = lane >> 3, lslot = lane & 7;
     const uint32_t lds_base = lds_offset(&lds[0][0]);
+    const uint32_t q_base = lds_offset(&qlds[0][wave][0]);
     uint64_t zero_addr = reinterpret_cast<uint64_t>(&g_attn_zero[0]);
     asm volatile("" : "+s"(zero_addr));
-
-    auto issue = [&](int t) __attribute__((always_inline)) {
-        const int hh = t / per_head;
-        const int kc = (t - hh * per_head) % chunks;
-        const int head = head0 + hh;
-        const uint32_t base = lds_base + (t % kWinStages) * (2 * kTileBytes);
-#pragma unroll
-        for (int j = 0; j < kInstr; ++j) {
-            const int unit = wave * kInstr + j;  // 0..15: 8 K blocks then 8 V blocks
-            const bool is_v = unit >= kKeys / 8;
-            const int row0 = (unit % (kKeys / 8)) * 8;
-            const int row = row0 + lrow;
-            const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
-            const int64_t kidx = static_cast<int64_t>(kc) * kKeys + row;
-            const void * g = reinterpret_cast<const void *>(zero_addr);
-            if (kidx < nk) {
-                const int64_t prow = k_row_of(kidx);
-                g = is_v ? static_cast<const void *>(vp + prow * a.ldv + head * 64 + piece * 8)
-                         : static_cast<const void *>(kp + prow * a.ldk + head * 64 + piece * 8);
-            }
-            lds_dma16(g, base + (is_v ? kTileBytes : 0) + row0 * 128);
-        }
-    };
-
-    // Q^T fragments (B operand) of one (head, pass): dims 32h + 8st ..
-    auto load_q = [&](int hh, int pass, bf16x8 (&dst)[4]) __attribute__((always_inline)) {
-        const int64_t qi = static_cast<int64_t>(pass) * 32 * NW + wave * 32 + r;
-        const int64_t prow = qi < nq ? q_row_of(qi) : -1;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (prow >= 0)
-                v = *reinterpret_cast<const uint4 *>(qp + prow * a.ldq + (head0 + hh) * 64 + 32 * h + 8 * st);
-            dst[st] = __builtin_bit_cast(bf16x8, v);
-        }
-    };
-
     const int G = lane >> 4, jl = lane & 15;
     const int v_key_off = 4 * (G >> 1) + (jl >> 2);
     const int v_dim_off = 16 * (G & 1) + 4 * (jl & 3);
     const float c = a.scale_log2;
 
-    bf16x8 qf[4], qn[4];
-    load_q(0, 0, qn);
+    // The item loop, for a row map staged in LDS (the segment's physical rows,
+    // row_map or identity) or read from global memory (longer segments).
+    auto run = [&](auto rows_in_lds) __attribute__((always_inline)) {
+        constexpr bool kLds = decltype(rows_in_lds)::value;
+        auto q_row_of = [&](int i) -> uint32_t {
+            if constexpr (kLds) return static_cast<uint32_t>(q_rows[i]);
+            else return static_cast<uint32_t>(a.row_map ? a.row_map[q0 + i] : q0 + i);
+        };
+        auto k_row_of = [&](int i) -> uint32_t {
+            if constexpr (kLds) return static_cast<uint32_t>(k_rows[i]);
+            else return static_cast<uint32_t>(a.row_map ? a.row_map[k0 + i] : k0 + i);
+        };
+        if (chunks == 0) {
+            // queries without keys: zeros, as the tiled kernels write
+            for (int hh = 0; hh < nheads; ++hh)
+                for (int i = wave * 32 + r; i < nq; i += 32 * NW) {
+                    if (h) continue;
+                    uint4 * dst = reinterpret_cast<uint4 *>(
+                        op + static_cast<int64_t>(q_row_of(i)) * a.ldo + (head0 + hh) * 64);
 #pragma unroll
-    for (int t = 0; t < kWinAhead; ++t)
-        if (t < items) issue(t);
+                    for (int j = 0; j < 8; ++j) dst[j] = make_uint4(0, 0, 0, 0);
+                }
+            return;
+        }
 
-    f32x16 oacc[2];
-    float m_run = -INFINITY, l_part = 0.0f;
-    for (int t = 0; t < items; ++t) {
-        const int hh = t / per_head;
-        const int rem = t - hh * per_head;
-        const int pass = rem / chunks, kc = rem - (rem / chunks) * chunks;
-        // Item t's chunk has landed: only the DMAs of the items after it may
-        // be in flight (loads return in order, so anything issued before
-        // them is in too).
-        wait_vmcnt(min(kWinAhead - 1, items - 1 - t) * kInstr);
-        barrier_no_fence();
-        if (kc == 0) {
+        // DMA instructions per wave that item t issues: its K/V chunk, plus
+        // this wave's query rows when it is the first chunk of a (head, pass).
+        auto instrs = [&](int t) -> int { return kInstr + (t % chunks == 0 ? kQInstr : 0); };
+        auto issue = [&](int t) __attribute__((always_inline)) {
+            const int hh = t / per_head;
+            const int rem = t - hh * per_head;
+            const int kc = rem % chunks;
+            const uint32_t head_b = static_cast<uint32_t>(head0 + hh) * 128u;
+            const uint32_t base = lds_base + (t % kWinStages) * (2 * kTileBytes);
+            // the lane's rows first, then the addresses: one LDS round trip
+            int32_t kidx[kInstr];
+            uint32_t prow[kInstr];
 #pragma unroll
-            for (int st = 0; st < 4; ++st) qf[st] = qn[st];
-            // the next (head, pass) group's Q, loaded one group ahead and
-            // issued before the next DMA issue
-            const int nxt = t + chunks;
-            if (nxt < items) {
-                const int nh = nxt / per_head;
-                load_q(nh, (nxt - nh * per_head) / chunks, qn);
+            for (int j = 0; j < kInstr; ++j) {
+                const int unit = wave * kInstr + j;  // 0..15: 8 K blocks then 8 V blocks
+                kidx[j] = kc * kKeys + (unit % (kKeys / 8)) * 8 + lrow;
+                prow[j] = kidx[j] < nk ? k_row_of(kidx[j]) : 0u;
             }
 #pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
+            for (int j = 0; j < kInstr; ++j) {
+                const int unit = wave * kInstr + j;
+                const int row0 = (unit % (kKeys / 8)) * 8;
+                const int row = row0 + lrow;
+                const uint32_t piece_b = static_cast<uint32_t>(lslot ^ (dma_v ? vswz(row) : kswz(row))) * 16u;
+                const uint64_t addr = static_cast<uint64_t>(prow[j]) * dma_ld + dma_base + (head_b + piece_b);
+                lds_dma16(reinterpret_cast<const void *>(kidx[j] < nk ? addr : zero_addr),
+                          base + (dma_v ? kTileBytes : 0) + row0 * 128);
+            }
+            if (kc == 0) {
+                // this wave's 32 query rows of (head, pass), K-swizzled like a key tile
+                const int pass = rem / chunks;
+                const uint32_t qb = q_base + ((t / chunks) % kWinStages) * (NW * kQSlotBytes);
+                int32_t qi[kQInstr];
+                uint32_t qrow[kQInstr];
 #pragma unroll
-                for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
-            m_run = -INFINITY;
-            l_part = 0.0f;
-        }
-        asm volatile("" ::: "memory");
-        if (t + kWinAhead < items) issue(t + kWinAhead);
-
-        const char * kl = lds[t % kWinStages];
-        const char * vl = kl + kTileBytes;
-        f32x16 sc[2];
+                for (int j = 0; j < kQInstr; ++j) {
+                    qi[j] = pass * 32 * NW + wave * 32 + j * 8 + lrow;
+                    qrow[j] = qi[j] < nq ? q_row_of(qi[j]) : 0u;
+                }
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            const int row = kt * 32 + r;
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(
-                    kl + row * 128 + (((4 * h + st) ^ kswz(row)) << 4));
-                if (st == 0) {
-                    const f32x16 zero = {};
-                    sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], zero, 0, 0, 0);
-                } else {
-                    sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], sc[kt], 0, 0, 0);
+                for (int j = 0; j < kQInstr; ++j) {
+                    const uint32_t piece_b = static_cast<uint32_t>(lslot ^ kswz(j * 8 + lrow)) * 16u;
+                    const uint64_t addr = static_cast<uint64_t>(qrow[j]) * ldq_b + q_addr + (head_b + piece_b);
+                    lds_dma16(reinterpret_cast<const void *>(qi[j] < nq ? addr : zero_addr),
+                              qb + j * 8 * 128);
                 }
             }
-        }
-        const int64_t valid = nk - static_cast<int64_t>(kc) * kKeys;
-        if (valid < kKeys) {
+        };
+
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                    if (key >= valid) sc[kt][v] = -INFINITY;
-                }
-        }
-        float mx = sc[0][0];
-#pragma unroll
-        for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sc[0][v]);
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[1][v]);
-        mx = lane_pair_max(mx);
-        const float m_new = fmaxf(m_run, mx);  // finite: every chunk has a valid key
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
-        m_run = m_new;
-        l_part *= alpha;
+        for (int t = 0; t < kWinStages; ++t)
+            if (t < items) issue(t);
+
+        // Zeroed once: each group's first item rescales the accumulators by
+        // exp2(-inf) = 0 (the scale is positive), which clears what the
+        // previous group left (finite).
+        f32x16 oacc[2];
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
-        const float mc = m_run * c;
-        const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-        bf16x8 pb[2][2];
+            for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
+        float m_run = -INFINITY, l_part = 0.0f;
+        for (int t = 0; t < items; ++t) {
+            const int hh = t / per_head;
+            const int rem = t - hh * per_head;
+            const int pass = rem / chunks, kc = rem - (rem / chunks) * chunks;
+            // Item t's DMAs have landed: only those of the items issued after
+            // it (t+1 .. t+kWinStages-1) may be in flight; loads return in order.
+            int after = 0;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
+            for (int u = 1; u < kWinStages; ++u)
+                if (t + u < items) after += instrs(t + u);
+            wait_vmcnt(after);
+            barrier_no_fence();
+            // A wave whose 32 queries all lie past the segment's end (the last
+            // pass of a segment that is not a multiple of 32 * NW) only keeps
+            // the pipeline going: its DMAs and barriers, no compute.
+            const bool active = pass * 32 * NW + wave * 32 < nq;
+            if (kc == 0) m_run = -INFINITY;
+            if (active) {
+                // This wave's query fragments, read again for every item (its
+                // slot holds them until the group's last item ends), so no
+                // registers stay tied up with them across items.
+                bf16x8 qf[4];
+                const char * qs = &qlds[(t / chunks) % kWinStages][wave][0];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                bf16x8 p8;
+                for (int st = 0; st < 4; ++st)
+                    qf[st] = *reinterpret_cast<const bf16x8 *>(qs + r * 128 + (((4 * h + st) ^ kswz(r)) << 4));
+
+                const char * kl = lds[t % kWinStages];
+                const char * vl = kl + kTileBytes;
+                f32x16 sc[2];
 #pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    bf16x2 pp;
-                    pp[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][8 * u + e], c, -mc)));
-                    pp[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][8 * u + e + 1], c, -mc)));
-                    p8[e] = pp[0];
-                    p8[e + 1] = pp[1];
-                    l_part = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, l_part, false);
+                for (int kt = 0; kt < 2; ++kt) {
+                    const int row = kt * 32 + r;
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(
+                            kl + row * 128 + (((4 * h + st) ^ kswz(row)) << 4));
+                        if (st == 0) {
+                            const f32x16 zero = {};
+                            sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], zero, 0, 0, 0);
+                        } else {
+                            sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], sc[kt], 0, 0, 0);
+                        }
+                    }
                 }
-                pb[kt][u] = p8;
-            }
-        }
+                // Keys past the segment's end: register v of sub-tile kt holds
+                // key kt*32 + 8*(v/4) + 4h + v%4, so each block of four
+                // registers spans keys base .. base+7 over the two lane halves
+                // and is wholly valid, wholly masked or split (one block).
+                const int valid = static_cast<int>(min<int64_t>(nk - static_cast<int64_t>(kc) * kKeys, kKeys));
+                if (valid < kKeys) {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
+                    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int key_a = kt * 32 + 16 * u + v_key_off;
-                const int key_b = key_a + 8;
+                        for (int b = 0; b < 4; ++b) {
+                            const int base = kt * 32 + 8 * b;
+                            if (base >= valid) {
 #pragma unroll
-                for (int dt = 0; dt < 2; ++dt) {
-                    const int dbyte = (dt * 32 + v_dim_off) * 2;
-                    const int piece = dbyte >> 4, within = dbyte & 15;
-                    const char * pa = vl + key_a * 128 + ((piece ^ vswz(key_a)) << 4) + within;
-                    const char * pbp = vl + key_b * 128 + ((piece ^ vswz(key_b)) << 4) + within;
-                    const v4i16 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (v4i16 __attribute__((address_space(3))) *)(pa));
-                    const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (v4i16 __attribute__((address_space(3))) *)(pbp));
-                    const uint2 lo2 = __builtin_bit_cast(uint2, lo4);
-                    const uint2 hi2 = __builtin_bit_cast(uint2, hi4);
-                    const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
-                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kt][u], oacc[dt], 0, 0, 0);
+                                for (int i = 0; i < 4; ++i) sc[kt][4 * b + i] = -INFINITY;
+                            } else if (base + 8 > valid) {
+#pragma unroll
+                                for (int i = 0; i < 4; ++i)
+                                    if (base + 4 * h + i >= valid) sc[kt][4 * b + i] = -INFINITY;
+                            }
+                        }
                 }
+                float mx = sc[0][0];
+#pragma unroll
+                for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sc[0][v]);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[1][v]);
+                mx = lane_pair_max(mx);
+                const float m_new = fmaxf(m_run, mx);  // finite: every chunk has a valid key
+                const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
+                m_run = m_new;
+                l_part *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+                const float mc = m_run * c;
+                const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+                bf16x8 pb[2][2];
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        bf16x8 p8;
+#pragma unroll
+                        for (int e = 0; e < 8; e += 2) {
+                            bf16x2 pp;
+                            pp[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][8 * u + e], c, -mc)));
+                            pp[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][8 * u + e + 1], c, -mc)));
+                            p8[e] = pp[0];
+                            p8[e + 1] = pp[1];
+                            l_part = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, l_part, false);
+                        }
+                        pb[kt][u] = p8;
+                    }
+                }
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int key_a = kt * 32 + 16 * u + v_key_off;
+                        const int key_b = key_a + 8;
+#pragma unroll
+                        for (int dt = 0; dt < 2; ++dt) {
+                            const int dbyte = (dt * 32 + v_dim_off) * 2;
+                            const int piece = dbyte >> 4, within = dbyte & 15;
+                            const char * pa = vl + key_a * 128 + ((piece ^ vswz(key_a)) << 4) + within;
+                            const char * pbp = vl + key_b * 128 + ((piece ^ vswz(key_b)) << 4) + within;
+                            const v4i16 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                (v4i16 __attribute__((address_space(3))) *)(pa));
+                            const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                (v4i16 __attribute__((address_space(3))) *)(pbp));
+                            const uint2 lo2 = __builtin_bit_cast(uint2, lo4);
+                            const uint2 hi2 = __builtin_bit_cast(uint2, hi4);
+                            const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
+                            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kt][u], oacc[dt], 0, 0, 0);
+                        }
+                    }
+                }
+            }  // active
+            // Every wave has read stage t % kWinStages (and its own query
+            // slot): refill them with item t + kWinStages.
+            if (t + kWinStages < items) {
+                barrier_no_fence();
+                issue(t + kWinStages);
             }
-        }
-        if (kc == chunks - 1) {
-            const float l_tot = lane_pair_sum(l_part);
-            const int64_t qi = static_cast<int64_t>(pass) * 32 * NW + wave * 32 + r;
-            if (qi < nq) {
-                const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-                uint16_t * dst = op + q_row_of(qi) * a.ldo + (head0 + hh) * 64;
+            if (active && kc == chunks - 1) {
+                const float l_tot = lane_pair_sum(l_part);
+                const int qi = pass * 32 * NW + wave * 32 + r;
+                if (qi < nq) {
+                    const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+                    uint16_t * dst = op + static_cast<int64_t>(q_row_of(qi)) * a.ldo + (head0 + hh) * 64;
 #pragma unroll
-                for (int dt = 0; dt < 2; ++dt) {
+                    for (int dt = 0; dt < 2; ++dt) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int d = dt * 32 + 8 * i + 4 * h;
-                        uint2 packed;
-                        packed.x = pack_bf16x2(oacc[dt][4 * i + 0] * inv_l, oacc[dt][4 * i + 1] * inv_l);
-                        packed.y = pack_bf16x2(oacc[dt][4 * i + 2] * inv_l, oacc[dt][4 * i + 3] * inv_l);
-                        *reinterpret_cast<uint2 *>(dst + d) = packed;
+                        for (int i = 0; i < 4; ++i) {
+                            const int d = dt * 32 + 8 * i + 4 * h;
+                            uint2 packed;
+                            packed.x = pack_bf16x2(oacc[dt][4 * i + 0] * inv_l, oacc[dt][4 * i + 1] * inv_l);
+                            packed.y = pack_bf16x2(oacc[dt][4 * i + 2] * inv_l, oacc[dt][4 * i + 3] * inv_l);
+                            *reinterpret_cast<uint2 *>(dst + d) = packed;
+                        }
                     }
                 }
             }
         }
+    };
+
+    // Physical rows of the segment's queries and keys (row_map or identity).
+    if (nq <= kWinRowsLds && nk <= kWinRowsLds) {
+        for (int i = tid; i < nq; i += NW * 64)
+            q_rows[i] = static_cast<int32_t>(a.row_map ? a.row_map[q0 + i] : q0 + i);
+        for (int i = tid; i < nk; i += NW * 64)
+            k_rows[i] = static_cast<int32_t>(a.row_map ? a.row_map[k0 + i] : k0 + i);
+        __syncthreads();
+        run(std::true_type{});
+    } else {
+        run(std::false_type{});
     }
 }
 

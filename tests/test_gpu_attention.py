@@ -174,3 +174,29 @@ def test_attention_wide_heads(px, orc, dtype, hd, vd):
                                  row_map=ti32(perm), value_dim=vd))
     ref = orc.varlen_attention(q[perm], k[perm], v[perm], cu, cu, heads, hd, np.float32(scale))
     check(o[perm], ref, what="wide permuted")
+
+
+@pytest.mark.parametrize("permuted", [False, True])
+def test_attention_bf16_short_segment_kernel(px, orc, permuted):
+    """Segments whose mean length selects the short-segment kernel, with
+    lengths on either side of its 64-key chunks and 128-query passes, an
+    empty segment, a single row, and one segment longer than its 512-row
+    staging (read through the row map in global memory)."""
+    lens = (700, 1, 0, 63, 64, 65, 128, 129, 200, 511, 512)
+    heads, hd = 3, 64
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    n, C = int(cu[-1]), heads * hd
+    assert n <= 512 * len(lens)
+    q = W.bf16_round(W.normal(67, n * C, 1).reshape(n, C))
+    k = W.bf16_round(W.normal(67, n * C, 2).reshape(n, C))
+    v = W.bf16_round(W.normal(67, n * C, 3).reshape(n, C))
+    perm = np.random.default_rng(8).permutation(n).astype(np.int32) if permuted else None
+    print(f"[attn short segments] permuted={permuted}", flush=True)
+    o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, 0.125,
+                                 row_map=None if perm is None else ti32(perm)))
+    if perm is None:
+        ref = orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.125))
+        assert_bf16(o, ref, what="short segments")
+    else:
+        ref = orc.varlen_attention(q[perm], k[perm], v[perm], cu, cu, heads, hd, np.float32(0.125))
+        assert_bf16(o[perm], ref, what="short segments permuted")
