@@ -88,6 +88,9 @@ __device__ __forceinline__ int find_segment(const int64_t * __restrict__ tile_st
 #ifndef PXS_ATTN_WINDOW_WAVES
 #define PXS_ATTN_WINDOW_WAVES 4
 #endif
+#ifndef PXS_ATTN_WINDOW_ORDER
+#define PXS_ATTN_WINDOW_ORDER 1  // segments costliest first (one 1024-thread sort launch)
+#endif
 #ifndef PXS_ATTN_WINDOW_HPG
 #define PXS_ATTN_WINDOW_HPG 1  // heads per workgroup; 0 = from the segment count
 #endif
@@ -113,6 +116,7 @@ struct AttnArgs {
     void * o;
     int64_t ldo;
     int vec_ok;
+    const int32_t * seg_order;  // short-segment kernel: segments, costliest first (or null)
 };
 
 template <typename T> struct AttnTraits;
@@ -770,12 +774,14 @@ window_attn_bf16_kernel(AttnArgs a, int heads, int heads_per_group, int groups) 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, r = lane & 31;
-    // Consecutive workgroups land on different XCDs, which spreads the
-    // segments (and the empty ones a window partition's bound appends) evenly;
-    // segments share no rows, so there is no L2 locality to keep.
+    // Workgroups take the segments costliest first (seg_order, when given:
+    // the last to start then are the shortest, which trims the tail);
+    // consecutive workgroups land on different XCDs, and segments share no
+    // rows, so there is no L2 locality to keep.
     const int64_t logical = blockIdx.x;
-    const int seg = static_cast<int>(logical / groups);
-    const int grp = static_cast<int>(logical - static_cast<int64_t>(seg) * groups);
+    const int slot = static_cast<int>(logical / groups);
+    const int grp = static_cast<int>(logical - static_cast<int64_t>(slot) * groups);
+    const int seg = a.seg_order ? a.seg_order[slot] : slot;
     const int head0 = grp * heads_per_group;
     const int nheads = min(heads_per_group, heads - head0);
     const int64_t q0 = a.cu_q[seg], k0 = a.cu_k[seg];
@@ -1064,6 +1070,40 @@ window_attn_bf16_kernel(AttnArgs a, int heads, int heads_per_group, int groups) 
     }
 }
 
+// Segments in the order the short-segment kernel takes them: a counting sort
+// by item count (query passes x key chunks, the same for every head group),
+// costliest class first, empty segments last.  The order within a class is
+// whatever the LDS atomics give; every segment's output rows are its own, so
+// results do not depend on it.
+constexpr int kOrderClasses = 17;
+constexpr int kOrderMaxSegments = 65536;
+__global__ void __launch_bounds__(1024)
+window_order_kernel(const int64_t * __restrict__ cu_q, const int64_t * __restrict__ cu_k, int nseg,
+                    int q_pass, int32_t * __restrict__ order) {
+    __shared__ int next[kOrderClasses];
+    const int tid = threadIdx.x;
+    auto cls = [&](int s) -> int {
+        const int64_t nq = cu_q[s + 1] - cu_q[s], nk = cu_k[s + 1] - cu_k[s];
+        if (nq <= 0) return 0;
+        const int64_t work = ((nq + q_pass - 1) / q_pass) * ((nk + kKeys - 1) / kKeys);
+        return static_cast<int>(min<int64_t>(max<int64_t>(work, 1), kOrderClasses - 1));
+    };
+    if (tid < kOrderClasses) next[tid] = 0;
+    __syncthreads();
+    for (int s = tid; s < nseg; s += 1024) atomicAdd(&next[cls(s)], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int c = kOrderClasses - 1; c >= 0; --c) {
+            const int n = next[c];
+            next[c] = run;
+            run += n;
+        }
+    }
+    __syncthreads();
+    for (int s = tid; s < nseg; s += 1024) order[atomicAdd(&next[cls(s)], 1)] = s;
+}
+
 template <int NW>
 int launch_attn_window(const AttnArgs & args, int heads, hipStream_t stream) {
     // Head groups: enough workgroups to give every CU a few (256 CUs).
@@ -1259,6 +1299,14 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
         a.q = q; a.k = k; a.v = v; a.ldq = ld_q; a.ldk = ld_k; a.ldv = ld_v;
         a.cu_q = cu_q; a.cu_k = cu_k; a.nseg = nseg; a.row_map = row_map;
         a.hd = head_dim; a.vd = value_dim; a.scale_log2 = scale * kLog2e; a.o = o; a.ldo = ld_o;
+        if (PXS_ATTN_WINDOW_ORDER && nseg <= kOrderMaxSegments) {
+            // the workspace's tile list holds the order (nseg entries)
+            int32_t * order = reinterpret_cast<int32_t *>(static_cast<int64_t *>(workspace) + nseg + 1);
+            hipLaunchKernelGGL(window_order_kernel, dim3(1), dim3(1024), 0, s, cu_q, cu_k, nseg,
+                               32 * PXS_ATTN_WINDOW_WAVES, order);
+            if (int rc = check_launch("attention segment order")) return rc;
+            a.seg_order = order;
+        }
         return launch_attn_window<PXS_ATTN_WINDOW_WAVES>(a, heads, s);
     }
     // Waves per workgroup (32 queries each, sharing the K/V tiles).  The bf16

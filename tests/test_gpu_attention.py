@@ -200,3 +200,19 @@ def test_attention_bf16_short_segment_kernel(px, orc, permuted):
     else:
         ref = orc.varlen_attention(q[perm], k[perm], v[perm], cu, cu, heads, hd, np.float32(0.125))
         assert_bf16(o[perm], ref, what="short segments permuted")
+
+
+def test_attention_bf16_many_short_segments(px, orc):
+    """More segments than the short-segment kernel sorts by cost (65,536):
+    the unsorted launch, over segments of 0 to 3 rows."""
+    lens = np.random.default_rng(9).integers(0, 4, 70000)
+    heads, hd = 1, 64
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    n, C = int(cu[-1]), heads * hd
+    q = W.bf16_round(W.normal(68, n * C, 1).reshape(n, C))
+    k = W.bf16_round(W.normal(68, n * C, 2).reshape(n, C))
+    v = W.bf16_round(W.normal(68, n * C, 3).reshape(n, C))
+    print(f"[attn many segments] nseg={len(lens)} n={n}", flush=True)
+    o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, 0.125))
+    assert_bf16(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.125)),
+                what="many short segments")
