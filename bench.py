@@ -551,6 +551,12 @@ def swin_64(args, torch, px, W):
     per_op = {k: round(timer.mean_ms(k), 4) for k in ("qkv", "window_attention", "out", "neighbor_map",
                                                       "up_conv", "c2s", "partition_0", "partition_4")}
     up_tf = f_up / (timer.mean_ms("up_conv") * 1e-3) / 1e12
+    # Window attention per shift reads Q, K, V (3C bf16 per row) and the
+    # row map, and writes O (C bf16 per row): about 68 flop per byte here,
+    # below the 312 flop/byte ridge of 2.5 PFLOP/s over 8 TB/s, so HBM bounds it.
+    win_ms = timer.mean_ms("window_attention")
+    win_bytes = n * (3 * C * 2 + C * 2 + 4)
+    win_gbs = win_bytes / (win_ms * 1e-3) / 1e9
     return {"metric": "shifted-window attention + C2S upsample TFLOP/s, bf16",
             "value": round(flops / dt / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4),
             "dtype": "bf16",
@@ -558,7 +564,12 @@ def swin_64(args, torch, px, W):
                                    f"up-conv 768->1536 ({pairs} pairs) + C2S to 128^3",
                        "per_op_ms": per_op,
                        "window_attention_tflops": round(
-                           f_win / len(wl["shifts"]) / (timer.mean_ms("window_attention") * 1e-3) / 1e12, 2)},
+                           f_win / len(wl["shifts"]) / (win_ms * 1e-3) / 1e12, 2),
+                       "window_attention_roofline": {
+                           "bound": "hbm", "achieved": round(win_gbs, 1), "peak": PEAK_HBM_GBS,
+                           "unit": "GB/s", "frac": round(win_gbs / PEAK_HBM_GBS, 4),
+                           "bytes_per_launch": win_bytes,
+                           "flop_per_byte": round(f_win / len(wl["shifts"]) / win_bytes, 1)}},
             "roofline": {"bound": "mfma", "kernel": "up_conv", "achieved": round(up_tf, 2),
                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(up_tf / PEAK_BF16_TFLOPS, 4), "traffic": None}}

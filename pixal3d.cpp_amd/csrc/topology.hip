@@ -610,6 +610,99 @@ __global__ void window_count_kernel(const int4 * __restrict__ coords, int64_t n,
     slot[p] = atomicAdd(counts + wid, 1);
 }
 
+// The same counts with each workgroup's rows aggregated first: an LDS table
+// (open addressing, load <= 1/2) gives every row a rank among the
+// workgroup's rows of its window, and each distinct window then takes one
+// global atomic for all of them, which returns the base of its slots.
+// slot[p] is unique within the window (in no particular order; the stable
+// order comes from window_sort_kernel).  Window ids fit in int32 here.
+constexpr int kWinTable = 2 * kThreads;
+__global__ void __launch_bounds__(kThreads)
+window_count_agg_kernel(const int4 * __restrict__ coords, int64_t n, int window, int shift,
+                        WindowGrid g, int32_t * __restrict__ counts, int32_t * __restrict__ slot) {
+    __shared__ int32_t keys[kWinTable];
+    __shared__ int32_t cnt[kWinTable];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kWinTable; i += kThreads) {
+        keys[i] = -1;
+        cnt[i] = 0;
+    }
+    __syncthreads();
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + tid;
+    int h = 0, local = 0;
+    if (p < n) {
+        const int32_t wid = static_cast<int32_t>(window_id(coords[p], window, shift, g));
+        h = static_cast<int>((static_cast<uint32_t>(wid) * 2654435761u) >> 23) & (kWinTable - 1);
+        for (;;) {
+            const int32_t prev = atomicCAS(&keys[h], -1, wid);
+            if (prev == -1 || prev == wid) break;
+            h = (h + 1) & (kWinTable - 1);
+        }
+        local = atomicAdd(&cnt[h], 1);
+    }
+    __syncthreads();
+    for (int i = tid; i < kWinTable; i += kThreads)
+        if (keys[i] >= 0) cnt[i] = atomicAdd(counts + keys[i], cnt[i]);
+    __syncthreads();
+    if (p < n) slot[p] = cnt[h] + local;
+}
+
+// start (exclusive scan of the counts), cu of the non-empty windows in
+// ascending id, *nwin and cu[nwin .. cap] = n, by one workgroup walking the
+// windows 1024 at a time (used up to kWinOffsetsMax windows).
+constexpr int64_t kWinOffsetsMax = 65536;
+__global__ void __launch_bounds__(1024)
+window_offsets_kernel(const int32_t * __restrict__ counts, int64_t windows, int64_t n, int64_t cap,
+                      int64_t * __restrict__ start, int64_t * __restrict__ cu,
+                      int64_t * __restrict__ nwin) {
+    __shared__ int32_t wave_tot[16][2];
+    __shared__ int64_t carry[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) {
+        carry[0] = 0;
+        carry[1] = 0;
+    }
+    __syncthreads();
+    for (int64_t w0 = 0; w0 < windows; w0 += 1024) {
+        const int64_t w = w0 + tid;
+        const int c = w < windows ? counts[w] : 0;
+        const int f = c > 0 ? 1 : 0;
+        int sc = c, sf = f;  // inclusive wave scans (a chunk's rows are at most n <= INT_MAX)
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int oc = __shfl_up(sc, d, 64), of = __shfl_up(sf, d, 64);
+            if (lane >= d) {
+                sc += oc;
+                sf += of;
+            }
+        }
+        if (lane == 63) {
+            wave_tot[wave][0] = sc;
+            wave_tot[wave][1] = sf;
+        }
+        __syncthreads();
+        int64_t bc = carry[0], bf = carry[1];
+        for (int j = 0; j < wave; ++j) {
+            bc += wave_tot[j][0];
+            bf += wave_tot[j][1];
+        }
+        const int64_t excl_c = bc + sc - c, excl_f = bf + sf - f;
+        if (w < windows) {
+            start[w] = excl_c;
+            if (f) cu[excl_f] = excl_c;
+        }
+        __syncthreads();  // carry and wave_tot read by every thread
+        if (tid == 1023) {
+            carry[0] = excl_c + c;
+            carry[1] = excl_f + f;
+        }
+        __syncthreads();
+    }
+    const int64_t nw = carry[1];
+    if (tid == 0) *nwin = nw;
+    for (int64_t i = nw + tid; i <= cap; i += 1024) cu[i] = n;
+}
+
 __global__ void window_flags_kernel(const int32_t * __restrict__ counts, int64_t windows,
                                     int32_t * __restrict__ flags) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1180,17 +1273,25 @@ int pxs_window_partition(const int32_t * coords, int64_t n, int batch_size, int 
     const int4 * c4 = reinterpret_cast<const int4 *>(coords);
     int rc = fill_i32(counts, windows, 0, s);
     if (rc) return rc;
-    hipLaunchKernelGGL(window_count_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
-                       n, window, shift, g, counts, slot);
-    rc = exclusive_scan_i32(counts, start, windows, nullptr, scan_ws, s);
-    if (rc) return rc;
-    hipLaunchKernelGGL(window_flags_kernel, dim3(grid_for(windows, kThreads)), dim3(kThreads), 0, s,
-                       counts, windows, flags);
-    rc = exclusive_scan_i32(flags, rank, windows, nwin_out, scan_ws, s);
-    if (rc) return rc;
     const int64_t cap = std::min<int64_t>(n, windows);
-    hipLaunchKernelGGL(window_cu_kernel, dim3(grid_for(windows + 1, kThreads)), dim3(kThreads), 0,
-                       s, counts, windows, start, rank, nwin_out, n, cap, cu_seqlens);
+    if (windows <= kWinOffsetsMax) {
+        // aggregated counts, then one workgroup for starts, cu and nwin
+        hipLaunchKernelGGL(window_count_agg_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+                           s, c4, n, window, shift, g, counts, slot);
+        hipLaunchKernelGGL(window_offsets_kernel, dim3(1), dim3(1024), 0, s, counts, windows, n, cap,
+                           start, cu_seqlens, nwin_out);
+    } else {
+        hipLaunchKernelGGL(window_count_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                           c4, n, window, shift, g, counts, slot);
+        rc = exclusive_scan_i32(counts, start, windows, nullptr, scan_ws, s);
+        if (rc) return rc;
+        hipLaunchKernelGGL(window_flags_kernel, dim3(grid_for(windows, kThreads)), dim3(kThreads), 0,
+                           s, counts, windows, flags);
+        rc = exclusive_scan_i32(flags, rank, windows, nwin_out, scan_ws, s);
+        if (rc) return rc;
+        hipLaunchKernelGGL(window_cu_kernel, dim3(grid_for(windows + 1, kThreads)), dim3(kThreads),
+                           0, s, counts, windows, start, rank, nwin_out, n, cap, cu_seqlens);
+    }
     hipLaunchKernelGGL(window_place_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s, c4,
                        n, window, shift, g, start, slot, tmp);
     // At most cap non-empty windows; workgroups past *nwin exit at once.

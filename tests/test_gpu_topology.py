@@ -148,6 +148,22 @@ def test_window_partition_many_windows(px, orc):
     np.testing.assert_array_equal(cu.cpu().numpy(), rcu)
 
 
+@pytest.mark.parametrize("window,shift", [(8, 4), (4, 2)])
+def test_window_partition_unsorted_rows(px, orc, window, shift):
+    """Rows in random order (the stable order then differs from any
+    coordinate order), with few windows (aggregated counts, one-workgroup
+    offsets) and with 71,874 windows (the multi-kernel path)."""
+    coords = W.shell_coords(128, W.UNET_ITEMS, 2)
+    coords = coords[np.random.default_rng(10).permutation(coords.shape[0])]
+    print(f"[window_partition unsorted] window={window} shift={shift}", flush=True)
+    fwd, bwd, cu, nwin = px.window_partition(ti32(coords), 2, (128, 128, 128), window, shift)
+    rfwd, rbwd, rcu = orc.window_partition(coords, (128, 128, 128), window, shift)
+    assert nwin == len(rcu) - 1
+    np.testing.assert_array_equal(fwd.cpu().numpy(), rfwd)
+    np.testing.assert_array_equal(bwd.cpu().numpy(), rbwd)
+    np.testing.assert_array_equal(cu.cpu().numpy(), rcu)
+
+
 def test_window_partition_padded_segments(px, orc):
     """Without reading the window count, cu_seqlens up to min(n, windows) ends
     in empty segments, and attention over that bound equals attention over
