@@ -4,11 +4,12 @@
 Default workload (one "step" = one pass over the batch, inputs resident in HBM):
   unet_stage_128 - batch 2 on a 128^3 grid (61,056 + 101,207 voxels, unions of
   three ellipsoid shells), bf16 features, fp32 accumulation:
-    voxel hash + 3x3x3 neighbor map at 128^3
+    generation-tagged voxel grid insert (with the stride-2 occupancy bits) +
+      3x3x3 neighbor map at 128^3
     SubMConv3d 3^3 128 -> 128
-    stride-2 topology (coarse cells, child map)
+    stride-2 topology (coarse cells, child map, the 64^3 grid)
     SparseConv3d 2^3 s2 128 -> 256
-    voxel hash + neighbor map at 64^3
+    neighbor map at 64^3 over the grid the topology wrote
     SubMConv3d 3^3 256 -> 256
   value = sum over the three convs of (active pairs x Cin x Cout) / step time,
   in voxel-GMAC/s.
@@ -20,9 +21,10 @@ Also reported on the same line:
   attention     - the varlen flash-attention kernel on 12,288 + 20,480
                   tokens, 16 heads x 64 (2.336 TFLOP per call), TFLOP/s and
                   fraction of the bf16 MFMA peak
-  cpu_baseline  - the reference CPU sparse_submanifold_conv3d (compiled from
-                  the reference sources, oracle/_ref) on item 0 of the same
-                  workload at fp32, all host threads, voxel-GMAC/s
+  cpu_baseline  - the same three convs on the host cores at fp32: the
+                  reference's sparse_submanifold_conv3d compiled from its
+                  sources (oracle/_ref, OpenMP) for A and C, the oracle for B,
+                  voxel-GMAC/s
 --workload selects another configuration for profiling (conv_fp32_64,
 attn_block, swin_64, flow_step); their lines are not the headline metric.
 """
@@ -173,9 +175,10 @@ def unet_stage(args, torch, px, W):
     def ws(nbytes):
         return torch.empty(max(int(nbytes), 8), dtype=torch.uint8, device=dev)
 
-    # Buffers sized once.  The voxel grids are generation-tagged: reset once
-    # here, then every step inserts its rows under a new generation, so no
-    # step refills a grid (O(rows) per build, not O(cells)).
+    # Buffers sized once.  The 128^3 voxel grid is generation-tagged: reset
+    # here, then every step inserts its rows under a new generation, so a
+    # step refills it only once per 255 generations (O(rows) per build, not
+    # O(cells)).
     grid1 = px.tagged_grid(2, (128, 128, 128))
     grid2 = ws(lib.pxs_voxel_grid_bytes(2, 64, 64, 64))  # rewritten whole by the s2 topology
     ds_ws = px.s2_tagged_workspace(2, (128, 128, 128))
@@ -201,18 +204,21 @@ def unet_stage(args, torch, px, W):
 
     def step():
         s = S()
-        gen[0] += 1
+        # generations 1..255 between resets: the step after generation 255
+        # refills the grid first (once per 255 steps, inside the timed op)
+        wrap = gen[0] == 255
+        gen[0] = gen[0] % 255 + 1
         g = C.c_uint32(gen[0])
-        timer.run("neighbor_map_128", lambda: (
-            chk(lib.pxs_voxel_grid_tagged_insert(P(coords), n, 2, 128, 128, 128, P(grid1), g, s),
-                "grid"),
-            chk(lib.pxs_neighbor_map_k3_grid_tagged(P(coords), n, 2, 128, 128, 128, P(grid1), g,
-                                                    P(nbr1), P(mask1), s), "map")))
+        # grid insert, 128^3 neighbour map and the stride-2 topology (which
+        # also writes the 64^3 grid) in three launches
+        timer.run("topology_128", lambda: (
+            chk(lib.pxs_voxel_grid_tagged_reset(P(grid1), 2, 128, 128, 128, s), "reset")
+            if wrap else None,
+            chk(lib.pxs_map_s2_topology_tagged(
+                P(coords), n, 2, 128, 128, 128, P(grid1), g, P(nbr1), P(mask1), P(oc), P(child), n,
+                P(m_dev), P(grid2), P(ds_ws), s), "topology")))
         timer.run("subm_conv_a", lambda: chk(lib.pxs_subm_conv3d(
             1, P(x), n, 128, P(w_a), P(b_a), 128, P(nbr1), P(mask1), P(y_a), s), "conv a"))
-        timer.run("downsample_s2", lambda: chk(lib.pxs_downsample_s2_topology_tagged(
-            P(coords), n, 2, 128, 128, 128, P(grid1), g, P(oc), P(child), n, P(m_dev), P(grid2),
-            P(ds_ws), s), "ds"))
         timer.run("sparse_conv_b", lambda: chk(lib.pxs_sparse_conv3d_s2(
             1, P(y_a), n, 128, P(w_b), P(b_b), 256, P(child), n, m, P(y_b), s), "conv b"))
         timer.run("neighbor_map_64", lambda: chk(lib.pxs_neighbor_map_k3_grid(
@@ -220,8 +226,7 @@ def unet_stage(args, torch, px, W):
         timer.run("subm_conv_c", lambda: chk(lib.pxs_subm_conv3d(
             1, P(y_b), m, 256, P(w_c), P(b_c), 256, P(nbr2), P(mask2), P(y_c), s), "conv c"))
 
-    ops = ("neighbor_map_128", "subm_conv_a", "downsample_s2", "sparse_conv_b",
-           "neighbor_map_64", "subm_conv_c")
+    ops = ("topology_128", "subm_conv_a", "sparse_conv_b", "neighbor_map_64", "subm_conv_c")
     timer.only = set()
     warm = warm_up(args, torch, step)
     # Active pair counts (algorithmic work) from the neighbor masks.
@@ -255,13 +260,15 @@ def unet_stage(args, torch, px, W):
     per_op = {k: {"ms": round(kern[k], 4),
                   "voxel_gmacs": round(macs[k] / (kern[k] * 1e-3) / 1e9, 1),
                   "tflops": round(2 * macs[k] / (kern[k] * 1e-3) / 1e12, 2)} for k in macs}
-    # Map kernels are HBM-bound: coords in (16 B/row, read twice), one 8-byte
-    # tagged cell written per row, 27 int32 + a mask out per row (the 27 cell
-    # reads per row hit cache lines shared with neighbouring rows).
-    map_bytes = n * (2 * 16 + 8 + 27 * 4 + 4)
-    per_op["neighbor_map_128"] = {"ms": round(kern["neighbor_map_128"], 4),
-                              "gbs": round(map_bytes / (kern["neighbor_map_128"] * 1e-3) / 1e9, 1)}
-    per_op["downsample_s2"] = {"ms": round(kern["downsample_s2"], 4)}
+    # The topology is HBM-bound: per fine row the coordinates (16 B, read
+    # twice), one 4-byte tagged cell written, 27 int32 + a mask out (the 27
+    # cell reads per row hit cache lines shared with neighbouring rows); per
+    # coarse cell one int32 of the 64^3 grid, per coarse row its coordinate
+    # and 8 child slots.
+    cells_64 = 2 * 64 * 64 * 64
+    topo_bytes = n * (2 * 16 + 4 + 27 * 4 + 4) + cells_64 * 4 + m * (16 + 8 * 4)
+    per_op["topology_128"] = {"ms": round(kern["topology_128"], 4),
+                              "gbs": round(topo_bytes / (kern["topology_128"] * 1e-3) / 1e9, 1)}
     per_op["neighbor_map_64"] = {"ms": round(kern["neighbor_map_64"], 4)}
     result = {
         "metric": "SubMConv3d voxel-GMAC/s & sparse-attn TFLOP/s vs roofline, 1 MI355X",
@@ -270,8 +277,8 @@ def unet_stage(args, torch, px, W):
         "ms_per_step": round(ms, 4),
         "dtype": "bf16",
         "config": {"workload": "unet_stage_128: batch 2 on 128^3 (61,056 + 101,207 voxels, "
-                               "3 ellipsoid shells each); tagged voxel grid + neighbour map, "
-                               "SubMConv3d 128->128, s2 topology (+ 64^3 grid), SparseConv3d "
+                               "3 ellipsoid shells each); tagged voxel grid, neighbour map and "
+                               "s2 topology (+ 64^3 grid), SubMConv3d 128->128, SparseConv3d "
                                "128->256, map at 64^3, SubMConv3d 256->256",
                    "voxels": n, "voxels_64": m, "pairs_a": pa, "pairs_c": pc,
                    "warmup_steps_run": warm,

@@ -125,16 +125,17 @@ int pxs_neighbor_map_k3_grid(const int32_t * coords, int64_t n, int batch_size, 
                              int sz, const void * grid, int32_t * nbr, uint32_t * masks,
                              void * stream);
 
-/* Generation-tagged voxel grid: one uint64 cell per (b, x, y, z) of the
- * extents (twice pxs_voxel_grid_bytes), holding ~generation in its high word
- * and a row in its low word.  It is reset (all ones) once per allocation;
- * after that every insert takes a generation larger than any earlier one
- * since the reset, and lookups with that generation see only its rows, so the
- * grid is never refilled: a build costs O(rows) instead of O(cells).  Within
- * a generation the smallest row of a coordinate wins, as in
- * pxs_voxel_grid_build.  Generation 0 is the reset state and is rejected.
- * A replacement, for hot loops that rebuild maps over fixed extents, of the
- * per-build std::unordered_map of src/slat_decoder.cpp:630-635. */
+/* Generation-tagged voxel grid: one 32-bit cell per (b, x, y, z) of the
+ * extents (pxs_voxel_grid_bytes), holding 255 - generation in its top 8 bits
+ * and a row (below 2^24) in its low 24.  After a reset (all ones) each insert
+ * takes a generation in 1..255 larger than any used since that reset, and
+ * lookups with that generation see only its rows, so the grid is refilled
+ * once per 255 builds, not per build: a build costs O(rows) instead of
+ * O(cells).  Within a generation the smallest row of a coordinate wins, as in
+ * pxs_voxel_grid_build.  Generations outside 1..255 and more than 2^24 - 1
+ * rows are rejected.  A replacement, for hot loops that rebuild maps over
+ * fixed extents, of the per-build std::unordered_map of
+ * src/slat_decoder.cpp:630-635. */
 size_t pxs_voxel_grid_tagged_bytes(int batch_size, int sx, int sy, int sz);
 int pxs_voxel_grid_tagged_reset(void * grid, int batch_size, int sx, int sy, int sz,
                                 void * stream);
@@ -196,6 +197,7 @@ int pxs_downsample_s2_topology(const int32_t * coords, int64_t n, int batch_size
  * which must be zero before the first call
  * (pxs_downsample_s2_tagged_workspace_reset) and which every call leaves zero. */
 size_t pxs_downsample_s2_tagged_workspace_bytes(int batch_size, int sx, int sy, int sz);
+
 int pxs_downsample_s2_tagged_workspace_reset(void * workspace, int batch_size, int sx, int sy,
                                              int sz, void * stream);
 int pxs_downsample_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size, int sx,
@@ -203,6 +205,17 @@ int pxs_downsample_s2_topology_tagged(const int32_t * coords, int64_t n, int bat
                                       uint32_t fine_generation, int32_t * out_coords,
                                       int32_t * child_map, int64_t ld_map, int64_t * m_out,
                                       void * coarse_grid, void * workspace, void * stream);
+/* One level of a U-Net's topology in three launches: pxs_voxel_grid_tagged_insert
+ * of coords under generation (which also marks each row's stride-2 cell in
+ * the occupancy bitmap of s2_workspace), pxs_neighbor_map_k3_grid_tagged (nbr,
+ * masks; its launch also scans the bitmap) and the emit of
+ * pxs_downsample_s2_topology_tagged (out_coords, child_map, *m_out,
+ * coarse_grid).  Outputs identical to those three calls; the same limits. */
+int pxs_map_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                               int sz, void * grid, uint32_t generation, int32_t * nbr,
+                               uint32_t * masks, int32_t * out_coords, int32_t * child_map,
+                               int64_t ld_map, int64_t * m_out, void * coarse_grid,
+                               void * s2_workspace, void * stream);
 
 /* The same topology for any factor f, as groups: output q (coordinates
  * (b, x/f, y/f, z/f), lexicographic) gathers input rows

@@ -259,25 +259,31 @@ neighbor_map_grid_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g
 }
 
 // ---- generation-tagged voxel grid ---------------------------------------------
-// One uint64 cell per (b, x, y, z): the high word holds ~generation, the low
-// word the row.  A cell belongs to the current build only when its high word
-// is ~generation, so the grid is never refilled: a reset (all ones) once per
-// allocation, then every build passes a larger generation and old entries
-// simply stop matching.  Insertion is an atomicMin, so within a generation the
-// smallest row wins (a newer generation has a smaller ~generation and always
-// replaces an older entry).
-__device__ __forceinline__ unsigned long long tag_cell(uint32_t generation, uint32_t row) {
-    return (static_cast<unsigned long long>(~generation) << 32) | row;
+// One 32-bit cell per (b, x, y, z): the top 8 bits hold 255 - generation
+// (generations 1 .. 255), the low 24 the row.  A cell belongs to the current
+// build only when its tag matches, so the grid is not refilled per build: a
+// reset (all ones, the tag of generation 0) once per 255 generations, and
+// between resets every build passes a larger generation, so old entries stop
+// matching.  Insertion is an atomicMin: within a generation the smallest row
+// wins, and a newer generation has a smaller tag and always replaces an
+// older entry.  Same cell size as the plain grid, so a map's lookups move the
+// same bytes as pxs_neighbor_map_k3_grid.
+constexpr uint32_t kTagRowBits = 24;
+constexpr uint32_t kTagMaxGeneration = 255;
+constexpr int64_t kTagMaxRows = (int64_t{1} << kTagRowBits) - 1;
+
+__device__ __forceinline__ uint32_t tag_cell(uint32_t generation, uint32_t row) {
+    return ((kTagMaxGeneration - generation) << kTagRowBits) | row;
 }
 
-__device__ __forceinline__ int32_t tag_lookup(unsigned long long cell, uint32_t generation) {
-    return static_cast<uint32_t>(cell >> 32) == ~generation ? static_cast<int32_t>(cell)
-                                                            : kGridEmpty;
+__device__ __forceinline__ int32_t tag_lookup(uint32_t cell, uint32_t generation) {
+    return (cell >> kTagRowBits) == kTagMaxGeneration - generation
+               ? static_cast<int32_t>(cell & ((1u << kTagRowBits) - 1u))
+               : kGridEmpty;
 }
 
 __global__ void tagged_scatter_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
-                                      unsigned long long * __restrict__ grid,
-                                      uint32_t generation) {
+                                      uint32_t * __restrict__ grid, uint32_t generation) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= n) return;
     const int4 c = coords[p];
@@ -288,11 +294,11 @@ __global__ void tagged_scatter_kernel(const int4 * __restrict__ coords, int64_t 
 }
 
 // neighbor_map_grid_kernel over a tagged grid: the same map and masks.
-__global__ void __launch_bounds__(kThreads)
-neighbor_map_tagged_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
-                           const unsigned long long * __restrict__ grid, uint32_t generation,
-                           int32_t * __restrict__ nbr, uint32_t * __restrict__ masks) {
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void map_row_tagged(int64_t p, const int4 * __restrict__ coords,
+                                               int64_t n, GridDims g,
+                                               const uint32_t * __restrict__ grid,
+                                               uint32_t generation, int32_t * __restrict__ nbr,
+                                               uint32_t * __restrict__ masks) {
     if (p >= n) return;
     const int4 c = coords[p];
     int32_t row[27];
@@ -312,6 +318,14 @@ neighbor_map_tagged_kernel(const int4 * __restrict__ coords, int64_t n, GridDims
         nbr[static_cast<int64_t>(k) * n + p] = hit ? row[k] : static_cast<int32_t>(n);
     }
     if (masks) masks[p] = present;
+}
+
+__global__ void __launch_bounds__(kThreads)
+neighbor_map_tagged_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
+                           const uint32_t * __restrict__ grid, uint32_t generation,
+                           int32_t * __restrict__ nbr, uint32_t * __restrict__ masks) {
+    map_row_tagged(static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x, coords, n, g, grid,
+                   generation, nbr, masks);
 }
 
 template <typename T>
@@ -386,7 +400,22 @@ __device__ __forceinline__ int64_t coarse_cell(int4 c, int f, int cx, int cy, in
 // Rows that share a bitmap word (the f^3 children of a cell and their
 // neighbours along z) are merged inside the wavefront first: one atomic per
 // distinct word instead of one per row.  Sorted input gives a handful of
-// words per wavefront.
+// words per wavefront.  Called by every lane of the wavefront.
+__device__ __forceinline__ void mark_bits(bool live, int64_t word, uint32_t bit,
+                                          uint32_t * __restrict__ bitmap) {
+    uint64_t pending = __ballot(live);
+    while (pending) {
+        const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+        const int64_t w0 = __shfl(word, leader, 64);
+        const bool mine = live && word == w0;
+        uint32_t v = mine ? bit : 0u;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) v |= __shfl_xor(v, d, 64);
+        if ((threadIdx.x & 63) == leader) atomicOr(bitmap + w0, v);
+        pending &= ~__ballot(mine);
+    }
+}
+
 // It also sets clear[k * n + p] = value for k < clear_rows (the child map or
 // the group counts the next kernels fill in), saving a fill launch.
 __global__ void coarse_mark_kernel(const int4 * __restrict__ coords, int64_t n, int f, int cx,
@@ -407,17 +436,32 @@ __global__ void coarse_mark_kernel(const int4 * __restrict__ coords, int64_t n, 
         word = live ? cell >> 5 : -1;
         bit = 1u << (cell & 31);
     }
-    uint64_t pending = __ballot(live);
-    while (pending) {
-        const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
-        const int64_t w0 = __shfl(word, leader, 64);
-        const bool mine = live && word == w0;
-        uint32_t v = mine ? bit : 0u;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) v |= __shfl_xor(v, d, 64);
-        if ((threadIdx.x & 63) == leader) atomicOr(bitmap + w0, v);
-        pending &= ~__ballot(mine);
+    mark_bits(live, word, bit, bitmap);
+}
+
+// pxs_voxel_grid_tagged_insert that also marks each row's stride-2 cell in
+// the occupancy bitmap (coarse_mark_kernel's work for factor 2), in the same
+// pass over the coordinates.
+__global__ void tagged_scatter_mark_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
+                                           uint32_t * __restrict__ grid, uint32_t generation,
+                                           int cx, int cy, int cz, int64_t words,
+                                           uint32_t * __restrict__ bitmap) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    bool live = p < n;
+    int64_t word = -1;
+    uint32_t bit = 0;
+    if (live) {
+        const int4 c = coords[p];
+        if (grid_inside(g, c.x, c.y, c.z, c.w)) {
+            atomicMin(grid + grid_cell(g, c.x, c.y, c.z, c.w),
+                      tag_cell(generation, static_cast<uint32_t>(p)));
+        }
+        const int64_t cell = coarse_cell(c, 2, cx, cy, cz);
+        live = c.x >= 0 && c.y >= 0 && c.z >= 0 && c.w >= 0 && cell >= 0 && (cell >> 5) < words;
+        word = live ? cell >> 5 : -1;
+        bit = 1u << (cell & 31);
     }
+    mark_bits(live, word, bit, bitmap);
 }
 
 __device__ __forceinline__ int64_t coarse_rank(int64_t cell, const uint32_t * __restrict__ bitmap,
@@ -448,12 +492,12 @@ __global__ void coarse_emit_kernel(const int4 * __restrict__ coords, int64_t n, 
 // dozen totals per block of words).
 constexpr int kWordBlock = 1024;
 
-__global__ void __launch_bounds__(kThreads)
-word_block_scan_kernel(const uint32_t * __restrict__ bitmap, int64_t words,
-                       int32_t * __restrict__ local_prefix, int32_t * __restrict__ block_totals) {
+__device__ __forceinline__ void word_block_scan(int64_t block, const uint32_t * __restrict__ bitmap,
+                                                int64_t words, int32_t * __restrict__ local_prefix,
+                                                int32_t * __restrict__ block_totals) {
     constexpr int kPer = kWordBlock / kThreads;  // 4 words per thread
     __shared__ int32_t wave_sums[kThreads / 64];
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kWordBlock;
+    const int64_t base = block * kWordBlock;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     int32_t cnt[kPer];
     int32_t mine = 0;
@@ -479,7 +523,31 @@ word_block_scan_kernel(const uint32_t * __restrict__ bitmap, int64_t words,
         if (w < words) local_prefix[w] = before;
         before += cnt[j];
     }
-    if (t == kThreads - 1) block_totals[blockIdx.x] = before;
+    if (t == kThreads - 1) block_totals[block] = before;
+}
+
+__global__ void __launch_bounds__(kThreads)
+word_block_scan_kernel(const uint32_t * __restrict__ bitmap, int64_t words,
+                       int32_t * __restrict__ local_prefix, int32_t * __restrict__ block_totals) {
+    word_block_scan(blockIdx.x, bitmap, words, local_prefix, block_totals);
+}
+
+// The fine neighbour map and the blocked scan of the stride-2 occupancy
+// counts in one launch: both need only the insert's results, so workgroups
+// [0, map_blocks) map rows and the rest scan bitmap blocks.
+__global__ void __launch_bounds__(kThreads)
+map_tagged_and_scan_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g,
+                           const uint32_t * __restrict__ grid, uint32_t generation,
+                           int32_t * __restrict__ nbr, uint32_t * __restrict__ masks,
+                           int64_t map_blocks, const uint32_t * __restrict__ bitmap, int64_t words,
+                           int32_t * __restrict__ local_prefix,
+                           int32_t * __restrict__ block_totals) {
+    const int64_t b = blockIdx.x;
+    if (b < map_blocks) {
+        map_row_tagged(b * kThreads + threadIdx.x, coords, n, g, grid, generation, nbr, masks);
+    } else {
+        word_block_scan(b - map_blocks, bitmap, words, local_prefix, block_totals);
+    }
 }
 
 // One thread per coarse cell (32 per bitmap word).  Every cell writes its
@@ -493,7 +561,7 @@ __global__ void __launch_bounds__(kThreads)
 coarse_emit_grid_kernel(uint32_t * __restrict__ bitmap, int64_t words, int64_t cells,
                         const int32_t * __restrict__ local_prefix,
                         const int32_t * __restrict__ block_totals, int nblocks, GridDims fine,
-                        GridDims coarse, const unsigned long long * __restrict__ fine_grid,
+                        GridDims coarse, const uint32_t * __restrict__ fine_grid,
                         uint32_t fine_gen, int32_t * __restrict__ coarse_grid,
                         int4 * __restrict__ out_coords, int32_t * __restrict__ child_map,
                         int64_t ld_map, int64_t * m_out) {
@@ -972,7 +1040,7 @@ int pxs_neighbor_map_k3_grid(const int32_t * coords, int64_t n, int batch_size, 
 }
 
 size_t pxs_voxel_grid_tagged_bytes(int batch_size, int sx, int sy, int sz) {
-    return 2 * pxs_voxel_grid_bytes(batch_size, sx, sy, sz);
+    return pxs_voxel_grid_bytes(batch_size, sx, sy, sz);
 }
 
 int pxs_voxel_grid_tagged_reset(void * grid, int batch_size, int sx, int sy, int sz,
@@ -980,45 +1048,45 @@ int pxs_voxel_grid_tagged_reset(void * grid, int batch_size, int sx, int sy, int
     const size_t bytes = pxs_voxel_grid_tagged_bytes(batch_size, sx, sy, sz);
     PXS_CHECK(bytes > 0, PXS_ERR_ARG, "pxs_voxel_grid_tagged_reset: invalid extents");
     PXS_CHECK(grid, PXS_ERR_ARG, "pxs_voxel_grid_tagged_reset: null pointer");
-    const int64_t cells = static_cast<int64_t>(bytes / 8);
+    const int64_t cells = static_cast<int64_t>(bytes / 4);
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((cells + kThreads - 1) / kThreads, 16384));
-    hipLaunchKernelGGL(fill_value_kernel<unsigned long long>, dim3(blocks), dim3(kThreads), 0,
-                       as_stream(stream), static_cast<unsigned long long *>(grid), cells,
-                       ~0ull);
+    hipLaunchKernelGGL(fill_value_kernel<uint32_t>, dim3(blocks), dim3(kThreads), 0,
+                       as_stream(stream), static_cast<uint32_t *>(grid), cells, ~0u);
     return check_launch("pxs_voxel_grid_tagged_reset");
 }
 
 int pxs_voxel_grid_tagged_insert(const int32_t * coords, int64_t n, int batch_size, int sx,
                                  int sy, int sz, void * grid, uint32_t generation, void * stream) {
-    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_voxel_grid_tagged_insert: bad row count");
+    PXS_CHECK(n >= 0 && n <= kTagMaxRows, PXS_ERR_ARG,
+              "pxs_voxel_grid_tagged_insert: bad row count (at most 2^24 - 1 rows)");
     PXS_CHECK(pxs_voxel_grid_tagged_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
               "pxs_voxel_grid_tagged_insert: invalid extents");
-    PXS_CHECK(generation != 0, PXS_ERR_ARG,
-              "pxs_voxel_grid_tagged_insert: generation 0 is the reset state");
+    PXS_CHECK(generation >= 1 && generation <= kTagMaxGeneration, PXS_ERR_ARG,
+              "pxs_voxel_grid_tagged_insert: generation must be in 1..255");
     if (n == 0) return PXS_OK;
     PXS_CHECK(grid && coords, PXS_ERR_ARG, "pxs_voxel_grid_tagged_insert: null pointer");
     hipLaunchKernelGGL(tagged_scatter_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
                        as_stream(stream), reinterpret_cast<const int4 *>(coords), n,
-                       GridDims{batch_size, sx, sy, sz},
-                       static_cast<unsigned long long *>(grid), generation);
+                       GridDims{batch_size, sx, sy, sz}, static_cast<uint32_t *>(grid),
+                       generation);
     return check_launch("pxs_voxel_grid_tagged_insert");
 }
 
 int pxs_neighbor_map_k3_grid_tagged(const int32_t * coords, int64_t n, int batch_size, int sx,
                                     int sy, int sz, const void * grid, uint32_t generation,
                                     int32_t * nbr, uint32_t * masks, void * stream) {
-    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG,
-              "pxs_neighbor_map_k3_grid_tagged: bad row count");
+    PXS_CHECK(n >= 0 && n <= kTagMaxRows, PXS_ERR_ARG,
+              "pxs_neighbor_map_k3_grid_tagged: bad row count (at most 2^24 - 1 rows)");
     PXS_CHECK(pxs_voxel_grid_tagged_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
               "pxs_neighbor_map_k3_grid_tagged: invalid extents");
-    PXS_CHECK(generation != 0, PXS_ERR_ARG,
-              "pxs_neighbor_map_k3_grid_tagged: generation 0 is the reset state");
+    PXS_CHECK(generation >= 1 && generation <= kTagMaxGeneration, PXS_ERR_ARG,
+              "pxs_neighbor_map_k3_grid_tagged: generation must be in 1..255");
     if (n == 0) return PXS_OK;
     PXS_CHECK(coords && grid && nbr, PXS_ERR_ARG, "pxs_neighbor_map_k3_grid_tagged: null pointer");
     hipLaunchKernelGGL(neighbor_map_tagged_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
                        as_stream(stream), reinterpret_cast<const int4 *>(coords), n,
                        GridDims{batch_size, sx, sy, sz},
-                       static_cast<const unsigned long long *>(grid), generation, nbr, masks);
+                       static_cast<const uint32_t *>(grid), generation, nbr, masks);
     return check_launch("pxs_neighbor_map_k3_grid_tagged");
 }
 
@@ -1144,12 +1212,12 @@ int pxs_downsample_s2_topology_tagged(const int32_t * coords, int64_t n, int bat
                                       int32_t * child_map, int64_t ld_map, int64_t * m_out,
                                       void * coarse_grid, void * workspace, void * stream) {
     PXS_CHECK_WORKSPACE(workspace, "pxs_downsample_s2_topology_tagged");
-    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG,
-              "pxs_downsample_s2_topology_tagged: bad row count");
+    PXS_CHECK(n >= 0 && n <= kTagMaxRows, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology_tagged: bad row count (at most 2^24 - 1 rows)");
     PXS_CHECK(pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
               "pxs_downsample_s2_topology_tagged: invalid shape");
-    PXS_CHECK(fine_generation != 0, PXS_ERR_ARG,
-              "pxs_downsample_s2_topology_tagged: generation 0 is the reset state");
+    PXS_CHECK(fine_generation >= 1 && fine_generation <= kTagMaxGeneration, PXS_ERR_ARG,
+              "pxs_downsample_s2_topology_tagged: generation must be in 1..255");
     PXS_CHECK(ld_map >= n, PXS_ERR_ARG,
               "pxs_downsample_s2_topology_tagged: child map stride below the row count");
     PXS_CHECK(m_out && workspace, PXS_ERR_ARG, "pxs_downsample_s2_topology_tagged: null pointer");
@@ -1175,10 +1243,56 @@ int pxs_downsample_s2_topology_tagged(const int32_t * coords, int64_t n, int bat
     hipLaunchKernelGGL(coarse_emit_grid_kernel, dim3(grid_for(words * 32, kThreads)), dim3(kThreads), 0,
                        s, bitmap, words, cells, local_prefix, totals, static_cast<int>(blocks),
                        GridDims{batch_size, sx, sy, sz}, GridDims{batch_size, cx, cy, cz},
-                       static_cast<const unsigned long long *>(fine_grid), fine_generation,
+                       static_cast<const uint32_t *>(fine_grid), fine_generation,
                        static_cast<int32_t *>(coarse_grid), reinterpret_cast<int4 *>(out_coords),
                        child_map, ld_map, m_out);
     return check_launch("pxs_downsample_s2_topology_tagged");
+}
+
+int pxs_map_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
+                               int sz, void * grid, uint32_t generation, int32_t * nbr,
+                               uint32_t * masks, int32_t * out_coords, int32_t * child_map,
+                               int64_t ld_map, int64_t * m_out, void * coarse_grid,
+                               void * s2_workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(s2_workspace, "pxs_map_s2_topology_tagged");
+    PXS_CHECK(n >= 0 && n <= kTagMaxRows, PXS_ERR_ARG,
+              "pxs_map_s2_topology_tagged: bad row count (at most 2^24 - 1 rows)");
+    PXS_CHECK(pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              "pxs_map_s2_topology_tagged: invalid extents");
+    PXS_CHECK(generation >= 1 && generation <= kTagMaxGeneration, PXS_ERR_ARG,
+              "pxs_map_s2_topology_tagged: generation must be in 1..255");
+    PXS_CHECK(ld_map >= n, PXS_ERR_ARG,
+              "pxs_map_s2_topology_tagged: child map stride below the row count");
+    PXS_CHECK(m_out && s2_workspace, PXS_ERR_ARG, "pxs_map_s2_topology_tagged: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) return fill_i64(m_out, 1, 0, s);
+    PXS_CHECK(coords && grid && nbr && out_coords && child_map && coarse_grid, PXS_ERR_ARG,
+              "pxs_map_s2_topology_tagged: null pointer");
+    const int cx = (sx + 1) / 2, cy = (sy + 1) / 2, cz = (sz + 1) / 2;
+    const int64_t cells = static_cast<int64_t>(batch_size) * cx * cy * cz;
+    const int64_t words = (cells + 31) / 32;
+    const int64_t blocks = (words + kWordBlock - 1) / kWordBlock;
+    const int64_t map_blocks = (n + kThreads - 1) / kThreads;
+    PXS_CHECK(blocks + map_blocks <= INT_MAX, PXS_ERR_ARG, "pxs_map_s2_topology_tagged: grid too large");
+    char * ws = static_cast<char *>(s2_workspace);
+    auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
+    uint32_t * bitmap = reinterpret_cast<uint32_t *>(ws);
+    int32_t * local_prefix = reinterpret_cast<int32_t *>(ws + up(words * 4));
+    int32_t * totals = reinterpret_cast<int32_t *>(ws + 2 * up(words * 4));
+    const GridDims fine{batch_size, sx, sy, sz};
+    const int4 * c4 = reinterpret_cast<const int4 *>(coords);
+    hipLaunchKernelGGL(tagged_scatter_mark_kernel, dim3(static_cast<unsigned>(map_blocks)),
+                       dim3(kThreads), 0, s, c4, n, fine, static_cast<uint32_t *>(grid), generation,
+                       cx, cy, cz, words, bitmap);
+    hipLaunchKernelGGL(map_tagged_and_scan_kernel, dim3(static_cast<unsigned>(map_blocks + blocks)),
+                       dim3(kThreads), 0, s, c4, n, fine, static_cast<const uint32_t *>(grid),
+                       generation, nbr, masks, map_blocks, bitmap, words, local_prefix, totals);
+    hipLaunchKernelGGL(coarse_emit_grid_kernel, dim3(grid_for(words * 32, kThreads)), dim3(kThreads), 0,
+                       s, bitmap, words, cells, local_prefix, totals, static_cast<int>(blocks), fine,
+                       GridDims{batch_size, cx, cy, cz}, static_cast<const uint32_t *>(grid),
+                       generation, static_cast<int32_t *>(coarse_grid),
+                       reinterpret_cast<int4 *>(out_coords), child_map, ld_map, m_out);
+    return check_launch("pxs_map_s2_topology_tagged");
 }
 
 int pxs_downsample_topology(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,

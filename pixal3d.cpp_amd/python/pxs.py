@@ -111,6 +111,8 @@ _SIGS = {
     "pxs_downsample_s2_tagged_workspace_reset": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "pxs_downsample_s2_topology_tagged": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp,
                                                  C.c_uint32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "pxs_map_s2_topology_tagged": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, C.c_uint32,
+                                          _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "pxs_voxel_grid_build": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
     "pxs_neighbor_map_k3_grid": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "pxs_convnext_block_workspace_bytes": (C.c_size_t, [_i32, _i64, _i32, _i32, _i32]),
@@ -346,6 +348,27 @@ class Pxs:
                                                           batch_size, *shape, _ptr(grid),
                                                           generation, self.stream()),
                     "pxs_voxel_grid_tagged_insert")
+
+    def map_s2_tagged(self, coords, batch_size, shape, grid, generation, coarse_grid, workspace,
+                      sync=True):
+        """pxs_map_s2_topology_tagged -> (nbr [27, n], masks [n], out_coords,
+        child_map [8, n], m); m is the host count when sync (else the device
+        int64)."""
+        n = coords.shape[0]
+        dev = coords.device
+        nbr = torch.empty((27, max(n, 1)), dtype=torch.int32, device=dev)
+        masks = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+        oc = torch.empty((max(n, 1), 4), dtype=torch.int32, device=dev)
+        child = torch.empty((8, max(n, 1)), dtype=torch.int32, device=dev)
+        m = torch.empty(1, dtype=torch.int64, device=dev)
+        self._check(self.lib.pxs_map_s2_topology_tagged(
+            _ptr(coords), n, batch_size, *shape, _ptr(grid), generation, _ptr(nbr), _ptr(masks),
+            _ptr(oc), _ptr(child), child.shape[1], _ptr(m), _ptr(coarse_grid), _ptr(workspace),
+            self.stream()), "pxs_map_s2_topology_tagged")
+        if not sync:
+            return nbr[:, :n], masks[:n], oc, child, m
+        mm = int(m.item())
+        return nbr[:, :n], masks[:n], oc[:mm], child, mm
 
     def neighbor_map_tagged(self, coords, batch_size, shape, grid, generation):
         n = coords.shape[0]

@@ -58,6 +58,20 @@ def downsample_topologies(px):
 
 
 @case
+def tagged_grid_topology(px):
+    c = empty((0, 4), torch.int32)
+    grid = px.tagged_grid(1, (8, 8, 8))
+    px.tagged_insert(c, 1, (8, 8, 8), grid, 1)
+    nbr, _ = px.neighbor_map_tagged(c, 1, (8, 8, 8), grid, 1)
+    assert nbr.shape == (27, 0)
+    coarse = empty((px.lib.pxs_voxel_grid_bytes(1, 4, 4, 4) // 4,), torch.int32)
+    ws = px.s2_tagged_workspace(1, (8, 8, 8))
+    assert px.downsample_s2_tagged(c, 1, (8, 8, 8), grid, 1, coarse, ws)[-1] == 0
+    nbr, _, _, _, m = px.map_s2_tagged(c, 1, (8, 8, 8), grid, 1, coarse, ws)
+    assert m == 0 and nbr.shape == (27, 0)
+
+
+@case
 def window_partition(px):
     res = px.window_partition(empty((0, 4), torch.int32), 1, (16, 16, 16), 8, 4)
     assert res is not None

@@ -309,13 +309,45 @@ def test_tagged_grid_map_across_generations(px, orc):
         np.testing.assert_array_equal(masks.cpu().numpy().astype(np.int64) & 0x7FFFFFF, ref_masks)
 
 
+def test_tagged_grid_generation_cycle(px, orc):
+    """Generations 254 and 255, a reset, then 1 and 2 again, over different
+    coordinate sets: every map equals the oracle's.  Generations outside
+    1..255 and row counts past 2^24 - 1 are rejected before any launch."""
+    import ctypes as C
+    import pxs
+    shape, batch = (24, 24, 24), 2
+    a = W.shell_coords(24, [[(6.0, 10.0)], [(5.0, 9.0)]], 55)
+    b = W.shell_coords(24, [[(4.0, 7.0)], [(8.0, 11.0)]], 56)
+    grid = px.tagged_grid(batch, shape)
+    for gen, coords, reset in ((254, a, False), (255, b, False), (1, a, True), (2, b, False)):
+        print(f"[tagged cycle] generation={gen} reset={reset} n={coords.shape[0]}", flush=True)
+        if reset:
+            px._check(px.lib.pxs_voxel_grid_tagged_reset(C.c_void_p(grid.data_ptr()), batch,
+                                                         *shape, px.stream()),
+                      "pxs_voxel_grid_tagged_reset")
+        c = ti32(coords)
+        px.tagged_insert(c, batch, shape, grid, gen)
+        nbr, _ = px.neighbor_map_tagged(c, batch, shape, grid, gen)
+        np.testing.assert_array_equal(nbr.cpu().numpy(), orc.neighbor_map(coords))
+    c = ti32(a)
+    for gen in (0, 256):
+        with pytest.raises(pxs.PxsError, match="generation must be in 1..255"):
+            px.tagged_insert(c, batch, shape, grid, gen)
+    rc = px.lib.pxs_voxel_grid_tagged_insert(C.c_void_p(c.data_ptr()), 1 << 24, batch, *shape,
+                                             C.c_void_p(grid.data_ptr()), 3, px.stream())
+    assert rc != 0 and "2^24 - 1" in px.lib.pxs_last_error().decode()
+
+
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("case", ["unet_stage_128", "small_2batch", "single", "odd"])
-def test_downsample_s2_tagged_bit_exact(px, orc, case):
+def test_downsample_s2_tagged_bit_exact(px, orc, case, fused):
     """The tagged stride-2 topology equals the oracle's (coordinates, count,
     all 8 child slots), the coarse grid it writes gives the oracle's map over
     the output coordinates, and later calls on the same workspace and grids
     with other coordinates are exact too (the occupancy bitmap is left zero,
-    stale fine-grid entries do not match, the coarse grid is rewritten whole)."""
+    stale fine-grid entries do not match, the coarse grid is rewritten whole).
+    fused: insert, fine map and topology by pxs_map_s2_topology_tagged, whose
+    fine map must equal the oracle's too."""
     if case == "odd":
         coords, batch, shape = (W.shell_coords(23, [[(5.0, 9.0)], [(4.0, 8.0)]], 54), 2,
                                 (23, 23, 23))
@@ -328,10 +360,18 @@ def test_downsample_s2_tagged_bit_exact(px, orc, case):
     ws = px.s2_tagged_workspace(batch, shape)
     other = coords[::2].copy()
     for gen, cc in ((1, coords), (2, other), (3, coords)):
-        print(f"[s2 tagged] case={case} generation={gen} n={cc.shape[0]}", flush=True)
+        print(f"[s2 tagged] case={case} fused={fused} generation={gen} n={cc.shape[0]}",
+              flush=True)
         c = ti32(cc)
-        px.tagged_insert(c, batch, shape, fine, gen)
-        oc, child, m = px.downsample_s2_tagged(c, batch, shape, fine, gen, coarse, ws)
+        if fused:
+            fnbr, fmasks, oc, child, m = px.map_s2_tagged(c, batch, shape, fine, gen, coarse, ws)
+            rmap = orc.neighbor_map(cc)
+            np.testing.assert_array_equal(fnbr.cpu().numpy(), rmap)
+            rmask = ((rmap != cc.shape[0]).astype(np.int64) << np.arange(27)[:, None]).sum(0)
+            np.testing.assert_array_equal(fmasks.cpu().numpy().astype(np.int64) & 0x7FFFFFF, rmask)
+        else:
+            px.tagged_insert(c, batch, shape, fine, gen)
+            oc, child, m = px.downsample_s2_tagged(c, batch, shape, fine, gen, coarse, ws)
         roc, rchild = orc.downsample_coords_s2(cc)
         assert m == roc.shape[0]
         np.testing.assert_array_equal(oc.cpu().numpy(), roc)
