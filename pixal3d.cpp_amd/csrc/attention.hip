@@ -392,6 +392,42 @@ __device__ __forceinline__ float lane_pair_sum(float v) {
 constexpr int kAttnStages = 4;
 // Raise the wave's issue priority while it queues a tile's MFMAs, so the
 // SIMD's other wave fills the matrix core's shadow with its VALU softmax.
+// Instruction interleave of one steady-state step (PV of the previous tile,
+// QK of the next, this tile's exponentials): 0 leaves it to the compiler,
+// 1..3 impose MFMA/VALU/LDS-read groups with sched_group_barrier.
+#ifndef PXS_ATTN_SCHED
+#define PXS_ATTN_SCHED 0
+#endif
+__device__ __forceinline__ void attn_step_schedule() {
+    // masks: 0x008 MFMA, 0x002 VALU, 0x100 LDS read
+#if PXS_ATTN_SCHED == 1
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+#elif PXS_ATTN_SCHED == 2
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+#elif PXS_ATTN_SCHED == 3
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+#endif
+}
+
 #ifndef PXS_ATTN_SETPRIO
 #define PXS_ATTN_SETPRIO 0
 #endif
@@ -631,6 +667,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     constexpr float kTileSumLimit = 1099511627776.0f;  // 2^40
     auto softmax_exp_checked = [&](f32x16 (&s)[2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
         float ts = softmax_exp(s, pb);
+        attn_step_schedule();
         if (__builtin_expect(__ballot(!(ts <= kTileSumLimit)) != 0, 0)) {
             const float mx = softmax_max(s, kKeys);
             const float m_new = fmaxf(m_run, mx);
