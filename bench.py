@@ -297,8 +297,7 @@ def unet_stage(args, torch, px, W):
 
 def measured_traffic(op):
     """HBM bytes per launch of `op` from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by the factor
-    the same counter reads for a plain copy of known size), or None when the
+    (reads counted by L2 request size, writes by WRITE_SIZE), or None when the
     summary does not cover this kernel."""
     path = ROOT / "profiles" / "unet_stage_128_traffic.json"
     if not path.exists():
@@ -306,8 +305,7 @@ def measured_traffic(op):
     rec = json.loads(path.read_text()).get(op)
     if not rec:
         return None
-    return int(round((rec["fetch_kib"] * rec["fetch_scale"] + rec["write_kib"] * rec["write_scale"])
-                     * 1024))
+    return int(rec["read_bytes"] + rec["write_bytes"])
 
 
 def attention_metric(args, torch, px, W):
