@@ -216,3 +216,45 @@ def test_attention_bf16_many_short_segments(px, orc):
     o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, 0.125))
     assert_bf16(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.125)),
                 what="many short segments")
+
+
+def _peaked_qk(family, gain, n, C, seed):
+    """Q and K whose logits are far sharper than unit Gaussians give: scaled
+    Gaussians, rows RMS-normalised then scaled (as after a QK norm), and keys
+    near one shared direction with a large norm (big common logit, small
+    differences)."""
+    rng = np.random.default_rng(seed)
+    if family == "gaussian":
+        q, k = rng.standard_normal((n, C)) * gain, rng.standard_normal((n, C)) * gain
+    elif family == "rms":
+        q, k = rng.standard_normal((n, C)), rng.standard_normal((n, C))
+        q = gain * q / np.sqrt((q * q).mean(1, keepdims=True))
+        k = gain * k / np.sqrt((k * k).mean(1, keepdims=True))
+    else:
+        u = rng.standard_normal(C)
+        q = gain * (u + 0.1 * rng.standard_normal((n, C)))
+        k = gain * (u + 0.1 * rng.standard_normal((n, C)))
+    return W.bf16_round(q.astype(np.float32)), W.bf16_round(k.astype(np.float32))
+
+
+@pytest.mark.parametrize("lens", [(1300, 200), (150, 90, 200)], ids=["long", "short"])
+@pytest.mark.parametrize("family,gain", [("gaussian", 8.0), ("gaussian", 16.0), ("rms", 16.0),
+                                         ("near_dup", 64.0)])
+def test_attention_bf16_peaked_logits(px, orc, lens, family, gain):
+    """Sharply peaked logits (scores tens to hundreds of units apart): the
+    scores must reach the exponent at fp32 precision.  Rounding q * scale to
+    bf16 before QK^T, for one, gives 1.1e-2 to 4.5e-2 relative L2 on such
+    inputs, while exact fp32 scores give about 1e-4 plus the bf16 rounding of
+    the output (about 1.1e-3), hence the bound of 5e-3 here.  The long
+    segments run the long-segment kernel, the short ones the per-segment
+    kernel."""
+    heads, hd = 2, 64
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    n, C = int(cu[-1]), heads * hd
+    q, k = _peaked_qk(family, gain, n, C, 21)
+    v = W.bf16_round(W.normal(69, n * C, 3).reshape(n, C))
+    print(f"[attn peaked] {family} gain={gain} lens={lens}", flush=True)
+    o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, 0.125))
+    assert np.isfinite(o).all()
+    assert_bf16(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(0.125)),
+                tol=5e-3, what=f"peaked {family} {gain}")
