@@ -56,6 +56,107 @@ layer_norm_kernel(const TX * __restrict__ x, int64_t rows, int channels, float e
     }
 }
 
+// Layer norm of rows that are L x NV 16-byte vectors wide: L lanes own a row
+// (64 / L rows per wave), each lane loads NV vectors of 16 bytes, keeps them
+// in registers and reduces over its L-lane group.  Rows of 64 bf16 channels
+// (the decoder's finest levels, millions of rows) get 8 rows per wave instead
+// of one, with 16-byte accesses.  Same two passes and formulas as
+// layer_norm_kernel (mean, then the mean of squared deviations, then
+// 1 / sqrt(var + eps)); only the summation order within a row differs.
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int d = L / 2; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+template <typename T> struct Vec16;
+template <> struct Vec16<float> {
+    static constexpr int kN = 4;
+    __device__ static void load(const float * p, float (&v)[4]) {
+        const float4 q = *reinterpret_cast<const float4 *>(p);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    }
+};
+template <> struct Vec16<uint16_t> {
+    static constexpr int kN = 8;
+    __device__ static void load(const uint16_t * p, float (&v)[8]) {
+        const uint4 q = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+};
+
+template <typename TY, int N>
+__device__ __forceinline__ void store_vec(TY * p, const float (&v)[N]) {
+    if constexpr (sizeof(TY) == 4) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4)
+            *reinterpret_cast<float4 *>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+    } else if constexpr (N == 8) {
+        *reinterpret_cast<uint4 *>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                   pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+    } else {
+        *reinterpret_cast<uint2 *>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+}
+
+template <typename TX, typename TY, int L, int NV>
+__global__ void __launch_bounds__(256)
+layer_norm_rows_kernel(const TX * __restrict__ x, int64_t rows, float eps,
+                       const float * __restrict__ gamma, const float * __restrict__ beta,
+                       TY * __restrict__ y) {
+    constexpr int V = Vec16<TX>::kN;
+    constexpr int C = L * NV * V;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * (64 / L) + lane / L;
+    const int part = lane % L;
+    const bool live = row < rows;  // every lane takes part in the group shuffles
+    float v[NV][V];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (live) {
+            Vec16<TX>::load(x + row * C + (j * L + part) * V, v[j]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[j][e] = 0.0f;
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < V; ++e) s += v[j][e];
+    const float mean = group_sum<L>(s) / static_cast<float>(C);
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const float d = v[j][e] - mean;
+            q += d * d;
+        }
+    const float var = group_sum<L>(q) / static_cast<float>(C);
+    const float inv = 1.0f / sqrtf(var + eps);
+    if (!live) return;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c0 = (j * L + part) * V;
+        float o[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            float val = (v[j][e] - mean) * inv;
+            if (gamma) val = val * gamma[c0 + e] + beta[c0 + e];
+            o[e] = val;
+        }
+        store_vec<TY, V>(y + row * C + c0, o);
+    }
+}
+
 // RoPE frequency table computed on the host exactly as the reference does
 // (std::pow in float), passed by value.
 struct RopeTable {
@@ -408,10 +509,47 @@ __global__ void timestep_embedding_kernel(const float * __restrict__ t, int64_t 
 
 int check_dtype(int dtype) { return dtype == PXS_F32 || dtype == PXS_BF16; }
 
+template <typename TX, typename TY, int L, int NV>
+void launch_ln_rows(const void * x, int64_t rows, float eps, const float * gamma,
+                    const float * beta, void * y, hipStream_t s) {
+    hipLaunchKernelGGL((layer_norm_rows_kernel<TX, TY, L, NV>), dim3(grid_for(rows, 4 * (64 / L))),
+                       dim3(256), 0, s, static_cast<const TX *>(x), rows, eps, gamma, beta,
+                       static_cast<TY *>(y));
+}
+
+// The row-group kernel when a row is 2^k 16-byte vectors (up to 64 lanes of
+// one vector, or 64 lanes of 2 or 4) and both buffers are 16-byte aligned.
+template <typename TX, typename TY>
+bool try_ln_rows(const void * x, int64_t rows, int channels, float eps, const float * gamma,
+                 const float * beta, void * y, hipStream_t s) {
+    constexpr int V = Vec16<TX>::kN;
+    if (channels % V != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0 ||
+        (reinterpret_cast<uintptr_t>(y) & 15) != 0)
+        return false;
+    switch (channels / V) {
+    case 1: launch_ln_rows<TX, TY, 1, 1>(x, rows, eps, gamma, beta, y, s); return true;
+    case 2: launch_ln_rows<TX, TY, 2, 1>(x, rows, eps, gamma, beta, y, s); return true;
+    case 4: launch_ln_rows<TX, TY, 4, 1>(x, rows, eps, gamma, beta, y, s); return true;
+    case 8: launch_ln_rows<TX, TY, 8, 1>(x, rows, eps, gamma, beta, y, s); return true;
+    case 16: launch_ln_rows<TX, TY, 16, 1>(x, rows, eps, gamma, beta, y, s); return true;
+    case 32: launch_ln_rows<TX, TY, 32, 1>(x, rows, eps, gamma, beta, y, s); return true;
+    case 64: launch_ln_rows<TX, TY, 64, 1>(x, rows, eps, gamma, beta, y, s); return true;
+    case 128: launch_ln_rows<TX, TY, 64, 2>(x, rows, eps, gamma, beta, y, s); return true;
+    case 256: launch_ln_rows<TX, TY, 64, 4>(x, rows, eps, gamma, beta, y, s); return true;
+    default: return false;
+    }
+}
+
 template <typename TX, typename TY, bool kMod>
 void launch_ln(const void * x, int64_t rows, int channels, float eps, const float * gamma,
                const float * beta, const int32_t * coords, const float * bm, const float * tm,
                int off, void * y, hipStream_t s) {
+#ifndef PXS_LN_ROWS
+#define PXS_LN_ROWS 1
+#endif
+    if constexpr (!kMod) {
+        if (PXS_LN_ROWS && try_ln_rows<TX, TY>(x, rows, channels, eps, gamma, beta, y, s)) return;
+    }
     hipLaunchKernelGGL((layer_norm_kernel<TX, TY, kMod>), dim3(grid_for(rows, kRowsPerBlock)),
                        dim3(64 * kRowsPerBlock), 0, s, static_cast<const TX *>(x), rows, channels,
                        eps, gamma, beta, coords, bm, tm, off, static_cast<TY *>(y));

@@ -90,6 +90,29 @@ def test_layer_norm(px, orc, dtype):
         (assert_fp32 if dtype == "f32" else assert_bf16)(y, ref, what=f"ln {dtype}")
 
 
+@pytest.mark.parametrize("channels", [4, 8, 64, 96, 128, 256, 512, 2048])
+@pytest.mark.parametrize("xd,yd", [("f32", "f32"), ("bf16", "bf16"), ("f32", "bf16"), ("bf16", "f32")])
+def test_layer_norm_row_layouts(px, orc, channels, xd, yd):
+    """Every row layout of the layer norm against the oracle: rows of 1 to 64
+    16-byte vectors (4 fp32 or 8 bf16 channels each) share a wave, 64/L rows
+    per wave; 128 and 256 vectors take 2 or 4 per lane; other widths (96
+    channels, 4 bf16 channels, 2048 fp32 channels) one wave per row.  1,237
+    rows leave the last wave part empty."""
+    import torch
+    rows = 1237
+    x = (W.normal(57, rows * channels, 1) * 2 - 0.3).reshape(rows, channels)
+    g, b = W.normal(57, channels, 2), W.normal(57, channels, 3)
+    conv = t32 if xd == "f32" else tbf
+    xr = x if xd == "f32" else W.bf16_round(x)
+    out = torch.float32 if yd == "f32" else torch.bfloat16
+    check = assert_fp32 if yd == "f32" else assert_bf16
+    print(f"[ln layouts] channels={channels} {xd}->{yd}", flush=True)
+    for gamma, beta, eps in ((g, b, 1e-6), (None, None, 1e-5)):
+        y = host(px.layer_norm(conv(x), eps, None if gamma is None else t32(gamma),
+                               None if beta is None else t32(beta), out_dtype=out))
+        check(y, orc.layer_norm(xr, eps, gamma, beta), what=f"ln {channels} {xd}->{yd}")
+
+
 def test_layer_norm_small_channels_and_kat(px):
     import json
     from pathlib import Path
