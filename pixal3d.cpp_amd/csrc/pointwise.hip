@@ -347,6 +347,56 @@ __global__ void split_copy_kernel(const T * __restrict__ qkv, int64_t rows, int 
     }
 }
 
+// 8 consecutive elements through 16-byte accesses (two for fp32): the
+// elementwise kernels below take this path when the count is a multiple of 8
+// and the buffers are 16-byte aligned, with the same per-element arithmetic
+// as their one-element loops (so the same bits).
+template <typename T> __device__ __forceinline__ void load8(const T * p, float (&v)[8]);
+template <> __device__ __forceinline__ void load8<float>(const float * p, float (&v)[8]) {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+template <> __device__ __forceinline__ void load8<uint16_t>(const uint16_t * p, float (&v)[8]) {
+    const uint4 q = *reinterpret_cast<const uint4 *>(p);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+template <typename T> __device__ __forceinline__ void store8(T * p, const float (&v)[8]);
+template <> __device__ __forceinline__ void store8<float>(float * p, const float (&v)[8]) {
+    reinterpret_cast<float4 *>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4 *>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+template <> __device__ __forceinline__ void store8<uint16_t>(uint16_t * p, const float (&v)[8]) {
+    *reinterpret_cast<uint4 *>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                               pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+}
+
+inline bool vec8_ok(int64_t count, const void * a, const void * b = nullptr) {
+    return count % 8 == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(b) & 15) == 0;
+}
+
+inline unsigned vec8_blocks(int64_t count) {
+    return static_cast<unsigned>(std::min<int64_t>((count / 8 + 255) / 256, 16384));
+}
+
+template <typename T>
+__global__ void activation8_kernel(T * __restrict__ x, int64_t nvec, int act) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec;
+         i += stride) {
+        float v[8];
+        load8(x + 8 * i, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = act == PXS_ACT_GELU_TANH ? gelu_tanh_f(v[e]) : silu_f(v[e]);
+        store8(x + 8 * i, v);
+    }
+}
+
 template <typename T>
 __global__ void activation_kernel(T * __restrict__ x, int64_t count, int act) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -461,6 +511,36 @@ value_stats_final_kernel(const float * __restrict__ x, int64_t count,
 }
 
 constexpr int kStatsMaxParts = 1024;
+
+template <typename TS, typename TD>
+__global__ void convert8_kernel(const TS * __restrict__ x, int64_t nvec, TD * __restrict__ y) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec;
+         i += stride) {
+        float v[8];
+        load8(x + 8 * i, v);
+        store8(y + 8 * i, v);
+    }
+}
+
+// add_repeat over 8-element pieces of a row (channels % 8 == 0); the row
+// index is 32-bit (the caller checks rows * channels / 8 < 2^32).
+template <typename T>
+__global__ void add_repeat8_kernel(const T * a, uint32_t nvec, uint32_t vpr,
+                                   const float * __restrict__ skip, int skip_channels, int repeats,
+                                   float * y) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < nvec; i += stride) {
+        const uint32_t r = i / vpr;
+        const int j0 = static_cast<int>(i - r * vpr) * 8;
+        const float * sk = skip + static_cast<int64_t>(r) * skip_channels;
+        float v[8];
+        load8(a + static_cast<int64_t>(i) * 8, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = v[e] + sk[(j0 + e) / repeats];
+        store8(y + static_cast<int64_t>(i) * 8, v);
+    }
+}
 
 template <typename TS, typename TD>
 __global__ void convert_kernel(const TS * __restrict__ x, int64_t count, TD * __restrict__ y) {
@@ -723,6 +803,15 @@ int pxs_activation(int dtype, void * x, int64_t count, int act, void * stream) {
               "pxs_activation: bad activation");
     if (count <= 0 || act == PXS_ACT_NONE) return PXS_OK;
     PXS_CHECK(x, PXS_ERR_ARG, "pxs_activation: null pointer");
+    if (vec8_ok(count, x)) {
+        if (dtype == PXS_F32)
+            hipLaunchKernelGGL(activation8_kernel<float>, dim3(vec8_blocks(count)), dim3(256), 0,
+                               as_stream(stream), static_cast<float *>(x), count / 8, act);
+        else
+            hipLaunchKernelGGL(activation8_kernel<uint16_t>, dim3(vec8_blocks(count)), dim3(256), 0,
+                               as_stream(stream), static_cast<uint16_t *>(x), count / 8, act);
+        return check_launch("pxs_activation");
+    }
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
     if (dtype == PXS_F32) {
         hipLaunchKernelGGL(activation_kernel<float>, dim3(blocks), dim3(256), 0, as_stream(stream),
@@ -786,8 +875,25 @@ int pxs_convert(int src_dtype, const void * x, int64_t count, int dst_dtype, voi
     PXS_CHECK(count >= 0, PXS_ERR_ARG, "pxs_convert: negative count");
     if (count == 0) return PXS_OK;
     PXS_CHECK(x && y, PXS_ERR_ARG, "pxs_convert: null pointer");
-    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
     hipStream_t s = as_stream(stream);
+    if (vec8_ok(count, x, y)) {
+        const unsigned vb = vec8_blocks(count);
+        const int64_t nv = count / 8;
+        if (src_dtype == PXS_F32 && dst_dtype == PXS_BF16)
+            hipLaunchKernelGGL((convert8_kernel<float, uint16_t>), dim3(vb), dim3(256), 0, s,
+                               static_cast<const float *>(x), nv, static_cast<uint16_t *>(y));
+        else if (src_dtype == PXS_BF16 && dst_dtype == PXS_F32)
+            hipLaunchKernelGGL((convert8_kernel<uint16_t, float>), dim3(vb), dim3(256), 0, s,
+                               static_cast<const uint16_t *>(x), nv, static_cast<float *>(y));
+        else if (src_dtype == PXS_F32)
+            hipLaunchKernelGGL((convert8_kernel<float, float>), dim3(vb), dim3(256), 0, s,
+                               static_cast<const float *>(x), nv, static_cast<float *>(y));
+        else
+            hipLaunchKernelGGL((convert8_kernel<uint16_t, uint16_t>), dim3(vb), dim3(256), 0, s,
+                               static_cast<const uint16_t *>(x), nv, static_cast<uint16_t *>(y));
+        return check_launch("pxs_convert");
+    }
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
     if (src_dtype == PXS_F32 && dst_dtype == PXS_BF16) {
         hipLaunchKernelGGL((convert_kernel<float, uint16_t>), dim3(blocks), dim3(256), 0, s,
                            static_cast<const float *>(x), count, static_cast<uint16_t *>(y));
@@ -812,8 +918,20 @@ int pxs_add_repeat(int a_dtype, const void * a, int64_t rows, int channels, cons
     if (rows == 0) return PXS_OK;
     PXS_CHECK(a && skip && y, PXS_ERR_ARG, "pxs_add_repeat: null pointer");
     const int64_t count = rows * channels;
-    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
     const int repeats = channels / skip_channels;
+    if (channels % 8 == 0 && count / 8 <= UINT32_MAX && vec8_ok(count, a, y)) {
+        const uint32_t nv = static_cast<uint32_t>(count / 8), vpr = static_cast<uint32_t>(channels / 8);
+        if (a_dtype == PXS_F32)
+            hipLaunchKernelGGL(add_repeat8_kernel<float>, dim3(vec8_blocks(count)), dim3(256), 0,
+                               as_stream(stream), static_cast<const float *>(a), nv, vpr, skip,
+                               skip_channels, repeats, y);
+        else
+            hipLaunchKernelGGL(add_repeat8_kernel<uint16_t>, dim3(vec8_blocks(count)), dim3(256), 0,
+                               as_stream(stream), static_cast<const uint16_t *>(a), nv, vpr, skip,
+                               skip_channels, repeats, y);
+        return check_launch("pxs_add_repeat");
+    }
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
     if (a_dtype == PXS_F32) {
         hipLaunchKernelGGL(add_repeat_kernel<float>, dim3(blocks), dim3(256), 0, as_stream(stream),
                            static_cast<const float *>(a), rows, channels, skip, skip_channels,

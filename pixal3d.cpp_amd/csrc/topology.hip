@@ -884,6 +884,33 @@ __global__ void c2s_coords_kernel(const int4 * __restrict__ coords, int64_t n, i
     src_of[dst] = t;  // source (parent * cc + child)
 }
 
+// The same copy in 16-byte pieces (8 elements; c_out % 8 == 0, 16-byte
+// aligned buffers): one source-row lookup per piece, 32-bit indices (the
+// caller bounds rows * cc by INT_MAX).
+template <typename T>
+__global__ void c2s_feats8_kernel(const T * __restrict__ x, int channels, int cc,
+                                  const int64_t * __restrict__ src_of,
+                                  const int64_t * __restrict__ m_dev, int64_t m_max,
+                                  T * __restrict__ y) {
+    constexpr int kWords = sizeof(T) == 4 ? 2 : 1;  // 16-byte words per 8 elements
+    const uint32_t vpr = static_cast<uint32_t>(channels / cc / 8);
+    const int64_t m = m_dev ? *m_dev : m_max;
+    const uint32_t total = static_cast<uint32_t>(m) * vpr;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const uint32_t r = i / vpr;
+        const uint32_t piece = i - r * vpr;
+        const uint32_t s = static_cast<uint32_t>(src_of[r]);
+        const uint32_t parent = s / static_cast<uint32_t>(cc);
+        const uint32_t slot = s - parent * static_cast<uint32_t>(cc);
+        const uint4 * src = reinterpret_cast<const uint4 *>(
+            x + static_cast<int64_t>(parent) * channels + (static_cast<int64_t>(slot) * vpr + piece) * 8);
+        uint4 * dst = reinterpret_cast<uint4 *>(y + static_cast<int64_t>(i) * 8);
+#pragma unroll
+        for (int w = 0; w < kWords; ++w) dst[w] = src[w];
+    }
+}
+
 template <typename T>
 __global__ void c2s_feats_kernel(const T * __restrict__ x, int channels, int cc,
                                  const int64_t * __restrict__ src_of,
@@ -1469,6 +1496,19 @@ int pxs_channel_to_spatial(int dtype, const int32_t * coords, int64_t n, const v
                        reinterpret_cast<const int4 *>(coords), n, factor, icc, subdivision, prefix,
                        reinterpret_cast<int4 *>(out_coords), src_of);
     const int64_t max_elems = n * channels;
+    if ((channels / icc) % 8 == 0 && max_elems / 8 <= UINT32_MAX &&
+        (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
+        const unsigned vb = static_cast<unsigned>(std::min<int64_t>((max_elems / 8 + 255) / 256, 16384));
+        if (dtype == PXS_F32)
+            hipLaunchKernelGGL(c2s_feats8_kernel<float>, dim3(vb), dim3(256), 0, s,
+                               static_cast<const float *>(x), channels, icc, src_of, m_out, n * cc,
+                               static_cast<float *>(y));
+        else
+            hipLaunchKernelGGL(c2s_feats8_kernel<uint16_t>, dim3(vb), dim3(256), 0, s,
+                               static_cast<const uint16_t *>(x), channels, icc, src_of, m_out,
+                               n * cc, static_cast<uint16_t *>(y));
+        return check_launch("pxs_channel_to_spatial");
+    }
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((max_elems + 255) / 256, 16384));
     if (dtype == PXS_F32) {
         hipLaunchKernelGGL(c2s_feats_kernel<float>, dim3(blocks), dim3(256), 0, s,

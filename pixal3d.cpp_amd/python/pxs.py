@@ -629,6 +629,14 @@ class Pxs:
                 "first_bad_value": float(f32[0]), "min": float(f32[1]), "max": float(f32[2]),
                 "max_abs": float(f32[3])}
 
+    def convert(self, x, dtype):
+        """x (fp32 or bf16, any shape) converted to dtype, elementwise."""
+        y = torch.empty(x.shape, dtype=dtype, device=x.device)
+        self._check(self.lib.pxs_convert(_dtype_code(x), _ptr(x), x.numel(), _dtype_code(y),
+                                         _ptr(y), self.stream()),
+                    "pxs_convert")
+        return y
+
     def activation(self, x, act):
         self._check(self.lib.pxs_activation(_dtype_code(x), _ptr(x), x.numel(), act, self.stream()),
                     "pxs_activation")

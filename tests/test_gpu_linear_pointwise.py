@@ -205,3 +205,37 @@ def test_value_stats(px, count):
     assert got["max"] == (fin.max() if fin.size else -np.inf)
     assert got["max_abs"] == (np.abs(fin).max() if fin.size else 0.0)
     assert abs(got["sum"] - fin.astype(np.float64).sum()) <= 1e-9 * max(1.0, np.abs(fin).sum())
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_elementwise_vector_paths_match_element_loops(px, dtype):
+    """Activations, conversions and add_repeat run 8 elements per thread when
+    the count is a multiple of 8 and the buffers are 16-byte aligned, one
+    element per thread otherwise; both forms must give the same bits (and
+    conversions torch's round-to-nearest-even)."""
+    import torch
+    import pxs
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    n = 8 * 40_000
+    base = torch.from_numpy(W.normal(58, n, 1).reshape(-1) * 3).to("cuda")
+    for act in (pxs.ACT_SILU, pxs.ACT_GELU_TANH):
+        vec = base.to(tdt).clone()
+        px.activation(vec, act)                   # multiple of 8, aligned
+        tail = base.to(tdt)[: n - 1].clone()
+        px.activation(tail, act)                  # n - 1 elements: the element loop
+        torch.cuda.synchronize()
+        assert torch.equal(vec[: n - 1], tail), f"activation {act} {dtype}"
+    src = base if dtype == "f32" else base.to(torch.bfloat16)
+    for out in (torch.float32, torch.bfloat16):
+        want = src.to(out)
+        assert torch.equal(px.convert(src, out), want), f"convert {dtype}->{out}"
+        assert torch.equal(px.convert(src[1:], out), want[1:]), f"convert unaligned {dtype}->{out}"
+    rows = 4_099
+    for ch, sk in ((64, 8), (48, 48), (12, 3)):   # vector path, repeats 1, element loop
+        a = torch.from_numpy(W.normal(59, rows * ch, 1).reshape(rows, ch)).to("cuda").to(tdt)
+        skip = torch.from_numpy(W.normal(59, rows * sk, 2).reshape(rows, sk)).to("cuda")
+        got = px.add_repeat(a, skip)
+        torch.cuda.synchronize()
+        want = a.float() + skip.repeat_interleave(ch // sk, dim=1)
+        assert torch.equal(got, want), f"add_repeat {ch}/{sk} {dtype}"
+
