@@ -1011,41 +1011,86 @@ __global__ void ordered_linear_kernel(const float * __restrict__ x, int64_t rows
 // outputs does not change any one sum's order).  Weights come from LDS.
 constexpr int kOrderedRowOut = 8;
 constexpr int kOrderedRowCin = 2048;
+constexpr int kOrderedRows = 256;                  // rows per workgroup, one per thread
+constexpr int kOrderedChunk = 32;                  // input channels staged per pass
+constexpr int kOrderedPitch = kOrderedChunk + 1;   // odd pitch: lane l reads bank (l + j) % 32
 
-__global__ void __launch_bounds__(256)
+// Rows pass through LDS 32 channels at a time, loaded by the whole workgroup
+// with coalesced (16-byte where possible) reads, so each thread walks its own
+// row from LDS instead of striding 4 x cin bytes between lanes in global
+// memory.  The weights sit in LDS too (read as broadcasts).  Dynamic LDS:
+// ordered_rows_lds_bytes(cout, cin).
+__global__ void __launch_bounds__(kOrderedRows)
 ordered_linear_rows_kernel(const float * __restrict__ x, int64_t rows, int cin,
                            const float * __restrict__ weight, const float * __restrict__ bias,
-                           int cout, float * __restrict__ y) {
+                           int cout, bool vec4, float * __restrict__ y) {
 #pragma clang fp contract(off)
-    __shared__ float w_lds[kOrderedRowOut * kOrderedRowCin];
+    extern __shared__ __align__(16) float ordered_lds[];
+    float * w_lds = ordered_lds;
+    float * x_lds = ordered_lds + ((cout * cin + 3) & ~3);
     for (int e = threadIdx.x; e < cout * cin; e += blockDim.x) w_lds[e] = weight[e];
-    __syncthreads();
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (row >= rows) return;
-    const float * xr = x + row * cin;
+    const int t = threadIdx.x;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kOrderedRows;
+    const int nrows = static_cast<int>(rows - row0 < kOrderedRows ? rows - row0 : kOrderedRows);
     float acc[kOrderedRowOut];
 #pragma unroll
     for (int o = 0; o < kOrderedRowOut; ++o) acc[o] = (o < cout && bias) ? bias[o] : 0.0f;
-    for (int i = 0; i < cin; i += 4) {
-        float xv[4];
-        if (i + 4 <= cin && (reinterpret_cast<uintptr_t>(xr + i) & 15) == 0) {
-            const float4 v = *reinterpret_cast<const float4 *>(xr + i);
-            xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+    for (int k0 = 0; k0 < cin; k0 += kOrderedChunk) {
+        const int kw = cin - k0 < kOrderedChunk ? cin - k0 : kOrderedChunk;
+        __syncthreads();  // the previous chunk is consumed (and the weights are in)
+        if (vec4) {
+            for (int e = t; e < kOrderedRows * (kOrderedChunk / 4); e += kOrderedRows) {
+                const int r = e / (kOrderedChunk / 4), c = (e % (kOrderedChunk / 4)) * 4;
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (r < nrows && c < kw)
+                    v = *reinterpret_cast<const float4 *>(x + (row0 + r) * cin + k0 + c);
+                float * d = x_lds + r * kOrderedPitch + c;
+                d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+            }
         } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xv[j] = i + j < cin ? xr[i + j] : 0.0f;
+            for (int e = t; e < kOrderedRows * kOrderedChunk; e += kOrderedRows) {
+                const int r = e / kOrderedChunk, c = e % kOrderedChunk;
+                x_lds[r * kOrderedPitch + c] =
+                    (r < nrows && c < kw) ? x[(row0 + r) * cin + k0 + c] : 0.0f;
+            }
         }
+        __syncthreads();
+        if (t < nrows) {
+            const float * xr = x_lds + t * kOrderedPitch;
+            for (int j = 0; j < kw; ++j) {
+                const float xv = xr[j];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (i + j >= cin) break;
-#pragma unroll
-            for (int o = 0; o < kOrderedRowOut; ++o)
-                if (o < cout) acc[o] += w_lds[o * cin + i + j] * xv[j];
+                for (int o = 0; o < kOrderedRowOut; ++o)
+                    if (o < cout) acc[o] += w_lds[o * cin + k0 + j] * xv;
+            }
         }
     }
+    if (t >= nrows) return;
 #pragma unroll
     for (int o = 0; o < kOrderedRowOut; ++o)
-        if (o < cout) y[row * cout + o] = acc[o];
+        if (o < cout) y[(row0 + t) * cout + o] = acc[o];
+}
+
+constexpr size_t ordered_rows_lds_bytes(int cout, int cin) {
+    return (static_cast<size_t>((cout * cin + 3) & ~3) + kOrderedRows * kOrderedPitch) * sizeof(float);
+}
+
+int launch_ordered_rows(const float * x, int64_t rows, int cin, const float * weight,
+                        const float * bias, int cout, float * y, hipStream_t s) {
+    static bool configured = false;
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&ordered_linear_rows_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(ordered_rows_lds_bytes(kOrderedRowOut, kOrderedRowCin)));
+        if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(ordered_linear_rows)");
+        configured = true;
+    }
+    const bool vec4 = cin % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    hipLaunchKernelGGL(ordered_linear_rows_kernel,
+                       dim3(static_cast<unsigned>((rows + kOrderedRows - 1) / kOrderedRows)),
+                       dim3(kOrderedRows), ordered_rows_lds_bytes(cout, cin), s, x, rows, cin, weight,
+                       bias, cout, vec4, y);
+    return check_launch("ordered linear (rows)");
 }
 
 } // namespace
@@ -1092,6 +1137,13 @@ int pxs_linear(int dtype, const void * x, int64_t rows, int cin, const void * we
               PXS_ERR_ARG, "pxs_linear: bad activation");
     if (rows == 0) return PXS_OK;
     PXS_CHECK(x && weight && y, PXS_ERR_ARG, "pxs_linear: null pointer");
+    // A few fp32 outputs over narrow rows (the decoder's output layer, 64 -> 7
+    // over millions of rows): the reference's own operation order, one thread
+    // per row, HBM-bound, instead of 64-column MFMA tiles 7/8 empty.
+    if (dtype == PXS_F32 && act == PXS_ACT_NONE && cout <= kOrderedRowOut && cin <= 256)
+        return launch_ordered_rows(static_cast<const float *>(x), rows, cin,
+                                   static_cast<const float *>(weight), bias, cout,
+                                   static_cast<float *>(y), as_stream(stream));
     GemmArgs a{};
     a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
     a.cout = cout; a.m = rows; a.rowmap = nullptr; a.ld_map = 0; a.noff = 1; a.masks = nullptr;
@@ -1156,11 +1208,8 @@ int pxs_linear_ordered(const float * x, int64_t rows, int cin, const float * wei
     PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear_ordered: bad shape");
     if (rows == 0) return PXS_OK;
     PXS_CHECK(x && weight && y, PXS_ERR_ARG, "pxs_linear_ordered: null pointer");
-    if (cout <= kOrderedRowOut && cin <= kOrderedRowCin) {
-        hipLaunchKernelGGL(ordered_linear_rows_kernel, dim3(static_cast<unsigned>((rows + 255) / 256)),
-                           dim3(256), 0, as_stream(stream), x, rows, cin, weight, bias, cout, y);
-        return check_launch("pxs_linear_ordered");
-    }
+    if (cout <= kOrderedRowOut && cin <= kOrderedRowCin)
+        return launch_ordered_rows(x, rows, cin, weight, bias, cout, y, as_stream(stream));
     const int64_t count = rows * cout;
     hipLaunchKernelGGL(ordered_linear_kernel, dim3(static_cast<unsigned>((count + 255) / 256)),
                        dim3(256), 0, as_stream(stream), x, rows, cin, weight, bias, cout, y);

@@ -172,16 +172,37 @@ def test_qkv_prepare(px, orc, dtype, hd, heads):
     np.testing.assert_array_equal(host(v), qkv[:, 2 * C:])
 
 
-@pytest.mark.parametrize("cin,cout", [(64, 8), (37, 8), (128, 3), (96, 24)])
-def test_linear_ordered_bit_exact(px, orc, cin, cout):
+@pytest.mark.parametrize("cin,cout,rows", [(64, 8, 1000), (37, 8, 1000), (128, 3, 1000),
+                                           (96, 24, 1000), (2048, 8, 300), (5, 1, 70_001),
+                                           (64, 7, 100_000)])
+def test_linear_ordered_bit_exact(px, orc, cin, cout, rows):
     """pxs_linear_ordered reproduces sparse_linear's operation order: bit-equal
-    to the oracle (itself bit-equal to the compiled reference)."""
-    rows = 1000
+    to the oracle (itself bit-equal to the compiled reference).  Up to 8
+    outputs run one thread per row over rows staged through LDS (16-byte loads
+    when cin % 4 == 0, single floats otherwise; 2,048 inputs take the largest
+    weight table); 24 outputs one thread per output."""
     x = W.normal(91, rows * cin, 1).reshape(rows, cin)
     w = W.normal(91, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin)
     b = W.normal(91, cout, 3)
     got = px.linear_ordered(t32(x), t32(w), t32(b))
     np.testing.assert_array_equal(host(got), orc.linear(x, w, b))
+
+
+@pytest.mark.parametrize("cin,cout", [(64, 7), (256, 8), (30, 2), (257, 8)])
+def test_linear_fp32_few_outputs(px, orc, cin, cout):
+    """fp32 linears with at most 8 outputs and at most 256 inputs run in the
+    reference's own order (bit-equal to the oracle); 257 inputs take the MFMA
+    path (the fp32 bar)."""
+    rows = 20_011
+    x = W.normal(92, rows * cin, 1).reshape(rows, cin)
+    w = W.normal(92, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin)
+    b = W.normal(92, cout, 3)
+    got = host(px.linear(t32(x), t32(w), t32(b)))
+    ref = orc.linear(x, w, b)
+    if cin <= 256:
+        np.testing.assert_array_equal(got, ref)
+    else:
+        assert_fp32(got, ref, what="fp32 linear, 8 outputs")
 
 
 @pytest.mark.parametrize("count", [0, 1, 777, 1_000_003])
