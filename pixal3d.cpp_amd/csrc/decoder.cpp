@@ -73,7 +73,10 @@ struct C2SBuffers {
     MapBuffers map2;
 };
 
-C2SBuffers carve_c2s(Carver & c, int dtype, int64_t rows, int channels, int out_channels) {
+// own_in / own_out: carve the block's own neighbour maps of its input and
+// output coordinates (a caller that keeps maps per level passes them in).
+C2SBuffers carve_c2s(Carver & c, int dtype, int64_t rows, int channels, int out_channels,
+                     bool own_in = true, bool own_out = true) {
     const size_t e = dtype_bytes(dtype);
     const size_t r = static_cast<size_t>(std::max<int64_t>(rows, 1));
     const size_t C = static_cast<size_t>(channels), O = static_cast<size_t>(out_channels);
@@ -87,23 +90,29 @@ C2SBuffers carve_c2s(Carver & c, int dtype, int64_t rows, int channels, int out_
     b.skip = static_cast<float *>(c.take(8 * r * (C / 8) * 4));
     b.m_dev = static_cast<int64_t *>(c.take(sizeof(int64_t)));
     b.c2s_ws = c.take(pxs_channel_to_spatial_workspace_bytes(rows, 2));
-    b.map1 = carve_map(c, rows);
-    b.map2 = carve_map(c, 8 * std::max<int64_t>(rows, 1));
+    if (own_in) b.map1 = carve_map(c, rows);
+    if (own_out) b.map2 = carve_map(c, 8 * std::max<int64_t>(rows, 1));
     return b;
+}
+
+size_t c2s_shared_maps_bytes(int dtype, int64_t rows, int channels, int out_channels) {
+    Carver c(nullptr);
+    carve_c2s(c, dtype, rows, channels, out_channels, false, false);
+    return c.used();
 }
 
 struct DecoderBuffers {
     float * hid[2];
     int32_t * crd[2];
-    MapBuffers map;
+    MapBuffers map[2];  // the current level's map and the next one's (built by the C2S block)
     void * block_ws;
 };
 
 int64_t grow8(int64_t n, int64_t cap) { return n > cap / 8 ? cap : 8 * n; }
 
 // Buffers sized for each level's capacity min(max_rows, rows * 8^l): two
-// hidden-state and two coordinate buffers (ping-pong across C2S levels), one
-// neighbour map, and the largest block workspace.  Blocks past n_blocks are
+// hidden-state, two coordinate and two neighbour-map buffers (ping-pong across
+// C2S levels), and the largest block workspace.  Blocks past n_blocks are
 // not sized (the forward rejects such a configuration).
 DecoderBuffers carve_decoder(Carver & c, int dtype, const pxs_decoder_config & cfg,
                              const pxs_decoder_block * blocks, int n_blocks, int64_t rows,
@@ -119,8 +128,8 @@ DecoderBuffers carve_decoder(Carver & c, int dtype, const pxs_decoder_config & c
         for (int k = 0; k < cfg.num_blocks[l] && bi < n_blocks; ++k, ++bi)
             ws = std::max(ws, pxs_convnext_block_workspace_bytes(dtype, cap, C, blocks[bi].mlp_hidden, 1));
         if (l + 1 < cfg.levels && bi < n_blocks) {
-            ws = std::max(ws, pxs_resblock_c2s_workspace_bytes(dtype, cap, blocks[bi].channels,
-                                                              blocks[bi].out_channels));
+            ws = std::max(ws, c2s_shared_maps_bytes(dtype, cap, blocks[bi].channels,
+                                                   blocks[bi].out_channels));
             ++bi;
         }
     }
@@ -131,7 +140,8 @@ DecoderBuffers carve_decoder(Carver & c, int dtype, const pxs_decoder_config & c
     b.hid[1] = static_cast<float *>(c.take(hid * 4));
     b.crd[0] = static_cast<int32_t *>(c.take(static_cast<size_t>(cap_max) * 16));
     b.crd[1] = static_cast<int32_t *>(c.take(static_cast<size_t>(cap_max) * 16));
-    b.map = carve_map(c, cap_max);
+    b.map[0] = carve_map(c, cap_max);
+    b.map[1] = carve_map(c, cap_max);
     b.block_ws = c.take(ws);
     return b;
 }
@@ -213,11 +223,15 @@ size_t pxs_resblock_c2s_workspace_bytes(int dtype, int64_t rows, int channels,
     return c.used();
 }
 
-int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const float * x,
-                     int channels, int out_channels, float eps,
-                     const pxs_decoder_block_weights * w, int pred_subdiv,
-                     const float * subdivision, float * predicted_subdiv, int32_t * out_coords,
-                     float * y, int64_t * rows_out, void * workspace, void * stream) {
+// The C2S block; in_map (the map of coords, already built) and out_map
+// (where to build the map of out_coords) come from a caller that keeps one
+// map per level, or are null for the block's own in its workspace.
+static int resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const float * x,
+                        int channels, int out_channels, float eps,
+                        const pxs_decoder_block_weights * w, int pred_subdiv,
+                        const float * subdivision, float * predicted_subdiv,
+                        int32_t * out_coords, float * y, int64_t * rows_out, void * workspace,
+                        void * stream, const MapBuffers * in_map, const MapBuffers * out_map) {
     PXS_CHECK_WORKSPACE(workspace, "pxs_resblock_c2s");
     PXS_CHECK(dtype == PXS_F32 || dtype == PXS_BF16, PXS_ERR_ARG, "pxs_resblock_c2s: bad dtype");
     PXS_CHECK(eps > 0.0f && std::isfinite(eps), PXS_ERR_ARG,
@@ -243,7 +257,10 @@ int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const floa
     PXS_CHECK(coords && x && out_coords && y && workspace, PXS_ERR_ARG,
               "pxs_resblock_c2s: null pointer");
     Carver c(workspace);
-    const C2SBuffers b = carve_c2s(c, dtype, rows, channels, out_channels);
+    const C2SBuffers b = carve_c2s(c, dtype, rows, channels, out_channels, in_map == nullptr,
+                                   out_map == nullptr);
+    const MapBuffers & map1 = in_map ? *in_map : b.map1;
+    const MapBuffers & map2 = out_map ? *out_map : b.map2;
     hipStream_t s = as_stream(stream);
     const int packed_ch = 8 * out_channels;
 
@@ -258,9 +275,9 @@ int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const floa
     PXS_TRY(pxs_layer_norm(PXS_F32, x, rows, channels, eps, w->norm1_weight, w->norm1_bias, dtype,
                            b.norm, stream));
     PXS_TRY(pxs_activation(dtype, b.norm, rows * channels, PXS_ACT_SILU, stream));
-    PXS_TRY(build_map(coords, rows, b.map1, stream));
+    if (!in_map) PXS_TRY(build_map(coords, rows, map1, stream));
     PXS_TRY(pxs_subm_conv3d(dtype, b.norm, rows, channels, w->conv1_weight, w->conv1_bias,
-                            packed_ch, b.map1.nbr, b.map1.masks, b.packed, stream));
+                            packed_ch, map1.nbr, map1.masks, b.packed, stream));
     PXS_TRY(pxs_channel_to_spatial(dtype, coords, rows, b.packed, packed_ch, 2, selected,
                                    out_coords, b.hidden, b.m_dev, b.c2s_ws, stream));
     // The skip path subdivides the fp32 input with the same selection; its
@@ -278,11 +295,21 @@ int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const floa
     PXS_TRY(pxs_layer_norm(dtype, b.hidden, m, out_channels, eps, nullptr, nullptr, dtype, b.hnorm,
                            stream));
     PXS_TRY(pxs_activation(dtype, b.hnorm, m * out_channels, PXS_ACT_SILU, stream));
-    PXS_TRY(build_map(out_coords, m, b.map2, stream));
+    PXS_TRY(build_map(out_coords, m, map2, stream));
     void * conv_out = dtype == PXS_BF16 ? b.conv2 : static_cast<void *>(y);
     PXS_TRY(pxs_subm_conv3d(dtype, b.hnorm, m, out_channels, w->conv2_weight, w->conv2_bias,
-                            out_channels, b.map2.nbr, b.map2.masks, conv_out, stream));
+                            out_channels, map2.nbr, map2.masks, conv_out, stream));
     return pxs_add_repeat(dtype, conv_out, m, out_channels, b.skip, channels / 8, y, stream);
+}
+
+int pxs_resblock_c2s(int dtype, const int32_t * coords, int64_t rows, const float * x,
+                     int channels, int out_channels, float eps,
+                     const pxs_decoder_block_weights * w, int pred_subdiv,
+                     const float * subdivision, float * predicted_subdiv, int32_t * out_coords,
+                     float * y, int64_t * rows_out, void * workspace, void * stream) {
+    return resblock_c2s(dtype, coords, rows, x, channels, out_channels, eps, w, pred_subdiv,
+                        subdivision, predicted_subdiv, out_coords, y, rows_out, workspace, stream,
+                        nullptr, nullptr);
 }
 
 size_t pxs_slat_decoder_workspace_bytes(int dtype, const pxs_decoder_config * cfg,
@@ -354,6 +381,11 @@ int pxs_slat_decoder_forward(int dtype, const pxs_decoder_config * cfg,
     PXS_TRY(pxs_linear(PXS_F32, x, rows, cfg->latent_channels, from_latent_weight, from_latent_bias,
                        cfg->model_channels[0], PXS_ACT_NONE, b.hid[0], stream));
     int bi = 0;
+    // Each level's coordinates are hashed once: the C2S block builds the next
+    // level's map into b.map[1 - mc] for its conv2, and the next level's
+    // ConvNeXt blocks and C2S conv1 reuse it.
+    int mc = 0;
+    bool map_ready = false;
     for (int l = 0; l < levels; ++l) {
         const int C = cfg->model_channels[l];
         if (upsample && l == upsample_times) {
@@ -365,7 +397,10 @@ int pxs_slat_decoder_forward(int dtype, const pxs_decoder_config * cfg,
             *rows_out = n;
             return check_launch("pxs_slat_decoder_forward");
         }
-        if (cfg->num_blocks[l] > 0) PXS_TRY(build_map(ccur, n, b.map, stream));
+        if ((cfg->num_blocks[l] > 0 || l + 1 < levels) && !map_ready) {
+            PXS_TRY(build_map(ccur, n, b.map[mc], stream));
+            map_ready = true;
+        }
         for (int k = 0; k < cfg->num_blocks[l]; ++k, ++bi) {
             const pxs_decoder_block & blk = blocks[bi];
             PXS_CHECK(blk.kind == PXS_DECODER_CONVNEXT, PXS_ERR_ARG,
@@ -374,7 +409,8 @@ int pxs_slat_decoder_forward(int dtype, const pxs_decoder_config * cfg,
             PXS_CHECK(blk.channels == C, PXS_ERR_ARG,
                       "pxs_slat_decoder_forward: block channels do not match the level");
             PXS_TRY(pxs_convnext_block(dtype, ccur, n, b.hid[cur], C, blk.mlp_hidden, eps, &blk.w,
-                                       b.map.nbr, b.map.masks, b.hid[cur], b.block_ws, stream));
+                                       b.map[mc].nbr, b.map[mc].masks, b.hid[cur], b.block_ws,
+                                       stream));
         }
         if (l + 1 == levels) break;
         const pxs_decoder_block & blk = blocks[bi++];
@@ -390,12 +426,14 @@ int pxs_slat_decoder_forward(int dtype, const pxs_decoder_config * cfg,
         const float * g = (!upsample && guide) ? guide[l] : nullptr;
         float * logits = (!upsample && predicted) ? predicted[l] : nullptr;
         int64_t m = 0;
-        PXS_TRY(pxs_resblock_c2s(dtype, ccur, n, b.hid[cur], C, blk.out_channels, eps, &blk.w,
-                                 pred ? 1 : 0, g, logits, b.crd[nxt], b.hid[nxt], &m, b.block_ws,
-                                 stream));
+        PXS_TRY(resblock_c2s(dtype, ccur, n, b.hid[cur], C, blk.out_channels, eps, &blk.w,
+                             pred ? 1 : 0, g, logits, b.crd[nxt], b.hid[nxt], &m, b.block_ws,
+                             stream, &b.map[mc], &b.map[1 - mc]));
         ccur = b.crd[nxt];
         cur = nxt;
         n = m;
+        mc = 1 - mc;
+        map_ready = m > 0;  // with no children the block returns before building it
         if (level_rows) level_rows[l + 1] = n;
     }
     // Final layer norm (eps 1e-5, no affine) and output linear
