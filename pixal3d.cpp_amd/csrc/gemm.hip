@@ -1018,26 +1018,24 @@ constexpr int kOrderedPitch = kOrderedChunk + 1;   // odd pitch: lane l reads ba
 // Rows pass through LDS 32 channels at a time, loaded by the whole workgroup
 // with coalesced (16-byte where possible) reads, so each thread walks its own
 // row from LDS instead of striding 4 x cin bytes between lanes in global
-// memory.  The weights sit in LDS too (read as broadcasts).  Dynamic LDS:
-// ordered_rows_lds_bytes(cout, cin).
+// memory.  The weights are read at wave-uniform addresses (scalar loads into
+// SGPRs, 8 inputs at a time), so the multiply-adds take them as operands.
+template <int COUT>
 __global__ void __launch_bounds__(kOrderedRows)
 ordered_linear_rows_kernel(const float * __restrict__ x, int64_t rows, int cin,
                            const float * __restrict__ weight, const float * __restrict__ bias,
-                           int cout, bool vec4, float * __restrict__ y) {
+                           bool vec4, float * __restrict__ y) {
 #pragma clang fp contract(off)
-    extern __shared__ __align__(16) float ordered_lds[];
-    float * w_lds = ordered_lds;
-    float * x_lds = ordered_lds + ((cout * cin + 3) & ~3);
-    for (int e = threadIdx.x; e < cout * cin; e += blockDim.x) w_lds[e] = weight[e];
+    __shared__ float x_lds[kOrderedRows * kOrderedPitch];
     const int t = threadIdx.x;
     const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kOrderedRows;
     const int nrows = static_cast<int>(rows - row0 < kOrderedRows ? rows - row0 : kOrderedRows);
-    float acc[kOrderedRowOut];
+    float acc[COUT];
 #pragma unroll
-    for (int o = 0; o < kOrderedRowOut; ++o) acc[o] = (o < cout && bias) ? bias[o] : 0.0f;
+    for (int o = 0; o < COUT; ++o) acc[o] = bias ? bias[o] : 0.0f;
     for (int k0 = 0; k0 < cin; k0 += kOrderedChunk) {
         const int kw = cin - k0 < kOrderedChunk ? cin - k0 : kOrderedChunk;
-        __syncthreads();  // the previous chunk is consumed (and the weights are in)
+        __syncthreads();  // the previous chunk is consumed
         if (vec4) {
             for (int e = t; e < kOrderedRows * (kOrderedChunk / 4); e += kOrderedRows) {
                 const int r = e / (kOrderedChunk / 4), c = (e % (kOrderedChunk / 4)) * 4;
@@ -1057,39 +1055,46 @@ ordered_linear_rows_kernel(const float * __restrict__ x, int64_t rows, int cin,
         __syncthreads();
         if (t < nrows) {
             const float * xr = x_lds + t * kOrderedPitch;
-            for (int j = 0; j < kw; ++j) {
+            const float * wk = weight + k0;  // row o of this chunk starts at wk + o * cin
+            int j = 0;
+            for (; j + 8 <= kw; j += 8) {
+                float xv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = xr[j + e];
+#pragma unroll
+                for (int o = 0; o < COUT; ++o) {
+                    const float * wo = wk + o * cin + j;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[o] += wo[e] * xv[e];
+                }
+            }
+            for (; j < kw; ++j) {
                 const float xv = xr[j];
 #pragma unroll
-                for (int o = 0; o < kOrderedRowOut; ++o)
-                    if (o < cout) acc[o] += w_lds[o * cin + k0 + j] * xv;
+                for (int o = 0; o < COUT; ++o) acc[o] += wk[o * cin + j] * xv;
             }
         }
     }
     if (t >= nrows) return;
 #pragma unroll
-    for (int o = 0; o < kOrderedRowOut; ++o)
-        if (o < cout) y[(row0 + t) * cout + o] = acc[o];
-}
-
-constexpr size_t ordered_rows_lds_bytes(int cout, int cin) {
-    return (static_cast<size_t>((cout * cin + 3) & ~3) + kOrderedRows * kOrderedPitch) * sizeof(float);
+    for (int o = 0; o < COUT; ++o) y[(row0 + t) * COUT + o] = acc[o];
 }
 
 int launch_ordered_rows(const float * x, int64_t rows, int cin, const float * weight,
                         const float * bias, int cout, float * y, hipStream_t s) {
-    static bool configured = false;
-    if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&ordered_linear_rows_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           static_cast<int>(ordered_rows_lds_bytes(kOrderedRowOut, kOrderedRowCin)));
-        if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(ordered_linear_rows)");
-        configured = true;
-    }
     const bool vec4 = cin % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    hipLaunchKernelGGL(ordered_linear_rows_kernel,
-                       dim3(static_cast<unsigned>((rows + kOrderedRows - 1) / kOrderedRows)),
-                       dim3(kOrderedRows), ordered_rows_lds_bytes(cout, cin), s, x, rows, cin, weight,
-                       bias, cout, vec4, y);
+    const dim3 grid(static_cast<unsigned>((rows + kOrderedRows - 1) / kOrderedRows));
+    switch (cout) {
+#define PXS_ORDERED_ROWS(N)                                                                       \
+    case N:                                                                                    \
+        hipLaunchKernelGGL(ordered_linear_rows_kernel<N>, grid, dim3(kOrderedRows), 0, s, x, rows, \
+                           cin, weight, bias, vec4, y);                                       \
+        break;
+        PXS_ORDERED_ROWS(1) PXS_ORDERED_ROWS(2) PXS_ORDERED_ROWS(3) PXS_ORDERED_ROWS(4)
+        PXS_ORDERED_ROWS(5) PXS_ORDERED_ROWS(6) PXS_ORDERED_ROWS(7) PXS_ORDERED_ROWS(8)
+#undef PXS_ORDERED_ROWS
+    default: return fail(PXS_ERR_ARG, "ordered linear (rows): at most 8 outputs");
+    }
     return check_launch("ordered linear (rows)");
 }
 
