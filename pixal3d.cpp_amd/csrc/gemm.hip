@@ -909,7 +909,11 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
             if (PXS_GEMM_WIDE && args.rowmap && args.cout > 128 && kstages >= 32)
                 return launch_lds_tile<T, 128, 256, EPI, 2, 8, 2, 1>(args, stream);
         }
-        return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES, 4, 2, 1>(args, stream)
+#ifndef PXS_GEMM_NARROW_KSPLIT
+#define PXS_GEMM_NARROW_KSPLIT 2
+#endif
+        constexpr int narrow_ks = sizeof(T) == 2 ? PXS_GEMM_NARROW_KSPLIT : 1;
+        return narrow ? launch_lds_tile<T, 128, 64, EPI, PXS_GEMM_STAGES, 4 * narrow_ks, 2, narrow_ks>(args, stream)
                       : launch_lds_tile<T, PXS_GEMM_BM, PXS_GEMM_BN, EPI, PXS_GEMM_STAGES,
                                         PXS_GEMM_WAVES, waves_m, ksplit>(args, stream);
     }
