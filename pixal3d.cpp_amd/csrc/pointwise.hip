@@ -336,6 +336,61 @@ qkv_prepare64_kernel(const T * __restrict__ qkv, int64_t rows, int heads,
     for (int c = lane * 8; c < C; c += 512) Vec8<T>::copy(src + 2 * C + c, vd + c);
 }
 
+// The standalone head RMS norm / RoPE (pxs_mh_rms_norm, pxs_rope) at
+// head_dim 64: the QKV prologue's layout (one wavefront per row, 8 lanes of
+// 8 dims per head, 8 heads per pass, the RMS over the head's 8 lanes, RoPE
+// pairs lane-local with per-row sin/cos).  x may be y.
+template <typename T>
+__global__ void __launch_bounds__(64 * kRowsPerBlock)
+head_op64_kernel(const T * __restrict__ x, int64_t ld_x, int64_t rows, int heads,
+                 const float * __restrict__ gamma, const int32_t * __restrict__ coords,
+                 RopeTable rope, T * __restrict__ y, int64_t ld_y) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int sub = lane & 7, hl = lane >> 3;
+    float cs[4] = {1.0f, 1.0f, 1.0f, 1.0f}, sn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (coords) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int p = sub * 4 + i;
+            if (p < 3 * rope.fdim) {
+                const float phase = static_cast<float>(coords[row * 4 + 1 + p / rope.fdim]) *
+                                    rope.freq[p % rope.fdim];
+                cs[i] = cosf(phase);
+                sn[i] = sinf(phase);
+            }
+        }
+    }
+    for (int hb = 0; hb < heads; hb += 8) {
+        const int h = hb + hl;
+        const bool on = h < heads;  // idle lanes still join the shuffles
+        const int d0 = (on ? h : 0) * 64 + sub * 8;
+        float val[8];
+        Vec8<T>::load(x + row * ld_x + d0, val);
+        if (gamma) {
+            float sq = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sq += val[i] * val[i];
+            sq += __shfl_xor(sq, 1, 64);
+            sq += __shfl_xor(sq, 2, 64);
+            sq += __shfl_xor(sq, 4, 64);
+            const float inv = 1.0f / fmaxf(sqrtf(sq), 1e-12f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) val[i] = val[i] * inv * 8.0f * gamma[d0 + i];  // sqrt(64) = 8
+        }
+        if (coords) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = val[2 * i], o = val[2 * i + 1];
+                val[2 * i] = e * cs[i] - o * sn[i];
+                val[2 * i + 1] = e * sn[i] + o * cs[i];
+            }
+        }
+        if (on) Vec8<T>::store(y + row * ld_y + d0, val);
+    }
+}
+
 template <typename T>
 __global__ void split_copy_kernel(const T * __restrict__ qkv, int64_t rows, int C, int part,
                                   T * __restrict__ out) {
@@ -654,6 +709,13 @@ template <typename T>
 int run_head_op(const void * x, int64_t ld_x, int64_t rows, int heads, int head_dim,
                 const float * gamma, const int32_t * coords, const RopeTable & rope, void * y,
                 int64_t ld_y, hipStream_t s) {
+    if (head_dim == 64 && ld_x % 8 == 0 && ld_y % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
+        hipLaunchKernelGGL(head_op64_kernel<T>, dim3(grid_for(rows, kRowsPerBlock)),
+                           dim3(64 * kRowsPerBlock), 0, s, static_cast<const T *>(x), ld_x, rows,
+                           heads, gamma, coords, rope, static_cast<T *>(y), ld_y);
+        return check_launch("head norm/rope");
+    }
     const int64_t items = rows * heads;
     hipLaunchKernelGGL(head_norm_rope_kernel<T>, dim3(grid_for(items, 256)), dim3(256), 0, s,
                        static_cast<const T *>(x), ld_x, rows, heads, head_dim, gamma, coords, rope,

@@ -260,3 +260,33 @@ def test_elementwise_vector_paths_match_element_loops(px, dtype):
         want = a.float() + skip.repeat_interleave(ch // sk, dim=1)
         assert torch.equal(got, want), f"add_repeat {ch}/{sk} {dtype}"
 
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_head_norm_rope_64(px, orc, dtype):
+    """pxs_mh_rms_norm and pxs_rope at head_dim 64 (one wavefront per row, 8
+    lanes of 8 dims per head): 12 heads (the second pass of 8 heads half
+    idle), a strided input (row stride 2C, as for the cross-attention keys)
+    and an in-place call, against the oracle."""
+    import torch
+    import pxs
+    rows, H, D = 3001, 12, 64
+    C = H * D
+    rng = np.random.default_rng(94)
+    coords = np.concatenate([np.zeros((rows, 1), np.int32),
+                             rng.integers(0, 64, (rows, 3)).astype(np.int32)], axis=1)
+    x2 = (W.normal(93, rows * 2 * C, 1) * 2).reshape(rows, 2 * C)
+    g = W.normal(93, C, 2) * np.float32(0.5) + np.float32(1.0)
+    conv = t32 if dtype == "f32" else tbf
+    check = assert_fp32 if dtype == "f32" else assert_bf16
+    xr = (x2 if dtype == "f32" else W.bf16_round(x2))[:, :C]
+    xd = conv(x2)
+    check(host(px.mh_rms_norm(xd[:, :C], H, D, t32(g))), orc.mh_rms_norm(xr, H, D, g),
+          what=f"rms strided {dtype}")
+    check(host(px.rope(ti32(coords), xd[:, :C], H, D)), orc.rope(coords, xr, H, D),
+          what=f"rope strided {dtype}")
+    xc = conv(np.ascontiguousarray(x2[:, :C]))
+    gd = t32(g)
+    px._check(px.lib.pxs_mh_rms_norm(pxs._dtype_code(xc), pxs._ptr(xc), C, rows, H, D,
+                                     pxs._ptr(gd), pxs._ptr(xc), C, px.stream()), "in place")
+    check(host(xc), orc.mh_rms_norm(xr, H, D, g), what=f"rms in place {dtype}")
+
