@@ -105,11 +105,12 @@ __device__ __forceinline__ void store_vec(TY * p, const float (&v)[N]) {
     }
 }
 
-template <typename TX, typename TY, int L, int NV>
+template <typename TX, typename TY, int L, int NV, bool kModulate>
 __global__ void __launch_bounds__(256)
 layer_norm_rows_kernel(const TX * __restrict__ x, int64_t rows, float eps,
                        const float * __restrict__ gamma, const float * __restrict__ beta,
-                       TY * __restrict__ y) {
+                       const int32_t * __restrict__ coords, const float * __restrict__ block_mod,
+                       const float * __restrict__ time_mod, int mod_offset, TY * __restrict__ y) {
     constexpr int V = Vec16<TX>::kN;
     constexpr int C = L * NV * V;
     const int lane = threadIdx.x & 63;
@@ -143,14 +144,40 @@ layer_norm_rows_kernel(const TX * __restrict__ x, int64_t rows, float eps,
     const float var = group_sum<L>(q) / static_cast<float>(C);
     const float inv = 1.0f / sqrtf(var + eps);
     if (!live) return;
+    const float * tm = nullptr;
+    if constexpr (kModulate) tm = time_mod + static_cast<int64_t>(coords[row * 4]) * 6 * C;
+    // Per-channel vectors in 16-byte pieces that match the lane's data (the
+    // row is 16-byte aligned and so are the channel offsets used here).
+    auto load_v = [&](const float * p, float (&w)[V]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < V; q += 4) {
+            const float4 f = *reinterpret_cast<const float4 *>(p + q);
+            w[q] = f.x; w[q + 1] = f.y; w[q + 2] = f.z; w[q + 3] = f.w;
+        }
+    };
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c0 = (j * L + part) * V;
-        float o[V];
+        float o[V], ga[V], be[V], bs[V], ts[V], bh[V], th[V];
+        if (gamma) {
+            load_v(gamma + c0, ga);
+            load_v(beta + c0, be);
+        }
+        if constexpr (kModulate) {
+            load_v(block_mod + mod_offset + C + c0, bs);
+            load_v(tm + mod_offset + C + c0, ts);
+            load_v(block_mod + mod_offset + c0, bh);
+            load_v(tm + mod_offset + c0, th);
+        }
 #pragma unroll
         for (int e = 0; e < V; ++e) {
             float val = (v[j][e] - mean) * inv;
-            if (gamma) val = val * gamma[c0 + e] + beta[c0 + e];
+            if (gamma) val = val * ga[e] + be[e];
+            if constexpr (kModulate) {
+                const float scale = bs[e] + ts[e];
+                const float shift = bh[e] + th[e];
+                val = val * (1.0f + scale) + shift;
+            }
             o[e] = val;
         }
         store_vec<TY, V>(y + row * C + c0, o);
@@ -644,33 +671,37 @@ __global__ void timestep_embedding_kernel(const float * __restrict__ t, int64_t 
 
 int check_dtype(int dtype) { return dtype == PXS_F32 || dtype == PXS_BF16; }
 
-template <typename TX, typename TY, int L, int NV>
+template <typename TX, typename TY, int L, int NV, bool kMod>
 void launch_ln_rows(const void * x, int64_t rows, float eps, const float * gamma,
-                    const float * beta, void * y, hipStream_t s) {
-    hipLaunchKernelGGL((layer_norm_rows_kernel<TX, TY, L, NV>), dim3(grid_for(rows, 4 * (64 / L))),
-                       dim3(256), 0, s, static_cast<const TX *>(x), rows, eps, gamma, beta,
+                    const float * beta, const int32_t * coords, const float * bm, const float * tm,
+                    int off, void * y, hipStream_t s) {
+    hipLaunchKernelGGL((layer_norm_rows_kernel<TX, TY, L, NV, kMod>),
+                       dim3(grid_for(rows, 4 * (64 / L))), dim3(256), 0, s,
+                       static_cast<const TX *>(x), rows, eps, gamma, beta, coords, bm, tm, off,
                        static_cast<TY *>(y));
 }
 
 // The row-group kernel when a row is 2^k 16-byte vectors (up to 64 lanes of
 // one vector, or 64 lanes of 2 or 4) and both buffers are 16-byte aligned.
-template <typename TX, typename TY>
+template <typename TX, typename TY, bool kMod>
 bool try_ln_rows(const void * x, int64_t rows, int channels, float eps, const float * gamma,
-                 const float * beta, void * y, hipStream_t s) {
+                 const float * beta, const int32_t * coords, const float * bm, const float * tm,
+                 int off, void * y, hipStream_t s) {
     constexpr int V = Vec16<TX>::kN;
-    if (channels % V != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0 ||
-        (reinterpret_cast<uintptr_t>(y) & 15) != 0)
+    auto a16 = [](const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (channels % V != 0 || !a16(x) || !a16(y) || (gamma && (!a16(gamma) || !a16(beta))))
         return false;
+    if (kMod && (!a16(bm) || !a16(tm) || off % 4 != 0)) return false;
     switch (channels / V) {
-    case 1: launch_ln_rows<TX, TY, 1, 1>(x, rows, eps, gamma, beta, y, s); return true;
-    case 2: launch_ln_rows<TX, TY, 2, 1>(x, rows, eps, gamma, beta, y, s); return true;
-    case 4: launch_ln_rows<TX, TY, 4, 1>(x, rows, eps, gamma, beta, y, s); return true;
-    case 8: launch_ln_rows<TX, TY, 8, 1>(x, rows, eps, gamma, beta, y, s); return true;
-    case 16: launch_ln_rows<TX, TY, 16, 1>(x, rows, eps, gamma, beta, y, s); return true;
-    case 32: launch_ln_rows<TX, TY, 32, 1>(x, rows, eps, gamma, beta, y, s); return true;
-    case 64: launch_ln_rows<TX, TY, 64, 1>(x, rows, eps, gamma, beta, y, s); return true;
-    case 128: launch_ln_rows<TX, TY, 64, 2>(x, rows, eps, gamma, beta, y, s); return true;
-    case 256: launch_ln_rows<TX, TY, 64, 4>(x, rows, eps, gamma, beta, y, s); return true;
+    case 1: launch_ln_rows<TX, TY, 1, 1, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
+    case 2: launch_ln_rows<TX, TY, 2, 1, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
+    case 4: launch_ln_rows<TX, TY, 4, 1, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
+    case 8: launch_ln_rows<TX, TY, 8, 1, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
+    case 16: launch_ln_rows<TX, TY, 16, 1, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
+    case 32: launch_ln_rows<TX, TY, 32, 1, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
+    case 64: launch_ln_rows<TX, TY, 64, 1, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
+    case 128: launch_ln_rows<TX, TY, 64, 2, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
+    case 256: launch_ln_rows<TX, TY, 64, 4, kMod>(x, rows, eps, gamma, beta, coords, bm, tm, off, y, s); return true;
     default: return false;
     }
 }
@@ -682,9 +713,9 @@ void launch_ln(const void * x, int64_t rows, int channels, float eps, const floa
 #ifndef PXS_LN_ROWS
 #define PXS_LN_ROWS 1
 #endif
-    if constexpr (!kMod) {
-        if (PXS_LN_ROWS && try_ln_rows<TX, TY>(x, rows, channels, eps, gamma, beta, y, s)) return;
-    }
+    if (PXS_LN_ROWS &&
+        try_ln_rows<TX, TY, kMod>(x, rows, channels, eps, gamma, beta, coords, bm, tm, off, y, s))
+        return;
     hipLaunchKernelGGL((layer_norm_kernel<TX, TY, kMod>), dim3(grid_for(rows, kRowsPerBlock)),
                        dim3(64 * kRowsPerBlock), 0, s, static_cast<const TX *>(x), rows, channels,
                        eps, gamma, beta, coords, bm, tm, off, static_cast<TY *>(y));
