@@ -1,0 +1,153 @@
+// Plain bf16 linears (sparse_linear / varlen_linear, src/sparse.cpp:337-488,
+// with the block's residual adds) through hipBLASLt: these are dense GEMMs
+// over rows, with no gather, where the library's kernels run 1.7-2x the
+// gather-GEMM kernel of gemm.hip.  Column-major view of the row-major
+// operands: D (cout x rows, ld cout) = op(A) B with A = the weight
+// [cout, cin] row-major read as cin x cout and transposed, B = x (cin x rows).
+// The fp32 bias is the epilogue's bias vector (one per D row, i.e. per output
+// channel); GELU (tanh form) is the epilogue's GELU; a residual add is
+// C = D = the fp32 residual with beta = 1.
+//
+// One handle per device; matrix layouts and the heuristic's algorithm are
+// cached per shape, the matmul descriptor (which holds the bias pointer) is
+// made per call.  No workspace is requested, so nothing is allocated per call;
+// a shape for which the heuristic offers no algorithm is left to the caller.
+
+#include "pxs_common.h"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+namespace pxs {
+namespace {
+
+struct Shape {
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    bool ok = false;
+};
+
+// (device, rows, cin, cout, epilogue, D type, accumulate)
+using ShapeKey = std::tuple<int, int64_t, int, int, int, int, int>;
+
+std::mutex g_mutex;
+std::map<int, hipblasLtHandle_t> g_handles;
+std::map<ShapeKey, Shape> g_shapes;
+
+bool set_desc(hipblasLtMatmulDesc_t desc, hipblasLtMatmulDescAttributes_t attr, const void * v,
+              size_t bytes) {
+    return hipblasLtMatmulDescSetAttribute(desc, attr, v, bytes) == HIPBLAS_STATUS_SUCCESS;
+}
+
+// The descriptor of one call: transposes, epilogue and its bias.
+hipblasLtMatmulDesc_t make_desc(hipblasLtEpilogue_t epi, const float * bias) {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    if (hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
+        return nullptr;
+    const hipblasOperation_t op_t = HIPBLAS_OP_T, op_n = HIPBLAS_OP_N;
+    const uint32_t e = static_cast<uint32_t>(epi);
+    bool ok = set_desc(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_t, sizeof(op_t)) &&
+              set_desc(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_n, sizeof(op_n)) &&
+              set_desc(desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &e, sizeof(e));
+    if (ok && bias) {
+        const hipDataType bt = HIP_R_32F;
+        ok = set_desc(desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) &&
+             set_desc(desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
+    }
+    if (!ok) {
+        hipblasLtMatmulDescDestroy(desc);
+        return nullptr;
+    }
+    return desc;
+}
+
+// The cached layouts and algorithm of a shape, or nullptr (no algorithm).
+const Shape * shape_for(int device, hipblasLtHandle_t handle, int64_t rows, int cin, int cout,
+                        hipblasLtEpilogue_t epi, hipDataType dtype_d, bool accumulate) {
+    const ShapeKey key{device, rows, cin, cout, static_cast<int>(epi), static_cast<int>(dtype_d),
+                       accumulate ? 1 : 0};
+    auto it = g_shapes.find(key);
+    if (it != g_shapes.end()) return it->second.ok ? &it->second : nullptr;
+    Shape sh;
+    bool ok = hipblasLtMatrixLayoutCreate(&sh.a, HIP_R_16BF, cin, cout, cin) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&sh.b, HIP_R_16BF, cin, rows, cin) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&sh.c, dtype_d, cout, rows, cout) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulDesc_t desc = ok ? make_desc(epi, nullptr) : nullptr;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    if (desc && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS) {
+        const uint64_t ws = 0;
+        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                              sizeof(ws));
+        hipblasLtMatmulHeuristicResult_t result{};
+        int found = 0;
+        if (hipblasLtMatmulAlgoGetHeuristic(handle, desc, sh.a, sh.b, sh.c, sh.c, pref, 1, &result,
+                                            &found) == HIPBLAS_STATUS_SUCCESS &&
+            found > 0 && result.state == HIPBLAS_STATUS_SUCCESS && result.workspaceSize == 0) {
+            sh.algo = result.algo;
+            sh.ok = true;
+        }
+        hipblasLtMatmulPreferenceDestroy(pref);
+    }
+    if (desc) hipblasLtMatmulDescDestroy(desc);
+    auto & slot = g_shapes[key];
+    slot = sh;
+    return slot.ok ? &slot : nullptr;
+}
+
+bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+} // namespace
+
+// y (rows x cout, y_dtype) = x W^T + bias, then act (PXS_ACT_NONE or
+// PXS_ACT_GELU_TANH); with accumulate, y (fp32) += x W^T + bias.  Returns
+// PXS_OK and sets *done when hipBLASLt ran it; leaves *done false when the
+// shape is not one it takes (the caller runs its own kernel).
+int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, const float * bias,
+                       int cout, int act, int y_dtype, void * y, bool accumulate, hipStream_t s,
+                       bool * done) {
+    *done = false;
+#ifndef PXS_BLASLT
+#define PXS_BLASLT 1
+#endif
+    if (!PXS_BLASLT) return PXS_OK;
+    if (act != PXS_ACT_NONE && act != PXS_ACT_GELU_TANH) return PXS_OK;
+    if (accumulate && (y_dtype != PXS_F32 || act != PXS_ACT_NONE)) return PXS_OK;
+    if (rows < 256 || cin % 8 != 0 || cout % 8 != 0 || !aligned16(x) || !aligned16(w) ||
+        !aligned16(y) || (bias && !aligned16(bias)))
+        return PXS_OK;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return PXS_OK;
+    const hipblasLtEpilogue_t epi =
+        act == PXS_ACT_GELU_TANH ? (bias ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_GELU)
+                                 : (bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT);
+    const hipDataType dtype_d = y_dtype == PXS_F32 ? HIP_R_32F : HIP_R_16BF;
+    hipblasLtHandle_t handle = nullptr;
+    const Shape * sh = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        auto hit = g_handles.find(device);
+        if (hit == g_handles.end()) {
+            hipblasLtHandle_t h = nullptr;
+            if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) h = nullptr;
+            hit = g_handles.emplace(device, h).first;
+        }
+        handle = hit->second;
+        if (!handle) return PXS_OK;
+        sh = shape_for(device, handle, rows, cin, cout, epi, dtype_d, accumulate);
+    }
+    if (!sh) return PXS_OK;
+    hipblasLtMatmulDesc_t desc = make_desc(epi, bias);
+    if (!desc) return PXS_OK;
+    const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
+    const hipblasStatus_t st = hipblasLtMatmul(handle, desc, &alpha, w, sh->a, x, sh->b, &beta, y,
+                                               sh->c, y, sh->c, &sh->algo, nullptr, 0, s);
+    hipblasLtMatmulDescDestroy(desc);
+    if (st != HIPBLAS_STATUS_SUCCESS) return fail(PXS_ERR_HIP, "hipblasLtMatmul failed");
+    *done = true;
+    return check_launch("hipblasLtMatmul");
+}
+
+} // namespace pxs

@@ -1153,6 +1153,13 @@ int pxs_linear(int dtype, const void * x, int64_t rows, int cin, const void * we
         return launch_ordered_rows(static_cast<const float *>(x), rows, cin,
                                    static_cast<const float *>(weight), bias, cout,
                                    static_cast<float *>(y), as_stream(stream));
+    if (dtype == PXS_BF16) {
+        bool done = false;
+        if (int rc = blaslt_linear_bf16(x, rows, cin, weight, bias, cout, act, PXS_BF16, y, false,
+                                        as_stream(stream), &done))
+            return rc;
+        if (done) return PXS_OK;
+    }
     GemmArgs a{};
     a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
     a.cout = cout; a.m = rows; a.rowmap = nullptr; a.ld_map = 0; a.noff = 1; a.masks = nullptr;
@@ -1185,6 +1192,13 @@ int pxs_linear_residual(int dtype, const void * x, int64_t rows, int cin, const 
     PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear_residual: bad shape");
     if (rows == 0) return PXS_OK;
     PXS_CHECK(x && weight && residual, PXS_ERR_ARG, "pxs_linear_residual: null pointer");
+    if (dtype == PXS_BF16) {
+        bool done = false;
+        if (int rc = blaslt_linear_bf16(x, rows, cin, weight, bias, cout, PXS_ACT_NONE, PXS_F32,
+                                        residual, true, as_stream(stream), &done))
+            return rc;
+        if (done) return PXS_OK;
+    }
     GemmArgs a{};
     a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
     a.cout = cout; a.m = rows; a.noff = 1; a.y = nullptr; a.ldy = cout; a.residual = residual;

@@ -18,6 +18,12 @@ int fail_workspace(const char * what) noexcept;
 int check_hip(hipError_t status, const char * what);
 int check_launch(const char * what);
 
+// Plain bf16 linears through hipBLASLt (csrc/blaslt.cpp): sets *done when it
+// ran the product, leaves it false for shapes it does not take.
+int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, const float * bias,
+                       int cout, int act, int y_dtype, void * y, bool accumulate, hipStream_t s,
+                       bool * done);
+
 #define PXS_CHECK(expr, code, msg)            \
     do {                                      \
         if (!(expr)) return ::pxs::fail((code), (msg)); \
