@@ -28,6 +28,7 @@ struct BlockBuffers {
     void * att;   // [rows, C]       attention output
     void * ckv;   // [T, 2C]         context K | V
     void * ck;    // [T, C]          RMS-normed context K
+    float * lin;  // [rows, C] fp32  a gated linear's output before its gate (bf16 only)
     void * attn_ws;
 };
 
@@ -47,6 +48,7 @@ BlockBuffers carve_block(Carver & c, int dtype, const pxs_block_config & cfg, in
     b.att = c.take(r * C * e);
     b.ckv = c.take(t * 2 * C * e);
     b.ck = c.take(t * C * e);
+    b.lin = dtype == PXS_BF16 ? static_cast<float *>(c.take(r * C * 4)) : nullptr;
     b.attn_ws = c.take(pxs_attention_workspace_bytes(batch_size));
     return b;
 }
@@ -98,9 +100,9 @@ int run_block(int dtype, const pxs_block_config & cfg, const pxs_block_weights &
                             cfg.rope_freq_base, b.q, b.k, b.v, stream));
     PXS_TRY(pxs_varlen_attention(dtype, b.q, C, b.k, C, b.v, C, cu_rows, cu_rows, batch_size, rows,
                                  nullptr, H, hd, hd, scale, b.att, C, b.attn_ws, stream));
-    PXS_TRY(pxs_linear_gate_residual(dtype, b.att, rows, C, w.self_to_out_weight,
-                                     w.self_to_out_bias, C, coords, w.modulation, time_mod, 2 * C,
-                                     hidden, stream));
+    PXS_TRY(linear_gate_residual_scratch(dtype, b.att, rows, C, w.self_to_out_weight,
+                                         w.self_to_out_bias, C, coords, w.modulation, time_mod,
+                                         2 * C, hidden, b.lin, as_stream(stream)));
 
     // Cross-attention branch.
     PXS_TRY(pxs_layer_norm(PXS_F32, hidden, rows, C, cfg.norm_eps, w.norm2_weight, w.norm2_bias,
@@ -136,9 +138,9 @@ int run_block(int dtype, const pxs_block_config & cfg, const pxs_block_weights &
                                     time_mod, 3 * C, dtype, b.xm, stream));
     PXS_TRY(pxs_linear(dtype, b.xm, rows, C, w.mlp0_weight, w.mlp0_bias, cfg.mlp_hidden,
                        PXS_ACT_GELU_TANH, b.big, stream));
-    PXS_TRY(pxs_linear_gate_residual(dtype, b.big, rows, cfg.mlp_hidden, w.mlp2_weight,
-                                     w.mlp2_bias, C, coords, w.modulation, time_mod, 5 * C,
-                                     hidden, stream));
+    PXS_TRY(linear_gate_residual_scratch(dtype, b.big, rows, cfg.mlp_hidden, w.mlp2_weight,
+                                         w.mlp2_bias, C, coords, w.modulation, time_mod, 5 * C,
+                                         hidden, b.lin, as_stream(stream)));
     return PXS_OK;
 }
 

@@ -1102,7 +1102,65 @@ int launch_ordered_rows(const float * x, int64_t rows, int cin, const float * we
     return check_launch("ordered linear (rows)");
 }
 
+// residual[r, c] += value[r, c] * (block_mod[off + c] + time_mod[batch(r), off + c]):
+// the gate-residual epilogue of gemm_epilogue over a linear's fp32 output
+// (value = x W^T + bias), 4 channels per thread.
+__global__ void gate_residual_kernel(const float * __restrict__ value, int64_t rows, int cout,
+                                     const int32_t * __restrict__ coords,
+                                     const float * __restrict__ block_mod,
+                                     const float * __restrict__ time_mod, int gate_offset,
+                                     float * __restrict__ residual) {
+    const int64_t vpr = cout / 4;
+    const int64_t total = rows * vpr;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += stride) {
+        const int64_t r = i / vpr;
+        const int c = static_cast<int>(i - r * vpr) * 4;
+        const int batch = coords[r * 4];
+        const float4 v = *reinterpret_cast<const float4 *>(value + r * cout + c);
+        const float4 b = *reinterpret_cast<const float4 *>(block_mod + gate_offset + c);
+        const float4 t = *reinterpret_cast<const float4 *>(
+            time_mod + static_cast<int64_t>(batch) * 6 * cout + gate_offset + c);
+        float4 * res = reinterpret_cast<float4 *>(residual + r * cout + c);
+        float4 o = *res;
+        o.x = o.x + v.x * (b.x + t.x);
+        o.y = o.y + v.y * (b.y + t.y);
+        o.z = o.z + v.z * (b.z + t.z);
+        o.w = o.w + v.w * (b.w + t.w);
+        *res = o;
+    }
+}
+
 } // namespace
+
+// pxs_linear_gate_residual with an fp32 scratch of rows x cout: bf16 products
+// hipBLASLt takes run there (bias in its epilogue), then the gate pass; the
+// rest run the fused kernel.
+int linear_gate_residual_scratch(int dtype, const void * x, int64_t rows, int cin,
+                                 const void * weight, const float * bias, int cout,
+                                 const int32_t * coords, const float * block_mod,
+                                 const float * time_mod, int gate_offset, float * residual,
+                                 float * scratch, hipStream_t s) {
+    auto a16 = [](const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (dtype == PXS_BF16 && scratch && rows > 0 && cout % 4 == 0 && gate_offset % 4 == 0 &&
+        a16(residual) && a16(block_mod) && a16(time_mod)) {
+        bool done = false;
+        if (int rc = blaslt_linear_bf16(x, rows, cin, weight, bias, cout, PXS_ACT_NONE, PXS_F32,
+                                        scratch, false, s, &done))
+            return rc;
+        if (done) {
+            const int64_t total = rows * (cout / 4);
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 16384));
+            hipLaunchKernelGGL(gate_residual_kernel, dim3(blocks), dim3(256), 0, s, scratch, rows,
+                               cout, coords, block_mod, time_mod, gate_offset, residual);
+            return check_launch("gate residual");
+        }
+    }
+    return pxs_linear_gate_residual(dtype, x, rows, cin, weight, bias, cout, coords, block_mod,
+                                    time_mod, gate_offset, residual, s);
+}
+
 } // namespace pxs
 
 using namespace pxs;

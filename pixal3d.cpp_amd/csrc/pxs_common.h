@@ -24,6 +24,13 @@ int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, co
                        int cout, int act, int y_dtype, void * y, bool accumulate, hipStream_t s,
                        bool * done);
 
+// pxs_linear_gate_residual given an fp32 scratch of rows x cout (csrc/gemm.hip).
+int linear_gate_residual_scratch(int dtype, const void * x, int64_t rows, int cin,
+                                 const void * weight, const float * bias, int cout,
+                                 const int32_t * coords, const float * block_mod,
+                                 const float * time_mod, int gate_offset, float * residual,
+                                 float * scratch, hipStream_t s);
+
 #define PXS_CHECK(expr, code, msg)            \
     do {                                      \
         if (!(expr)) return ::pxs::fail((code), (msg)); \
