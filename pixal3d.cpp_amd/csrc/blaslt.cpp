@@ -5,7 +5,8 @@
 // operands: D (cout x rows, ld cout) = op(A) B with A = the weight
 // [cout, cin] row-major read as cin x cout and transposed, B = x (cin x rows).
 // The fp32 bias is the epilogue's bias vector (one per D row, i.e. per output
-// channel); GELU (tanh form) is the epilogue's GELU; a residual add is
+// channel); GELU (tanh form) and SiLU are the epilogue's GELU and Swish(x, 1)
+// (x * sigmoid(x)); a residual add is
 // C = D = the fp32 residual with beta = 1.
 //
 // One handle per device; matrix layouts and the heuristic's algorithm are
@@ -101,10 +102,10 @@ bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) =
 
 } // namespace
 
-// y (rows x cout, y_dtype) = x W^T + bias, then act (PXS_ACT_NONE or
-// PXS_ACT_GELU_TANH); with accumulate, y (fp32) += x W^T + bias.  Returns
-// PXS_OK and sets *done when hipBLASLt ran it; leaves *done false when the
-// shape is not one it takes (the caller runs its own kernel).
+// y (rows x cout, y_dtype) = x W^T + bias, then act (PXS_ACT_NONE,
+// PXS_ACT_GELU_TANH or PXS_ACT_SILU); with accumulate, y (fp32) += x W^T +
+// bias.  Returns PXS_OK and sets *done when hipBLASLt ran it; leaves *done
+// false when the shape is not one it takes (the caller runs its own kernel).
 int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, const float * bias,
                        int cout, int act, int y_dtype, void * y, bool accumulate, hipStream_t s,
                        bool * done) {
@@ -113,7 +114,7 @@ int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, co
 #define PXS_BLASLT 1
 #endif
     if (!PXS_BLASLT) return PXS_OK;
-    if (act != PXS_ACT_NONE && act != PXS_ACT_GELU_TANH) return PXS_OK;
+    if (act != PXS_ACT_NONE && act != PXS_ACT_GELU_TANH && act != PXS_ACT_SILU) return PXS_OK;
     if (accumulate && (y_dtype != PXS_F32 || act != PXS_ACT_NONE)) return PXS_OK;
     if (rows < 256 || cin % 8 != 0 || cout % 8 != 0 || !aligned16(x) || !aligned16(w) ||
         !aligned16(y) || (bias && !aligned16(bias)))
@@ -122,6 +123,8 @@ int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, co
     if (hipGetDevice(&device) != hipSuccess) return PXS_OK;
     const hipblasLtEpilogue_t epi =
         act == PXS_ACT_GELU_TANH ? (bias ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_GELU)
+        : act == PXS_ACT_SILU
+            ? (bias ? HIPBLASLT_EPILOGUE_SWISH_BIAS_EXT : HIPBLASLT_EPILOGUE_SWISH_EXT)
                                  : (bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT);
     const hipDataType dtype_d = y_dtype == PXS_F32 ? HIP_R_32F : HIP_R_16BF;
     hipblasLtHandle_t handle = nullptr;
