@@ -290,3 +290,31 @@ def test_head_norm_rope_64(px, orc, dtype):
                                      pxs._ptr(gd), pxs._ptr(xc), C, px.stream()), "in place")
     check(host(xc), orc.mh_rms_norm(xr, H, D, g), what=f"rms in place {dtype}")
 
+
+@pytest.mark.parametrize("rows,cin,cout", [(4096, 256, 512), (300, 64, 96), (200, 64, 64),
+                                           (1000, 60, 64)])
+def test_linear_bf16_library_and_fallback(px, orc, rows, cin, cout):
+    """Plain bf16 linears: with at least 256 rows and widths that are
+    multiples of 8 they run through hipBLASLt (bias, GELU, SiLU epilogues, and
+    the residual add as beta = 1 into the fp32 residual); 200 rows and 60
+    inputs take the gather-GEMM kernel.  Against the oracle on the same
+    bf16-rounded operands, at the bf16 bar; without a bias too."""
+    import torch
+    import pxs
+    x = W.bf16_round(W.normal(95, rows * cin, 1).reshape(rows, cin))
+    w = W.bf16_round(W.normal(95, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin))
+    b = W.normal(95, cout, 3, std=0.1)
+    print(f"[linear bf16 paths] {rows}x{cin}->{cout}", flush=True)
+    lin = orc.linear(x, w, b)
+    for act, f in ((pxs.ACT_NONE, lambda v: v), (pxs.ACT_GELU_TANH, orc.gelu_tanh),
+                   (pxs.ACT_SILU, orc.silu)):
+        y = host(px.linear(tbf(x), tbf(w), t32(b), act=act))
+        assert_bf16(y, f(lin), what=f"bf16 linear act {act}")
+    y = host(px.linear(tbf(x), tbf(w), None))
+    assert_bf16(y, orc.linear(x, w, np.zeros(cout, np.float32)), what="bf16 linear, no bias")
+    res0 = W.normal(95, rows * cout, 4).reshape(rows, cout)
+    res = t32(res0)
+    px.linear_residual(tbf(x), tbf(w), t32(b), res)
+    torch.cuda.synchronize()
+    assert_bf16(host(res), res0 + lin, what="bf16 linear residual")
+
