@@ -1,7 +1,8 @@
-// Plain bf16 linears (sparse_linear / varlen_linear, src/sparse.cpp:337-488,
-// with the block's residual adds) through hipBLASLt: these are dense GEMMs
-// over rows, with no gather, where the library's kernels run 1.7-2x the
-// gather-GEMM kernel of gemm.hip.  Column-major view of the row-major
+// Plain linears (sparse_linear / varlen_linear, src/sparse.cpp:337-488, with
+// the block's residual adds), bf16 or fp32, through hipBLASLt: these are dense
+// GEMMs over rows, with no gather, where the library's kernels run 1.7-2x the
+// gather-GEMM kernels of gemm.hip (fp32 ones in full fp32: compute type 32F,
+// v_mfma_f32_*_f32).  Column-major view of the row-major
 // operands: D (cout x rows, ld cout) = op(A) B with A = the weight
 // [cout, cin] row-major read as cin x cout and transposed, B = x (cin x rows).
 // The fp32 bias is the epilogue's bias vector (one per D row, i.e. per output
@@ -10,9 +11,15 @@
 // C = D = the fp32 residual with beta = 1.
 //
 // One handle per device; matrix layouts and the heuristic's algorithm are
-// cached per shape, the matmul descriptor (which holds the bias pointer) is
-// made per call.  No workspace is requested, so nothing is allocated per call;
-// a shape for which the heuristic offers no algorithm is left to the caller.
+// cached per shape and workspace cap, the matmul descriptor (which holds the
+// bias pointer) is made per call.  The library's workspace is the caller's
+// (compositions carve kLibWorkspaceBytes from their own workspace; the plain
+// entry points have none, and then only algorithms that need no workspace
+// qualify): nothing is allocated per call.  Tall products over few channels
+// run 2-5x faster with one (2.5M x 64 -> 256 bf16: 377 against 866 us).  A
+// shape for which the heuristic offers no algorithm is left to the caller, and
+// so are the ones the gemm.hip kernels run faster: bf16 with at most 64 input
+// and output channels, fp32 under 2^26 multiply-adds.
 
 #include "pxs_common.h"
 
@@ -28,11 +35,12 @@ namespace {
 struct Shape {
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
+    size_t workspace = 0;
     bool ok = false;
 };
 
-// (device, rows, cin, cout, epilogue, D type, accumulate)
-using ShapeKey = std::tuple<int, int64_t, int, int, int, int, int>;
+// (device, rows, cin, cout, epilogue, A/B type, D type, accumulate, workspace cap)
+using ShapeKey = std::tuple<int, int64_t, int, int, int, int, int, int, size_t>;
 
 std::mutex g_mutex;
 std::map<int, hipblasLtHandle_t> g_handles;
@@ -67,27 +75,29 @@ hipblasLtMatmulDesc_t make_desc(hipblasLtEpilogue_t epi, const float * bias) {
 
 // The cached layouts and algorithm of a shape, or nullptr (no algorithm).
 const Shape * shape_for(int device, hipblasLtHandle_t handle, int64_t rows, int cin, int cout,
-                        hipblasLtEpilogue_t epi, hipDataType dtype_d, bool accumulate) {
-    const ShapeKey key{device, rows, cin, cout, static_cast<int>(epi), static_cast<int>(dtype_d),
-                       accumulate ? 1 : 0};
+                        hipblasLtEpilogue_t epi, hipDataType dtype_in, hipDataType dtype_d,
+                        bool accumulate, size_t ws_cap) {
+    const ShapeKey key{device, rows, cin, cout, static_cast<int>(epi), static_cast<int>(dtype_in),
+                       static_cast<int>(dtype_d), accumulate ? 1 : 0, ws_cap};
     auto it = g_shapes.find(key);
     if (it != g_shapes.end()) return it->second.ok ? &it->second : nullptr;
     Shape sh;
-    bool ok = hipblasLtMatrixLayoutCreate(&sh.a, HIP_R_16BF, cin, cout, cin) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&sh.b, HIP_R_16BF, cin, rows, cin) == HIPBLAS_STATUS_SUCCESS &&
+    bool ok = hipblasLtMatrixLayoutCreate(&sh.a, dtype_in, cin, cout, cin) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&sh.b, dtype_in, cin, rows, cin) == HIPBLAS_STATUS_SUCCESS &&
               hipblasLtMatrixLayoutCreate(&sh.c, dtype_d, cout, rows, cout) == HIPBLAS_STATUS_SUCCESS;
     hipblasLtMatmulDesc_t desc = ok ? make_desc(epi, nullptr) : nullptr;
     hipblasLtMatmulPreference_t pref = nullptr;
     if (desc && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS) {
-        const uint64_t ws = 0;
+        const uint64_t ws = ws_cap;
         hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
                                               sizeof(ws));
         hipblasLtMatmulHeuristicResult_t result{};
         int found = 0;
         if (hipblasLtMatmulAlgoGetHeuristic(handle, desc, sh.a, sh.b, sh.c, sh.c, pref, 1, &result,
                                             &found) == HIPBLAS_STATUS_SUCCESS &&
-            found > 0 && result.state == HIPBLAS_STATUS_SUCCESS && result.workspaceSize == 0) {
+            found > 0 && result.state == HIPBLAS_STATUS_SUCCESS && result.workspaceSize <= ws_cap) {
             sh.algo = result.algo;
+            sh.workspace = result.workspaceSize;
             sh.ok = true;
         }
         hipblasLtMatmulPreferenceDestroy(pref);
@@ -103,12 +113,14 @@ bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) =
 } // namespace
 
 // y (rows x cout, y_dtype) = x W^T + bias, then act (PXS_ACT_NONE,
-// PXS_ACT_GELU_TANH or PXS_ACT_SILU); with accumulate, y (fp32) += x W^T +
-// bias.  Returns PXS_OK and sets *done when hipBLASLt ran it; leaves *done
-// false when the shape is not one it takes (the caller runs its own kernel).
-int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, const float * bias,
-                       int cout, int act, int y_dtype, void * y, bool accumulate, hipStream_t s,
-                       bool * done) {
+// PXS_ACT_GELU_TANH or PXS_ACT_SILU), x and w of type dtype; with accumulate,
+// y (fp32) += x W^T + bias.  ws (256-byte aligned, ws_bytes; may be null) is
+// the library's workspace for this call.  Returns PXS_OK and sets *done when
+// hipBLASLt ran it; leaves *done false when the shape is not one it takes
+// (the caller runs its own kernel).
+int blaslt_linear(int dtype, const void * x, int64_t rows, int cin, const void * w,
+                  const float * bias, int cout, int act, int y_dtype, void * y, bool accumulate,
+                  void * ws, size_t ws_bytes, hipStream_t s, bool * done) {
     *done = false;
 #ifndef PXS_BLASLT
 #define PXS_BLASLT 1
@@ -116,9 +128,17 @@ int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, co
     if (!PXS_BLASLT) return PXS_OK;
     if (act != PXS_ACT_NONE && act != PXS_ACT_GELU_TANH && act != PXS_ACT_SILU) return PXS_OK;
     if (accumulate && (y_dtype != PXS_F32 || act != PXS_ACT_NONE)) return PXS_OK;
-    if (rows < 256 || cin % 8 != 0 || cout % 8 != 0 || !aligned16(x) || !aligned16(w) ||
+    if (dtype != PXS_BF16 && dtype != PXS_F32) return PXS_OK;
+    if (dtype == PXS_F32 && y_dtype != PXS_F32) return PXS_OK;
+    const int vec = dtype == PXS_BF16 ? 8 : 4;  // elements per 16 bytes
+    if (rows < 256 || cin % vec != 0 || cout % 8 != 0 || !aligned16(x) || !aligned16(w) ||
         !aligned16(y) || (bias && !aligned16(bias)))
         return PXS_OK;
+    // Shapes the gemm.hip kernels run faster (measured: bf16 64 -> 64 over
+    // 2.5M rows 228 against 258 us, fp32 16k x 64 -> 64 13 against 17 us).
+    if (dtype == PXS_BF16 && cin <= 64 && cout <= 64) return PXS_OK;
+    if (dtype == PXS_F32 && static_cast<double>(rows) * cin * cout < 67108864.0) return PXS_OK;
+    const size_t ws_cap = ws ? ws_bytes : 0;
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return PXS_OK;
     const hipblasLtEpilogue_t epi =
@@ -126,6 +146,7 @@ int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, co
         : act == PXS_ACT_SILU
             ? (bias ? HIPBLASLT_EPILOGUE_SWISH_BIAS_EXT : HIPBLASLT_EPILOGUE_SWISH_EXT)
                                  : (bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT);
+    const hipDataType dtype_in = dtype == PXS_F32 ? HIP_R_32F : HIP_R_16BF;
     const hipDataType dtype_d = y_dtype == PXS_F32 ? HIP_R_32F : HIP_R_16BF;
     hipblasLtHandle_t handle = nullptr;
     const Shape * sh = nullptr;
@@ -139,14 +160,15 @@ int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, co
         }
         handle = hit->second;
         if (!handle) return PXS_OK;
-        sh = shape_for(device, handle, rows, cin, cout, epi, dtype_d, accumulate);
+        sh = shape_for(device, handle, rows, cin, cout, epi, dtype_in, dtype_d, accumulate, ws_cap);
     }
     if (!sh) return PXS_OK;
     hipblasLtMatmulDesc_t desc = make_desc(epi, bias);
     if (!desc) return PXS_OK;
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     const hipblasStatus_t st = hipblasLtMatmul(handle, desc, &alpha, w, sh->a, x, sh->b, &beta, y,
-                                               sh->c, y, sh->c, &sh->algo, nullptr, 0, s);
+                                               sh->c, y, sh->c, &sh->algo,
+                                               sh->workspace ? ws : nullptr, sh->workspace, s);
     hipblasLtMatmulDescDestroy(desc);
     if (st != HIPBLAS_STATUS_SUCCESS) return fail(PXS_ERR_HIP, "hipblasLtMatmul failed");
     *done = true;

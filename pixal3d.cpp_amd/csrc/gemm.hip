@@ -1134,20 +1134,20 @@ __global__ void gate_residual_kernel(const float * __restrict__ value, int64_t r
 
 } // namespace
 
-// pxs_linear_gate_residual with an fp32 scratch of rows x cout: bf16 products
-// hipBLASLt takes run there (bias in its epilogue), then the gate pass; the
-// rest run the fused kernel.
+// pxs_linear_gate_residual with an fp32 scratch of rows x cout: products
+// hipBLASLt takes (bf16 or fp32) run there (bias in its epilogue), then the
+// gate pass; the rest run the fused kernel.
 int linear_gate_residual_scratch(int dtype, const void * x, int64_t rows, int cin,
                                  const void * weight, const float * bias, int cout,
                                  const int32_t * coords, const float * block_mod,
                                  const float * time_mod, int gate_offset, float * residual,
-                                 float * scratch, hipStream_t s) {
+                                 float * scratch, void * ws, size_t ws_bytes, hipStream_t s) {
     auto a16 = [](const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (dtype == PXS_BF16 && scratch && rows > 0 && cout % 4 == 0 && gate_offset % 4 == 0 &&
-        a16(residual) && a16(block_mod) && a16(time_mod)) {
+    if (scratch && rows > 0 && cout % 4 == 0 && gate_offset % 4 == 0 && a16(residual) &&
+        a16(block_mod) && a16(time_mod)) {
         bool done = false;
-        if (int rc = blaslt_linear_bf16(x, rows, cin, weight, bias, cout, PXS_ACT_NONE, PXS_F32,
-                                        scratch, false, s, &done))
+        if (int rc = blaslt_linear(dtype, x, rows, cin, weight, bias, cout, PXS_ACT_NONE, PXS_F32,
+                                   scratch, false, ws, ws_bytes, s, &done))
             return rc;
         if (done) {
             const int64_t total = rows * (cout / 4);
@@ -1159,6 +1159,56 @@ int linear_gate_residual_scratch(int dtype, const void * x, int64_t rows, int ci
     }
     return pxs_linear_gate_residual(dtype, x, rows, cin, weight, bias, cout, coords, block_mod,
                                     time_mod, gate_offset, residual, s);
+}
+
+int linear_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+              const float * bias, int cout, int act, void * y, void * ws, size_t ws_bytes,
+              hipStream_t s) {
+    if (int rc = check_dtype(dtype, "pxs_linear")) return rc;
+    PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear: bad shape");
+    PXS_CHECK(act == PXS_ACT_NONE || act == PXS_ACT_GELU_TANH || act == PXS_ACT_SILU,
+              PXS_ERR_ARG, "pxs_linear: bad activation");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x && weight && y, PXS_ERR_ARG, "pxs_linear: null pointer");
+    // A few fp32 outputs over narrow rows (the decoder's output layer, 64 -> 7
+    // over millions of rows): the reference's own operation order, one thread
+    // per row, HBM-bound, instead of 64-column MFMA tiles 7/8 empty.
+    if (dtype == PXS_F32 && act == PXS_ACT_NONE && cout <= kOrderedRowOut && cin <= 256)
+        return launch_ordered_rows(static_cast<const float *>(x), rows, cin,
+                                   static_cast<const float *>(weight), bias, cout,
+                                   static_cast<float *>(y), s);
+    {
+        bool done = false;
+        if (int rc = blaslt_linear(dtype, x, rows, cin, weight, bias, cout, act, dtype, y, false,
+                                   ws, ws_bytes, s, &done))
+            return rc;
+        if (done) return PXS_OK;
+    }
+    GemmArgs a{};
+    a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
+    a.cout = cout; a.m = rows; a.rowmap = nullptr; a.ld_map = 0; a.noff = 1; a.masks = nullptr;
+    a.y = y; a.ldy = cout; a.act = act;
+    return run_gemm(dtype, a, kEpiStore, s);
+}
+
+int linear_residual_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+                       const float * bias, int cout, float * residual, void * ws, size_t ws_bytes,
+                       hipStream_t s) {
+    if (int rc = check_dtype(dtype, "pxs_linear_residual")) return rc;
+    PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear_residual: bad shape");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x && weight && residual, PXS_ERR_ARG, "pxs_linear_residual: null pointer");
+    {
+        bool done = false;
+        if (int rc = blaslt_linear(dtype, x, rows, cin, weight, bias, cout, PXS_ACT_NONE, PXS_F32,
+                                   residual, true, ws, ws_bytes, s, &done))
+            return rc;
+        if (done) return PXS_OK;
+    }
+    GemmArgs a{};
+    a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
+    a.cout = cout; a.m = rows; a.noff = 1; a.y = nullptr; a.ldy = cout; a.residual = residual;
+    return run_gemm(dtype, a, kEpiAddResidual, s);
 }
 
 } // namespace pxs
@@ -1198,31 +1248,7 @@ int pxs_sparse_conv3d_s2(int dtype, const void * x, int64_t n_in, int cin, const
 
 int pxs_linear(int dtype, const void * x, int64_t rows, int cin, const void * weight,
                const float * bias, int cout, int act, void * y, void * stream) {
-    if (int rc = check_dtype(dtype, "pxs_linear")) return rc;
-    PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear: bad shape");
-    PXS_CHECK(act == PXS_ACT_NONE || act == PXS_ACT_GELU_TANH || act == PXS_ACT_SILU,
-              PXS_ERR_ARG, "pxs_linear: bad activation");
-    if (rows == 0) return PXS_OK;
-    PXS_CHECK(x && weight && y, PXS_ERR_ARG, "pxs_linear: null pointer");
-    // A few fp32 outputs over narrow rows (the decoder's output layer, 64 -> 7
-    // over millions of rows): the reference's own operation order, one thread
-    // per row, HBM-bound, instead of 64-column MFMA tiles 7/8 empty.
-    if (dtype == PXS_F32 && act == PXS_ACT_NONE && cout <= kOrderedRowOut && cin <= 256)
-        return launch_ordered_rows(static_cast<const float *>(x), rows, cin,
-                                   static_cast<const float *>(weight), bias, cout,
-                                   static_cast<float *>(y), as_stream(stream));
-    if (dtype == PXS_BF16) {
-        bool done = false;
-        if (int rc = blaslt_linear_bf16(x, rows, cin, weight, bias, cout, act, PXS_BF16, y, false,
-                                        as_stream(stream), &done))
-            return rc;
-        if (done) return PXS_OK;
-    }
-    GemmArgs a{};
-    a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
-    a.cout = cout; a.m = rows; a.rowmap = nullptr; a.ld_map = 0; a.noff = 1; a.masks = nullptr;
-    a.y = y; a.ldy = cout; a.act = act;
-    return run_gemm(dtype, a, kEpiStore, as_stream(stream));
+    return linear_ws(dtype, x, rows, cin, weight, bias, cout, act, y, nullptr, 0, as_stream(stream));
 }
 
 int pxs_linear_gate_residual(int dtype, const void * x, int64_t rows, int cin,
@@ -1246,21 +1272,8 @@ int pxs_linear_gate_residual(int dtype, const void * x, int64_t rows, int cin,
 
 int pxs_linear_residual(int dtype, const void * x, int64_t rows, int cin, const void * weight,
                         const float * bias, int cout, float * residual, void * stream) {
-    if (int rc = check_dtype(dtype, "pxs_linear_residual")) return rc;
-    PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear_residual: bad shape");
-    if (rows == 0) return PXS_OK;
-    PXS_CHECK(x && weight && residual, PXS_ERR_ARG, "pxs_linear_residual: null pointer");
-    if (dtype == PXS_BF16) {
-        bool done = false;
-        if (int rc = blaslt_linear_bf16(x, rows, cin, weight, bias, cout, PXS_ACT_NONE, PXS_F32,
-                                        residual, true, as_stream(stream), &done))
-            return rc;
-        if (done) return PXS_OK;
-    }
-    GemmArgs a{};
-    a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
-    a.cout = cout; a.m = rows; a.noff = 1; a.y = nullptr; a.ldy = cout; a.residual = residual;
-    return run_gemm(dtype, a, kEpiAddResidual, as_stream(stream));
+    return linear_residual_ws(dtype, x, rows, cin, weight, bias, cout, residual, nullptr, 0,
+                              as_stream(stream));
 }
 
 int pxs_downsample_mean(int dtype, const void * x, int channels, const int64_t * group_offsets,

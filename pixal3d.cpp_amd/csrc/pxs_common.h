@@ -18,18 +18,32 @@ int fail_workspace(const char * what) noexcept;
 int check_hip(hipError_t status, const char * what);
 int check_launch(const char * what);
 
-// Plain bf16 linears through hipBLASLt (csrc/blaslt.cpp): sets *done when it
-// ran the product, leaves it false for shapes it does not take.
-int blaslt_linear_bf16(const void * x, int64_t rows, int cin, const void * w, const float * bias,
-                       int cout, int act, int y_dtype, void * y, bool accumulate, hipStream_t s,
-                       bool * done);
+// Workspace a composition carves for the library GEMMs of its linears.
+constexpr size_t kLibWorkspaceBytes = size_t(64) << 20;
 
-// pxs_linear_gate_residual given an fp32 scratch of rows x cout (csrc/gemm.hip).
+// Plain linears (x and w both PXS_BF16 or both PXS_F32) through hipBLASLt
+// (csrc/blaslt.cpp), with ws (nullable, ws_bytes) as the library's workspace:
+// sets *done when it ran the product, leaves it false for shapes it does not
+// take.
+int blaslt_linear(int dtype, const void * x, int64_t rows, int cin, const void * w,
+                  const float * bias, int cout, int act, int y_dtype, void * y, bool accumulate,
+                  void * ws, size_t ws_bytes, hipStream_t s, bool * done);
+
+// pxs_linear and pxs_linear_residual with a library workspace (csrc/gemm.hip).
+int linear_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+              const float * bias, int cout, int act, void * y, void * ws, size_t ws_bytes,
+              hipStream_t s);
+int linear_residual_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+                       const float * bias, int cout, float * residual, void * ws, size_t ws_bytes,
+                       hipStream_t s);
+
+// pxs_linear_gate_residual given an fp32 scratch of rows x cout and a library
+// workspace (csrc/gemm.hip).
 int linear_gate_residual_scratch(int dtype, const void * x, int64_t rows, int cin,
                                  const void * weight, const float * bias, int cout,
                                  const int32_t * coords, const float * block_mod,
                                  const float * time_mod, int gate_offset, float * residual,
-                                 float * scratch, hipStream_t s);
+                                 float * scratch, void * ws, size_t ws_bytes, hipStream_t s);
 
 #define PXS_CHECK(expr, code, msg)            \
     do {                                      \

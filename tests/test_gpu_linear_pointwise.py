@@ -292,12 +292,12 @@ def test_head_norm_rope_64(px, orc, dtype):
 
 
 @pytest.mark.parametrize("rows,cin,cout", [(4096, 256, 512), (300, 64, 96), (200, 64, 64),
-                                           (1000, 60, 64)])
+                                           (1000, 60, 64), (1000, 64, 64)])
 def test_linear_bf16_library_and_fallback(px, orc, rows, cin, cout):
     """Plain bf16 linears: with at least 256 rows and widths that are
     multiples of 8 they run through hipBLASLt (bias, GELU, SiLU epilogues, and
-    the residual add as beta = 1 into the fp32 residual); 200 rows and 60
-    inputs take the gather-GEMM kernel.  Against the oracle on the same
+    the residual add as beta = 1 into the fp32 residual); 200 rows, 60 inputs
+    and 64 -> 64 take the gather-GEMM kernel.  Against the oracle on the same
     bf16-rounded operands, at the bf16 bar; without a bias too."""
     import torch
     import pxs
@@ -318,3 +318,28 @@ def test_linear_bf16_library_and_fallback(px, orc, rows, cin, cout):
     torch.cuda.synchronize()
     assert_bf16(host(res), res0 + lin, what="bf16 linear residual")
 
+
+
+@pytest.mark.parametrize("rows,cin,cout", [(2048, 512, 512), (1024, 768, 96), (4096, 136, 128)])
+def test_linear_fp32_library(px, orc, rows, cin, cout):
+    """fp32 linears of at least 2^26 multiply-adds run through hipBLASLt in
+    full fp32 (bias, GELU, SiLU epilogues, residual add); against the oracle
+    (sparse_linear's serial fp32 order) at the fp32 bar."""
+    import torch
+    import pxs
+    x = W.normal(96, rows * cin, 1).reshape(rows, cin)
+    w = W.normal(96, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin)
+    b = W.normal(96, cout, 3, std=0.1)
+    print(f"[linear fp32 library] {rows}x{cin}->{cout}", flush=True)
+    lin = orc.linear(x, w, b)
+    for act, f in ((pxs.ACT_NONE, lambda v: v), (pxs.ACT_GELU_TANH, orc.gelu_tanh),
+                   (pxs.ACT_SILU, orc.silu)):
+        y = host(px.linear(t32(x), t32(w), t32(b), act=act))
+        assert_fp32(y, f(lin), what=f"fp32 linear act {act}")
+    y = host(px.linear(t32(x), t32(w), None))
+    assert_fp32(y, orc.linear(x, w, np.zeros(cout, np.float32)), what="fp32 linear, no bias")
+    res0 = W.normal(96, rows * cout, 4).reshape(rows, cout)
+    res = t32(res0)
+    px.linear_residual(t32(x), t32(w), t32(b), res)
+    torch.cuda.synchronize()
+    assert_fp32(host(res), res0 + lin, what="fp32 linear residual")
