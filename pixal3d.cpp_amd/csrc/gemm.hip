@@ -1276,6 +1276,24 @@ int pxs_linear_residual(int dtype, const void * x, int64_t rows, int cin, const 
                               as_stream(stream));
 }
 
+size_t pxs_linear_workspace_bytes(void) { return kLibWorkspaceBytes; }
+
+int pxs_linear_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+                  const float * bias, int cout, int act, void * y, void * workspace,
+                  void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_linear_ws");
+    return linear_ws(dtype, x, rows, cin, weight, bias, cout, act, y, workspace,
+                     workspace ? kLibWorkspaceBytes : 0, as_stream(stream));
+}
+
+int pxs_linear_residual_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+                           const float * bias, int cout, float * residual, void * workspace,
+                           void * stream) {
+    PXS_CHECK_WORKSPACE(workspace, "pxs_linear_residual_ws");
+    return linear_residual_ws(dtype, x, rows, cin, weight, bias, cout, residual, workspace,
+                              workspace ? kLibWorkspaceBytes : 0, as_stream(stream));
+}
+
 int pxs_downsample_mean(int dtype, const void * x, int channels, const int64_t * group_offsets,
                         const int32_t * group_rows, int64_t m, void * y, void * stream) {
     if (int rc = check_dtype(dtype, "pxs_downsample_mean")) return rc;

@@ -343,3 +343,32 @@ def test_linear_fp32_library(px, orc, rows, cin, cout):
     px.linear_residual(t32(x), t32(w), t32(b), res)
     torch.cuda.synchronize()
     assert_fp32(host(res), res0 + lin, what="fp32 linear residual")
+
+
+@pytest.mark.parametrize("dtype,rows,cin,cout", [("bf16", 70000, 64, 256), ("bf16", 70000, 256, 64),
+                                                 ("bf16", 30000, 256, 256), ("f32", 20000, 128, 128),
+                                                 ("f32", 20000, 64, 256)])
+def test_linear_with_workspace(px, orc, dtype, rows, cin, cout):
+    """pxs_linear_ws / pxs_linear_residual_ws: tall products over few channels
+    whose library algorithms need a workspace; against the oracle at the
+    dtype's bar, with and without GELU, and the residual form."""
+    import torch
+    import pxs
+    conv = t32 if dtype == "f32" else tbf
+    rnd = (lambda a: a) if dtype == "f32" else W.bf16_round
+    check = assert_fp32 if dtype == "f32" else assert_bf16
+    x = rnd(W.normal(97, rows * cin, 1).reshape(rows, cin))
+    w = rnd(W.normal(97, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin))
+    b = W.normal(97, cout, 3, std=0.1)
+    print(f"[linear ws] {dtype} {rows}x{cin}->{cout}", flush=True)
+    ws = px.linear_workspace()
+    lin = orc.linear(x, w, b)
+    y = host(px.linear(conv(x), conv(w), t32(b), workspace=ws))
+    check(y, lin, what="linear ws")
+    y = host(px.linear(conv(x), conv(w), t32(b), act=pxs.ACT_GELU_TANH, workspace=ws))
+    check(y, orc.gelu_tanh(lin), what="linear ws gelu")
+    res0 = W.normal(97, rows * cout, 4).reshape(rows, cout)
+    res = t32(res0)
+    px.linear_residual(conv(x), conv(w), t32(b), res, workspace=ws)
+    torch.cuda.synchronize()
+    check(host(res), res0 + lin, what="linear residual ws")
