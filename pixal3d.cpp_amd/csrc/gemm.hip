@@ -676,22 +676,25 @@ gather_gemm_lds_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// fp32 split-K gather GEMM for small and medium problems (16k-voxel, 64-channel
-// convolutions, fp32 linears).  A workgroup owns 32 output rows x 64 output
-// channels; its (offset, 32-channel chunk) steps are dealt round-robin to
-// the 4 waves, so even a few hundred tiles keep every CU busy.  Each wave
-// loads its operands straight into VGPRs -- lane (h, r) takes the 64
-// contiguous bytes k = 16h .. 16h+15 of A row r and of weight row r, the
-// same K permutation on both sides of v_mfma_f32_32x32x2_f32 -- with the
-// next step's loads in flight during the current step's 32 MFMAs, and no
-// barrier until the end, where waves 1-3 hand their partial sums to wave 0
-// through LDS (a fixed summation order: deterministic).
+// fp32 split-K gather GEMM (SubMConv3d and linears in fp32).  A workgroup
+// owns 32*TI output rows x 64 output channels; its (offset, 32-channel chunk)
+// steps are dealt round-robin to the 4 waves, so even a few hundred tiles
+// keep every CU busy.  Each wave loads its operands straight into VGPRs --
+// lane (h, r) takes the 64 contiguous bytes k = 16h .. 16h+15 of A row r (of
+// each 32-row block) and of weight row r, the same K permutation on both
+// sides of v_mfma_f32_32x32x2_f32 -- with the next step's loads in flight
+// during the current step's MFMAs, and no barrier until the end, where waves
+// 1-3 hand their partial sums to wave 0 through LDS (a fixed summation order:
+// deterministic).  The operand loads return through the per-CU vector-memory
+// path, which bounds the kernel: TI = 2 reads each weight chunk once for 64
+// rows instead of 32 (16 KB per 64x64x32 step instead of 24 KB), at 64
+// accumulator registers per lane.
 
-template <int EPI>
+template <int EPI, int TI>
 __global__ void __launch_bounds__(256)
 split_gemm_f32_kernel(GemmArgs a) {
-    constexpr int BM = 32, BN = 64, NW = 4;
-    __shared__ float red[NW - 1][2][16][64];
+    constexpr int BM = 32 * TI, BN = 64, NW = 4;
+    __shared__ float red[NW - 1][TI * 2][16][64];
     __shared__ int32_t idx_lds[32 * BM];
     __shared__ uint32_t tile_mask;
     __shared__ int koff[32];
@@ -753,12 +756,12 @@ split_gemm_f32_kernel(GemmArgs a) {
     const int my_steps = steps > wave ? (steps - wave + NW - 1) / NW : 0;
     const float4 * zero4 = reinterpret_cast<const float4 *>(g_zero_chunk);
 
-    // Operands of one step: A (16 floats of row r) and B (16 floats of each
-    // of the two 32-column weight tiles).  Steps past the end load zeros, so
-    // every iteration issues the same loads and the compiler's waits count
-    // exactly one step in flight.
+    // Operands of one step: A (16 floats of row r of each 32-row block) and B
+    // (16 floats of each of the two 32-column weight tiles).  Steps past the
+    // end load zeros, so every iteration issues the same loads and the
+    // compiler's waits count exactly one step in flight.
     struct Ops {
-        float4 av[4];
+        float4 av[TI][4];
         float4 bv[2][4];
     };
     auto load = [&](int t, Ops & o) __attribute__((always_inline)) {
@@ -766,14 +769,17 @@ split_gemm_f32_kernel(GemmArgs a) {
         const bool live = t < my_steps;
         const int i = live ? s / chunks : 0, chunk = live ? s - i * chunks : 0;
         const int k = live ? koff[i] : 0;
-        const int32_t src = live ? idx_lds[i * BM + r] : -1;
         const int col0 = chunk * 32 + 16 * h;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int col = col0 + 4 * q;
-            o.av[q] = (src >= 0 && col < a.cin)
-                          ? *reinterpret_cast<const float4 *>(x + static_cast<int64_t>(src) * a.ldx + col)
-                          : *zero4;
+        for (int ti = 0; ti < TI; ++ti) {
+            const int32_t src = live ? idx_lds[i * BM + ti * 32 + r] : -1;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int col = col0 + 4 * q;
+                o.av[ti][q] = (src >= 0 && col < a.cin)
+                                  ? *reinterpret_cast<const float4 *>(x + static_cast<int64_t>(src) * a.ldx + col)
+                                  : *zero4;
+            }
         }
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
@@ -788,20 +794,24 @@ split_gemm_f32_kernel(GemmArgs a) {
         }
     };
 
-    f32x16 acc[2];
+    f32x16 acc[TI][2];
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
+    for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[ct][v] = 0.0f;
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[ti][ct][v] = 0.0f;
     auto compute = [&](const Ops & o) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct)
-                    acc[ct] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.av[q][e], o.bv[ct][q][e],
-                                                                   acc[ct], 0, 0, 0);
+                for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+                        acc[ti][ct] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            o.av[ti][q][e], o.bv[ct][q][e], acc[ti][ct], 0, 0, 0);
     };
 
     Ops o0, o1;
@@ -815,35 +825,61 @@ split_gemm_f32_kernel(GemmArgs a) {
 
     if (wave > 0) {
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
+        for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) red[wave - 1][ct][v][lane] = acc[ct][v];
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) red[wave - 1][ti * 2 + ct][v][lane] = acc[ti][ct][v];
     }
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
     for (int wv = 0; wv < NW - 1; ++wv)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
+        for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[ct][v] += red[wv][ct][v][lane];
-    f32x16 (&acc2)[1][2] = reinterpret_cast<f32x16 (&)[1][2]>(acc);
-    gemm_epilogue<float, 1, 2, 32, 64, EPI>(a, acc2, p0, n0, 0, 0, h, r);
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[ti][ct][v] += red[wv][ti * 2 + ct][v][lane];
+    gemm_epilogue<float, TI, 2, 32 * TI, 64, EPI>(a, acc, p0, n0, 0, 0, h, r);
 }
 
 #ifndef PXS_SPLIT_F32
 #define PXS_SPLIT_F32 1
 #endif
+// 64-row tiles (one workgroup, one wave per SIMD, per CU) for grids of
+// about one to four rounds over the 256 CUs; past that, 32-row tiles at two
+// workgroups per CU hide more latency.  Measured on SubMConv3d over shell
+// voxels: 64 -> 64 at 16k rows 57 against 67 us, 128 -> 128 at 8k-32k rows
+// 0.79-0.89x; at 8k rows 64 -> 64 (128 wide tiles) 1.66x slower, at 96k rows
+// 1.03-1.12x slower.
+#ifndef PXS_SPLIT_F32_WIDE_MIN
+#define PXS_SPLIT_F32_WIDE_MIN 224
+#endif
+#ifndef PXS_SPLIT_F32_WIDE_MAX
+#define PXS_SPLIT_F32_WIDE_MAX 1024
+#endif
 
-template <int EPI>
-int launch_split_f32(const GemmArgs & args, hipStream_t stream) {
-    const int64_t tiles_m = (args.m + 31) / 32;
+template <int EPI, int TI>
+int launch_split_f32_ti(const GemmArgs & args, hipStream_t stream) {
+    const int64_t tiles_m = (args.m + 32 * TI - 1) / (32 * TI);
     const int64_t tiles_n = (args.cout + 63) / 64;
     const int64_t blocks = tiles_m * tiles_n;
     if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "gather GEMM grid too large");
-    hipLaunchKernelGGL((split_gemm_f32_kernel<EPI>), dim3(static_cast<unsigned>(blocks)), dim3(256),
-                       0, stream, args);
+    hipLaunchKernelGGL((split_gemm_f32_kernel<EPI, TI>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, stream, args);
     return check_launch("gather GEMM (fp32 split-K)");
+}
+
+template <int EPI>
+int launch_split_f32(const GemmArgs & args, hipStream_t stream) {
+    const int64_t wide = ((args.m + 63) / 64) * ((args.cout + 63) / 64);
+    // (Only for the 27-offset gathers: plain linears, with 2 K steps per
+    // tile, run 1.5x slower on 64-row tiles, 19 against 13 us at 16k x 64.)
+    if (args.rowmap && args.noff >= 27 && wide >= PXS_SPLIT_F32_WIDE_MIN &&
+        wide <= PXS_SPLIT_F32_WIDE_MAX)
+        return launch_split_f32_ti<EPI, 2>(args, stream);
+    return launch_split_f32_ti<EPI, 1>(args, stream);
 }
 
 template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M, int KSPLIT>
