@@ -433,6 +433,9 @@ __device__ __forceinline__ void attn_step_schedule() {
 #endif
 constexpr bool kSetPrio = PXS_ATTN_SETPRIO != 0;
 constexpr int kKeyRowsLds = 1024;  // longest permuted segment whose key rows are staged in LDS
+#ifndef PXS_ATTN_SADDR
+#define PXS_ATTN_SADDR 1
+#endif
 
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
@@ -503,10 +506,45 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         src0[j] = (is_v ? vp : kp) + (k_begin + row) * ld + head * 64 + piece * 8;
         src_step[j] = kKeys * ld;
     }
+#if PXS_ATTN_SADDR
+    // Full unpermuted tiles: the K and V tile bases (wave-uniform, scalar
+    // registers) advance by 64 rows per tile; each lane's byte offset within
+    // a tile (row * ld + piece) stays fixed, so a tile's loads need no vector
+    // address arithmetic.  Offsets fit 32 bits for rows of up to 2^25 bytes.
+    const char * kbase = reinterpret_cast<const char *>(kp + k_begin * a.ldk + head * 64);
+    const char * vbase = reinterpret_cast<const char *>(vp + k_begin * a.ldv + head * 64);
+    const int64_t kstep = static_cast<int64_t>(kKeys) * a.ldk * 2;
+    const int64_t vstep = static_cast<int64_t>(kKeys) * a.ldv * 2;
+    uint32_t voff[kInstr];
+#pragma unroll
+    for (int j = 0; j < kInstr; ++j) {
+        const int unit = wave * kInstr + j;
+        const bool is_v = unit >= kKeys / 8;
+        const int row = (unit % (kKeys / 8)) * 8 + lrow;
+        const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
+        voff[j] = static_cast<uint32_t>((row * (is_v ? a.ldv : a.ldk) + piece * 8) * 2);
+    }
+    const bool saddr_ok = a.ldk < (int64_t(1) << 24) && a.ldv < (int64_t(1) << 24);
+#endif
     auto issue = [&](int tile) __attribute__((always_inline)) {
         const uint32_t base = lds_base + (tile % kAttnStages) * (2 * kTileBytes);
         const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeys;
         if (a.row_map == nullptr && kt0 + kKeys <= k_end) {
+#if PXS_ATTN_SADDR
+            if (saddr_ok) {
+                const char * kt_base = kbase + tile * kstep;
+                const char * vt_base = vbase + tile * vstep;
+#pragma unroll
+                for (int j = 0; j < kInstr; ++j) {
+                    const int unit = wave * kInstr + j;
+                    const bool is_v = unit >= kKeys / 8;
+                    const int row0 = (unit % (kKeys / 8)) * 8;
+                    lds_dma16_sbase(is_v ? vt_base : kt_base, voff[j],
+                                    base + (is_v ? kTileBytes : 0) + row0 * 128);
+                }
+                return;
+            }
+#endif
 #pragma unroll
             for (int j = 0; j < kInstr; ++j) {
                 const int unit = wave * kInstr + j;

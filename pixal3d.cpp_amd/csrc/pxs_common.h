@@ -126,6 +126,17 @@ __device__ __forceinline__ void lds_dma16(const void * g, uint32_t lds_base) {
                  : "m0");
 }
 
+// lds_dma16 with a wave-uniform base in SGPRs and a per-lane 32-bit byte
+// offset (the instruction's saddr form): a loop that walks the base keeps its
+// per-lane offsets fixed and advances the base with scalar arithmetic.
+__device__ __forceinline__ void lds_dma16_sbase(const void * sbase, uint32_t voff,
+                                                uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_base)
+                 : "m0");
+}
+
 // lds_dma16 for the lanes set in `lanes` only (EXEC narrowed inside the asm
 // and restored after it); the other lanes leave their 16 LDS bytes as they
 // were.  `lanes` must not be empty: the instruction is then always issued, so
