@@ -4,13 +4,12 @@
 Default workload (one "step" = one pass over the batch, inputs resident in HBM):
   unet_stage_128 - batch 2 on a 128^3 grid (61,056 + 101,207 voxels, unions of
   three ellipsoid shells), bf16 features, fp32 accumulation:
-    generation-tagged voxel grid insert (with the stride-2 occupancy bits) +
-      3x3x3 neighbor map at 128^3
-    SubMConv3d 3^3 128 -> 128
+    generation-tagged voxel grid insert (with the stride-2 occupancy bits)
     stride-2 topology (coarse cells, child map, the 64^3 grid)
+    SubMConv3d 3^3 128 -> 128, its 3x3x3 neighbours looked up in the 128^3
+      grid inside its tiles (the neighbor map fused into the gather)
     SparseConv3d 2^3 s2 128 -> 256
-    neighbor map at 64^3 over the grid the topology wrote
-    SubMConv3d 3^3 256 -> 256
+    SubMConv3d 3^3 256 -> 256 over the 64^3 grid the topology wrote
   value = sum over the three convs of (active pairs x Cin x Cout) / step time,
   in voxel-GMAC/s.
 
@@ -182,8 +181,6 @@ def unet_stage(args, torch, px, W):
     grid1 = px.tagged_grid(2, (128, 128, 128))
     grid2 = ws(lib.pxs_voxel_grid_bytes(2, 64, 64, 64))  # rewritten whole by the s2 topology
     ds_ws = px.s2_tagged_workspace(2, (128, 128, 128))
-    nbr1 = torch.empty((27, n), dtype=torch.int32, device=dev)
-    mask1 = torch.empty(n, dtype=torch.int32, device=dev)
     y_a = torch.empty((n, 128), dtype=torch.bfloat16, device=dev)
     oc = torch.empty((n, 4), dtype=torch.int32, device=dev)
     child = torch.empty((8, n), dtype=torch.int32, device=dev)
@@ -192,9 +189,16 @@ def unet_stage(args, torch, px, W):
     # outside the timed region; every step recomputes the topology itself.
     _, _, m = px.downsample_s2(coords, 2, (128, 128, 128))
     y_b = torch.empty((m, 256), dtype=torch.bfloat16, device=dev)
-    nbr2 = torch.empty((27, m), dtype=torch.int32, device=dev)
-    mask2 = torch.empty(m, dtype=torch.int32, device=dev)
     y_c = torch.empty((m, 256), dtype=torch.bfloat16, device=dev)
+    # Active pair counts (the algorithmic work) from the neighbour maps of
+    # both levels, built here once: the timed step builds no map (the
+    # convolutions look their neighbours up in the grids).
+    _, mask1 = px.neighbor_map_grid(coords, 2, (128, 128, 128))
+    oc_host, _, _ = px.downsample_s2(coords, 2, (128, 128, 128))
+    _, mask2 = px.neighbor_map_grid(oc_host[:m].contiguous(), 2, (64, 64, 64))
+    pa = int(np.unpackbits(mask1.cpu().numpy().view(np.uint8)).sum())
+    pc = int(np.unpackbits(mask2.cpu().numpy().view(np.uint8)).sum())
+    del mask1, mask2, oc_host
     timer = Timer(torch)
     gen = [0]
 
@@ -209,29 +213,27 @@ def unet_stage(args, torch, px, W):
         wrap = gen[0] == 255
         gen[0] = gen[0] % 255 + 1
         g = C.c_uint32(gen[0])
-        # grid insert, 128^3 neighbour map and the stride-2 topology (which
-        # also writes the 64^3 grid) in three launches
+        # grid insert and the stride-2 topology (which also writes the 64^3
+        # grid) in three launches; no neighbour maps: both SubMConv3d look
+        # their 27 neighbours up in the grids inside their tiles
         timer.run("topology_128", lambda: (
             chk(lib.pxs_voxel_grid_tagged_reset(P(grid1), 2, 128, 128, 128, s), "reset")
             if wrap else None,
             chk(lib.pxs_map_s2_topology_tagged(
-                P(coords), n, 2, 128, 128, 128, P(grid1), g, P(nbr1), P(mask1), P(oc), P(child), n,
+                P(coords), n, 2, 128, 128, 128, P(grid1), g, None, None, P(oc), P(child), n,
                 P(m_dev), P(grid2), P(ds_ws), s), "topology")))
-        timer.run("subm_conv_a", lambda: chk(lib.pxs_subm_conv3d(
-            1, P(x), n, 128, P(w_a), P(b_a), 128, P(nbr1), P(mask1), P(y_a), s), "conv a"))
+        timer.run("subm_conv_a", lambda: chk(lib.pxs_subm_conv3d_grid(
+            1, P(x), P(coords), n, 128, P(w_a), P(b_a), 128, 2, 128, 128, 128, P(grid1), g,
+            P(y_a), s), "conv a"))
         timer.run("sparse_conv_b", lambda: chk(lib.pxs_sparse_conv3d_s2(
             1, P(y_a), n, 128, P(w_b), P(b_b), 256, P(child), n, m, P(y_b), s), "conv b"))
-        timer.run("neighbor_map_64", lambda: chk(lib.pxs_neighbor_map_k3_grid(
-            P(oc), m, 2, 64, 64, 64, P(grid2), P(nbr2), P(mask2), s), "map2"))
-        timer.run("subm_conv_c", lambda: chk(lib.pxs_subm_conv3d(
-            1, P(y_b), m, 256, P(w_c), P(b_c), 256, P(nbr2), P(mask2), P(y_c), s), "conv c"))
+        timer.run("subm_conv_c", lambda: chk(lib.pxs_subm_conv3d_grid(
+            1, P(y_b), P(oc), m, 256, P(w_c), P(b_c), 256, 2, 64, 64, 64, P(grid2), 0, P(y_c), s),
+            "conv c"))
 
-    ops = ("topology_128", "subm_conv_a", "sparse_conv_b", "neighbor_map_64", "subm_conv_c")
+    ops = ("topology_128", "subm_conv_a", "sparse_conv_b", "subm_conv_c")
     timer.only = set()
     warm = warm_up(args, torch, step)
-    # Active pair counts (algorithmic work) from the neighbor masks.
-    pa = int(np.unpackbits(mask1.cpu().numpy().view(np.uint8)).sum())
-    pc = int(np.unpackbits(mask2.cpu().numpy().view(np.uint8)).sum())
     macs = {"subm_conv_a": pa * 128 * 128, "sparse_conv_b": n * 128 * 256,
             "subm_conv_c": pc * 256 * 256}
     # Per-op breakdown: a pass of its own with every op bracketed by events.
@@ -260,16 +262,14 @@ def unet_stage(args, torch, px, W):
     per_op = {k: {"ms": round(kern[k], 4),
                   "voxel_gmacs": round(macs[k] / (kern[k] * 1e-3) / 1e9, 1),
                   "tflops": round(2 * macs[k] / (kern[k] * 1e-3) / 1e12, 2)} for k in macs}
-    # The topology is HBM-bound: per fine row the coordinates (16 B, read
-    # twice), one 4-byte tagged cell written, 27 int32 + a mask out (the 27
-    # cell reads per row hit cache lines shared with neighbouring rows); per
+    # The topology is HBM-bound: per fine row its coordinate (16 B) and one
+    # 4-byte tagged cell written (and its bit in the occupancy bitmap); per
     # coarse cell one int32 of the 64^3 grid, per coarse row its coordinate
-    # and 8 child slots.
+    # and 8 child slots (the child lookups read cells the insert just wrote).
     cells_64 = 2 * 64 * 64 * 64
-    topo_bytes = n * (2 * 16 + 4 + 27 * 4 + 4) + cells_64 * 4 + m * (16 + 8 * 4)
+    topo_bytes = n * (16 + 4) + cells_64 * 4 + m * (16 + 8 * 4)
     per_op["topology_128"] = {"ms": round(kern["topology_128"], 4),
                               "gbs": round(topo_bytes / (kern["topology_128"] * 1e-3) / 1e9, 1)}
-    per_op["neighbor_map_64"] = {"ms": round(kern["neighbor_map_64"], 4)}
     result = {
         "metric": "SubMConv3d voxel-GMAC/s & sparse-attn TFLOP/s vs roofline, 1 MI355X",
         "value": round(value, 2),
@@ -277,9 +277,10 @@ def unet_stage(args, torch, px, W):
         "ms_per_step": round(ms, 4),
         "dtype": "bf16",
         "config": {"workload": "unet_stage_128: batch 2 on 128^3 (61,056 + 101,207 voxels, "
-                               "3 ellipsoid shells each); tagged voxel grid, neighbour map and "
-                               "s2 topology (+ 64^3 grid), SubMConv3d 128->128, SparseConv3d "
-                               "128->256, map at 64^3, SubMConv3d 256->256",
+                               "3 ellipsoid shells each); tagged voxel grid and s2 topology "
+                               "(+ 64^3 grid), SubMConv3d 128->128, SparseConv3d 128->256, "
+                               "SubMConv3d 256->256; the SubMConv3d take their 27 neighbours "
+                               "from the grids inside their tiles (no neighbour map)",
                    "voxels": n, "voxels_64": m, "pairs_a": pa, "pairs_c": pc,
                    "warmup_steps_run": warm,
                    "per_op_note": "per-op times from a pass of args.steps steps with every op "

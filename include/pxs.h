@@ -167,6 +167,19 @@ int pxs_subm_conv3d(int dtype, const void * x, int64_t n, int cin, const void * 
                     const float * bias, int cout, const int32_t * nbr, const uint32_t * masks,
                     void * y, void * stream);
 
+/* pxs_subm_conv3d with the neighbours looked up in a dense voxel grid of the
+ * same coords and extents inside the convolution (each tile reads the 27
+ * cells around its rows' coordinates), so no neighbour map is built or read:
+ * the map of src/slat_decoder.cpp:609-668 fused into the gather.  grid is a
+ * plain grid (pxs_voxel_grid_build, generation 0) or a tagged one
+ * (pxs_voxel_grid_tagged_insert or pxs_map_s2_topology_tagged with that
+ * generation, 1..255, at most 2^24 - 1 rows).  Output identical to
+ * pxs_subm_conv3d over the grid's map. */
+int pxs_subm_conv3d_grid(int dtype, const void * x, const int32_t * coords, int64_t n, int cin,
+                         const void * weight, const float * bias, int cout, int batch_size,
+                         int sx, int sy, int sz, const void * grid, uint32_t generation, void * y,
+                         void * stream);
+
 /* ---- a4, a15: factor-f topology, strided conv, mean downsample ------------- */
 
 /* Workspace of pxs_downsample_topology / pxs_downsample_s2_topology (factor 2)
@@ -210,7 +223,9 @@ int pxs_downsample_s2_topology_tagged(const int32_t * coords, int64_t n, int bat
  * the occupancy bitmap of s2_workspace), pxs_neighbor_map_k3_grid_tagged (nbr,
  * masks; its launch also scans the bitmap) and the emit of
  * pxs_downsample_s2_topology_tagged (out_coords, child_map, *m_out,
- * coarse_grid).  Outputs identical to those three calls; the same limits. */
+ * coarse_grid).  Outputs identical to those three calls; the same limits.
+ * nbr and masks may both be NULL: the map is then not built (for a consumer
+ * that reads the grid itself, pxs_subm_conv3d_grid). */
 int pxs_map_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,
                                int sz, void * grid, uint32_t generation, int32_t * nbr,
                                uint32_t * masks, int32_t * out_coords, int32_t * child_map,

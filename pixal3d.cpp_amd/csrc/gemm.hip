@@ -53,7 +53,57 @@ struct GemmArgs {
     const float * time_mod;
     int gate_offset;
     float * residual;
+    // Neighbours from a dense voxel grid instead of rowmap (SubMConv3d only,
+    // noff = 27): output row p's source at offset k is the grid cell next to
+    // coords[p] (voxel_grid_row; generation 0 = plain grid).
+    const uint32_t * grid;
+    int grid_b, grid_x, grid_y, grid_z;
+    uint32_t grid_gen;
 };
+
+// Source row of output row p (coordinates c) at 3x3x3 offset k = kd*9 + kh*3
+// + kw, looked up in the grid, or -1: the entry pxs_neighbor_map_k3_grid
+// (or _tagged) would write, computed where the convolution needs it.  The
+// centre is the row itself, as in the map.
+__device__ __forceinline__ int32_t grid_src(const GemmArgs & a, int4 c, int k, int64_t p) {
+    if (k == 13) return static_cast<int32_t>(p);
+    const int x = c.y + k / 9 - 1, y = c.z + (k / 3) % 3 - 1, z = c.w + k % 3 - 1;
+    if (static_cast<unsigned>(c.x) >= static_cast<unsigned>(a.grid_b) ||
+        static_cast<unsigned>(x) >= static_cast<unsigned>(a.grid_x) ||
+        static_cast<unsigned>(y) >= static_cast<unsigned>(a.grid_y) ||
+        static_cast<unsigned>(z) >= static_cast<unsigned>(a.grid_z))
+        return -1;
+    const int64_t cell = ((static_cast<int64_t>(c.x) * a.grid_x + x) * a.grid_y + y) * a.grid_z + z;
+    const int32_t s = voxel_grid_row(a.grid[cell], a.grid_gen);
+    return s < a.rows_in ? s : -1;
+}
+
+// Grid mode prologue: all 27 sources of the tile's rows into idx[k * BM +
+// row] (-1 absent or past the end), OR-ing each row's present offsets into
+// *tile_mask.  Each thread takes one row and a quarter of the offsets, so a
+// row's coordinates are read once per thread.
+template <int BM>
+__device__ __forceinline__ void grid_tile_sources(const GemmArgs & a, int64_t p0, int tid,
+                                                  int nthreads, int32_t * idx,
+                                                  uint32_t * tile_mask) {
+    const int4 * crd = reinterpret_cast<const int4 *>(a.coords);
+    uint32_t local = 0;
+    for (int t = tid; t < 4 * BM; t += nthreads) {
+        const int row = t % BM, kb = (t / BM) * 7, ke = kb + 7 < 27 ? kb + 7 : 27;
+        const int64_t p = p0 + row;
+        if (p < a.m) {
+            const int4 c = crd[p];
+            for (int k = kb; k < ke; ++k) {
+                const int32_t src = grid_src(a, c, k, p);
+                idx[k * BM + row] = src;
+                if (src >= 0) local |= 1u << k;
+            }
+        } else {
+            for (int k = kb; k < ke; ++k) idx[k * BM + row] = -1;
+        }
+    }
+    if (local) atomicOr(tile_mask, local);
+}
 
 template <typename T> struct Mfma;
 
@@ -160,7 +210,11 @@ gather_gemm_kernel(GemmArgs a) {
         uint32_t local = 0;
         if (tid < BM && p0 + tid < a.m) {
             const int64_t p = p0 + tid;
-            if (a.masks) {
+            if (a.grid) {
+                const int4 c = reinterpret_cast<const int4 *>(a.coords)[p];
+                for (int k = 0; k < 27; ++k)
+                    if (grid_src(a, c, k, p) >= 0) local |= 1u << k;
+            } else if (a.masks) {
                 local = a.masks[p];
             } else if (a.rowmap) {
                 for (int k = 0; k < a.noff; ++k) {
@@ -193,7 +247,8 @@ gather_gemm_kernel(GemmArgs a) {
             const int64_t p = p0 + i * 32 + srow;
             int64_t src = -1;
             if (p < a.m) {
-                src = a.rowmap ? static_cast<int64_t>(a.rowmap[k * a.ld_map + p]) : p;
+                if (a.grid) src = grid_src(a, reinterpret_cast<const int4 *>(a.coords)[p], k, p);
+                else src = a.rowmap ? static_cast<int64_t>(a.rowmap[k * a.ld_map + p]) : p;
                 if (src >= a.rows_in) src = -1;
             }
             ra[i] = src >= 0 ? load_chunk16<T>(x, src, a.ldx, col, a.cin, a.vec_ok)
@@ -450,7 +505,9 @@ gather_gemm_lds_kernel(GemmArgs a) {
 
     if (tid == 0) tile_mask = 0;
     __syncthreads();
-    {
+    if (a.grid) {
+        grid_tile_sources<BM>(a, p0, tid, kThreads, idx_lds, &tile_mask);
+    } else {
         uint32_t local = 0;
         for (int row = tid; row < BM; row += kThreads) {
             if (p0 + row >= a.m) break;
@@ -479,7 +536,9 @@ gather_gemm_lds_kernel(GemmArgs a) {
         }
     }
     __syncthreads();
-    for (int e = tid; e < kcount * BM; e += kThreads) {
+    // idx_lds rows: the tile's present offsets in order (i), or in grid mode
+    // all 27 (k = koff[i]).
+    for (int e = tid; !a.grid && e < kcount * BM; e += kThreads) {
         const int i = e / BM, row = e % BM;
         int32_t src = -1;
         if (p0 + row < a.m) {
@@ -520,8 +579,9 @@ gather_gemm_lds_kernel(GemmArgs a) {
         const int k = koff[i];
         char * base = smem + (s % NSTAGE) * kStageBytes;
         int32_t src[AI];
+        const int slot = a.grid ? k : i;
 #pragma unroll
-        for (int j = 0; j < AI; ++j) src[j] = idx_lds[i * BM + a_row[j]];
+        for (int j = 0; j < AI; ++j) src[j] = idx_lds[slot * BM + a_row[j]];
 #pragma unroll
         for (int j = 0; j < AI; ++j) {
             const int col = chunk * kChunk + a_piece[j] * kVec;
@@ -570,7 +630,8 @@ gather_gemm_lds_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
             row_ok[i] = true;
-            if constexpr (kMaskAbsent) row_ok[i] = idx_lds[(s / chunks) * BM + wm * WM + i * 32 + r] >= 0;
+            if constexpr (kMaskAbsent)
+                row_ok[i] = idx_lds[(a.grid ? koff[s / chunks] : s / chunks) * BM + wm * WM + i * 32 + r] >= 0;
         }
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
@@ -713,7 +774,9 @@ split_gemm_f32_kernel(GemmArgs a) {
 
     if (tid == 0) tile_mask = 0;
     __syncthreads();
-    if (tid < BM && p0 + tid < a.m) {
+    if (a.grid) {
+        grid_tile_sources<BM>(a, p0, tid, NW * 64, idx_lds, &tile_mask);
+    } else if (tid < BM && p0 + tid < a.m) {
         const int64_t p = p0 + tid;
         uint32_t local = 0;
         if (a.masks) {
@@ -739,7 +802,7 @@ split_gemm_f32_kernel(GemmArgs a) {
         }
     }
     __syncthreads();
-    for (int e = tid; e < kcount * BM; e += NW * 64) {
+    for (int e = tid; !a.grid && e < kcount * BM; e += NW * 64) {
         const int i = e / BM, row = e % BM;
         int32_t src = -1;
         if (p0 + row < a.m) {
@@ -772,7 +835,7 @@ split_gemm_f32_kernel(GemmArgs a) {
         const int col0 = chunk * 32 + 16 * h;
 #pragma unroll
         for (int ti = 0; ti < TI; ++ti) {
-            const int32_t src = live ? idx_lds[i * BM + ti * 32 + r] : -1;
+            const int32_t src = live ? idx_lds[(a.grid ? k : i) * BM + ti * 32 + r] : -1;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int col = col0 + 4 * q;
@@ -876,7 +939,7 @@ int launch_split_f32(const GemmArgs & args, hipStream_t stream) {
     const int64_t wide = ((args.m + 63) / 64) * ((args.cout + 63) / 64);
     // (Only for the 27-offset gathers: plain linears, with 2 K steps per
     // tile, run 1.5x slower on 64-row tiles, 19 against 13 us at 16k x 64.)
-    if (args.rowmap && args.noff >= 27 && wide >= PXS_SPLIT_F32_WIDE_MIN &&
+    if ((args.rowmap || args.grid) && args.noff >= 27 && wide >= PXS_SPLIT_F32_WIDE_MIN &&
         wide <= PXS_SPLIT_F32_WIDE_MAX)
         return launch_split_f32_ti<EPI, 2>(args, stream);
     return launch_split_f32_ti<EPI, 1>(args, stream);
@@ -942,7 +1005,7 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
             // (192-row tiles, which put SubMConv3d 256->256 on ~40k rows in
             // one round of tiles instead of 1.2, measured the same: the
             // chip-wide operand rate bounds it, not the last round.)
-            if (PXS_GEMM_WIDE && args.rowmap && args.cout > 128 && kstages >= 32)
+            if (PXS_GEMM_WIDE && (args.rowmap || args.grid) && args.cout > 128 && kstages >= 32)
                 return launch_lds_tile<T, 128, 256, EPI, 2, 8, 2, 1>(args, stream);
         }
 #ifndef PXS_GEMM_NARROW_KSPLIT
@@ -1264,6 +1327,33 @@ int pxs_subm_conv3d(int dtype, const void * x, int64_t n, int cin, const void * 
     a.x = x; a.rows_in = n; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
     a.cout = cout; a.m = n; a.rowmap = nbr; a.ld_map = n; a.noff = 27; a.masks = masks;
     a.y = y; a.ldy = cout; a.act = PXS_ACT_NONE;
+    return run_gemm(dtype, a, kEpiStore, as_stream(stream));
+}
+
+int pxs_subm_conv3d_grid(int dtype, const void * x, const int32_t * coords, int64_t n, int cin,
+                         const void * weight, const float * bias, int cout, int batch_size,
+                         int sx, int sy, int sz, const void * grid, uint32_t generation, void * y,
+                         void * stream) {
+    if (int rc = check_dtype(dtype, "pxs_subm_conv3d_grid")) return rc;
+    PXS_CHECK(n >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_subm_conv3d_grid: bad shape");
+    PXS_CHECK(batch_size > 0 && sx > 0 && sy > 0 && sz > 0, PXS_ERR_ARG,
+              "pxs_subm_conv3d_grid: invalid extents");
+    PXS_CHECK(generation <= kVoxelTagMax, PXS_ERR_ARG,
+              "pxs_subm_conv3d_grid: generation must be 0 (plain grid) or 1..255");
+    PXS_CHECK(generation == 0 || n < (int64_t{1} << kVoxelTagShift), PXS_ERR_ARG,
+              "pxs_subm_conv3d_grid: a tagged grid holds at most 2^24 - 1 rows");
+    PXS_CHECK(n <= INT32_MAX, PXS_ERR_ARG, "pxs_subm_conv3d_grid: bad row count");
+    if (n == 0) return PXS_OK;
+    PXS_CHECK(x && coords && weight && grid && y, PXS_ERR_ARG,
+              "pxs_subm_conv3d_grid: null pointer");
+    PXS_CHECK((reinterpret_cast<uintptr_t>(coords) & 15u) == 0, PXS_ERR_ARG,
+              "pxs_subm_conv3d_grid: coordinates must be 16-byte aligned");
+    GemmArgs a{};
+    a.x = x; a.rows_in = n; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
+    a.cout = cout; a.m = n; a.rowmap = nullptr; a.ld_map = 0; a.noff = 27; a.masks = nullptr;
+    a.y = y; a.ldy = cout; a.act = PXS_ACT_NONE; a.coords = coords;
+    a.grid = static_cast<const uint32_t *>(grid);
+    a.grid_b = batch_size; a.grid_x = sx; a.grid_y = sy; a.grid_z = sz; a.grid_gen = generation;
     return run_gemm(dtype, a, kEpiStore, as_stream(stream));
 }
 

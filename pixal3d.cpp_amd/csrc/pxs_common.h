@@ -163,6 +163,21 @@ __device__ __forceinline__ void barrier_no_fence() {
     asm volatile("" ::: "memory");
 }
 
+// ---- dense voxel grid cells ---------------------------------------------------
+// The row a cell of a dense voxel grid holds, or -1.  generation 0: a plain
+// grid (pxs_voxel_grid_build), each cell the row or INT_MAX; 1..255: a
+// generation-tagged grid (pxs_voxel_grid_tagged_insert), each cell
+// (255 - generation) << 24 | row, other tags being other builds.
+constexpr uint32_t kVoxelGridEmpty = 0x7FFFFFFFu;
+constexpr uint32_t kVoxelTagShift = 24;
+constexpr uint32_t kVoxelTagMax = 255;
+__device__ __forceinline__ int32_t voxel_grid_row(uint32_t cell, uint32_t generation) {
+    if (generation == 0) return cell == kVoxelGridEmpty ? -1 : static_cast<int32_t>(cell);
+    return (cell >> kVoxelTagShift) == kVoxelTagMax - generation
+               ? static_cast<int32_t>(cell & ((1u << kVoxelTagShift) - 1u))
+               : -1;
+}
+
 // ---- math helpers ------------------------------------------------------------
 __device__ __forceinline__ float gelu_tanh_f(float v) {
     const float k = 0.7978845608028654f;

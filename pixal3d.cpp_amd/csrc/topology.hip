@@ -271,6 +271,9 @@ neighbor_map_grid_kernel(const int4 * __restrict__ coords, int64_t n, GridDims g
 constexpr uint32_t kTagRowBits = 24;
 constexpr uint32_t kTagMaxGeneration = 255;
 constexpr int64_t kTagMaxRows = (int64_t{1} << kTagRowBits) - 1;
+static_assert(kTagRowBits == kVoxelTagShift && kTagMaxGeneration == kVoxelTagMax &&
+                  static_cast<uint32_t>(kGridEmpty) == kVoxelGridEmpty,
+              "grid cell layout shared with voxel_grid_row");
 
 __device__ __forceinline__ uint32_t tag_cell(uint32_t generation, uint32_t row) {
     return ((kTagMaxGeneration - generation) << kTagRowBits) | row;
@@ -1293,8 +1296,10 @@ int pxs_map_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size
     PXS_CHECK(m_out && s2_workspace, PXS_ERR_ARG, "pxs_map_s2_topology_tagged: null pointer");
     hipStream_t s = as_stream(stream);
     if (n == 0) return fill_i64(m_out, 1, 0, s);
-    PXS_CHECK(coords && grid && nbr && out_coords && child_map && coarse_grid, PXS_ERR_ARG,
+    PXS_CHECK(coords && grid && out_coords && child_map && coarse_grid, PXS_ERR_ARG,
               "pxs_map_s2_topology_tagged: null pointer");
+    PXS_CHECK(nbr || !masks, PXS_ERR_ARG,
+              "pxs_map_s2_topology_tagged: masks without a neighbour map");
     const int cx = (sx + 1) / 2, cy = (sy + 1) / 2, cz = (sz + 1) / 2;
     const int64_t cells = static_cast<int64_t>(batch_size) * cx * cy * cz;
     const int64_t words = (cells + 31) / 32;
@@ -1311,9 +1316,11 @@ int pxs_map_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size
     hipLaunchKernelGGL(tagged_scatter_mark_kernel, dim3(static_cast<unsigned>(map_blocks)),
                        dim3(kThreads), 0, s, c4, n, fine, static_cast<uint32_t *>(grid), generation,
                        cx, cy, cz, words, bitmap);
-    hipLaunchKernelGGL(map_tagged_and_scan_kernel, dim3(static_cast<unsigned>(map_blocks + blocks)),
+    // Without nbr only the bitmap scan runs (the map's workgroups are left out).
+    const int64_t row_blocks = nbr ? map_blocks : 0;
+    hipLaunchKernelGGL(map_tagged_and_scan_kernel, dim3(static_cast<unsigned>(row_blocks + blocks)),
                        dim3(kThreads), 0, s, c4, n, fine, static_cast<const uint32_t *>(grid),
-                       generation, nbr, masks, map_blocks, bitmap, words, local_prefix, totals);
+                       generation, nbr, masks, row_blocks, bitmap, words, local_prefix, totals);
     hipLaunchKernelGGL(coarse_emit_grid_kernel, dim3(grid_for(words * 32, kThreads)), dim3(kThreads), 0,
                        s, bitmap, words, cells, local_prefix, totals, static_cast<int>(blocks), fine,
                        GridDims{batch_size, cx, cy, cz}, static_cast<const uint32_t *>(grid),

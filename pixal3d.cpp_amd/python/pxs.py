@@ -48,6 +48,8 @@ _SIGS = {
     "pxs_neighbor_pairs_workspace_bytes": (C.c_size_t, [_i64]),
     "pxs_neighbor_pairs": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
     "pxs_subm_conv3d": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "pxs_subm_conv3d_grid": (_i32, [_i32, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i32,
+                                    _i32, _vp, C.c_uint32, _vp, _vp]),
     "pxs_status_reset": (_i32, [_vp, _vp]),
     "pxs_check_finite": (_i32, [_i32, _vp, _i64, _i32, _i64, _vp, _vp]),
     "pxs_value_stats_workspace_bytes": (C.c_size_t, [_i64]),
@@ -353,14 +355,14 @@ class Pxs:
                     "pxs_voxel_grid_tagged_insert")
 
     def map_s2_tagged(self, coords, batch_size, shape, grid, generation, coarse_grid, workspace,
-                      sync=True):
+                      sync=True, with_map=True):
         """pxs_map_s2_topology_tagged -> (nbr [27, n], masks [n], out_coords,
         child_map [8, n], m); m is the host count when sync (else the device
-        int64)."""
+        int64).  with_map=False builds no map (nbr and masks None)."""
         n = coords.shape[0]
         dev = coords.device
-        nbr = torch.empty((27, max(n, 1)), dtype=torch.int32, device=dev)
-        masks = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+        nbr = torch.empty((27, max(n, 1)), dtype=torch.int32, device=dev) if with_map else None
+        masks = torch.empty(max(n, 1), dtype=torch.int32, device=dev) if with_map else None
         oc = torch.empty((max(n, 1), 4), dtype=torch.int32, device=dev)
         child = torch.empty((8, max(n, 1)), dtype=torch.int32, device=dev)
         m = torch.empty(1, dtype=torch.int64, device=dev)
@@ -368,10 +370,12 @@ class Pxs:
             _ptr(coords), n, batch_size, *shape, _ptr(grid), generation, _ptr(nbr), _ptr(masks),
             _ptr(oc), _ptr(child), child.shape[1], _ptr(m), _ptr(coarse_grid), _ptr(workspace),
             self.stream()), "pxs_map_s2_topology_tagged")
+        if with_map:
+            nbr, masks = nbr[:, :n], masks[:n]
         if not sync:
-            return nbr[:, :n], masks[:n], oc, child, m
+            return nbr, masks, oc, child, m
         mm = int(m.item())
-        return nbr[:, :n], masks[:n], oc[:mm], child, mm
+        return nbr, masks, oc[:mm], child, mm
 
     def neighbor_map_tagged(self, coords, batch_size, shape, grid, generation):
         n = coords.shape[0]
@@ -522,6 +526,20 @@ class Pxs:
                                              _ptr(bias), cout, _ptr(nbr), _ptr(masks), _ptr(y),
                                              self.stream()),
                     "pxs_subm_conv3d")
+        return y
+
+    def subm_conv3d_grid(self, x, weight, bias, coords, batch_size, shape, grid, generation=0,
+                         out=None):
+        """pxs_subm_conv3d_grid: neighbours looked up in a dense voxel grid
+        (generation 0: plain grid; 1..255: tagged)."""
+        n, cin = x.shape
+        cout = weight.shape[1]
+        y = torch.empty((n, cout), dtype=x.dtype, device=x.device) if out is None else out
+        self._check(self.lib.pxs_subm_conv3d_grid(_dtype_code(x), _ptr(x), _ptr(coords), n, cin,
+                                                  _ptr(weight), _ptr(bias), cout, batch_size,
+                                                  *shape, _ptr(grid), generation, _ptr(y),
+                                                  self.stream()),
+                    "pxs_subm_conv3d_grid")
         return y
 
     def sparse_conv3d_s2(self, x, weight, bias, child_map, m, out=None):

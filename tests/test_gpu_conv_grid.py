@@ -1,0 +1,128 @@
+"""GPU parity: SubMConv3d with the neighbours looked up in a dense voxel grid
+inside the convolution (pxs_subm_conv3d_grid), against the same convolution
+over the grid's neighbour map (bit for bit: same sources, same tiles, same
+summation order) and against the oracle; the fused U-Net topology without
+its map."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import workloads as W
+from gpu_common import assert_fp32, host, t32, tbf, ti32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def px():
+    import pxs
+    return pxs.Pxs()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return O.Oracle()
+
+
+def _bits(t):
+    import torch
+    return t.view(torch.int32 if t.dtype == torch.float32 else torch.int16).cpu().numpy()
+
+
+def _box_coords(seed, batch, shape, fill):
+    """Random voxels of a small box, every face touched: lookups past the extents."""
+    rng = np.random.default_rng(seed)
+    cells = np.argwhere(rng.random((batch,) + shape) < fill).astype(np.int32)
+    for b in range(batch):  # the box's corners, so every boundary is present
+        for x in (0, shape[0] - 1):
+            for y in (0, shape[1] - 1):
+                for z in (0, shape[2] - 1):
+                    cells = np.vstack([cells, [[b, x, y, z]]])
+    cells = np.unique(cells, axis=0)
+    return np.ascontiguousarray(cells, np.int32)
+
+
+CASES = [
+    # (name, coords builder, batch, extents, cin, cout, dtype)
+    ("config1_f32", lambda: W.conv_fp32_64()["coords"], 1, (64, 64, 64), 64, 64, "f32"),
+    ("config1_bf16", lambda: W.conv_fp32_64()["coords"], 1, (64, 64, 64), 64, 64, "bf16"),
+    ("unet_a_bf16", lambda: W.unet_stage_128()["coords"], 2, (128, 128, 128), 128, 128, "bf16"),
+    ("box_f32", lambda: _box_coords(7, 2, (6, 5, 7), 0.5), 2, (6, 5, 7), 16, 24, "f32"),
+    ("box_bf16", lambda: _box_coords(8, 2, (6, 5, 7), 0.5), 2, (6, 5, 7), 32, 256, "bf16"),
+    ("box_odd_f32", lambda: _box_coords(9, 1, (5, 9, 4), 0.6), 1, (5, 9, 4), 3, 5, "f32"),
+    ("box_odd_bf16", lambda: _box_coords(10, 1, (5, 9, 4), 0.6), 1, (5, 9, 4), 12, 20, "bf16"),
+]
+
+
+@pytest.mark.parametrize("name,make,batch,shape,cin,cout,dtype", CASES, ids=[c[0] for c in CASES])
+def test_conv_grid_matches_map(px, name, make, batch, shape, cin, cout, dtype):
+    """Plain and tagged grids: bit-equal to pxs_subm_conv3d over the grid's map.
+    The tagged grid first holds another coordinate set under an older
+    generation, whose cells must read as absent."""
+    coords = make()
+    n = coords.shape[0]
+    rng = np.random.default_rng(n + cin)
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    w = (rng.standard_normal((27, cout, cin)) * cin ** -0.5).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    conv = tbf if dtype == "bf16" else t32
+    print(f"[conv grid] {name} n={n} {cin}->{cout} {dtype}", flush=True)
+    c = ti32(coords)
+    xd, wd, bd = conv(x), conv(w), t32(b)
+    grid = px.grid_build(c, batch, shape)
+    nbr, masks = px.neighbor_map_grid(c, batch, shape, grid=grid)
+    y_map = px.subm_conv3d(xd, wd, bd, nbr.contiguous(), masks)
+    y_grid = px.subm_conv3d_grid(xd, wd, bd, c, batch, shape, grid, 0)
+    np.testing.assert_array_equal(_bits(y_grid), _bits(y_map))
+    tg = px.tagged_grid(batch, shape)
+    other = _box_coords(11, batch, shape, 0.3) if max(shape) < 16 else coords[::-3].copy()
+    other = np.ascontiguousarray(other[(other[:, 1:] < np.array(shape)).all(1)], np.int32)
+    px.tagged_insert(ti32(other), batch, shape, tg, 3)
+    px.tagged_insert(c, batch, shape, tg, 4)
+    y_tag = px.subm_conv3d_grid(xd, wd, bd, c, batch, shape, tg, 4)
+    np.testing.assert_array_equal(_bits(y_tag), _bits(y_map))
+
+
+def test_conv_grid_fp32_vs_oracle(px, orc):
+    """The reference's CPU-runnable case through the grid convolution, against
+    the oracle at the fp32 bar."""
+    wl = W.conv_fp32_64()
+    c = ti32(wl["coords"])
+    grid = px.grid_build(c, 1, (64, 64, 64))
+    y = px.subm_conv3d_grid(t32(wl["feats"]), t32(wl["weight"]), t32(wl["bias"]), c, 1,
+                            (64, 64, 64), grid, 0)
+    ref = orc.subm_conv3d(wl["coords"], wl["feats"], wl["weight"], wl["bias"])
+    assert_fp32(host(y), ref, what="grid conv fp32 64^3")
+
+
+def test_conv_grid_rejects_bad_arguments(px):
+    import pxs
+    c = ti32(_box_coords(12, 1, (4, 4, 4), 0.5))
+    x = t32(np.ones((c.shape[0], 8), np.float32))
+    w = t32(np.ones((27, 8, 8), np.float32))
+    grid = px.grid_build(c, 1, (4, 4, 4))
+    with pytest.raises(pxs.PxsError, match="generation"):
+        px.subm_conv3d_grid(x, w, None, c, 1, (4, 4, 4), grid, 256)
+    with pytest.raises(pxs.PxsError, match="extents"):
+        px.subm_conv3d_grid(x, w, None, c, 1, (0, 4, 4), grid, 0)
+
+
+def test_map_s2_topology_without_map(px):
+    """pxs_map_s2_topology_tagged with no map: the same coarse coordinates,
+    child slots, count and coarse grid as with it."""
+    import torch
+    wl = W.unet_stage_128()
+    c = ti32(wl["coords"])
+    shape = (128, 128, 128)
+    out = []
+    for with_map in (True, False):
+        tg = px.tagged_grid(2, shape)
+        ws = px.s2_tagged_workspace(2, shape)
+        cg = torch.empty(px.lib.pxs_voxel_grid_bytes(2, 64, 64, 64) // 4, dtype=torch.int32,
+                         device=c.device)
+        nbr, masks, oc, child, m = px.map_s2_tagged(c, 2, shape, tg, 1, cg, ws,
+                                                    with_map=with_map)
+        out.append((oc.cpu().numpy(), child[:, :m].cpu().numpy(), m, cg.cpu().numpy()))
+    for a, b in zip(out[0], out[1]):
+        np.testing.assert_array_equal(a, b)
