@@ -537,8 +537,15 @@ def swin_64(args, torch, px, W):
     qkv = torch.empty((n, 3 * C), dtype=torch.bfloat16, device=dev)
     o = torch.empty((n, C), dtype=torch.bfloat16, device=dev)
     packed = torch.empty((n, 8 * 192), dtype=torch.bfloat16, device=dev)
+    grid = torch.empty(px.lib.pxs_voxel_grid_bytes(1, *wl["shape"]) // 4, dtype=torch.int32,
+                       device=dev)
     timer = Timer(torch)
     win_flops = []
+
+    def build():
+        px._check(px.lib.pxs_voxel_grid_build(coords.data_ptr(), n, 1, *wl["shape"],
+                                              grid.data_ptr(), px.stream()),
+                  "pxs_voxel_grid_build")
 
     def step():
         for shift in wl["shifts"]:
@@ -552,8 +559,10 @@ def swin_64(args, torch, px, W):
             timer.run("window_attention", lambda: px.varlen_attention(
                 q, k, v, cu, cu, H, D, D ** -0.5, row_map=fwd, out=o, nseg=nw))
             timer.run("out", lambda: px.linear(o, w_out, b_out, out=h))
-        nbr, masks = timer.run("neighbor_map", lambda: px.neighbor_map_grid(coords, 1, wl["shape"]))
-        timer.run("up_conv", lambda: px.subm_conv3d(h, w_up, b_up, nbr, masks, out=packed))
+        # the up-conv looks its neighbours up in the voxel grid (no map)
+        timer.run("voxel_grid", build)
+        timer.run("up_conv", lambda: px.subm_conv3d_grid(h, w_up, b_up, coords, 1, wl["shape"],
+                                                         grid, 0, out=packed))
         timer.run("c2s", lambda: px.channel_to_spatial(coords, packed))
 
     dt = timed_steps(args, torch, step, timer)
@@ -564,7 +573,7 @@ def swin_64(args, torch, px, W):
     f_lin = len(wl["shifts"]) * (2.0 * n * C * 3 * C + 2.0 * n * C * C)
     f_up = 2.0 * pairs * C * 8 * 192
     flops = f_win + f_lin + f_up
-    per_op = {k: round(timer.mean_ms(k), 4) for k in ("qkv", "window_attention", "out", "neighbor_map",
+    per_op = {k: round(timer.mean_ms(k), 4) for k in ("qkv", "window_attention", "out", "voxel_grid",
                                                       "up_conv", "c2s", "partition_0", "partition_4")}
     up_tf = f_up / (timer.mean_ms("up_conv") * 1e-3) / 1e12
     # Window attention per shift reads Q, K, V (3C bf16 per row) and the

@@ -1005,6 +1005,18 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
             // (192-row tiles, which put SubMConv3d 256->256 on ~40k rows in
             // one round of tiles instead of 1.2, measured the same: the
             // chip-wide operand rate bounds it, not the last round.)
+            // Long gathers of at least 512 output channels, with two or more
+            // rounds of 256x256 tiles: each stage's 64 KB feed 2x the MACs
+            // of a 128x256 stage's 48 KB (one workgroup per CU either way;
+            // 155.6 KB of LDS with the 27-offset source table).  The C2S
+            // up-convolution 768 -> 1536 at 64^3: 1.97 -> 1.61 ms; the SLat
+            // decoder 27.3 -> 25.6 ms.
+#ifndef PXS_GEMM_SQUARE256
+#define PXS_GEMM_SQUARE256 1
+#endif
+            if (PXS_GEMM_SQUARE256 && (args.rowmap || args.grid) && args.cout >= 512 &&
+                kstages >= 32 && ((args.m + 255) / 256) * ((args.cout + 255) / 256) >= 512)
+                return launch_lds_tile<T, 256, 256, EPI, 2, 8, 2, 1>(args, stream);
             if (PXS_GEMM_WIDE && (args.rowmap || args.grid) && args.cout > 128 && kstages >= 32)
                 return launch_lds_tile<T, 128, 256, EPI, 2, 8, 2, 1>(args, stream);
         }

@@ -126,3 +126,32 @@ def test_map_s2_topology_without_map(px):
         out.append((oc.cpu().numpy(), child[:, :m].cpu().numpy(), m, cg.cpu().numpy()))
     for a, b in zip(out[0], out[1]):
         np.testing.assert_array_equal(a, b)
+
+
+def test_conv_bf16_square_tiles(px):
+    """A gather wide enough for 256 x 256 tiles (2,112 outputs: a partial last
+    column tile; 16,344 rows: a partial last row tile): sampled rows in float64
+    from the GPU map, and the grid form bit-equal to the map form."""
+    coords = W.shell_coords(48, [[(12.0, 22.0)], [(10.0, 20.0)]], 43)
+    n, cin, cout = coords.shape[0], 128, 2112  # 54 K stages: the 256 x 256 tiles' condition
+    x = W.bf16_round(W.normal(44, n * cin, 1).reshape(n, cin))
+    w = W.bf16_round(W.normal(44, 27 * cout * cin, 2, std=float(np.sqrt(2 / (27 * cin))))
+                     .reshape(27, cout, cin))
+    b = W.normal(44, cout, 3, std=0.1)
+    print(f"[conv bf16 256x256 tiles] n={n} {cin}->{cout}", flush=True)
+    c = ti32(coords)
+    grid = px.grid_build(c, 2, (48, 48, 48))
+    nbr, masks = px.neighbor_map_grid(c, 2, (48, 48, 48), grid=grid)
+    xd, wd, bd = tbf(x), tbf(w), t32(b)
+    y_map = px.subm_conv3d(xd, wd, bd, nbr.contiguous(), masks)
+    idx = nbr.cpu().numpy()
+    rows = np.linspace(0, n - 1, 700).astype(np.int64)
+    ref = np.tile(b.astype(np.float64), (rows.size, 1))
+    for k in range(27):
+        src = idx[k, rows]
+        ok = src != n
+        ref[ok] += x[src[ok]].astype(np.float64) @ w[k].astype(np.float64).T
+    from gpu_common import assert_bf16
+    assert_bf16(host(y_map)[rows], ref, what="bf16 conv 256x256 tiles")
+    y_grid = px.subm_conv3d_grid(xd, wd, bd, c, 2, (48, 48, 48), grid, 0)
+    np.testing.assert_array_equal(_bits(y_grid), _bits(y_map))
