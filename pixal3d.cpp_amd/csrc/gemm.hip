@@ -1014,8 +1014,11 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
 #ifndef PXS_GEMM_SQUARE256
 #define PXS_GEMM_SQUARE256 1
 #endif
+#ifndef PXS_GEMM_SQUARE256_TILES
+#define PXS_GEMM_SQUARE256_TILES 512
+#endif
             if (PXS_GEMM_SQUARE256 && (args.rowmap || args.grid) && args.cout >= 512 &&
-                kstages >= 32 && ((args.m + 255) / 256) * ((args.cout + 255) / 256) >= 512)
+                kstages >= 32 && ((args.m + 255) / 256) * ((args.cout + 255) / 256) >= PXS_GEMM_SQUARE256_TILES)
                 return launch_lds_tile<T, 256, 256, EPI, 2, 8, 2, 1>(args, stream);
             if (PXS_GEMM_WIDE && (args.rowmap || args.grid) && args.cout > 128 && kstages >= 32)
                 return launch_lds_tile<T, 128, 256, EPI, 2, 8, 2, 1>(args, stream);
