@@ -106,6 +106,10 @@ def test_conv_grid_rejects_bad_arguments(px):
         px.subm_conv3d_grid(x, w, None, c, 1, (4, 4, 4), grid, 256)
     with pytest.raises(pxs.PxsError, match="extents"):
         px.subm_conv3d_grid(x, w, None, c, 1, (0, 4, 4), grid, 0)
+    # zero rows: nothing to do, no error
+    px._check(px.lib.pxs_subm_conv3d_grid(pxs.PXS_F32, x.data_ptr(), c.data_ptr(), 0, 8,
+                                          w.data_ptr(), None, 8, 1, 4, 4, 4, grid.data_ptr(), 0,
+                                          x.data_ptr(), px.stream()), "zero rows")
 
 
 def test_map_s2_topology_without_map(px):
