@@ -11,8 +11,8 @@
 // C = D = the fp32 residual with beta = 1.
 //
 // One handle per device; matrix layouts and the heuristic's algorithm are
-// cached per shape and workspace cap, the matmul descriptor (which holds the
-// bias pointer) is made per call.  The library's workspace is the caller's
+// cached per shape and workspace cap (at most 4096 shapes), the matmul
+// descriptor (which holds the bias pointer) is made per call.  The library's workspace is the caller's
 // (compositions carve kLibWorkspaceBytes from their own workspace; the plain
 // entry points have none, and then only algorithms that need no workspace
 // qualify): nothing is allocated per call.  Tall products over few channels
@@ -26,17 +26,28 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
+#include <memory>
 #include <mutex>
 #include <tuple>
 
 namespace pxs {
 namespace {
 
+// Layouts and algorithm of one shape.  Held by shared pointer: a call keeps
+// its shape alive while it runs, even if another thread's miss evicts it.
 struct Shape {
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
     size_t workspace = 0;
     bool ok = false;
+    Shape() = default;
+    Shape(const Shape &) = delete;
+    Shape & operator=(const Shape &) = delete;
+    ~Shape() {
+        if (a) hipblasLtMatrixLayoutDestroy(a);
+        if (b) hipblasLtMatrixLayoutDestroy(b);
+        if (c) hipblasLtMatrixLayoutDestroy(c);
+    }
 };
 
 // (device, rows, cin, cout, epilogue, A/B type, D type, accumulate, workspace cap)
@@ -44,7 +55,11 @@ using ShapeKey = std::tuple<int, int64_t, int, int, int, int, int, int, size_t>;
 
 std::mutex g_mutex;
 std::map<int, hipblasLtHandle_t> g_handles;
-std::map<ShapeKey, Shape> g_shapes;
+std::map<ShapeKey, std::shared_ptr<const Shape>> g_shapes;
+
+// Row counts vary from call to call (each input has its own voxel count), so
+// the cache is bounded: past this many entries it starts over.
+constexpr size_t kMaxShapes = 4096;
 
 bool set_desc(hipblasLtMatmulDesc_t desc, hipblasLtMatmulDescAttributes_t attr, const void * v,
               size_t bytes) {
@@ -74,14 +89,17 @@ hipblasLtMatmulDesc_t make_desc(hipblasLtEpilogue_t epi, const float * bias) {
 }
 
 // The cached layouts and algorithm of a shape, or nullptr (no algorithm).
-const Shape * shape_for(int device, hipblasLtHandle_t handle, int64_t rows, int cin, int cout,
+// Called with g_mutex held.
+std::shared_ptr<const Shape> shape_for(int device, hipblasLtHandle_t handle, int64_t rows, int cin, int cout,
                         hipblasLtEpilogue_t epi, hipDataType dtype_in, hipDataType dtype_d,
                         bool accumulate, size_t ws_cap) {
     const ShapeKey key{device, rows, cin, cout, static_cast<int>(epi), static_cast<int>(dtype_in),
                        static_cast<int>(dtype_d), accumulate ? 1 : 0, ws_cap};
     auto it = g_shapes.find(key);
-    if (it != g_shapes.end()) return it->second.ok ? &it->second : nullptr;
-    Shape sh;
+    if (it != g_shapes.end()) return it->second->ok ? it->second : nullptr;
+    if (g_shapes.size() >= kMaxShapes) g_shapes.clear();  // shapes in use stay alive
+    auto made = std::make_shared<Shape>();
+    Shape & sh = *made;
     bool ok = hipblasLtMatrixLayoutCreate(&sh.a, dtype_in, cin, cout, cin) == HIPBLAS_STATUS_SUCCESS &&
               hipblasLtMatrixLayoutCreate(&sh.b, dtype_in, cin, rows, cin) == HIPBLAS_STATUS_SUCCESS &&
               hipblasLtMatrixLayoutCreate(&sh.c, dtype_d, cout, rows, cout) == HIPBLAS_STATUS_SUCCESS;
@@ -103,9 +121,8 @@ const Shape * shape_for(int device, hipblasLtHandle_t handle, int64_t rows, int 
         hipblasLtMatmulPreferenceDestroy(pref);
     }
     if (desc) hipblasLtMatmulDescDestroy(desc);
-    auto & slot = g_shapes[key];
-    slot = sh;
-    return slot.ok ? &slot : nullptr;
+    g_shapes[key] = made;
+    return sh.ok ? made : nullptr;
 }
 
 bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -149,7 +166,7 @@ int blaslt_linear(int dtype, const void * x, int64_t rows, int cin, const void *
     const hipDataType dtype_in = dtype == PXS_F32 ? HIP_R_32F : HIP_R_16BF;
     const hipDataType dtype_d = y_dtype == PXS_F32 ? HIP_R_32F : HIP_R_16BF;
     hipblasLtHandle_t handle = nullptr;
-    const Shape * sh = nullptr;
+    std::shared_ptr<const Shape> sh;
     {
         std::lock_guard<std::mutex> lock(g_mutex);
         auto hit = g_handles.find(device);
