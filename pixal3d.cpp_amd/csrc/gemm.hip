@@ -505,8 +505,26 @@ gather_gemm_lds_kernel(GemmArgs a) {
 
     if (tid == 0) tile_mask = 0;
     __syncthreads();
+    // A map without masks (the stride-2 conv's child map) is read once: every
+    // offset's sources go into idx_lds[k * BM + row] while the mask is formed,
+    // as in grid mode, instead of a mask pass and then a pass over the
+    // present offsets.
+    const bool full_table = a.grid || (a.rowmap && !a.masks);
     if (a.grid) {
         grid_tile_sources<BM>(a, p0, tid, kThreads, idx_lds, &tile_mask);
+    } else if (full_table) {
+        uint32_t local = 0;
+        for (int e = tid; e < a.noff * BM; e += kThreads) {
+            const int k = e / BM, row = e % BM;
+            int32_t src = -1;
+            if (p0 + row < a.m) {
+                const int32_t s = a.rowmap[k * a.ld_map + p0 + row];
+                src = (s >= 0 && s < a.rows_in) ? s : -1;
+            }
+            idx_lds[e] = src;
+            if (src >= 0) local |= 1u << k;
+        }
+        if (local) atomicOr(&tile_mask, local);
     } else {
         uint32_t local = 0;
         for (int row = tid; row < BM; row += kThreads) {
@@ -536,9 +554,9 @@ gather_gemm_lds_kernel(GemmArgs a) {
         }
     }
     __syncthreads();
-    // idx_lds rows: the tile's present offsets in order (i), or in grid mode
-    // all 27 (k = koff[i]).
-    for (int e = tid; !a.grid && e < kcount * BM; e += kThreads) {
+    // idx_lds rows: the tile's present offsets in order (i), or with a full
+    // table every offset (k = koff[i]).
+    for (int e = tid; !full_table && e < kcount * BM; e += kThreads) {
         const int i = e / BM, row = e % BM;
         int32_t src = -1;
         if (p0 + row < a.m) {
@@ -579,7 +597,7 @@ gather_gemm_lds_kernel(GemmArgs a) {
         const int k = koff[i];
         char * base = smem + (s % NSTAGE) * kStageBytes;
         int32_t src[AI];
-        const int slot = a.grid ? k : i;
+        const int slot = full_table ? k : i;
 #pragma unroll
         for (int j = 0; j < AI; ++j) src[j] = idx_lds[slot * BM + a_row[j]];
 #pragma unroll
@@ -631,7 +649,7 @@ gather_gemm_lds_kernel(GemmArgs a) {
         for (int i = 0; i < TI; ++i) {
             row_ok[i] = true;
             if constexpr (kMaskAbsent)
-                row_ok[i] = idx_lds[(a.grid ? koff[s / chunks] : s / chunks) * BM + wm * WM + i * 32 + r] >= 0;
+                row_ok[i] = idx_lds[(full_table ? koff[s / chunks] : s / chunks) * BM + wm * WM + i * 32 + r] >= 0;
         }
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
