@@ -167,10 +167,11 @@ int pxs_subm_conv3d(int dtype, const void * x, int64_t n, int cin, const void * 
                     const float * bias, int cout, const int32_t * nbr, const uint32_t * masks,
                     void * y, void * stream);
 
-/* pxs_subm_conv3d with the neighbours looked up in a dense voxel grid of the
- * same coords and extents inside the convolution (each tile reads the 27
- * cells around its rows' coordinates), so no neighbour map is built or read:
- * the map of src/slat_decoder.cpp:609-668 fused into the gather.  grid is a
+/* sparse_submanifold_conv3d (src/sparse.cpp:999-1055) as pxs_subm_conv3d,
+ * with the neighbours looked up in a dense voxel grid of the same coords and
+ * extents inside the convolution (each tile reads the 27 cells around its
+ * rows' coordinates), so no neighbour map is built or read: the map of
+ * src/slat_decoder.cpp:609-668 fused into the gather.  grid is a
  * plain grid (pxs_voxel_grid_build, generation 0) or a tagged one
  * (pxs_voxel_grid_tagged_insert or pxs_map_s2_topology_tagged with that
  * generation, 1..255, at most 2^24 - 1 rows).  Output identical to
