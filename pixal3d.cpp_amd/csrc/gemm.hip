@@ -1381,6 +1381,8 @@ int pxs_subm_conv3d_grid(int dtype, const void * x, const int32_t * coords, int6
               "pxs_subm_conv3d_grid: null pointer");
     PXS_CHECK((reinterpret_cast<uintptr_t>(coords) & 15u) == 0, PXS_ERR_ARG,
               "pxs_subm_conv3d_grid: coordinates must be 16-byte aligned");
+    PXS_CHECK((reinterpret_cast<uintptr_t>(grid) & 3u) == 0, PXS_ERR_ARG,
+              "pxs_subm_conv3d_grid: the grid must be 4-byte aligned");
     GemmArgs a{};
     a.x = x; a.rows_in = n; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
     a.cout = cout; a.m = n; a.rowmap = nullptr; a.ld_map = 0; a.noff = 27; a.masks = nullptr;
