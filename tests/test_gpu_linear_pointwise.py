@@ -372,3 +372,20 @@ def test_linear_with_workspace(px, orc, dtype, rows, cin, cout):
     px.linear_residual(conv(x), conv(w), t32(b), res, workspace=ws)
     torch.cuda.synchronize()
     check(host(res), res0 + lin, what="linear residual ws")
+
+
+def test_linear_workspace_misaligned_rejected(px):
+    """pxs_linear_ws rejects a workspace that is not 256-byte aligned, before
+    anything is enqueued, and takes NULL (no workspace) as the plain call."""
+    import pxs
+    x = tbf(np.ones((512, 64), np.float32))
+    w = tbf(np.full((256, 64), 0.5, np.float32))
+    ws = px.linear_workspace()
+    y = px.linear(x, w, None, workspace=ws)
+    with pytest.raises(pxs.PxsError, match="workspace"):
+        px._check(px.lib.pxs_linear_ws(pxs.PXS_BF16, x.data_ptr(), 512, 64, w.data_ptr(), None,
+                                       256, pxs.ACT_NONE, y.data_ptr(), ws.data_ptr() + 16,
+                                       px.stream()), "pxs_linear_ws")
+    px._check(px.lib.pxs_linear_ws(pxs.PXS_BF16, x.data_ptr(), 512, 64, w.data_ptr(), None, 256,
+                                   pxs.ACT_NONE, y.data_ptr(), None, px.stream()), "no workspace")
+    np.testing.assert_array_equal(host(y), np.full((512, 256), 32.0, np.float32))
