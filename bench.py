@@ -53,7 +53,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="unet_stage_128",
                     choices=["unet_stage_128", "conv_fp32_64", "attn_block", "swin_64",
-                             "flow_step", "flow_sample", "decoder", "pack_load", "hash_map_128"])
+                             "flow_step", "flow_sample", "decoder", "pack_load", "hash_map_128",
+                             "linear_dense"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     return ap.parse_args()
@@ -539,7 +540,6 @@ def swin_64(args, torch, px, W):
     packed = torch.empty((n, 8 * 192), dtype=torch.bfloat16, device=dev)
     grid = torch.empty(px.lib.pxs_voxel_grid_bytes(1, *wl["shape"]) // 4, dtype=torch.int32,
                        device=dev)
-    lws = px.linear_workspace()  # the library GEMMs' workspace (QKV 768 -> 2304: 231 -> 159 us)
     timer = Timer(torch)
     win_flops = []
 
@@ -555,11 +555,11 @@ def swin_64(args, torch, px, W):
             if len(win_flops) < len(wl["shifts"]):
                 lens = (cu[1:] - cu[:-1]).cpu().double()
                 win_flops.append(float(4.0 * (lens * lens).sum() * D * H))
-            timer.run("qkv", lambda: px.linear(h, w_qkv, b_qkv, out=qkv, workspace=lws))
+            timer.run("qkv", lambda: px.linear(h, w_qkv, b_qkv, out=qkv))
             q, k, v = qkv[:, :C], qkv[:, C:2 * C], qkv[:, 2 * C:]
             timer.run("window_attention", lambda: px.varlen_attention(
                 q, k, v, cu, cu, H, D, D ** -0.5, row_map=fwd, out=o, nseg=nw))
-            timer.run("out", lambda: px.linear(o, w_out, b_out, out=h, workspace=lws))
+            timer.run("out", lambda: px.linear(o, w_out, b_out, out=h))
         # the up-conv looks its neighbours up in the voxel grid (no map)
         timer.run("voxel_grid", build)
         timer.run("up_conv", lambda: px.subm_conv3d_grid(h, w_up, b_up, coords, 1, wl["shape"],
@@ -933,9 +933,87 @@ def hash_map_128(args, torch, px, W):
                          "traffic": None}}
 
 
+# Linear shapes: the configs' block linears (bf16) and the reference's hot
+# sparse_linear shapes (tests/sparse_linear_cuda_benchmark.cpp:42-52, fp32).
+LINEAR_SHAPES = [
+    ("attn_block qkv", "bf16", 32768, 1024, 3072), ("attn_block out", "bf16", 32768, 1024, 1024),
+    ("flow mlp0", "bf16", 40960, 1024, 4096), ("flow mlp2", "bf16", 40960, 4096, 1024),
+    ("flow qkv", "bf16", 40960, 1024, 3072), ("swin qkv", "bf16", 29700, 768, 2304),
+    ("swin out", "bf16", 29700, 768, 768), ("decoder mlp0", "bf16", 2492211, 64, 256),
+    ("decoder mlp2", "bf16", 2492211, 256, 64),
+    ("hot n46537 2048->512", "f32", 46537, 2048, 512), ("hot n46537 512->2048", "f32", 46537, 512, 2048),
+    ("hot n206980 1024->256", "f32", 206980, 1024, 256), ("hot n206980 256->1024", "f32", 206980, 256, 1024),
+    ("hot n909164 512->128", "f32", 909164, 512, 128), ("hot n909164 128->512", "f32", 909164, 128, 512),
+    ("hot n9857 4096->1024", "f32", 9857, 4096, 1024), ("hot n9857 1024->4096", "f32", 9857, 1024, 4096),
+]
+
+
+def linear_dense(args, torch, px, W):
+    """pxs_linear (the dense MFMA kernel) on each shape of LINEAR_SHAPES, timed
+    with HIP events, next to torch's linear on the same operands (hipBLASLt:
+    a comparison leg only).  value = all shapes' flops / all shapes' time."""
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    steps = max(5, min(args.steps, 50))
+    rows_out, total_f, total_t = [], 0.0, 0.0
+    qkv = None
+    for name, dt, m, k, n in LINEAR_SHAPES:
+        tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+        g = torch.Generator(device=dev).manual_seed(m + k + n)
+        x = torch.randn(m, k, device=dev, generator=g).to(tdt)
+        w = (torch.randn(n, k, device=dev, generator=g) * k ** -0.5).to(tdt)
+        b = torch.randn(n, device=dev, generator=g) * 0.1
+        y = torch.empty(m, n, device=dev, dtype=tdt)
+        bt = b.to(tdt)
+
+        def ours():
+            px.linear(x, w, b, out=y)
+
+        def lib():
+            torch.nn.functional.linear(x, w, bt)
+
+        res = {}
+        for leg, fn in (("pxs", ours), ("hipblaslt", lib)):
+            t0 = time.perf_counter()  # warm up for 0.2 s so the clocks settle
+            while time.perf_counter() - t0 < 0.2:
+                for _ in range(3):
+                    fn()
+                torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            res[leg] = e0.elapsed_time(e1) / steps
+        flops = 2.0 * m * k * n
+        total_f += flops
+        total_t += res["pxs"] * 1e-3
+        row = {"shape": name, "dtype": dt, "rows": m, "cin": k, "cout": n,
+               "pxs_us": round(res["pxs"] * 1e3, 1), "hipblaslt_us": round(res["hipblaslt"] * 1e3, 1),
+               "pxs_tflops": round(flops / (res["pxs"] * 1e-3) / 1e12, 1),
+               "hipblaslt_tflops": round(flops / (res["hipblaslt"] * 1e-3) / 1e12, 1),
+               "ratio": round(res["hipblaslt"] / res["pxs"], 3)}
+        rows_out.append(row)
+        if name == "attn_block qkv":
+            qkv = row
+        del x, w, y
+        torch.cuda.empty_cache()
+    achieved = qkv["pxs_tflops"]
+    return {"metric": "dense linear TFLOP/s (pxs_linear), bf16 block shapes and fp32 reference shapes",
+            "value": round(total_f / total_t / 1e12, 2), "unit": "TFLOP/s",
+            "ms_per_step": round(total_t * 1e3, 4), "dtype": "bf16+f32",
+            "config": {"workload": f"linear_dense: {len(LINEAR_SHAPES)} shapes, {steps} calls each, "
+                                   "torch.nn.functional.linear (hipBLASLt) timed beside each",
+                       "shapes": rows_out},
+            "roofline": {"bound": "mfma", "kernel": "dense_gemm (attn_block qkv 32768x1024->3072)",
+                         "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}}
+
+
 OTHER_WORKLOADS = {"conv_fp32_64": conv_fp32_64, "attn_block": attn_block, "swin_64": swin_64,
                    "flow_sample": flow_sample, "decoder": decoder, "pack_load": pack_load,
-                   "flow_step": flow_step, "hash_map_128": hash_map_128}
+                   "flow_step": flow_step, "hash_map_128": hash_map_128, "linear_dense": linear_dense}
 
 
 def main():

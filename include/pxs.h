@@ -302,21 +302,6 @@ int pxs_linear_gate_residual(int dtype, const void * x, int64_t rows, int cin,
 int pxs_linear_residual(int dtype, const void * x, int64_t rows, int cin, const void * weight,
                         const float * bias, int cout, float * residual, void * stream);
 
-/* pxs_linear and pxs_linear_residual (sparse_linear / varlen_linear,
- * src/sparse.cpp:337-488, and the residual add of
- * src/sparse_transformer.cpp:57-69) with a workspace for the library GEMM: pxs_linear_workspace_bytes() bytes, 256-byte aligned
- * (NULL: none, as in the plain calls).  Products over many rows and few
- * channels have faster algorithms that need one (2.5M rows, 64 -> 256 bf16:
- * 2.3x; fp32 tall products 2-5x); without it only algorithms that need none
- * are used.  Calls that overlap on one workspace race. */
-size_t pxs_linear_workspace_bytes(void);
-int pxs_linear_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
-                  const float * bias, int cout, int act, void * y, void * workspace,
-                  void * stream);
-int pxs_linear_residual_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
-                           const float * bias, int cout, float * residual, void * workspace,
-                           void * stream);
-
 /* ---- a10-a12: row-wise normalisation and position embedding ------------------- */
 
 /* sparse_layer_norm (src/sparse.cpp:490-534); gamma/beta both NULL or both set.

@@ -28,7 +28,6 @@ struct BlockBuffers {
     void * att;   // [rows, C]       attention output
     void * ckv;   // [T, 2C]         context K | V
     void * ck;    // [T, C]          RMS-normed context K
-    float * lin;  // [rows, C] fp32  a gated linear's output before its gate (fp32: xm)
     void * attn_ws;
 };
 
@@ -48,9 +47,6 @@ BlockBuffers carve_block(Carver & c, int dtype, const pxs_block_config & cfg, in
     b.att = c.take(r * C * e);
     b.ckv = c.take(t * 2 * C * e);
     b.ck = c.take(t * C * e);
-    // xm (the LN output) is consumed before each gated linear runs, so in
-    // fp32 it serves as that linear's scratch.
-    b.lin = dtype == PXS_BF16 ? static_cast<float *>(c.take(r * C * 4)) : static_cast<float *>(b.xm);
     b.attn_ws = c.take(pxs_attention_workspace_bytes(batch_size));
     return b;
 }
@@ -90,38 +86,32 @@ int run_block(int dtype, const pxs_block_config & cfg, const pxs_block_weights &
     const int C = cfg.channels, H = cfg.num_heads, hd = C / H;
     const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
     const size_t e = dtype_bytes(dtype);
-    // v is dead outside the self-attention (qkv_prepare writes it, the
-    // attention reads it), so it serves every linear as the library GEMM's
-    // workspace.
-    hipStream_t s = as_stream(stream);
-    void * const lws = b.v;
-    const size_t lws_bytes = static_cast<size_t>(std::max<int64_t>(rows, 1)) * C * e;
 
     // Self-attention branch.
     PXS_TRY(pxs_layer_norm_modulate(PXS_F32, hidden, rows, C, cfg.norm_eps, coords, w.modulation,
                                     time_mod, 0, dtype, b.xm, stream));
-    PXS_TRY(linear_ws(dtype, b.xm, rows, C, w.self_to_qkv_weight, w.self_to_qkv_bias, 3 * C,
-                      PXS_ACT_NONE, b.big, lws, lws_bytes, s));
+    PXS_TRY(pxs_linear(dtype, b.xm, rows, C, w.self_to_qkv_weight, w.self_to_qkv_bias, 3 * C,
+                       PXS_ACT_NONE, b.big, stream));
     PXS_TRY(pxs_qkv_prepare(dtype, b.big, rows, H, hd, cfg.qk_rms_norm ? w.self_q_gamma : nullptr,
                             cfg.qk_rms_norm ? w.self_k_gamma : nullptr,
                             cfg.use_rope ? coords : nullptr, cfg.rope_freq_min,
                             cfg.rope_freq_base, b.q, b.k, b.v, stream));
     PXS_TRY(pxs_varlen_attention(dtype, b.q, C, b.k, C, b.v, C, cu_rows, cu_rows, batch_size, rows,
                                  nullptr, H, hd, hd, scale, b.att, C, b.attn_ws, stream));
-    PXS_TRY(linear_gate_residual_scratch(dtype, b.att, rows, C, w.self_to_out_weight,
-                                         w.self_to_out_bias, C, coords, w.modulation, time_mod,
-                                         2 * C, hidden, b.lin, lws, lws_bytes, s));
+    PXS_TRY(pxs_linear_gate_residual(dtype, b.att, rows, C, w.self_to_out_weight,
+                                     w.self_to_out_bias, C, coords, w.modulation, time_mod, 2 * C,
+                                     hidden, stream));
 
     // Cross-attention branch.
     PXS_TRY(pxs_layer_norm(PXS_F32, hidden, rows, C, cfg.norm_eps, w.norm2_weight, w.norm2_bias,
                            dtype, b.xm, stream));
-    PXS_TRY(linear_ws(dtype, b.xm, rows, C, w.cross_to_q_weight, w.cross_to_q_bias, C,
-                      PXS_ACT_NONE, b.q, lws, lws_bytes, s));
+    PXS_TRY(pxs_linear(dtype, b.xm, rows, C, w.cross_to_q_weight, w.cross_to_q_bias, C,
+                       PXS_ACT_NONE, b.q, stream));
     if (cfg.qk_rms_norm_cross) {
         PXS_TRY(pxs_mh_rms_norm(dtype, b.q, C, rows, H, hd, w.cross_q_gamma, b.q, C, stream));
     }
-    PXS_TRY(linear_ws(dtype, context, tokens, cfg.context_channels, w.cross_to_kv_weight,
-                      w.cross_to_kv_bias, 2 * C, PXS_ACT_NONE, b.ckv, lws, lws_bytes, s));
+    PXS_TRY(pxs_linear(dtype, context, tokens, cfg.context_channels, w.cross_to_kv_weight,
+                       w.cross_to_kv_bias, 2 * C, PXS_ACT_NONE, b.ckv, stream));
     const void * ck = b.ckv;
     int64_t ld_k = 2 * C;
     if (cfg.qk_rms_norm_cross) {
@@ -134,21 +124,21 @@ int run_block(int dtype, const pxs_block_config & cfg, const pxs_block_weights &
     PXS_TRY(pxs_varlen_attention(dtype, b.q, C, ck, ld_k, cv, 2 * C, cu_rows, context_offsets,
                                  batch_size, rows, nullptr, H, hd, hd, scale, b.att, C, b.attn_ws,
                                  stream));
-    PXS_TRY(linear_residual_ws(dtype, b.att, rows, C, w.cross_to_out_weight, w.cross_to_out_bias,
-                               C, hidden, lws, lws_bytes, s));
+    PXS_TRY(pxs_linear_residual(dtype, b.att, rows, C, w.cross_to_out_weight, w.cross_to_out_bias,
+                                C, hidden, stream));
     if (cfg.use_projection) {
-        PXS_TRY(linear_residual_ws(dtype, projected, rows, cfg.proj_in_channels, w.proj_weight,
-                                   w.proj_bias, C, hidden, lws, lws_bytes, s));
+        PXS_TRY(pxs_linear_residual(dtype, projected, rows, cfg.proj_in_channels, w.proj_weight,
+                                    w.proj_bias, C, hidden, stream));
     }
 
     // MLP branch.
     PXS_TRY(pxs_layer_norm_modulate(PXS_F32, hidden, rows, C, cfg.norm_eps, coords, w.modulation,
                                     time_mod, 3 * C, dtype, b.xm, stream));
-    PXS_TRY(linear_ws(dtype, b.xm, rows, C, w.mlp0_weight, w.mlp0_bias, cfg.mlp_hidden,
-                      PXS_ACT_GELU_TANH, b.big, lws, lws_bytes, s));
-    PXS_TRY(linear_gate_residual_scratch(dtype, b.big, rows, cfg.mlp_hidden, w.mlp2_weight,
-                                         w.mlp2_bias, C, coords, w.modulation, time_mod, 5 * C,
-                                         hidden, b.lin, lws, lws_bytes, s));
+    PXS_TRY(pxs_linear(dtype, b.xm, rows, C, w.mlp0_weight, w.mlp0_bias, cfg.mlp_hidden,
+                       PXS_ACT_GELU_TANH, b.big, stream));
+    PXS_TRY(pxs_linear_gate_residual(dtype, b.big, rows, cfg.mlp_hidden, w.mlp2_weight,
+                                     w.mlp2_bias, C, coords, w.modulation, time_mod, 5 * C, hidden,
+                                     stream));
     return PXS_OK;
 }
 

@@ -202,11 +202,8 @@ int pxs_convnext_block(int dtype, const int32_t * coords, int64_t rows, const fl
                             nbr, masks, b.conv, stream));
     PXS_TRY(pxs_layer_norm(dtype, b.conv, rows, channels, eps, w->norm_weight, w->norm_bias, dtype,
                            b.norm, stream));
-    // The convolution output is dead once normed: it is the library GEMMs'
-    // workspace for both MLP linears.
-    const size_t lws_bytes = static_cast<size_t>(rows) * channels * dtype_bytes(dtype);
-    PXS_TRY(linear_ws(dtype, b.norm, rows, channels, w->mlp0_weight, w->mlp0_bias, mlp_hidden,
-                      PXS_ACT_SILU, b.hid, b.conv, lws_bytes, s));
+    PXS_TRY(pxs_linear(dtype, b.norm, rows, channels, w->mlp0_weight, w->mlp0_bias, mlp_hidden,
+                       PXS_ACT_SILU, b.hid, stream));
     // The residual add is the epilogue of the second MLP linear; the input is
     // read by the convolution above, so y may alias x.
     if (y != x) {
@@ -214,8 +211,8 @@ int pxs_convnext_block(int dtype, const int32_t * coords, int64_t rows, const fl
                                          hipMemcpyDeviceToDevice, s),
                           "pxs_convnext_block: copy"));
     }
-    return linear_residual_ws(dtype, b.hid, rows, mlp_hidden, w->mlp2_weight, w->mlp2_bias,
-                              channels, y, b.conv, lws_bytes, s);
+    return pxs_linear_residual(dtype, b.hid, rows, mlp_hidden, w->mlp2_weight, w->mlp2_bias,
+                               channels, y, stream);
 }
 
 size_t pxs_resblock_c2s_workspace_bytes(int dtype, int64_t rows, int channels,

@@ -117,15 +117,6 @@ template <> struct Mfma<float> {
     static constexpr int kChunk = 32;
 };
 
-__device__ __forceinline__ int remap_xcd(int bid, int blocks) {
-    // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
-    // contiguous range of logical tiles so neighbouring tiles (which share
-    // gathered rows and weights) share one L2.
-    const int q = blocks / 8, rem = blocks % 8;
-    const int xcd = bid % 8, slot = bid / 8;
-    return (xcd < rem) ? xcd * (q + 1) + slot : rem * (q + 1) + (xcd - rem) * q + slot;
-}
-
 template <typename T>
 __device__ __forceinline__ uint4 load_chunk16(const T * base, int64_t row, int64_t ld, int col,
                                               int limit, bool vec_ok) {
@@ -422,38 +413,6 @@ __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1
 #define PXS_GEMM_MASK_ABSENT 0
 #endif
 constexpr bool kMaskAbsent = PXS_GEMM_MASK_ABSENT != 0;
-
-__device__ __forceinline__ void wait_vmcnt(int n) {
-    // s_waitcnt with expcnt/lgkmcnt at their maxima: only vmcnt is waited on.
-    switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
-    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
-    case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
-    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-    case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
-    case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
-    case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
-    case 16: __builtin_amdgcn_s_waitcnt(0x4F70); break;
-    case 17: __builtin_amdgcn_s_waitcnt(0x4F71); break;
-    case 18: __builtin_amdgcn_s_waitcnt(0x4F72); break;
-    case 19: __builtin_amdgcn_s_waitcnt(0x4F73); break;
-    case 20: __builtin_amdgcn_s_waitcnt(0x4F74); break;
-    case 21: __builtin_amdgcn_s_waitcnt(0x4F75); break;
-    case 22: __builtin_amdgcn_s_waitcnt(0x4F76); break;
-    case 23: __builtin_amdgcn_s_waitcnt(0x4F77); break;
-    case 24: __builtin_amdgcn_s_waitcnt(0x4F78); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    }
-}
 
 template <int BM, int BN, int NSTAGE>
 constexpr int lds_gemm_bytes(int noff) {
@@ -1234,68 +1193,13 @@ int launch_ordered_rows(const float * x, int64_t rows, int cin, const float * we
     return check_launch("ordered linear (rows)");
 }
 
-// residual[r, c] += value[r, c] * (block_mod[off + c] + time_mod[batch(r), off + c]):
-// the gate-residual epilogue of gemm_epilogue over a linear's fp32 output
-// (value = x W^T + bias), 4 channels per thread.
-__global__ void gate_residual_kernel(const float * __restrict__ value, int64_t rows, int cout,
-                                     const int32_t * __restrict__ coords,
-                                     const float * __restrict__ block_mod,
-                                     const float * __restrict__ time_mod, int gate_offset,
-                                     float * __restrict__ residual) {
-    const int64_t vpr = cout / 4;
-    const int64_t total = rows * vpr;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-         i += stride) {
-        const int64_t r = i / vpr;
-        const int c = static_cast<int>(i - r * vpr) * 4;
-        const int batch = coords[r * 4];
-        const float4 v = *reinterpret_cast<const float4 *>(value + r * cout + c);
-        const float4 b = *reinterpret_cast<const float4 *>(block_mod + gate_offset + c);
-        const float4 t = *reinterpret_cast<const float4 *>(
-            time_mod + static_cast<int64_t>(batch) * 6 * cout + gate_offset + c);
-        float4 * res = reinterpret_cast<float4 *>(residual + r * cout + c);
-        float4 o = *res;
-        o.x = o.x + v.x * (b.x + t.x);
-        o.y = o.y + v.y * (b.y + t.y);
-        o.z = o.z + v.z * (b.z + t.z);
-        o.w = o.w + v.w * (b.w + t.w);
-        *res = o;
-    }
-}
-
 } // namespace
 
-// pxs_linear_gate_residual with an fp32 scratch of rows x cout: products
-// hipBLASLt takes (bf16 or fp32) run there (bias in its epilogue), then the
-// gate pass; the rest run the fused kernel.
-int linear_gate_residual_scratch(int dtype, const void * x, int64_t rows, int cin,
-                                 const void * weight, const float * bias, int cout,
-                                 const int32_t * coords, const float * block_mod,
-                                 const float * time_mod, int gate_offset, float * residual,
-                                 float * scratch, void * ws, size_t ws_bytes, hipStream_t s) {
-    auto a16 = [](const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (scratch && rows > 0 && cout % 4 == 0 && gate_offset % 4 == 0 && a16(residual) &&
-        a16(block_mod) && a16(time_mod)) {
-        bool done = false;
-        if (int rc = blaslt_linear(dtype, x, rows, cin, weight, bias, cout, PXS_ACT_NONE, PXS_F32,
-                                   scratch, false, ws, ws_bytes, s, &done))
-            return rc;
-        if (done) {
-            const int64_t total = rows * (cout / 4);
-            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 16384));
-            hipLaunchKernelGGL(gate_residual_kernel, dim3(blocks), dim3(256), 0, s, scratch, rows,
-                               cout, coords, block_mod, time_mod, gate_offset, residual);
-            return check_launch("gate residual");
-        }
-    }
-    return pxs_linear_gate_residual(dtype, x, rows, cin, weight, bias, cout, coords, block_mod,
-                                    time_mod, gate_offset, residual, s);
-}
-
-int linear_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
-              const float * bias, int cout, int act, void * y, void * ws, size_t ws_bytes,
-              hipStream_t s) {
+// The plain linears: the dense MFMA kernels (csrc/dense.hip) for operands of
+// whole 16-byte pieces, the gather-GEMM kernels (one offset, no row map)
+// otherwise.
+int linear_rows(int dtype, const void * x, int64_t rows, int cin, const void * weight,
+                const float * bias, int cout, int act, void * y, hipStream_t s) {
     if (int rc = check_dtype(dtype, "pxs_linear")) return rc;
     PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear: bad shape");
     PXS_CHECK(act == PXS_ACT_NONE || act == PXS_ACT_GELU_TANH || act == PXS_ACT_SILU,
@@ -1304,43 +1208,19 @@ int linear_ws(int dtype, const void * x, int64_t rows, int cin, const void * wei
     PXS_CHECK(x && weight && y, PXS_ERR_ARG, "pxs_linear: null pointer");
     // A few fp32 outputs over narrow rows (the decoder's output layer, 64 -> 7
     // over millions of rows): the reference's own operation order, one thread
-    // per row, HBM-bound, instead of 64-column MFMA tiles 7/8 empty.
+    // per row, HBM-bound, instead of MFMA tiles 7/8 empty.
     if (dtype == PXS_F32 && act == PXS_ACT_NONE && cout <= kOrderedRowOut && cin <= 256)
         return launch_ordered_rows(static_cast<const float *>(x), rows, cin,
                                    static_cast<const float *>(weight), bias, cout,
                                    static_cast<float *>(y), s);
-    {
-        bool done = false;
-        if (int rc = blaslt_linear(dtype, x, rows, cin, weight, bias, cout, act, dtype, y, false,
-                                   ws, ws_bytes, s, &done))
-            return rc;
-        if (done) return PXS_OK;
-    }
+    bool done = false;
+    if (int rc = dense_linear(dtype, x, rows, cin, weight, bias, cout, act, y, s, &done)) return rc;
+    if (done) return PXS_OK;
     GemmArgs a{};
     a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
     a.cout = cout; a.m = rows; a.rowmap = nullptr; a.ld_map = 0; a.noff = 1; a.masks = nullptr;
     a.y = y; a.ldy = cout; a.act = act;
     return run_gemm(dtype, a, kEpiStore, s);
-}
-
-int linear_residual_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
-                       const float * bias, int cout, float * residual, void * ws, size_t ws_bytes,
-                       hipStream_t s) {
-    if (int rc = check_dtype(dtype, "pxs_linear_residual")) return rc;
-    PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear_residual: bad shape");
-    if (rows == 0) return PXS_OK;
-    PXS_CHECK(x && weight && residual, PXS_ERR_ARG, "pxs_linear_residual: null pointer");
-    {
-        bool done = false;
-        if (int rc = blaslt_linear(dtype, x, rows, cin, weight, bias, cout, PXS_ACT_NONE, PXS_F32,
-                                   residual, true, ws, ws_bytes, s, &done))
-            return rc;
-        if (done) return PXS_OK;
-    }
-    GemmArgs a{};
-    a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
-    a.cout = cout; a.m = rows; a.noff = 1; a.y = nullptr; a.ldy = cout; a.residual = residual;
-    return run_gemm(dtype, a, kEpiAddResidual, s);
 }
 
 } // namespace pxs
@@ -1409,7 +1289,7 @@ int pxs_sparse_conv3d_s2(int dtype, const void * x, int64_t n_in, int cin, const
 
 int pxs_linear(int dtype, const void * x, int64_t rows, int cin, const void * weight,
                const float * bias, int cout, int act, void * y, void * stream) {
-    return linear_ws(dtype, x, rows, cin, weight, bias, cout, act, y, nullptr, 0, as_stream(stream));
+    return linear_rows(dtype, x, rows, cin, weight, bias, cout, act, y, as_stream(stream));
 }
 
 int pxs_linear_gate_residual(int dtype, const void * x, int64_t rows, int cin,
@@ -1423,6 +1303,11 @@ int pxs_linear_gate_residual(int dtype, const void * x, int64_t rows, int cin,
     if (rows == 0) return PXS_OK;
     PXS_CHECK(x && weight && coords && block_mod && time_mod && residual, PXS_ERR_ARG,
               "pxs_linear_gate_residual: null pointer");
+    bool done = false;
+    if (int rc = dense_linear_gate(dtype, x, rows, cin, weight, bias, cout, coords, block_mod,
+                                   time_mod, gate_offset, residual, as_stream(stream), &done))
+        return rc;
+    if (done) return PXS_OK;
     GemmArgs a{};
     a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
     a.cout = cout; a.m = rows; a.noff = 1; a.y = nullptr; a.ldy = cout;
@@ -1433,26 +1318,19 @@ int pxs_linear_gate_residual(int dtype, const void * x, int64_t rows, int cin,
 
 int pxs_linear_residual(int dtype, const void * x, int64_t rows, int cin, const void * weight,
                         const float * bias, int cout, float * residual, void * stream) {
-    return linear_residual_ws(dtype, x, rows, cin, weight, bias, cout, residual, nullptr, 0,
-                              as_stream(stream));
-}
-
-size_t pxs_linear_workspace_bytes(void) { return kLibWorkspaceBytes; }
-
-int pxs_linear_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
-                  const float * bias, int cout, int act, void * y, void * workspace,
-                  void * stream) {
-    PXS_CHECK_WORKSPACE(workspace, "pxs_linear_ws");
-    return linear_ws(dtype, x, rows, cin, weight, bias, cout, act, y, workspace,
-                     workspace ? kLibWorkspaceBytes : 0, as_stream(stream));
-}
-
-int pxs_linear_residual_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
-                           const float * bias, int cout, float * residual, void * workspace,
-                           void * stream) {
-    PXS_CHECK_WORKSPACE(workspace, "pxs_linear_residual_ws");
-    return linear_residual_ws(dtype, x, rows, cin, weight, bias, cout, residual, workspace,
-                              workspace ? kLibWorkspaceBytes : 0, as_stream(stream));
+    if (int rc = check_dtype(dtype, "pxs_linear_residual")) return rc;
+    PXS_CHECK(rows >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, "pxs_linear_residual: bad shape");
+    if (rows == 0) return PXS_OK;
+    PXS_CHECK(x && weight && residual, PXS_ERR_ARG, "pxs_linear_residual: null pointer");
+    bool done = false;
+    if (int rc = dense_linear_residual(dtype, x, rows, cin, weight, bias, cout, residual,
+                                       as_stream(stream), &done))
+        return rc;
+    if (done) return PXS_OK;
+    GemmArgs a{};
+    a.x = x; a.rows_in = rows; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
+    a.cout = cout; a.m = rows; a.noff = 1; a.y = nullptr; a.ldy = cout; a.residual = residual;
+    return run_gemm(dtype, a, kEpiAddResidual, as_stream(stream));
 }
 
 int pxs_downsample_mean(int dtype, const void * x, int channels, const int64_t * group_offsets,

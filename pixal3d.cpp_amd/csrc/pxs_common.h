@@ -18,32 +18,23 @@ int fail_workspace(const char * what) noexcept;
 int check_hip(hipError_t status, const char * what);
 int check_launch(const char * what);
 
-// Workspace a composition carves for the library GEMMs of its linears.
-constexpr size_t kLibWorkspaceBytes = size_t(64) << 20;
-
-// Plain linears (x and w both PXS_BF16 or both PXS_F32) through hipBLASLt
-// (csrc/blaslt.cpp), with ws (nullable, ws_bytes) as the library's workspace:
-// sets *done when it ran the product, leaves it false for shapes it does not
-// take.
-int blaslt_linear(int dtype, const void * x, int64_t rows, int cin, const void * w,
-                  const float * bias, int cout, int act, int y_dtype, void * y, bool accumulate,
-                  void * ws, size_t ws_bytes, hipStream_t s, bool * done);
-
-// pxs_linear and pxs_linear_residual with a library workspace (csrc/gemm.hip).
-int linear_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
-              const float * bias, int cout, int act, void * y, void * ws, size_t ws_bytes,
-              hipStream_t s);
-int linear_residual_ws(int dtype, const void * x, int64_t rows, int cin, const void * weight,
-                       const float * bias, int cout, float * residual, void * ws, size_t ws_bytes,
-                       hipStream_t s);
-
-// pxs_linear_gate_residual given an fp32 scratch of rows x cout and a library
-// workspace (csrc/gemm.hip).
-int linear_gate_residual_scratch(int dtype, const void * x, int64_t rows, int cin,
-                                 const void * weight, const float * bias, int cout,
-                                 const int32_t * coords, const float * block_mod,
-                                 const float * time_mod, int gate_offset, float * residual,
-                                 float * scratch, void * ws, size_t ws_bytes, hipStream_t s);
+// Dense linears on MFMA (csrc/dense.hip): x [rows, cin] and w [cout, cin],
+// both PXS_BF16 or both PXS_F32.  Each sets *done when it ran the product and
+// leaves it false for operands it does not take (rows of x or w not whole
+// 16-byte pieces, or not 16-byte aligned), which the caller then runs on the
+// gather-GEMM kernels.
+//   dense_linear:          y (dtype) = act(x w^T + bias)
+//   dense_linear_residual: residual (fp32) += x w^T + bias
+//   dense_linear_gate:     residual += (x w^T + bias) * (block_mod[o + c] + time_mod[b, o + c])
+int dense_linear(int dtype, const void * x, int64_t rows, int cin, const void * w,
+                 const float * bias, int cout, int act, void * y, hipStream_t s, bool * done);
+int dense_linear_residual(int dtype, const void * x, int64_t rows, int cin, const void * w,
+                          const float * bias, int cout, float * residual, hipStream_t s,
+                          bool * done);
+int dense_linear_gate(int dtype, const void * x, int64_t rows, int cin, const void * w,
+                      const float * bias, int cout, const int32_t * coords,
+                      const float * block_mod, const float * time_mod, int gate_offset,
+                      float * residual, hipStream_t s, bool * done);
 
 #define PXS_CHECK(expr, code, msg)            \
     do {                                      \
@@ -161,6 +152,48 @@ __device__ __forceinline__ void barrier_no_fence() {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt unbounded
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(n) with expcnt/lgkmcnt at their maxima: waits until at most
+// n of the wave's vector-memory instructions (LDS DMA included) are in flight.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+    case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+    case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+    case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
+    case 16: __builtin_amdgcn_s_waitcnt(0x4F70); break;
+    case 17: __builtin_amdgcn_s_waitcnt(0x4F71); break;
+    case 18: __builtin_amdgcn_s_waitcnt(0x4F72); break;
+    case 19: __builtin_amdgcn_s_waitcnt(0x4F73); break;
+    case 20: __builtin_amdgcn_s_waitcnt(0x4F74); break;
+    case 21: __builtin_amdgcn_s_waitcnt(0x4F75); break;
+    case 22: __builtin_amdgcn_s_waitcnt(0x4F76); break;
+    case 23: __builtin_amdgcn_s_waitcnt(0x4F77); break;
+    case 24: __builtin_amdgcn_s_waitcnt(0x4F78); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
+// contiguous range of logical tiles so neighbouring tiles (which share
+// operand rows and weights) share one L2.
+__device__ __forceinline__ int remap_xcd(int bid, int blocks) {
+    const int q = blocks / 8, rem = blocks % 8;
+    const int xcd = bid % 8, slot = bid / 8;
+    return (xcd < rem) ? xcd * (q + 1) + slot : rem * (q + 1) + (xcd - rem) * q + slot;
 }
 
 // ---- dense voxel grid cells ---------------------------------------------------

@@ -86,9 +86,6 @@ _SIGS = {
     "pxs_slat_flow_forward": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                                      _i64, _vp, _vp, _vp, _vp]),
     "pxs_linear": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp]),
-    "pxs_linear_workspace_bytes": (C.c_size_t, []),
-    "pxs_linear_ws": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
-    "pxs_linear_residual_ws": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp]),
     "pxs_linear_gate_residual": (_i32, [_i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "pxs_layer_norm": (_i32, [_i32, _vp, _i64, _i32, _f, _vp, _vp, _i32, _vp, _vp]),
     "pxs_layer_norm_modulate": (_i32, [_i32, _vp, _i64, _i32, _f, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
@@ -560,35 +557,20 @@ class Pxs:
                     "pxs_downsample_mean")
         return y[:m]
 
-    def linear_residual(self, x, weight, bias, residual, workspace=None):
-        """pxs_linear_residual; with a workspace (pxs_linear_workspace_bytes()),
-        pxs_linear_residual_ws."""
+    def linear_residual(self, x, weight, bias, residual):
+        """pxs_linear_residual: residual (fp32) += x W^T + bias."""
         rows, cin = x.shape
-        if workspace is not None:
-            self._check(self.lib.pxs_linear_residual_ws(
-                _dtype_code(x), _ptr(x), rows, cin, _ptr(weight), _ptr(bias), weight.shape[0],
-                _ptr(residual), _ptr(workspace), self.stream()), "pxs_linear_residual_ws")
-            return residual
         self._check(self.lib.pxs_linear_residual(_dtype_code(x), _ptr(x), rows, cin, _ptr(weight),
                                                  _ptr(bias), weight.shape[0], _ptr(residual),
                                                  self.stream()),
                     "pxs_linear_residual")
         return residual
 
-    def linear_workspace(self, device="cuda"):
-        """A workspace for linear(..., workspace=) and linear_residual(..., workspace=)."""
-        return self._ws(self.lib.pxs_linear_workspace_bytes(), device)
-
-    def linear(self, x, weight, bias=None, act=ACT_NONE, out=None, workspace=None):
-        """pxs_linear; with a workspace (pxs_linear_workspace_bytes()), pxs_linear_ws."""
+    def linear(self, x, weight, bias=None, act=ACT_NONE, out=None):
+        """pxs_linear: act(x W^T + bias) in x's dtype."""
         rows, cin = x.shape
         cout = weight.shape[0]
         y = torch.empty((rows, cout), dtype=x.dtype, device=x.device) if out is None else out
-        if workspace is not None:
-            self._check(self.lib.pxs_linear_ws(_dtype_code(x), _ptr(x), rows, cin, _ptr(weight),
-                                               _ptr(bias), cout, act, _ptr(y), _ptr(workspace),
-                                               self.stream()), "pxs_linear_ws")
-            return y
         self._check(self.lib.pxs_linear(_dtype_code(x), _ptr(x), rows, cin, _ptr(weight),
                                         _ptr(bias), cout, act, _ptr(y), self.stream()),
                     "pxs_linear")

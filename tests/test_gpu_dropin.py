@@ -103,6 +103,34 @@ def test_dropin_reference_block_kat(di):
     close(feats.ravel(), gold, "block KAT")
 
 
+# The binary-fraction fixtures of tests/sparse_linear_cuda_benchmark.cpp:53-57
+# (points, input and output channels, batch size, spatial extent, bias) with
+# the inputs of its fill_fixture_values (:200-216) and coordinates of its
+# make_coords (:166-186): every product and partial sum is exact, so the
+# drop-in's sparse_linear must equal the compiled reference bit for bit
+# whatever its summation order (the 4-channel case runs the dense MFMA
+# kernel, the others the gather-GEMM fallback).
+@pytest.mark.parametrize("points,cin,cout,batch,spatial,with_bias", [
+    (11, 3, 5, 2, 8, True), (13, 4, 4, 2, 8, False), (17, 5, 2, 1, 8, True)])
+def test_dropin_linear_binary_fixtures(di, points, cin, cout, batch, spatial, with_bias):
+    per = (points + batch - 1) // batch
+    p = np.arange(points)
+    local = p % per
+    coords = np.stack([p // per, local % spatial, (local % (spatial * spatial)) // spatial,
+                       local // (spatial * spatial)], 1).astype(np.int32)
+    x = (0.125 * ((np.arange(points * cin) % 13) + 1)).astype(np.float32).reshape(points, cin)
+    w = (0.0625 * ((np.arange(cout * cin) % 11) + 1)).astype(np.float32).reshape(cout, cin)
+    b = (0.25 * (np.arange(cout) + 1)).astype(np.float32) if with_bias else np.zeros(cout, np.float32)
+    want = x.astype(np.float64) @ w.astype(np.float64).T + b
+    shape = (spatial, spatial, spatial)
+    got = di.linear(di.sparse(coords, x, batch, shape), w, b).read()
+    np.testing.assert_array_equal(got[0], coords)
+    np.testing.assert_array_equal(got[1], want.astype(np.float32))
+    if O.REF_LIB.exists():  # the compiled reference, where it was built
+        ref = O.Reference()
+        np.testing.assert_array_equal(got[1], ref.linear(ref.sparse(coords, x, batch, shape), w, b).read()[1])
+
+
 def test_dropin_block_alias_safe(di):
     """Callers pass the same tensor as input and output (src/slat_flow.cpp:238-241)."""
     gold = np.array(json.loads((GOLD / "sparse_transformer_fixture.json").read_text())

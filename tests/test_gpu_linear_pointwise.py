@@ -291,101 +291,160 @@ def test_head_norm_rope_64(px, orc, dtype):
     check(host(xc), orc.mh_rms_norm(xr, H, D, g), what=f"rms in place {dtype}")
 
 
-@pytest.mark.parametrize("rows,cin,cout", [(4096, 256, 512), (300, 64, 96), (200, 64, 64),
-                                           (1000, 60, 64), (1000, 64, 64)])
-def test_linear_bf16_library_and_fallback(px, orc, rows, cin, cout):
-    """Plain bf16 linears: with at least 256 rows and widths that are
-    multiples of 8 they run through hipBLASLt (bias, GELU, SiLU epilogues, and
-    the residual add as beta = 1 into the fp32 residual); 200 rows, 60 inputs
-    and 64 -> 64 take the gather-GEMM kernel.  Against the oracle on the same
-    bf16-rounded operands, at the bf16 bar; without a bias too."""
-    import torch
-    import pxs
-    x = W.bf16_round(W.normal(95, rows * cin, 1).reshape(rows, cin))
-    w = W.bf16_round(W.normal(95, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin))
-    b = W.normal(95, cout, 3, std=0.1)
-    print(f"[linear bf16 paths] {rows}x{cin}->{cout}", flush=True)
-    lin = orc.linear(x, w, b)
-    for act, f in ((pxs.ACT_NONE, lambda v: v), (pxs.ACT_GELU_TANH, orc.gelu_tanh),
-                   (pxs.ACT_SILU, orc.silu)):
-        y = host(px.linear(tbf(x), tbf(w), t32(b), act=act))
-        assert_bf16(y, f(lin), what=f"bf16 linear act {act}")
-    y = host(px.linear(tbf(x), tbf(w), None))
-    assert_bf16(y, orc.linear(x, w, np.zeros(cout, np.float32)), what="bf16 linear, no bias")
-    res0 = W.normal(95, rows * cout, 4).reshape(rows, cout)
-    res = t32(res0)
-    px.linear_residual(tbf(x), tbf(w), t32(b), res)
-    torch.cuda.synchronize()
-    assert_bf16(host(res), res0 + lin, what="bf16 linear residual")
-
-
-
-@pytest.mark.parametrize("rows,cin,cout", [(2048, 512, 512), (1024, 768, 96), (4096, 136, 128)])
-def test_linear_fp32_library(px, orc, rows, cin, cout):
-    """fp32 linears of at least 2^26 multiply-adds run through hipBLASLt in
-    full fp32 (bias, GELU, SiLU epilogues, residual add); against the oracle
-    (sparse_linear's serial fp32 order) at the fp32 bar."""
-    import torch
-    import pxs
-    x = W.normal(96, rows * cin, 1).reshape(rows, cin)
-    w = W.normal(96, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin)
-    b = W.normal(96, cout, 3, std=0.1)
-    print(f"[linear fp32 library] {rows}x{cin}->{cout}", flush=True)
-    lin = orc.linear(x, w, b)
-    for act, f in ((pxs.ACT_NONE, lambda v: v), (pxs.ACT_GELU_TANH, orc.gelu_tanh),
-                   (pxs.ACT_SILU, orc.silu)):
-        y = host(px.linear(t32(x), t32(w), t32(b), act=act))
-        assert_fp32(y, f(lin), what=f"fp32 linear act {act}")
-    y = host(px.linear(t32(x), t32(w), None))
-    assert_fp32(y, orc.linear(x, w, np.zeros(cout, np.float32)), what="fp32 linear, no bias")
-    res0 = W.normal(96, rows * cout, 4).reshape(rows, cout)
-    res = t32(res0)
-    px.linear_residual(t32(x), t32(w), t32(b), res)
-    torch.cuda.synchronize()
-    assert_fp32(host(res), res0 + lin, what="fp32 linear residual")
-
-
-@pytest.mark.parametrize("dtype,rows,cin,cout", [("bf16", 70000, 64, 256), ("bf16", 70000, 256, 64),
-                                                 ("bf16", 30000, 256, 256), ("f32", 20000, 128, 128),
-                                                 ("f32", 20000, 64, 256)])
-def test_linear_with_workspace(px, orc, dtype, rows, cin, cout):
-    """pxs_linear_ws / pxs_linear_residual_ws: tall products over few channels
-    whose library algorithms need a workspace; against the oracle at the
-    dtype's bar, with and without GELU, and the residual form."""
+def _dense_case(px, orc, dtype, rows, cin, cout, seed):
+    """Every epilogue of the plain linears at one shape against the oracle
+    (sparse_linear's serial fp32 order) on the same (bf16-rounded) operands:
+    bias with no activation, GELU, SiLU, no bias, the fp32 residual add and
+    the adaLN gate with the residual add (two batch items)."""
     import torch
     import pxs
     conv = t32 if dtype == "f32" else tbf
-    rnd = (lambda a: a) if dtype == "f32" else W.bf16_round
+    rnd = (lambda v: v) if dtype == "f32" else W.bf16_round
     check = assert_fp32 if dtype == "f32" else assert_bf16
-    x = rnd(W.normal(97, rows * cin, 1).reshape(rows, cin))
-    w = rnd(W.normal(97, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin))
-    b = W.normal(97, cout, 3, std=0.1)
-    print(f"[linear ws] {dtype} {rows}x{cin}->{cout}", flush=True)
-    ws = px.linear_workspace()
+    x = rnd(W.normal(seed, rows * cin, 1).reshape(rows, cin))
+    w = rnd(W.normal(seed, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin))
+    b = W.normal(seed, cout, 3, std=0.1)
     lin = orc.linear(x, w, b)
-    y = host(px.linear(conv(x), conv(w), t32(b), workspace=ws))
-    check(y, lin, what="linear ws")
-    y = host(px.linear(conv(x), conv(w), t32(b), act=pxs.ACT_GELU_TANH, workspace=ws))
-    check(y, orc.gelu_tanh(lin), what="linear ws gelu")
-    res0 = W.normal(97, rows * cout, 4).reshape(rows, cout)
+    for act, f in ((pxs.ACT_NONE, lambda v: v), (pxs.ACT_GELU_TANH, orc.gelu_tanh),
+                   (pxs.ACT_SILU, orc.silu)):
+        y = host(px.linear(conv(x), conv(w), t32(b), act=act))
+        check(y, f(lin), what=f"{dtype} linear act {act}")
+    y = host(px.linear(conv(x), conv(w), None))
+    check(y, orc.linear(x, w, np.zeros(cout, np.float32)), what=f"{dtype} linear, no bias")
+    res0 = W.normal(seed, rows * cout, 4).reshape(rows, cout)
     res = t32(res0)
-    px.linear_residual(conv(x), conv(w), t32(b), res, workspace=ws)
+    px.linear_residual(conv(x), conv(w), t32(b), res)
     torch.cuda.synchronize()
-    check(host(res), res0 + lin, what="linear residual ws")
+    check(host(res), res0 + lin, what=f"{dtype} linear residual")
+    coords = np.zeros((rows, 4), np.int32)
+    coords[rows // 3:, 0] = 1
+    bmod = W.normal(seed, 6 * cout, 5)
+    tmod = W.normal(seed, 2 * 6 * cout, 6)
+    res = t32(res0)
+    px.linear_gate_residual(conv(x), conv(w), t32(b), ti32(coords), t32(bmod), t32(tmod), 2 * cout,
+                            res)
+    torch.cuda.synchronize()
+    check(host(res), res0 + orc.gate(coords, lin, bmod, tmod, 2 * cout),
+          what=f"{dtype} linear gate residual")
 
 
-def test_linear_workspace_misaligned_rejected(px):
-    """pxs_linear_ws rejects a workspace that is not 256-byte aligned, before
-    anything is enqueued, and takes NULL (no workspace) as the plain call."""
+# Shapes for every tile of the dense kernels (256 x 256, 128 x 128, 128 x 64),
+# K ragged against the 128-byte chunk (72, 136, 40), outputs not a multiple
+# of 8 or 4 (the per-element epilogue), rows past one tile, and the
+# gather-GEMM fallback (60 inputs: rows not whole 16-byte pieces).
+@pytest.mark.parametrize("rows,cin,cout", [(4096, 256, 512), (300, 64, 96), (200, 64, 64),
+                                           (1000, 60, 64), (1000, 72, 64), (257, 136, 130),
+                                           (520, 40, 1000), (3000, 1024, 1024), (70000, 64, 256),
+                                           (70000, 256, 64), (30000, 256, 256), (777, 128, 36)])
+def test_linear_dense_bf16(px, orc, rows, cin, cout):
+    print(f"[linear dense bf16] {rows}x{cin}->{cout}", flush=True)
+    _dense_case(px, orc, "bf16", rows, cin, cout, 95)
+
+
+@pytest.mark.parametrize("rows,cin,cout", [(2048, 512, 512), (1024, 768, 96), (4096, 136, 128),
+                                           (20000, 128, 128), (20000, 64, 256), (333, 36, 70),
+                                           (100, 8, 1024), (513, 1024, 12)])
+def test_linear_dense_fp32(px, orc, rows, cin, cout):
+    print(f"[linear dense fp32] {rows}x{cin}->{cout}", flush=True)
+    _dense_case(px, orc, "f32", rows, cin, cout, 96)
+
+
+def _sampled_rows(m, count=256, seed=0):
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([rng.integers(0, m, count), [0, m - 1]]))
+    return rows
+
+
+# The linears configs 3, 4 and 5 and the decoder run, at full size: inputs
+# drawn on the device, sampled output rows recomputed in float64 on the host
+# from the same bf16 operands (the gate and residual forms with fp32
+# residuals), at the bf16 bar.
+@pytest.mark.parametrize("rows,cin,cout,form", [
+    (32768, 1024, 3072, "plain"), (32768, 1024, 1024, "gate"), (40960, 1024, 4096, "gelu"),
+    (40960, 4096, 1024, "gate"), (40960, 1024, 1024, "residual"), (29700, 768, 2304, "plain"),
+    (2492211, 64, 256, "silu"), (2492211, 256, 64, "residual")])
+def test_linear_dense_config_shapes(px, rows, cin, cout, form):
+    import torch
     import pxs
-    x = tbf(np.ones((512, 64), np.float32))
-    w = tbf(np.full((256, 64), 0.5, np.float32))
-    ws = px.linear_workspace()
-    y = px.linear(x, w, None, workspace=ws)
-    with pytest.raises(pxs.PxsError, match="workspace"):
-        px._check(px.lib.pxs_linear_ws(pxs.PXS_BF16, x.data_ptr(), 512, 64, w.data_ptr(), None,
-                                       256, pxs.ACT_NONE, y.data_ptr(), ws.data_ptr() + 16,
-                                       px.stream()), "pxs_linear_ws")
-    px._check(px.lib.pxs_linear_ws(pxs.PXS_BF16, x.data_ptr(), 512, 64, w.data_ptr(), None, 256,
-                                   pxs.ACT_NONE, y.data_ptr(), None, px.stream()), "no workspace")
-    np.testing.assert_array_equal(host(y), np.full((512, 256), 32.0, np.float32))
+    print(f"[linear dense config] {rows}x{cin}->{cout} {form}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows + cin + cout)
+    x = torch.randn(rows, cin, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(cout, cin, device="cuda", generator=g) * cin ** -0.5).to(torch.bfloat16)
+    b = torch.randn(cout, device="cuda", generator=g) * 0.1
+    sel = _sampled_rows(rows, seed=rows)
+    xs = x[torch.from_numpy(sel).cuda()].double().cpu().numpy()
+    wd = w.double().cpu().numpy()
+    lin = xs @ wd.T + b.double().cpu().numpy()
+    if form in ("plain", "gelu", "silu"):
+        act = {"plain": pxs.ACT_NONE, "gelu": pxs.ACT_GELU_TANH, "silu": pxs.ACT_SILU}[form]
+        y = px.linear(x, w, b, act=act)
+        got = host(y[torch.from_numpy(sel).cuda()])
+        if form == "gelu":
+            lin = 0.5 * lin * (1.0 + np.tanh(0.7978845608028654 * (lin + 0.044715 * lin ** 3)))
+        elif form == "silu":
+            lin = lin / (1.0 + np.exp(-lin))
+        assert_bf16(got, lin, what=f"{form} {rows}x{cin}->{cout}")
+        return
+    res0 = torch.randn(rows, cout, device="cuda", generator=g)
+    res = res0.clone()
+    want = res0[torch.from_numpy(sel).cuda()].double().cpu().numpy()
+    if form == "residual":
+        px.linear_residual(x, w, b, res)
+        want = want + lin
+    else:
+        batch = torch.zeros(rows, 4, dtype=torch.int32, device="cuda")
+        batch[rows // 2:, 0] = 1
+        bmod = torch.randn(6 * cout, device="cuda", generator=g)
+        tmod = torch.randn(2 * 6 * cout, device="cuda", generator=g)
+        px.linear_gate_residual(x, w, b, batch, bmod, tmod, 2 * cout, res)
+        bsel = batch[torch.from_numpy(sel).cuda(), 0].cpu().numpy()
+        gate = (bmod[2 * cout:3 * cout].double().cpu().numpy()[None, :] +
+                tmod.double().cpu().numpy().reshape(2, 6 * cout)[bsel, 2 * cout:3 * cout])
+        want = want + lin * gate
+    got = host(res[torch.from_numpy(sel).cuda()])
+    # the residual part is exact; the bar applies to the product's share
+    assert_bf16(got - res0[torch.from_numpy(sel).cuda()].cpu().numpy(),
+                want - res0[torch.from_numpy(sel).cuda()].double().cpu().numpy(),
+                what=f"{form} {rows}x{cin}->{cout}")
+
+
+def _ref_bench_values(count, salt, scale, start=0):
+    """tests/sparse_linear_cuda_benchmark.cpp:188-199 (deterministic_value):
+    bucket = ((index * 6364136223846793005 + salt) >> 32) % 251 - 125, times
+    scale, for indices start .. start + count - 1 (uint64 arithmetic)."""
+    idx = np.arange(start, start + count, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        mixed = idx * np.uint64(6364136223846793005) + np.uint64(salt)
+    bucket = ((mixed >> np.uint64(32)) % np.uint64(251)).astype(np.int64) - 125
+    return (bucket.astype(np.float32) * np.float32(scale)).astype(np.float32)
+
+
+# The reference's hot sparse_linear shapes
+# (tests/sparse_linear_cuda_benchmark.cpp:42-52), fp32 as there, with its
+# deterministic inputs (salts and scales of :228, :709-710): sampled rows
+# against float64 at the fp32 bar; the 64 -> 7 shape takes the ordered-row
+# kernel (bit-equal order) and is checked on every row of a prefix.
+@pytest.mark.parametrize("points,cin,cout", [
+    (46537, 2048, 512), (46537, 512, 2048), (206980, 1024, 256), (206980, 256, 1024),
+    (909164, 512, 128), (909164, 128, 512), (9857, 4096, 1024), (9857, 1024, 4096),
+    (4005638, 64, 7)])
+def test_linear_reference_hot_shapes(px, points, cin, cout):
+    import torch
+    print(f"[linear reference hot shape] {points}x{cin}->{cout}", flush=True)
+    # inputs generated on the device in chunks with the same integer recipe
+    x = torch.empty(points, cin, dtype=torch.float32, device="cuda")
+    total = points * cin
+    step = 1 << 26
+    flat = x.view(-1)
+    for s0 in range(0, total, step):
+        n = min(step, total - s0)
+        flat[s0:s0 + n] = torch.from_numpy(_ref_bench_values(n, 0x13579bdf2468ace0, 0.00075, s0)).cuda()
+    w = _ref_bench_values(cout * cin, 0x0f1e2d3c4b5a6978, 0.00055).reshape(cout, cin)
+    b = _ref_bench_values(cout, 0xa5a5a5a55a5a5a5a, 0.0008)
+    y = px.linear(x, t32(w), t32(b))
+    sel = _sampled_rows(points, seed=points)
+    xs = np.stack([_ref_bench_values(cin, 0x13579bdf2468ace0, 0.00075, int(r) * cin) for r in sel])
+    ref = xs.astype(np.float64) @ w.astype(np.float64).T + b
+    got = host(y[torch.from_numpy(sel).cuda()])
+    assert_fp32(got, ref, what=f"hot shape {points}x{cin}->{cout}")
+
