@@ -57,6 +57,8 @@ def parse():
                              "linear_dense"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave configs 1 and 4 off the default line")
     return ap.parse_args()
 
 
@@ -291,7 +293,7 @@ def unet_stage(args, torch, px, W):
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic,
+                     "traffic": traffic, "traffic_source": traffic_note(dom),
                      "algorithmic_flop": 2 * macs[dom]},
     }
     return result
@@ -308,6 +310,17 @@ def measured_traffic(op):
     if not rec:
         return None
     return int(rec["read_bytes"] + rec["write_bytes"])
+
+
+def traffic_note(op):
+    """Where the traffic figure of `op` comes from (it is not measured in the
+    bench run: counters need the profiler)."""
+    path = ROOT / "profiles" / "unet_stage_128_traffic.json"
+    rec = json.loads(path.read_text()).get(op) if path.exists() else None
+    if not rec:
+        return None
+    return (f"not measured in this run: rocprofv3 --pmc of {rec['kernel']} (grid {rec['grid']}) "
+            f"at commit {rec['measured_at_commit']}, {rec['method']} ({rec['source']})")
 
 
 def attention_metric(args, torch, px, W):
@@ -425,6 +438,237 @@ def cpu_baseline_attention():
 
 
 # ---------------------------------------------------------------------------
+# CPU baselines of the other configurations: the reference's own CPU
+# primitives (compiled from its sources into oracle/_ref, OpenMP where the
+# reference parallelises) timed by the reference benchmark's method (2
+# untimed calls, median and min of 3).  Row-wise work (linears, norms) is
+# timed on LIN_CPU_ROWS sampled rows and scaled by the row count (its cost is
+# linear in rows); attention on ATTN_CPU_ROWS query rows per segment against
+# every key and scaled by the query count; window attention on a sample of
+# the windows, scaled by sum(L^2); a SubMConv3d on a slab of the voxels,
+# scaled by active pairs.  Each result says what was sampled.
+LIN_CPU_ROWS = 256
+
+
+def _reference():
+    import oracle as O
+
+    if not O.REF_LIB.exists():
+        return None, 0, {}
+    ref = O.Reference()
+    threads, limits = cpu_threads()
+    ref.set_threads(threads)
+    return ref, threads, limits
+
+
+def _line_coords(rows):
+    """rows distinct voxels of one item (valid coordinates for row-wise ops)."""
+    import numpy as np
+
+    i = np.arange(rows, dtype=np.int32)
+    return np.stack([np.zeros_like(i), i % 64, (i // 64) % 64, i // 4096], 1).astype(np.int32)
+
+
+def _cpu_rowwise(ref, rows, fn_of_tensor, cin, seed):
+    """Seconds for `rows` rows of a row-wise op, from LIN_CPU_ROWS sampled rows."""
+    import workloads as W
+
+    r = min(rows, LIN_CPU_ROWS)
+    t = ref.sparse(_line_coords(r), W.normal(seed, r * cin, 1).reshape(r, cin), 1, (64, 64, 64))
+    med, _ = cpu_timing(lambda: fn_of_tensor(t))
+    return med * rows / r
+
+
+def _cpu_linear(ref, rows, cin, cout, seed):
+    import workloads as W
+
+    w = W.normal(seed, cout * cin, 2, std=cin ** -0.5).reshape(cout, cin)
+    b = W.normal(seed, cout, 3, std=0.1)
+    return _cpu_rowwise(ref, rows, lambda t: ref.linear(t, w, b), cin, seed)
+
+
+def _cpu_attention(ref, coords, lens, heads, hd, seed, keys=None):
+    """Seconds of the reference's sparse_scaled_dot_product_attention over
+    segments of `lens` rows (batch items of `coords`), from ATTN_CPU_ROWS
+    query rows per segment; with keys=(T, ctx) the reference's
+    sparse_cross_attention against T context tokens per item instead."""
+    import numpy as np
+
+    import workloads as W
+
+    c = heads * hd
+    n = int(sum(lens))
+    starts = np.cumsum((0,) + tuple(lens[:-1]))
+    rows = np.concatenate([s + np.linspace(0, L - 1, min(ATTN_CPU_ROWS_BLOCK, L)).astype(np.int64)
+                           for s, L in zip(starts, lens)])
+    q = W.normal(seed, rows.size * c, 1).reshape(rows.size, c)
+    b = len(lens)
+    tq = ref.sparse(coords[rows], q, b, (64, 64, 64) if coords.max() < 64 else (128, 128, 128))
+    if keys is None:
+        k = W.normal(seed, n * c, 2).reshape(n, c)
+        tk = ref.sparse(coords, k, b, (64, 64, 64) if coords.max() < 64 else (128, 128, 128))
+        fn = lambda: ref.sdpa(tq, tk, tk, heads, hd, hd ** -0.5)  # noqa: E731
+    else:
+        T = keys
+        kv = ref.varlen(np.arange(b + 1, dtype=np.int64) * T, W.normal(seed, b * T * c, 3).reshape(b * T, c))
+        fn = lambda: ref.cross_attention(tq, kv, kv, heads, hd, hd ** -0.5)  # noqa: E731
+    med, _ = cpu_timing(fn)
+    return med * n / rows.size
+
+
+ATTN_CPU_ROWS_BLOCK = 32  # sampled query rows per segment for the block baselines
+
+
+def cpu_baseline_conv_fp32_64(wl, pairs):
+    """Config 1 in full: the reference's sparse_submanifold_conv3d on the
+    16k-voxel 64^3 shell, fp32, 64 -> 64."""
+    ref, threads, limits = _reference()
+    if ref is None:
+        return None
+    n = wl["coords"].shape[0]
+    t = ref.sparse(wl["coords"], wl["feats"], 1, (64, 64, 64))
+    med, best = cpu_timing(lambda: ref.subm_conv3d(t, wl["weight"], wl["bias"]))
+    return {"value": round(pairs * 64 * 64 / med / 1e9, 3), "unit": "voxel-GMAC/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"the whole call: reference sparse_submanifold_conv3d (compiled from its "
+                      f"sources, OpenMP, {threads} threads; CPU limits {limits}) on {n} voxels, "
+                      f"{pairs} pairs, fp32 64 -> 64; warmup 2, iterations 3: median {med:.4f} s, "
+                      f"min {best:.4f} s",
+            "median_s": round(med, 5), "min_s": round(best, 5)}
+
+
+def cpu_baseline_attn_block(wl, flops):
+    """Config 3's block on the host: QKV linear, per-head RMS of q and k,
+    attention, output linear, by the reference's primitives (fp32)."""
+    ref, threads, limits = _reference()
+    if ref is None:
+        return None
+    n, C, H, D = wl["x"].shape[0], 1024, wl["heads"], wl["head_dim"]
+    lens = tuple(int(v) for v in (wl["cu_seqlens"][1:] - wl["cu_seqlens"][:-1]))
+    g = wl["gamma_q"]
+    parts = {"qkv": _cpu_linear(ref, n, C, 3 * C, 81),
+             "rms": 2 * _cpu_rowwise(ref, n, lambda t: ref.mh_rms_norm(t, H, D, g), C, 82),
+             "attention": _cpu_attention(ref, wl["coords"], lens, H, D, 83),
+             "out": _cpu_linear(ref, n, C, C, 84)}
+    total = sum(parts.values())
+    return {"value": round(flops / total / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"extrapolated: reference sparse_linear, sparse_multi_head_rms_norm (on "
+                      f"{LIN_CPU_ROWS} sampled rows, scaled by rows) and "
+                      f"sparse_scaled_dot_product_attention ({ATTN_CPU_ROWS_BLOCK} query rows per "
+                      f"segment against all keys, scaled by queries), {threads} threads (CPU limits "
+                      f"{limits}), warmup 2, iterations 3 (median); the block's {n} rows take "
+                      + ", ".join(f"{k} {v:.2f} s" for k, v in parts.items()) + f" = {total:.1f} s",
+            "extrapolated_s": round(total, 3)}
+
+
+def cpu_baseline_swin_64(wl, pairs, flops):
+    """Config 4 on the host: per shift the window partition (the oracle: the
+    reference has none), QKV and output linears and the reference's
+    attention over the windows (each window a batch item); then the up-conv
+    SubMConv3d 768 -> 1536 and the channel-to-spatial subdivision."""
+    import numpy as np
+
+    import oracle as O
+    import workloads as W
+
+    ref, threads, limits = _reference()
+    if ref is None:
+        return None
+    orc = O.Oracle()
+    coords = wl["coords"]
+    n, C, H, D = coords.shape[0], 768, wl["heads"], wl["head_dim"]
+    parts = {}
+    for shift in wl["shifts"]:
+        t0 = time.perf_counter()
+        fwd, _, cu = orc.window_partition(coords, wl["shape"], wl["window"], shift)
+        t_part = time.perf_counter() - t0
+        lens = cu[1:] - cu[:-1]
+        # every 16th window (by id), as batch items of their own
+        pick = np.arange(0, lens.size, 16)
+        rows = np.concatenate([fwd[cu[i]:cu[i + 1]] for i in pick])
+        bidx = np.concatenate([np.full(lens[i], j, np.int32) for j, i in enumerate(pick)])
+        wc = coords[rows].copy()
+        wc[:, 0] = bidx
+        q = W.normal(91 + shift, rows.size * C, 1).reshape(rows.size, C)
+        t = ref.sparse(wc, q, pick.size, wl["shape"])
+        med, _ = cpu_timing(lambda: ref.sdpa(t, t, t, H, D, D ** -0.5))
+        scale = float((lens.astype(np.float64) ** 2).sum() / (lens[pick].astype(np.float64) ** 2).sum())
+        parts[f"partition_{shift}"] = t_part
+        parts[f"window_attention_{shift}"] = med * scale
+        parts[f"qkv_{shift}"] = _cpu_linear(ref, n, C, 3 * C, 92 + shift)
+        parts[f"out_{shift}"] = _cpu_linear(ref, n, C, C, 94 + shift)
+    # the up-conv on the voxels of a slab (x below a cut holding ~1/64 of the
+    # voxels), scaled by the pair count
+    cut = int(np.quantile(coords[:, 1], 1.0 / 64))
+    sub = np.ascontiguousarray(coords[coords[:, 1] < cut])
+    sub_pairs = int((orc.neighbor_map(sub) != sub.shape[0]).sum())
+    rng = np.random.default_rng(95)  # values do not change the reference's time
+    w_up = (rng.standard_normal((27, 1536, C), dtype=np.float32) * 0.02).astype(np.float32)
+    b_up = np.zeros(1536, np.float32)
+    t_up = ref.sparse(sub, W.normal(96, sub.shape[0] * C, 1).reshape(-1, C), 1, wl["shape"])
+    med, _ = cpu_timing(lambda: ref.subm_conv3d(t_up, w_up, b_up), warmup=1, iterations=3)
+    parts["up_conv"] = med * pairs / sub_pairs
+    t_c2s = ref.sparse(coords, rng.standard_normal((n, 1536), dtype=np.float32), 1, wl["shape"])
+    med, _ = cpu_timing(lambda: ref.channel_to_spatial(t_c2s, 2))
+    parts["c2s"] = med
+    total = sum(parts.values())
+    return {"value": round(flops / total / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"extrapolated: reference sparse_linear ({LIN_CPU_ROWS} sampled rows, scaled "
+                      f"by rows), sparse_scaled_dot_product_attention over every 16th window "
+                      f"(scaled by sum L^2), sparse_submanifold_conv3d 768 -> 1536 on the voxels of "
+                      f"a slab ({sub.shape[0]} voxels, {sub_pairs} of {pairs} pairs; scaled by "
+                      f"pairs), sparse_channel_to_spatial in full; window partition by the oracle "
+                      f"(no reference); {threads} threads (CPU limits {limits}), warmup 2 (1 for the "
+                      f"conv), iterations 3 (median): "
+                      + ", ".join(f"{k} {v:.2f} s" for k, v in parts.items()) + f" = {total:.1f} s",
+            "extrapolated_s": round(total, 3)}
+
+
+def cpu_baseline_flow_step(wl, flops):
+    """Config 5 on the host: one transformer block's primitives (adaLN layer
+    norms, QKV, RMS, RoPE, self-attention, output, cross-attention with its
+    context linears, MLP) by the reference, times 24 blocks, plus the input and
+    output linears."""
+    ref, threads, limits = _reference()
+    if ref is None:
+        return None
+    coords = wl["coords"]
+    n, C, H, M, T = coords.shape[0], wl["width"], wl["heads"], wl["mlp_hidden"], wl["context_tokens"]
+    D = C // H
+    import numpy as np
+
+    one = np.ones(C, np.float32)
+    zero = np.zeros(C, np.float32)
+    blk = {"layer_norms": 3 * _cpu_rowwise(ref, n, lambda t: ref.layer_norm(t, 1e-6, one, zero), C, 61),
+           "qkv": _cpu_linear(ref, n, C, 3 * C, 62),
+           "rms_rope": 2 * _cpu_rowwise(ref, n, lambda t: ref.mh_rms_norm(t, H, D, one), C, 63)
+                       + 2 * _cpu_rowwise(ref, n, lambda t: ref.rope(t, H, D), C, 64),
+           "self_attention": _cpu_attention(ref, coords, (n,), H, D, 65),
+           "out": _cpu_linear(ref, n, C, C, 66),
+           "cross_q": _cpu_linear(ref, n, C, C, 67),
+           "cross_kv": _cpu_linear(ref, T, C, 2 * C, 68),
+           "cross_attention": _cpu_attention(ref, coords, (n,), H, D, 69, keys=T),
+           "cross_out": _cpu_linear(ref, n, C, C, 70),
+           "mlp0": _cpu_linear(ref, n, C, M, 71),
+           "mlp2": _cpu_linear(ref, n, M, C, 72)}
+    per_block = sum(blk.values())
+    io = _cpu_linear(ref, n, 8, C, 73) + _cpu_linear(ref, n, C, 8, 74)
+    total = wl["blocks"] * per_block + io
+    return {"value": round(flops / total / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"extrapolated: one block's reference primitives (row-wise ops on "
+                      f"{LIN_CPU_ROWS} sampled rows scaled by rows; self- and cross-attention on "
+                      f"{ATTN_CPU_ROWS_BLOCK} query rows scaled by queries), {threads} threads (CPU "
+                      f"limits {limits}), warmup 2, iterations 3 (median); per block "
+                      + ", ".join(f"{k} {v:.2f} s" for k, v in blk.items())
+                      + f" = {per_block:.1f} s; x {wl['blocks']} blocks + input/output linears "
+                        f"{io:.2f} s = {total:.0f} s per step",
+            "extrapolated_s": round(total, 2)}
+
+
+# ---------------------------------------------------------------------------
 # The other configurations (parity cases; timed here for profiling).
 
 def timed_steps(args, torch, step, timer=None):
@@ -473,7 +717,9 @@ def conv_fp32_64(args, torch, px, W):
     macs = pairs * 64 * 64
     conv_ms = timer.mean_ms("conv")
     achieved = 2.0 * macs / (conv_ms * 1e-3) / 1e12
+    cpu = None if args.no_cpu_baseline else cpu_baseline_conv_fp32_64(wl, pairs)
     return {"metric": "SubMConv3d voxel-GMAC/s, fp32 64->64 at 64^3", "value": round(macs / dt / 1e9, 2),
+            "cpu_baseline": cpu,
             "unit": "voxel-GMAC/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "f32",
             "config": {"workload": f"conv_fp32_64: {n} voxels, {pairs} pairs, voxel grid + "
                                    "SubMConv3d with its neighbours looked up in the grid",
@@ -513,7 +759,9 @@ def attn_block(args, torch, px, W):
     a_ms = timer.mean_ms("attention")
     achieved = f_attn / (a_ms * 1e-3) / 1e12
     per_op = {k: round(timer.mean_ms(k), 4) for k in ("qkv", "prepare", "attention", "out")}
+    cpu = None if args.no_cpu_baseline else cpu_baseline_attn_block(wl, flops)
     return {"metric": "sparse full-attention block TFLOP/s, bf16", "value": round(flops / dt / 1e12, 2),
+            "cpu_baseline": cpu,
             "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "bf16",
             "config": {"workload": "attn_block: 12,288 + 20,480 tokens, width 1024, 16 x 64",
                        "per_op_ms": per_op, "flop_per_step": flops},
@@ -583,8 +831,10 @@ def swin_64(args, torch, px, W):
     win_ms = timer.mean_ms("window_attention")
     win_bytes = n * (3 * C * 2 + C * 2 + 4)
     win_gbs = win_bytes / (win_ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline_swin_64(wl, pairs, flops)
     return {"metric": "shifted-window attention + C2S upsample TFLOP/s, bf16",
             "value": round(flops / dt / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4),
+            "cpu_baseline": cpu,
             "dtype": "bf16",
             "config": {"workload": f"swin_64: {n} voxels, window 8 shift 0/4, 12 x 64, "
                                    f"up-conv 768->1536 ({pairs} pairs) + C2S to 128^3",
@@ -660,7 +910,9 @@ def flow_step(args, torch, px, W):
     dt = timed_steps(args, torch, step)
     flops = m["flops"]
     assert torch.isfinite(out).all().item()
+    cpu = None if args.no_cpu_baseline else cpu_baseline_flow_step(W.flow_step_64(), flops)
     return {"metric": "SLat-flow step TFLOP/s, bf16", "value": round(flops / dt / 1e12, 2),
+            "cpu_baseline": cpu,
             "unit": "TFLOP/s", "ms_per_step": round(dt * 1e3, 4), "dtype": "bf16",
             "config": {"workload": f"flow_step: {n} voxels at 64^3, 24 blocks width 1024 "
                                    f"(16 x 64, MLP 4096), 1,370 context tokens",
@@ -1046,6 +1298,13 @@ def main():
         base["cpu_baseline"] = cpu_baseline_conv()
         if "attention" in base:
             base["attention"]["cpu_baseline"] = cpu_baseline_attention()
+    if args.workload == "unet_stage_128" and not args.no_configs:
+        # Configs 1 and 4 ride on the default line (with their CPU baselines),
+        # each at up to 100 timed steps after 20 warm-up steps.
+        sub = argparse.Namespace(**vars(args))
+        sub.steps, sub.warmup = min(args.steps, 100), min(args.warmup, 20)
+        for key, fn in (("config1_conv_fp32_64", conv_fp32_64), ("config4_swin_64", swin_64)):
+            base[key] = fn(sub, torch, px, W)
     print(json.dumps(base), flush=True)
 
 

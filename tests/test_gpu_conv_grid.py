@@ -159,3 +159,32 @@ def test_conv_bf16_square_tiles(px):
     assert_bf16(host(y_map)[rows], ref, what="bf16 conv 256x256 tiles")
     y_grid = px.subm_conv3d_grid(xd, wd, bd, c, 2, (48, 48, 48), grid, 0)
     np.testing.assert_array_equal(_bits(y_grid), _bits(y_map))
+
+
+def test_unet_conv_c_grid_from_topology(px):
+    """The U-Net step's conv C exactly as the bench calls it: the 64^3 grid
+    that pxs_map_s2_topology_tagged writes (no map), SubMConv3d 256 -> 256 in
+    bf16 on 128 x 256 tiles over the coarse rows; bit-equal to the same
+    convolution over the neighbour map of that grid, and the coarse grid
+    bit-equal to one built from the coarse coordinates."""
+    import torch
+    wl = W.unet_stage_128()
+    c = ti32(wl["coords"])
+    shape = (128, 128, 128)
+    tg = px.tagged_grid(2, shape)
+    ws = px.s2_tagged_workspace(2, shape)
+    cg = torch.empty(px.lib.pxs_voxel_grid_bytes(2, 64, 64, 64) // 4, dtype=torch.int32,
+                     device=c.device)
+    _, _, oc, child, m = px.map_s2_tagged(c, 2, shape, tg, 1, cg, ws, with_map=False)
+    oc = oc[:m].contiguous()
+    print(f"[conv C over the topology's grid] m={m} 256->256 bf16", flush=True)
+    built = px.grid_build(oc, 2, (64, 64, 64))
+    np.testing.assert_array_equal(cg.cpu().numpy(), built.cpu().numpy()[:cg.numel()])
+    rng = np.random.default_rng(m)
+    x = tbf(rng.standard_normal((m, 256)).astype(np.float32))
+    w = tbf((rng.standard_normal((27, 256, 256)) * (2.0 / (27 * 256)) ** 0.5).astype(np.float32))
+    b = t32(rng.standard_normal(256).astype(np.float32) * 0.1)
+    y_grid = px.subm_conv3d_grid(x, w, b, oc, 2, (64, 64, 64), cg, 0)
+    nbr, masks = px.neighbor_map_grid(oc, 2, (64, 64, 64), grid=cg)
+    y_map = px.subm_conv3d(x, w, b, nbr.contiguous(), masks)
+    np.testing.assert_array_equal(_bits(y_grid), _bits(y_map))
