@@ -366,3 +366,101 @@ def test_decoder_stack_closed_form(px, orc, dtype):
     oc2, oy = oracle_decoder(orc, case, pxs.PXS_F32, lambda level, h, w: guides[level])
     np.testing.assert_array_equal(oc2, rc)
     assert_fp32(oy, ry, what="chained oracle blocks vs closed form")
+
+
+def _bench_scale_decoder(dtype):
+    """The decoder stack at the reference's decode scale (the decoder bench
+    workload): ~10.6k latent voxels at 64^3, levels of 1024, 512, 256, 128, 64
+    channels, one ConvNeXt block each, predicted subdivisions; random weights
+    drawn on the device (conv and MLP operands in the call's dtype)."""
+    wl = W.decoder_64()
+    dev = torch.device("cuda")
+    coords = torch.from_numpy(wl["coords"]).to(dev)
+    chans, nblk = wl["model_channels"], wl["num_blocks"]
+    wdt = torch.bfloat16 if dtype == pxs.PXS_BF16 else torch.float32
+    g = torch.Generator(device=dev).manual_seed(17)
+
+    def rnd(*s, std=0.02, dt=torch.float32):
+        return (torch.randn(*s, generator=g, device=dev) * std).to(dt)
+
+    keep, blocks = [], []
+    for level, C in enumerate(chans):
+        for _ in range(nblk[level]):
+            w = {"norm_weight": 1.0 + rnd(C), "norm_bias": rnd(C),
+                 "conv1_weight": rnd(27, C, C, std=(27 * C) ** -0.5, dt=wdt), "conv1_bias": rnd(C),
+                 "mlp0_weight": rnd(4 * C, C, std=C ** -0.5, dt=wdt), "mlp0_bias": rnd(4 * C),
+                 "mlp2_weight": rnd(C, 4 * C, std=(4 * C) ** -0.5, dt=wdt), "mlp2_bias": rnd(C)}
+            keep.append(w)
+            blocks.append(pxs.DecoderBlock(pxs.PXS_DECODER_CONVNEXT, C, C, 4 * C,
+                                           pxs.decoder_block_weights(w)))
+        if level + 1 < len(chans):
+            O_ = chans[level + 1]
+            w = {"norm1_weight": torch.ones(C, device=dev), "norm1_bias": rnd(C),
+                 "conv1_weight": rnd(27, 8 * O_, C, std=(27 * C) ** -0.5, dt=wdt),
+                 "conv1_bias": rnd(8 * O_),
+                 "conv2_weight": rnd(27, O_, O_, std=(27 * O_) ** -0.5, dt=wdt), "conv2_bias": rnd(O_),
+                 "to_subdiv_weight": rnd(8, C, std=C ** -0.5), "to_subdiv_bias": rnd(8, std=0.0)}
+            keep.append(w)
+            blocks.append(pxs.DecoderBlock(pxs.PXS_DECODER_C2S, C, O_, 0, pxs.decoder_block_weights(w)))
+    cfg = pxs.decoder_config(wl["latent_channels"], wl["out_channels"], 1e-6, True, chans, nblk)
+    head = (rnd(chans[0], wl["latent_channels"], std=0.2), rnd(chans[0]),
+            rnd(wl["out_channels"], chans[-1], std=0.1), rnd(wl["out_channels"]))
+    x = torch.randn(coords.shape[0], wl["latent_channels"], generator=g, device=dev)
+    return wl, cfg, blocks, keep, head, coords, x
+
+
+@pytest.mark.parametrize("dtype", [pxs.PXS_BF16])
+def test_decoder_stack_production_scale(px, orc, dtype):
+    """The 5-level stack at the reference's decode scale (troubleshooting
+    history of 9,857 -> 4,005,638 rows; here 10,624 -> ~2.5M), predicted
+    subdivisions: every level's coordinates and row count bit-exact against the
+    oracle's channel-to-spatial chain driven by the device's logits; the last
+    level's ConvNeXt block, final layer norm and output linear on 300 sampled
+    rows against float64, from the device's level-4 hidden state (the same
+    stack stopped there); and a second decode bit-equal to the first."""
+    wl, cfg, blocks, keep, (fl_w, fl_b, out_w, out_b), coords, x = _bench_scale_decoder(dtype)
+    max_rows = 8_000_000
+    oc, y, level_rows, preds = px.slat_decoder_forward(dtype, cfg, fl_w, fl_b, out_w, out_b, blocks,
+                                                      coords, x, predict=True, max_rows=max_rows)
+    torch.cuda.synchronize()
+    print(f"[decoder production scale] level rows {level_rows}", flush=True)
+    assert level_rows[-1] > 1_000_000 and torch.isfinite(y).all().item()
+    # coordinates: the oracle's channel-to-spatial chain with the device's logits
+    c = wl["coords"]
+    for level, logits in enumerate(preds):
+        lg = host(logits)
+        c, _ = orc.channel_to_spatial(c, np.zeros((c.shape[0], 8), np.float32), 2, lg)
+        assert c.shape[0] == level_rows[level + 1], f"level {level + 1} rows"
+    np.testing.assert_array_equal(host(oc).astype(np.int32), c)
+    # the last level from the device's level-4 hidden state
+    oc4, h4, _, _ = px.slat_decoder_forward(dtype, cfg, fl_w, fl_b, out_w, out_b, blocks, coords, x,
+                                            upsample_times=4, max_rows=max_rows)
+    np.testing.assert_array_equal(host(oc4), host(oc))
+    n4, C = h4.shape
+    nbr, _ = px.neighbor_map(oc4.contiguous())
+    sel = np.unique(np.linspace(0, n4 - 1, 300).astype(np.int64))
+    idx = nbr[:, torch.from_numpy(sel).cuda()].cpu().numpy()
+    hh = host(h4)
+    rnd = W.bf16_round if dtype == pxs.PXS_BF16 else (lambda a: a)
+    w = {k: v.float().cpu().numpy().astype(np.float64) for k, v in keep[-1].items()}
+    xin = rnd(hh).astype(np.float64)
+    conv = np.tile(w["conv1_bias"], (sel.size, 1))
+    for k in range(27):
+        ok = idx[k] != n4
+        conv[ok] += xin[idx[k][ok]] @ w["conv1_weight"][k].T
+
+    def ln(v, eps, gamma=None, beta=None):
+        mu = v.mean(1, keepdims=True)
+        var = ((v - mu) ** 2).mean(1, keepdims=True)
+        out = (v - mu) / np.sqrt(var + eps)
+        return out if gamma is None else out * gamma + beta
+
+    hid = ln(conv, 1e-6, w["norm_weight"], w["norm_bias"]) @ w["mlp0_weight"].T + w["mlp0_bias"]
+    hid = hid / (1.0 + np.exp(-hid))
+    blk = hh[sel].astype(np.float64) + hid @ w["mlp2_weight"].T + w["mlp2_bias"]
+    ref = ln(blk, 1e-5) @ host(out_w).astype(np.float64).T + host(out_b).astype(np.float64)
+    assert_bf16(host(y)[sel], ref, what="decoder last level, sampled rows")
+    oc2, y2, _, _ = px.slat_decoder_forward(dtype, cfg, fl_w, fl_b, out_w, out_b, blocks, coords, x,
+                                            predict=True, max_rows=max_rows)
+    np.testing.assert_array_equal(host(oc2), host(oc))
+    np.testing.assert_array_equal(host(y2), host(y))
