@@ -714,6 +714,270 @@ gather_gemm_lds_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Neighbourhood-staged SubMConv3d over a voxel grid (bf16).  A tile of
+// kHaloBM consecutive output rows reads its 27 x kHaloBM neighbour sources
+// from only H distinct input rows (474 on average for 128 rows of the U-Net
+// shells, against 3,456 gathered row chunks).  The tile deduplicates its
+// sources in an LDS hash table, stages the H rows' 64-channel chunk in LDS
+// once per chunk, and then streams only the weights W_k (a 4-stage ring) for
+// the present offsets k: the MFMA operand of output row p at offset k is the
+// staged row slot[k][p] (a zero row for absent neighbours).  A tile whose
+// halo exceeds kHaloMax rows reads its gathered operands from global memory
+// instead.  MFMA operands are swapped (W fragment as A, X fragment as B), so
+// a lane holds 4 consecutive output channels of one row.
+#ifndef PXS_GEMM_HALO
+#define PXS_GEMM_HALO 0
+#endif
+constexpr int kHaloBM = 128, kHaloBN = 128, kHaloMax = 576, kHaloNW = 8, kHaloWStages = 4;
+// Distinct sources are found with a byte map over the tile's source range
+// [lo, hi] (at most kHaloRange rows; wider tiles read their operands from
+// global memory) and ranked by a prefix sum, so halo slots follow the input
+// row order: the 16 tile rows one LDS cycle serves at an offset read mostly
+// consecutive slots, on distinct banks.
+constexpr int kHaloRange = 8192;
+static_assert(kHaloRange * 2 <= kHaloMax * 128, "byte map and word prefix in the halo area");
+constexpr int kHaloLds = (kHaloMax + 1) * 128 + kHaloWStages * kHaloBN * 128 + 27 * kHaloBM * 4 +
+                         kHaloMax * 4;
+
+__global__ void __launch_bounds__(kHaloNW * 64)
+halo_conv_bf16_kernel(GemmArgs a) {
+    constexpr int BM = kHaloBM, BN = kHaloBN, HMAX = kHaloMax;
+    constexpr int WAVES_N = 4;           // 2 x 4 waves of 64 rows x 32 channels
+    constexpr int TI = 2;                // 32-row blocks per wave
+    constexpr int WI = BN / (8 * kHaloNW);  // weight DMA instructions per wave per stage (2)
+    extern __shared__ __align__(16) char smem[];
+    char * halo = smem;                                           // (HMAX + 1) rows x 128 B
+    char * wring = halo + (HMAX + 1) * 128;                       // 4 x BN rows x 128 B
+    int32_t * tab = reinterpret_cast<int32_t *>(wring + kHaloWStages * BN * 128);  // [27][BM]
+    int32_t * rows = tab + 27 * BM;                               // [HMAX] halo rows
+    uint8_t * marks = reinterpret_cast<uint8_t *>(halo);                    // prologue only:
+    int32_t * wpre = reinterpret_cast<int32_t *>(halo + kHaloRange);        // byte map, word prefix
+    __shared__ uint32_t tile_mask;
+    __shared__ int lo_s, hi_s, wsum[kHaloNW];
+    __shared__ int koff[27];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int h = lane >> 5, r = lane & 31;
+    const int tiles_n = a.cout / BN;
+    const int logical = remap_xcd(blockIdx.x, gridDim.x);
+    const int64_t p0 = static_cast<int64_t>(logical / tiles_n) * BM;
+    const int n0 = (logical % tiles_n) * BN;
+    const uint16_t * __restrict__ x = static_cast<const uint16_t *>(a.x);
+    constexpr int NT = kHaloNW * 64;
+
+    if (tid == 0) { tile_mask = 0; lo_s = INT_MAX; hi_s = -1; }
+    if (tid < 8) *reinterpret_cast<uint4 *>(halo + HMAX * 128 + tid * 16) = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    grid_tile_sources<BM>(a, p0, tid, NT, tab, &tile_mask);
+    __syncthreads();
+    {
+        int lo = INT_MAX, hi = -1;
+        for (int e = tid; e < 27 * BM; e += NT) {
+            const int32_t src = tab[e];
+            if (src >= 0) { lo = min(lo, src); hi = max(hi, src); }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            lo = min(lo, __shfl_xor(lo, o));
+            hi = max(hi, __shfl_xor(hi, o));
+        }
+        if (lane == 0) { atomicMin(&lo_s, lo); atomicMax(&hi_s, hi); }
+    }
+    __syncthreads();
+    const int lo = __builtin_amdgcn_readfirstlane(lo_s);
+    const int range = __builtin_amdgcn_readfirstlane(hi_s) - lo + 1;  // >= 1: the centre is present
+    int H = HMAX + 1;  // no staging unless the range fits and the halo is small enough
+    if (range <= kHaloRange) {
+        const int words = (range + 3) >> 2;
+        uint32_t * mw = reinterpret_cast<uint32_t *>(marks);
+        for (int i = tid; i < words; i += NT) mw[i] = 0;
+        __syncthreads();
+        for (int e = tid; e < 27 * BM; e += NT) {
+            const int32_t src = tab[e];
+            if (src >= 0) marks[src - lo] = 1;  // equal values: the race is harmless
+        }
+        __syncthreads();
+        // Exclusive prefix of the set bytes per 4-byte word: 4 words a thread.
+        constexpr int WPT = kHaloRange / 4 / NT;
+        int cnt[WPT], run = 0;
+#pragma unroll
+        for (int q = 0; q < WPT; ++q) {
+            const int w = tid * WPT + q;
+            cnt[q] = w < words ? static_cast<int>((mw[w] * 0x01010101u) >> 24) : 0;
+            run += cnt[q];
+        }
+        int incl = run;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (lane >= o) incl += v;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int base = incl - run;
+        for (int wv = 0; wv < wave; ++wv) base += wsum[wv];
+#pragma unroll
+        for (int q = 0; q < WPT; ++q) {
+            const int w = tid * WPT + q;
+            if (w < words) wpre[w] = base;
+            base += cnt[q];
+        }
+        int total = 0;
+        for (int wv = 0; wv < kHaloNW; ++wv) total += wsum[wv];
+        H = __builtin_amdgcn_readfirstlane(total);
+        __syncthreads();
+        if (H <= HMAX) {
+            // slots of the sources, and the halo's row list in input order
+            for (int e = tid; e < 27 * BM; e += NT) {
+                const int32_t src = tab[e];
+                int32_t slot = HMAX;  // the zero row
+                if (src >= 0) {
+                    const int d = src - lo, w = d >> 2;
+                    const uint32_t below = mw[w] & ((1u << (8 * (d & 3))) - 1u);
+                    slot = wpre[w] + static_cast<int>((below * 0x01010101u) >> 24);
+                }
+                tab[e] = slot;
+            }
+            for (int w = tid; w < words; w += NT) {
+                uint32_t v = mw[w];
+                int slot = wpre[w];
+                for (int b = 0; b < 4; ++b)
+                    if ((v >> (8 * b)) & 1u) rows[slot++] = lo + 4 * w + b;
+            }
+        }
+    }
+    const bool staged = H <= HMAX;
+    if (tid == 0) {
+        uint32_t m = tile_mask;
+        int i = 0;
+        while (m) { koff[i++] = __ffs(m) - 1; m &= m - 1; }
+    }
+    __syncthreads();  // the byte map is dead: the halo rows may overwrite it
+    const int kcount = __builtin_amdgcn_readfirstlane(__popc(tile_mask));
+    const int chunks = a.cin / 64;
+    const int stages = kcount * chunks;
+    const int lrow = lane >> 3, lslot = lane & 7;
+
+    // Weight stage s = (chunk c, offset koff[i]): rows n0 .. n0 + BN - 1 of W_k,
+    // bytes 128 c .. of each, into ring slot s % 4.
+    const char * wbase = static_cast<const char *>(a.w) + static_cast<int64_t>(n0) * a.cin * 2;
+    uint32_t w_off[WI];
+#pragma unroll
+    for (int j = 0; j < WI; ++j) {
+        const int row = (wave * WI + j) * 8 + lrow;
+        w_off[j] = static_cast<uint32_t>(row * a.cin * 2 + ((lslot ^ swz(row)) << 4));
+    }
+    // (chunk, present offset) of the next weight stage to issue
+    int wc = 0, wi = 0;
+    auto issue_w = [&](int st) __attribute__((always_inline)) {
+        const int k = __builtin_amdgcn_readfirstlane(koff[wi]);
+        const char * sb = wbase + (static_cast<int64_t>(k) * a.cout * a.cin + wc * 64) * 2;
+        if (++wi == kcount) { wi = 0; ++wc; }
+        char * dst = wring + (st % kHaloWStages) * BN * 128;
+#pragma unroll
+        for (int j = 0; j < WI; ++j)
+            lds_dma16_sbase(sb, w_off[j], lds_offset(dst + (wave * WI + j) * 8 * 128));
+    };
+    // The halo's 64-channel chunk c: slot i holds row rows[i] (i < H).
+    auto issue_halo = [&](int c) __attribute__((always_inline)) {
+        for (int j = wave; j * 8 < H; j += kHaloNW) {
+            const int slot = j * 8 + lrow;
+            const void * g = g_zero_chunk;
+            if (slot < H)
+                g = x + static_cast<int64_t>(rows[slot]) * a.ldx + c * 64 + (lslot ^ swz(slot)) * 8;
+            lds_dma16(g, lds_offset(halo + j * 8 * 128));
+        }
+    };
+
+    f32x16 acc[TI];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+
+    if (staged && stages > 0) issue_halo(0);
+#pragma unroll
+    for (int q = 0; q < kHaloWStages - 1; ++q)
+        if (q < stages) issue_w(q);
+    wait_vmcnt(0);
+    barrier_no_fence();
+    int c = 0, i_k = 0;  // stage s = (chunk c, present offset i_k), walked without divisions
+    for (int s = 0; s < stages; ++s) {
+        const int k = __builtin_amdgcn_readfirstlane(koff[i_k]);
+        if (s > 0) {
+            if (i_k == 0) wait_vmcnt(0);  // a new chunk: its halo was issued last
+            else wait_vmcnt(min(kHaloWStages - 2, stages - 1 - s) * WI);
+            barrier_no_fence();
+        }
+        if (s + kHaloWStages - 1 < stages) issue_w(s + kHaloWStages - 1);
+        const char * wl = wring + (s % kHaloWStages) * BN * 128;
+        int32_t src[TI];
+#pragma unroll
+        for (int i = 0; i < TI; ++i) src[i] = tab[k * BM + wm * 64 + i * 32 + r];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int piece = 4 * h + u;
+            const int wrow = wn * 32 + r;
+            const bf16x8 wf = *reinterpret_cast<const bf16x8 *>(wl + wrow * 128 + ((piece ^ swz(wrow)) << 4));
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                uint4 xv;
+                if (staged) {
+                    xv = *reinterpret_cast<const uint4 *>(halo + src[i] * 128 + ((piece ^ swz(src[i])) << 4));
+                } else {
+                    xv = src[i] >= 0 ? *reinterpret_cast<const uint4 *>(
+                                           x + static_cast<int64_t>(src[i]) * a.ldx + c * 64 + piece * 8)
+                                     : make_uint4(0, 0, 0, 0);
+                }
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, __builtin_bit_cast(bf16x8, xv), acc[i], 0, 0, 0);
+            }
+        }
+        if (++i_k == kcount) {
+            i_k = 0;
+            ++c;
+            if (staged && s + 1 < stages) {
+                barrier_no_fence();  // every wave is done with this chunk's halo
+                issue_halo(c);
+            }
+        }
+    }
+    // Lane (h, r) holds row wm*64 + 32 i + r, channels wn*32 + 8 g + 4 h + e.
+    uint16_t * y = static_cast<uint16_t *>(a.y);
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const int64_t row = p0 + wm * 64 + i * 32 + r;
+        if (row >= a.m) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int ch = n0 + wn * 32 + 8 * g + 4 * h;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[i][4 * g + e] + (a.bias ? a.bias[ch + e] : 0.0f);
+            uint2 u;
+            u.x = pack_bf16x2(v[0], v[1]);
+            u.y = pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<uint2 *>(y + row * a.ldy + ch) = u;
+        }
+    }
+}
+
+int launch_halo_conv(const GemmArgs & args, hipStream_t stream) {
+    static bool configured = false;
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&halo_conv_bf16_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kHaloLds);
+        if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(halo_conv)");
+        configured = true;
+    }
+    const int64_t blocks = ((args.m + kHaloBM - 1) / kHaloBM) * (args.cout / kHaloBN);
+    if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "halo conv grid too large");
+    hipLaunchKernelGGL(halo_conv_bf16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kHaloNW * 64),
+                       kHaloLds, stream, args);
+    return check_launch("SubMConv3d (staged neighbourhood)");
+}
+
+// ---------------------------------------------------------------------------
 // fp32 split-K gather GEMM (SubMConv3d and linears in fp32).  A workgroup
 // owns 32*TI output rows x 64 output channels; its (offset, 32-channel chunk)
 // steps are dealt round-robin to the 4 waves, so even a few hundred tiles
@@ -1038,6 +1302,11 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
         return launch_split_f32<kEpiGateResidual>(args, stream);
     }
     if (dtype == PXS_BF16) {
+        if (PXS_GEMM_HALO && epi == kEpiStore && args.grid && args.noff == 27 && args.vec_ok &&
+            args.cin % 64 == 0 && args.cout % kHaloBN == 0 && args.ldx == args.cin &&
+            args.ldy == args.cout && args.m > 0 && (!args.bias || aligned16(args.bias)) &&
+            aligned16(args.y))
+            return launch_halo_conv(args, stream);
         if (epi == kEpiStore) return dispatch<uint16_t, kEpiStore>(args, stream);
         if (epi == kEpiAddResidual) return dispatch<uint16_t, kEpiAddResidual>(args, stream);
         return dispatch<uint16_t, kEpiGateResidual>(args, stream);
