@@ -390,6 +390,26 @@ __device__ __forceinline__ float lane_pair_sum(float v) {
 // cores and the VALU work at the same time.  K/V tiles stream HBM -> LDS with
 // global_load_lds through a ring of 4 stages (tiles j-1 .. j+2 live).
 constexpr int kAttnStages = 4;
+// PXS_ATTN_W3=1 builds the three-waves-per-SIMD form: K and V in rings of
+// their own, 2 K stages (tile j+1 read while j+2 lands in the slot tile j
+// left) and 4 V stages (tiles j-1 .. j+2), 48 KB of tiles instead of 64, so
+// three workgroups fit a CU, and the register budget capped at 168 VGPRs.
+#ifndef PXS_ATTN_W3
+#define PXS_ATTN_W3 0
+#endif
+constexpr bool kAttnW3 = PXS_ATTN_W3 != 0;
+// PXS_ATTN_OACC_AGPR=1 keeps the O accumulators in AGPRs: the PV products are
+// issued as inline-asm MFMAs whose C/D operands are accumulation registers,
+// so their 32 accumulator reads and writes per MFMA stay off the VGPR file
+// the softmax works in.  Inline asm hides the MFMA from the compiler's hazard
+// checks, so the asm carries its own wait states: 2 before each MFMA (VALU or
+// accvgpr write of an operand, then an MFMA read of it) and 24 before the
+// accumulators are read back (an MFMA result read by a VALU).
+#ifndef PXS_ATTN_OACC_AGPR
+#define PXS_ATTN_OACC_AGPR 0
+#endif
+constexpr int kAttnWavesPerEu = kAttnW3 ? 3 : 2;
+constexpr int kAttnTileSlots = kAttnW3 ? 6 : 2 * kAttnStages;  // 8 KB K or V tile slots
 // Raise the wave's issue priority while it queues a tile's MFMAs, so the
 // SIMD's other wave fills the matrix core's shadow with its VALU softmax.
 // Instruction interleave of one steady-state step (PV of the previous tile,
@@ -438,11 +458,16 @@ constexpr int kKeyRowsLds = 1024;  // longest permuted segment whose key rows ar
 #endif
 
 template <int NW>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(kAttnWavesPerEu)))
 flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     constexpr int kTileBytes = kKeys * 128;           // one 64-key x 64-dim bf16 tile
     constexpr int kInstr = 2 * (kKeys / 8) / NW;      // K + V wave instructions per tile
-    __shared__ __align__(16) char lds[kAttnStages][2 * kTileBytes];
+    __shared__ __align__(16) char lds[kAttnTileSlots * kTileBytes];
+    // Byte offsets of tile t's K and V slots.
+    auto k_slot = [](int t) { return kAttnW3 ? (t & 1) * kTileBytes : (t % kAttnStages) * 2 * kTileBytes; };
+    auto v_slot = [](int t) {
+        return kAttnW3 ? (2 + (t & 3)) * kTileBytes : (t % kAttnStages) * 2 * kTileBytes + kTileBytes;
+    };
     __shared__ int32_t key_rows[kKeyRowsLds];  // row_map of the segment's keys
 
     const int tid = threadIdx.x;
@@ -488,10 +513,11 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         for (int64_t i = tid; i < klen_all; i += NW * 64) key_rows[i] = a.row_map[k_begin + i];
         __syncthreads();
     }
-    const uint32_t lds_base = lds_offset(&lds[0][0]);
+    const uint32_t lds_base = lds_offset(&lds[0]);
     // The zero source of masked rows, kept in registers across the loop.
     uint64_t zero_addr = reinterpret_cast<uint64_t>(&g_attn_zero[0]);
     asm volatile("" : "+s"(zero_addr));
+#if !PXS_ATTN_SADDR
     // Per-lane source pointers of this wave's kInstr load units for tile 0;
     // a full tile of unpermuted keys advances them by 64 rows.
     const uint16_t * src0[kInstr];
@@ -506,7 +532,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         src0[j] = (is_v ? vp : kp) + (k_begin + row) * ld + head * 64 + piece * 8;
         src_step[j] = kKeys * ld;
     }
-#if PXS_ATTN_SADDR
+#else
     // Full unpermuted tiles: the K and V tile bases (wave-uniform, scalar
     // registers) advance by 64 rows per tile; each lane's byte offset within
     // a tile (row * ld + piece) stays fixed, so a tile's loads need no vector
@@ -527,7 +553,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     const bool saddr_ok = a.ldk < (int64_t(1) << 24) && a.ldv < (int64_t(1) << 24);
 #endif
     auto issue = [&](int tile) __attribute__((always_inline)) {
-        const uint32_t base = lds_base + (tile % kAttnStages) * (2 * kTileBytes);
+        const uint32_t kbase_lds = lds_base + k_slot(tile), vbase_lds = lds_base + v_slot(tile);
         const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeys;
         if (a.row_map == nullptr && kt0 + kKeys <= k_end) {
 #if PXS_ATTN_SADDR
@@ -540,19 +566,21 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
                     const bool is_v = unit >= kKeys / 8;
                     const int row0 = (unit % (kKeys / 8)) * 8;
                     lds_dma16_sbase(is_v ? vt_base : kt_base, voff[j],
-                                    base + (is_v ? kTileBytes : 0) + row0 * 128);
+                                    (is_v ? vbase_lds : kbase_lds) + row0 * 128);
                 }
                 return;
             }
-#endif
+            // Row strides of 2^24 elements or more: the per-row loads below.
+#else
 #pragma unroll
             for (int j = 0; j < kInstr; ++j) {
                 const int unit = wave * kInstr + j;
                 const bool is_v = unit >= kKeys / 8;
                 const int row0 = (unit % (kKeys / 8)) * 8;
-                lds_dma16(src0[j] + tile * src_step[j], base + (is_v ? kTileBytes : 0) + row0 * 128);
+                lds_dma16(src0[j] + tile * src_step[j], (is_v ? vbase_lds : kbase_lds) + row0 * 128);
             }
             return;
+#endif
         }
 #pragma unroll
         for (int j = 0; j < kInstr; ++j) {
@@ -569,13 +597,13 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
                 g = is_v ? static_cast<const void *>(vp + prow * a.ldv + head * 64 + piece * 8)
                          : static_cast<const void *>(kp + prow * a.ldk + head * 64 + piece * 8);
             }
-            lds_dma16(g, base + (is_v ? kTileBytes : 0) + row0 * 128);
+            lds_dma16(g, (is_v ? vbase_lds : kbase_lds) + row0 * 128);
         }
     };
 
     // S^T (keys x queries) for one tile: 2 sub-tiles of 32 keys, 4 K-steps each.
     auto qk = [&](int tile, f32x16 (&s)[2]) {
-        const char * kl = lds[tile % kAttnStages];
+        const char * kl = lds + k_slot(tile);
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const int row = kt * 32 + r;
@@ -604,10 +632,17 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
+    // Orders VALU reads of the accumulators after the last PV MFMA's result
+    // (a no-op unless they live in AGPRs).
+    auto oacc_ready = [&]() __attribute__((always_inline)) {
+#if PXS_ATTN_OACC_AGPR
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(oacc[0]), "+a"(oacc[1]));
+#endif
+    };
 
     // O^T += V^T P^T for one tile (P^T fragments pb[kt][u] from softmax).
     auto pv = [&](int tile, const bf16x8 (&pb)[2][2]) {
-        const char * vl = lds[tile % kAttnStages] + kTileBytes;
+        const char * vl = lds + v_slot(tile);
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
@@ -627,7 +662,12 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
                     const uint2 lo2 = __builtin_bit_cast(uint2, lo4);
                     const uint2 hi2 = __builtin_bit_cast(uint2, hi4);
                     const bf16x8 va = __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
+#if PXS_ATTN_OACC_AGPR
+                    asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                        : "+a"(oacc[dt]) : "v"(va), "v"(pb[kt][u]));
+#else
                     oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kt][u], oacc[dt], 0, 0, 0);
+#endif
                 }
             }
         }
@@ -669,6 +709,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
             const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
             m_run = m_new;
             l_part *= alpha;
+            oacc_ready();
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -712,6 +753,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
             const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
             m_run = m_new;
             l_part *= alpha;
+            oacc_ready();
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -786,6 +828,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 
     const float l_tot = lane_pair_sum(l_part);
     if (!q_valid) return;
+    oacc_ready();
     const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     uint16_t * op = static_cast<uint16_t *>(a.o) + q_row * a.ldo + head * 64;
 #pragma unroll
