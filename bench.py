@@ -5,9 +5,10 @@ Default workload (one "step" = one pass over the batch, inputs resident in HBM):
   unet_stage_128 - batch 2 on a 128^3 grid (61,056 + 101,207 voxels, unions of
   three ellipsoid shells), bf16 features, fp32 accumulation:
     generation-tagged voxel grid insert (with the stride-2 occupancy bits)
-    stride-2 topology (coarse cells, child map, the 64^3 grid)
     SubMConv3d 3^3 128 -> 128, its 3x3x3 neighbours looked up in the 128^3
-      grid inside its tiles (the neighbor map fused into the gather)
+      grid inside its tiles (the neighbor map fused into the gather); extra
+      workgroups of the same launch emit the stride-2 topology (coarse
+      cells, child map, the 64^3 grid)
     SparseConv3d 2^3 s2 128 -> 256
     SubMConv3d 3^3 256 -> 256 over the 64^3 grid the topology wrote
   value = sum over the three convs of (active pairs x Cin x Cout) / step time,
@@ -59,6 +60,9 @@ def parse():
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="leave configs 1 and 4 off the default line")
+    ap.add_argument("--topology", default="fused", choices=["fused", "separate"],
+                    help="U-Net step: the stride-2 emit inside conv A's launch (fused) or the "
+                         "three-launch topology before it (separate)")
     return ap.parse_args()
 
 
@@ -212,22 +216,36 @@ def unet_stage(args, torch, px, W):
     def step():
         s = S()
         # generations 1..255 between resets: the step after generation 255
-        # refills the grid first (once per 255 steps, inside the timed op)
+        # refills the grid (and the s2 workspace's tagged bitmap) first (once
+        # per 255 steps, inside the timed op)
         wrap = gen[0] == 255
         gen[0] = gen[0] % 255 + 1
         g = C.c_uint32(gen[0])
-        # grid insert and the stride-2 topology (which also writes the 64^3
-        # grid) in three launches; no neighbour maps: both SubMConv3d look
-        # their 27 neighbours up in the grids inside their tiles
-        timer.run("topology_128", lambda: (
-            chk(lib.pxs_voxel_grid_tagged_reset(P(grid1), 2, 128, 128, 128, s), "reset")
-            if wrap else None,
-            chk(lib.pxs_map_s2_topology_tagged(
+
+        def resets():
+            if wrap:
+                chk(lib.pxs_voxel_grid_tagged_reset(P(grid1), 2, 128, 128, 128, s), "reset")
+                chk(lib.pxs_downsample_s2_tagged_workspace_reset(P(ds_ws), 2, 128, 128, 128, s),
+                    "reset s2")
+        # no neighbour maps: both SubMConv3d look their 27 neighbours up in the
+        # grids inside their tiles
+        if args.topology == "fused":
+            # grid insert (+ the stride-2 occupancy bits), then conv A, whose
+            # launch also emits the coarse rows, child slots and 64^3 grid in
+            # extra workgroups
+            timer.run("topology_128", lambda: (resets(), chk(lib.pxs_s2_tagged_insert(
+                P(coords), n, 2, 128, 128, 128, P(grid1), g, P(ds_ws), s), "insert")))
+            timer.run("subm_conv_a", lambda: chk(lib.pxs_subm_conv3d_grid_s2_emit(
+                1, P(x), P(coords), n, 128, P(w_a), P(b_a), 128, 2, 128, 128, 128, P(grid1), g,
+                P(y_a), P(oc), P(child), n, P(m_dev), P(grid2), P(ds_ws), s), "conv a"))
+        else:
+            # grid insert and the stride-2 topology in three launches
+            timer.run("topology_128", lambda: (resets(), chk(lib.pxs_map_s2_topology_tagged(
                 P(coords), n, 2, 128, 128, 128, P(grid1), g, None, None, P(oc), P(child), n,
                 P(m_dev), P(grid2), P(ds_ws), s), "topology")))
-        timer.run("subm_conv_a", lambda: chk(lib.pxs_subm_conv3d_grid(
-            1, P(x), P(coords), n, 128, P(w_a), P(b_a), 128, 2, 128, 128, 128, P(grid1), g,
-            P(y_a), s), "conv a"))
+            timer.run("subm_conv_a", lambda: chk(lib.pxs_subm_conv3d_grid(
+                1, P(x), P(coords), n, 128, P(w_a), P(b_a), 128, 2, 128, 128, 128, P(grid1), g,
+                P(y_a), s), "conv a"))
         timer.run("sparse_conv_b", lambda: chk(lib.pxs_sparse_conv3d_s2(
             1, P(y_a), n, 128, P(w_b), P(b_b), 256, P(child), n, m, P(y_b), s), "conv b"))
         timer.run("subm_conv_c", lambda: chk(lib.pxs_subm_conv3d_grid(
@@ -269,8 +287,10 @@ def unet_stage(args, torch, px, W):
     # 4-byte tagged cell written (and its bit in the occupancy bitmap); per
     # coarse cell one int32 of the 64^3 grid, per coarse row its coordinate
     # and 8 child slots (the child lookups read cells the insert just wrote).
+    # With the fused topology the timed op is the insert alone (the emit's
+    # bytes move inside conv A's launch).
     cells_64 = 2 * 64 * 64 * 64
-    topo_bytes = n * (16 + 4) + cells_64 * 4 + m * (16 + 8 * 4)
+    topo_bytes = n * (16 + 4) + (0 if args.topology == "fused" else cells_64 * 4 + m * (16 + 8 * 4))
     per_op["topology_128"] = {"ms": round(kern["topology_128"], 4),
                               "gbs": round(topo_bytes / (kern["topology_128"] * 1e-3) / 1e9, 1)}
     result = {
@@ -284,6 +304,9 @@ def unet_stage(args, torch, px, W):
                                "(+ 64^3 grid), SubMConv3d 128->128, SparseConv3d 128->256, "
                                "SubMConv3d 256->256; the SubMConv3d take their 27 neighbours "
                                "from the grids inside their tiles (no neighbour map)",
+                   "topology": ("grid insert + stride-2 marks, then the coarse emit in extra "
+                                "workgroups of conv A's launch" if args.topology == "fused" else
+                                "three launches before conv A"),
                    "voxels": n, "voxels_64": m, "pairs_a": pa, "pairs_c": pc,
                    "warmup_steps_run": warm,
                    "per_op_note": "per-op times from a pass of args.steps steps with every op "

@@ -233,6 +233,37 @@ int pxs_map_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size
                                int64_t ld_map, int64_t * m_out, void * coarse_grid,
                                void * s2_workspace, void * stream);
 
+/* The same level split so that its emit rides on the level's first
+ * convolution (the reference builds this topology inside sparse_downsample
+ * and the strided conv's gather, src/sparse.cpp:553-597 and 682-686, and the
+ * neighbour map inside sparse_submanifold_conv3d, src/sparse.cpp:999-1055):
+ *   pxs_s2_tagged_insert: the rows into the tagged grid under generation,
+ *     each row's stride-2 cell marked in bitmap (generation & 1) of a pair in
+ *     s2_workspace (a region of its own); the emit of generation g clears
+ *     the other bitmap, so successive builds on one workspace use successive
+ *     generations, and pxs_downsample_s2_tagged_workspace_reset precedes the
+ *     first and every restart of the generations (as for the grid);
+ *   pxs_subm_conv3d_grid_s2_emit: pxs_subm_conv3d_grid over that grid, with
+ *     the emit (out_coords, child_map, *m_out, coarse_grid, as
+ *     pxs_map_s2_topology_tagged writes them) done by extra workgroups of the
+ *     same launch on the bf16 16-byte path, or by a launch after it;
+ *   pxs_s2_tagged_emit: the emit alone (n = the fine row count, for the
+ *     child map stride check).
+ * Outputs identical to pxs_map_s2_topology_tagged without a map followed by
+ * pxs_subm_conv3d_grid; the same limits. */
+int pxs_s2_tagged_insert(const int32_t * coords, int64_t n, int batch_size, int sx, int sy, int sz,
+                         void * grid, uint32_t generation, void * s2_workspace, void * stream);
+int pxs_subm_conv3d_grid_s2_emit(int dtype, const void * x, const int32_t * coords, int64_t n,
+                                 int cin, const void * weight, const float * bias, int cout,
+                                 int batch_size, int sx, int sy, int sz, const void * grid,
+                                 uint32_t generation, void * y, int32_t * out_coords,
+                                 int32_t * child_map, int64_t ld_map, int64_t * m_out,
+                                 void * coarse_grid, void * s2_workspace, void * stream);
+int pxs_s2_tagged_emit(int64_t n, int batch_size, int sx, int sy, int sz, const void * grid,
+                       uint32_t generation, int32_t * out_coords, int32_t * child_map,
+                       int64_t ld_map, int64_t * m_out, void * coarse_grid, void * s2_workspace,
+                       void * stream);
+
 /* The same topology for any factor f, as groups: output q (coordinates
  * (b, x/f, y/f, z/f), lexicographic) gathers input rows
  * group_rows[group_offsets[q] .. group_offsets[q+1]) in ascending order.

@@ -19,6 +19,8 @@
 // lane reads 16 contiguous bytes per LDS access.
 
 #include "pxs_common.h"
+#include "s2emit.h"
+#include "scan.h"
 
 #include <type_traits>
 
@@ -59,6 +61,10 @@ struct GemmArgs {
     const uint32_t * grid;
     int grid_b, grid_x, grid_y, grid_z;
     uint32_t grid_gen;
+    // Side work carried by the launch (LDS-pipeline kernels only): workgroups
+    // [0, s2.blocks) run the stride-2 emit (s2emit.h) instead of a tile.
+    int side_blocks;
+    S2EmitArgs s2;
 };
 
 // Source row of output row p (coordinates c) at 3x3x3 offset k = kd*9 + kh*3
@@ -456,7 +462,14 @@ gather_gemm_lds_kernel(GemmArgs a) {
     const int h = lane >> 5, r = lane & 31;
 
     const int tiles_n = (a.cout + BN - 1) / BN;
-    const int logical = remap_xcd(blockIdx.x, gridDim.x);
+    // Side workgroups last: dispatched in order, they take the slots the
+    // tiles' last, partial round leaves free.
+    const int tiles = static_cast<int>(gridDim.x) - a.side_blocks;
+    if (static_cast<int>(blockIdx.x) >= tiles) {
+        s2_emit_block(a.s2, blockIdx.x - tiles, tid, kThreads, smem);
+        return;
+    }
+    const int logical = remap_xcd(blockIdx.x, tiles);
     const int64_t p0 = static_cast<int64_t>(logical / tiles_n) * BM;
     const int n0 = (logical % tiles_n) * BN;
     const T * __restrict__ x = static_cast<const T *>(a.x);
@@ -728,6 +741,7 @@ gather_gemm_lds_kernel(GemmArgs a) {
 #ifndef PXS_GEMM_HALO
 #define PXS_GEMM_HALO 0
 #endif
+constexpr int kSideEmitWords = 32;  // bitmap words per emit side workgroup (1,024 cells)
 constexpr int kHaloBM = 128, kHaloBN = 128, kHaloMax = 576, kHaloNW = 8, kHaloWStages = 4;
 // Distinct sources are found with a byte map over the tile's source range
 // [lo, hi] (at most kHaloRange rows; wider tiles read their operands from
@@ -1199,8 +1213,11 @@ int launch_lds_tile(const GemmArgs & args, hipStream_t stream) {
     }
     const int64_t tiles_m = (args.m + BM - 1) / BM;
     const int64_t tiles_n = (args.cout + BN - 1) / BN;
-    const int64_t blocks = tiles_m * tiles_n;
+    const int64_t blocks = tiles_m * tiles_n + args.side_blocks;
     if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "gather GEMM grid too large");
+    if (args.side_blocks > 0 &&
+        smem < s2_emit_lds_bytes(args.s2.words_per_block, NW * 64))
+        return fail(PXS_ERR_ARG, "gather GEMM: side work needs more LDS than the tile");
     hipLaunchKernelGGL((gather_gemm_lds_kernel<T, BM, BN, EPI, NSTAGE, NW, WAVES_M, KSPLIT>),
                        dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), smem, stream, args);
     return check_launch("gather GEMM (LDS pipeline)");
@@ -1539,6 +1556,53 @@ int pxs_subm_conv3d_grid(int dtype, const void * x, const int32_t * coords, int6
     a.grid = static_cast<const uint32_t *>(grid);
     a.grid_b = batch_size; a.grid_x = sx; a.grid_y = sy; a.grid_z = sz; a.grid_gen = generation;
     return run_gemm(dtype, a, kEpiStore, as_stream(stream));
+}
+
+int pxs_subm_conv3d_grid_s2_emit(int dtype, const void * x, const int32_t * coords, int64_t n,
+                                 int cin, const void * weight, const float * bias, int cout,
+                                 int batch_size, int sx, int sy, int sz, const void * grid,
+                                 uint32_t generation, void * y, int32_t * out_coords,
+                                 int32_t * child_map, int64_t ld_map, int64_t * m_out,
+                                 void * coarse_grid, void * s2_workspace, void * stream) {
+    const char * who = "pxs_subm_conv3d_grid_s2_emit";
+    if (int rc = check_dtype(dtype, who)) return rc;
+    PXS_CHECK(n >= 0 && cin > 0 && cout > 0, PXS_ERR_ARG, std::string(who) + ": bad shape");
+    PXS_CHECK(pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              std::string(who) + ": invalid extents");
+    PXS_CHECK(generation >= 1 && generation <= kVoxelTagMax, PXS_ERR_ARG,
+              std::string(who) + ": generation must be in 1..255");
+    PXS_CHECK(n < (int64_t{1} << kVoxelTagShift), PXS_ERR_ARG,
+              std::string(who) + ": bad row count (at most 2^24 - 1 rows)");
+    PXS_CHECK(ld_map >= n, PXS_ERR_ARG, std::string(who) + ": child map stride below the row count");
+    PXS_CHECK_WORKSPACE(s2_workspace, who);
+    PXS_CHECK(m_out && s2_workspace, PXS_ERR_ARG, std::string(who) + ": null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) return fill_i64(m_out, 1, 0, s);
+    PXS_CHECK(x && coords && weight && grid && y && out_coords && child_map && coarse_grid,
+              PXS_ERR_ARG, std::string(who) + ": null pointer");
+    PXS_CHECK((reinterpret_cast<uintptr_t>(coords) & 15u) == 0, PXS_ERR_ARG,
+              std::string(who) + ": coordinates must be 16-byte aligned");
+    PXS_CHECK((reinterpret_cast<uintptr_t>(grid) & 3u) == 0, PXS_ERR_ARG,
+              std::string(who) + ": the grid must be 4-byte aligned");
+    GemmArgs a{};
+    a.x = x; a.rows_in = n; a.ldx = cin; a.cin = cin; a.w = weight; a.bias = bias;
+    a.cout = cout; a.m = n; a.rowmap = nullptr; a.ld_map = 0; a.noff = 27; a.masks = nullptr;
+    a.y = y; a.ldy = cout; a.act = PXS_ACT_NONE; a.coords = coords;
+    a.grid = static_cast<const uint32_t *>(grid);
+    a.grid_b = batch_size; a.grid_x = sx; a.grid_y = sy; a.grid_z = sz; a.grid_gen = generation;
+    // The bf16 16-byte path runs on the LDS-pipeline kernel, which carries the
+    // emit in side workgroups; otherwise the emit follows as its own launch.
+    const bool fuse = dtype == PXS_BF16 && cin % 8 == 0 && aligned16(x) && aligned16(weight) &&
+                      !PXS_GEMM_HALO;
+    if (fuse) {
+        a.s2 = make_s2_emit_args(batch_size, sx, sy, sz, grid, generation, out_coords, child_map,
+                                 ld_map, m_out, coarse_grid, s2_workspace, kSideEmitWords);
+        a.side_blocks = a.s2.blocks;
+        return run_gemm(dtype, a, kEpiStore, s);
+    }
+    if (int rc = run_gemm(dtype, a, kEpiStore, s)) return rc;
+    return pxs_s2_tagged_emit(n, batch_size, sx, sy, sz, grid, generation, out_coords, child_map,
+                              ld_map, m_out, coarse_grid, s2_workspace, stream);
 }
 
 int pxs_sparse_conv3d_s2(int dtype, const void * x, int64_t n_in, int cin, const void * weight,

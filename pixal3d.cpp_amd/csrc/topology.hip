@@ -6,6 +6,7 @@
 // outputs so a wavefront writes 64 consecutive entries of one offset).
 
 #include "pxs_common.h"
+#include "s2emit.h"
 #include "scan.h"
 
 #include <algorithm>
@@ -465,6 +466,12 @@ __global__ void tagged_scatter_mark_kernel(const int4 * __restrict__ coords, int
         bit = 1u << (cell & 31);
     }
     mark_bits(live, word, bit, bitmap);
+}
+
+constexpr int kEmitWords = 256;  // bitmap words per emit workgroup
+__global__ void __launch_bounds__(kThreads) s2_emit_tagged_kernel(S2EmitArgs e) {
+    __shared__ __align__(16) char lds[s2_emit_lds_bytes(kEmitWords, kThreads)];
+    s2_emit_block(e, blockIdx.x, threadIdx.x, kThreads, lds);
 }
 
 __device__ __forceinline__ int64_t coarse_rank(int64_t cell, const uint32_t * __restrict__ bitmap,
@@ -1223,8 +1230,47 @@ size_t pxs_downsample_s2_tagged_workspace_bytes(int batch_size, int sx, int sy, 
     const int64_t words = (cells + 31) / 32;
     const int64_t blocks = (words + kWordBlock - 1) / kWordBlock;
     auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
-    return static_cast<size_t>(up(words * 4) + up(words * 4) + up(blocks * 4));
+    // bitmap, word prefixes, block totals; then the bitmap pair of the fused
+    // emit (pxs_s2_tagged_insert / pxs_subm_conv3d_grid_s2_emit)
+    return static_cast<size_t>(up(words * 4) + up(words * 4) + up(blocks * 4) + 2 * up(words * 4));
 }
+
+}  // extern "C"
+
+namespace pxs {
+// The emit's arguments over a workspace of pxs_downsample_s2_tagged_workspace_bytes.
+S2EmitArgs make_s2_emit_args(int batch_size, int sx, int sy, int sz, const void * fine_grid,
+                             uint32_t generation, int32_t * out_coords, int32_t * child_map,
+                             int64_t ld_map, int64_t * m_out, void * coarse_grid,
+                             void * s2_workspace, int words_per_block) {
+    const int cx = (sx + 1) / 2, cy = (sy + 1) / 2, cz = (sz + 1) / 2;
+    const int64_t cells = static_cast<int64_t>(batch_size) * cx * cy * cz;
+    const int64_t words = (cells + 31) / 32;
+    const int64_t blocks = (words + kWordBlock - 1) / kWordBlock;
+    auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
+    S2EmitArgs e{};
+    char * pair = static_cast<char *>(s2_workspace) + 2 * up(words * 4) + up(blocks * 4);
+    e.bits = reinterpret_cast<const uint32_t *>(pair + (generation & 1) * up(words * 4));
+    e.clear_bits = reinterpret_cast<uint32_t *>(pair + ((generation + 1) & 1) * up(words * 4));
+    e.words = words;
+    e.cells = cells;
+    e.b = batch_size; e.fx = sx; e.fy = sy; e.fz = sz;
+    e.cx = cx; e.cy = cy; e.cz = cz;
+    e.fine_grid = static_cast<const uint32_t *>(fine_grid);
+    e.generation = generation;
+    e.coarse_grid = static_cast<int32_t *>(coarse_grid);
+    e.out_coords = reinterpret_cast<int4 *>(out_coords);
+    e.child_map = child_map;
+    e.ld_map = ld_map;
+    e.m_out = m_out;
+    e.words_per_block = words_per_block;
+    // a multiple of 8, so that workgroups after the emit's keep their XCD
+    e.blocks = static_cast<int>(((words + words_per_block - 1) / words_per_block + 7) / 8 * 8);
+    return e;
+}
+}  // namespace pxs
+
+extern "C" {
 
 int pxs_downsample_s2_tagged_workspace_reset(void * workspace, int batch_size, int sx, int sy,
                                              int sz, void * stream) {
@@ -1277,6 +1323,51 @@ int pxs_downsample_s2_topology_tagged(const int32_t * coords, int64_t n, int bat
                        static_cast<int32_t *>(coarse_grid), reinterpret_cast<int4 *>(out_coords),
                        child_map, ld_map, m_out);
     return check_launch("pxs_downsample_s2_topology_tagged");
+}
+
+int pxs_s2_tagged_insert(const int32_t * coords, int64_t n, int batch_size, int sx, int sy, int sz,
+                         void * grid, uint32_t generation, void * s2_workspace, void * stream) {
+    PXS_CHECK_WORKSPACE(s2_workspace, "pxs_s2_tagged_insert");
+    PXS_CHECK(n >= 0 && n <= kTagMaxRows, PXS_ERR_ARG,
+              "pxs_s2_tagged_insert: bad row count (at most 2^24 - 1 rows)");
+    PXS_CHECK(pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              "pxs_s2_tagged_insert: invalid extents");
+    PXS_CHECK(generation >= 1 && generation <= kTagMaxGeneration, PXS_ERR_ARG,
+              "pxs_s2_tagged_insert: generation must be in 1..255");
+    if (n == 0) return PXS_OK;
+    PXS_CHECK(coords && grid && s2_workspace, PXS_ERR_ARG, "pxs_s2_tagged_insert: null pointer");
+    const S2EmitArgs e = make_s2_emit_args(batch_size, sx, sy, sz, grid, generation, nullptr,
+                                           nullptr, 0, nullptr, nullptr, s2_workspace, kEmitWords);
+    hipLaunchKernelGGL(tagged_scatter_mark_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads),
+                       0, as_stream(stream), reinterpret_cast<const int4 *>(coords), n,
+                       GridDims{batch_size, sx, sy, sz}, static_cast<uint32_t *>(grid), generation,
+                       e.cx, e.cy, e.cz, e.words, const_cast<uint32_t *>(e.bits));
+    return check_launch("pxs_s2_tagged_insert");
+}
+
+int pxs_s2_tagged_emit(int64_t n, int batch_size, int sx, int sy, int sz, const void * grid,
+                       uint32_t generation, int32_t * out_coords, int32_t * child_map,
+                       int64_t ld_map, int64_t * m_out, void * coarse_grid, void * s2_workspace,
+                       void * stream) {
+    PXS_CHECK_WORKSPACE(s2_workspace, "pxs_s2_tagged_emit");
+    PXS_CHECK(n >= 0 && n <= kTagMaxRows, PXS_ERR_ARG,
+              "pxs_s2_tagged_emit: bad row count (at most 2^24 - 1 rows)");
+    PXS_CHECK(pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              "pxs_s2_tagged_emit: invalid extents");
+    PXS_CHECK(generation >= 1 && generation <= kTagMaxGeneration, PXS_ERR_ARG,
+              "pxs_s2_tagged_emit: generation must be in 1..255");
+    PXS_CHECK(ld_map >= n, PXS_ERR_ARG, "pxs_s2_tagged_emit: child map stride below the row count");
+    PXS_CHECK(m_out && s2_workspace, PXS_ERR_ARG, "pxs_s2_tagged_emit: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) return fill_i64(m_out, 1, 0, s);
+    PXS_CHECK(grid && out_coords && child_map && coarse_grid, PXS_ERR_ARG,
+              "pxs_s2_tagged_emit: null pointer");
+    const S2EmitArgs e = make_s2_emit_args(batch_size, sx, sy, sz, grid, generation, out_coords,
+                                           child_map, ld_map, m_out, coarse_grid, s2_workspace,
+                                           kEmitWords);
+    hipLaunchKernelGGL(s2_emit_tagged_kernel, dim3(static_cast<unsigned>(e.blocks)), dim3(kThreads),
+                       0, s, e);
+    return check_launch("pxs_s2_tagged_emit");
 }
 
 int pxs_map_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,

@@ -115,6 +115,13 @@ _SIGS = {
                                                  C.c_uint32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "pxs_map_s2_topology_tagged": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, C.c_uint32,
                                           _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "pxs_s2_tagged_insert": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, C.c_uint32, _vp,
+                                    _vp]),
+    "pxs_subm_conv3d_grid_s2_emit": (_i32, [_i32, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32,
+                                            _i32, _i32, _i32, _vp, C.c_uint32, _vp, _vp, _vp,
+                                            _i64, _vp, _vp, _vp, _vp]),
+    "pxs_s2_tagged_emit": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, C.c_uint32, _vp, _vp, _i64,
+                                  _vp, _vp, _vp, _vp]),
     "pxs_voxel_grid_build": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
     "pxs_neighbor_map_k3_grid": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "pxs_convnext_block_workspace_bytes": (C.c_size_t, [_i32, _i64, _i32, _i32, _i32]),
@@ -538,6 +545,43 @@ class Pxs:
                                                   self.stream()),
                     "pxs_subm_conv3d_grid")
         return y
+
+    def s2_tagged_insert(self, coords, batch_size, shape, grid, generation, workspace):
+        """pxs_s2_tagged_insert: rows into the tagged grid, their stride-2
+        cells marked in the workspace's generation-tagged bitmap."""
+        self._check(self.lib.pxs_s2_tagged_insert(_ptr(coords), coords.shape[0], batch_size,
+                                                  *shape, _ptr(grid), generation, _ptr(workspace),
+                                                  self.stream()), "pxs_s2_tagged_insert")
+
+    def _s2_outputs(self, n, dev):
+        oc = torch.empty((max(n, 1), 4), dtype=torch.int32, device=dev)
+        child = torch.empty((8, max(n, 1)), dtype=torch.int32, device=dev)
+        m = torch.empty(1, dtype=torch.int64, device=dev)
+        return oc, child, m
+
+    def subm_conv3d_grid_s2_emit(self, x, weight, bias, coords, batch_size, shape, grid,
+                                 generation, coarse_grid, workspace, out=None, s2_out=None):
+        """pxs_subm_conv3d_grid_s2_emit -> (y, out_coords, child_map [8, n],
+        m as a device int64)."""
+        n, cin = x.shape
+        cout = weight.shape[1]
+        y = torch.empty((n, cout), dtype=x.dtype, device=x.device) if out is None else out
+        oc, child, m = self._s2_outputs(n, x.device) if s2_out is None else s2_out
+        self._check(self.lib.pxs_subm_conv3d_grid_s2_emit(
+            _dtype_code(x), _ptr(x), _ptr(coords), n, cin, _ptr(weight), _ptr(bias), cout,
+            batch_size, *shape, _ptr(grid), generation, _ptr(y), _ptr(oc), _ptr(child),
+            child.shape[1], _ptr(m), _ptr(coarse_grid), _ptr(workspace), self.stream()),
+            "pxs_subm_conv3d_grid_s2_emit")
+        return y, oc, child, m
+
+    def s2_tagged_emit(self, n, batch_size, shape, grid, generation, coarse_grid, workspace):
+        """pxs_s2_tagged_emit -> (out_coords, child_map [8, n], m as a device int64)."""
+        oc, child, m = self._s2_outputs(n, grid.device)
+        self._check(self.lib.pxs_s2_tagged_emit(n, batch_size, *shape, _ptr(grid), generation,
+                                                _ptr(oc), _ptr(child), child.shape[1], _ptr(m),
+                                                _ptr(coarse_grid), _ptr(workspace),
+                                                self.stream()), "pxs_s2_tagged_emit")
+        return oc, child, m
 
     def sparse_conv3d_s2(self, x, weight, bias, child_map, m, out=None):
         n, cin = x.shape

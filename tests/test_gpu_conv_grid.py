@@ -188,3 +188,78 @@ def test_unet_conv_c_grid_from_topology(px):
     nbr, masks = px.neighbor_map_grid(oc, 2, (64, 64, 64), grid=cg)
     y_map = px.subm_conv3d(x, w, b, nbr.contiguous(), masks)
     np.testing.assert_array_equal(_bits(y_grid), _bits(y_map))
+
+
+S2_CASES = [
+    # (name, coords builder, batch, extents, cin, cout)
+    ("unet_a", lambda: W.unet_stage_128()["coords"], 2, (128, 128, 128), 128, 128),
+    ("box_odd", lambda: _box_coords(11, 1, (5, 9, 4), 0.6), 1, (5, 9, 4), 16, 24),
+    ("box_wide", lambda: _box_coords(12, 3, (40, 22, 30), 0.3), 3, (40, 22, 30), 32, 64),
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("name,make,batch,shape,cin,cout", S2_CASES, ids=[c[0] for c in S2_CASES])
+def test_s2_emit_fused_matches_topology(px, name, make, batch, shape, cin, cout, dtype):
+    """pxs_s2_tagged_insert then pxs_subm_conv3d_grid_s2_emit (bf16: the emit
+    in extra workgroups of the convolution's launch; fp32: a launch after it)
+    against pxs_map_s2_topology_tagged without a map then pxs_subm_conv3d_grid:
+    the convolution, coarse coordinates, child slots, count and coarse grid
+    bit-equal, and pxs_s2_tagged_emit alone the same.  Three successive
+    generations over one grid and workspace, the second on a subset of the
+    rows: each emit must clear the bitmap the next build marks."""
+    import torch
+    full = make()
+    rng = np.random.default_rng(len(full))
+    subset = full[np.sort(rng.choice(len(full), len(full) // 3, replace=False))]
+    cx, cy, cz = [(s + 1) // 2 for s in shape]
+    cells = px.lib.pxs_voxel_grid_bytes(batch, cx, cy, cz) // 4
+    dev = torch.device("cuda")
+    tg_ref, ws_ref = px.tagged_grid(batch, shape), px.s2_tagged_workspace(batch, shape)
+    tg, ws = px.tagged_grid(batch, shape), px.s2_tagged_workspace(batch, shape)
+    for gen, coords in ((1, full), (2, subset), (3, full)):
+        n = len(coords)
+        print(f"[s2 emit fused] {name} {dtype} gen={gen} n={n}", flush=True)
+        c = ti32(coords)
+        xr = rng.standard_normal((n, cin)).astype(np.float32)
+        wr = (rng.standard_normal((27, cout, cin)) * (2.0 / (27 * cin)) ** 0.5).astype(np.float32)
+        br = (rng.standard_normal(cout) * 0.1).astype(np.float32)
+        x, w = (tbf(xr), tbf(wr)) if dtype == "bf16" else (t32(xr), t32(wr))
+        b = t32(br)
+        cg_ref = torch.full((cells,), 7, dtype=torch.int32, device=dev)
+        _, _, oc_ref, child_ref, m_ref = px.map_s2_tagged(c, batch, shape, tg_ref, gen, cg_ref,
+                                                          ws_ref, with_map=False)
+        y_ref = px.subm_conv3d_grid(x, w, b, c, batch, shape, tg_ref, gen)
+        cg = torch.full((cells,), 9, dtype=torch.int32, device=dev)
+        px.s2_tagged_insert(c, batch, shape, tg, gen, ws)
+        y, oc, child, m = px.subm_conv3d_grid_s2_emit(x, w, b, c, batch, shape, tg, gen, cg, ws)
+        m = int(m.item())
+        assert m == m_ref
+        np.testing.assert_array_equal(_bits(y), _bits(y_ref))
+        np.testing.assert_array_equal(oc[:m].cpu().numpy(), oc_ref.cpu().numpy())
+        np.testing.assert_array_equal(child[:, :m].cpu().numpy(), child_ref[:, :m].cpu().numpy())
+        np.testing.assert_array_equal(cg.cpu().numpy(), cg_ref.cpu().numpy())
+        cg2 = torch.full((cells,), 5, dtype=torch.int32, device=dev)
+        oc2, child2, m2 = px.s2_tagged_emit(n, batch, shape, tg, gen, cg2, ws)
+        assert int(m2.item()) == m
+        np.testing.assert_array_equal(oc2[:m].cpu().numpy(), oc_ref.cpu().numpy())
+        np.testing.assert_array_equal(child2[:, :m].cpu().numpy(), child_ref[:, :m].cpu().numpy())
+        np.testing.assert_array_equal(cg2.cpu().numpy(), cg_ref.cpu().numpy())
+
+
+def test_s2_emit_rejects_bad_arguments(px):
+    import pxs
+    import torch
+    c = ti32(np.zeros((4, 4), np.int32))
+    grid = px.tagged_grid(1, (4, 4, 4))
+    ws = px.s2_tagged_workspace(1, (4, 4, 4))
+    with pytest.raises(pxs.PxsError, match="generation must be in 1..255"):
+        px.s2_tagged_insert(c, 1, (4, 4, 4), grid, 0, ws)
+    x = torch.zeros((4, 8), dtype=torch.bfloat16, device=c.device)
+    w = torch.zeros((27, 8, 8), dtype=torch.bfloat16, device=c.device)
+    cg = torch.zeros(8, dtype=torch.int32, device=c.device)
+    outs = (torch.zeros((4, 4), dtype=torch.int32, device=c.device),
+            torch.zeros((8, 2), dtype=torch.int32, device=c.device),
+            torch.zeros(1, dtype=torch.int64, device=c.device))
+    with pytest.raises(pxs.PxsError, match="child map stride below the row count"):
+        px.subm_conv3d_grid_s2_emit(x, w, None, c, 1, (4, 4, 4), grid, 1, cg, ws, s2_out=outs)
