@@ -60,9 +60,10 @@ def parse():
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="leave configs 1 and 4 off the default line")
-    ap.add_argument("--topology", default="fused", choices=["fused", "separate"],
-                    help="U-Net step: the stride-2 emit inside conv A's launch (fused) or the "
-                         "three-launch topology before it (separate)")
+    ap.add_argument("--topology", default="fused", choices=["chained", "fused", "separate"],
+                    help="U-Net step: conv A, the stride-2 emit and conv B in one launch "
+                         "(chained), the emit inside conv A's launch (fused), or the "
+                         "three-launch topology before conv A (separate)")
     return ap.parse_args()
 
 
@@ -229,6 +230,20 @@ def unet_stage(args, torch, px, W):
                     "reset s2")
         # no neighbour maps: both SubMConv3d look their 27 neighbours up in the
         # grids inside their tiles
+        if args.topology == "chained":
+            # grid insert (+ the stride-2 occupancy bits), then one launch of
+            # conv A, the coarse emit and conv B, whose tiles wait inside the
+            # launch only for the conv A tiles (and the emit) they read
+            timer.run("topology_128", lambda: (resets(), chk(lib.pxs_s2_tagged_insert(
+                P(coords), n, 2, 128, 128, 128, P(grid1), g, P(ds_ws), s), "insert")))
+            timer.run("conv_a_b_chained", lambda: chk(lib.pxs_unet_s2_level(
+                1, P(x), P(coords), n, 128, P(w_a), P(b_a), 128, 2, 128, 128, 128, P(grid1), g,
+                P(y_a), P(w_b), P(b_b), 256, m, P(y_b), P(oc), P(child), n, P(m_dev), P(grid2),
+                P(ds_ws), s), "conv a + b"))
+            timer.run("subm_conv_c", lambda: chk(lib.pxs_subm_conv3d_grid(
+                1, P(y_b), P(oc), m, 256, P(w_c), P(b_c), 256, 2, 64, 64, 64, P(grid2), 0,
+                P(y_c), s), "conv c"))
+            return
         if args.topology == "fused":
             # grid insert (+ the stride-2 occupancy bits), then conv A, whose
             # launch also emits the coarse rows, child slots and 64^3 grid in
@@ -252,11 +267,14 @@ def unet_stage(args, torch, px, W):
             1, P(y_b), P(oc), m, 256, P(w_c), P(b_c), 256, 2, 64, 64, 64, P(grid2), 0, P(y_c), s),
             "conv c"))
 
-    ops = ("topology_128", "subm_conv_a", "sparse_conv_b", "subm_conv_c")
-    timer.only = set()
-    warm = warm_up(args, torch, step)
     macs = {"subm_conv_a": pa * 128 * 128, "sparse_conv_b": n * 128 * 256,
             "subm_conv_c": pc * 256 * 256}
+    if args.topology == "chained":
+        macs = {"conv_a_b_chained": macs["subm_conv_a"] + macs["sparse_conv_b"],
+                "subm_conv_c": macs["subm_conv_c"]}
+    ops = ("topology_128",) + tuple(macs)
+    timer.only = set()
+    warm = warm_up(args, torch, step)
     # Per-op breakdown: a pass of its own with every op bracketed by events.
     timer.only = None
     timer.reset()
@@ -290,7 +308,7 @@ def unet_stage(args, torch, px, W):
     # With the fused topology the timed op is the insert alone (the emit's
     # bytes move inside conv A's launch).
     cells_64 = 2 * 64 * 64 * 64
-    topo_bytes = n * (16 + 4) + (0 if args.topology == "fused" else cells_64 * 4 + m * (16 + 8 * 4))
+    topo_bytes = n * (16 + 4) + (0 if args.topology != "separate" else cells_64 * 4 + m * (16 + 8 * 4))
     per_op["topology_128"] = {"ms": round(kern["topology_128"], 4),
                               "gbs": round(topo_bytes / (kern["topology_128"] * 1e-3) / 1e9, 1)}
     result = {
@@ -304,9 +322,12 @@ def unet_stage(args, torch, px, W):
                                "(+ 64^3 grid), SubMConv3d 128->128, SparseConv3d 128->256, "
                                "SubMConv3d 256->256; the SubMConv3d take their 27 neighbours "
                                "from the grids inside their tiles (no neighbour map)",
-                   "topology": ("grid insert + stride-2 marks, then the coarse emit in extra "
-                                "workgroups of conv A's launch" if args.topology == "fused" else
-                                "three launches before conv A"),
+                   "topology": {"chained": "grid insert + stride-2 marks, then one launch of "
+                                           "conv A, the coarse emit and conv B (conv B's tiles "
+                                           "wait in the launch for the conv A tiles they read)",
+                                "fused": "grid insert + stride-2 marks, then the coarse emit in "
+                                         "extra workgroups of conv A's launch",
+                                "separate": "three launches before conv A"}[args.topology],
                    "voxels": n, "voxels_64": m, "pairs_a": pa, "pairs_c": pc,
                    "warmup_steps_run": warm,
                    "per_op_note": "per-op times from a pass of args.steps steps with every op "

@@ -264,6 +264,34 @@ int pxs_s2_tagged_emit(int64_t n, int batch_size, int sx, int sy, int sz, const 
                        int64_t ld_map, int64_t * m_out, void * coarse_grid, void * s2_workspace,
                        void * stream);
 
+/* A U-Net encoder level after pxs_s2_tagged_insert, in one launch: the
+ * SubMConv3d of pxs_subm_conv3d_grid_s2_emit (x -> y_a, weights w_a
+ * [27, cout_a, cin]) with its stride-2 emit, then the strided conv of
+ * pxs_sparse_conv3d_s2 (y_a -> y_b, weights w_b [8, cout_b, cout_a]) over the
+ * child map the emit writes.  The reference runs these as
+ * sparse_submanifold_conv3d (src/sparse.cpp:999-1055) and a strided conv over
+ * the sparse_downsample topology (src/sparse.cpp:553-597, 682-686).  Each
+ * strided-conv tile waits, inside the launch, only for the emit and the
+ * SubMConv3d tiles that write its inputs, so it runs in the slots the
+ * SubMConv3d's last round leaves free.  m is the coarse row count (known on
+ * the host from an earlier build of these coordinates; y_b holds m rows); the
+ * emit still writes it to *m_out.  bf16 with 65..128 SubMConv3d outputs and
+ * more than 64 strided outputs run chained; other shapes and fp32 run the
+ * two calls in sequence.  Outputs identical to pxs_subm_conv3d_grid_s2_emit
+ * then pxs_sparse_conv3d_s2.  The waits are bounded: one that gives up (after
+ * about a second, which a correct launch never needs) sets an error word,
+ * read back (to host or device memory) by pxs_unet_s2_level_error; its
+ * launch's results are void.  The word is cleared by
+ * pxs_downsample_s2_tagged_workspace_reset. */
+int pxs_unet_s2_level(int dtype, const void * x, const int32_t * coords, int64_t n, int cin,
+                      const void * w_a, const float * b_a, int cout_a, int batch_size, int sx,
+                      int sy, int sz, const void * grid, uint32_t generation, void * y_a,
+                      const void * w_b, const float * b_b, int cout_b, int64_t m, void * y_b,
+                      int32_t * out_coords, int32_t * child_map, int64_t ld_map, int64_t * m_out,
+                      void * coarse_grid, void * s2_workspace, void * stream);
+int pxs_unet_s2_level_error(const void * s2_workspace, int batch_size, int sx, int sy, int sz,
+                            uint32_t * error_out, void * stream);
+
 /* The same topology for any factor f, as groups: output q (coordinates
  * (b, x/f, y/f, z/f), lexicographic) gathers input rows
  * group_rows[group_offsets[q] .. group_offsets[q+1]) in ascending order.

@@ -139,7 +139,7 @@ __device__ __forceinline__ uint4 load_chunk16(const T * base, int64_t row, int64
 
 // Epilogue.  32x32 accumulator layout: lane (h, r), register v holds row
 // 8*(v/4) + 4*h + v%4, column r of the 32x32 tile.
-template <typename T, int TI, int TJ, int WM, int WN, int EPI>
+template <typename T, int TI, int TJ, int WM, int WN, int EPI, bool COHERENT = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs & a, const f32x16 (&acc)[TI][TJ],
                                               int64_t p0, int n0, int wm, int wn, int h, int r) {
 #pragma unroll
@@ -157,7 +157,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs & a, const f32x16 (
                 if constexpr (EPI == kEpiStore) {
                     if (a.act == PXS_ACT_GELU_TANH) val = gelu_tanh_f(val);
                     else if (a.act == PXS_ACT_SILU) val = silu_f(val);
-                    store_f32(static_cast<T *>(a.y) + row * a.ldy + col, val);
+                    if constexpr (COHERENT)
+                        store_f32_coherent(static_cast<T *>(a.y) + row * a.ldy + col, val);
+                    else
+                        store_f32(static_cast<T *>(a.y) + row * a.ldy + col, val);
                 } else if constexpr (EPI == kEpiAddResidual) {
                     float * res = a.residual + row * a.cout + col;
                     *res = *res + val;
@@ -425,14 +428,45 @@ constexpr int lds_gemm_bytes(int noff) {
     return NSTAGE * (BM + BN) * kChunkBytes + noff * BM * 4;
 }
 
+// Dependencies between the workgroups of one launch (the chained U-Net
+// level): flags in global memory set to the launch's generation when a
+// producer's results are visible to the device.  A producer writes what
+// consumers read with device-coherent stores (sc1) and waits for them to
+// complete before it sets its flag; a consumer reads the flag and then the
+// produced data with device-coherent loads.  So no L2 is written back or
+// invalidated, which would stall, or cost every other tile on that XCD its
+// cached operands.  A consumer
+// workgroup only waits for workgroups with a lower index, which the
+// dispatcher places before it on every XCD, so the waits end.  The spin is
+// bounded all the same: a wait that gives up (after about a second) sets
+// *error and goes on, so the launch always completes and the caller can see
+// that its results are void.
+struct TileSync {
+    const uint32_t * emit_flags;  // wait for emit_flags[0, emit_count) == gen
+    int emit_count;
+    const uint32_t * src_flags;   // wait for the producer tiles holding this tile's sources
+    int src_bm, src_tiles_n;      // producer rows per tile, producer column tiles
+    uint32_t * done_flags;        // set done_flags[logical] = gen when this tile is stored
+    uint32_t gen;
+    uint32_t * error;
+};
+
+__device__ __forceinline__ void spin_until(const uint32_t * flag, uint32_t gen, uint32_t * error) {
+    for (int it = 0; it < (1 << 20); ++it) {
+        if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) return;
+        __builtin_amdgcn_s_sleep(4);
+    }
+    atomicOr(error, 1u);
+}
+
 // NW waves per workgroup in KSPLIT groups; the waves of a group form a
 // WAVES_M x (NW / KSPLIT / WAVES_M) grid, each owning a block of the output
 // tile.  With KSPLIT = 2 the two groups take alternate 16-element K steps
 // of every stage and add their partial sums once at the end: 8 waves of
 // 64x64 blocks read each LDS fragment for two MFMAs instead of 1.5.
-template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M, int KSPLIT>
-__global__ void __launch_bounds__(NW * 64)
-gather_gemm_lds_kernel(GemmArgs a) {
+template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M, int KSPLIT, bool SYNC>
+__device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, const TileSync & sync,
+                                              char * smem) {
     constexpr int kVec = Mfma<T>::kVec;
     constexpr int kChunk = Mfma<T>::kChunk;
     constexpr int kThreads = NW * 64;
@@ -449,10 +483,10 @@ gather_gemm_lds_kernel(GemmArgs a) {
     constexpr int kPerStage = AI + BI;
     static_assert(AI * 8 * NW == BM && BI * 8 * NW == BN, "tile rows must split over the waves");
 
-    extern __shared__ __align__(16) char smem[];
     int32_t * idx_lds = reinterpret_cast<int32_t *>(smem + NSTAGE * kStageBytes);
     __shared__ uint32_t tile_mask;
     __shared__ int koff[32];
+    __shared__ int src_lo, src_hi;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -462,19 +496,18 @@ gather_gemm_lds_kernel(GemmArgs a) {
     const int h = lane >> 5, r = lane & 31;
 
     const int tiles_n = (a.cout + BN - 1) / BN;
-    // Side workgroups last: dispatched in order, they take the slots the
-    // tiles' last, partial round leaves free.
-    const int tiles = static_cast<int>(gridDim.x) - a.side_blocks;
-    if (static_cast<int>(blockIdx.x) >= tiles) {
-        s2_emit_block(a.s2, blockIdx.x - tiles, tid, kThreads, smem);
-        return;
-    }
-    const int logical = remap_xcd(blockIdx.x, tiles);
     const int64_t p0 = static_cast<int64_t>(logical / tiles_n) * BM;
     const int n0 = (logical % tiles_n) * BN;
     const T * __restrict__ x = static_cast<const T *>(a.x);
     const T * __restrict__ w = static_cast<const T *>(a.w);
 
+    if constexpr (SYNC) {
+        // A consumer waits for the side workgroups that wrote its map.
+        if (sync.emit_flags) {
+            for (int i = tid; i < sync.emit_count; i += kThreads) spin_until(sync.emit_flags + i, sync.gen, sync.error);
+            __syncthreads();
+        }
+    }
     if (tid == 0) tile_mask = 0;
     __syncthreads();
     // A map without masks (the stride-2 conv's child map) is read once: every
@@ -490,7 +523,15 @@ gather_gemm_lds_kernel(GemmArgs a) {
             const int k = e / BM, row = e % BM;
             int32_t src = -1;
             if (p0 + row < a.m) {
-                const int32_t s = a.rowmap[k * a.ld_map + p0 + row];
+                const int32_t * q = a.rowmap + k * a.ld_map + p0 + row;
+                int32_t s;
+                if constexpr (SYNC) {
+                    // a map written in this launch: a device-coherent load
+                    s = sync.emit_flags ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                        : *q;
+                } else {
+                    s = *q;
+                }
                 src = (s >= 0 && s < a.rows_in) ? s : -1;
             }
             idx_lds[e] = src;
@@ -539,6 +580,42 @@ gather_gemm_lds_kernel(GemmArgs a) {
         idx_lds[e] = src;
     }
     __syncthreads();
+    if constexpr (SYNC) {
+        // A consumer waits for the producer tiles that wrote its source rows
+        // (rows [t * src_bm, (t + 1) * src_bm) of producer row tile t).
+        if (sync.src_flags) {
+            if (tid == 0) {
+                src_lo = INT_MAX;
+                src_hi = -1;
+            }
+            __syncthreads();
+            int lo = INT_MAX, hi = -1;
+            const int entries = (full_table ? a.noff : kcount) * BM;
+            for (int e = tid; e < entries; e += kThreads) {
+                const int src = idx_lds[e];
+                if (src >= 0) {
+                    lo = min(lo, src);
+                    hi = max(hi, src);
+                }
+            }
+            if (hi >= 0) {
+                atomicMin(&src_lo, lo);
+                atomicMax(&src_hi, hi);
+            }
+            __syncthreads();
+            if (src_hi >= 0) {
+                const int t0 = src_lo / sync.src_bm, t1 = src_hi / sync.src_bm;
+                const int count = (t1 - t0 + 1) * sync.src_tiles_n;
+                for (int i = tid; i < count; i += kThreads)
+                    spin_until(sync.src_flags + static_cast<int64_t>(t0) * sync.src_tiles_n + i, sync.gen,
+                               sync.error);
+            }
+            __syncthreads();
+        }
+    }
+    // Sources written in this launch are read with device-coherent loads.
+    bool coherent_x = false;
+    if constexpr (SYNC) coherent_x = sync.src_flags != nullptr;
 
     const int chunks = (a.cin + kChunk - 1) / kChunk;
     const int stages = kcount * chunks;
@@ -582,6 +659,8 @@ gather_gemm_lds_kernel(GemmArgs a) {
                 // lane 0 always issues (zero line when its row is absent)
                 const uint64_t lanes = __ballot(src[j] >= 0) | 1ull;
                 lds_dma16_masked(g, lds_offset(base + (wave * AI + j) * 8 * kChunkBytes), lanes);
+            } else if (SYNC && coherent_x) {
+                lds_dma16_coherent(g, lds_offset(base + (wave * AI + j) * 8 * kChunkBytes));
             } else {
                 lds_dma16(g, lds_offset(base + (wave * AI + j) * 8 * kChunkBytes));
             }
@@ -686,8 +765,14 @@ gather_gemm_lds_kernel(GemmArgs a) {
             if (s + NSTAGE - 1 < stages) issue(s + NSTAGE - 1);
         }
     }
+    // A producer of the chained launch stores device-coherently.
+    bool coherent_y = false;
+    if constexpr (SYNC) coherent_y = sync.done_flags != nullptr;
     if constexpr (KSPLIT == 1) {
-        gemm_epilogue<T, TI, TJ, WM, WN, EPI>(a, acc, p0, n0, wm, wn, h, r);
+        if (SYNC && coherent_y)
+            gemm_epilogue<T, TI, TJ, WM, WN, EPI, true>(a, acc, p0, n0, wm, wn, h, r);
+        else
+            gemm_epilogue<T, TI, TJ, WM, WN, EPI>(a, acc, p0, n0, wm, wn, h, r);
     } else {
         // Group 0 finishes the upper 32-row blocks of each wave's tile and
         // group 1 the lower ones; each hands the other half of its partial
@@ -718,12 +803,124 @@ gather_gemm_lds_kernel(GemmArgs a) {
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
                         fin[i][j][v] = acc[KEEP + i][j][v] + xch[slot(1 - kg, i, j, v)];
-            gemm_epilogue<T, HI, TJ, WM, WN, EPI>(a, fin, p0 + KEEP * 32, n0, wm, wn, h, r);
+            if (SYNC && coherent_y) {
+                // A producer of the chained launch stages its tile in LDS and
+                // writes whole 16-byte pieces device-coherently (2-byte
+                // write-through stores would each go to memory on their own).
+                if constexpr (EPI == kEpiStore && sizeof(T) == 2) {
+                    constexpr int kPitch = BN * 2 + 16;
+                    static_assert(BM * kPitch <= NSTAGE * kStageBytes, "staged tile fits the stages");
+                    barrier_no_fence();  // the partner's sums are read: the exchange area is free
+                    char * stage = smem;
+#pragma unroll
+                    for (int i = 0; i < HI; ++i)
+#pragma unroll
+                        for (int j = 0; j < TJ; ++j) {
+                            const int cl = wn * WN + j * 32 + r;
+                            const float b = (a.bias && n0 + cl < a.cout) ? a.bias[n0 + cl] : 0.0f;
+#pragma unroll
+                            for (int v = 0; v < 16; ++v) {
+                                const int rl = KEEP * 32 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                                *reinterpret_cast<uint16_t *>(stage + rl * kPitch + cl * 2) =
+                                    f32_to_bf16(fin[i][j][v] + b);
+                            }
+                        }
+                    barrier_no_fence();
+                    for (int q = tid; q < BM * (BN / 8); q += kThreads) {
+                        const int rl = q / (BN / 8), piece = q % (BN / 8);
+                        const int64_t row = p0 + rl;
+                        const int col = n0 + piece * 8;
+                        if (row < a.m && col < a.cout)
+                            store16_coherent(static_cast<T *>(a.y) + row * a.ldy + col,
+                                             *reinterpret_cast<const uint4 *>(stage + rl * kPitch + piece * 16));
+                    }
+                } else {
+                    gemm_epilogue<T, HI, TJ, WM, WN, EPI, true>(a, fin, p0 + KEEP * 32, n0, wm, wn, h, r);
+                }
+            } else {
+                gemm_epilogue<T, HI, TJ, WM, WN, EPI>(a, fin, p0 + KEEP * 32, n0, wm, wn, h, r);
+            }
         };
         barrier_no_fence();  // every wave is done reading the stage buffers
         if (kg == 0) finish(std::integral_constant<int, 0>{});
         else finish(std::integral_constant<int, HI>{});
     }
+    if constexpr (SYNC) {
+        // A producer publishes the tile: every thread's stores made visible
+        // to the device, then the tile's flag set to this launch's value.
+        if (sync.done_flags) {
+            release_stores();
+            __syncthreads();
+            if (tid == 0)
+                __hip_atomic_store(sync.done_flags + logical, sync.gen, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+template <typename T, int BM, int BN, int EPI, int NSTAGE, int NW, int WAVES_M, int KSPLIT>
+__global__ void __launch_bounds__(NW * 64)
+gather_gemm_lds_kernel(GemmArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    // Side workgroups last: dispatched in order, they take the slots the
+    // tiles' last, partial round leaves free.
+    const int tiles = static_cast<int>(gridDim.x) - a.side_blocks;
+    if (static_cast<int>(blockIdx.x) >= tiles) {
+        s2_emit_block(a.s2, blockIdx.x - tiles, threadIdx.x, NW * 64, smem);
+        return;
+    }
+    gemm_lds_tile<T, BM, BN, EPI, NSTAGE, NW, WAVES_M, KSPLIT, false>(
+        a, remap_xcd(blockIdx.x, tiles), TileSync{}, smem);
+}
+
+// One U-Net level in one launch (pxs_unet_s2_level): workgroups [0, tiles_a)
+// are SubMConv3d tiles (a), then `side` workgroups emit the stride-2
+// topology (a.s2), then tiles_b stride-2 convolution tiles (b), which read
+// the child map the emit writes and the rows conv a's tiles write.  Each
+// consumer waits only on its own producers (TileSync), so the strided conv's
+// tiles run in the slots conv a's last round leaves free.  tiles_a + side is
+// a multiple of 8, so every role keeps its XCD mapping.
+struct ChainArgs {
+    int tiles_a, side, tiles_b, tiles_n_a;
+    uint32_t * emit_flags;
+    uint32_t * a_flags;
+    uint32_t gen;
+    uint32_t * error;
+};
+
+template <typename T, int BM, int BN, int NSTAGE, int NW, int WAVES_M, int KSPLIT>
+__global__ void __launch_bounds__(NW * 64)
+gather_gemm_lds_chain_kernel(GemmArgs a, GemmArgs b, ChainArgs c) {
+    extern __shared__ __align__(16) char smem[];
+    const int bid = blockIdx.x;
+    if (bid < c.tiles_a) {
+        TileSync sync{};
+        sync.done_flags = c.a_flags;
+        sync.gen = c.gen;
+        sync.error = c.error;
+        gemm_lds_tile<T, BM, BN, kEpiStore, NSTAGE, NW, WAVES_M, KSPLIT, true>(
+            a, remap_xcd(bid, c.tiles_a), sync, smem);
+        return;
+    }
+    if (bid < c.tiles_a + c.side) {
+        s2_emit_block(a.s2, bid - c.tiles_a, threadIdx.x, NW * 64, smem);
+        release_stores();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(c.emit_flags + (bid - c.tiles_a), c.gen, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    TileSync sync{};
+    sync.emit_flags = c.emit_flags;
+    sync.emit_count = c.side;
+    sync.src_flags = c.a_flags;
+    sync.src_bm = BM;
+    sync.src_tiles_n = c.tiles_n_a;
+    sync.gen = c.gen;
+    sync.error = c.error;
+    gemm_lds_tile<T, BM, BN, kEpiStore, NSTAGE, NW, WAVES_M, KSPLIT, true>(
+        b, remap_xcd(bid - c.tiles_a - c.side, c.tiles_b), sync, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -741,7 +938,6 @@ gather_gemm_lds_kernel(GemmArgs a) {
 #ifndef PXS_GEMM_HALO
 #define PXS_GEMM_HALO 0
 #endif
-constexpr int kSideEmitWords = 32;  // bitmap words per emit side workgroup (1,024 cells)
 constexpr int kHaloBM = 128, kHaloBN = 128, kHaloMax = 576, kHaloNW = 8, kHaloWStages = 4;
 // Distinct sources are found with a byte map over the tile's source range
 // [lo, hi] (at most kHaloRange rows; wider tiles read their operands from
@@ -1223,6 +1419,35 @@ int launch_lds_tile(const GemmArgs & args, hipStream_t stream) {
     return check_launch("gather GEMM (LDS pipeline)");
 }
 
+// The chained level runs the default bf16 tile of both convolutions
+// (128 x 128, 2 stages, 8 waves in two K groups), the one dispatch picks for
+// them.
+int launch_unet_chain(const GemmArgs & a, const GemmArgs & b, ChainArgs c, hipStream_t stream) {
+    constexpr int BM = 128, BN = 128, NSTAGE = 2, NW = 8, WAVES_M = 2, KSPLIT = 2;
+    const int smem = lds_gemm_bytes<BM, BN, NSTAGE>(27);
+    static bool configured = false;
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(
+                &gather_gemm_lds_chain_kernel<uint16_t, BM, BN, NSTAGE, NW, WAVES_M, KSPLIT>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+        if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(gather_gemm_lds_chain)");
+        configured = true;
+    }
+    c.tiles_a = static_cast<int>((a.m + BM - 1) / BM) * ((a.cout + BN - 1) / BN);
+    c.tiles_n_a = (a.cout + BN - 1) / BN;
+    c.tiles_b = static_cast<int>((b.m + BM - 1) / BM) * ((b.cout + BN - 1) / BN);
+    c.side = a.s2.blocks;
+    while ((c.tiles_a + c.side) % 8 != 0) ++c.side;
+    const int64_t blocks = static_cast<int64_t>(c.tiles_a) + c.side + c.tiles_b;
+    if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "chained level: grid too large");
+    if (smem < s2_emit_lds_bytes(a.s2.words_per_block, NW * 64))
+        return fail(PXS_ERR_ARG, "chained level: side work needs more LDS than the tile");
+    hipLaunchKernelGGL((gather_gemm_lds_chain_kernel<uint16_t, BM, BN, NSTAGE, NW, WAVES_M, KSPLIT>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), smem, stream, a, b, c);
+    return check_launch("chained U-Net level");
+}
+
 template <typename T, int BM, int BN, int EPI>
 int launch_tile(const GemmArgs & args, hipStream_t stream) {
     constexpr int kStageBytes = (BM + BN) * kPitch;
@@ -1596,13 +1821,82 @@ int pxs_subm_conv3d_grid_s2_emit(int dtype, const void * x, const int32_t * coor
                       !PXS_GEMM_HALO;
     if (fuse) {
         a.s2 = make_s2_emit_args(batch_size, sx, sy, sz, grid, generation, out_coords, child_map,
-                                 ld_map, m_out, coarse_grid, s2_workspace, kSideEmitWords);
+                                 ld_map, m_out, coarse_grid, s2_workspace, kS2SideWords);
         a.side_blocks = a.s2.blocks;
         return run_gemm(dtype, a, kEpiStore, s);
     }
     if (int rc = run_gemm(dtype, a, kEpiStore, s)) return rc;
     return pxs_s2_tagged_emit(n, batch_size, sx, sy, sz, grid, generation, out_coords, child_map,
                               ld_map, m_out, coarse_grid, s2_workspace, stream);
+}
+
+int pxs_unet_s2_level(int dtype, const void * x, const int32_t * coords, int64_t n, int cin,
+                      const void * w_a, const float * b_a, int cout_a, int batch_size, int sx,
+                      int sy, int sz, const void * grid, uint32_t generation, void * y_a,
+                      const void * w_b, const float * b_b, int cout_b, int64_t m, void * y_b,
+                      int32_t * out_coords, int32_t * child_map, int64_t ld_map, int64_t * m_out,
+                      void * coarse_grid, void * s2_workspace, void * stream) {
+    const char * who = "pxs_unet_s2_level";
+    if (int rc = check_dtype(dtype, who)) return rc;
+    PXS_CHECK(n >= 0 && cin > 0 && cout_a > 0 && cout_b > 0 && m >= 0 && m <= n, PXS_ERR_ARG,
+              std::string(who) + ": bad shape");
+    PXS_CHECK(pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              std::string(who) + ": invalid extents");
+    PXS_CHECK(generation >= 1 && generation <= kVoxelTagMax, PXS_ERR_ARG,
+              std::string(who) + ": generation must be in 1..255");
+    PXS_CHECK(n < (int64_t{1} << kVoxelTagShift), PXS_ERR_ARG,
+              std::string(who) + ": bad row count (at most 2^24 - 1 rows)");
+    PXS_CHECK(ld_map >= n, PXS_ERR_ARG, std::string(who) + ": child map stride below the row count");
+    PXS_CHECK_WORKSPACE(s2_workspace, who);
+    PXS_CHECK(m_out && s2_workspace, PXS_ERR_ARG, std::string(who) + ": null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) return fill_i64(m_out, 1, 0, s);
+    PXS_CHECK(x && coords && w_a && grid && y_a && w_b && y_b && out_coords && child_map &&
+                  coarse_grid, PXS_ERR_ARG, std::string(who) + ": null pointer");
+    PXS_CHECK((reinterpret_cast<uintptr_t>(coords) & 15u) == 0, PXS_ERR_ARG,
+              std::string(who) + ": coordinates must be 16-byte aligned");
+    PXS_CHECK((reinterpret_cast<uintptr_t>(grid) & 3u) == 0, PXS_ERR_ARG,
+              std::string(who) + ": the grid must be 4-byte aligned");
+    // The chain runs both convolutions on the default bf16 tile, the one
+    // dispatch picks for a 27-offset gather of 65..128 outputs and an
+    // 8-offset gather of 16 K stages over more than 64 outputs.
+    constexpr bool kDefaultTile = PXS_GEMM_BM == 128 && PXS_GEMM_BN == 128 &&
+                                  PXS_GEMM_STAGES == 2 && PXS_GEMM_WAVES == 8 &&
+                                  PXS_GEMM_KSPLIT == 2 && !PXS_GEMM_HALO;
+    const bool chain = kDefaultTile && dtype == PXS_BF16 && cin % 8 == 0 && cout_a % 8 == 0 &&
+                       cout_a > 64 && cout_a <= 128 && cout_b > 64 && m > 0 && aligned16(x) &&
+                       aligned16(w_a) && aligned16(y_a) && aligned16(w_b);
+    if (!chain) {
+        if (int rc = pxs_subm_conv3d_grid_s2_emit(dtype, x, coords, n, cin, w_a, b_a, cout_a,
+                                                  batch_size, sx, sy, sz, grid, generation, y_a,
+                                                  out_coords, child_map, ld_map, m_out,
+                                                  coarse_grid, s2_workspace, stream))
+            return rc;
+        return pxs_sparse_conv3d_s2(dtype, y_a, n, cout_a, w_b, b_b, cout_b, child_map, ld_map, m,
+                                    y_b, stream);
+    }
+    GemmArgs a{};
+    a.x = x; a.rows_in = n; a.ldx = cin; a.cin = cin; a.w = w_a; a.bias = b_a;
+    a.cout = cout_a; a.m = n; a.rowmap = nullptr; a.ld_map = 0; a.noff = 27; a.masks = nullptr;
+    a.y = y_a; a.ldy = cout_a; a.act = PXS_ACT_NONE; a.coords = coords; a.vec_ok = 1;
+    a.grid = static_cast<const uint32_t *>(grid);
+    a.grid_b = batch_size; a.grid_x = sx; a.grid_y = sy; a.grid_z = sz; a.grid_gen = generation;
+    a.s2 = make_s2_emit_args(batch_size, sx, sy, sz, grid, generation, out_coords, child_map,
+                             ld_map, m_out, coarse_grid, s2_workspace, kS2SideWords);
+    a.s2.coherent_children = 1;  // read by the strided conv's tiles of the same launch
+    GemmArgs b{};
+    b.x = y_a; b.rows_in = n; b.ldx = cout_a; b.cin = cout_a; b.w = w_b; b.bias = b_b;
+    b.cout = cout_b; b.m = m; b.rowmap = child_map; b.ld_map = ld_map; b.noff = 8;
+    b.masks = nullptr; b.y = y_b; b.ldy = cout_b; b.act = PXS_ACT_NONE; b.vec_ok = 1;
+    const S2ChainFlags f = s2_chain_flags(s2_workspace, batch_size, sx, sy, sz);
+    ChainArgs c{};
+    c.emit_flags = f.emit;
+    c.a_flags = f.tiles;
+    c.gen = generation;
+    c.error = f.error;
+    PXS_CHECK((n + 127) / 128 <= f.tiles_cap && a.s2.blocks + 7 <= f.emit_cap, PXS_ERR_ARG,
+              std::string(who) + ": flag space exceeded");
+    return launch_unet_chain(a, b, c, s);
 }
 
 int pxs_sparse_conv3d_s2(int dtype, const void * x, int64_t n_in, int cin, const void * weight,

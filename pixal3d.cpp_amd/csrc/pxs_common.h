@@ -94,6 +94,25 @@ template <> __device__ __forceinline__ void store_f32<uint16_t>(uint16_t * p, fl
     *p = f32_to_bf16(v);
 }
 
+// Device-coherent stores (sc1): written through to the level every XCD reads
+// with device-coherent loads, for data that other workgroups of the same
+// launch consume.  A wave that has issued them waits with release_stores()
+// before the workgroup publishes a flag.
+template <typename T> __device__ __forceinline__ void store_f32_coherent(T * p, float v);
+template <> __device__ __forceinline__ void store_f32_coherent<float>(float * p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <> __device__ __forceinline__ void store_f32_coherent<uint16_t>(uint16_t * p, float v) {
+    const uint32_t bits = f32_to_bf16(v);
+    asm volatile("global_store_short %0, %1, off sc1" : : "v"(p), "v"(bits) : "memory");
+}
+__device__ __forceinline__ void store16_coherent(void * p, uint4 v) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 d = {v.x, v.y, v.z, v.w};
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(d) : "memory");
+}
+__device__ __forceinline__ void release_stores() { asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); }
+
 // ---- LDS DMA pipelines ----------------------------------------------------------
 // LDS byte offset of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_offset(const void * p) {
@@ -112,6 +131,17 @@ __device__ __forceinline__ uint32_t lds_offset(const void * p) {
 // written by the kernels that use it.
 __device__ __forceinline__ void lds_dma16(const void * g, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(g), "s"(lds_base)
+                 : "m0");
+}
+
+// lds_dma16 as a device-coherent load (sc1): it reads the level where data
+// that other workgroups of the same launch, on other XCDs, have released
+// (written back and flagged) is visible, instead of a line this XCD's L2 may
+// still hold from before.
+__device__ __forceinline__ void lds_dma16_coherent(const void * g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1"
                  :
                  : "v"(g), "s"(lds_base)
                  : "m0");

@@ -35,6 +35,7 @@ struct S2EmitArgs {
     int64_t * m_out;
     int blocks;                  // workgroups sharing the emit
     int words_per_block;         // a multiple of 4, at most the workgroup's thread count
+    int coherent_children;       // child map stored device-coherently (read in the same launch)
 };
 
 // The emit's arguments over a workspace of pxs_downsample_s2_tagged_workspace_bytes
@@ -44,6 +45,22 @@ S2EmitArgs make_s2_emit_args(int batch_size, int sx, int sy, int sz, const void 
                              uint32_t generation, int32_t * out_coords, int32_t * child_map,
                              int64_t ld_map, int64_t * m_out, void * coarse_grid,
                              void * s2_workspace, int words_per_block);
+
+// Bitmap words per emit workgroup when the emit rides in a convolution's
+// launch (1,024 cells: short workgroups that fill the launch's tail).
+constexpr int kS2SideWords = 32;
+
+// The flags of the chained U-Net level (pxs_unet_s2_level) in the same
+// workspace: one per emit workgroup and one per row tile of the first
+// convolution, each set to the generation when its results are visible.
+struct S2ChainFlags {
+    uint32_t * emit;
+    int64_t emit_cap;
+    uint32_t * tiles;
+    int64_t tiles_cap;
+    uint32_t * error;  // nonzero once a dependency wait gave up (cleared by the reset)
+};
+S2ChainFlags s2_chain_flags(void * s2_workspace, int batch_size, int sx, int sy, int sz);
 
 // Bytes of LDS s2_emit_block needs.
 constexpr int s2_emit_lds_bytes(int words_per_block, int threads) {
@@ -78,8 +95,15 @@ __device__ __forceinline__ void s2_emit_cell(const S2EmitArgs & e, int64_t cell,
             child[c] = voxel_grid_row(e.fine_grid[f], e.generation);
         }
     }
+    if (e.coherent_children) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) e.child_map[c * e.ld_map + rank] = child[c];
+        for (int c = 0; c < 8; ++c)
+            __hip_atomic_store(e.child_map + c * e.ld_map + rank, child[c], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) e.child_map[c * e.ld_map + rank] = child[c];
+    }
 }
 
 // Workgroup sb of e.blocks emits the cells of bitmap words [w0, w1),

@@ -469,6 +469,16 @@ __global__ void tagged_scatter_mark_kernel(const int4 * __restrict__ coords, int
 }
 
 constexpr int kEmitWords = 256;  // bitmap words per emit workgroup
+
+// Flag counts of the chained level: every emit workgroup of kS2SideWords
+// words (rounded up to 8, plus up to 7 more that align the next role to an
+// XCD boundary), and every 128-row tile of at most min(fine cells, 2^24 - 1)
+// rows.
+int64_t s2_emit_flag_cap(int64_t words) { return (words + kS2SideWords - 1) / kS2SideWords + 16; }
+int64_t s2_tile_flag_cap(int batch_size, int sx, int sy, int sz) {
+    const int64_t cells = static_cast<int64_t>(batch_size) * sx * sy * sz;
+    return (std::min<int64_t>(cells, kTagMaxRows) + 127) / 128 + 1;
+}
 __global__ void __launch_bounds__(kThreads) s2_emit_tagged_kernel(S2EmitArgs e) {
     __shared__ __align__(16) char lds[s2_emit_lds_bytes(kEmitWords, kThreads)];
     s2_emit_block(e, blockIdx.x, threadIdx.x, kThreads, lds);
@@ -1231,8 +1241,11 @@ size_t pxs_downsample_s2_tagged_workspace_bytes(int batch_size, int sx, int sy, 
     const int64_t blocks = (words + kWordBlock - 1) / kWordBlock;
     auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
     // bitmap, word prefixes, block totals; then the bitmap pair of the fused
-    // emit (pxs_s2_tagged_insert / pxs_subm_conv3d_grid_s2_emit)
-    return static_cast<size_t>(up(words * 4) + up(words * 4) + up(blocks * 4) + 2 * up(words * 4));
+    // emit (pxs_s2_tagged_insert / pxs_subm_conv3d_grid_s2_emit) and the flags
+    // of the chained level (pxs_unet_s2_level)
+    return static_cast<size_t>(up(words * 4) + up(words * 4) + up(blocks * 4) + 2 * up(words * 4) +
+                               up(s2_emit_flag_cap(words) * 4) +
+                               up(s2_tile_flag_cap(batch_size, sx, sy, sz) * 4) + 256);
 }
 
 }  // extern "C"
@@ -1267,6 +1280,23 @@ S2EmitArgs make_s2_emit_args(int batch_size, int sx, int sy, int sz, const void 
     // a multiple of 8, so that workgroups after the emit's keep their XCD
     e.blocks = static_cast<int>(((words + words_per_block - 1) / words_per_block + 7) / 8 * 8);
     return e;
+}
+
+S2ChainFlags s2_chain_flags(void * s2_workspace, int batch_size, int sx, int sy, int sz) {
+    const int64_t cells = static_cast<int64_t>(batch_size) * ((sx + 1) / 2) * ((sy + 1) / 2) *
+                          ((sz + 1) / 2);
+    const int64_t words = (cells + 31) / 32;
+    const int64_t blocks = (words + kWordBlock - 1) / kWordBlock;
+    auto up = [](int64_t b) { return (b + 255) / 256 * 256; };
+    char * base = static_cast<char *>(s2_workspace) + 2 * up(words * 4) + up(blocks * 4) +
+                  2 * up(words * 4);
+    S2ChainFlags f;
+    f.emit = reinterpret_cast<uint32_t *>(base);
+    f.emit_cap = s2_emit_flag_cap(words);
+    f.tiles = reinterpret_cast<uint32_t *>(base + up(f.emit_cap * 4));
+    f.tiles_cap = s2_tile_flag_cap(batch_size, sx, sy, sz);
+    f.error = reinterpret_cast<uint32_t *>(base + up(f.emit_cap * 4) + up(f.tiles_cap * 4));
+    return f;
 }
 }  // namespace pxs
 
@@ -1368,6 +1398,17 @@ int pxs_s2_tagged_emit(int64_t n, int batch_size, int sx, int sy, int sz, const 
     hipLaunchKernelGGL(s2_emit_tagged_kernel, dim3(static_cast<unsigned>(e.blocks)), dim3(kThreads),
                        0, s, e);
     return check_launch("pxs_s2_tagged_emit");
+}
+
+int pxs_unet_s2_level_error(const void * s2_workspace, int batch_size, int sx, int sy, int sz,
+                            uint32_t * error_out, void * stream) {
+    PXS_CHECK(pxs_downsample_s2_tagged_workspace_bytes(batch_size, sx, sy, sz) > 0, PXS_ERR_ARG,
+              "pxs_unet_s2_level_error: invalid extents");
+    PXS_CHECK(s2_workspace && error_out, PXS_ERR_ARG, "pxs_unet_s2_level_error: null pointer");
+    const S2ChainFlags f = s2_chain_flags(const_cast<void *>(s2_workspace), batch_size, sx, sy, sz);
+    return check_hip(hipMemcpyAsync(error_out, f.error, sizeof(uint32_t), hipMemcpyDefault,
+                                    as_stream(stream)),
+                     "pxs_unet_s2_level_error");
 }
 
 int pxs_map_s2_topology_tagged(const int32_t * coords, int64_t n, int batch_size, int sx, int sy,

@@ -122,6 +122,10 @@ _SIGS = {
                                             _i64, _vp, _vp, _vp, _vp]),
     "pxs_s2_tagged_emit": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, C.c_uint32, _vp, _vp, _i64,
                                   _vp, _vp, _vp, _vp]),
+    "pxs_unet_s2_level": (_i32, [_i32, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _i32,
+                                 _i32, _vp, C.c_uint32, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp,
+                                 _i64, _vp, _vp, _vp, _vp]),
+    "pxs_unet_s2_level_error": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "pxs_voxel_grid_build": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
     "pxs_neighbor_map_k3_grid": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "pxs_convnext_block_workspace_bytes": (C.c_size_t, [_i32, _i64, _i32, _i32, _i32]),
@@ -582,6 +586,27 @@ class Pxs:
                                                 _ptr(coarse_grid), _ptr(workspace),
                                                 self.stream()), "pxs_s2_tagged_emit")
         return oc, child, m
+
+    def unet_s2_level(self, x, w_a, b_a, w_b, b_b, coords, batch_size, shape, grid, generation,
+                      m, coarse_grid, workspace):
+        """pxs_unet_s2_level -> (y_a, y_b [m rows], out_coords, child_map, m_out device int64)."""
+        n, cin = x.shape
+        cout_a, cout_b = w_a.shape[1], w_b.shape[1]
+        y_a = torch.empty((n, cout_a), dtype=x.dtype, device=x.device)
+        y_b = torch.empty((max(m, 1), cout_b), dtype=x.dtype, device=x.device)
+        oc, child, m_out = self._s2_outputs(n, x.device)
+        self._check(self.lib.pxs_unet_s2_level(
+            _dtype_code(x), _ptr(x), _ptr(coords), n, cin, _ptr(w_a), _ptr(b_a), cout_a,
+            batch_size, *shape, _ptr(grid), generation, _ptr(y_a), _ptr(w_b), _ptr(b_b), cout_b,
+            m, _ptr(y_b), _ptr(oc), _ptr(child), child.shape[1], _ptr(m_out), _ptr(coarse_grid),
+            _ptr(workspace), self.stream()), "pxs_unet_s2_level")
+        return y_a, y_b[:m], oc, child, m_out
+
+    def unet_s2_level_error(self, workspace, batch_size, shape):
+        err = torch.zeros(1, dtype=torch.int32, device=workspace.device)
+        self._check(self.lib.pxs_unet_s2_level_error(_ptr(workspace), batch_size, *shape, _ptr(err),
+                                                     self.stream()), "pxs_unet_s2_level_error")
+        return int(err.item())
 
     def sparse_conv3d_s2(self, x, weight, bias, child_map, m, out=None):
         n, cin = x.shape

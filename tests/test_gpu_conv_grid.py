@@ -263,3 +263,63 @@ def test_s2_emit_rejects_bad_arguments(px):
             torch.zeros(1, dtype=torch.int64, device=c.device))
     with pytest.raises(pxs.PxsError, match="child map stride below the row count"):
         px.subm_conv3d_grid_s2_emit(x, w, None, c, 1, (4, 4, 4), grid, 1, cg, ws, s2_out=outs)
+
+
+LEVEL_CASES = [
+    # (name, coords builder, batch, extents, cin, cout_a, cout_b, dtype): chained when bf16
+    # with 65..128 SubMConv3d outputs and more than 64 strided outputs
+    ("unet_bf16", lambda: W.unet_stage_128()["coords"], 2, (128, 128, 128), 128, 128, 256, "bf16"),
+    ("box_bf16", lambda: _box_coords(13, 2, (40, 22, 30), 0.3), 2, (40, 22, 30), 32, 96, 72, "bf16"),
+    ("box_bf16_unchained", lambda: _box_coords(14, 1, (9, 7, 11), 0.5), 1, (9, 7, 11), 16, 64, 32,
+     "bf16"),
+    ("box_f32", lambda: _box_coords(15, 1, (9, 7, 11), 0.5), 1, (9, 7, 11), 16, 24, 40, "f32"),
+]
+
+
+@pytest.mark.parametrize("name,make,batch,shape,cin,cout_a,cout_b,dtype", LEVEL_CASES,
+                         ids=[c[0] for c in LEVEL_CASES])
+def test_unet_s2_level_matches_two_calls(px, name, make, batch, shape, cin, cout_a, cout_b,
+                                         dtype):
+    """pxs_unet_s2_level (the strided conv's tiles waiting inside the launch
+    for the emit and the SubMConv3d tiles they read) against
+    pxs_subm_conv3d_grid_s2_emit then pxs_sparse_conv3d_s2: both convolutions,
+    the coarse coordinates, child slots, count and coarse grid bit-equal, and
+    no dependency wait given up; three successive generations on one grid and
+    workspace, the second over a subset of the rows."""
+    import torch
+    full = make()
+    rng = np.random.default_rng(len(full) + cout_b)
+    subset = full[np.sort(rng.choice(len(full), len(full) // 3, replace=False))]
+    cx, cy, cz = [(s + 1) // 2 for s in shape]
+    cells = px.lib.pxs_voxel_grid_bytes(batch, cx, cy, cz) // 4
+    dev = torch.device("cuda")
+    tg_ref, ws_ref = px.tagged_grid(batch, shape), px.s2_tagged_workspace(batch, shape)
+    tg, ws = px.tagged_grid(batch, shape), px.s2_tagged_workspace(batch, shape)
+    for gen, coords in ((1, full), (2, subset), (3, full)):
+        n = len(coords)
+        c = ti32(coords)
+        xr = rng.standard_normal((n, cin)).astype(np.float32)
+        war = (rng.standard_normal((27, cout_a, cin)) * (2.0 / (27 * cin)) ** 0.5).astype(np.float32)
+        wbr = (rng.standard_normal((8, cout_b, cout_a)) * (2.0 / (8 * cout_a)) ** 0.5).astype(np.float32)
+        cast = tbf if dtype == "bf16" else t32
+        x, wa, wb = cast(xr), cast(war), cast(wbr)
+        ba = t32((rng.standard_normal(cout_a) * 0.1).astype(np.float32))
+        bb = t32((rng.standard_normal(cout_b) * 0.1).astype(np.float32))
+        cg_ref = torch.full((cells,), 3, dtype=torch.int32, device=dev)
+        px.s2_tagged_insert(c, batch, shape, tg_ref, gen, ws_ref)
+        ya_ref, oc_ref, child_ref, m_ref = px.subm_conv3d_grid_s2_emit(
+            x, wa, ba, c, batch, shape, tg_ref, gen, cg_ref, ws_ref)
+        m = int(m_ref.item())
+        yb_ref = px.sparse_conv3d_s2(ya_ref, wb, bb, child_ref, m)
+        print(f"[unet s2 level] {name} gen={gen} n={n} m={m}", flush=True)
+        cg = torch.full((cells,), 4, dtype=torch.int32, device=dev)
+        px.s2_tagged_insert(c, batch, shape, tg, gen, ws)
+        ya, yb, oc, child, m_out = px.unet_s2_level(x, wa, ba, wb, bb, c, batch, shape, tg, gen,
+                                                    m, cg, ws)
+        assert px.unet_s2_level_error(ws, batch, shape) == 0
+        assert int(m_out.item()) == m
+        np.testing.assert_array_equal(_bits(ya), _bits(ya_ref))
+        np.testing.assert_array_equal(_bits(yb), _bits(yb_ref))
+        np.testing.assert_array_equal(oc[:m].cpu().numpy(), oc_ref[:m].cpu().numpy())
+        np.testing.assert_array_equal(child[:, :m].cpu().numpy(), child_ref[:, :m].cpu().numpy())
+        np.testing.assert_array_equal(cg.cpu().numpy(), cg_ref.cpu().numpy())
