@@ -1177,16 +1177,18 @@ def decoder(args, torch, px, W):
 
 
 def hash_map_128(args, torch, px, W):
-    """The hash path of the neighbour map on the U-Net stage's coordinates
-    (162,263 voxels at 128^3, batch 2): open-addressing voxel hash build
-    (pxs_voxel_hash_build: table init + insert) and the 3x3x3 map over it
-    (pxs_neighbor_map_k3: mask fill + lookups), the path for coordinates
-    without known extents.  Also one 256 MiB device copy, the plain-copy
-    reference for the FETCH_SIZE / WRITE_SIZE counters."""
+    """The extent-free paths of the neighbour map on the U-Net stage's
+    coordinates (162,263 voxels at 128^3, batch 2): the brick table
+    (pxs_voxel_bricks_build + pxs_neighbor_map_k3_bricks, the decoder's path)
+    and the voxel hash (pxs_voxel_hash_build + pxs_neighbor_map_k3).  Rates
+    count the map's compulsory bytes: 16 B of coordinates read and 27 x 4 B of
+    map + a 4 B mask written per row.  Also one 256 MiB device copy, the
+    plain-copy reference for the FETCH_SIZE / WRITE_SIZE counters."""
     dev = torch.device("cuda:0")
     coords = torch.from_numpy(W.unet_stage_128()["coords"]).to(dev)
     n = coords.shape[0]
     table = torch.empty(px.lib.pxs_voxel_hash_bytes(n), dtype=torch.uint8, device=dev)
+    bricks = torch.empty(px.lib.pxs_voxel_bricks_bytes(n), dtype=torch.uint8, device=dev)
     nbr = torch.empty((27, n), dtype=torch.int32, device=dev)
     masks = torch.empty(n, dtype=torch.int32, device=dev)
     timer = Timer(torch)
@@ -1197,35 +1199,42 @@ def hash_map_128(args, torch, px, W):
     import ctypes as C
 
     lib = px.lib
+    P = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
 
     def step():
         s = px.stream()
+        timer.run("bricks_build", lambda: px._check(lib.pxs_voxel_bricks_build(
+            P(coords), n, P(bricks), s), "pxs_voxel_bricks_build"))
+        timer.run("neighbor_map_bricks", lambda: px._check(lib.pxs_neighbor_map_k3_bricks(
+            P(coords), n, P(bricks), P(nbr), P(masks), s), "pxs_neighbor_map_k3_bricks"))
         timer.run("hash_build", lambda: px._check(lib.pxs_voxel_hash_build(
-            C.c_void_p(coords.data_ptr()), n, C.c_void_p(table.data_ptr()), s),
-            "pxs_voxel_hash_build"))
+            P(coords), n, P(table), s), "pxs_voxel_hash_build"))
         timer.run("neighbor_map", lambda: px._check(lib.pxs_neighbor_map_k3(
-            C.c_void_p(coords.data_ptr()), n, C.c_void_p(table.data_ptr()),
-            C.c_void_p(nbr.data_ptr()), C.c_void_p(masks.data_ptr()), s), "pxs_neighbor_map_k3"))
+            P(coords), n, P(table), P(nbr), P(masks), s), "pxs_neighbor_map_k3"))
 
     dt = timed_steps(args, torch, step, timer)
-    hb, nm = timer.mean_ms("hash_build"), timer.mean_ms("neighbor_map")
-    slots = px.lib.pxs_voxel_hash_bytes(n)
-    # algorithmic bytes: build = slot init (table bytes) + coords 16 B/row + one
-    # 16-byte slot written per row; map = coords 16 B/row, 27 slot probes of
-    # 16 B (at least one each), 27 int32 out + a mask per row
-    b_build = slots + n * (16 + 16)
-    b_map = n * (16 + 27 * 16 + 27 * 4 + 4)
-    return {"metric": "voxel hash + neighbour map GB/s (algorithmic bytes)",
-            "value": round((b_build + b_map) / dt / 1e9, 1), "unit": "GB/s",
+    ms = {k: timer.mean_ms(k) for k in ("bricks_build", "neighbor_map_bricks", "hash_build",
+                                        "neighbor_map")}
+    compulsory = n * (16 + 27 * 4 + 4)
+    gbs = lambda b, t: round(b / (t * 1e-3) / 1e9, 1)  # noqa: E731
+    brick_ms = ms["bricks_build"] + ms["neighbor_map_bricks"]
+    return {"metric": "neighbour map GB/s (compulsory bytes), brick table",
+            "value": gbs(compulsory, brick_ms), "unit": "GB/s",
             "ms_per_step": round(dt * 1e3, 4), "dtype": "int32",
-            "config": {"workload": f"hash_map_128: {n} voxels at 128^3 (batch 2), hash build + 3x3x3 map",
-                       "hash_build_ms": round(hb, 4), "neighbor_map_ms": round(nm, 4),
-                       "hash_build_gbs": round(b_build / (hb * 1e-3) / 1e9, 1),
-                       "neighbor_map_gbs": round(b_map / (nm * 1e-3) / 1e9, 1),
-                       "table_bytes": slots},
-            "roofline": {"bound": "hbm", "kernel": "neighbor_map",
-                         "achieved": round(b_map / (nm * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(b_map / (nm * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "config": {"workload": f"hash_map_128: {n} voxels at 128^3 (batch 2), brick table "
+                                   "and voxel hash builds + 3x3x3 maps",
+                       "compulsory_bytes_per_row": 16 + 27 * 4 + 4,
+                       "per_op_ms": {k: round(v, 4) for k, v in ms.items()},
+                       "bricks_build_plus_map_ms": round(brick_ms, 4),
+                       "hash_build_plus_map_ms": round(ms["hash_build"] + ms["neighbor_map"], 4),
+                       "neighbor_map_bricks_gbs": gbs(compulsory, ms["neighbor_map_bricks"]),
+                       "neighbor_map_hash_gbs": gbs(compulsory, ms["neighbor_map"]),
+                       "table_bytes": {"bricks": bricks.numel(), "hash": table.numel()}},
+            "roofline": {"bound": "hbm", "kernel": "neighbor_map_bricks",
+                         "achieved": gbs(compulsory, ms["neighbor_map_bricks"]),
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(compulsory / (ms["neighbor_map_bricks"] * 1e-3) / 1e9
+                                       / PEAK_HBM_GBS, 4),
                          "traffic": None}}
 
 

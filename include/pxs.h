@@ -109,6 +109,20 @@ int pxs_value_stats_f32(const float * x, int64_t count, pxs_value_stats * stats,
 int pxs_neighbor_map_k3(const int32_t * coords, int64_t n, const void * table, int32_t * nbr,
                         uint32_t * masks, void * stream);
 
+/* The same map from a locality-preserving table (the extent-free
+ * alternative to the voxel grid): a hash of 4x4x4 bricks, each owning 64
+ * entries of a pool that hold the smallest row at each voxel, so a row's 27
+ * neighbours come from the few bricks (3.4 on average) its window touches
+ * instead of 27 unrelated hash lines.  pxs_voxel_bricks_bytes(n) bytes
+ * (16-byte aligned): the hash of the voxel-hash size plus 256 bytes per row
+ * for the worst case of one brick per row.  Outputs identical to
+ * pxs_voxel_hash_build + pxs_neighbor_map_k3 (the same map the reference
+ * builds per convolution, src/slat_decoder.cpp:609-668). */
+size_t pxs_voxel_bricks_bytes(int64_t n);
+int pxs_voxel_bricks_build(const int32_t * coords, int64_t n, void * table, void * stream);
+int pxs_neighbor_map_k3_bricks(const int32_t * coords, int64_t n, const void * table, int32_t * nbr,
+                               uint32_t * masks, void * stream);
+
 /* Dense voxel grid: one int32 cell per (b, x, y, z) of the extents
  * [batch_size, sx, sy, sz] (batch_size * sx * sy * sz * 4 bytes; 0 when the
  * extents are invalid) holding the smallest row with that coordinate.  Rows

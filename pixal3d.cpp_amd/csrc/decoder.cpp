@@ -26,15 +26,18 @@ struct MapBuffers {
 MapBuffers carve_map(Carver & c, int64_t rows) {
     const size_t r = static_cast<size_t>(std::max<int64_t>(rows, 1));
     MapBuffers m;
-    m.table = c.take(pxs_voxel_hash_bytes(rows));
+    m.table = c.take(pxs_voxel_bricks_bytes(rows));
     m.nbr = static_cast<int32_t *>(c.take(27 * r * 4));
     m.masks = static_cast<uint32_t *>(c.take(r * 4));
     return m;
 }
 
+// The level's map from the brick table: the decoder's levels reach 1024^3,
+// where a dense grid would be gigabytes, and the voxel hash puts a row's 27
+// neighbours in 27 unrelated lines.
 int build_map(const int32_t * coords, int64_t rows, const MapBuffers & m, void * stream) {
-    PXS_TRY(pxs_voxel_hash_build(coords, rows, m.table, stream));
-    return pxs_neighbor_map_k3(coords, rows, m.table, m.nbr, m.masks, stream);
+    PXS_TRY(pxs_voxel_bricks_build(coords, rows, m.table, stream));
+    return pxs_neighbor_map_k3_bricks(coords, rows, m.table, m.nbr, m.masks, stream);
 }
 
 struct ConvNextBuffers {

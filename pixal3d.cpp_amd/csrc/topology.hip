@@ -90,7 +90,10 @@ __device__ __forceinline__ int32_t hash_find(const HashSlot * __restrict__ slots
     return probe_from(slots, mask, key, slot, load_slot(slots, slot));
 }
 
-__global__ void hash_init_kernel(HashSlot * slots, int64_t cap) {
+__global__ void hash_init_kernel(HashSlot * slots, int64_t cap, int32_t * counters = nullptr,
+                                 int ncounters = 0) {
+    // (counters: the brick table's, zeroed in the same launch)
+    if (counters && blockIdx.x == 0 && static_cast<int>(threadIdx.x) < ncounters) counters[threadIdx.x] = 0;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < cap;
          i += stride) {
@@ -199,6 +202,172 @@ neighbor_map_kernel(const int4 * __restrict__ coords, int64_t n,
         nbr[static_cast<int64_t>(k) * n + p] = row >= 0 ? row : static_cast<int32_t>(n);
     }
     if (masks && present) atomicOr(masks + p, present);
+}
+
+// ---- voxel bricks: a locality-preserving hash --------------------------------------
+// The voxel hash puts the 27 neighbours of a row in 27 unrelated 128-byte
+// lines.  Here the hash holds 4x4x4 bricks: a slot keys brick (b, x>>2,
+// y>>2, z>>2) to its id, and brick id owns 64 consecutive int32 entries of a
+// pool, entry ((x&3)*4 + (y&3))*4 + (z&3) holding the row at that voxel (the
+// smallest, as in the voxel hash) or INT_MAX.  A row's 3x3x3 neighbourhood
+// spans 1..8 bricks (3.4 on average), found with as many probes, and its 27
+// entries sit in those bricks' 256 bytes, shared with the rows around it.
+// Brick ids come from kBrickCounters counters: wavefront w (64 rows) takes
+// its new bricks' ids from counter w % kBrickCounters, which owns the ids
+// [k * per, (k + 1) * per), per = 64 * ceil(waves / kBrickCounters), enough
+// for every brick of its wavefronts.  So no single counter serialises the
+// claims.  Layout of the table: hash slots (hash_capacity(n), as the voxel
+// hash), then the pool (kBrickCounters * per bricks of 256 bytes, about one
+// per row, the worst case), then the counters.
+constexpr int kBrickShift = 2;
+constexpr int kBrickCells = 64;
+constexpr int kBrickCounters = 64;
+
+int64_t bricks_per_counter(int64_t n) {
+    const int64_t waves = (std::max<int64_t>(n, 1) + 63) / 64;
+    return 64 * ((waves + kBrickCounters - 1) / kBrickCounters);
+}
+
+struct BrickView {
+    HashSlot * slots;
+    uint64_t mask;
+    int32_t * pool;
+    int32_t * counters;
+    int32_t per;
+};
+
+BrickView brick_view(void * table, int64_t n) {
+    BrickView v;
+    const int64_t cap = hash_capacity(n);
+    v.slots = static_cast<HashSlot *>(table);
+    v.mask = static_cast<uint64_t>(cap - 1);
+    v.pool = reinterpret_cast<int32_t *>(static_cast<char *>(table) + cap * sizeof(HashSlot));
+    v.per = static_cast<int32_t>(bricks_per_counter(n));
+    v.counters = v.pool + static_cast<int64_t>(kBrickCounters) * v.per * kBrickCells;
+    return v;
+}
+
+__device__ __forceinline__ uint64_t brick_key(int b, int x, int y, int z) {
+    return voxel_key(b, x >> kBrickShift, y >> kBrickShift, z >> kBrickShift);
+}
+__device__ __forceinline__ int brick_local(int x, int y, int z) {
+    return ((x & 3) * 4 + (y & 3)) * 4 + (z & 3);
+}
+
+// Claim each brick once: every lane whose key differs from the lane before
+// it (sorted rows repeat a brick in runs) inserts it, all at once, with a
+// plain load first (a key already there never changes, so seeing it skips
+// the compare-and-swap); the lanes that won a new slot take consecutive ids
+// from one add per wavefront on the wavefront's counter, and fill their
+// brick's 64 pool entries with INT_MAX.
+__global__ void brick_claim_kernel(const int4 * __restrict__ coords, int64_t n, HashSlot * slots,
+                                   uint64_t mask, int32_t * __restrict__ pool,
+                                   int32_t * __restrict__ counters, int32_t per) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const bool live = p < n;
+    uint64_t key = kEmptyKey;
+    if (live) {
+        const int4 c = coords[p];
+        key = brick_key(c.x, c.y, c.z, c.w);
+    }
+    const uint64_t before = __shfl_up(key, 1, 64);
+    bool won = false;
+    uint64_t slot = 0;
+    if (live && (lane == 0 || before != key)) {
+        slot = home_slot(key, mask);
+        for (uint64_t probe = 0; probe <= mask; ++probe) {
+            const unsigned long long seen = slots[slot].key;
+            if (seen == key) break;
+            if (seen == kEmptyKey) {
+                const unsigned long long prev =
+                    atomicCAS(&slots[slot].key, static_cast<unsigned long long>(kEmptyKey),
+                              static_cast<unsigned long long>(key));
+                if (prev == kEmptyKey) {
+                    won = true;
+                    break;
+                }
+                if (prev == key) break;
+            }
+            slot = (slot + 1) & mask;
+        }
+    }
+    const uint64_t winners = __ballot(won);
+    if (winners == 0) return;
+    const int leader = __ffsll(static_cast<unsigned long long>(winners)) - 1;
+    const int k = static_cast<int>((p >> 6) % kBrickCounters);
+    int32_t base = 0;
+    if (lane == leader) base = k * per + atomicAdd(counters + k, __popcll(winners));
+    base = __shfl(base, leader, 64);
+    if (!won) return;
+    const int32_t id = base + __popcll(winners & ((1ull << lane) - 1ull));
+    slots[slot].val = id;
+    uint4 * b = reinterpret_cast<uint4 *>(pool + static_cast<int64_t>(id) * kBrickCells);
+#pragma unroll
+    for (int i = 0; i < kBrickCells / 4; ++i) b[i] = make_uint4(INT_MAX, INT_MAX, INT_MAX, INT_MAX);
+}
+
+// Each row into its brick's entry (the smallest row when coordinates repeat).
+__global__ void brick_place_kernel(const int4 * __restrict__ coords, int64_t n,
+                                   const HashSlot * __restrict__ slots, uint64_t mask,
+                                   int32_t * __restrict__ pool) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    const int32_t id = hash_find(slots, mask, brick_key(c.x, c.y, c.z, c.w));
+    if (id < 0) return;
+    atomicMin(pool + static_cast<int64_t>(id) * kBrickCells + brick_local(c.y, c.z, c.w),
+              static_cast<int32_t>(p));
+}
+
+// One thread per row: the ids of the (up to 8) bricks its 3x3x3 window
+// touches, then its 27 entries; the same map and masks as neighbor_map_kernel
+// (masks written, not ORed).
+__global__ void __launch_bounds__(kThreads)
+neighbor_map_bricks_kernel(const int4 * __restrict__ coords, int64_t n,
+                           const HashSlot * __restrict__ slots, uint64_t mask,
+                           const int32_t * __restrict__ pool, int32_t * __restrict__ nbr,
+                           uint32_t * __restrict__ masks) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int4 c = coords[p];
+    // per axis: the window's first brick and whether it spans a second one
+    const int bx = (c.y - 1) >> kBrickShift, by = (c.z - 1) >> kBrickShift, bz = (c.w - 1) >> kBrickShift;
+    const int nx = ((c.y + 1) >> kBrickShift) - bx, ny = ((c.z + 1) >> kBrickShift) - by,
+              nz = ((c.w + 1) >> kBrickShift) - bz;
+    int32_t id[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int ix = q >> 2, iy = (q >> 1) & 1, iz = q & 1;
+        const int X = bx + ix, Y = by + iy, Z = bz + iz;
+        id[q] = -1;
+        if (ix <= nx && iy <= ny && iz <= nz && X >= 0 && Y >= 0 && Z >= 0)
+            id[q] = hash_find(slots, mask, voxel_key(c.x, X, Y, Z));
+    }
+    uint32_t present = 0;
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+        const int x = c.y + k / 9 - 1, y = c.z + (k / 3) % 3 - 1, z = c.w + k % 3 - 1;
+        int32_t row = -1;
+        if (k == 13) {
+            row = static_cast<int32_t>(p);
+        } else {
+            // id[q] by selects on q's bits, so the ids stay in registers
+            const int qx = (x >> kBrickShift) - bx, qy = (y >> kBrickShift) - by,
+                      qz = (z >> kBrickShift) - bz;
+            const int32_t l0 = qz ? id[1] : id[0], l1 = qz ? id[3] : id[2];
+            const int32_t l2 = qz ? id[5] : id[4], l3 = qz ? id[7] : id[6];
+            const int32_t m0 = qy ? l1 : l0, m1 = qy ? l3 : l2;
+            const int32_t b = qx ? m1 : m0;
+            if (b >= 0) {
+                const int32_t v = pool[static_cast<int64_t>(b) * kBrickCells + brick_local(x, y, z)];
+                if (v != INT_MAX) row = v;
+            }
+        }
+        if (row >= 0) present |= 1u << k;
+        nbr[static_cast<int64_t>(k) * n + p] = row >= 0 ? row : static_cast<int32_t>(n);
+    }
+    if (masks) masks[p] = present;
 }
 
 // ---- dense voxel grid -----------------------------------------------------------
@@ -972,7 +1141,7 @@ int pxs_voxel_hash_build(const int32_t * coords, int64_t n, void * table, void *
     const int64_t cap = static_cast<int64_t>(h.mask) + 1;
     hipStream_t s = as_stream(stream);
     hipLaunchKernelGGL(hash_init_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((cap + 255) / 256, 8192))),
-                       dim3(256), 0, s, h.slots, cap);
+                       dim3(256), 0, s, h.slots, cap, nullptr, 0);
     if (n > 0) {
         hipLaunchKernelGGL(hash_insert_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
                            reinterpret_cast<const int4 *>(coords), n, h.slots, h.mask);
@@ -1044,6 +1213,47 @@ int pxs_neighbor_map_k3(const int32_t * coords, int64_t n, const void * table, i
     hipLaunchKernelGGL(neighbor_map_kernel, dim3(grid_for(3 * n, kThreads)), dim3(kThreads), 0, s,
                        reinterpret_cast<const int4 *>(coords), n, h.slots, h.mask, nbr, masks);
     return check_launch("pxs_neighbor_map_k3");
+}
+
+size_t pxs_voxel_bricks_bytes(int64_t n) {
+    if (n < 0) return 0;
+    return static_cast<size_t>(hash_capacity(n)) * sizeof(HashSlot) +
+           static_cast<size_t>(kBrickCounters) * bricks_per_counter(n) * kBrickCells *
+               sizeof(int32_t) +
+           kBrickCounters * sizeof(int32_t);
+}
+
+int pxs_voxel_bricks_build(const int32_t * coords, int64_t n, void * table, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_voxel_bricks_build: bad row count");
+    PXS_CHECK(table != nullptr, PXS_ERR_ARG, "pxs_voxel_bricks_build: null table");
+    PXS_CHECK(n == 0 || coords != nullptr, PXS_ERR_ARG, "pxs_voxel_bricks_build: null coords");
+    PXS_CHECK((reinterpret_cast<uintptr_t>(table) & 15u) == 0, PXS_ERR_ARG,
+              "pxs_voxel_bricks_build: the table must be 16-byte aligned");
+    const BrickView v = brick_view(table, n);
+    const int64_t cap = static_cast<int64_t>(v.mask) + 1;
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(hash_init_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((cap + 255) / 256, 8192))),
+                       dim3(256), 0, s, v.slots, cap, v.counters, kBrickCounters);
+    if (n > 0) {
+        const int4 * c4 = reinterpret_cast<const int4 *>(coords);
+        hipLaunchKernelGGL(brick_claim_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                           c4, n, v.slots, v.mask, v.pool, v.counters, v.per);
+        hipLaunchKernelGGL(brick_place_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, s,
+                           c4, n, v.slots, v.mask, v.pool);
+    }
+    return check_launch("pxs_voxel_bricks_build");
+}
+
+int pxs_neighbor_map_k3_bricks(const int32_t * coords, int64_t n, const void * table, int32_t * nbr,
+                               uint32_t * masks, void * stream) {
+    PXS_CHECK(n >= 0 && n <= INT_MAX, PXS_ERR_ARG, "pxs_neighbor_map_k3_bricks: bad row count");
+    if (n == 0) return PXS_OK;
+    PXS_CHECK(coords && table && nbr, PXS_ERR_ARG, "pxs_neighbor_map_k3_bricks: null pointer");
+    const BrickView v = brick_view(const_cast<void *>(table), n);
+    hipLaunchKernelGGL(neighbor_map_bricks_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+                       as_stream(stream), reinterpret_cast<const int4 *>(coords), n, v.slots,
+                       v.mask, v.pool, nbr, masks);
+    return check_launch("pxs_neighbor_map_k3_bricks");
 }
 
 size_t pxs_voxel_grid_bytes(int batch_size, int sx, int sy, int sz) {

@@ -126,6 +126,9 @@ _SIGS = {
                                  _i32, _vp, C.c_uint32, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp,
                                  _i64, _vp, _vp, _vp, _vp]),
     "pxs_unet_s2_level_error": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "pxs_voxel_bricks_bytes": (C.c_size_t, [_i64]),
+    "pxs_voxel_bricks_build": (_i32, [_vp, _i64, _vp, _vp]),
+    "pxs_neighbor_map_k3_bricks": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp]),
     "pxs_voxel_grid_build": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
     "pxs_neighbor_map_k3_grid": (_i32, [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "pxs_convnext_block_workspace_bytes": (C.c_size_t, [_i32, _i64, _i32, _i32, _i32]),
@@ -337,6 +340,20 @@ class Pxs:
                                                  _ptr(masks), self.stream()),
                     "pxs_neighbor_map_k3")
         return nbr, masks
+
+    def neighbor_map_bricks(self, coords, want_masks=True):
+        """pxs_voxel_bricks_build + pxs_neighbor_map_k3_bricks -> (nbr [27, n], masks [n])."""
+        n = coords.shape[0]
+        table = self._ws(self.lib.pxs_voxel_bricks_bytes(n), coords.device)
+        self._check(self.lib.pxs_voxel_bricks_build(_ptr(coords), n, _ptr(table), self.stream()),
+                    "pxs_voxel_bricks_build")
+        nbr = torch.empty((27, max(n, 1)), dtype=torch.int32, device=coords.device)
+        masks = torch.empty(max(n, 1), dtype=torch.int32, device=coords.device) if want_masks \
+            else None
+        self._check(self.lib.pxs_neighbor_map_k3_bricks(_ptr(coords), n, _ptr(table), _ptr(nbr),
+                                                        _ptr(masks), self.stream()),
+                    "pxs_neighbor_map_k3_bricks")
+        return nbr[:, :n], (masks[:n] if masks is not None else None)
 
     def grid_build(self, coords, batch_size, shape):
         nbytes = self.lib.pxs_voxel_grid_bytes(batch_size, *shape)

@@ -68,6 +68,56 @@ def test_neighbor_map_grid_bit_exact(px, orc, case):
     np.testing.assert_array_equal(masks.cpu().numpy().astype(np.int64) & 0x7FFFFFF, ref_masks)
 
 
+def _brick_case(case):
+    if case in coord_cases():
+        return coord_cases()[case][0]
+    if case == "edges":
+        return np.array([[0, 0, 0, 0], [0, 0, 0, 1], [0, 0, 1, 0], [0, 7, 7, 7], [0, 7, 7, 6],
+                         [1, 0, 0, 0], [1, 7, 0, 7], [1, 3, 4, 4], [1, 4, 4, 4], [1, 4, 3, 5]],
+                        np.int32)
+    if case == "offset_1024":  # the U-Net shells moved up to coordinates near 730
+        return W.unet_stage_128()["coords"] + np.array([0, 600, 600, 600], np.int32)
+    if case == "spaced":  # every third cell: bricks holding a few voxels, most neighbours absent
+        return W.conv_fp32_64()["coords"] * np.array([1, 3, 3, 3], np.int32)
+    rng = np.random.default_rng(5)  # "scattered": about one voxel per brick
+    pts = np.unique(rng.integers(0, 200, size=(20000, 3)), axis=0)
+    return np.ascontiguousarray(np.hstack([np.zeros((len(pts), 1), np.int64), pts]).astype(np.int32))
+
+
+BRICK_CASES = ["conv_fp32_64", "unet_stage_128", "small_2batch", "single", "edges", "offset_1024",
+               "spaced", "scattered"]
+
+
+@pytest.mark.parametrize("case", BRICK_CASES)
+def test_neighbor_map_bricks_bit_exact(px, orc, case):
+    """The brick-table map equals the oracle's and the voxel hash's bit for
+    bit: grid faces, brick faces in every direction, several batch items,
+    coordinates near 730, sparse bricks and voxels about one per brick."""
+    coords = _brick_case(case)
+    print(f"[neighbor_map_bricks] case={case} n={coords.shape[0]}", flush=True)
+    c = ti32(coords)
+    nbr, masks = px.neighbor_map_bricks(c)
+    ref = orc.neighbor_map(coords)
+    np.testing.assert_array_equal(nbr.cpu().numpy(), ref)
+    present = (ref != coords.shape[0])
+    ref_masks = (present.astype(np.int64) << np.arange(27)[:, None]).sum(0)
+    np.testing.assert_array_equal(masks.cpu().numpy().astype(np.int64) & 0x7FFFFFF, ref_masks)
+    hnbr, hmasks = px.neighbor_map(c)
+    np.testing.assert_array_equal(nbr.cpu().numpy(), hnbr.cpu().numpy())
+    np.testing.assert_array_equal(masks.cpu().numpy(), hmasks.cpu().numpy())
+
+
+def test_neighbor_map_bricks_duplicates_keep_smallest_row(px):
+    """A repeated coordinate resolves to its smallest row, as in the voxel hash."""
+    coords = np.array([[0, 5, 5, 5], [0, 5, 5, 6], [0, 5, 5, 5], [0, 6, 5, 5], [0, 5, 5, 6]],
+                      np.int32)
+    c = ti32(coords)
+    nbr, masks = px.neighbor_map_bricks(c)
+    hnbr, hmasks = px.neighbor_map(c)
+    np.testing.assert_array_equal(nbr.cpu().numpy(), hnbr.cpu().numpy())
+    np.testing.assert_array_equal(masks.cpu().numpy(), hmasks.cpu().numpy())
+
+
 def test_neighbor_map_grid_skips_out_of_extent_rows(px):
     coords = np.array([[0, 1, 1, 1], [0, 1, 1, 2], [0, 9, 1, 1]], np.int32)  # x = 9 >= 8
     nbr, masks = px.neighbor_map_grid(ti32(coords), 1, (8, 8, 8))
