@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--workload", default="unet_stage_128",
                     choices=["unet_stage_128", "conv_fp32_64", "attn_block", "swin_64",
                              "flow_step", "flow_sample", "decoder", "pack_load", "hash_map_128",
-                             "linear_dense"])
+                             "linear_dense", "attn_wide"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
@@ -282,6 +282,20 @@ def unet_stage(args, torch, px, W):
         step()
     torch.cuda.synchronize()
     kern = {k: timer.mean_ms(k) for k in ops}
+    # The insert is a few microseconds of GPU work, shorter than the host's
+    # issue of an event-bracketed op: its events would time the host.  It is
+    # timed instead as a run of back-to-back inserts (same rows, same
+    # generation: idempotent) between two events.
+    if args.topology != "separate":
+        g_last = C.c_uint32(gen[0])
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(args.steps):
+            chk(lib.pxs_s2_tagged_insert(P(coords), n, 2, 128, 128, 128, P(grid1), g_last,
+                                         P(ds_ws), S()), "insert")
+        ev1.record()
+        torch.cuda.synchronize()
+        kern["topology_128"] = ev0.elapsed_time(ev1) / args.steps
     dom = max(macs, key=lambda k: kern[k])
     # Timed region: only the dominant kernel carries events.
     timer.only = {dom}
@@ -367,12 +381,11 @@ def traffic_note(op):
             f"at commit {rec['measured_at_commit']}, {rec['method']} ({rec['source']})")
 
 
-def attention_metric(args, torch, px, W):
+def attention_metric(args, torch, px, W, heads=16, hd=64):
     import numpy as np
 
     dev = torch.device("cuda:0")
     lens = (12288, 20480)
-    heads, hd = 16, 64
     n = sum(lens)
     C = heads * hd
     q = torch.from_numpy(W.normal(71, n * C, 1).reshape(n, C)).to(dev).to(torch.bfloat16)
@@ -381,15 +394,16 @@ def attention_metric(args, torch, px, W):
     cu = torch.tensor([0, lens[0], n], dtype=torch.int64, device=dev)
     o = torch.empty_like(q)
     timer = Timer(torch)
-    warm_up(args, torch, lambda: px.varlen_attention(q, k, v, cu, cu, heads, hd, 0.125, out=o))
+    scale = hd ** -0.5
+    warm_up(args, torch, lambda: px.varlen_attention(q, k, v, cu, cu, heads, hd, scale, out=o))
     steps = max(args.steps, 5)
     for _ in range(steps):
-        timer.run("attn", lambda: px.varlen_attention(q, k, v, cu, cu, heads, hd, 0.125, out=o))
+        timer.run("attn", lambda: px.varlen_attention(q, k, v, cu, cu, heads, hd, scale, out=o))
     torch.cuda.synchronize()
     flops = 4.0 * sum(L * L for L in lens) * hd * heads
     ms = timer.mean_ms("attn")
     tf = flops / (ms * 1e-3) / 1e12
-    return {"workload": "varlen self-attention 12,288 + 20,480 tokens, 16 heads x 64, bf16",
+    return {"workload": f"varlen self-attention 12,288 + 20,480 tokens, {heads} heads x {hd}, bf16",
             "ms": round(ms, 4), "tflops": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
             "frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_call": flops}
 
@@ -1153,13 +1167,14 @@ def decoder(args, torch, px, W):
                                                      max_rows=max_rows)[0]
                              for u in range(1, len(chans))]
     macs = 0
+    # (pair counts outside the timed region, from the decoder's own map path)
     for level, (c, C) in enumerate(zip(lvl_coords, chans)):
-        _, masks = px.neighbor_map(c)
+        _, masks = px.neighbor_map_bricks(c)
         pairs = int(np.unpackbits(masks.cpu().numpy().view(np.uint8)).sum())
         macs += nblk[level] * (pairs * C * C + 2 * c.shape[0] * C * 4 * C)
         if level + 1 < len(chans):
             O_ = chans[level + 1]
-            _, m_next = px.neighbor_map(lvl_coords[level + 1])
+            _, m_next = px.neighbor_map_bricks(lvl_coords[level + 1])
             pairs_next = int(np.unpackbits(m_next.cpu().numpy().view(np.uint8)).sum())
             macs += pairs * C * 8 * O_ + pairs_next * O_ * O_
     macs += n * wl["latent_channels"] * chans[0] + level_rows[-1] * chans[-1] * wl["out_channels"]
@@ -1316,9 +1331,24 @@ def linear_dense(args, torch, px, W):
                          "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}}
 
 
+def attn_wide(args, torch, px, W):
+    """Head dims above 64 (the wavefront-per-query kernel) against the tiled
+    head_dim-64 kernel on config 3's tokens at the same width (1,024)."""
+    res = {hd: attention_metric(args, torch, px, W, heads=1024 // hd, hd=hd) for hd in (64, 128)}
+    wide = res[128]
+    return {"metric": "varlen attention TFLOP/s, head_dim 128 (8 heads) vs 64 (16 heads)",
+            "value": wide["tflops"], "unit": "TFLOP/s", "ms_per_step": wide["ms"], "dtype": "bf16",
+            "config": {"workload": "attn_wide: 12,288 + 20,480 tokens, width 1,024",
+                       "head_dim_128": wide, "head_dim_64": res[64]},
+            "roofline": {"bound": "mfma", "kernel": "attention head_dim 128",
+                         "achieved": wide["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": wide["frac"], "traffic": None}}
+
+
 OTHER_WORKLOADS = {"conv_fp32_64": conv_fp32_64, "attn_block": attn_block, "swin_64": swin_64,
                    "flow_sample": flow_sample, "decoder": decoder, "pack_load": pack_load,
-                   "flow_step": flow_step, "hash_map_128": hash_map_128, "linear_dense": linear_dense}
+                   "flow_step": flow_step, "hash_map_128": hash_map_128, "linear_dense": linear_dense,
+                   "attn_wide": attn_wide}
 
 
 def main():
