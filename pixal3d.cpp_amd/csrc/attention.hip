@@ -457,11 +457,33 @@ constexpr int kKeyRowsLds = 1024;  // longest permuted segment whose key rows ar
 #define PXS_ATTN_SADDR 1
 #endif
 
-template <int NW>
+template <int NW, int DH>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(kAttnWavesPerEu)))
 flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
-    constexpr int kTileBytes = kKeys * 128;           // one 64-key x 64-dim bf16 tile
-    constexpr int kInstr = 2 * (kKeys / 8) / NW;      // K + V wave instructions per tile
+    // DH = 64: 64-key tiles (two 32-key sub-tiles); DH = 128: 32-key tiles of
+    // two 64-dim halves.  Either way a K or V tile is 8 KB and a step issues
+    // 16 MFMAs; a tile row is stored as DH / 64 halves of 128 bytes, each
+    // half laid out (and swizzled) as the 64-dim tile.
+    static_assert(DH == 64 || DH == 128, "head dim 64 or 128");
+    constexpr int KT = DH == 64 ? 2 : 1;              // 32-key sub-tiles per tile
+    constexpr int kKeysT = 32 * KT;                   // keys per tile
+    constexpr int NHALF = DH / 64;                    // 64-dim halves of a row
+    constexpr int NST = DH / 16;                      // K steps of K Q^T
+    constexpr int NDT = DH / 32;                      // 32-dim blocks of O
+    constexpr int kHalfBytes = kKeysT * 128;          // one half of a tile
+    constexpr int kTileBytes = NHALF * kHalfBytes;    // one K or V tile (8 KB)
+    constexpr int kUnitsHalf = kKeysT / 8;            // 8-row load units per half
+    constexpr int kInstr = 2 * NHALF * kUnitsHalf / NW;  // K + V wave instructions per tile
+    // Load unit u (8 rows of one half of the K or V tile): its half and first
+    // row.  (For one half, the plain forms, so the 64-dim code is as before.)
+    auto unit_half = [](int u) {
+        if constexpr (NHALF == 1) return 0;
+        else return (u % (NHALF * kUnitsHalf)) / kUnitsHalf;
+    };
+    auto unit_row0 = [](int u) {
+        if constexpr (NHALF == 1) return (u % kUnitsHalf) * 8;
+        else return ((u % (NHALF * kUnitsHalf)) % kUnitsHalf) * 8;
+    };
     __shared__ __align__(16) char lds[kAttnTileSlots * kTileBytes];
     // Byte offsets of tile t's K and V slots.
     auto k_slot = [](int t) { return kAttnW3 ? (t & 1) * kTileBytes : (t % kAttnStages) * 2 * kTileBytes; };
@@ -493,15 +515,17 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     const int64_t qi = q_begin + wave * 32 + r;
     const bool q_valid = qi < q_end;
     const int64_t q_row = q_valid ? (a.row_map ? a.row_map[qi] : qi) : -1;
-    bf16x8 qf[4];
+    bf16x8 qf[NST];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
+    for (int st = 0; st < NST; ++st) {
         uint4 v = make_uint4(0, 0, 0, 0);
-        if (q_valid) v = *reinterpret_cast<const uint4 *>(qp + q_row * a.ldq + head * 64 + 32 * h + 8 * st);
+        if (q_valid)
+            v = *reinterpret_cast<const uint4 *>(qp + q_row * a.ldq + head * DH + (st / 4) * 64 +
+                                                 32 * h + 8 * (st % 4));
         qf[st] = __builtin_bit_cast(bf16x8, v);
     }
 
-    const int ntiles = static_cast<int>((k_end - k_begin + kKeys - 1) / kKeys);
+    const int ntiles = static_cast<int>((k_end - k_begin + kKeysT - 1) / kKeysT);
     const int lrow = lane >> 3, lslot = lane & 7;
     // Permuted keys (windows): stage the segment's row indices in LDS, so the
     // tile loads below need no global index load (whose wait would also wait
@@ -525,37 +549,42 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 #pragma unroll
     for (int j = 0; j < kInstr; ++j) {
         const int unit = wave * kInstr + j;           // 0..15: 8 K blocks then 8 V blocks
-        const bool is_v = unit >= kKeys / 8;
-        const int row = (unit % (kKeys / 8)) * 8 + lrow;
+        const bool is_v = unit >= NHALF * kUnitsHalf;
+        const int half = unit_half(unit);
+        const int row = unit_row0(unit) + lrow;
         const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
         const int64_t ld = is_v ? a.ldv : a.ldk;
-        src0[j] = (is_v ? vp : kp) + (k_begin + row) * ld + head * 64 + piece * 8;
-        src_step[j] = kKeys * ld;
+        src0[j] = (is_v ? vp : kp) + (k_begin + row) * ld + head * DH + half * 64 + piece * 8;
+        src_step[j] = kKeysT * ld;
     }
 #else
     // Full unpermuted tiles: the K and V tile bases (wave-uniform, scalar
     // registers) advance by 64 rows per tile; each lane's byte offset within
     // a tile (row * ld + piece) stays fixed, so a tile's loads need no vector
     // address arithmetic.  Offsets fit 32 bits for rows of up to 2^25 bytes.
-    const char * kbase = reinterpret_cast<const char *>(kp + k_begin * a.ldk + head * 64);
-    const char * vbase = reinterpret_cast<const char *>(vp + k_begin * a.ldv + head * 64);
-    const int64_t kstep = static_cast<int64_t>(kKeys) * a.ldk * 2;
-    const int64_t vstep = static_cast<int64_t>(kKeys) * a.ldv * 2;
+    const char * kbase = reinterpret_cast<const char *>(kp + k_begin * a.ldk + head * DH);
+    const char * vbase = reinterpret_cast<const char *>(vp + k_begin * a.ldv + head * DH);
+    const int64_t kstep = static_cast<int64_t>(kKeysT) * a.ldk * 2;
+    const int64_t vstep = static_cast<int64_t>(kKeysT) * a.ldv * 2;
     uint32_t voff[kInstr];
 #pragma unroll
     for (int j = 0; j < kInstr; ++j) {
         const int unit = wave * kInstr + j;
-        const bool is_v = unit >= kKeys / 8;
-        const int row = (unit % (kKeys / 8)) * 8 + lrow;
+        const bool is_v = unit >= NHALF * kUnitsHalf;
+        const int half = unit_half(unit);
+        const int row = unit_row0(unit) + lrow;
         const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
-        voff[j] = static_cast<uint32_t>((row * (is_v ? a.ldv : a.ldk) + piece * 8) * 2);
+        if constexpr (NHALF == 1)
+            voff[j] = static_cast<uint32_t>((row * (is_v ? a.ldv : a.ldk) + piece * 8) * 2);
+        else
+            voff[j] = static_cast<uint32_t>((row * (is_v ? a.ldv : a.ldk) + half * 64 + piece * 8) * 2);
     }
     const bool saddr_ok = a.ldk < (int64_t(1) << 24) && a.ldv < (int64_t(1) << 24);
 #endif
     auto issue = [&](int tile) __attribute__((always_inline)) {
         const uint32_t kbase_lds = lds_base + k_slot(tile), vbase_lds = lds_base + v_slot(tile);
-        const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeys;
-        if (a.row_map == nullptr && kt0 + kKeys <= k_end) {
+        const int64_t kt0 = k_begin + static_cast<int64_t>(tile) * kKeysT;
+        if (a.row_map == nullptr && kt0 + kKeysT <= k_end) {
 #if PXS_ATTN_SADDR
             if (saddr_ok) {
                 const char * kt_base = kbase + tile * kstep;
@@ -563,10 +592,12 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 #pragma unroll
                 for (int j = 0; j < kInstr; ++j) {
                     const int unit = wave * kInstr + j;
-                    const bool is_v = unit >= kKeys / 8;
-                    const int row0 = (unit % (kKeys / 8)) * 8;
+                    const bool is_v = unit >= NHALF * kUnitsHalf;
+                    const int half = unit_half(unit);
+                    const int row0 = unit_row0(unit);
                     lds_dma16_sbase(is_v ? vt_base : kt_base, voff[j],
-                                    (is_v ? vbase_lds : kbase_lds) + row0 * 128);
+                                    (is_v ? vbase_lds : kbase_lds) + half * kHalfBytes + row0 * 128);
+                    (void)half;
                 }
                 return;
             }
@@ -575,9 +606,11 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 #pragma unroll
             for (int j = 0; j < kInstr; ++j) {
                 const int unit = wave * kInstr + j;
-                const bool is_v = unit >= kKeys / 8;
-                const int row0 = (unit % (kKeys / 8)) * 8;
-                lds_dma16(src0[j] + tile * src_step[j], (is_v ? vbase_lds : kbase_lds) + row0 * 128);
+                const bool is_v = unit >= NHALF * kUnitsHalf;
+                const int half = unit_half(unit);
+                const int row0 = unit_row0(unit);
+                lds_dma16(src0[j] + tile * src_step[j],
+                          (is_v ? vbase_lds : kbase_lds) + half * kHalfBytes + row0 * 128);
             }
             return;
 #endif
@@ -585,8 +618,9 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 #pragma unroll
         for (int j = 0; j < kInstr; ++j) {
             const int unit = wave * kInstr + j;
-            const bool is_v = unit >= kKeys / 8;
-            const int row0 = (unit % (kKeys / 8)) * 8;
+            const bool is_v = unit >= NHALF * kUnitsHalf;
+            const int half = unit_half(unit);
+            const int row0 = unit_row0(unit);
             const int row = row0 + lrow;
             const int piece = lslot ^ (is_v ? vswz(row) : kswz(row));
             const int64_t kidx = kt0 + row;
@@ -594,23 +628,29 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
             if (kidx < k_end) {
                 const int64_t prow = keys_in_lds ? key_rows[kidx - k_begin]
                                                  : (a.row_map ? a.row_map[kidx] : kidx);
-                g = is_v ? static_cast<const void *>(vp + prow * a.ldv + head * 64 + piece * 8)
-                         : static_cast<const void *>(kp + prow * a.ldk + head * 64 + piece * 8);
+                if constexpr (NHALF == 1) {
+                    g = is_v ? static_cast<const void *>(vp + prow * a.ldv + head * 64 + piece * 8)
+                             : static_cast<const void *>(kp + prow * a.ldk + head * 64 + piece * 8);
+                } else {
+                    const int col = head * DH + half * 64 + piece * 8;
+                    g = is_v ? static_cast<const void *>(vp + prow * a.ldv + col)
+                             : static_cast<const void *>(kp + prow * a.ldk + col);
+                }
             }
-            lds_dma16(g, (is_v ? vbase_lds : kbase_lds) + row0 * 128);
+            lds_dma16(g, (is_v ? vbase_lds : kbase_lds) + half * kHalfBytes + row0 * 128);
         }
     };
 
     // S^T (keys x queries) for one tile: 2 sub-tiles of 32 keys, 4 K-steps each.
-    auto qk = [&](int tile, f32x16 (&s)[2]) {
+    auto qk = [&](int tile, f32x16 (&s)[KT]) {
         const char * kl = lds + k_slot(tile);
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
+        for (int kt = 0; kt < KT; ++kt) {
             const int row = kt * 32 + r;
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
+            for (int st = 0; st < NST; ++st) {
                 const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(
-                    kl + row * 128 + (((4 * h + st) ^ kswz(row)) << 4));
+                    kl + (st / 4) * kHalfBytes + row * 128 + (((4 * h + st % 4) ^ kswz(row)) << 4));
                 if (st == 0) {
                     const f32x16 zero = {};
                     s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], zero, 0, 0, 0);
@@ -627,34 +667,36 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     const int v_key_off = 4 * (G >> 1) + (jl >> 2);
     const int v_dim_off = 16 * (G & 1) + 4 * (jl & 3);
 
-    f32x16 oacc[2];
+    f32x16 oacc[NDT];
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) oacc[dt][v] = 0.0f;
     // Orders VALU reads of the accumulators after the last PV MFMA's result
     // (a no-op unless they live in AGPRs).
     auto oacc_ready = [&]() __attribute__((always_inline)) {
 #if PXS_ATTN_OACC_AGPR
+        static_assert(NDT == 2, "the AGPR form covers two O blocks");
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(oacc[0]), "+a"(oacc[1]));
 #endif
     };
 
     // O^T += V^T P^T for one tile (P^T fragments pb[kt][u] from softmax).
-    auto pv = [&](int tile, const bf16x8 (&pb)[2][2]) {
+    auto pv = [&](int tile, const bf16x8 (&pb)[KT][2]) {
         const char * vl = lds + v_slot(tile);
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
+        for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int key_a = kt * 32 + 16 * u + v_key_off;
                 const int key_b = key_a + 8;
 #pragma unroll
-                for (int dt = 0; dt < 2; ++dt) {
-                    const int dbyte = (dt * 32 + v_dim_off) * 2;
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const int dbyte = ((dt % 2) * 32 + v_dim_off) * 2;
                     const int piece = dbyte >> 4, within = dbyte & 15;
-                    const char * pa = vl + key_a * 128 + ((piece ^ vswz(key_a)) << 4) + within;
-                    const char * pbp = vl + key_b * 128 + ((piece ^ vswz(key_b)) << 4) + within;
+                    const char * vh = vl + (dt / 2) * kHalfBytes;
+                    const char * pa = vh + key_a * 128 + ((piece ^ vswz(key_a)) << 4) + within;
+                    const char * pbp = vh + key_b * 128 + ((piece ^ vswz(key_b)) << 4) + within;
                     const v4i16 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                         (v4i16 __attribute__((address_space(3))) *)(pa));
                     const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -683,10 +725,10 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     // that independent MFMAs can be interleaved with each: the max (and the
     // rare lazy rescale of O), then the exponentials and row sums.  valid < 64
     // masks the keys past the segment end (only the last tile).
-    auto softmax_max = [&](f32x16 (&s)[2], int valid) {
-        if (valid < kKeys) {
+    auto softmax_max = [&](f32x16 (&s)[KT], int valid) {
+        if (valid < kKeysT) {
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+            for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
@@ -697,7 +739,9 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
 #pragma unroll
         for (int v = 2; v < 16; ++v) mx = fmaxf(mx, s[0][v]);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[1][v]);
+        for (int kt = 1; kt < KT; ++kt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt][v]);
         return lane_pair_max(mx);
     };
     // Raise the running max only when this tile would overflow the lazy
@@ -711,16 +755,16 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
             l_part *= alpha;
             oacc_ready();
 #pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
         }
     };
-    auto softmax_exp = [&](const f32x16 (&s)[2], bf16x8 (&pb)[2][2]) {
+    auto softmax_exp = [&](const f32x16 (&s)[KT], bf16x8 (&pb)[KT][2]) {
         const float mc = m_run * c;
         float lsum = 0.0f;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
+        for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 bf16x8 p8;
@@ -744,18 +788,18 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     // kTileSumLimit (or to inf) is redone with its true max.  p then stays
     // below 2^40, far from fp32 and bf16 overflow in O and l.
     constexpr float kTileSumLimit = 1099511627776.0f;  // 2^40
-    auto softmax_exp_checked = [&](f32x16 (&s)[2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+    auto softmax_exp_checked = [&](f32x16 (&s)[KT], bf16x8 (&pb)[KT][2]) __attribute__((always_inline)) {
         float ts = softmax_exp(s, pb);
         attn_step_schedule();
         if (__builtin_expect(__ballot(!(ts <= kTileSumLimit)) != 0, 0)) {
-            const float mx = softmax_max(s, kKeys);
+            const float mx = softmax_max(s, kKeysT);
             const float m_new = fmaxf(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
             m_run = m_new;
             l_part *= alpha;
             oacc_ready();
 #pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
             ts = softmax_exp(s, pb);
@@ -768,7 +812,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     // One steady-state step for full tile j > 0: PV(j-1), QK(j+1), then tile
     // j's exponentials (overflow-checked) while those MFMAs run.  The first
     // tile (step_first) takes its max to set m_run.
-    auto step = [&](int j, f32x16 (&s_cur)[2], f32x16 (&s_next)[2], bf16x8 (&p)[2][2]) {
+    auto step = [&](int j, f32x16 (&s_cur)[KT], f32x16 (&s_next)[KT], bf16x8 (&p)[KT][2]) {
         // Tile j+1 has landed (it is the newest load); the barrier also frees
         // the stage of tile j-2 for tile j+2.
         wait_vmcnt0();
@@ -780,11 +824,11 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         if constexpr (kSetPrio) __builtin_amdgcn_s_setprio(0);
         softmax_exp_checked(s_cur, p);
     };
-    auto step_first = [&](f32x16 (&s_cur)[2], f32x16 (&s_next)[2], bf16x8 (&p)[2][2]) {
+    auto step_first = [&](f32x16 (&s_cur)[KT], f32x16 (&s_next)[KT], bf16x8 (&p)[KT][2]) {
         wait_vmcnt0();
         barrier_no_fence();
         if (2 < ntiles) issue(2);
-        rescale(softmax_max(s_cur, kKeys));
+        rescale(softmax_max(s_cur, kKeysT));
         qk(1, s_next);
         softmax_exp_checked(s_cur, p);
     };
@@ -796,8 +840,8 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         if (ntiles > 1) wait_vmcnt(kInstr);
         else wait_vmcnt0();
         barrier_no_fence();
-        f32x16 s_a[2], s_b[2];
-        bf16x8 p_prev[2][2];
+        f32x16 s_a[KT], s_b[KT];
+        bf16x8 p_prev[KT][2];
         qk(0, s_a);
         // Steady state over tiles 0 .. ntiles-2 (only the last can be
         // partial): the first tile peeled, the rest unrolled by two so the S
@@ -806,7 +850,7 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         if (ntiles > 1) {
             step_first(s_a, s_b, p_prev);
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) s_a[kt] = s_b[kt];
+            for (int kt = 0; kt < KT; ++kt) s_a[kt] = s_b[kt];
         }
         for (; j + 2 < ntiles; j += 2) {
             step(j, s_a, s_b, p_prev);
@@ -815,12 +859,12 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
         if (j + 1 < ntiles) {
             step(j, s_a, s_b, p_prev);
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) s_a[kt] = s_b[kt];
+            for (int kt = 0; kt < KT; ++kt) s_a[kt] = s_b[kt];
         }
         // Last tile (possibly partial), then the two outstanding PV products.
         const int last = ntiles - 1;
         if (last > 0) pv(last - 1, p_prev);
-        const float mx = softmax_max(s_a, static_cast<int>(klen - static_cast<int64_t>(last) * kKeys));
+        const float mx = softmax_max(s_a, static_cast<int>(klen - static_cast<int64_t>(last) * kKeysT));
         rescale(mx);
         l_part += softmax_exp(s_a, p_prev);
         pv(last, p_prev);
@@ -830,9 +874,9 @@ flash_attn_bf16_kernel(AttnArgs a, int heads, int64_t tiles_bound) {
     if (!q_valid) return;
     oacc_ready();
     const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    uint16_t * op = static_cast<uint16_t *>(a.o) + q_row * a.ldo + head * 64;
+    uint16_t * op = static_cast<uint16_t *>(a.o) + q_row * a.ldo + head * DH;
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
+    for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int d = dt * 32 + 8 * i + 4 * h;
@@ -1237,11 +1281,11 @@ int launch_attn_window(const AttnArgs & args, int heads, hipStream_t stream) {
     return check_launch("window attention (bf16)");
 }
 
-template <int NW>
+template <int NW, int DH>
 int launch_attn_bf16(const AttnArgs & args, int64_t total_q, int heads, hipStream_t stream) {
     const int64_t bound = total_q / (32 * NW) + args.nseg + 1;
     if (bound * heads > INT32_MAX) return fail(PXS_ERR_ARG, "attention grid too large");
-    hipLaunchKernelGGL((flash_attn_bf16_kernel<NW>), dim3(static_cast<unsigned>(bound * heads)),
+    hipLaunchKernelGGL((flash_attn_bf16_kernel<NW, DH>), dim3(static_cast<unsigned>(bound * heads)),
                        dim3(NW * 64), 0, stream, args, heads, bound);
     return check_launch("flash attention (bf16)");
 }
@@ -1395,7 +1439,12 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     PXS_CHECK(q && k && v && o && cu_q && cu_k && workspace, PXS_ERR_ARG,
               "pxs_varlen_attention: null pointer");
     hipStream_t s = as_stream(stream);
-    if (head_dim > 64 || value_dim > 64) {
+    // bf16 head_dim 128 runs the tiled kernel too (32-key tiles of two 64-dim halves)
+    const bool fast128 = dtype == PXS_BF16 && head_dim == 128 && value_dim == 128 &&
+                         (ld_q % 8 == 0) && (ld_k % 8 == 0) && (ld_v % 8 == 0) && (ld_o % 4 == 0) &&
+                         aligned16(q) && aligned16(k) && aligned16(v) &&
+                         (reinterpret_cast<uintptr_t>(o) & 7u) == 0;
+    if ((head_dim > 64 || value_dim > 64) && !fast128) {
         PXS_CHECK(total_q <= INT32_MAX, PXS_ERR_ARG, "attention grid too large");
         AttnArgs a{};
         a.q = q; a.k = k; a.v = v; a.ldq = ld_q; a.ldk = ld_k; a.ldv = ld_v;
@@ -1432,7 +1481,7 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     // workgroup whatever the wave count, so fewer waves only lower occupancy
     // (windows of ~100 rows run 3.6x faster with 4 waves than with 1).  The
     // generic kernel drops to one wave for short segments.
-    const int nw = (fast || total_q / nseg >= PXS_ATTN_NW4_MIN) ? 4 : 1;
+    const int nw = (fast || fast128 || total_q / nseg >= PXS_ATTN_NW4_MIN) ? 4 : 1;
     const int q_tile = 32 * nw;
     int64_t * tile_start = static_cast<int64_t *>(workspace);
     int32_t * tiles = reinterpret_cast<int32_t *>(tile_start + nseg + 1);
@@ -1451,7 +1500,8 @@ int pxs_varlen_attention(int dtype, const void * q, int64_t ld_q, const void * k
     a.vec_ok = (head_dim % vec == 0) && (value_dim % vec == 0) && (ld_q % vec == 0) && (ld_k % vec == 0) &&
                (ld_v % vec == 0) && aligned16(q) && aligned16(k) && aligned16(v);
     if (dtype == PXS_BF16) {
-        if (fast) return launch_attn_bf16<4>(a, total_q, heads, s);
+        if (fast) return launch_attn_bf16<4, 64>(a, total_q, heads, s);
+        if (fast128) return launch_attn_bf16<4, 128>(a, total_q, heads, s);
         return nw == 4 ? launch_attn<uint16_t, 4>(a, total_q, heads, s)
                        : launch_attn<uint16_t, 1>(a, total_q, heads, s);
     }

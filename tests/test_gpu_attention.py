@@ -143,6 +143,49 @@ def test_attention_empty_key_segment_gives_zeros(px):
     assert np.all(o[6:] == 0) and np.all(np.isfinite(o))
 
 
+@pytest.mark.parametrize("jump", [1.0, 40.0])
+def test_attention_bf16_hd128_tiled(px, orc, jump):
+    """bf16 head_dim 128 on the tiled MFMA kernel (32-key tiles of two
+    64-dim halves): segments ending mid-tile, one shorter than a tile, keys
+    after the first tile scored up to 40x higher (the lazy-max rescale),
+    against the oracle."""
+    lens = (1000, 1536, 77, 31)
+    heads, hd = 3, 128
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    n, C = int(cu[-1]), heads * hd
+    q = W.bf16_round(W.normal(67, n * C, 1).reshape(n, C))
+    k = W.normal(67, n * C, 2).reshape(n, C)
+    for b in range(len(lens)):
+        k[cu[b] + 32:cu[b + 1]] *= jump
+    k = W.bf16_round(k)
+    v = W.bf16_round(W.normal(67, n * C, 3).reshape(n, C))
+    scale = hd ** -0.5
+    print(f"[attn bf16 hd128] jump={jump}", flush=True)
+    o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, scale))
+    assert np.isfinite(o).all()
+    assert_bf16(o, orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(scale)),
+                what=f"bf16 attn hd128 jump {jump}")
+
+
+def test_attention_bf16_hd128_full_size_sampled_rows(px, orc):
+    """Config 3's tokens (12,288 + 20,480) at 8 heads x 128, sampled query
+    rows against the oracle."""
+    wl = W.attn_full()
+    n = wl["x"].shape[0]
+    heads, hd = 8, 128
+    C = heads * hd
+    q = W.bf16_round(W.normal(68, n * C, 1).reshape(n, C))
+    k = W.bf16_round(W.normal(68, n * C, 2).reshape(n, C))
+    v = W.bf16_round(W.normal(68, n * C, 3).reshape(n, C))
+    cu = wl["cu_seqlens"]
+    scale = hd ** -0.5
+    print(f"[attn bf16 hd128 full] n={n}", flush=True)
+    o = host(px.varlen_attention(tbf(q), tbf(k), tbf(v), ti64(cu), ti64(cu), heads, hd, scale))
+    rows = np.concatenate([np.arange(0, 12288, 131), np.arange(12288, n, 173), [12287, n - 1]])
+    ref = orc.varlen_attention(q, k, v, cu, cu, heads, hd, np.float32(scale), rows=rows)
+    assert_bf16(o[rows], ref[rows], what="attn hd128 full sampled")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("hd,vd", [(128, 128), (96, 160), (200, 40)])
 def test_attention_wide_heads(px, orc, dtype, hd, vd):
