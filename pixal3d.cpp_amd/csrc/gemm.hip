@@ -1493,7 +1493,11 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
             // of a 128x256 stage's 48 KB (one workgroup per CU either way;
             // 155.6 KB of LDS with the 27-offset source table).  The C2S
             // up-convolution 768 -> 1536 at 64^3: 1.97 -> 1.61 ms; the SLat
-            // decoder 27.3 -> 25.6 ms.
+            // decoder 27.3 -> 25.6 ms.  Sixteen waves (4 x 4, a 64x64 block
+            // of the tile each, 100 VGPRs) instead of eight (2 x 4, 128x64
+            // each) keep more loads in flight per CU and take half the
+            // epilogue per wave: the up-convolution 1.62 -> 1.56 ms, the
+            // decoder 25.1 -> 24.8 ms.
 #ifndef PXS_GEMM_SQUARE256
 #define PXS_GEMM_SQUARE256 1
 #endif
@@ -1502,7 +1506,15 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
 #endif
             if (PXS_GEMM_SQUARE256 && (args.rowmap || args.grid) && args.cout >= 512 &&
                 kstages >= 32 && ((args.m + 255) / 256) * ((args.cout + 255) / 256) >= PXS_GEMM_SQUARE256_TILES)
-                return launch_lds_tile<T, 256, 256, EPI, 2, 8, 2, 1>(args, stream);
+            {
+#ifndef PXS_GEMM_SQUARE256_WAVES
+#define PXS_GEMM_SQUARE256_WAVES 16
+#endif
+                if constexpr (PXS_GEMM_SQUARE256_WAVES == 16)
+                    return launch_lds_tile<T, 256, 256, EPI, 2, 16, 4, 1>(args, stream);
+                else
+                    return launch_lds_tile<T, 256, 256, EPI, 2, 8, 2, 1>(args, stream);
+            }
             if (PXS_GEMM_WIDE && (args.rowmap || args.grid) && args.cout > 128 && kstages >= 32)
                 return launch_lds_tile<T, 128, 256, EPI, 2, 8, 2, 1>(args, stream);
         }
