@@ -780,29 +780,39 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
         // its own register index, so the exchange is conflict-free, and the
         // sum a + b is the same whichever group adds it.
         constexpr int HI = TI / 2;
-        static_assert(NW * HI * TJ * 16 * 64 * 4 <= NSTAGE * kStageBytes,
-                      "exchange must fit in the stage buffers");
+        // The exchange runs in PASSES rounds over the 32-column blocks j when
+        // the whole of it does not fit in the stage buffers.
+        constexpr int kXchBytes = NW * HI * TJ * 16 * 64 * 4;
+        constexpr int PASSES = (kXchBytes + NSTAGE * kStageBytes - 1) / (NSTAGE * kStageBytes);
+        constexpr int TJP = TJ / PASSES;
+        static_assert(TJP * PASSES == TJ, "exchange passes must split the column blocks");
         float * xch = reinterpret_cast<float *>(smem);
         auto slot = [&](int group, int i, int j, int v) {
-            return ((((group * NWG + wl) * HI + i) * TJ + j) * 16 + v) * 64 + lane;
+            return ((((group * NWG + wl) * HI + i) * TJP + j) * 16 + v) * 64 + lane;
         };
         auto finish = [&](auto keep_tag) {
             constexpr int KEEP = decltype(keep_tag)::value, GIVE = HI - KEEP;
-#pragma unroll
-            for (int i = 0; i < HI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) xch[slot(kg, i, j, v)] = acc[GIVE + i][j][v];
-            barrier_no_fence();
             f32x16 fin[HI][TJ];
 #pragma unroll
-            for (int i = 0; i < HI; ++i)
+            for (int pass = 0; pass < PASSES; ++pass) {
+                if (pass > 0) barrier_no_fence();  // the previous pass's sums are read
 #pragma unroll
-                for (int j = 0; j < TJ; ++j)
+                for (int i = 0; i < HI; ++i)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v)
-                        fin[i][j][v] = acc[KEEP + i][j][v] + xch[slot(1 - kg, i, j, v)];
+                    for (int j = 0; j < TJP; ++j)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v)
+                            xch[slot(kg, i, j, v)] = acc[GIVE + i][pass * TJP + j][v];
+                barrier_no_fence();
+#pragma unroll
+                for (int i = 0; i < HI; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJP; ++j)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v)
+                            fin[i][pass * TJP + j][v] =
+                                acc[KEEP + i][pass * TJP + j][v] + xch[slot(1 - kg, i, j, v)];
+            }
             if (SYNC && coherent_y) {
                 // A producer of the chained launch stages its tile in LDS and
                 // writes whole 16-byte pieces device-coherently (2-byte
@@ -1515,6 +1525,11 @@ int dispatch(const GemmArgs & args, hipStream_t stream) {
                 else
                     return launch_lds_tile<T, 256, 256, EPI, 2, 8, 2, 1>(args, stream);
             }
+            // (Sixteen waves on the 128x256 tile -- two K groups with 2 or 3
+            // stages, or 4 x 4 blocks of 32x64 -- measured the same as eight
+            // on the U-Net stage's 256-channel conv; four waves of 128x128 on
+            // the 256x256 tile, one per SIMD, ran the up-convolution 26%
+            // slower.)
             if (PXS_GEMM_WIDE && (args.rowmap || args.grid) && args.cout > 128 && kstages >= 32)
                 return launch_lds_tile<T, 128, 256, EPI, 2, 8, 2, 1>(args, stream);
         }
