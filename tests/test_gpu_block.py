@@ -16,7 +16,7 @@ import oracle as O
 import pxs
 import workloads as W
 from fixtures import flow_case
-from gpu_common import assert_bf16, assert_fp32, dev, host, t32, ti32, ti64
+from gpu_common import assert_bf16, assert_fp32, dev, host, rel_l2, t32, ti32, ti64
 
 pytestmark = pytest.mark.gpu
 GOLD = Path(__file__).resolve().parent / "golden"
@@ -116,6 +116,21 @@ def test_flow_bf16_reduced_config(px, orc):
     ref = oracle_flow(orc, case, bf16=True)
     assert np.isfinite(got).all()
     assert_bf16(got, ref, what="flow bf16 reduced")
+
+
+def test_flow_bf16_full_depth(px, orc):
+    """The SLat-flow step at its full depth and width: 24 blocks of width 1024
+    (16 heads x 64, MLP 4096), 864 voxels in 2 batches, 137 context tokens
+    each; bf16 GEMMs against the oracle's fp32 forward on the same
+    bf16-rounded weights, so rounding that compounds over the 24 residual
+    updates is held to the same 1e-2 relative L2 as one block."""
+    case = flow_case(33, [[(4.0, 6.0)], [(3.0, 5.0)]], 24, 1024, 16, 24, 137)
+    print(f"flow bf16 24 blocks: n={case['n']}", flush=True)
+    got = run_flow(px, case, torch.bfloat16)
+    ref = oracle_flow(orc, case, bf16=True)
+    assert np.isfinite(got).all()
+    print(f"flow bf16 24 blocks: rel L2 {rel_l2(got, ref):.3e}", flush=True)
+    assert_bf16(got, ref, what="flow bf16 24 blocks")
 
 
 def test_block_fp32_wide_heads(px, orc):
