@@ -423,6 +423,22 @@ __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1
 #endif
 constexpr bool kMaskAbsent = PXS_GEMM_MASK_ABSENT != 0;
 
+// Stage order: offset-major (every K chunk of one offset, then the next
+// offset) or chunk-major (one K chunk over every present offset, then the
+// next chunk).  Chunk-major puts the offsets (kd, kh, 0..2), whose gathered
+// rows are mostly the same rows shifted by one, in consecutive stages.
+#ifndef PXS_GEMM_CHUNK_MAJOR
+#define PXS_GEMM_CHUNK_MAJOR 0
+#endif
+constexpr bool kChunkMajor = PXS_GEMM_CHUNK_MAJOR != 0;
+// Cache policy of the weight chunks' loads: 0 the default, 1 non-temporal
+// (nt), 2 device scope (sc1: read from L2 without allocating in the L1), so
+// they do not displace gathered rows from the L1 (every tile reads the same
+// weights; they stay in L2).
+#ifndef PXS_GEMM_W_CACHE
+#define PXS_GEMM_W_CACHE 0
+#endif
+
 template <int BM, int BN, int NSTAGE>
 constexpr int lds_gemm_bytes(int noff) {
     return NSTAGE * (BM + BN) * kChunkBytes + noff * BM * 4;
@@ -642,7 +658,8 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
     }
 
     auto issue = [&](int s) {
-        const int i = s / chunks, chunk = s - i * chunks;
+        const int i = kChunkMajor ? s % kcount : s / chunks;
+        const int chunk = kChunkMajor ? s / kcount : s - i * chunks;
         const int k = koff[i];
         char * base = smem + (s % NSTAGE) * kStageBytes;
         int32_t src[AI];
@@ -670,7 +687,12 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
         for (int j = 0; j < BI; ++j) {
             const int col = chunk * kChunk + b_piece[j] * kVec;
             const void * g = (b_ok[j] && col < a.cin) ? static_cast<const void *>(w + kbase + b_off[j]) : zero;
-            lds_dma16(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
+            if constexpr (PXS_GEMM_W_CACHE == 1)
+                lds_dma16_nt(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
+            else if constexpr (PXS_GEMM_W_CACHE == 2)
+                lds_dma16_coherent(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
+            else
+                lds_dma16(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
         }
     };
 
@@ -700,7 +722,10 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
         for (int i = 0; i < TI; ++i) {
             row_ok[i] = true;
             if constexpr (kMaskAbsent)
-                row_ok[i] = idx_lds[(full_table ? koff[s / chunks] : s / chunks) * BM + wm * WM + i * 32 + r] >= 0;
+            {
+                const int si = kChunkMajor ? s % kcount : s / chunks;
+                row_ok[i] = idx_lds[(full_table ? koff[si] : si) * BM + wm * WM + i * 32 + r] >= 0;
+            }
         }
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
@@ -934,267 +959,439 @@ gather_gemm_lds_chain_kernel(GemmArgs a, GemmArgs b, ChainArgs c) {
 }
 
 // ---------------------------------------------------------------------------
-// Neighbourhood-staged SubMConv3d over a voxel grid (bf16).  A tile of
-// kHaloBM consecutive output rows reads its 27 x kHaloBM neighbour sources
-// from only H distinct input rows (474 on average for 128 rows of the U-Net
-// shells, against 3,456 gathered row chunks).  The tile deduplicates its
-// sources in an LDS hash table, stages the H rows' 64-channel chunk in LDS
-// once per chunk, and then streams only the weights W_k (a 4-stage ring) for
-// the present offsets k: the MFMA operand of output row p at offset k is the
-// staged row slot[k][p] (a zero row for absent neighbours).  A tile whose
-// halo exceeds kHaloMax rows reads its gathered operands from global memory
-// instead.  MFMA operands are swapped (W fragment as A, X fragment as B), so
-// a lane holds 4 consecutive output channels of one row.
-#ifndef PXS_GEMM_HALO
-#define PXS_GEMM_HALO 0
+// SubMConv3d (bf16, 27 offsets) over neighbourhood ranges.  The 9 offsets
+// (kh, kw) of one x-plane kd take their sources for a tile of 128
+// consecutive output rows from an almost contiguous range of input rows: rows
+// are sorted by (b, x, y, z), so the neighbours in plane x + kd - 1 of a run
+// of rows lie between those of its first and last row (163 rows at the
+// median on the U-Net shells, against 9 x 128 gathered row chunks).  A tile
+// stages each plane's range [lo, hi] once per 64-channel chunk (one
+// contiguous DMA, no index table) and then streams only the weights W_k of
+// that plane's offsets; the MFMA operand of output row p at offset k is the
+// staged row src(k, p) - lo, or a zero row where the neighbour is absent.
+// A plane whose range exceeds kRangeCap rows is split into its three kh rows
+// of offsets; a kh row that still exceeds it is staged per offset as the
+// offset's 128 gathered rows.  The vector-memory instructions per tile fall
+// from 1,728 to about 1,000 (the weights are now most of them).
+//
+// Pipeline: a 3-stage weight ring (each stage's weights issued two stages
+// ahead) and one halo buffer, which the next (group, chunk) refills after
+// every wave has read its operands of the group's last stage (a barrier
+// inside that stage, the DMA then overlapping its MFMAs); 78 KB of LDS, so
+// two workgroups share a CU; 8 waves in two K groups of 2 x 2 blocks
+// (64 x BN/2 each).  Stages run chunk by chunk, within a chunk group by group
+// (planes ascending), within a group offsets ascending.  The tile is written
+// through LDS as whole 16-byte row pieces.
+#ifndef PXS_GEMM_RANGE
+#define PXS_GEMM_RANGE 1
 #endif
-constexpr int kHaloBM = 128, kHaloBN = 128, kHaloMax = 576, kHaloNW = 8, kHaloWStages = 4;
-// Distinct sources are found with a byte map over the tile's source range
-// [lo, hi] (at most kHaloRange rows; wider tiles read their operands from
-// global memory) and ranked by a prefix sum, so halo slots follow the input
-// row order: the 16 tile rows one LDS cycle serves at an offset read mostly
-// consecutive slots, on distinct banks.
-constexpr int kHaloRange = 8192;
-static_assert(kHaloRange * 2 <= kHaloMax * 128, "byte map and word prefix in the halo area");
-constexpr int kHaloLds = (kHaloMax + 1) * 128 + kHaloWStages * kHaloBN * 128 + 27 * kHaloBM * 4 +
-                         kHaloMax * 4;
+// Widest output for which the range kernel is used (conv C, 256 channels,
+// keeps its 128 x 256 gather tiles unless this is raised).
+#ifndef PXS_GEMM_RANGE_MAXN
+#define PXS_GEMM_RANGE_MAXN 128
+#endif
+constexpr int kRangeBM = 128, kRangeNW = 8, kRangeCap = 192, kRangeWStages = 3;
+constexpr int kRangeHaloBytes = (kRangeCap + 1) * kChunkBytes;  // its zero row last
+template <int BN> constexpr int range_lds_bytes() {
+    return kRangeWStages * BN * kChunkBytes + kRangeHaloBytes + 27 * kRangeBM * 2;
+}
 
-__global__ void __launch_bounds__(kHaloNW * 64)
-halo_conv_bf16_kernel(GemmArgs a) {
-    constexpr int BM = kHaloBM, BN = kHaloBN, HMAX = kHaloMax;
-    constexpr int WAVES_N = 4;           // 2 x 4 waves of 64 rows x 32 channels
-    constexpr int TI = 2;                // 32-row blocks per wave
-    constexpr int WI = BN / (8 * kHaloNW);  // weight DMA instructions per wave per stage (2)
+template <int BN>
+__global__ void __launch_bounds__(kRangeNW * 64)
+range_conv_bf16_kernel(GemmArgs a) {
+    constexpr int BM = kRangeBM, NW = kRangeNW, CAP = kRangeCap, NT = NW * 64, WS = kRangeWStages;
+    constexpr int NWG = NW / 2;               // waves per K group
+    constexpr int WAVES_N = 2;                // each group: 2 x 2 blocks
+    constexpr int WM = BM / 2, WN = BN / WAVES_N;
+    constexpr int TI = WM / 32, TJ = WN / 32, HI = TI / 2;
+    constexpr int BI = BN / (8 * NW);         // weight DMA instructions per wave per stage
+    constexpr int kWBytes = BN * kChunkBytes;
+    constexpr int kStagePitch = BN * 2 + 16;  // the output tile staged in LDS
+    static_assert(BI >= 1 && TJ >= 1 && TI == 2, "tile shape");
+    static_assert(27 * BM * 4 <= WS * kWBytes, "source table inside the weight ring");
+    static_assert(NW * HI * TJ * 16 * 64 * 4 <= range_lds_bytes<BN>(), "exchange fits");
+    static_assert(BM * kStagePitch <= range_lds_bytes<BN>(), "staged tile fits");
     extern __shared__ __align__(16) char smem[];
-    char * halo = smem;                                           // (HMAX + 1) rows x 128 B
-    char * wring = halo + (HMAX + 1) * 128;                       // 4 x BN rows x 128 B
-    int32_t * tab = reinterpret_cast<int32_t *>(wring + kHaloWStages * BN * 128);  // [27][BM]
-    int32_t * rows = tab + 27 * BM;                               // [HMAX] halo rows
-    uint8_t * marks = reinterpret_cast<uint8_t *>(halo);                    // prologue only:
-    int32_t * wpre = reinterpret_cast<int32_t *>(halo + kHaloRange);        // byte map, word prefix
+    const int tiles = static_cast<int>(gridDim.x) - a.side_blocks;
+    if (static_cast<int>(blockIdx.x) >= tiles) {
+        s2_emit_block(a.s2, blockIdx.x - tiles, threadIdx.x, NT, smem);
+        return;
+    }
+    char * wring = smem;
+    char * halo = smem + WS * kWBytes;
+    // slots[k][p]: byte address in the halo of output row p's operand at
+    // offset k, row * 128 + (swz(row) << 4), so a lane's 16-byte piece P is at
+    // slots ^ (P << 4)
+    uint16_t * slots = reinterpret_cast<uint16_t *>(halo + kRangeHaloBytes);
+    int32_t * idx = reinterpret_cast<int32_t *>(smem);                     // prologue only
     __shared__ uint32_t tile_mask;
-    __shared__ int lo_s, hi_s, wsum[kHaloNW];
-    __shared__ int koff[27];
+    __shared__ int rlo[9], rhi[9];        // source range of each kh row q = k / 3
+    __shared__ int g_lo[27], g_rows[27];  // range start (-1 - k: offset k gathered), rows staged
+    __shared__ uint32_t g_mask[27];       // offsets of each group
+    __shared__ int g_of[27];              // group of each present offset
+    // The stages of a chunk: the present offsets in ascending k (the group
+    // order), entry i = {k * BM | group << 12 | first << 17 | last << 18, k * W_k bytes}.
+    __shared__ uint2 ent[27];
+    __shared__ int n_pos;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int kg = wave / NWG, wl = wave % NWG;
+    const int wm = wl / WAVES_N, wn = wl % WAVES_N;
     const int h = lane >> 5, r = lane & 31;
-    const int tiles_n = a.cout / BN;
-    const int logical = remap_xcd(blockIdx.x, gridDim.x);
+    const int lrow = lane >> 3, lslot = lane & 7;
+    const int tiles_n = (a.cout + BN - 1) / BN;
+    const int logical = remap_xcd(blockIdx.x, tiles);
     const int64_t p0 = static_cast<int64_t>(logical / tiles_n) * BM;
     const int n0 = (logical % tiles_n) * BN;
     const uint16_t * __restrict__ x = static_cast<const uint16_t *>(a.x);
-    constexpr int NT = kHaloNW * 64;
+    const int4 * crd = reinterpret_cast<const int4 *>(a.coords);
 
-    if (tid == 0) { tile_mask = 0; lo_s = INT_MAX; hi_s = -1; }
-    if (tid < 8) *reinterpret_cast<uint4 *>(halo + HMAX * 128 + tid * 16) = make_uint4(0, 0, 0, 0);
-    __syncthreads();
-    grid_tile_sources<BM>(a, p0, tid, NT, tab, &tile_mask);
+    // ---- the tile's sources and the range of each kh row ----
+    if (tid == 0) tile_mask = 0;
+    if (tid < 9) {
+        rlo[tid] = INT_MAX;
+        rhi[tid] = -1;
+    }
+    if (tid < 8) *reinterpret_cast<uint4 *>(halo + CAP * kChunkBytes + tid * 16) = make_uint4(0, 0, 0, 0);
     __syncthreads();
     {
+        // Thread: one row, offsets [kb, kb + 7) (kb wave-uniform); all its
+        // lookups are issued before any is used.
+        const int row = tid % BM, kb = 7 * (tid / BM);
+        const int64_t p = p0 + row;
+        const bool live = p < a.m;
+        int32_t src[7];
+        if (a.grid) {
+            const int4 c = live ? crd[p] : make_int4(0, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 7; ++i) src[i] = (live && kb + i < 27) ? grid_src(a, c, kb + i, p) : -1;
+        } else {
+            const uint32_t pm = (live && a.masks) ? a.masks[p] : ~0u;
+#pragma unroll
+            for (int i = 0; i < 7; ++i) {
+                const int k = kb + i;
+                int32_t s = -1;
+                if (live && k < 27 && ((pm >> k) & 1u)) {
+                    s = a.rowmap[k * a.ld_map + p];
+                    if (s < 0 || s >= a.rows_in) s = -1;
+                }
+                src[i] = s;
+            }
+        }
+        uint32_t local = 0;
         int lo = INT_MAX, hi = -1;
-        for (int e = tid; e < 27 * BM; e += NT) {
-            const int32_t src = tab[e];
-            if (src >= 0) { lo = min(lo, src); hi = max(hi, src); }
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+            const int k = kb + i;
+            if (k >= 27) break;  // wave-uniform
+            idx[k * BM + row] = src[i];
+            if (src[i] >= 0) {
+                local |= 1u << k;
+                lo = min(lo, src[i]);
+                hi = max(hi, src[i]);
+            }
+            if (k % 3 == 2 || i == 6) {  // the end of a kh row or of this thread's offsets
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) {
+                    lo = min(lo, __shfl_xor(lo, o));
+                    hi = max(hi, __shfl_xor(hi, o));
+                }
+                if (lane == 0 && hi >= 0) {
+                    atomicMin(&rlo[k / 3], lo);
+                    atomicMax(&rhi[k / 3], hi);
+                }
+                lo = INT_MAX;
+                hi = -1;
+            }
         }
-        for (int o = 32; o > 0; o >>= 1) {
-            lo = min(lo, __shfl_xor(lo, o));
-            hi = max(hi, __shfl_xor(hi, o));
-        }
-        if (lane == 0) { atomicMin(&lo_s, lo); atomicMax(&hi_s, hi); }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) local |= __shfl_xor(local, o);
+        if (lane == 0 && local) atomicOr(&tile_mask, local);
     }
     __syncthreads();
-    const int lo = __builtin_amdgcn_readfirstlane(lo_s);
-    const int range = __builtin_amdgcn_readfirstlane(hi_s) - lo + 1;  // >= 1: the centre is present
-    int H = HMAX + 1;  // no staging unless the range fits and the halo is small enough
-    if (range <= kHaloRange) {
-        const int words = (range + 3) >> 2;
-        uint32_t * mw = reinterpret_cast<uint32_t *>(marks);
-        for (int i = tid; i < words; i += NT) mw[i] = 0;
-        __syncthreads();
-        for (int e = tid; e < 27 * BM; e += NT) {
-            const int32_t src = tab[e];
-            if (src >= 0) marks[src - lo] = 1;  // equal values: the race is harmless
-        }
-        __syncthreads();
-        // Exclusive prefix of the set bytes per 4-byte word: 4 words a thread.
-        constexpr int WPT = kHaloRange / 4 / NT;
-        int cnt[WPT], run = 0;
-#pragma unroll
-        for (int q = 0; q < WPT; ++q) {
-            const int w = tid * WPT + q;
-            cnt[q] = w < words ? static_cast<int>((mw[w] * 0x01010101u) >> 24) : 0;
-            run += cnt[q];
-        }
-        int incl = run;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(incl, o);
-            if (lane >= o) incl += v;
-        }
-        if (lane == 63) wsum[wave] = incl;
-        __syncthreads();
-        int base = incl - run;
-        for (int wv = 0; wv < wave; ++wv) base += wsum[wv];
-#pragma unroll
-        for (int q = 0; q < WPT; ++q) {
-            const int w = tid * WPT + q;
-            if (w < words) wpre[w] = base;
-            base += cnt[q];
-        }
-        int total = 0;
-        for (int wv = 0; wv < kHaloNW; ++wv) total += wsum[wv];
-        H = __builtin_amdgcn_readfirstlane(total);
-        __syncthreads();
-        if (H <= HMAX) {
-            // slots of the sources, and the halo's row list in input order
-            for (int e = tid; e < 27 * BM; e += NT) {
-                const int32_t src = tab[e];
-                int32_t slot = HMAX;  // the zero row
-                if (src >= 0) {
-                    const int d = src - lo, w = d >> 2;
-                    const uint32_t below = mw[w] & ((1u << (8 * (d & 3))) - 1u);
-                    slot = wpre[w] + static_cast<int>((below * 0x01010101u) >> 24);
+    // ---- the groups and the stage sequence (wave 0, every lane the same
+    // scalar decisions) ----
+    if (wave == 0) {
+        const uint32_t present = tile_mask;
+        int ng = 0;
+        auto add = [&](int lo, int rows, uint32_t mask) {
+            if (lane == 0) {
+                g_lo[ng] = lo;
+                g_rows[ng] = rows;
+                g_mask[ng] = mask;
+            }
+            if (lane < 27 && ((mask >> lane) & 1u)) g_of[lane] = ng;
+            ++ng;
+        };
+        const int rows_here = static_cast<int>(min<int64_t>(BM, a.m - p0));
+        for (int kd = 0; kd < 3; ++kd) {
+            const uint32_t pm = present & (0x1FFu << (9 * kd));
+            if (!pm) continue;
+            const int plo = min(rlo[3 * kd], min(rlo[3 * kd + 1], rlo[3 * kd + 2]));
+            const int phi = max(rhi[3 * kd], max(rhi[3 * kd + 1], rhi[3 * kd + 2]));
+            if (phi - plo < CAP) {
+                add(plo, phi - plo + 1, pm);
+                continue;
+            }
+            for (int kh = 0; kh < 3; ++kh) {
+                const int q = 3 * kd + kh;
+                const uint32_t hm = present & (0x7u << (3 * q));
+                if (!hm) continue;
+                if (rhi[q] - rlo[q] < CAP) {
+                    add(rlo[q], rhi[q] - rlo[q] + 1, hm);
+                    continue;
                 }
-                tab[e] = slot;
-            }
-            for (int w = tid; w < words; w += NT) {
-                uint32_t v = mw[w];
-                int slot = wpre[w];
-                for (int b = 0; b < 4; ++b)
-                    if ((v >> (8 * b)) & 1u) rows[slot++] = lo + 4 * w + b;
+                for (uint32_t m = hm; m; m &= m - 1) add(-1 - (__ffs(m) - 1), rows_here, 1u << (__ffs(m) - 1));
             }
         }
+        // every lane k < 27 writes its offset's entry (g_of is this wave's own writes)
+        if (lane < 27 && ((present >> lane) & 1u)) {
+            const uint32_t below = present & ((1u << lane) - 1u);
+            const uint32_t above = present & ~((2u << lane) - 1u);
+            const int g = g_of[lane];
+            const bool first = below == 0 || g_of[31 - __clz(below)] != g;
+            const bool last = above == 0 || g_of[__ffs(above) - 1] != g;
+            ent[__popc(below)] = make_uint2(static_cast<uint32_t>(lane * BM) | (static_cast<uint32_t>(g) << 12) |
+                                                (first ? 1u << 17 : 0u) | (last ? 1u << 18 : 0u),
+                                            static_cast<uint32_t>(lane) * static_cast<uint32_t>(a.cout) *
+                                                static_cast<uint32_t>(a.cin) * 2u);
+        }
+        if (lane == 0) n_pos = __popc(present);
     }
-    const bool staged = H <= HMAX;
-    if (tid == 0) {
-        uint32_t m = tile_mask;
-        int i = 0;
-        while (m) { koff[i++] = __ffs(m) - 1; m &= m - 1; }
+    __syncthreads();
+    for (int e = tid; e < 27 * BM; e += NT) {
+        const int k = e / BM, row = e % BM;  // k wave-uniform
+        if (!((tile_mask >> k) & 1u)) continue;
+        const int32_t src = idx[e];
+        const int lo = g_lo[g_of[k]];
+        const int sl = src < 0 ? CAP : (lo < 0 ? row : src - lo);
+        slots[e] = static_cast<uint16_t>(sl * kChunkBytes + (swz(sl) << 4));
     }
-    __syncthreads();  // the byte map is dead: the halo rows may overwrite it
-    const int kcount = __builtin_amdgcn_readfirstlane(__popc(tile_mask));
-    const int chunks = a.cin / 64;
-    const int stages = kcount * chunks;
-    const int lrow = lane >> 3, lslot = lane & 7;
+    __syncthreads();  // the source table is dead: the weight ring may be filled
 
-    // Weight stage s = (chunk c, offset koff[i]): rows n0 .. n0 + BN - 1 of W_k,
-    // bytes 128 c .. of each, into ring slot s % 4.
-    const char * wbase = static_cast<const char *>(a.w) + static_cast<int64_t>(n0) * a.cin * 2;
-    uint32_t w_off[WI];
+    const int kcount = __builtin_amdgcn_readfirstlane(n_pos);  // stages per chunk
+    const int total = (a.cin / 64) * kcount;
+
+    // Weight stage (k, c): rows n0 .. n0 + BN - 1 of W_k (rows past cout
+    // repeat the last row: their products land in columns never stored),
+    // bytes 128 c .. 128 c + 127 of each; a scalar base and fixed lane offsets.
+    const char * wbase = static_cast<const char *>(a.w);
+    uint32_t b_voff[BI];
 #pragma unroll
-    for (int j = 0; j < WI; ++j) {
-        const int row = (wave * WI + j) * 8 + lrow;
-        w_off[j] = static_cast<uint32_t>(row * a.cin * 2 + ((lslot ^ swz(row)) << 4));
+    for (int j = 0; j < BI; ++j) {
+        const int row = (wave * BI + j) * 8 + lrow;
+        b_voff[j] = static_cast<uint32_t>(min(n0 + row, a.cout - 1)) * static_cast<uint32_t>(a.cin) * 2u +
+                    static_cast<uint32_t>((lslot ^ swz(row)) << 4);
     }
-    // (chunk, present offset) of the next weight stage to issue
-    int wc = 0, wi = 0;
-    auto issue_w = [&](int st) __attribute__((always_inline)) {
-        const int k = __builtin_amdgcn_readfirstlane(koff[wi]);
-        const char * sb = wbase + (static_cast<int64_t>(k) * a.cout * a.cin + wc * 64) * 2;
-        if (++wi == kcount) { wi = 0; ++wc; }
-        char * dst = wring + (st % kHaloWStages) * BN * 128;
+    auto issue_w = [&](uint32_t wk, int c, int ring) __attribute__((always_inline)) {
+        const char * sb = wbase + (wk + static_cast<uint32_t>(c) * 128u);
+        char * dst = wring + ring * kWBytes;
 #pragma unroll
-        for (int j = 0; j < WI; ++j)
-            lds_dma16_sbase(sb, w_off[j], lds_offset(dst + (wave * WI + j) * 8 * 128));
+        for (int j = 0; j < BI; ++j) lds_dma16_sbase(sb, b_voff[j], lds_offset(dst + (wave * BI + j) * 8 * kChunkBytes));
     };
-    // The halo's 64-channel chunk c: slot i holds row rows[i] (i < H).
-    auto issue_halo = [&](int c) __attribute__((always_inline)) {
-        for (int j = wave; j * 8 < H; j += kHaloNW) {
-            const int slot = j * 8 + lrow;
-            const void * g = g_zero_chunk;
-            if (slot < H)
-                g = x + static_cast<int64_t>(rows[slot]) * a.ldx + c * 64 + (lslot ^ swz(slot)) * 8;
-            lds_dma16(g, lds_offset(halo + j * 8 * 128));
+    // The halo of group g, chunk c.  Halo row hr holds input row lo + hr, or
+    // for a gathered offset k tile row hr's source; rows no slot refers to
+    // (past the range, absent sources) load row lo or row 0.
+    auto issue_h = [&](int g, int c) __attribute__((always_inline)) {
+        const int lo = g_lo[g], rows = g_rows[g];
+        if (lo >= 0) {
+            const char * sb = reinterpret_cast<const char *>(x + static_cast<int64_t>(lo) * a.ldx + c * 64);
+            const uint32_t pitch = static_cast<uint32_t>(a.ldx) * 2u;
+            for (int q = wave; q * 8 < rows; q += NW) {
+                const int hr = min(q * 8 + lrow, rows - 1);
+                lds_dma16_sbase(sb, static_cast<uint32_t>(hr) * pitch + static_cast<uint32_t>((lslot ^ swz(q * 8 + lrow)) << 4),
+                                lds_offset(halo + q * 8 * kChunkBytes));
+            }
+        } else {
+            const int k = -1 - lo;
+            for (int q = wave; q * 8 < rows; q += NW) {
+                const int hr = q * 8 + lrow;
+                int64_t src = -1;
+                if (hr < rows) {
+                    const int64_t p = p0 + hr;
+                    src = a.grid ? grid_src(a, crd[p], k, p)
+                                 : ((!a.masks || ((a.masks[p] >> k) & 1u)) ? a.rowmap[k * a.ld_map + p] : -1);
+                    if (src >= a.rows_in) src = -1;
+                }
+                lds_dma16(x + (src > 0 ? src : int64_t{0}) * a.ldx + c * 64 + (lslot ^ swz(hr)) * 8,
+                          lds_offset(halo + q * 8 * kChunkBytes));
+            }
         }
     };
 
-    f32x16 acc[TI];
+    f32x16 acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
-
-    if (staged && stages > 0) issue_halo(0);
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
-    for (int q = 0; q < kHaloWStages - 1; ++q)
-        if (q < stages) issue_w(q);
-    wait_vmcnt(0);
-    barrier_no_fence();
-    int c = 0, i_k = 0;  // stage s = (chunk c, present offset i_k), walked without divisions
-    for (int s = 0; s < stages; ++s) {
-        const int k = __builtin_amdgcn_readfirstlane(koff[i_k]);
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    // Stage s is position i0 of chunk c0; info0, info1 describe stages s and
+    // s + 1; (i2, c2) is the position of the next stage to issue (s + 2), into
+    // ring slot r2, its table entry e2 read one stage ahead.
+    int i0 = 0, c0 = 0, i2 = 0, c2 = 0, r2 = 2;
+    uint32_t info0 = 0, info1 = 0;
+    uint2 e2 = make_uint2(0, 0);
+    const uint32_t pmask = static_cast<uint32_t>((4 * h + kg * 2) << 4);  // this lane's first piece
+    uint32_t slot_nx[TI];
+    auto adv = [&](int & i, int & c) __attribute__((always_inline)) {
+        if (++i == kcount) {
+            i = 0;
+            ++c;
+        }
+    };
+    auto rd = [&](int i) __attribute__((always_inline)) {
+        const uint2 v = ent[i];
+        return make_uint2(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y));
+    };
+    if (total > 0) {
+        const uint2 e0 = rd(0);
+        info0 = e0.x;
+        issue_h((info0 >> 12) & 31, 0);
+        issue_w(e0.y, 0, 0);
+        adv(i2, c2);
+        if (total > 1) {
+            const uint2 e1 = rd(i2);
+            info1 = e1.x;
+            issue_w(e1.y, c2, 1);
+            adv(i2, c2);
+        }
+        if (total > 2) e2 = ent[i2];
+#pragma unroll
+        for (int i = 0; i < TI; ++i) slot_nx[i] = slots[(info0 & 4095) + wm * WM + i * 32 + r];
+        if (total > 1) wait_vmcnt(BI);
+        else wait_vmcnt(0);
+        barrier_no_fence();
+    }
+    bool wait_all = false;  // stage s starts a halo issued in stage s - 1
+    for (int s = 0; s < total; ++s) {
         if (s > 0) {
-            if (i_k == 0) wait_vmcnt(0);  // a new chunk: its halo was issued last
-            else wait_vmcnt(min(kHaloWStages - 2, stages - 1 - s) * WI);
+            // this stage's weights (and halo) are in; the next stage's weights
+            // may still be in flight
+            if (wait_all || s + 1 >= total) wait_vmcnt(0);
+            else wait_vmcnt(BI);
             barrier_no_fence();
         }
-        if (s + kHaloWStages - 1 < stages) issue_w(s + kHaloWStages - 1);
-        const char * wl = wring + (s % kHaloWStages) * BN * 128;
-        int32_t src[TI];
+        uint32_t slot[TI];
 #pragma unroll
-        for (int i = 0; i < TI; ++i) src[i] = tab[k * BM + wm * 64 + i * 32 + r];
+        for (int i = 0; i < TI; ++i) slot[i] = slot_nx[i];
+        if (s + 1 < total) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int piece = 4 * h + u;
-            const int wrow = wn * 32 + r;
-            const bf16x8 wf = *reinterpret_cast<const bf16x8 *>(wl + wrow * 128 + ((piece ^ swz(wrow)) << 4));
-#pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                uint4 xv;
-                if (staged) {
-                    xv = *reinterpret_cast<const uint4 *>(halo + src[i] * 128 + ((piece ^ swz(src[i])) << 4));
-                } else {
-                    xv = src[i] >= 0 ? *reinterpret_cast<const uint4 *>(
-                                           x + static_cast<int64_t>(src[i]) * a.ldx + c * 64 + piece * 8)
-                                     : make_uint4(0, 0, 0, 0);
-                }
-                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, __builtin_bit_cast(bf16x8, xv), acc[i], 0, 0, 0);
-            }
+            for (int i = 0; i < TI; ++i) slot_nx[i] = slots[(info1 & 4095) + wm * WM + i * 32 + r];
         }
-        if (++i_k == kcount) {
-            i_k = 0;
-            ++c;
-            if (staged && s + 1 < stages) {
-                barrier_no_fence();  // every wave is done with this chunk's halo
-                issue_halo(c);
-            }
+        uint32_t info2 = 0;
+        if (s + 2 < total) {
+            // stage s + 2 into the ring slot stage s - 1 used
+            info2 = __builtin_amdgcn_readfirstlane(e2.x);
+            issue_w(__builtin_amdgcn_readfirstlane(e2.y), c2, r2);
+            adv(i2, c2);
+            r2 = r2 == WS - 1 ? 0 : r2 + 1;
+            if (s + 3 < total) e2 = ent[i2];
         }
+        bf16x8 af[2][TI];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+                af[kk][i] = *reinterpret_cast<const bf16x8 *>(halo + (slot[i] ^ pmask ^ (kk << 4)));
+        const bool last = ((info0 >> 18) & 1) && s + 1 < total;  // the halo is refilled in this stage
+        if (last) {
+            barrier_no_fence();  // every wave holds its operands from the halo
+            issue_h((info1 >> 12) & 31, i0 + 1 == kcount ? c0 + 1 : c0);
+        }
+        wait_all = last;
+        const char * wb = wring + (s % WS) * kWBytes;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int piece = 4 * h + kg * 2 + kk;
+            bf16x8 bfr[TJ];
+#pragma unroll
+            for (int jn = 0; jn < TJ; ++jn) {
+                const int row = wn * WN + jn * 32 + r;
+                bfr[jn] = *reinterpret_cast<const bf16x8 *>(wb + row * kChunkBytes + ((piece ^ swz(row)) << 4));
+            }
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int jn = 0; jn < TJ; ++jn)
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk][i], bfr[jn], acc[i][jn], 0, 0, 0);
+        }
+        info0 = info1;
+        info1 = info2;
+        adv(i0, c0);
     }
-    // Lane (h, r) holds row wm*64 + 32 i + r, channels wn*32 + 8 g + 4 h + e.
-    uint16_t * y = static_cast<uint16_t *>(a.y);
+
+    // Group 0 finishes the upper 32-row block of each wave's 64 rows, group 1
+    // the lower one; each hands the other half of its partial sums over
+    // through the (now idle) buffers, then the tile is staged in LDS as bf16
+    // and written as whole 16-byte row pieces.  (The kept block is a
+    // compile-time index in each branch: a run-time index into acc would put
+    // the accumulators in scratch memory.)
+    float * xch = reinterpret_cast<float *>(smem);
+    auto xslot = [&](int group, int jn, int v) { return (((group * NWG + wl) * TJ + jn) * 16 + v) * 64 + lane; };
+    auto finish = [&](auto keep_tag) __attribute__((always_inline)) {
+        constexpr int KEEP = decltype(keep_tag)::value, GIVE = 1 - KEEP;
+        f32x16 fin[TJ];
 #pragma unroll
-    for (int i = 0; i < TI; ++i) {
-        const int64_t row = p0 + wm * 64 + i * 32 + r;
-        if (row >= a.m) continue;
+        for (int jn = 0; jn < TJ; ++jn)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int ch = n0 + wn * 32 + 8 * g + 4 * h;
-            float v[4];
+            for (int v = 0; v < 16; ++v) xch[xslot(KEEP, jn, v)] = acc[GIVE][jn][v];
+        barrier_no_fence();
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[i][4 * g + e] + (a.bias ? a.bias[ch + e] : 0.0f);
-            uint2 u;
-            u.x = pack_bf16x2(v[0], v[1]);
-            u.y = pack_bf16x2(v[2], v[3]);
-            *reinterpret_cast<uint2 *>(y + row * a.ldy + ch) = u;
+        for (int jn = 0; jn < TJ; ++jn)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) fin[jn][v] = acc[KEEP][jn][v] + xch[xslot(GIVE, jn, v)];
+        barrier_no_fence();  // the exchange is read: the area may hold the staged tile
+#pragma unroll
+        for (int jn = 0; jn < TJ; ++jn) {
+            const int cl = wn * WN + jn * 32 + r;
+            const float b = (a.bias && n0 + cl < a.cout) ? a.bias[n0 + cl] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int rl = KEEP * 32 + wm * WM + 8 * (v >> 2) + 4 * h + (v & 3);
+                float val = fin[jn][v] + b;
+                if (a.act == PXS_ACT_GELU_TANH) val = gelu_tanh_f(val);
+                else if (a.act == PXS_ACT_SILU) val = silu_f(val);
+                *reinterpret_cast<uint16_t *>(smem + rl * kStagePitch + cl * 2) = f32_to_bf16(val);
+            }
         }
+    };
+    barrier_no_fence();
+    if (kg == 0) finish(std::integral_constant<int, 0>{});
+    else finish(std::integral_constant<int, 1>{});
+    barrier_no_fence();
+    uint16_t * y = static_cast<uint16_t *>(a.y);
+    for (int q = tid; q < BM * (BN / 8); q += NT) {
+        const int rl = q / (BN / 8), piece = q % (BN / 8);
+        const int64_t row = p0 + rl;
+        const int col = n0 + piece * 8;
+        if (row < a.m && col < a.cout)
+            *reinterpret_cast<uint4 *>(y + row * a.ldy + col) =
+                *reinterpret_cast<const uint4 *>(smem + rl * kStagePitch + piece * 16);
     }
 }
 
-int launch_halo_conv(const GemmArgs & args, hipStream_t stream) {
+template <int BN>
+int launch_range_conv(const GemmArgs & args, hipStream_t stream) {
+    constexpr int smem = range_lds_bytes<BN>();
     static bool configured = false;
     if (!configured) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&halo_conv_bf16_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kHaloLds);
-        if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(halo_conv)");
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&range_conv_bf16_kernel<BN>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+        if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(range_conv)");
         configured = true;
     }
-    const int64_t blocks = ((args.m + kHaloBM - 1) / kHaloBM) * (args.cout / kHaloBN);
-    if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "halo conv grid too large");
-    hipLaunchKernelGGL(halo_conv_bf16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kHaloNW * 64),
-                       kHaloLds, stream, args);
-    return check_launch("SubMConv3d (staged neighbourhood)");
+    const int64_t tiles = ((args.m + kRangeBM - 1) / kRangeBM) * ((args.cout + BN - 1) / BN);
+    const int64_t blocks = tiles + args.side_blocks;
+    if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "range conv grid too large");
+    if (args.side_blocks > 0 && smem < s2_emit_lds_bytes(args.s2.words_per_block, kRangeNW * 64))
+        return fail(PXS_ERR_ARG, "range conv: side work needs more LDS than the tile");
+    hipLaunchKernelGGL((range_conv_bf16_kernel<BN>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kRangeNW * 64), smem, stream, args);
+    return check_launch("SubMConv3d (neighbourhood ranges)");
 }
 
 // ---------------------------------------------------------------------------
@@ -1571,11 +1768,16 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
         return launch_split_f32<kEpiGateResidual>(args, stream);
     }
     if (dtype == PXS_BF16) {
-        if (PXS_GEMM_HALO && epi == kEpiStore && args.grid && args.noff == 27 && args.vec_ok &&
-            args.cin % 64 == 0 && args.cout % kHaloBN == 0 && args.ldx == args.cin &&
-            args.ldy == args.cout && args.m > 0 && (!args.bias || aligned16(args.bias)) &&
-            aligned16(args.y))
-            return launch_halo_conv(args, stream);
+        // SubMConv3d over a voxel grid: neighbourhood ranges.  (Over a
+        // neighbour map, the SLat decoder's 128-channel levels at up to 1024^3
+        // ran 3.7% slower on them: their planes' ranges exceed the halo more
+        // often, and 256-channel outputs on two 128-column range tiles 14%
+        // slower than one 128 x 256 gather tile.)
+        if (PXS_GEMM_RANGE && epi == kEpiStore && args.noff == 27 &&
+            args.grid && args.vec_ok && args.cin % 64 == 0 && args.m > 0 &&
+            args.cout > 64 && args.cout <= PXS_GEMM_RANGE_MAXN && args.cout % 8 == 0 &&
+            args.ldy % 8 == 0 && aligned16(args.y))
+            return launch_range_conv<128>(args, stream);
         if (epi == kEpiStore) return dispatch<uint16_t, kEpiStore>(args, stream);
         if (epi == kEpiAddResidual) return dispatch<uint16_t, kEpiAddResidual>(args, stream);
         return dispatch<uint16_t, kEpiGateResidual>(args, stream);
@@ -1842,10 +2044,10 @@ int pxs_subm_conv3d_grid_s2_emit(int dtype, const void * x, const int32_t * coor
     a.y = y; a.ldy = cout; a.act = PXS_ACT_NONE; a.coords = coords;
     a.grid = static_cast<const uint32_t *>(grid);
     a.grid_b = batch_size; a.grid_x = sx; a.grid_y = sy; a.grid_z = sz; a.grid_gen = generation;
-    // The bf16 16-byte path runs on the LDS-pipeline kernel, which carries the
-    // emit in side workgroups; otherwise the emit follows as its own launch.
-    const bool fuse = dtype == PXS_BF16 && cin % 8 == 0 && aligned16(x) && aligned16(weight) &&
-                      !PXS_GEMM_HALO;
+    // The bf16 16-byte path runs on the LDS-pipeline or neighbourhood-range
+    // kernel, both of which carry the emit in side workgroups; otherwise the
+    // emit follows as its own launch.
+    const bool fuse = dtype == PXS_BF16 && cin % 8 == 0 && aligned16(x) && aligned16(weight);
     if (fuse) {
         a.s2 = make_s2_emit_args(batch_size, sx, sy, sz, grid, generation, out_coords, child_map,
                                  ld_map, m_out, coarse_grid, s2_workspace, kS2SideWords);
@@ -1886,11 +2088,14 @@ int pxs_unet_s2_level(int dtype, const void * x, const int32_t * coords, int64_t
               std::string(who) + ": the grid must be 4-byte aligned");
     // The chain runs both convolutions on the default bf16 tile, the one
     // dispatch picks for a 27-offset gather of 65..128 outputs and an
-    // 8-offset gather of 16 K stages over more than 64 outputs.
+    // 8-offset gather of 16 K stages over more than 64 outputs.  Inputs of a
+    // multiple of 64 channels, whose SubMConv3d runs on neighbourhood ranges,
+    // take the two launches instead.
     constexpr bool kDefaultTile = PXS_GEMM_BM == 128 && PXS_GEMM_BN == 128 &&
                                   PXS_GEMM_STAGES == 2 && PXS_GEMM_WAVES == 8 &&
-                                  PXS_GEMM_KSPLIT == 2 && !PXS_GEMM_HALO;
-    const bool chain = kDefaultTile && dtype == PXS_BF16 && cin % 8 == 0 && cout_a % 8 == 0 &&
+                                  PXS_GEMM_KSPLIT == 2;
+    const bool ranged = PXS_GEMM_RANGE && cin % 64 == 0 && cout_a <= PXS_GEMM_RANGE_MAXN;
+    const bool chain = kDefaultTile && !ranged && dtype == PXS_BF16 && cin % 8 == 0 && cout_a % 8 == 0 &&
                        cout_a > 64 && cout_a <= 128 && cout_b > 64 && m > 0 && aligned16(x) &&
                        aligned16(w_a) && aligned16(y_a) && aligned16(w_b);
     if (!chain) {
