@@ -423,21 +423,6 @@ __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1
 #endif
 constexpr bool kMaskAbsent = PXS_GEMM_MASK_ABSENT != 0;
 
-// Stage order: offset-major (every K chunk of one offset, then the next
-// offset) or chunk-major (one K chunk over every present offset, then the
-// next chunk).  Chunk-major puts the offsets (kd, kh, 0..2), whose gathered
-// rows are mostly the same rows shifted by one, in consecutive stages.
-#ifndef PXS_GEMM_CHUNK_MAJOR
-#define PXS_GEMM_CHUNK_MAJOR 0
-#endif
-constexpr bool kChunkMajor = PXS_GEMM_CHUNK_MAJOR != 0;
-// Cache policy of the weight chunks' loads: 0 the default, 1 non-temporal
-// (nt), 2 device scope (sc1: read from L2 without allocating in the L1), so
-// they do not displace gathered rows from the L1 (every tile reads the same
-// weights; they stay in L2).
-#ifndef PXS_GEMM_W_CACHE
-#define PXS_GEMM_W_CACHE 0
-#endif
 
 template <int BM, int BN, int NSTAGE>
 constexpr int lds_gemm_bytes(int noff) {
@@ -658,8 +643,7 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
     }
 
     auto issue = [&](int s) {
-        const int i = kChunkMajor ? s % kcount : s / chunks;
-        const int chunk = kChunkMajor ? s / kcount : s - i * chunks;
+        const int i = s / chunks, chunk = s - i * chunks;
         const int k = koff[i];
         char * base = smem + (s % NSTAGE) * kStageBytes;
         int32_t src[AI];
@@ -687,12 +671,7 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
         for (int j = 0; j < BI; ++j) {
             const int col = chunk * kChunk + b_piece[j] * kVec;
             const void * g = (b_ok[j] && col < a.cin) ? static_cast<const void *>(w + kbase + b_off[j]) : zero;
-            if constexpr (PXS_GEMM_W_CACHE == 1)
-                lds_dma16_nt(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
-            else if constexpr (PXS_GEMM_W_CACHE == 2)
-                lds_dma16_coherent(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
-            else
-                lds_dma16(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
+            lds_dma16(g, lds_offset(base + (BM + (wave * BI + j) * 8) * kChunkBytes));
         }
     };
 
@@ -722,10 +701,7 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
         for (int i = 0; i < TI; ++i) {
             row_ok[i] = true;
             if constexpr (kMaskAbsent)
-            {
-                const int si = kChunkMajor ? s % kcount : s / chunks;
-                row_ok[i] = idx_lds[(full_table ? koff[si] : si) * BM + wm * WM + i * 32 + r] >= 0;
-            }
+                row_ok[i] = idx_lds[(full_table ? koff[s / chunks] : s / chunks) * BM + wm * WM + i * 32 + r] >= 0;
         }
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
@@ -1009,7 +985,10 @@ range_conv_bf16_kernel(GemmArgs a) {
     constexpr int kStagePitch = BN * 2 + 16;  // the output tile staged in LDS
     static_assert(BI >= 1 && TJ >= 1 && TI == 2, "tile shape");
     static_assert(27 * BM * 4 <= WS * kWBytes, "source table inside the weight ring");
-    static_assert(NW * HI * TJ * 16 * 64 * 4 <= range_lds_bytes<BN>(), "exchange fits");
+    // the K groups' partial sums are exchanged in XP passes over the column blocks
+    constexpr int XP = (NW * HI * TJ * 16 * 64 * 4 + range_lds_bytes<BN>() - 1) / range_lds_bytes<BN>();
+    constexpr int TJP = TJ / XP;
+    static_assert(TJP * XP == TJ, "exchange passes split the column blocks");
     static_assert(BM * kStagePitch <= range_lds_bytes<BN>(), "staged tile fits");
     extern __shared__ __align__(16) char smem[];
     const int tiles = static_cast<int>(gridDim.x) - a.side_blocks;
@@ -1331,20 +1310,24 @@ range_conv_bf16_kernel(GemmArgs a) {
     // compile-time index in each branch: a run-time index into acc would put
     // the accumulators in scratch memory.)
     float * xch = reinterpret_cast<float *>(smem);
-    auto xslot = [&](int group, int jn, int v) { return (((group * NWG + wl) * TJ + jn) * 16 + v) * 64 + lane; };
+    auto xslot = [&](int group, int jn, int v) { return (((group * NWG + wl) * TJP + jn) * 16 + v) * 64 + lane; };
     auto finish = [&](auto keep_tag) __attribute__((always_inline)) {
         constexpr int KEEP = decltype(keep_tag)::value, GIVE = 1 - KEEP;
         f32x16 fin[TJ];
 #pragma unroll
-        for (int jn = 0; jn < TJ; ++jn)
+        for (int pass = 0; pass < XP; ++pass) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) xch[xslot(KEEP, jn, v)] = acc[GIVE][jn][v];
-        barrier_no_fence();
+            for (int jn = 0; jn < TJP; ++jn)
 #pragma unroll
-        for (int jn = 0; jn < TJ; ++jn)
+                for (int v = 0; v < 16; ++v) xch[xslot(KEEP, jn, v)] = acc[GIVE][pass * TJP + jn][v];
+            barrier_no_fence();
 #pragma unroll
-            for (int v = 0; v < 16; ++v) fin[jn][v] = acc[KEEP][jn][v] + xch[xslot(GIVE, jn, v)];
-        barrier_no_fence();  // the exchange is read: the area may hold the staged tile
+            for (int jn = 0; jn < TJP; ++jn)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    fin[pass * TJP + jn][v] = acc[KEEP][pass * TJP + jn][v] + xch[xslot(GIVE, jn, v)];
+            barrier_no_fence();  // the exchange is read: the area may take the next pass or the staged tile
+        }
 #pragma unroll
         for (int jn = 0; jn < TJ; ++jn) {
             const int cl = wn * WN + jn * 32 + r;
@@ -1770,9 +1753,11 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
     if (dtype == PXS_BF16) {
         // SubMConv3d over a voxel grid: neighbourhood ranges.  (Over a
         // neighbour map, the SLat decoder's 128-channel levels at up to 1024^3
-        // ran 3.7% slower on them: their planes' ranges exceed the halo more
-        // often, and 256-channel outputs on two 128-column range tiles 14%
-        // slower than one 128 x 256 gather tile.)
+        // ran 3.7% slower on them.  The U-Net's 256 -> 256 conv at 64^3 ran
+        // 0.150 ms on two 128-column range tiles and 0.150 ms on one 256-column
+        // range tile, one workgroup per CU, against 0.133 ms on 128 x 256
+        // gather tiles: its 254 tiles are one round, so nothing hides a tile's
+        // prologue and halo switches.)
         if (PXS_GEMM_RANGE && epi == kEpiStore && args.noff == 27 &&
             args.grid && args.vec_ok && args.cin % 64 == 0 && args.m > 0 &&
             args.cout > 64 && args.cout <= PXS_GEMM_RANGE_MAXN && args.cout % 8 == 0 &&

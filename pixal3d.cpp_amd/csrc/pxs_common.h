@@ -136,15 +136,6 @@ __device__ __forceinline__ void lds_dma16(const void * g, uint32_t lds_base) {
                  : "m0");
 }
 
-// lds_dma16 as a non-temporal load (nt): data read once per workgroup that
-// should not displace reused lines from the L1.
-__device__ __forceinline__ void lds_dma16_nt(const void * g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
-                 :
-                 : "v"(g), "s"(lds_base)
-                 : "m0");
-}
-
 // lds_dma16 as a device-coherent load (sc1): it reads the level where data
 // that other workgroups of the same launch, on other XCDs, have released
 // (written back and flagged) is visible, instead of a line this XCD's L2 may
