@@ -370,15 +370,30 @@ def measured_traffic(op):
     return int(rec["read_bytes"] + rec["write_bytes"])
 
 
+def kernel_source_digest(rec):
+    """SHA-256 (first 16 hex digits) of the kernel sources a traffic record
+    names, as they are in this tree."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in rec.get("sources", []):
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()[:16]
+
+
 def traffic_note(op):
     """Where the traffic figure of `op` comes from (it is not measured in the
-    bench run: counters need the profiler)."""
+    bench run: counters need the profiler), and whether the kernel sources
+    are still the ones it was measured on."""
     path = ROOT / "profiles" / "unet_stage_128_traffic.json"
     rec = json.loads(path.read_text()).get(op) if path.exists() else None
     if not rec:
         return None
+    same = rec.get("sources_sha16") == kernel_source_digest(rec)
     return (f"not measured in this run: rocprofv3 --pmc of {rec['kernel']} (grid {rec['grid']}) "
-            f"at commit {rec['measured_at_commit']}, {rec['method']} ({rec['source']})")
+            f"at commit {rec['measured_at_commit']}, {rec['method']} ({rec['source']}); "
+            + (f"{', '.join(rec['sources'])} unchanged since" if same else
+               f"STALE: {', '.join(rec.get('sources', [])) or 'the kernel sources'} changed since"))
 
 
 def attention_metric(args, torch, px, W, heads=16, hd=64):

@@ -31,6 +31,18 @@ def test_traffic_comes_from_the_committed_summary():
     assert bench.measured_traffic("not_a_kernel") is None
 
 
+def test_traffic_note_flags_changed_kernel_sources(monkeypatch):
+    """The note names the commit the traffic was measured at and says whether
+    the kernel sources the record lists still hash as they did then."""
+    rec = json.loads((ROOT / "profiles" / "unet_stage_128_traffic.json").read_text())["subm_conv_a"]
+    assert rec["sources"] and all((ROOT / p).exists() for p in rec["sources"])
+    assert rec["measured_at_commit"] in bench.traffic_note("subm_conv_a")
+    monkeypatch.setattr(bench, "kernel_source_digest", lambda r: rec["sources_sha16"])
+    assert "unchanged since" in bench.traffic_note("subm_conv_a")
+    monkeypatch.setattr(bench, "kernel_source_digest", lambda r: "0" * 16)
+    assert "STALE" in bench.traffic_note("subm_conv_a")
+
+
 def test_cpu_threads_respect_every_limit(monkeypatch):
     monkeypatch.setenv("OMP_NUM_THREADS", "3")
     threads, limits = bench.cpu_threads()
