@@ -972,6 +972,27 @@ template <int BN> constexpr int range_lds_bytes() {
     return kRangeWStages * BN * kChunkBytes + kRangeHaloBytes + 27 * kRangeBM * 2;
 }
 
+// Min, max and or over each 16-lane row by DPP row shifts (VALU, no LDS
+// round trip): lane 15 of every row ends with its row's result.
+__device__ __forceinline__ int dpp_row_min(int v) {
+    v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x111, 0xf, 0xf, false));  // row_shr:1
+    v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x112, 0xf, 0xf, false));  // row_shr:2
+    v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x114, 0xf, 0xf, false));  // row_shr:4
+    return min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x118, 0xf, 0xf, false));  // row_shr:8
+}
+__device__ __forceinline__ int dpp_row_max(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x111, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x112, 0xf, 0xf, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x114, 0xf, 0xf, false));
+    return max(v, __builtin_amdgcn_update_dpp(-1, v, 0x118, 0xf, 0xf, false));
+}
+__device__ __forceinline__ uint32_t dpp_row_or(uint32_t v) {
+    v |= __builtin_amdgcn_update_dpp(0u, v, 0x111, 0xf, 0xf, false);
+    v |= __builtin_amdgcn_update_dpp(0u, v, 0x112, 0xf, 0xf, false);
+    v |= __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xf, 0xf, false);
+    return v | __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xf, 0xf, false);
+}
+
 template <int BN>
 __global__ void __launch_bounds__(kRangeNW * 64)
 range_conv_bf16_kernel(GemmArgs a) {
@@ -984,7 +1005,7 @@ range_conv_bf16_kernel(GemmArgs a) {
     constexpr int kWBytes = BN * kChunkBytes;
     constexpr int kStagePitch = BN * 2 + 16;  // the output tile staged in LDS
     static_assert(BI >= 1 && TJ >= 1 && TI == 2, "tile shape");
-    static_assert(27 * BM * 4 <= WS * kWBytes, "source table inside the weight ring");
+    static_assert(WS == 3 && 27 * BM * 4 <= kWBytes, "source table inside the third weight slot");
     // the K groups' partial sums are exchanged in XP passes over the column blocks
     constexpr int XP = (NW * HI * TJ * 16 * 64 * 4 + range_lds_bytes<BN>() - 1) / range_lds_bytes<BN>();
     constexpr int TJP = TJ / XP;
@@ -1002,7 +1023,8 @@ range_conv_bf16_kernel(GemmArgs a) {
     // offset k, row * 128 + (swz(row) << 4), so a lane's 16-byte piece P is at
     // slots ^ (P << 4)
     uint16_t * slots = reinterpret_cast<uint16_t *>(halo + kRangeHaloBytes);
-    int32_t * idx = reinterpret_cast<int32_t *>(smem);                     // prologue only
+    // prologue only, in the ring slot the first two stages' weights do not use
+    int32_t * idx = reinterpret_cast<int32_t *>(smem + 2 * kWBytes);
     __shared__ uint32_t tile_mask;
     __shared__ int rlo[9], rhi[9];        // source range of each kh row q = k / 3
     __shared__ int g_lo[27], g_rows[27];  // range start (-1 - k: offset k gathered), rows staged
@@ -1035,7 +1057,68 @@ range_conv_bf16_kernel(GemmArgs a) {
     }
     if (tid < 8) *reinterpret_cast<uint4 *>(halo + CAP * kChunkBytes + tid * 16) = make_uint4(0, 0, 0, 0);
     __syncthreads();
-    {
+    if (a.grid && a.grid_z >= 3) {
+        // Over a grid, the 3 offsets kw of a kh row q = (kd, kh) are the cells
+        // z - 1, z, z + 1 of one grid column: one 12-byte load each.  Thread:
+        // one row, kh rows q = part, part + 4, part + 8 (part wave-uniform).
+        const int row = tid % BM, part = tid / BM;
+        const int64_t p = p0 + row;
+        const bool live = p < a.m;
+        const int4 c = live ? crd[p] : make_int4(0, 0, 0, 0);
+        const int z0 = min(max(c.w - 1, 0), a.grid_z - 3);  // first cell loaded
+        uint32_t cell[3][3];
+        bool col_ok[3];
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            const int q = part + 4 * u;
+            const int x = c.y + q / 3 - 1, y = c.z + q % 3 - 1;
+            col_ok[u] = live && q < 9 && static_cast<unsigned>(c.x) < static_cast<unsigned>(a.grid_b) &&
+                        static_cast<unsigned>(x) < static_cast<unsigned>(a.grid_x) &&
+                        static_cast<unsigned>(y) < static_cast<unsigned>(a.grid_y);
+            if (col_ok[u]) {
+                typedef uint32_t u32x3 __attribute__((ext_vector_type(3), aligned(4)));
+                const u32x3 v = *reinterpret_cast<const u32x3 *>(
+                    a.grid + ((static_cast<int64_t>(c.x) * a.grid_x + x) * a.grid_y + y) * a.grid_z + z0);
+                cell[u][0] = v.x;
+                cell[u][1] = v.y;
+                cell[u][2] = v.z;
+            } else {
+                cell[u][0] = cell[u][1] = cell[u][2] = kVoxelGridEmpty;
+            }
+        }
+        uint32_t local = 0;
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            const int q = part + 4 * u;
+            if (q >= 9) break;  // wave-uniform
+            int lo = INT_MAX, hi = -1;
+#pragma unroll
+            for (int dz = 0; dz < 3; ++dz) {
+                const int k = 3 * q + dz, z = c.w + dz - 1;
+                int32_t src = -1;
+                if (col_ok[u] && static_cast<unsigned>(z) < static_cast<unsigned>(a.grid_z)) {
+                    const int e = z - z0;  // 0..2, selected without indexing the registers
+                    const uint32_t v = e == 0 ? cell[u][0] : (e == 1 ? cell[u][1] : cell[u][2]);
+                    src = k == 13 ? static_cast<int32_t>(p) : voxel_grid_row(v, a.grid_gen);
+                    if (src >= a.rows_in) src = -1;
+                }
+                idx[k * BM + row] = src;
+                if (src >= 0) {
+                    local |= 1u << k;
+                    lo = min(lo, src);
+                    hi = max(hi, src);
+                }
+            }
+            lo = dpp_row_min(lo);
+            hi = dpp_row_max(hi);
+            if ((lane & 15) == 15 && hi >= 0) {
+                atomicMin(&rlo[q], lo);
+                atomicMax(&rhi[q], hi);
+            }
+        }
+        local = dpp_row_or(local);
+        if ((lane & 15) == 15 && local) atomicOr(&tile_mask, local);
+    } else {
         // Thread: one row, offsets [kb, kb + 7) (kb wave-uniform); all its
         // lookups are issued before any is used.
         const int row = tid % BM, kb = 7 * (tid / BM);
@@ -1072,12 +1155,9 @@ range_conv_bf16_kernel(GemmArgs a) {
                 hi = max(hi, src[i]);
             }
             if (k % 3 == 2 || i == 6) {  // the end of a kh row or of this thread's offsets
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) {
-                    lo = min(lo, __shfl_xor(lo, o));
-                    hi = max(hi, __shfl_xor(hi, o));
-                }
-                if (lane == 0 && hi >= 0) {
+                lo = dpp_row_min(lo);
+                hi = dpp_row_max(hi);
+                if ((lane & 15) == 15 && hi >= 0) {
                     atomicMin(&rlo[k / 3], lo);
                     atomicMax(&rhi[k / 3], hi);
                 }
@@ -1085,9 +1165,8 @@ range_conv_bf16_kernel(GemmArgs a) {
                 hi = -1;
             }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) local |= __shfl_xor(local, o);
-        if (lane == 0 && local) atomicOr(&tile_mask, local);
+        local = dpp_row_or(local);
+        if ((lane & 15) == 15 && local) atomicOr(&tile_mask, local);
     }
     __syncthreads();
     // ---- the groups and the stage sequence (wave 0, every lane the same
@@ -1140,15 +1219,6 @@ range_conv_bf16_kernel(GemmArgs a) {
         if (lane == 0) n_pos = __popc(present);
     }
     __syncthreads();
-    for (int e = tid; e < 27 * BM; e += NT) {
-        const int k = e / BM, row = e % BM;  // k wave-uniform
-        if (!((tile_mask >> k) & 1u)) continue;
-        const int32_t src = idx[e];
-        const int lo = g_lo[g_of[k]];
-        const int sl = src < 0 ? CAP : (lo < 0 ? row : src - lo);
-        slots[e] = static_cast<uint16_t>(sl * kChunkBytes + (swz(sl) << 4));
-    }
-    __syncthreads();  // the source table is dead: the weight ring may be filled
 
     const int kcount = __builtin_amdgcn_readfirstlane(n_pos);  // stages per chunk
     const int total = (a.cin / 64) * kcount;
@@ -1239,6 +1309,17 @@ range_conv_bf16_kernel(GemmArgs a) {
             adv(i2, c2);
         }
         if (total > 2) e2 = ent[i2];
+    }
+    for (int e = tid; e < 27 * BM; e += NT) {
+        const int k = e / BM, row = e % BM;  // k wave-uniform
+        if (!((tile_mask >> k) & 1u)) continue;
+        const int32_t src = idx[e];
+        const int lo = g_lo[g_of[k]];
+        const int sl = src < 0 ? CAP : (lo < 0 ? row : src - lo);
+        slots[e] = static_cast<uint16_t>(sl * kChunkBytes + (swz(sl) << 4));
+    }
+    barrier_no_fence();  // the slot table is complete (no fence: the first DMAs stay in flight)
+    if (total > 0) {
 #pragma unroll
         for (int i = 0; i < TI; ++i) slot_nx[i] = slots[(info0 & 4095) + wm * WM + i * 32 + r];
         if (total > 1) wait_vmcnt(BI);
