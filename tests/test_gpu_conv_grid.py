@@ -52,6 +52,12 @@ CASES = [
     ("box_bf16", lambda: _box_coords(8, 2, (6, 5, 7), 0.5), 2, (6, 5, 7), 32, 256, "bf16"),
     ("box_odd_f32", lambda: _box_coords(9, 1, (5, 9, 4), 0.6), 1, (5, 9, 4), 3, 5, "f32"),
     ("box_odd_bf16", lambda: _box_coords(10, 1, (5, 9, 4), 0.6), 1, (5, 9, 4), 12, 20, "bf16"),
+    # neighbourhood ranges: four 64-channel chunks and 96 outputs (the last
+    # weight rows of the 128-column tile repeat row 95); a grid only 2 deep
+    # in z (each offset looked up on its own instead of three cells a load)
+    ("ranges_cin256_bf16", lambda: _box_coords(16, 2, (20, 18, 22), 0.35), 2, (20, 18, 22), 256, 96,
+     "bf16"),
+    ("ranges_z2_bf16", lambda: _box_coords(17, 2, (30, 26, 2), 0.8), 2, (30, 26, 2), 64, 72, "bf16"),
 ]
 
 
@@ -141,6 +147,25 @@ def test_conv_grid_range_gathered_planes(px, orc, cin):
     grid = px.grid_build(c, 2, (24, 72, 72))
     y = px.subm_conv3d_grid(tbf(x), tbf(w), t32(b), c, 2, (24, 72, 72), grid, 0)
     assert_bf16(host(y), orc.subm_conv3d(coords, x, w, b), what="slab on neighbourhood ranges")
+
+
+@pytest.mark.parametrize("name,make,batch,shape,cin,cout", [
+    ("cin256_cout96", lambda: _box_coords(16, 2, (20, 18, 22), 0.35), 2, (20, 18, 22), 256, 96),
+    ("z2_cout72", lambda: _box_coords(17, 2, (30, 26, 2), 0.8), 2, (30, 26, 2), 64, 72)])
+def test_conv_grid_range_shapes_vs_oracle(px, orc, name, make, batch, shape, cin, cout):
+    """Neighbourhood ranges over more K chunks, a partial column tile and the
+    per-offset lookups of a grid under 3 cells deep, against the oracle."""
+    coords = make()
+    n = coords.shape[0]
+    x = W.bf16_round(W.normal(47, n * cin, 1).reshape(n, cin))
+    w = W.bf16_round(W.normal(47, 27 * cout * cin, 2, std=float(np.sqrt(2 / (27 * cin))))
+                     .reshape(27, cout, cin))
+    b = W.normal(47, cout, 3, std=0.1)
+    print(f"[conv grid ranges] {name} n={n} {cin}->{cout}", flush=True)
+    c = ti32(coords)
+    grid = px.grid_build(c, batch, shape)
+    y = px.subm_conv3d_grid(tbf(x), tbf(w), t32(b), c, batch, shape, grid, 0)
+    assert_bf16(host(y), orc.subm_conv3d(coords, x, w, b), what=f"ranges {name}")
 
 
 def test_conv_grid_fp32_vs_oracle(px, orc):
