@@ -88,12 +88,58 @@ __device__ __forceinline__ int32_t grid_src(const GemmArgs & a, int4 c, int k, i
 // row] (-1 absent or past the end), OR-ing each row's present offsets into
 // *tile_mask.  Each thread takes one row and a quarter of the offsets, so a
 // row's coordinates are read once per thread.
+//
+// Over a grid at least 3 cells deep in z, the 3 offsets kw of a kh row q =
+// (kd, kh) are the cells z - 1, z, z + 1 of one grid column: each thread takes
+// one row and the kh rows q = part, part + 4, part + 8, one 12-byte load each.
 template <int BM>
 __device__ __forceinline__ void grid_tile_sources(const GemmArgs & a, int64_t p0, int tid,
                                                   int nthreads, int32_t * idx,
                                                   uint32_t * tile_mask) {
     const int4 * crd = reinterpret_cast<const int4 *>(a.coords);
     uint32_t local = 0;
+    if (a.grid_z >= 3) {
+        for (int t = tid; t < 4 * BM; t += nthreads) {
+            const int row = t % BM, part = t / BM;
+            const int64_t p = p0 + row;
+            const bool live = p < a.m;
+            const int4 c = live ? crd[p] : make_int4(0, 0, 0, 0);
+            const int z0 = min(max(c.w - 1, 0), a.grid_z - 3);  // first cell loaded
+#pragma unroll
+            for (int u = 0; u < 3; ++u) {
+                const int q = part + 4 * u;
+                if (q >= 9) break;
+                const int x = c.y + q / 3 - 1, y = c.z + q % 3 - 1;
+                const bool ok = live && static_cast<unsigned>(c.x) < static_cast<unsigned>(a.grid_b) &&
+                                static_cast<unsigned>(x) < static_cast<unsigned>(a.grid_x) &&
+                                static_cast<unsigned>(y) < static_cast<unsigned>(a.grid_y);
+                uint32_t cell[3] = {kVoxelGridEmpty, kVoxelGridEmpty, kVoxelGridEmpty};
+                if (ok) {
+                    typedef uint32_t u32x3 __attribute__((ext_vector_type(3), aligned(4)));
+                    const u32x3 v = *reinterpret_cast<const u32x3 *>(
+                        a.grid + ((static_cast<int64_t>(c.x) * a.grid_x + x) * a.grid_y + y) * a.grid_z + z0);
+                    cell[0] = v.x;
+                    cell[1] = v.y;
+                    cell[2] = v.z;
+                }
+#pragma unroll
+                for (int dz = 0; dz < 3; ++dz) {
+                    const int k = 3 * q + dz, z = c.w + dz - 1;
+                    int32_t src = -1;
+                    if (ok && static_cast<unsigned>(z) < static_cast<unsigned>(a.grid_z)) {
+                        const int e = z - z0;  // 0..2, selected without indexing the registers
+                        const uint32_t v = e == 0 ? cell[0] : (e == 1 ? cell[1] : cell[2]);
+                        src = k == 13 ? static_cast<int32_t>(p) : voxel_grid_row(v, a.grid_gen);
+                        if (src >= a.rows_in) src = -1;
+                    }
+                    idx[k * BM + row] = src;
+                    if (src >= 0) local |= 1u << k;
+                }
+            }
+        }
+        if (local) atomicOr(tile_mask, local);
+        return;
+    }
     for (int t = tid; t < 4 * BM; t += nthreads) {
         const int row = t % BM, kb = (t / BM) * 7, ke = kb + 7 < 27 ? kb + 7 : 27;
         const int64_t p = p0 + row;
