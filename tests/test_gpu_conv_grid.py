@@ -168,6 +168,44 @@ def test_conv_grid_range_shapes_vs_oracle(px, orc, name, make, batch, shape, cin
     assert_bf16(host(y), orc.subm_conv3d(coords, x, w, b), what=f"ranges {name}")
 
 
+RANDOM_RANGE_CASES = [
+    # (seed, batch, extents, density, cin, cout, tagged)
+    (101, 1, (12, 40, 9), 0.5, 64, 128, False),
+    (102, 3, (17, 13, 29), 0.15, 128, 72, True),
+    (103, 2, (33, 9, 3), 0.9, 192, 104, False),
+    (104, 1, (64, 64, 5), 0.05, 64, 128, True),
+    (105, 2, (7, 70, 31), 0.3, 128, 128, False),
+]
+
+
+@pytest.mark.parametrize("seed,batch,shape,density,cin,cout,tagged", RANDOM_RANGE_CASES,
+                         ids=[f"seed{c[0]}" for c in RANDOM_RANGE_CASES])
+def test_conv_grid_range_random_boxes(px, orc, seed, batch, shape, density, cin, cout, tagged):
+    """Neighbourhood ranges on random voxel sets: densities from 5% to 90%
+    (planes staged whole, per kh row or per offset), thin and wide extents
+    (z down to 3 cells), 1-3 batch items, 1-3 K chunks, partial column tiles,
+    plain and tagged grids (the tagged grid first holding an older
+    generation's voxels); against the oracle."""
+    rng = np.random.default_rng(seed)
+    coords = np.ascontiguousarray(np.argwhere(rng.random((batch,) + shape) < density).astype(np.int32))
+    n = coords.shape[0]
+    x = W.bf16_round(rng.standard_normal((n, cin)).astype(np.float32))
+    w = W.bf16_round((rng.standard_normal((27, cout, cin)) * (2.0 / (27 * cin)) ** 0.5).astype(np.float32))
+    b = (rng.standard_normal(cout) * 0.1).astype(np.float32)
+    print(f"[conv grid ranges, random] seed={seed} n={n} {cin}->{cout} tagged={tagged}", flush=True)
+    c = ti32(coords)
+    if tagged:
+        grid = px.tagged_grid(batch, shape)
+        other = np.ascontiguousarray(coords[::2].copy())
+        px.tagged_insert(ti32(other), batch, shape, grid, 5)
+        px.tagged_insert(c, batch, shape, grid, 6)
+        y = px.subm_conv3d_grid(tbf(x), tbf(w), t32(b), c, batch, shape, grid, 6)
+    else:
+        grid = px.grid_build(c, batch, shape)
+        y = px.subm_conv3d_grid(tbf(x), tbf(w), t32(b), c, batch, shape, grid, 0)
+    assert_bf16(host(y), orc.subm_conv3d(coords, x, w, b), what=f"random ranges seed {seed}")
+
+
 def test_conv_grid_fp32_vs_oracle(px, orc):
     """The reference's CPU-runnable case through the grid convolution, against
     the oracle at the fp32 bar."""
