@@ -223,6 +223,46 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs & a, const f32x16 (
     }
 }
 
+// The bf16 store epilogue through LDS.  Each lane writes its 32x32 blocks
+// (bias and activation applied) into a BM x BN tile staged at `stage`; tile
+// rows row0 + wm*WM + i*32 + ... come from this call's accumulators.  Then the
+// workgroup writes whole 16-byte row pieces, where 2-byte element stores
+// would take eight times the store instructions.  The caller has made
+// `stage` free; cout and ldy are multiples of 8 and y is 16-byte aligned.
+template <int BM, int BN, int TI, int TJ, int WM, int WN, int NT, bool COHERENT>
+__device__ __forceinline__ void gemm_epilogue_staged(const GemmArgs & a, const f32x16 (&acc)[TI][TJ],
+                                                     char * stage, int64_t p0, int n0, int row0,
+                                                     int wm, int wn, int h, int r, int tid) {
+    constexpr int kPitch = BN * 2 + 16;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int cl = wn * WN + j * 32 + r;
+            const float b = (a.bias && n0 + cl < a.cout) ? a.bias[n0 + cl] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int rl = row0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                float val = acc[i][j][v] + b;
+                if (a.act == PXS_ACT_GELU_TANH) val = gelu_tanh_f(val);
+                else if (a.act == PXS_ACT_SILU) val = silu_f(val);
+                *reinterpret_cast<uint16_t *>(stage + rl * kPitch + cl * 2) = f32_to_bf16(val);
+            }
+        }
+    barrier_no_fence();
+    uint16_t * y = static_cast<uint16_t *>(a.y);
+    for (int q = tid; q < BM * (BN / 8); q += NT) {
+        const int rl = q / (BN / 8), piece = q % (BN / 8);
+        const int64_t row = p0 + rl;
+        const int col = n0 + piece * 8;
+        if (row < a.m && col < a.cout) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(stage + rl * kPitch + piece * 16);
+            if constexpr (COHERENT) store16_coherent(y + row * a.ldy + col, v);
+            else *reinterpret_cast<uint4 *>(y + row * a.ldy + col) = v;
+        }
+    }
+}
+
 template <typename T, int BM, int BN, int EPI>
 __global__ void __launch_bounds__(kGemmThreads)
 gather_gemm_kernel(GemmArgs a) {
@@ -815,11 +855,28 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
     // A producer of the chained launch stores device-coherently.
     bool coherent_y = false;
     if constexpr (SYNC) coherent_y = sync.done_flags != nullptr;
+    // bf16 stores go through a tile staged in the stage buffers when it fits
+    // there and whole 16-byte row pieces are aligned (the same for every
+    // thread of the launch).
+    constexpr int kStagedPitch = BN * 2 + 16;
+    constexpr bool kStageable =
+        EPI == kEpiStore && sizeof(T) == 2 && BM * kStagedPitch <= NSTAGE * kStageBytes;
+    const bool staged = kStageable && a.cout % 8 == 0 && a.ldy % 8 == 0 &&
+                        (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
     if constexpr (KSPLIT == 1) {
-        if (SYNC && coherent_y)
+        if (kStageable && staged) {
+            barrier_no_fence();  // every wave is done reading the stage buffers
+            if (SYNC && coherent_y)
+                gemm_epilogue_staged<BM, BN, TI, TJ, WM, WN, kThreads, true>(a, acc, smem, p0, n0, 0, wm, wn,
+                                                                           h, r, tid);
+            else
+                gemm_epilogue_staged<BM, BN, TI, TJ, WM, WN, kThreads, false>(a, acc, smem, p0, n0, 0, wm, wn,
+                                                                            h, r, tid);
+        } else if (SYNC && coherent_y) {
             gemm_epilogue<T, TI, TJ, WM, WN, EPI, true>(a, acc, p0, n0, wm, wn, h, r);
-        else
+        } else {
             gemm_epilogue<T, TI, TJ, WM, WN, EPI>(a, acc, p0, n0, wm, wn, h, r);
+        }
     } else {
         // Group 0 finishes the upper 32-row blocks of each wave's tile and
         // group 1 the lower ones; each hands the other half of its partial
@@ -860,40 +917,19 @@ __device__ __forceinline__ void gemm_lds_tile(const GemmArgs & a, int logical, c
                             fin[i][pass * TJP + j][v] =
                                 acc[KEEP + i][pass * TJP + j][v] + xch[slot(1 - kg, i, j, v)];
             }
-            if (SYNC && coherent_y) {
-                // A producer of the chained launch stages its tile in LDS and
-                // writes whole 16-byte pieces device-coherently (2-byte
-                // write-through stores would each go to memory on their own).
-                if constexpr (EPI == kEpiStore && sizeof(T) == 2) {
-                    constexpr int kPitch = BN * 2 + 16;
-                    static_assert(BM * kPitch <= NSTAGE * kStageBytes, "staged tile fits the stages");
-                    barrier_no_fence();  // the partner's sums are read: the exchange area is free
-                    char * stage = smem;
-#pragma unroll
-                    for (int i = 0; i < HI; ++i)
-#pragma unroll
-                        for (int j = 0; j < TJ; ++j) {
-                            const int cl = wn * WN + j * 32 + r;
-                            const float b = (a.bias && n0 + cl < a.cout) ? a.bias[n0 + cl] : 0.0f;
-#pragma unroll
-                            for (int v = 0; v < 16; ++v) {
-                                const int rl = KEEP * 32 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                                *reinterpret_cast<uint16_t *>(stage + rl * kPitch + cl * 2) =
-                                    f32_to_bf16(fin[i][j][v] + b);
-                            }
-                        }
-                    barrier_no_fence();
-                    for (int q = tid; q < BM * (BN / 8); q += kThreads) {
-                        const int rl = q / (BN / 8), piece = q % (BN / 8);
-                        const int64_t row = p0 + rl;
-                        const int col = n0 + piece * 8;
-                        if (row < a.m && col < a.cout)
-                            store16_coherent(static_cast<T *>(a.y) + row * a.ldy + col,
-                                             *reinterpret_cast<const uint4 *>(stage + rl * kPitch + piece * 16));
-                    }
-                } else {
-                    gemm_epilogue<T, HI, TJ, WM, WN, EPI, true>(a, fin, p0 + KEEP * 32, n0, wm, wn, h, r);
-                }
+            if (kStageable && staged) {
+                // A producer of the chained launch writes whole 16-byte
+                // pieces device-coherently (2-byte write-through stores would
+                // each go to memory on their own).
+                barrier_no_fence();  // the partner's sums are read: the exchange area is free
+                if (SYNC && coherent_y)
+                    gemm_epilogue_staged<BM, BN, HI, TJ, WM, WN, kThreads, true>(a, fin, smem, p0, n0, KEEP * 32,
+                                                                               wm, wn, h, r, tid);
+                else
+                    gemm_epilogue_staged<BM, BN, HI, TJ, WM, WN, kThreads, false>(a, fin, smem, p0, n0, KEEP * 32,
+                                                                                wm, wn, h, r, tid);
+            } else if (SYNC && coherent_y) {
+                gemm_epilogue<T, HI, TJ, WM, WN, EPI, true>(a, fin, p0 + KEEP * 32, n0, wm, wn, h, r);
             } else {
                 gemm_epilogue<T, HI, TJ, WM, WN, EPI>(a, fin, p0 + KEEP * 32, n0, wm, wn, h, r);
             }
