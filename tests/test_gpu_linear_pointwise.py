@@ -408,6 +408,41 @@ def test_linear_dense_config_shapes(px, rows, cin, cout, form):
                 what=f"{form} {rows}x{cin}->{cout}")
 
 
+# 256 x 256 tiles over hundreds of tiles: every output row of the three
+# epilogues against a float32 product of the same bf16 operands on the
+# device, row by row, so a tile stored at the wrong place or a K chunk
+# carried into the wrong tile shows in the rows it touches.  Rows, K and
+# outputs are ragged against the tile and the 64-element chunk.
+@pytest.mark.parametrize("rows,cin,cout", [(16500, 520, 2000), (33000, 1024, 1024)])
+def test_linear_dense_large_tiles_every_row(px, rows, cin, cout):
+    import torch
+    print(f"[linear dense 256x256 every row] {rows}x{cin}->{cout}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows + cin)
+    x = torch.randn(rows, cin, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(cout, cin, device="cuda", generator=g) * cin ** -0.5).to(torch.bfloat16)
+    b = torch.randn(cout, device="cuda", generator=g) * 0.1
+    want = (x.float() @ w.float().t().contiguous()) + b
+
+    def rows_ok(got, ref, what):
+        err = (got.double() - ref.double()).norm(dim=1) / ref.double().norm(dim=1).clamp_min(1e-30)
+        worst = int(err.argmax())
+        assert float(err.max()) <= 1e-2, f"{what}: row {worst} rel L2 {float(err.max()):.3e}"
+
+    rows_ok(px.linear(x, w, b).float(), want, "plain")
+    res0 = torch.randn(rows, cout, device="cuda", generator=g)
+    res = res0.clone()
+    px.linear_residual(x, w, b, res)
+    rows_ok(res - res0, want, "residual")
+    batch = torch.zeros(rows, 4, dtype=torch.int32, device="cuda")
+    batch[rows // 3:, 0] = 1
+    bmod = torch.randn(6 * cout, device="cuda", generator=g)
+    tmod = torch.randn(2 * 6 * cout, device="cuda", generator=g)
+    res = res0.clone()
+    px.linear_gate_residual(x, w, b, batch, bmod, tmod, cout, res)
+    gate = bmod[cout:2 * cout][None, :] + tmod.view(2, 6 * cout)[batch[:, 0].long(), cout:2 * cout]
+    rows_ok(res - res0, want * gate, "gate")
+
+
 def _ref_bench_values(count, salt, scale, start=0):
     """tests/sparse_linear_cuda_benchmark.cpp:188-199 (deterministic_value):
     bucket = ((index * 6364136223846793005 + salt) >> 32) % 251 - 125, times
