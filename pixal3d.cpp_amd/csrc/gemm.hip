@@ -1035,23 +1035,30 @@ gather_gemm_lds_chain_kernel(GemmArgs a, GemmArgs b, ChainArgs c) {
 // Pipeline: a 3-stage weight ring (each stage's weights issued two stages
 // ahead) and one halo buffer, which the next (group, chunk) refills after
 // every wave has read its operands of the group's last stage (a barrier
-// inside that stage, the DMA then overlapping its MFMAs); 78 KB of LDS, so
-// two workgroups share a CU; 8 waves in two K groups of 2 x 2 blocks
-// (64 x BN/2 each).  Stages run chunk by chunk, within a chunk group by group
+// inside that stage, the DMA then overlapping its MFMAs); 8 waves in two K
+// groups of 2 x 2 blocks (64 x BN/2 each).  BN = 128 with a 192-row halo is
+// 79 KB of LDS, so two workgroups share a CU; BN = 256 with a 256-row halo
+// (outputs of 129..256 channels) is 136 KB, one workgroup per CU, 207 VGPRs.
+// Stages run chunk by chunk, within a chunk group by group
 // (planes ascending), within a group offsets ascending.  The tile is written
 // through LDS as whole 16-byte row pieces.
 #ifndef PXS_GEMM_RANGE
 #define PXS_GEMM_RANGE 1
 #endif
-// Widest output for which the range kernel is used (conv C, 256 channels,
-// keeps its 128 x 256 gather tiles unless this is raised).
+// Widest output of the 128-column range tile; wider outputs up to 256 take
+// the 256-column tile (PXS_GEMM_RANGE_WIDE = 0 keeps them on gather tiles).
 #ifndef PXS_GEMM_RANGE_MAXN
 #define PXS_GEMM_RANGE_MAXN 128
 #endif
-constexpr int kRangeBM = 128, kRangeNW = 8, kRangeCap = 192, kRangeWStages = 3;
-constexpr int kRangeHaloBytes = (kRangeCap + 1) * kChunkBytes;  // its zero row last
-template <int BN> constexpr int range_lds_bytes() {
-    return kRangeWStages * BN * kChunkBytes + kRangeHaloBytes + 27 * kRangeBM * 2;
+#ifndef PXS_GEMM_RANGE_WIDE
+#define PXS_GEMM_RANGE_WIDE 1
+#endif
+// Halo rows: 192 for the 128-column tile (the most two workgroups per CU
+// leave), 256 for the 256-column tile (one workgroup per CU).
+constexpr int kRangeBM = 128, kRangeNW = 8, kRangeCap = 192, kRangeWideCap = 256, kRangeWStages = 3;
+template <int CAP> constexpr int range_halo_bytes() { return (CAP + 1) * kChunkBytes; }  // its zero row last
+template <int BN, int CAP> constexpr int range_lds_bytes() {
+    return kRangeWStages * BN * kChunkBytes + range_halo_bytes<CAP>() + 27 * kRangeBM * 2;
 }
 
 // Min, max and or over each 16-lane row by DPP row shifts (VALU, no LDS
@@ -1075,10 +1082,10 @@ __device__ __forceinline__ uint32_t dpp_row_or(uint32_t v) {
     return v | __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xf, 0xf, false);
 }
 
-template <int BN>
+template <int BN, int CAP>
 __global__ void __launch_bounds__(kRangeNW * 64)
 range_conv_bf16_kernel(GemmArgs a) {
-    constexpr int BM = kRangeBM, NW = kRangeNW, CAP = kRangeCap, NT = NW * 64, WS = kRangeWStages;
+    constexpr int BM = kRangeBM, NW = kRangeNW, NT = NW * 64, WS = kRangeWStages;
     constexpr int NWG = NW / 2;               // waves per K group
     constexpr int WAVES_N = 2;                // each group: 2 x 2 blocks
     constexpr int WM = BM / 2, WN = BN / WAVES_N;
@@ -1089,10 +1096,10 @@ range_conv_bf16_kernel(GemmArgs a) {
     static_assert(BI >= 1 && TJ >= 1 && TI == 2, "tile shape");
     static_assert(WS == 3 && 27 * BM * 4 <= kWBytes, "source table inside the third weight slot");
     // the K groups' partial sums are exchanged in XP passes over the column blocks
-    constexpr int XP = (NW * HI * TJ * 16 * 64 * 4 + range_lds_bytes<BN>() - 1) / range_lds_bytes<BN>();
+    constexpr int XP = (NW * HI * TJ * 16 * 64 * 4 + range_lds_bytes<BN, CAP>() - 1) / range_lds_bytes<BN, CAP>();
     constexpr int TJP = TJ / XP;
     static_assert(TJP * XP == TJ, "exchange passes split the column blocks");
-    static_assert(BM * kStagePitch <= range_lds_bytes<BN>(), "staged tile fits");
+    static_assert(BM * kStagePitch <= range_lds_bytes<BN, CAP>(), "staged tile fits");
     extern __shared__ __align__(16) char smem[];
     const int tiles = static_cast<int>(gridDim.x) - a.side_blocks;
     if (static_cast<int>(blockIdx.x) >= tiles) {
@@ -1104,7 +1111,7 @@ range_conv_bf16_kernel(GemmArgs a) {
     // slots[k][p]: byte address in the halo of output row p's operand at
     // offset k, row * 128 + (swz(row) << 4), so a lane's 16-byte piece P is at
     // slots ^ (P << 4)
-    uint16_t * slots = reinterpret_cast<uint16_t *>(halo + kRangeHaloBytes);
+    uint16_t * slots = reinterpret_cast<uint16_t *>(halo + range_halo_bytes<CAP>());
     // prologue only, in the ring slot the first two stages' weights do not use
     int32_t * idx = reinterpret_cast<int32_t *>(smem + 2 * kWBytes);
     __shared__ uint32_t tile_mask;
@@ -1520,12 +1527,12 @@ range_conv_bf16_kernel(GemmArgs a) {
     }
 }
 
-template <int BN>
+template <int BN, int CAP>
 int launch_range_conv(const GemmArgs & args, hipStream_t stream) {
-    constexpr int smem = range_lds_bytes<BN>();
+    constexpr int smem = range_lds_bytes<BN, CAP>();
     static bool configured = false;
     if (!configured) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&range_conv_bf16_kernel<BN>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&range_conv_bf16_kernel<BN, CAP>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, smem);
         if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(range_conv)");
         configured = true;
@@ -1535,7 +1542,7 @@ int launch_range_conv(const GemmArgs & args, hipStream_t stream) {
     if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "range conv grid too large");
     if (args.side_blocks > 0 && smem < s2_emit_lds_bytes(args.s2.words_per_block, kRangeNW * 64))
         return fail(PXS_ERR_ARG, "range conv: side work needs more LDS than the tile");
-    hipLaunchKernelGGL((range_conv_bf16_kernel<BN>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((range_conv_bf16_kernel<BN, CAP>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kRangeNW * 64), smem, stream, args);
     return check_launch("SubMConv3d (neighbourhood ranges)");
 }
@@ -1914,18 +1921,23 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
         return launch_split_f32<kEpiGateResidual>(args, stream);
     }
     if (dtype == PXS_BF16) {
-        // SubMConv3d over a voxel grid: neighbourhood ranges.  (Over a
-        // neighbour map, the SLat decoder's 128-channel levels at up to 1024^3
-        // ran 3.7% slower on them.  The U-Net's 256 -> 256 conv at 64^3 ran
-        // 0.150 ms on two 128-column range tiles and 0.150 ms on one 256-column
-        // range tile, one workgroup per CU, against 0.133 ms on 128 x 256
-        // gather tiles: its 254 tiles are one round, so nothing hides a tile's
-        // prologue and halo switches.)
-        if (PXS_GEMM_RANGE && epi == kEpiStore && args.noff == 27 &&
-            args.grid && args.vec_ok && args.cin % 64 == 0 && args.m > 0 &&
-            args.cout > 64 && args.cout <= PXS_GEMM_RANGE_MAXN && args.cout % 8 == 0 &&
-            args.ldy % 8 == 0 && aligned16(args.y))
-            return launch_range_conv<128>(args, stream);
+        // SubMConv3d over a voxel grid: neighbourhood ranges.  65..128
+        // outputs: 128-column tiles with a 192-row halo, two workgroups per
+        // CU.  129..256 outputs: one 256-column tile with a 256-row halo per
+        // CU (136 KB of LDS), which stages every plane of the U-Net's coarse
+        // rows whole: its 256 -> 256 conv at 64^3 (254 tiles, one round)
+        // 0.118-0.119 ms against 0.128-0.129 ms on 128 x 256 gather tiles, and
+        // 0.151 ms with a 192-row halo, whose kh-row and per-offset fallbacks
+        // nothing hides at one workgroup per CU.  (Over a neighbour map, the
+        // SLat decoder's 128-channel levels at up to 1024^3 ran 3.7% slower on
+        // ranges.)
+        const bool range_ok = PXS_GEMM_RANGE && epi == kEpiStore && args.noff == 27 && args.grid &&
+                              args.vec_ok && args.cin % 64 == 0 && args.m > 0 && args.cout % 8 == 0 &&
+                              args.ldy % 8 == 0 && aligned16(args.y);
+        if (range_ok && args.cout > 64 && args.cout <= PXS_GEMM_RANGE_MAXN)
+            return launch_range_conv<128, kRangeCap>(args, stream);
+        if (range_ok && PXS_GEMM_RANGE_WIDE && args.cout > PXS_GEMM_RANGE_MAXN && args.cout <= 256)
+            return launch_range_conv<256, kRangeWideCap>(args, stream);
         if (epi == kEpiStore) return dispatch<uint16_t, kEpiStore>(args, stream);
         if (epi == kEpiAddResidual) return dispatch<uint16_t, kEpiAddResidual>(args, stream);
         return dispatch<uint16_t, kEpiGateResidual>(args, stream);
