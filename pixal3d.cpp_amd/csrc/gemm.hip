@@ -1032,33 +1032,34 @@ gather_gemm_lds_chain_kernel(GemmArgs a, GemmArgs b, ChainArgs c) {
 // offset's 128 gathered rows.  The vector-memory instructions per tile fall
 // from 1,728 to about 1,000 (the weights are now most of them).
 //
-// Pipeline: a 3-stage weight ring (each stage's weights issued two stages
-// ahead) and one halo buffer, which the next (group, chunk) refills after
-// every wave has read its operands of the group's last stage (a barrier
-// inside that stage, the DMA then overlapping its MFMAs); 8 waves in two K
-// groups of 2 x 2 blocks (64 x BN/2 each).  BN = 128 with a 192-row halo is
-// 79 KB of LDS, so two workgroups share a CU; BN = 256 with a 256-row halo
-// (outputs of 129..256 channels) is 136 KB, one workgroup per CU, 207 VGPRs.
-// Stages run chunk by chunk, within a chunk group by group
-// (planes ascending), within a group offsets ascending.  The tile is written
-// through LDS as whole 16-byte row pieces.
+// Pipeline: a ring of WS weight stages (each stage's weights issued WS - 1
+// stages ahead) and one halo buffer, which the next (group, chunk) refills
+// after every wave has read its operands of the group's last stage (a
+// barrier inside that stage, the DMA then overlapping its MFMAs); 8 waves in
+// two K groups of 2 x 2 blocks (64 x BN/2 each).  As launched: BN = 128, a
+// 256-row halo and WS = 2, 72.6 KB of LDS, so two workgroups share a CU
+// (outputs wider than 128 channels take one tile per 128 columns).  Stages
+// run chunk by chunk, within a chunk group by group (planes ascending),
+// within a group offsets ascending.  The tile is written through LDS as
+// whole 16-byte row pieces.
 #ifndef PXS_GEMM_RANGE
 #define PXS_GEMM_RANGE 1
 #endif
-// Widest output of the 128-column range tile; wider outputs up to 256 take
-// the 256-column tile (PXS_GEMM_RANGE_WIDE = 0 keeps them on gather tiles).
+// Outputs of 65..PXS_GEMM_RANGE_MAXN channels run on range tiles (256: the
+// U-Net's conv A and conv C; 128 keeps wider ones on gather tiles).
 #ifndef PXS_GEMM_RANGE_MAXN
-#define PXS_GEMM_RANGE_MAXN 128
+#define PXS_GEMM_RANGE_MAXN 256
 #endif
-#ifndef PXS_GEMM_RANGE_WIDE
-#define PXS_GEMM_RANGE_WIDE 1
+// Weight ring slots: 2 (weights one stage ahead) leaves room for a 256-row
+// halo at two workgroups per CU; 3 (two stages ahead) for 192 rows.
+#ifndef PXS_GEMM_RANGE_WS
+#define PXS_GEMM_RANGE_WS 2
 #endif
-// Halo rows: 192 for the 128-column tile (the most two workgroups per CU
-// leave), 256 for the 256-column tile (one workgroup per CU).
-constexpr int kRangeBM = 128, kRangeNW = 8, kRangeCap = 192, kRangeWideCap = 256, kRangeWStages = 3;
+constexpr int kRangeBM = 128, kRangeNW = 8, kRangeWS = PXS_GEMM_RANGE_WS;
+constexpr int kRangeCap = kRangeWS == 2 ? 256 : 192;
 template <int CAP> constexpr int range_halo_bytes() { return (CAP + 1) * kChunkBytes; }  // its zero row last
-template <int BN, int CAP> constexpr int range_lds_bytes() {
-    return kRangeWStages * BN * kChunkBytes + range_halo_bytes<CAP>() + 27 * kRangeBM * 2;
+template <int BN, int CAP, int WS> constexpr int range_lds_bytes() {
+    return WS * BN * kChunkBytes + range_halo_bytes<CAP>() + 27 * kRangeBM * 2;
 }
 
 // Min, max and or over each 16-lane row by DPP row shifts (VALU, no LDS
@@ -1082,10 +1083,11 @@ __device__ __forceinline__ uint32_t dpp_row_or(uint32_t v) {
     return v | __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xf, 0xf, false);
 }
 
-template <int BN, int CAP>
+template <int BN, int CAP, int WS>
 __global__ void __launch_bounds__(kRangeNW * 64)
 range_conv_bf16_kernel(GemmArgs a) {
-    constexpr int BM = kRangeBM, NW = kRangeNW, NT = NW * 64, WS = kRangeWStages;
+    constexpr int BM = kRangeBM, NW = kRangeNW, NT = NW * 64;
+    constexpr int L = WS - 1;  // weight stages issued ahead
     constexpr int NWG = NW / 2;               // waves per K group
     constexpr int WAVES_N = 2;                // each group: 2 x 2 blocks
     constexpr int WM = BM / 2, WN = BN / WAVES_N;
@@ -1094,12 +1096,12 @@ range_conv_bf16_kernel(GemmArgs a) {
     constexpr int kWBytes = BN * kChunkBytes;
     constexpr int kStagePitch = BN * 2 + 16;  // the output tile staged in LDS
     static_assert(BI >= 1 && TJ >= 1 && TI == 2, "tile shape");
-    static_assert(WS == 3 && 27 * BM * 4 <= kWBytes, "source table inside the third weight slot");
+    static_assert((WS == 2 || WS == 3) && 27 * BM * 4 <= kWBytes, "source table inside the last weight slot");
     // the K groups' partial sums are exchanged in XP passes over the column blocks
-    constexpr int XP = (NW * HI * TJ * 16 * 64 * 4 + range_lds_bytes<BN, CAP>() - 1) / range_lds_bytes<BN, CAP>();
+    constexpr int XP = (NW * HI * TJ * 16 * 64 * 4 + range_lds_bytes<BN, CAP, WS>() - 1) / range_lds_bytes<BN, CAP, WS>();
     constexpr int TJP = TJ / XP;
     static_assert(TJP * XP == TJ, "exchange passes split the column blocks");
-    static_assert(BM * kStagePitch <= range_lds_bytes<BN, CAP>(), "staged tile fits");
+    static_assert(BM * kStagePitch <= range_lds_bytes<BN, CAP, WS>(), "staged tile fits");
     extern __shared__ __align__(16) char smem[];
     const int tiles = static_cast<int>(gridDim.x) - a.side_blocks;
     if (static_cast<int>(blockIdx.x) >= tiles) {
@@ -1112,8 +1114,8 @@ range_conv_bf16_kernel(GemmArgs a) {
     // offset k, row * 128 + (swz(row) << 4), so a lane's 16-byte piece P is at
     // slots ^ (P << 4)
     uint16_t * slots = reinterpret_cast<uint16_t *>(halo + range_halo_bytes<CAP>());
-    // prologue only, in the ring slot the first two stages' weights do not use
-    int32_t * idx = reinterpret_cast<int32_t *>(smem + 2 * kWBytes);
+    // prologue only, in the ring slot the stages issued before the loop do not use
+    int32_t * idx = reinterpret_cast<int32_t *>(smem + L * kWBytes);
     __shared__ uint32_t tile_mask;
     __shared__ int rlo[9], rhi[9];        // source range of each kh row q = k / 3
     __shared__ int g_lo[27], g_rows[27];  // range start (-1 - k: offset k gathered), rows staged
@@ -1324,7 +1326,7 @@ range_conv_bf16_kernel(GemmArgs a) {
                     static_cast<uint32_t>((lslot ^ swz(row)) << 4);
     }
     auto issue_w = [&](uint32_t wk, int c, int ring) __attribute__((always_inline)) {
-        const char * sb = wbase + (wk + static_cast<uint32_t>(c) * 128u);
+        const char * sb = uniform_ptr(wbase + (wk + static_cast<uint32_t>(c) * 128u));
         char * dst = wring + ring * kWBytes;
 #pragma unroll
         for (int j = 0; j < BI; ++j) lds_dma16_sbase(sb, b_voff[j], lds_offset(dst + (wave * BI + j) * 8 * kChunkBytes));
@@ -1335,7 +1337,7 @@ range_conv_bf16_kernel(GemmArgs a) {
     auto issue_h = [&](int g, int c) __attribute__((always_inline)) {
         const int lo = g_lo[g], rows = g_rows[g];
         if (lo >= 0) {
-            const char * sb = reinterpret_cast<const char *>(x + static_cast<int64_t>(lo) * a.ldx + c * 64);
+            const char * sb = uniform_ptr(reinterpret_cast<const char *>(x + static_cast<int64_t>(lo) * a.ldx + c * 64));
             const uint32_t pitch = static_cast<uint32_t>(a.ldx) * 2u;
             for (int q = wave; q * 8 < rows; q += NW) {
                 const int hr = min(q * 8 + lrow, rows - 1);
@@ -1368,9 +1370,9 @@ range_conv_bf16_kernel(GemmArgs a) {
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
     // Stage s is position i0 of chunk c0; info0, info1 describe stages s and
-    // s + 1; (i2, c2) is the position of the next stage to issue (s + 2), into
+    // s + 1; (i2, c2) is the position of the next stage to issue (s + L), into
     // ring slot r2, its table entry e2 read one stage ahead.
-    int i0 = 0, c0 = 0, i2 = 0, c2 = 0, r2 = 2;
+    int i0 = 0, c0 = 0, i2 = 0, c2 = 0, r2 = L;
     uint32_t info0 = 0, info1 = 0;
     uint2 e2 = make_uint2(0, 0);
     const uint32_t pmask = static_cast<uint32_t>((4 * h + kg * 2) << 4);  // this lane's first piece
@@ -1394,10 +1396,12 @@ range_conv_bf16_kernel(GemmArgs a) {
         if (total > 1) {
             const uint2 e1 = rd(i2);
             info1 = e1.x;
-            issue_w(e1.y, c2, 1);
-            adv(i2, c2);
+            if constexpr (L == 2) {
+                issue_w(e1.y, c2, 1);
+                adv(i2, c2);
+            }
         }
-        if (total > 2) e2 = ent[i2];
+        if (total > L) e2 = ent[i2];
     }
     for (int e = tid; e < 27 * BM; e += NT) {
         const int k = e / BM, row = e % BM;  // k wave-uniform
@@ -1411,16 +1415,16 @@ range_conv_bf16_kernel(GemmArgs a) {
     if (total > 0) {
 #pragma unroll
         for (int i = 0; i < TI; ++i) slot_nx[i] = slots[(info0 & 4095) + wm * WM + i * 32 + r];
-        if (total > 1) wait_vmcnt(BI);
+        if (L == 2 && total > 1) wait_vmcnt(BI);
         else wait_vmcnt(0);
         barrier_no_fence();
     }
     bool wait_all = false;  // stage s starts a halo issued in stage s - 1
     for (int s = 0; s < total; ++s) {
         if (s > 0) {
-            // this stage's weights (and halo) are in; the next stage's weights
-            // may still be in flight
-            if (wait_all || s + 1 >= total) wait_vmcnt(0);
+            // this stage's weights (and halo) are in; with L = 2 the next
+            // stage's weights may still be in flight
+            if (L == 1 || wait_all || s + 1 >= total) wait_vmcnt(0);
             else wait_vmcnt(BI);
             barrier_no_fence();
         }
@@ -1431,14 +1435,16 @@ range_conv_bf16_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < TI; ++i) slot_nx[i] = slots[(info1 & 4095) + wm * WM + i * 32 + r];
         }
-        uint32_t info2 = 0;
-        if (s + 2 < total) {
-            // stage s + 2 into the ring slot stage s - 1 used
-            info2 = __builtin_amdgcn_readfirstlane(e2.x);
+        uint32_t info2 = 0;  // stage s + 2
+        if (s + L < total) {
+            // stage s + L into the ring slot stage s - 1 used
+            const uint32_t ex = __builtin_amdgcn_readfirstlane(e2.x);
             issue_w(__builtin_amdgcn_readfirstlane(e2.y), c2, r2);
             adv(i2, c2);
             r2 = r2 == WS - 1 ? 0 : r2 + 1;
-            if (s + 3 < total) e2 = ent[i2];
+            if (s + L + 1 < total) e2 = ent[i2];
+            if constexpr (L == 2) info2 = ex;
+            else if (s + 2 < total) info2 = __builtin_amdgcn_readfirstlane(e2.x);
         }
         bf16x8 af[2][TI];
 #pragma unroll
@@ -1527,12 +1533,12 @@ range_conv_bf16_kernel(GemmArgs a) {
     }
 }
 
-template <int BN, int CAP>
+template <int BN, int CAP, int WS>
 int launch_range_conv(const GemmArgs & args, hipStream_t stream) {
-    constexpr int smem = range_lds_bytes<BN, CAP>();
+    constexpr int smem = range_lds_bytes<BN, CAP, WS>();
     static bool configured = false;
     if (!configured) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&range_conv_bf16_kernel<BN, CAP>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&range_conv_bf16_kernel<BN, CAP, WS>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, smem);
         if (e != hipSuccess) return check_hip(e, "hipFuncSetAttribute(range_conv)");
         configured = true;
@@ -1542,7 +1548,7 @@ int launch_range_conv(const GemmArgs & args, hipStream_t stream) {
     if (blocks > INT32_MAX) return fail(PXS_ERR_ARG, "range conv grid too large");
     if (args.side_blocks > 0 && smem < s2_emit_lds_bytes(args.s2.words_per_block, kRangeNW * 64))
         return fail(PXS_ERR_ARG, "range conv: side work needs more LDS than the tile");
-    hipLaunchKernelGGL((range_conv_bf16_kernel<BN, CAP>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((range_conv_bf16_kernel<BN, CAP, WS>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kRangeNW * 64), smem, stream, args);
     return check_launch("SubMConv3d (neighbourhood ranges)");
 }
@@ -1921,23 +1927,21 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
         return launch_split_f32<kEpiGateResidual>(args, stream);
     }
     if (dtype == PXS_BF16) {
-        // SubMConv3d over a voxel grid: neighbourhood ranges.  65..128
-        // outputs: 128-column tiles with a 192-row halo, two workgroups per
-        // CU.  129..256 outputs: one 256-column tile with a 256-row halo per
-        // CU (136 KB of LDS), which stages every plane of the U-Net's coarse
-        // rows whole: its 256 -> 256 conv at 64^3 (254 tiles, one round)
-        // 0.118-0.119 ms against 0.128-0.129 ms on 128 x 256 gather tiles, and
-        // 0.151 ms with a 192-row halo, whose kh-row and per-offset fallbacks
-        // nothing hides at one workgroup per CU.  (Over a neighbour map, the
-        // SLat decoder's 128-channel levels at up to 1024^3 ran 3.7% slower on
-        // ranges.)
-        const bool range_ok = PXS_GEMM_RANGE && epi == kEpiStore && args.noff == 27 && args.grid &&
-                              args.vec_ok && args.cin % 64 == 0 && args.m > 0 && args.cout % 8 == 0 &&
-                              args.ldy % 8 == 0 && aligned16(args.y);
-        if (range_ok && args.cout > 64 && args.cout <= PXS_GEMM_RANGE_MAXN)
-            return launch_range_conv<128, kRangeCap>(args, stream);
-        if (range_ok && PXS_GEMM_RANGE_WIDE && args.cout > PXS_GEMM_RANGE_MAXN && args.cout <= 256)
-            return launch_range_conv<256, kRangeWideCap>(args, stream);
+        // SubMConv3d over a voxel grid: neighbourhood ranges, 128-column
+        // tiles with a 256-row halo and a 2-slot weight ring (72.6 KB, two
+        // workgroups per CU).  Measured on one box against the forms before
+        // it: the U-Net's conv A (128 -> 128 at 128^3) 0.1692-0.1699 ms
+        // against 0.1745 ms with a 192-row halo and a 3-slot ring, whose
+        // planes of over 192 rows fall back to kh rows or single offsets; its
+        // conv C (256 -> 256 at 64^3) 0.1136-0.1139 ms against 0.1172-0.1175
+        // ms on one 256-column tile per CU (256-row halo, 3 slots) and
+        // 0.128-0.129 ms on 128 x 256 gather tiles.  (Over a neighbour map,
+        // the SLat decoder's 128-channel levels at up to 1024^3 ran 3.7%
+        // slower on ranges.)
+        if (PXS_GEMM_RANGE && epi == kEpiStore && args.noff == 27 && args.grid && args.vec_ok &&
+            args.cin % 64 == 0 && args.m > 0 && args.cout > 64 && args.cout <= PXS_GEMM_RANGE_MAXN &&
+            args.cout % 8 == 0 && args.ldy % 8 == 0 && aligned16(args.y))
+            return launch_range_conv<128, kRangeCap, kRangeWS>(args, stream);
         if (epi == kEpiStore) return dispatch<uint16_t, kEpiStore>(args, stream);
         if (epi == kEpiAddResidual) return dispatch<uint16_t, kEpiAddResidual>(args, stream);
         return dispatch<uint16_t, kEpiGateResidual>(args, stream);
@@ -2254,7 +2258,7 @@ int pxs_unet_s2_level(int dtype, const void * x, const int32_t * coords, int64_t
     constexpr bool kDefaultTile = PXS_GEMM_BM == 128 && PXS_GEMM_BN == 128 &&
                                   PXS_GEMM_STAGES == 2 && PXS_GEMM_WAVES == 8 &&
                                   PXS_GEMM_KSPLIT == 2;
-    const bool ranged = PXS_GEMM_RANGE && cin % 64 == 0 && cout_a <= PXS_GEMM_RANGE_MAXN;
+    const bool ranged = PXS_GEMM_RANGE && cin % 64 == 0 && cout_a > 64 && cout_a <= PXS_GEMM_RANGE_MAXN;
     const bool chain = kDefaultTile && !ranged && dtype == PXS_BF16 && cin % 8 == 0 && cout_a % 8 == 0 &&
                        cout_a > 64 && cout_a <= 128 && cout_b > 64 && m > 0 && aligned16(x) &&
                        aligned16(w_a) && aligned16(y_a) && aligned16(w_b);

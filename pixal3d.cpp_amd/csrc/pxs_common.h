@@ -147,6 +147,16 @@ __device__ __forceinline__ void lds_dma16_coherent(const void * g, uint32_t lds_
                  : "m0");
 }
 
+// A wave-uniform pointer the compiler cannot prove uniform, as a scalar value
+// (lane 0's, which every lane holds): the operand lds_dma16_sbase needs in
+// SGPRs.
+__device__ __forceinline__ const char * uniform_ptr(const char * p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<const char *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // lds_dma16 with a wave-uniform base in SGPRs and a per-lane 32-bit byte
 // offset (the instruction's saddr form): a loop that walks the base keeps its
 // per-lane offsets fixed and advances the base with scalar arithmetic.
