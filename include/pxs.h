@@ -289,9 +289,10 @@ int pxs_s2_tagged_emit(int64_t n, int batch_size, int sx, int sy, int sz, const 
  * SubMConv3d tiles that write its inputs, so it runs in the slots the
  * SubMConv3d's last round leaves free.  m is the coarse row count (known on
  * the host from an earlier build of these coordinates; y_b holds m rows); the
- * emit still writes it to *m_out.  bf16 with 65..128 SubMConv3d outputs and
- * more than 64 strided outputs run chained; other shapes and fp32 run the
- * two calls in sequence.  Outputs identical to pxs_subm_conv3d_grid_s2_emit
+ * emit still writes it to *m_out.  bf16 with 65..128 SubMConv3d outputs,
+ * more than 64 strided outputs and inputs of other than a multiple of 64
+ * channels run chained; other shapes (the SubMConv3d then on neighbourhood
+ * ranges) and fp32 run the two calls in sequence.  Outputs identical to pxs_subm_conv3d_grid_s2_emit
  * then pxs_sparse_conv3d_s2.  The waits are bounded: one that gives up (after
  * about a second, which a correct launch never needs) sets an error word,
  * read back (to host or device memory) by pxs_unet_s2_level_error; its
