@@ -404,8 +404,11 @@ def test_s2_emit_rejects_bad_arguments(px):
 LEVEL_CASES = [
     # (name, coords builder, batch, extents, cin, cout_a, cout_b, dtype): chained when bf16
     # with 65..128 SubMConv3d outputs and more than 64 strided outputs, and inputs of other
-    # than a multiple of 64 channels (those run the SubMConv3d on neighbourhood ranges)
+    # than a multiple of 64 channels (those run the SubMConv3d on neighbourhood ranges, in
+    # two launches)
     ("unet_bf16", lambda: W.unet_stage_128()["coords"], 2, (128, 128, 128), 128, 128, 256, "bf16"),
+    ("box_bf16_ranges", lambda: _box_coords(20, 2, (34, 21, 40), 0.3), 2, (34, 21, 40), 64, 96, 136,
+     "bf16"),
     ("unet_bf16_cin96", lambda: W.unet_stage_128()["coords"], 2, (128, 128, 128), 96, 128, 256,
      "bf16"),
     ("box_bf16", lambda: _box_coords(13, 2, (40, 22, 30), 0.3), 2, (40, 22, 30), 32, 96, 72, "bf16"),
