@@ -1037,7 +1037,7 @@ gather_gemm_lds_chain_kernel(GemmArgs a, GemmArgs b, ChainArgs c) {
 // after every wave has read its operands of the group's last stage (a
 // barrier inside that stage, the DMA then overlapping its MFMAs); 8 waves in
 // two K groups of 2 x 2 blocks (64 x BN/2 each).  As launched: BN = 128, a
-// 256-row halo and WS = 2, 72.6 KB of LDS, so two workgroups share a CU
+// 320-row halo and WS = 2, 80.8 KB of LDS, so two workgroups share a CU
 // (outputs wider than 128 channels take one tile per 128 columns).  Stages
 // run chunk by chunk, within a chunk group by group (planes ascending),
 // within a group offsets ascending.  The tile is written through LDS as
@@ -1050,13 +1050,14 @@ gather_gemm_lds_chain_kernel(GemmArgs a, GemmArgs b, ChainArgs c) {
 #ifndef PXS_GEMM_RANGE_MAXN
 #define PXS_GEMM_RANGE_MAXN 256
 #endif
-// Weight ring slots: 2 (weights one stage ahead) leaves room for a 256-row
-// halo at two workgroups per CU; 3 (two stages ahead) for 192 rows.
+// Weight ring slots: 2 (weights one stage ahead) leaves room for a 320-row
+// halo at two workgroups per CU (81.4 KB with the static tables); 3 (two
+// stages ahead) for 192 rows.
 #ifndef PXS_GEMM_RANGE_WS
 #define PXS_GEMM_RANGE_WS 2
 #endif
 constexpr int kRangeBM = 128, kRangeNW = 8, kRangeWS = PXS_GEMM_RANGE_WS;
-constexpr int kRangeCap = kRangeWS == 2 ? 256 : 192;
+constexpr int kRangeCap = kRangeWS == 2 ? 320 : 192;
 template <int CAP> constexpr int range_halo_bytes() { return (CAP + 1) * kChunkBytes; }  // its zero row last
 template <int BN, int CAP, int WS> constexpr int range_lds_bytes() {
     return WS * BN * kChunkBytes + range_halo_bytes<CAP>() + 27 * kRangeBM * 2;
@@ -1928,14 +1929,15 @@ int run_gemm(int dtype, GemmArgs & args, int epi, hipStream_t stream) {
     }
     if (dtype == PXS_BF16) {
         // SubMConv3d over a voxel grid: neighbourhood ranges, 128-column
-        // tiles with a 256-row halo and a 2-slot weight ring (72.6 KB, two
+        // tiles with a 320-row halo and a 2-slot weight ring (80.8 KB, two
         // workgroups per CU).  Measured on one box against the forms before
-        // it: the U-Net's conv A (128 -> 128 at 128^3) 0.1692-0.1699 ms
-        // against 0.1745 ms with a 192-row halo and a 3-slot ring, whose
-        // planes of over 192 rows fall back to kh rows or single offsets; its
-        // conv C (256 -> 256 at 64^3) 0.1136-0.1139 ms against 0.1172-0.1175
-        // ms on one 256-column tile per CU (256-row halo, 3 slots) and
-        // 0.128-0.129 ms on 128 x 256 gather tiles.  (Over a neighbour map,
+        // it: the U-Net's conv A (128 -> 128 at 128^3) 0.1629-0.1640 ms
+        // against 0.1709-0.1714 ms with a 256-row halo and 0.1745 ms with a
+        // 192-row halo and a 3-slot ring (planes wider than the halo fall
+        // back to kh rows or single offsets, whose refills the tile then
+        // waits for); its conv C (256 -> 256 at 64^3) 0.1136-0.1139 ms
+        // against 0.1172-0.1175 ms on one 256-column tile per CU (256-row
+        // halo, 3 slots) and 0.128-0.129 ms on 128 x 256 gather tiles.  (Over a neighbour map,
         // the SLat decoder's 128-channel levels at up to 1024^3 ran 3.7%
         // slower on ranges.)
         if (PXS_GEMM_RANGE && epi == kEpiStore && args.noff == 27 && args.grid && args.vec_ok &&
