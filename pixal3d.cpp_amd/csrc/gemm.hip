@@ -1063,6 +1063,22 @@ template <int BN, int CAP, int WS> constexpr int range_lds_bytes() {
     return WS * BN * kChunkBytes + range_halo_bytes<CAP>() + 27 * kRangeBM * 2;
 }
 
+// Tile of workgroup `bid`.  PXS_GEMM_RANGE_ORDER 1: chunks of 8 consecutive
+// tiles dealt to the XCDs (bid % 8) in turn, so every XCD's share samples the
+// whole volume and the XCDs finish together (the last partial block of 64
+// tiles in order): conv A 0.1547-0.1552 against 0.1588-0.1596 ms with
+// 0, each XCD a contiguous range of tiles (remap_xcd), whose last tiles
+// ended up to 13 us apart.
+#ifndef PXS_GEMM_RANGE_ORDER
+#define PXS_GEMM_RANGE_ORDER 1
+#endif
+__device__ __forceinline__ int range_tile_order(int bid, int tiles) {
+    if (PXS_GEMM_RANGE_ORDER == 0) return remap_xcd(bid, tiles);
+    if (bid >= tiles / 64 * 64) return bid;
+    const int x = bid & 7, i = bid >> 3;
+    return (((i >> 3) << 3) + x) * 8 + (i & 7);
+}
+
 // Min, max and or over each 16-lane row by DPP row shifts (VALU, no LDS
 // round trip): lane 15 of every row ends with its row's result.
 __device__ __forceinline__ int dpp_row_min(int v) {
@@ -1135,7 +1151,7 @@ range_conv_bf16_kernel(GemmArgs a) {
     const int h = lane >> 5, r = lane & 31;
     const int lrow = lane >> 3, lslot = lane & 7;
     const int tiles_n = (a.cout + BN - 1) / BN;
-    const int logical = remap_xcd(blockIdx.x, tiles);
+    const int logical = range_tile_order(blockIdx.x, tiles);
     const int64_t p0 = static_cast<int64_t>(logical / tiles_n) * BM;
     const int n0 = (logical % tiles_n) * BN;
     const uint16_t * __restrict__ x = static_cast<const uint16_t *>(a.x);
