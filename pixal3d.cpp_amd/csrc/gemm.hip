@@ -1063,20 +1063,26 @@ template <int BN, int CAP, int WS> constexpr int range_lds_bytes() {
     return WS * BN * kChunkBytes + range_halo_bytes<CAP>() + 27 * kRangeBM * 2;
 }
 
-// Tile of workgroup `bid`.  PXS_GEMM_RANGE_ORDER 1: chunks of 8 consecutive
-// tiles dealt to the XCDs (bid % 8) in turn, so every XCD's share samples the
-// whole volume and the XCDs finish together (the last partial block of 64
-// tiles in order): conv A 0.1547-0.1552 against 0.1588-0.1596 ms with
-// 0, each XCD a contiguous range of tiles (remap_xcd), whose last tiles
-// ended up to 13 us apart.
+// Tile of workgroup `bid`.  PXS_GEMM_RANGE_ORDER 1: chunks of
+// PXS_GEMM_RANGE_CHUNK consecutive tiles dealt to the XCDs (bid % 8) in turn,
+// so every XCD's share samples the whole volume and the XCDs finish together
+// (the last partial block of 8 chunks in order).  Conv A (1,268 tiles), one
+// box: 0.1588-0.1596 ms with 0 (each XCD a contiguous range of tiles,
+// remap_xcd, whose last tiles ended up to 13 us apart); chunks of 8
+// 0.1547-0.1552 ms, then on another box chunks of 4 and 8 0.1538-0.1539 ms,
+// of 16 0.1520-0.1525 ms.
 #ifndef PXS_GEMM_RANGE_ORDER
 #define PXS_GEMM_RANGE_ORDER 1
 #endif
+#ifndef PXS_GEMM_RANGE_CHUNK
+#define PXS_GEMM_RANGE_CHUNK 16
+#endif
 __device__ __forceinline__ int range_tile_order(int bid, int tiles) {
+    constexpr int C = PXS_GEMM_RANGE_CHUNK;
     if (PXS_GEMM_RANGE_ORDER == 0) return remap_xcd(bid, tiles);
-    if (bid >= tiles / 64 * 64) return bid;
+    if (bid >= tiles / (8 * C) * (8 * C)) return bid;
     const int x = bid & 7, i = bid >> 3;
-    return (((i >> 3) << 3) + x) * 8 + (i & 7);
+    return ((i / C) * 8 + x) * C + i % C;
 }
 
 // Min, max and or over each 16-lane row by DPP row shifts (VALU, no LDS
