@@ -1070,12 +1070,16 @@ template <int BN, int CAP, int WS> constexpr int range_lds_bytes() {
 // box: 0.1588-0.1596 ms with 0 (each XCD a contiguous range of tiles,
 // remap_xcd, whose last tiles ended up to 13 us apart); chunks of 8
 // 0.1547-0.1552 ms, then on another box chunks of 4 and 8 0.1538-0.1539 ms,
-// of 16 0.1520-0.1525 ms.
+// of 16 0.1520-0.1525 ms, and on a third chunks of 16 0.1560-0.1563 ms, of 32
+// 0.1544-0.1547 ms, of 64 0.1601-0.1605 ms.  Dealing tiles out fetches the
+// rows of neighbouring planes into several XCDs' L2s: the launch reads
+// 114.4 MB from HBM with chunks of 32 (126.8 MB with 16, 103.9 MB with 64,
+// 77.3 MB with contiguous ranges), far from what binds it.
 #ifndef PXS_GEMM_RANGE_ORDER
 #define PXS_GEMM_RANGE_ORDER 1
 #endif
 #ifndef PXS_GEMM_RANGE_CHUNK
-#define PXS_GEMM_RANGE_CHUNK 16
+#define PXS_GEMM_RANGE_CHUNK 32
 #endif
 __device__ __forceinline__ int range_tile_order(int bid, int tiles) {
     constexpr int C = PXS_GEMM_RANGE_CHUNK;
